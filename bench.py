@@ -1,0 +1,268 @@
+"""Benchmark of the Ozaki-scheme hot path on one MI355X.
+
+Default workload (BASELINE.json metric, config 3): FP64 -> INT8 slices,
+num_splits = 4, M = N = K = 8192, batch 1, A and B entries N(0,1) * 2^e with e
+drawn per row of A / per column of B from Uniform-int[-8, 8]
+(torch.Generator seed 2).  A "step" is one ozaki_matmul call (split B, split A,
+fused cross-GEMM) on inputs already resident in HBM.
+
+Prints one JSON line:
+  value        emulated TFLOP/s = 2*M*N*K*batch / (time per step), whole job
+  rel_err      ||C - A@B||_F / ||A@B||_F with A@B in float64 (torch.matmul)
+  roofline     the cross-GEMM (dominant kernel): int8 ops / its average
+               duration from HIP events recorded on the launch stream inside
+               the timed region, against MI355X's dense INT8 MFMA peak
+  split        both split kernels: algorithmic HBM bytes / their event time
+               against the 8 TB/s HBM peak
+  cpu_baseline the CPU oracle (a scalar C port of the reference's algorithm)
+               on a bounded block of the same workload, host cores
+  cpu_torch_matmul  torch.matmul in the input dtype on the host cores
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "emulated TFLOP/s (2MNK/t) FP64→INT8 split=4 at 8192³; rel err vs FP64"
+
+# MI355X published dense peaks
+PEAK_INT8_TOPS = 5000.0       # TOP/s dense INT8 MFMA
+PEAK_FP16_TFLOPS = 2500.0     # TFLOP/s dense FP16 MFMA
+PEAK_HBM_GBS = 8000.0         # GB/s HBM3E
+
+CONFIGS = {
+    # name: (input dtype, slice dtype, L, A shape, B shape, seed, distribution)
+    "C2": ("float32", "float16", 2, (4096, 4096), (4096, 4096), 1, "uniform"),
+    "C3": ("float64", "int8", 4, (8192, 8192), (8192, 8192), 2, "exp8"),
+    "C4": ("float64", "float16", 3, (16, 1024, 2048), (2048, 1024), 3, "normal"),
+    "C5": ("float32", "int8", 3, (1024, 65536), (65536, 1024), 4, "outliers"),
+}
+
+
+def make_inputs(cfg):
+    import torch
+    xdt, _, _, sa, sb, seed, dist = cfg
+    g = torch.Generator().manual_seed(seed)
+    if dist == "exp8":
+        A = torch.randn(*sa, generator=g, dtype=torch.float64)
+        B = torch.randn(*sb, generator=g, dtype=torch.float64)
+        A *= torch.pow(2.0, torch.randint(-8, 9, (*sa[:-1], 1), generator=g).double())
+        B *= torch.pow(2.0, torch.randint(-8, 9, (1, sb[-1]), generator=g).double())
+    elif dist == "normal":
+        A = torch.randn(*sa, generator=g, dtype=torch.float64)
+        B = torch.randn(*sb, generator=g, dtype=torch.float64)
+    else:
+        A = torch.rand(*sa, generator=g, dtype=torch.float32) * 2 - 1
+        B = torch.rand(*sb, generator=g, dtype=torch.float32) * 2 - 1
+        if dist == "outliers":
+            A[torch.rand(*sa, generator=g) < 0.01] *= 1e4
+            B[torch.rand(*sb, generator=g) < 0.01] *= 1e4
+    return A.to(getattr(torch, xdt)), B.to(getattr(torch, xdt))
+
+
+def cpu_oracle_baseline(A_cpu, B_cpu, slice_dtype, L, block):
+    """Time the C oracle on a block x block corner of the output with the full
+    K: split `block` rows of A and `block` columns of B, then the L^2 slice
+    GEMMs and the ordered epilogue.  Single-threaded."""
+    import numpy as np
+    import oracle
+    a = A_cpu.reshape(-1, A_cpu.shape[-1])[:block].numpy()
+    b = B_cpu.reshape(-1, B_cpu.shape[-1])[:, :block].numpy() if B_cpu.dim() == 2 else \
+        B_cpu[0][:, :block].numpy()
+    K = a.shape[1]
+    sd = slice_dtype
+    alpha = oracle.compute_split_bits(K, sd, "int32" if sd == "int8" else "float32")
+    t0 = time.perf_counter()
+    a_sl, a_sc = oracle.split(a, L, alpha, sd)
+    b_sl, b_sc = oracle.split(np.ascontiguousarray(b).T, L, alpha, sd)
+    oracle.cross_gemm(a_sl, b_sl, a_sc, b_sc, str(a.dtype))
+    dt = time.perf_counter() - t0
+    return 2.0 * block * block * K / dt / 1e12, dt
+
+
+def cpu_torch_matmul(A_cpu, B_cpu, reps):
+    import torch
+    ncores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(ncores)
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        torch.matmul(A_cpu, B_cpu)
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    t = ts[len(ts) // 2]
+    flops = 2.0 * A_cpu.shape[-2] * A_cpu.shape[-1] * B_cpu.shape[-1]
+    if A_cpu.dim() == 3:
+        flops *= A_cpu.shape[0]
+    return flops / t / 1e12, ncores, torch.get_num_threads()
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="C3", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--cpu-block", type=int, default=256)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build has no "
+              "multi-GPU path; the sharding design is described in DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import ozaki_triton_amd as ozk
+    from ozaki_triton_amd.ozaki import _ozaki_matmul_impl
+
+    cfg = CONFIGS[args.config]
+    xdt, sdt, L = cfg[0], cfg[1], cfg[2]
+    slice_dtype = getattr(torch, sdt)
+    dev = torch.device("cuda:0")
+    A_cpu, B_cpu = make_inputs(cfg)
+    A, B = A_cpu.to(dev), B_cpu.to(dev)
+    M, K = A.shape[-2:]
+    N = B.shape[-1]
+    batch = A.shape[0] if A.dim() == 3 else 1
+    print(f"[bench] {args.config}: {xdt}->{sdt} L={L} A{tuple(A.shape)} B{tuple(B.shape)}",
+          file=sys.stderr, flush=True)
+
+    phases = ("split_b", "split_a", "cross_gemm", "end")
+    events = []
+
+    def marker(step_events):
+        def mark(name):
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            step_events[name] = ev
+        return mark
+
+    for _ in range(args.warmup):
+        _ozaki_matmul_impl(A, B, L, slice_dtype, False, None)
+    torch.cuda.synchronize()
+
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ev = {}
+        C = _ozaki_matmul_impl(A, B, L, slice_dtype, False, marker(ev))
+        events.append(ev)
+    torch.cuda.synchronize()
+    t = time.perf_counter() - t0
+    ms = t / args.steps * 1e3
+
+    def avg_ms(a, b):
+        return sum(e[a].elapsed_time(e[b]) for e in events) / len(events)
+
+    t_split_b = avg_ms("split_b", "split_a")
+    t_split_a = avg_ms("split_a", "cross_gemm")
+    t_cross = avg_ms("cross_gemm", "end")
+
+    emu_flops = 2.0 * M * N * K * batch
+    value = emu_flops / (ms * 1e-3) / 1e12
+
+    # accuracy vs FP64 torch.matmul
+    C64 = torch.matmul(A.double(), B.double())
+    rel = float((C.double() - C64).norm() / C64.norm())
+    del C64
+
+    # dominant kernel: cross-GEMM, L^2 slice GEMMs of 2*M*N*K ops each
+    cross_ops = L * L * 2.0 * M * N * K * batch
+    if sdt == "int8":
+        peak, unit_c = PEAK_INT8_TOPS, "TOP/s"
+    else:
+        peak, unit_c = PEAK_FP16_TFLOPS, "TFLOP/s"
+    achieved = cross_ops / (t_cross * 1e-3) / 1e12
+    # split: read the unique inputs, write the unique slices and scales
+    xsz = 8 if xdt == "float64" else 4
+    ssz = 1 if sdt == "int8" else 2
+    a_elems = A.numel()
+    b_elems = B.numel()
+    a_rows = A.numel() // K
+    b_cols = (B.numel() // K)
+    split_bytes = (a_elems + b_elems) * (xsz + L * ssz) + (a_rows + b_cols) * L * 4
+    split_ms = t_split_a + t_split_b
+    split_gbs = split_bytes / (split_ms * 1e-3) / 1e9
+
+    rec = {
+        "metric": METRIC if args.config == "C3" else f"emulated TFLOP/s (2MNK/t) {args.config}",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": f"{'f64' if xdt == 'float64' else 'f32'} via {'i8' if sdt == 'int8' else 'f16'} "
+                 "slices",
+        "data": "synthetic",
+        "config": {
+            "workload": {
+                "C2": "FP32->FP16 num_splits=2, M=N=K=4096",
+                "C3": "FP64->INT8 num_splits=4, M=N=K=8192, batch 1",
+                "C4": "FP64->FP16 num_splits=3, A[16,1024,2048] x B[2048,1024] (broadcast)",
+                "C5": "FP32->INT8 num_splits=3, M=N=1024, K=65536, 1% outliers x1e4",
+            }[args.config],
+            "input_dtype": xdt, "slice_dtype": sdt, "num_splits": L,
+            "M": M, "N": N, "K": K, "batch": batch, "seed": cfg[5],
+        },
+        "rel_err": rel,
+        "roofline": {
+            "kernel": "cross_gemm_kernel",
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": peak,
+            "unit": unit_c,
+            "frac": round(achieved / peak, 4),
+            "traffic": None,
+            "avg_ms": round(t_cross, 4),
+        },
+        "split": {
+            "kernels": "split_strip_kernel (B) + split_rows_kernel (A)",
+            "bound": "hbm",
+            "bytes": split_bytes,
+            "achieved": round(split_gbs, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(split_gbs / PEAK_HBM_GBS, 4),
+            "ms_a": round(t_split_a, 4),
+            "ms_b": round(t_split_b, 4),
+        },
+    }
+    if not args.no_cpu:
+        block = args.cpu_block
+        v, dt = cpu_oracle_baseline(A_cpu, B_cpu, sdt, L, block)
+        rec["cpu_baseline"] = {
+            "value": round(v, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"oracle (C, scalar) on a {block}x{block} output block with the full "
+                      f"K={K}: split {block} rows of A + {block} columns of B + {L * L} slice "
+                      f"GEMMs + epilogue, {dt:.1f} s",
+        }
+        tv, ncores, nthr = cpu_torch_matmul(A_cpu[:1] if A_cpu.dim() == 3 else A_cpu, B_cpu, 3)
+        rec["cpu_torch_matmul"] = {"value": round(tv, 4), "unit": "TFLOP/s", "cores": ncores,
+                                   "threads": nthr, "dtype": xdt, "cpu": cpu_model(),
+                                   "reps": 3, "stat": "median"}
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

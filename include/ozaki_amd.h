@@ -1,0 +1,128 @@
+/*
+ * ozaki_amd.h -- C ABI of the MI355X-native Ozaki-scheme matmul (libozaki_amd.so).
+ *
+ * The reference (WhFanatic/Ozaki_triton) has no FFI: its hot path sits behind
+ * the Python functions of ozaki_triton.py and, below them, the Triton launch
+ * ABI of two JIT kernels.  Each entry point here replaces one of those launch
+ * sites; the Python package ozaki_triton_amd binds them with ctypes.
+ *
+ * Conventions
+ *   - Plain pointers to device memory, sizes and element strides (int64, in
+ *     elements of the tensor they describe).  A batch stride may be 0
+ *     (broadcast operand).
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).  All
+ *     work is enqueued asynchronously on it; nothing synchronises the host.
+ *   - Return 0 on success and a negative OZK_ERR_* code on failure;
+ *     ozk_strerror() names the code.  Argument checks run on the host before
+ *     anything is enqueued, so a rejected call has no device side effect.
+ *   - No device memory is allocated.  Scratch space comes from the caller
+ *     through (workspace, workspace_bytes); *_workspace_bytes() says how much.
+ *   - No mutable global state: calls are re-entrant and thread-safe.
+ */
+#ifndef OZAKI_AMD_H
+#define OZAKI_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes (torch dtype names in comments) */
+enum {
+    OZK_F64 = 0,  /* torch.float64 */
+    OZK_F32 = 1,  /* torch.float32 */
+    OZK_F16 = 2,  /* torch.float16 */
+    OZK_BF16 = 3, /* torch.bfloat16 */
+    OZK_I8 = 4,   /* torch.int8 */
+    OZK_I32 = 5   /* torch.int32 */
+};
+
+/* status codes */
+enum {
+    OZK_OK = 0,
+    OZK_ERR_NULL = -1,        /* a required pointer is NULL */
+    OZK_ERR_DTYPE = -2,       /* dtype combination not supported */
+    OZK_ERR_SPLITS = -3,      /* num_splits outside [0, OZK_MAX_SPLITS] */
+    OZK_ERR_SHAPE = -4,       /* negative size, or K mismatch */
+    OZK_ERR_ALPHA = -5,       /* alpha < 1 (K too large for the accumulator) */
+    OZK_ERR_WORKSPACE = -6,   /* workspace missing or too small */
+    OZK_ERR_LAUNCH = -7,      /* a HIP launch failed (hipGetLastError) */
+    OZK_ERR_ACCUM = -8        /* unsupported dot accumulator dtype */
+};
+
+#define OZK_MAX_SPLITS 4
+
+/* Name of a status code (static string). */
+const char *ozk_strerror(int status);
+
+/* ABI version: major * 10000 + minor * 100 + patch. */
+int ozk_version(void);
+
+/*
+ * compute_split_bits -- replaces ozaki_triton.py:76-98.
+ *   alpha = min(int((acc_bits - log2 n) / 2), slice_bits), acc_bits 31 for an
+ *   int32 dot accumulator and 23 for fp32.  Writes alpha (which may be < 1) to
+ *   *alpha_out; returns OZK_ERR_ALPHA when alpha < 1 (the reference asserts),
+ *   OZK_ERR_ACCUM / OZK_ERR_DTYPE for an unknown accumulator / slice dtype.
+ */
+int ozk_compute_split_bits(int64_t n, int slice_dtype, int dot_accum_dtype, int *alpha_out);
+
+/*
+ * Split -- replaces the launch of split_matrix_kernel in split_matrix
+ * (ozaki_triton.py:214-256; kernel 137-211).
+ *   X       [batch, rows, K]      x_dtype OZK_F64 or OZK_F32, strides x_strides
+ *   slices  [batch, L, rows, K]   slice_dtype OZK_I8 or OZK_F16, strides slice_strides
+ *   scales  [batch, L, rows]      fp32, strides scale_strides
+ * For each row: L levels of (row max -> power-of-two scale -> quantise ->
+ * residual), with the residual rounded to fp32 between levels exactly as the
+ * reference's fp32 residual buffer does.  B is split through its transposed
+ * view (rows = columns of B, x_strides = {K*N, 1, N}).
+ * Workspace: 0 bytes on the resident fast paths; otherwise
+ * ozk_split_workspace_bytes() (an fp32 residual, batch*rows*K*4 bytes).
+ */
+int ozk_split_workspace_bytes(int x_dtype, int64_t batch, int64_t rows, int64_t K,
+                              const int64_t x_strides[3], int num_splits, int slice_dtype,
+                              const int64_t slice_strides[4], size_t *bytes_out);
+
+int ozk_split(const void *X, int x_dtype, int64_t batch, int64_t rows, int64_t K,
+              const int64_t x_strides[3], int num_splits, int alpha, int slice_dtype,
+              void *slices, const int64_t slice_strides[4], float *scales,
+              const int64_t scale_strides[3], void *workspace, size_t workspace_bytes,
+              void *stream);
+
+/*
+ * Cross-GEMM -- replaces the launch of cross_gemm_kernel in cross_gemm
+ * (ozaki_triton.py:455-498; kernel 306-452).
+ *   A_slices [batch, L, M, K]  strides a_strides
+ *   B_slices [batch, L, K, N]  strides b_strides (logical K x N; ozaki_matmul
+ *                              passes a K-contiguous view, b_strides[2] == 1)
+ *   A_scales [batch, L, M] fp32, B_scales [batch, L, N] fp32
+ *   C        [batch, M, N]  out_dtype OZK_F64 (fp64 outer accumulator) or
+ *                           OZK_F32 (fp32 outer accumulator)
+ *   C = sum_{i,j} fl32(fl32(fl32(A_i B_j) * sa_i) * sb_j), summed i-major,
+ *   j-minor from 0 in the outer accumulator.  int8 slices use an exact int32
+ *   dot (MFMA i8), fp16 slices an fp32-accumulated dot (MFMA f16).
+ * Workspace: 0 bytes when both slice operands are K-contiguous with 16-byte
+ * aligned rows; otherwise ozk_cross_gemm_workspace_bytes() for a packed copy.
+ */
+int ozk_cross_gemm_workspace_bytes(int64_t batch, int64_t M, int64_t N, int64_t K,
+                                   int num_splits, int slice_dtype,
+                                   const void *A_slices, const int64_t a_strides[4],
+                                   const void *B_slices, const int64_t b_strides[4],
+                                   size_t *bytes_out);
+
+int ozk_cross_gemm(const void *A_slices, const int64_t a_strides[4], const void *B_slices,
+                   const int64_t b_strides[4], const float *A_scales,
+                   const int64_t sa_strides[3], const float *B_scales,
+                   const int64_t sb_strides[3], int64_t batch, int64_t M, int64_t N, int64_t K,
+                   int num_splits, int slice_dtype, void *C, int out_dtype,
+                   const int64_t c_strides[3], void *workspace, size_t workspace_bytes,
+                   void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OZAKI_AMD_H */

@@ -1,0 +1,93 @@
+"""ctypes binding of libozaki_amd.so (declarations: include/ozaki_amd.h).
+
+The library is the only compute path of this package.  If it is missing the
+import of the product API fails loudly; there is no CPU or eager fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libozaki_amd.so")
+
+# dtype and status codes (include/ozaki_amd.h)
+OZK_F64, OZK_F32, OZK_F16, OZK_BF16, OZK_I8, OZK_I32 = 0, 1, 2, 3, 4, 5
+OZK_OK = 0
+OZK_ERR_NULL = -1
+OZK_ERR_DTYPE = -2
+OZK_ERR_SPLITS = -3
+OZK_ERR_SHAPE = -4
+OZK_ERR_ALPHA = -5
+OZK_ERR_WORKSPACE = -6
+OZK_ERR_LAUNCH = -7
+OZK_ERR_ACCUM = -8
+OZK_MAX_SPLITS = 4
+
+# every symbol include/ozaki_amd.h declares
+EXPORTED = (
+    "ozk_strerror",
+    "ozk_version",
+    "ozk_compute_split_bits",
+    "ozk_split_workspace_bytes",
+    "ozk_split",
+    "ozk_cross_gemm_workspace_bytes",
+    "ozk_cross_gemm",
+)
+
+_lib = None
+
+
+class OzakiLibError(RuntimeError):
+    """A C-ABI call returned a non-zero status."""
+
+    def __init__(self, fn: str, status: int):
+        self.status = status
+        super().__init__(f"{fn} failed: {strerror(status)} (status {status})")
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "
+            "(ozaki_triton_amd has no fallback path)")
+    L = ctypes.CDLL(LIB_PATH)
+    i64, i32, vp, sz = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t
+    p64 = ctypes.POINTER(ctypes.c_int64)
+    L.ozk_strerror.argtypes = [i32]
+    L.ozk_strerror.restype = ctypes.c_char_p
+    L.ozk_version.argtypes = []
+    L.ozk_version.restype = i32
+    L.ozk_compute_split_bits.argtypes = [i64, i32, i32, ctypes.POINTER(ctypes.c_int)]
+    L.ozk_compute_split_bits.restype = i32
+    L.ozk_split_workspace_bytes.argtypes = [i32, i64, i64, i64, p64, i32, i32, p64,
+                                            ctypes.POINTER(sz)]
+    L.ozk_split_workspace_bytes.restype = i32
+    L.ozk_split.argtypes = [vp, i32, i64, i64, i64, p64, i32, i32, i32, vp, p64, vp, p64,
+                            vp, sz, vp]
+    L.ozk_split.restype = i32
+    L.ozk_cross_gemm_workspace_bytes.argtypes = [i64, i64, i64, i64, i32, i32, vp, p64, vp,
+                                                 p64, ctypes.POINTER(sz)]
+    L.ozk_cross_gemm_workspace_bytes.restype = i32
+    L.ozk_cross_gemm.argtypes = [vp, p64, vp, p64, vp, p64, vp, p64, i64, i64, i64, i64, i32,
+                                 i32, vp, i32, p64, vp, sz, vp]
+    L.ozk_cross_gemm.restype = i32
+    _lib = L
+    return L
+
+
+def strerror(status: int) -> str:
+    return load().ozk_strerror(int(status)).decode()
+
+
+def i64arr(vals) -> ctypes.Array:
+    vals = [int(v) for v in vals]
+    return (ctypes.c_int64 * len(vals))(*vals)
+
+
+def check(fn: str, status: int) -> None:
+    if status != OZK_OK:
+        raise OzakiLibError(fn, status)

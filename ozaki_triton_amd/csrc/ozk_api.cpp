@@ -1,0 +1,241 @@
+// ozk_api.cpp -- the extern "C" boundary of libozaki_amd.so (include/ozaki_amd.h).
+//
+// Host-side only: argument validation, path planning and the launches.  No
+// device memory is allocated here; scratch comes from the caller's workspace.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+
+#include "../../include/ozaki_amd.h"
+#include "ozk_internal.h"
+
+namespace {
+
+bool is_input_dtype(int d) { return d == OZK_F64 || d == OZK_F32; }
+bool is_slice_dtype(int d) { return d == OZK_I8 || d == OZK_F16; }
+int slice_size(int d) { return d == OZK_I8 ? 1 : 2; }
+int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+int hip_status(hipError_t e) { return e == hipSuccess ? OZK_OK : OZK_ERR_LAUNCH; }
+
+ozk::SplitParams make_split_params(const void *X, int64_t batch, int64_t rows, int64_t K,
+                                   const int64_t xs[3], int L, int alpha, void *slices,
+                                   const int64_t ss[4], float *scales, const int64_t cs[3]) {
+    ozk::SplitParams p;
+    p.X = X;
+    p.batch = batch;
+    p.rows = rows;
+    p.K = K;
+    p.xs_b = xs[0];
+    p.xs_r = xs[1];
+    p.xs_k = xs[2];
+    p.L = L;
+    p.alpha = alpha;
+    p.slices = slices;
+    p.ss_b = ss[0];
+    p.ss_l = ss[1];
+    p.ss_r = ss[2];
+    p.ss_k = ss[3];
+    p.scales = scales;
+    p.cs_b = cs[0];
+    p.cs_l = cs[1];
+    p.cs_r = cs[2];
+    p.resid = nullptr;
+    return p;
+}
+
+// Bytes of the packed copy of one slice operand, or 0 when it is already in
+// the layout the MFMA kernel reads: K-contiguous, 16-byte aligned rows/planes.
+int64_t pack_bytes(const void *ptr, const int64_t s[4], int64_t batch, int L, int64_t rows,
+                   int64_t K, int es, bool is_b) {
+    // a_strides = (b, l, m, k); b_strides = (b, l, k, n)
+    const int64_t sk = is_b ? s[2] : s[3];
+    const int64_t sr = is_b ? s[3] : s[2];
+    const bool ok = sk == 1 && ((uintptr_t)ptr % 16) == 0 && (sr * es) % 16 == 0 &&
+                    (s[1] * es) % 16 == 0 && (s[0] * es) % 16 == 0 && (K * es) % 16 == 0;
+    if (ok || rows == 0 || K == 0 || L == 0) return 0;
+    const int64_t kp = round_up(K * es, 16) / es;
+    return round_up(batch * L * rows * kp * es, 256);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *ozk_strerror(int status) {
+    switch (status) {
+    case OZK_OK: return "ok";
+    case OZK_ERR_NULL: return "required pointer is NULL";
+    case OZK_ERR_DTYPE: return "unsupported dtype combination";
+    case OZK_ERR_SPLITS: return "num_splits out of range";
+    case OZK_ERR_SHAPE: return "invalid shape";
+    case OZK_ERR_ALPHA: return "alpha < 1: K too large to split safely";
+    case OZK_ERR_WORKSPACE: return "workspace missing or too small";
+    case OZK_ERR_LAUNCH: return "HIP launch failed";
+    case OZK_ERR_ACCUM: return "unsupported dot accumulator dtype";
+    default: return "unknown status";
+    }
+}
+
+int ozk_version(void) { return 100; }
+
+int ozk_compute_split_bits(int64_t n, int slice_dtype, int dot_accum_dtype, int *alpha_out) {
+    if (!alpha_out) return OZK_ERR_NULL;
+    int acc_bits;
+    if (dot_accum_dtype == OZK_I32) acc_bits = 31;
+    else if (dot_accum_dtype == OZK_F32) acc_bits = 23;
+    else return OZK_ERR_ACCUM;
+    int slice_bits;
+    switch (slice_dtype) {
+    case OZK_F32: slice_bits = 23; break;
+    case OZK_F16: slice_bits = 10; break;
+    case OZK_BF16: slice_bits = 7; break;
+    case OZK_I8: slice_bits = 7; break;
+    default: return OZK_ERR_DTYPE;
+    }
+    if (n <= 0) return OZK_ERR_SHAPE;   // log2(0) raises in the reference
+    const double a = ((double)acc_bits - log2((double)n)) / 2.0;
+    int alpha = (int)a;                 // int(): truncation toward zero
+    if (alpha > slice_bits) alpha = slice_bits;
+    *alpha_out = alpha;
+    return alpha >= 1 ? OZK_OK : OZK_ERR_ALPHA;
+}
+
+int ozk_split_workspace_bytes(int x_dtype, int64_t batch, int64_t rows, int64_t K,
+                              const int64_t x_strides[3], int num_splits, int slice_dtype,
+                              const int64_t slice_strides[4], size_t *bytes_out) {
+    if (!bytes_out || !x_strides || !slice_strides) return OZK_ERR_NULL;
+    if (!is_input_dtype(x_dtype) || !is_slice_dtype(slice_dtype)) return OZK_ERR_DTYPE;
+    if (num_splits < 0 || num_splits > OZK_MAX_SPLITS) return OZK_ERR_SPLITS;
+    if (batch < 0 || rows < 0 || K < 0) return OZK_ERR_SHAPE;
+    *bytes_out = 0;
+    if (num_splits <= 1) return OZK_OK;
+    // the plan depends on pointer alignment only through 16-byte checks; a
+    // 256-byte aligned stand-in pointer gives the plan of any aligned tensor
+    ozk::SplitParams p = make_split_params((const void *)256, batch, rows, K, x_strides,
+                                           num_splits, 1, (void *)256, slice_strides, nullptr,
+                                           x_strides);
+    const ozk::SplitPlan plan = ozk::plan_split(p, x_dtype, slice_dtype);
+    if (plan.path == ozk::kSplitGeneric) *bytes_out = (size_t)(batch * rows * K * 4);
+    return OZK_OK;
+}
+
+int ozk_split(const void *X, int x_dtype, int64_t batch, int64_t rows, int64_t K,
+              const int64_t x_strides[3], int num_splits, int alpha, int slice_dtype,
+              void *slices, const int64_t slice_strides[4], float *scales,
+              const int64_t scale_strides[3], void *workspace, size_t workspace_bytes,
+              void *stream) {
+    if (!x_strides || !slice_strides || !scale_strides) return OZK_ERR_NULL;
+    if (!is_input_dtype(x_dtype) || !is_slice_dtype(slice_dtype)) return OZK_ERR_DTYPE;
+    if (num_splits < 0 || num_splits > OZK_MAX_SPLITS) return OZK_ERR_SPLITS;
+    if (batch < 0 || rows < 0 || K < 0) return OZK_ERR_SHAPE;
+    if (num_splits > 0 && alpha < 1) return OZK_ERR_ALPHA;
+    if (batch * rows == 0 || num_splits == 0) return OZK_OK;
+    if (!X || !slices || !scales) return OZK_ERR_NULL;
+    ozk::SplitParams p = make_split_params(X, batch, rows, K, x_strides, num_splits, alpha,
+                                           slices, slice_strides, scales, scale_strides);
+    const ozk::SplitPlan plan = ozk::plan_split(p, x_dtype, slice_dtype);
+    if (plan.path == ozk::kSplitGeneric && num_splits > 1) {
+        const size_t need = (size_t)(batch * rows * K * 4);
+        if (!workspace || workspace_bytes < need) return OZK_ERR_WORKSPACE;
+        p.resid = (float *)workspace;
+    }
+    return hip_status(ozk::launch_split(p, plan, x_dtype, slice_dtype, (hipStream_t)stream));
+}
+
+int ozk_cross_gemm_workspace_bytes(int64_t batch, int64_t M, int64_t N, int64_t K,
+                                   int num_splits, int slice_dtype, const void *A_slices,
+                                   const int64_t a_strides[4], const void *B_slices,
+                                   const int64_t b_strides[4], size_t *bytes_out) {
+    if (!bytes_out || !a_strides || !b_strides) return OZK_ERR_NULL;
+    if (!is_slice_dtype(slice_dtype)) return OZK_ERR_DTYPE;
+    if (num_splits < 0 || num_splits > OZK_MAX_SPLITS) return OZK_ERR_SPLITS;
+    if (batch < 0 || M < 0 || N < 0 || K < 0) return OZK_ERR_SHAPE;
+    const int es = slice_size(slice_dtype);
+    const int64_t a = pack_bytes(A_slices, a_strides, batch, num_splits, M, K, es, false);
+    const int64_t b = pack_bytes(B_slices, b_strides, batch, num_splits, N, K, es, true);
+    *bytes_out = (size_t)(a + b);
+    return OZK_OK;
+}
+
+int ozk_cross_gemm(const void *A_slices, const int64_t a_strides[4], const void *B_slices,
+                   const int64_t b_strides[4], const float *A_scales,
+                   const int64_t sa_strides[3], const float *B_scales,
+                   const int64_t sb_strides[3], int64_t batch, int64_t M, int64_t N, int64_t K,
+                   int num_splits, int slice_dtype, void *C, int out_dtype,
+                   const int64_t c_strides[3], void *workspace, size_t workspace_bytes,
+                   void *stream) {
+    if (!a_strides || !b_strides || !sa_strides || !sb_strides || !c_strides)
+        return OZK_ERR_NULL;
+    if (!is_slice_dtype(slice_dtype) || !is_input_dtype(out_dtype)) return OZK_ERR_DTYPE;
+    if (num_splits < 0 || num_splits > OZK_MAX_SPLITS) return OZK_ERR_SPLITS;
+    if (batch < 0 || M < 0 || N < 0 || K < 0) return OZK_ERR_SHAPE;
+    if (batch * M * N == 0) return OZK_OK;
+    if (!C) return OZK_ERR_NULL;
+    hipStream_t st = (hipStream_t)stream;
+
+    ozk::GemmParams p;
+    p.sa = A_scales;
+    p.sb = B_scales;
+    p.sas_b = sa_strides[0];
+    p.sas_l = sa_strides[1];
+    p.sas_m = sa_strides[2];
+    p.sbs_b = sb_strides[0];
+    p.sbs_l = sb_strides[1];
+    p.sbs_n = sb_strides[2];
+    p.C = C;
+    p.cs_b = c_strides[0];
+    p.cs_m = c_strides[1];
+    p.cs_n = c_strides[2];
+    p.batch = batch;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    if (num_splits == 0) return hip_status(ozk::launch_zero_c(p, out_dtype, st));
+    if (!A_slices || !B_slices || !A_scales || !B_scales) return OZK_ERR_NULL;
+
+    const int es = slice_size(slice_dtype);
+    const int64_t abytes = pack_bytes(A_slices, a_strides, batch, num_splits, M, K, es, false);
+    const int64_t bbytes = pack_bytes(B_slices, b_strides, batch, num_splits, N, K, es, true);
+    if (abytes + bbytes > 0 && (!workspace || workspace_bytes < (size_t)(abytes + bbytes)))
+        return OZK_ERR_WORKSPACE;
+    const int64_t kp = round_up(K * es, 16) / es;
+    char *ws = (char *)workspace;
+
+    if (abytes > 0) {
+        ozk::PackParams pk{A_slices, a_strides[0], a_strides[1], a_strides[2], a_strides[3],
+                           ws, batch, num_splits, M, K, kp, es};
+        hipError_t e = ozk::launch_pack(pk, st);
+        if (e != hipSuccess) return OZK_ERR_LAUNCH;
+        p.A = ws;
+        p.as_b = num_splits * M * kp;
+        p.as_l = M * kp;
+        p.as_m = kp;
+        ws += abytes;
+    } else {
+        p.A = A_slices;
+        p.as_b = a_strides[0];
+        p.as_l = a_strides[1];
+        p.as_m = a_strides[2];
+    }
+    if (bbytes > 0) {
+        ozk::PackParams pk{B_slices, b_strides[0], b_strides[1], b_strides[3], b_strides[2],
+                           ws, batch, num_splits, N, K, kp, es};
+        hipError_t e = ozk::launch_pack(pk, st);
+        if (e != hipSuccess) return OZK_ERR_LAUNCH;
+        p.B = ws;
+        p.bs_b = num_splits * N * kp;
+        p.bs_l = N * kp;
+        p.bs_n = kp;
+    } else {
+        p.B = B_slices;
+        p.bs_b = b_strides[0];
+        p.bs_l = b_strides[1];
+        p.bs_n = b_strides[3];
+    }
+    const ozk::GemmPlan plan = ozk::plan_gemm(p, num_splits, slice_dtype);
+    return hip_status(ozk::launch_gemm(p, plan, num_splits, slice_dtype, out_dtype, st));
+}
+
+}  // extern "C"

@@ -1,0 +1,157 @@
+// ozk_common.h -- device arithmetic shared by the split and cross-GEMM kernels.
+//
+// Every helper reproduces one rounding step of the reference exactly (IEEE
+// binary32/binary64, round-to-nearest-even, denormals kept).  The library is
+// compiled with -ffp-contract=off so that no multiply-add pair is fused where
+// the reference rounds the product.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define OZK_DEV __device__ __forceinline__
+
+namespace ozk {
+
+// ---------------------------------------------------------------------------
+// Exponent rule of ozaki_triton.py:174: E = ceil(log2(mu)) where log2 is the
+// correctly rounded float32 log2 (the value numpy's float32 log2 returns).
+// For normal mu = 2^k (1 + j 2^-23) the result is k when j == 0 or j <= J(k),
+// else k + 1.  J(k) = floor(2^(p-1) ln 2): p = floor(log2 k) for k >= 4,
+// p = ceil(log2 |k|) - 1 for k <= -5, J = 0 for -4 <= k <= 3; byte p of
+// kBandJ holds J for that p (p = 2..6 -> 1, 2, 5, 11, 22).  mu is never below
+// 1e-38f (ozaki_triton.py:172), so a subnormal mu lies in [1e-38f, 2^-126) and
+// its ceiling is -126.
+// ---------------------------------------------------------------------------
+constexpr uint64_t kBandJ = 0x00160B0502010000ull;
+
+OZK_DEV int ceil_log2_f32(float mu) {
+    uint32_t u = __float_as_uint(mu);
+    int be = (int)((u >> 23) & 0xFFu);
+    uint32_t j = u & 0x7FFFFFu;
+    if (be == 0) return -126;
+    int k = be - 127;
+    int p = -1;
+    if (k >= 4) p = 31 - __clz(k);                 // floor(log2 k)
+    else if (k <= -5) p = 31 - __clz(-k - 1);       // ceil(log2 |k|) - 1
+    int J = (p >= 0) ? (int)((kBandJ >> (8 * p)) & 0xFFu) : 0;
+    return (j == 0u || (int)j <= J) ? k : k + 1;
+}
+
+// exact 2^e as float, e in [-149, 127]
+OZK_DEV float pow2f(int e) {
+    return (e >= -126) ? __uint_as_float((uint32_t)(e + 127) << 23)
+                       : __uint_as_float(1u << (e + 149));
+}
+
+// exact 2^e as double, e in [-1022, 1023]
+OZK_DEV double pow2d(int e) {
+    return __longlong_as_double((long long)(e + 1023) << 52);
+}
+
+// q = src / s with s = 2^(E - alpha), computed as an exact scaling.  For fp64
+// the factor 2^(alpha - E) is always a normal double and the product is the
+// correctly rounded quotient.  For fp32: when alpha - E > 0 the scaling is up
+// and exact, done in two normal steps if the factor exceeds 2^64; when
+// alpha - E <= 0 the factor is >= 2^-127 (a normal or subnormal float) and one
+// IEEE multiply gives the correctly rounded quotient.
+struct ScaleF64 {
+    double inv;
+    OZK_DEV double apply(double x) const { return x * inv; }
+};
+struct ScaleF32 {
+    float inv_a, inv_b;
+    bool two;
+    OZK_DEV float apply(float x) const { return two ? (x * inv_a) * inv_b : x * inv_a; }
+};
+OZK_DEV ScaleF64 make_scale_f64(int e_minus_alpha) {
+    ScaleF64 s;
+    s.inv = pow2d(-e_minus_alpha);
+    return s;
+}
+OZK_DEV ScaleF32 make_scale_f32(int e_minus_alpha) {
+    ScaleF32 s;
+    int up = -e_minus_alpha;
+    if (up > 64) {
+        s.two = true;
+        s.inv_a = pow2f(64);
+        s.inv_b = pow2f(up - 64);
+    } else {
+        s.two = false;
+        s.inv_a = pow2f(up);
+        s.inv_b = 1.0f;
+    }
+    return s;
+}
+
+// int8 slice of ozaki_triton.py:199-200 in the residual dtype R:
+// t = fl_R(q + 0.5) if q >= 0 else fl_R(q - 0.5); clamp to [-128, 127];
+// convert toward zero.
+OZK_DEV int quant_i8(double q) {
+    double t = (q >= 0.0) ? q + 0.5 : q - 0.5;
+    t = fmin(fmax(t, -128.0), 127.0);
+    return (int)t;
+}
+OZK_DEV int quant_i8(float q) {
+    float t = (q >= 0.0f) ? q + 0.5f : q - 0.5f;
+    t = fminf(fmaxf(t, -128.0f), 127.0f);
+    return (int)t;
+}
+
+// Single round-to-nearest-even conversions to binary16 (bit patterns), written
+// with integer arithmetic so the result does not depend on the denormal mode.
+OZK_DEV uint32_t f64_to_f16_bits(double x) {
+    uint64_t u = (uint64_t)__double_as_longlong(x);
+    uint32_t s = (uint32_t)((u >> 48) & 0x8000u);
+    int be = (int)((u >> 52) & 0x7FF);
+    uint64_t m = u & 0xFFFFFFFFFFFFFull;
+    if (be == 0x7FF) return s | (m ? 0x7E00u : 0x7C00u);
+    if (be == 0) return s;
+    uint64_t sig = (1ull << 52) | m;
+    int e = be - 1023;
+    int qe = (e < -14 ? -14 : e) - 10;
+    int shift = qe - (e - 52);
+    if (shift > 63) return s;
+    uint64_t n = sig >> shift;
+    uint64_t rem = sig & ((1ull << shift) - 1ull);
+    uint64_t half = 1ull << (shift - 1);
+    if (rem > half || (rem == half && (n & 1ull))) ++n;
+    uint32_t b = (e <= -14) ? (uint32_t)n : (uint32_t)(((e + 14) << 10) + (int)n);
+    if (b >= 0x7C00u) b = 0x7C00u;
+    return s | b;
+}
+OZK_DEV uint32_t f32_to_f16_bits(float x) {
+    uint32_t u = __float_as_uint(x);
+    uint32_t s = (u >> 16) & 0x8000u;
+    int be = (int)((u >> 23) & 0xFFu);
+    uint32_t m = u & 0x7FFFFFu;
+    if (be == 0xFF) return s | (m ? 0x7E00u : 0x7C00u);
+    if (be == 0) return s;
+    uint32_t sig = (1u << 23) | m;
+    int e = be - 127;
+    int qe = (e < -14 ? -14 : e) - 10;
+    int shift = qe - (e - 23);          // >= 13
+    if (shift > 24) return s;           // |x| < 2^(qe-1): rounds to 0
+    uint32_t n = sig >> shift;
+    uint32_t rem = sig & ((1u << shift) - 1u);
+    uint32_t half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (n & 1u))) ++n;
+    uint32_t b = (e <= -14) ? n : (uint32_t)(((e + 14) << 10) + (int)n);
+    if (b >= 0x7C00u) b = 0x7C00u;
+    return s | b;
+}
+// exact binary16 -> binary32 (every binary16 value is a binary32 value)
+OZK_DEV float f16_bits_to_f32(uint32_t h) {
+    uint32_t s = (h & 0x8000u) << 16;
+    uint32_t be = (h >> 10) & 0x1Fu;
+    uint32_t m = h & 0x3FFu;
+    if (be == 0x1F) return __uint_as_float(s | 0x7F800000u | (m << 13));
+    if (be == 0) {
+        // subnormal: m * 2^-24, exact in binary32
+        float v = (float)m * 5.9604644775390625e-08f;
+        return s ? -v : v;
+    }
+    return __uint_as_float(s | ((be + 112u) << 23) | (m << 13));
+}
+
+}  // namespace ozk

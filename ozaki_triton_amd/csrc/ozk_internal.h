@@ -1,0 +1,75 @@
+// ozk_internal.h -- parameter blocks and launchers shared between the C ABI
+// layer (ozk_api.cpp) and the kernel translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace ozk {
+
+// One split launch: X [batch, rows, K] -> slices [batch, L, rows, K] and
+// scales [batch, L, rows].  All strides in elements.
+struct SplitParams {
+    const void *X;
+    int64_t batch, rows, K;
+    int64_t xs_b, xs_r, xs_k;
+    int L, alpha;
+    void *slices;
+    int64_t ss_b, ss_l, ss_r, ss_k;
+    float *scales;
+    int64_t cs_b, cs_l, cs_r;
+    float *resid;  // generic path only: fp32 residual [batch, rows, K]
+};
+
+enum SplitPath { kSplitRows = 0, kSplitStrip = 1, kSplitGeneric = 2 };
+
+// Chooses the split kernel for p (x_dtype: 0 = f64, 1 = f32; slice: 4 = i8,
+// 2 = f16).  Returns the path and, for the resident paths, the variant index.
+struct SplitPlan {
+    SplitPath path;
+    int variant;
+};
+SplitPlan plan_split(const SplitParams &p, int x_dtype, int slice_dtype);
+hipError_t launch_split(const SplitParams &p, const SplitPlan &plan, int x_dtype,
+                        int slice_dtype, hipStream_t stream);
+
+// One cross-GEMM launch.  A slices [batch, L, M, K] and B slices presented as
+// [batch, L, N, K] (K-contiguous rows of B^T).  Strides in elements of the
+// slice dtype; scales and C strides in their own elements.
+struct GemmParams {
+    const void *A;
+    const void *B;
+    int64_t as_b, as_l, as_m;   // A: k stride is 1
+    int64_t bs_b, bs_l, bs_n;   // B^T: k stride is 1
+    const float *sa;
+    const float *sb;
+    int64_t sas_b, sas_l, sas_m;
+    int64_t sbs_b, sbs_l, sbs_n;
+    void *C;
+    int64_t cs_b, cs_m, cs_n;
+    int64_t batch, M, N, K;
+};
+
+struct GemmPlan {
+    int mi, ni;       // wave tile = (32*mi) x (32*ni), workgroup tile = 2x2 waves
+    int group_m;      // tile-row group for L2 reuse
+};
+GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype);
+hipError_t launch_gemm(const GemmParams &p, const GemmPlan &plan, int L, int slice_dtype,
+                       int out_dtype, hipStream_t stream);
+
+hipError_t launch_zero_c(const GemmParams &p, int out_dtype, hipStream_t stream);
+
+// Packs slices [batch, L, rows, K] (any strides) into a K-contiguous buffer
+// [batch, L, rows, Kp] with Kp = K rounded up to 16 bytes and zero padding.
+struct PackParams {
+    const void *src;
+    int64_t s_b, s_l, s_r, s_k;
+    void *dst;
+    int64_t batch, L, rows, K, Kp;
+    int esize;
+};
+hipError_t launch_pack(const PackParams &p, hipStream_t stream);
+
+}  // namespace ozk

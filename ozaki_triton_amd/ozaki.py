@@ -1,0 +1,379 @@
+"""Ozaki-scheme matmul on MI355X: host side of the hot path.
+
+Public API mirrors /root/reference/ozaki_triton.py (same names, arguments,
+dtype policy and assertion messages):
+
+* ``compute_split_bits(n, slice_dtype, dot_accum_dtype)``   ozaki_triton.py:76-98
+* ``split_matrix(A, num_splits, alpha, slice_dtype)``        ozaki_triton.py:214-256
+* ``cross_gemm(A_slices, B_slices, A_scales, B_scales, num_splits, output_dtype)``
+                                                             ozaki_triton.py:455-498
+* ``ozaki_matmul(A, B, num_splits=3, slice_dtype=torch.float16, verbose=False)``
+                                                             ozaki_triton.py:534-606
+
+All arithmetic runs in the HIP kernels of libozaki_amd.so, called through the C
+ABI of include/ozaki_amd.h.  Tensors must live on a ROCm GPU; there is no CPU
+path.  Supported dtype combinations: input float64 / float32 with int8 or
+float16 slices (the others the reference accepts raise NotImplementedError).
+
+Differences from the reference that do not change any value:
+* both splits run on the caller's current stream (the reference's two side
+  streams, ozaki_triton.py:588-601, race with the .contiguous() copy on the
+  main stream and buy nothing for kernels that each saturate HBM);
+* a batch-broadcast operand (torch.matmul semantics, ozaki_triton.py:504-531)
+  is split once and read with batch stride 0 instead of being copied and split
+  once per batch;
+* operands whose last two dims are row- or column-contiguous are read in place
+  (the split kernels take strides), other layouts are made contiguous first.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+
+# ============================================================
+# 0. dtype policy (ozaki_triton.py:31-98)
+# ============================================================
+
+# slice dtype -> (mantissa bits, is integer)   ozaki_triton.py:36-41
+_SLICE_DTYPE_INFO = {
+    torch.float32: (23, False),
+    torch.float16: (10, False),
+    torch.bfloat16: (7, False),
+    torch.int8: (7, True),
+}
+
+# accepted input dtypes   ozaki_triton.py:43-49
+_INPUT_DTYPES = {
+    torch.float64,
+    torch.float32,
+    torch.float16,
+    torch.bfloat16,
+    torch.int8,
+}
+
+# combinations the HIP kernels implement
+_SUPPORTED_INPUTS = (torch.float64, torch.float32)
+_SUPPORTED_SLICES = (torch.int8, torch.float16)
+
+_TORCH_TO_OZK = {
+    torch.float64: _lib.OZK_F64,
+    torch.float32: _lib.OZK_F32,
+    torch.float16: _lib.OZK_F16,
+    torch.bfloat16: _lib.OZK_BF16,
+    torch.int8: _lib.OZK_I8,
+    torch.int32: _lib.OZK_I32,
+}
+
+
+def _select_dot_accum_dtype(slice_dtype: torch.dtype) -> torch.dtype:
+    """Dot-product accumulator of one slice pair (ozaki_triton.py:62-66)."""
+    if slice_dtype == torch.int8:
+        return torch.int32
+    return torch.float32
+
+
+def _select_out_accum_dtype(input_dtype: torch.dtype) -> torch.dtype:
+    """Outer accumulator over slice pairs, also the residual compute dtype
+    (ozaki_triton.py:69-73, 227)."""
+    if input_dtype == torch.float64:
+        return torch.float64
+    return torch.float32
+
+
+def compute_split_bits(n: int, slice_dtype: torch.dtype = torch.float16,
+                       dot_accum_dtype: torch.dtype = torch.float32) -> int:
+    """alpha = min(int((acc_bits - log2 n) / 2), slice_bits) (ozaki_triton.py:76-98),
+    evaluated by ozk_compute_split_bits."""
+    if dot_accum_dtype not in (torch.int32, torch.float32):
+        raise ValueError(f"unsupported dot_accum_dtype: {dot_accum_dtype}")
+    _SLICE_DTYPE_INFO[slice_dtype]  # KeyError for an unknown slice dtype, as the reference
+    if n <= 0:
+        math.log2(n)  # ValueError: math domain error, as the reference for n == 0
+    alpha = ctypes.c_int(0)
+    st = _lib.load().ozk_compute_split_bits(int(n), _TORCH_TO_OZK[slice_dtype],
+                                            _TORCH_TO_OZK[dot_accum_dtype], ctypes.byref(alpha))
+    if st not in (_lib.OZK_OK, _lib.OZK_ERR_ALPHA):
+        _lib.check("ozk_compute_split_bits", st)
+    alpha = int(alpha.value)
+    assert alpha >= 1, f"n={n} 太大, 无法安全分片 (alpha={alpha})"
+    return alpha
+
+
+# ============================================================
+# helpers
+# ============================================================
+
+def _require_gpu(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if not t.is_cuda:
+            raise RuntimeError(
+                "ozaki_triton_amd runs only on a ROCm GPU device (got a tensor on "
+                f"{t.device}); there is no CPU path")
+
+
+def _require_supported(input_dtype: torch.dtype, slice_dtype: torch.dtype) -> None:
+    if input_dtype not in _SUPPORTED_INPUTS or slice_dtype not in _SUPPORTED_SLICES:
+        raise NotImplementedError(
+            f"input {input_dtype} with {slice_dtype} slices is not implemented by the "
+            "MI355X kernels (supported: float64/float32 inputs, int8/float16 slices)")
+
+
+def _stream(dev: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _workspace(nbytes: int, dev: torch.device):
+    if nbytes == 0:
+        return None, ctypes.c_void_p(0)
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    return buf, ctypes.c_void_p(buf.data_ptr())
+
+
+# ============================================================
+# 1. split (ozaki_triton.py:214-256)
+# ============================================================
+
+def _split_into(A: torch.Tensor, num_splits: int, alpha: int, slice_dtype: torch.dtype,
+                slices: torch.Tensor, scales: torch.Tensor) -> None:
+    """Launch ozk_split for A [B, rows, K] (any strides) into preallocated
+    slices [B, L, rows, K] and scales [B, L, rows]."""
+    L = _lib.load()
+    Bn, M, K = A.shape
+    xd = _TORCH_TO_OZK[A.dtype]
+    sd = _TORCH_TO_OZK[slice_dtype]
+    xs = _lib.i64arr(A.stride())
+    ss = _lib.i64arr(slices.stride())
+    cs = _lib.i64arr(scales.stride())
+    nbytes = ctypes.c_size_t(0)
+    _lib.check("ozk_split_workspace_bytes",
+               L.ozk_split_workspace_bytes(xd, Bn, M, K, xs, num_splits, sd, ss,
+                                           ctypes.byref(nbytes)))
+    ws, wsp = _workspace(int(nbytes.value), A.device)
+    with torch.cuda.device(A.device):
+        st = L.ozk_split(ctypes.c_void_p(A.data_ptr()), xd, Bn, M, K, xs, num_splits, alpha, sd,
+                         ctypes.c_void_p(slices.data_ptr()), ss,
+                         ctypes.c_void_p(scales.data_ptr()), cs, wsp, nbytes.value,
+                         _stream(A.device))
+    _lib.check("ozk_split", st)
+    if ws is not None:
+        ws.record_stream(torch.cuda.current_stream(A.device))
+
+
+def split_matrix(A: torch.Tensor, num_splits: int, alpha: int, slice_dtype: torch.dtype):
+    """
+    Args:
+        A: (B, M, K) float64 / float32 on a ROCm GPU
+        num_splits: number of slices
+        alpha: mantissa bits per slice (compute_split_bits)
+    Returns:
+        slices: (B, num_splits, M, K), dtype=slice_dtype
+        scales: (B, num_splits, M), dtype=float32, powers of two
+    """
+    assert A.dim() == 3
+    B, M, K = A.shape
+    _require_gpu(A)
+    _require_supported(A.dtype, slice_dtype)
+    slices = torch.empty((B, num_splits, M, K), dtype=slice_dtype, device=A.device)
+    scales = torch.empty((B, num_splits, M), dtype=torch.float32, device=A.device)
+    _split_into(A, num_splits, alpha, slice_dtype, slices, scales)
+    return slices, scales
+
+
+# ============================================================
+# 2. cross-GEMM (ozaki_triton.py:455-498)
+# ============================================================
+
+def _batch_strides(t: torch.Tensor, BN: int):
+    """Strides of a 4-D/3-D tensor with a batch dim of 1 broadcast to BN."""
+    st = list(t.stride())
+    if t.shape[0] == 1 and BN != 1:
+        st[0] = 0
+    elif t.shape[0] != BN:
+        raise AssertionError(f"batch mismatch: {t.shape[0]} vs {BN}")
+    return st
+
+
+def cross_gemm(A_slices, B_slices, A_scales, B_scales, num_splits, output_dtype):
+    """
+    C = sum_{i,j} scale_A_i * scale_B_j * (A_slice_i @ B_slice_j)
+    Args:
+        A_slices: (B, num_splits, M, K), slice dtype
+        B_slices: (B, num_splits, K, N), same dtype (any strides; a batch of 1
+                  is broadcast)
+        A_scales: (B, num_splits, M), float32
+        B_scales: (B, num_splits, N), float32 (a batch of 1 is broadcast)
+        num_splits: number of slices
+        output_dtype: dtype of C (the original input dtype)
+    Returns:
+        C: (B, M, N), dtype=output_dtype
+    """
+    assert A_slices.dim() == 4 and B_slices.dim() == 4
+    BN, _, M, K = A_slices.shape
+    _, _, K2, N = B_slices.shape
+    assert K == K2
+    slice_dtype = A_slices.dtype
+    _require_gpu(A_slices, B_slices, A_scales, B_scales)
+    _require_supported(output_dtype, slice_dtype)
+    if B_slices.dtype != slice_dtype:
+        raise AssertionError(f"slice dtype mismatch: {slice_dtype} vs {B_slices.dtype}")
+    C = torch.empty((BN, M, N), dtype=output_dtype, device=A_slices.device)
+    _cross_gemm_into(A_slices, B_slices, A_scales, B_scales, num_splits, C)
+    return C
+
+
+def _cross_gemm_into(A_slices, B_slices, A_scales, B_scales, num_splits, C) -> None:
+    L = _lib.load()
+    BN, _, M, K = A_slices.shape
+    N = B_slices.shape[-1]
+    sd = _TORCH_TO_OZK[A_slices.dtype]
+    od = _TORCH_TO_OZK[C.dtype]
+    a_st = _lib.i64arr(_batch_strides(A_slices, BN))
+    b_st = _lib.i64arr(_batch_strides(B_slices, BN))
+    sa_st = _lib.i64arr(_batch_strides(A_scales, BN))
+    sb_st = _lib.i64arr(_batch_strides(B_scales, BN))
+    c_st = _lib.i64arr(C.stride())
+    nbytes = ctypes.c_size_t(0)
+    ap = ctypes.c_void_p(A_slices.data_ptr())
+    bp = ctypes.c_void_p(B_slices.data_ptr())
+    _lib.check("ozk_cross_gemm_workspace_bytes",
+               L.ozk_cross_gemm_workspace_bytes(BN, M, N, K, num_splits, sd, ap, a_st, bp, b_st,
+                                                ctypes.byref(nbytes)))
+    ws, wsp = _workspace(int(nbytes.value), C.device)
+    with torch.cuda.device(C.device):
+        st = L.ozk_cross_gemm(ap, a_st, bp, b_st, ctypes.c_void_p(A_scales.data_ptr()), sa_st,
+                              ctypes.c_void_p(B_scales.data_ptr()), sb_st, BN, M, N, K,
+                              num_splits, sd, ctypes.c_void_p(C.data_ptr()), od, c_st, wsp,
+                              nbytes.value, _stream(C.device))
+    _lib.check("ozk_cross_gemm", st)
+    if ws is not None:
+        ws.record_stream(torch.cuda.current_stream(C.device))
+
+
+# ============================================================
+# 3. ozaki_matmul (ozaki_triton.py:500-606)
+# ============================================================
+
+def _last2_ok(t: torch.Tensor) -> bool:
+    """True when the kernels can read t's last two dims in place."""
+    return t.stride(-1) == 1 or t.stride(-2) == 1
+
+
+def _canonicalize_batch(A, B):
+    """Broadcast the batch dims of A (..., M, K) and B (..., K, N) like
+    torch.matmul and flatten them (ozaki_triton.py:504-531).
+
+    Returns A3 (BN_A, M, K), B3 (BN_B, K, N) and the batch shape, where BN_A
+    and BN_B are either BN or 1: an operand whose batch is a pure broadcast is
+    returned with a batch of 1 (split once, read with stride 0).
+    """
+    assert A.dim() >= 2 and B.dim() >= 2
+    M, K = A.shape[-2:]
+    K2, N = B.shape[-2:]
+    assert K == K2, f"contraction dim mismatch: A K={K}, B K={K2}"
+
+    batch_shape = torch.broadcast_shapes(A.shape[:-2], B.shape[:-2])
+    BN = math.prod(batch_shape)
+
+    def flat(T, rows, cols):
+        if math.prod(T.shape[:-2]) == 1:
+            T3 = T.reshape(1, rows, cols)
+        else:
+            T3 = T.expand(*batch_shape, rows, cols).reshape(BN, rows, cols)
+        if not _last2_ok(T3):
+            T3 = T3.contiguous()
+        return T3
+
+    return flat(A, M, K), flat(B, K, N), batch_shape
+
+
+def ozaki_matmul(
+    A: torch.Tensor,
+    B: torch.Tensor,
+    num_splits: int = 3,
+    slice_dtype: torch.dtype = torch.float16,
+    verbose: bool = False,
+) -> torch.Tensor:
+    """Ozaki-scheme C = A @ B (ozaki_triton.py:534-606); see _ozaki_matmul_impl."""
+    return _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, None)
+
+
+def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, mark):
+    """
+    Ozaki-scheme matrix product C = A @ B with torch.matmul batch broadcasting.
+
+    1. Split: A into num_splits (slice, per-row scale) pairs, B likewise per
+       column (through B^T).
+    2. Compute & sum: all num_splits^2 slice products with the scaled outer
+       accumulation fused in one MFMA kernel.
+
+    Args:
+        A: (..., M, K) float64 / float32 on a ROCm GPU
+        B: (..., K, N), same dtype as A
+        num_splits: number of slices (<= 4)
+        slice_dtype: torch.int8 or torch.float16
+        verbose: print the chosen parameters
+
+    Returns:
+        C: (broadcast(...), M, N), dtype of A
+
+    ``mark`` (internal, used by bench.py) is called with a phase name
+    ("split_b", "split_a", "cross_gemm", "end") just before each phase is
+    enqueued, so a caller can record stream events between them.
+    """
+    assert A.dtype == B.dtype, f"A/B dtype mismatch: {A.dtype} vs {B.dtype}"
+    assert A.dtype in _INPUT_DTYPES, f"unsupported input dtype: {A.dtype}"
+    assert slice_dtype in _SLICE_DTYPE_INFO, f"unsupported slice dtype: {slice_dtype}"
+    assert num_splits <= 4, f"num_splits must be <= 4, got {num_splits}"
+
+    input_dtype = A.dtype
+    dot_accum_dtype = _select_dot_accum_dtype(slice_dtype)
+    out_accum_dtype = _select_out_accum_dtype(input_dtype)
+
+    M, K = A.shape[-2:]
+    N = B.shape[-1]
+
+    A3, B3, batch_shape = _canonicalize_batch(A, B)
+    BN = math.prod(batch_shape)
+    out_shape = (*batch_shape, M, N)
+
+    if BN == 0:
+        return torch.empty(out_shape, dtype=input_dtype, device=A.device)
+
+    alpha = compute_split_bits(K, slice_dtype=slice_dtype, dot_accum_dtype=dot_accum_dtype)
+    if verbose:
+        print(f"[Ozaki] batch={batch_shape}, M={M}, K={K}, N={N}, "
+              f"input={input_dtype}, slice={slice_dtype}, "
+              f"dot_accum={dot_accum_dtype}, out_accum={out_accum_dtype}, "
+              f"splits={num_splits}, alpha={alpha}")
+
+    _require_gpu(A, B)
+    _require_supported(input_dtype, slice_dtype)
+    dev = A.device
+
+    # 2. split: B through its transposed view, so B slices come out [.., N, K]
+    #    (K-contiguous), the layout the MFMA kernel reads
+    if mark:
+        mark("split_b")
+    B_T = B3.transpose(-1, -2)
+    B_slices_T = torch.empty((B3.shape[0], num_splits, N, K), dtype=slice_dtype, device=dev)
+    B_scales = torch.empty((B3.shape[0], num_splits, N), dtype=torch.float32, device=dev)
+    _split_into(B_T, num_splits, alpha, slice_dtype, B_slices_T, B_scales)
+    if mark:
+        mark("split_a")
+    A_slices = torch.empty((A3.shape[0], num_splits, M, K), dtype=slice_dtype, device=dev)
+    A_scales = torch.empty((A3.shape[0], num_splits, M), dtype=torch.float32, device=dev)
+    _split_into(A3, num_splits, alpha, slice_dtype, A_slices, A_scales)
+    B_slices = B_slices_T.transpose(-1, -2)
+
+    # 3. fused cross-GEMM
+    C = torch.empty((BN, M, N), dtype=input_dtype, device=dev)
+    if mark:
+        mark("cross_gemm")
+    _cross_gemm_into(A_slices, B_slices, A_scales, B_scales, num_splits, C)
+    if mark:
+        mark("end")
+    return C.view(out_shape)

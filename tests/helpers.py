@@ -1,0 +1,74 @@
+"""Shared helpers for the parity tests (test infrastructure only)."""
+import numpy as np
+import torch
+
+NP_OF = {torch.float64: np.float64, torch.float32: np.float32, torch.int8: np.int8,
+         torch.float16: np.float16}
+NAME_OF = {torch.int8: "int8", torch.float16: "float16", torch.float64: "float64",
+           torch.float32: "float32"}
+
+
+def to_np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().numpy()
+
+
+def oracle_split_batched(oracle, X3: np.ndarray, L: int, alpha: int, slice_dtype):
+    """Oracle split of every batch of X3 [B, rows, K] (any strides)."""
+    sl, sc = [], []
+    for b in range(X3.shape[0]):
+        s, c = oracle.split(X3[b], L, alpha, NAME_OF.get(slice_dtype, slice_dtype))
+        sl.append(s)
+        sc.append(c)
+    return np.stack(sl), np.stack(sc)
+
+
+def bits(a: np.ndarray) -> np.ndarray:
+    """View an array's bytes as unsigned ints (bitwise comparison, -0 != +0)."""
+    a = np.ascontiguousarray(a)
+    return a.view({1: np.uint8, 2: np.uint16, 4: np.uint32, 8: np.uint64}[a.itemsize])
+
+
+def assert_bitwise_equal(got: np.ndarray, want: np.ndarray, what: str = ""):
+    assert got.shape == want.shape, (what, got.shape, want.shape)
+    gb, wb = bits(got), bits(want)
+    if not np.array_equal(gb, wb):
+        idx = np.argwhere(gb != wb)
+        first = tuple(idx[0])
+        raise AssertionError(
+            f"{what}: {len(idx)} of {got.size} elements differ; first at {first}: "
+            f"got {got[first]!r} want {want[first]!r}")
+
+
+def fp16_cross_bound(oracle_np, A_sl, B_slT, sa, sb):
+    """Error bound for a GPU fp16-slice cross-GEMM against the oracle's (binary64
+    accumulated) result, per output element:
+        sum_ij sa_i sb_j gamma_{K+2} (|A_i| |B_j|^T)  (fp32 dot of K products,
+        the fl32 of the accumulator and of the scaled term)
+    with gamma_n = n u / (1 - n u), u = 2^-24, plus the rounding of the outer
+    accumulation (L^2 terms)."""
+    L, M, K = A_sl.shape
+    u = 2.0 ** -24
+    g = (K + 2) * u / (1 - (K + 2) * u)
+    Aa = np.abs(A_sl.astype(np.float64))
+    Ba = np.abs(B_slT.astype(np.float64))
+    bound = np.zeros((M, B_slT.shape[1]))
+    mag = np.zeros_like(bound)
+    for i in range(L):
+        for j in range(L):
+            t = (Aa[i] @ Ba[j].T) * sa[i][:, None].astype(np.float64) * sb[j][None, :].astype(np.float64)
+            bound += g * t
+            mag += t
+    return bound + 2 * L * L * u * mag
+
+
+def c3_like(shape_a, shape_b, seed, dtype=torch.float64, exp_range=8):
+    """Inputs of BASELINE config 3's distribution: N(0,1) * 2^e with e drawn per
+    row of A / per column of B from Uniform-int[-exp_range, exp_range]."""
+    g = torch.Generator().manual_seed(seed)
+    A = torch.randn(*shape_a, generator=g, dtype=torch.float64)
+    B = torch.randn(*shape_b, generator=g, dtype=torch.float64)
+    ea = torch.randint(-exp_range, exp_range + 1, (*shape_a[:-1], 1), generator=g)
+    eb = torch.randint(-exp_range, exp_range + 1, (*shape_b[:-2], 1, shape_b[-1]), generator=g)
+    A = A * torch.pow(2.0, ea.double())
+    B = B * torch.pow(2.0, eb.double())
+    return A.to(dtype), B.to(dtype)

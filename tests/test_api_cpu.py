@@ -1,0 +1,212 @@
+"""Host-side tests (no GPU): the C ABI loads and exports every declared
+symbol, its argument checks return the documented codes without touching a
+device, and the Python API keeps the reference's assertions and messages."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_symbols():
+    with open(os.path.join(ROOT, "include", "ozaki_amd.h")) as f:
+        text = f.read()
+    return sorted(set(re.findall(r"^\w[\w\s\*]*?\b(ozk_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    from ozaki_triton_amd import _lib
+    L = _lib.load()
+    declared = _declared_symbols()
+    assert declared == sorted(_lib.EXPORTED)
+    for name in declared:
+        assert hasattr(L, name), name
+    assert L.ozk_version() >= 100
+
+
+def test_strerror_names_every_code():
+    from ozaki_triton_amd import _lib
+    for code in range(0, -9, -1):
+        assert _lib.strerror(code) != "unknown status"
+    assert _lib.strerror(-99) == "unknown status"
+
+
+def test_compute_split_bits_abi_matches_python_formula():
+    import math
+    from ozaki_triton_amd import _lib
+    L = _lib.load()
+    out = ctypes.c_int(0)
+    for acc, acc_bits in ((_lib.OZK_I32, 31), (_lib.OZK_F32, 23)):
+        for sd, sbits in ((_lib.OZK_I8, 7), (_lib.OZK_F16, 10), (_lib.OZK_BF16, 7),
+                          (_lib.OZK_F32, 23)):
+            for n in [1, 2, 3, 100, 255, 256, 4096, 8192, 65536, 1 << 20, (1 << 21) + 1,
+                      1 << 28, 1 << 30]:
+                st = L.ozk_compute_split_bits(n, sd, acc, ctypes.byref(out))
+                want = min(int((acc_bits - math.log2(n)) / 2), sbits)
+                assert out.value == want
+                assert st == (_lib.OZK_OK if want >= 1 else _lib.OZK_ERR_ALPHA)
+    assert L.ozk_compute_split_bits(8, _lib.OZK_I8, _lib.OZK_F64, ctypes.byref(out)) == \
+        _lib.OZK_ERR_ACCUM
+    assert L.ozk_compute_split_bits(0, _lib.OZK_I8, _lib.OZK_I32, ctypes.byref(out)) == \
+        _lib.OZK_ERR_SHAPE
+
+
+def test_split_abi_rejects_bad_arguments_on_host():
+    from ozaki_triton_amd import _lib
+    L = _lib.load()
+    s3 = _lib.i64arr([6, 3, 1])
+    s4 = _lib.i64arr([12, 6, 3, 1])
+    p = ctypes.c_void_p(0x1000)
+    null = ctypes.c_void_p(0)
+
+    def call(**kw):
+        a = dict(X=p, xd=_lib.OZK_F64, B=1, R=2, K=3, L=2, alpha=7, sd=_lib.OZK_I8, S=p, C=p,
+                 ws=null, wsb=0)
+        a.update(kw)
+        return L.ozk_split(a["X"], a["xd"], a["B"], a["R"], a["K"], s3, a["L"], a["alpha"],
+                           a["sd"], a["S"], s4, a["C"], s3, a["ws"], a["wsb"], null)
+
+    assert call(xd=_lib.OZK_F16) == _lib.OZK_ERR_DTYPE
+    assert call(sd=_lib.OZK_BF16) == _lib.OZK_ERR_DTYPE
+    assert call(L=5) == _lib.OZK_ERR_SPLITS
+    assert call(L=-1) == _lib.OZK_ERR_SPLITS
+    assert call(K=-1) == _lib.OZK_ERR_SHAPE
+    assert call(alpha=0) == _lib.OZK_ERR_ALPHA
+    assert call(X=null) == _lib.OZK_ERR_NULL
+    # nothing to do: returns OK without any device call
+    assert call(B=0) == _lib.OZK_OK
+    assert call(L=0) == _lib.OZK_OK
+    # the generic (strided) path needs a residual workspace
+    nb = ctypes.c_size_t(0)
+    xs_bad = _lib.i64arr([6, 3, 2])
+    assert L.ozk_split_workspace_bytes(_lib.OZK_F64, 1, 2, 3, xs_bad, 2, _lib.OZK_I8, s4,
+                                       ctypes.byref(nb)) == 0
+    assert nb.value == 1 * 2 * 3 * 4
+    assert L.ozk_split(p, _lib.OZK_F64, 1, 2, 3, xs_bad, 2, 7, _lib.OZK_I8, p, s4, p, s3, null,
+                       0, null) == _lib.OZK_ERR_WORKSPACE
+
+
+def test_split_workspace_zero_on_resident_paths():
+    from ozaki_triton_amd import _lib
+    L = _lib.load()
+    nb = ctypes.c_size_t(123)
+    K, M, N = 8192, 8192, 8192
+    sl = _lib.i64arr([4 * M * K, M * K, K, 1])
+    # A rows (K-contiguous)
+    assert L.ozk_split_workspace_bytes(_lib.OZK_F64, 1, M, K, _lib.i64arr([M * K, K, 1]), 4,
+                                       _lib.OZK_I8, sl, ctypes.byref(nb)) == 0
+    assert nb.value == 0
+    # B^T view (rows contiguous)
+    assert L.ozk_split_workspace_bytes(_lib.OZK_F64, 1, N, K, _lib.i64arr([K * N, 1, N]), 4,
+                                       _lib.OZK_I8, sl, ctypes.byref(nb)) == 0
+    assert nb.value == 0
+
+
+def test_cross_gemm_abi_checks_and_workspace():
+    from ozaki_triton_amd import _lib
+    L = _lib.load()
+    nb = ctypes.c_size_t(0)
+    p = ctypes.c_void_p(0x1000)
+    null = ctypes.c_void_p(0)
+    M, N, K, Ls = 64, 48, 256, 3
+    a = _lib.i64arr([Ls * M * K, M * K, K, 1])
+    b_kcontig = _lib.i64arr([Ls * N * K, N * K, 1, K])
+    b_ncontig = _lib.i64arr([Ls * N * K, N * K, N, 1])
+    assert L.ozk_cross_gemm_workspace_bytes(1, M, N, K, Ls, _lib.OZK_I8, p, a, p, b_kcontig,
+                                            ctypes.byref(nb)) == 0
+    assert nb.value == 0
+    assert L.ozk_cross_gemm_workspace_bytes(1, M, N, K, Ls, _lib.OZK_I8, p, a, p, b_ncontig,
+                                            ctypes.byref(nb)) == 0
+    assert nb.value == Ls * N * K
+    s3 = _lib.i64arr([M * N, N, 1])
+    sc = _lib.i64arr([Ls * M, M, 1])
+
+    def call(**kw):
+        d = dict(L=Ls, sd=_lib.OZK_I8, od=_lib.OZK_F64, B=1, K=K, C=p, b=b_kcontig, ws=null,
+                 wsb=0)
+        d.update(kw)
+        return L.ozk_cross_gemm(p, a, p, d["b"], p, sc, p, sc, d["B"], M, N, d["K"], d["L"],
+                                d["sd"], d["C"], d["od"], s3, d["ws"], d["wsb"], null)
+
+    assert call(sd=_lib.OZK_F32) == _lib.OZK_ERR_DTYPE
+    assert call(od=_lib.OZK_F16) == _lib.OZK_ERR_DTYPE
+    assert call(L=5) == _lib.OZK_ERR_SPLITS
+    assert call(K=-3) == _lib.OZK_ERR_SHAPE
+    assert call(C=null) == _lib.OZK_ERR_NULL
+    assert call(b=b_ncontig) == _lib.OZK_ERR_WORKSPACE
+    assert call(B=0) == _lib.OZK_OK
+
+
+# --------------------------------------------------------------------------- #
+# Python API: the reference's checks and messages (ozaki_triton.py:97,560-563)
+# --------------------------------------------------------------------------- #
+def test_ozaki_matmul_assertions():
+    import ozaki_triton_amd as ozk
+    a64 = torch.zeros(4, 8, dtype=torch.float64)
+    a32 = torch.zeros(8, 4, dtype=torch.float32)
+    with pytest.raises(AssertionError, match="A/B dtype mismatch"):
+        ozk.ozaki_matmul(a64, a32)
+    with pytest.raises(AssertionError, match="unsupported input dtype"):
+        ozk.ozaki_matmul(a64.to(torch.int32), a64.to(torch.int32))
+    with pytest.raises(AssertionError, match="unsupported slice dtype"):
+        ozk.ozaki_matmul(a64, a64.T, slice_dtype=torch.float64)
+    with pytest.raises(AssertionError, match="num_splits must be <= 4, got 5"):
+        ozk.ozaki_matmul(a64, a64.T, num_splits=5)
+    with pytest.raises(AssertionError, match="contraction dim mismatch: A K=8, B K=4"):
+        ozk.ozaki_matmul(a64, a64)
+    # a 1-D operand fails unpacking A.shape[-2:] before any assert, as in the
+    # reference (ozaki_triton.py:569)
+    with pytest.raises(ValueError):
+        ozk.ozaki_matmul(torch.zeros(4, dtype=torch.float64), a64)
+
+
+def test_ozaki_matmul_refuses_cpu_tensors():
+    import ozaki_triton_amd as ozk
+    a = torch.zeros(4, 8, dtype=torch.float64)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        ozk.ozaki_matmul(a, a.T, 2, torch.int8)
+
+
+def test_unsupported_combinations_raise():
+    import ozaki_triton_amd as ozk
+    from ozaki_triton_amd.ozaki import _require_supported
+    with pytest.raises(NotImplementedError):
+        _require_supported(torch.bfloat16, torch.float32)
+    with pytest.raises(NotImplementedError):
+        _require_supported(torch.float64, torch.bfloat16)
+    _require_supported(torch.float64, torch.int8)
+    assert ozk.compute_split_bits(8192, torch.int8, torch.int32) == 7
+
+
+def test_compute_split_bits_errors():
+    import ozaki_triton_amd as ozk
+    with pytest.raises(AssertionError, match=r"n=1073741824 .* \(alpha=-3\)"):
+        ozk.compute_split_bits(1 << 30, torch.float16, torch.float32)
+    with pytest.raises(ValueError, match="unsupported dot_accum_dtype"):
+        ozk.compute_split_bits(16, torch.float16, torch.float64)
+    with pytest.raises(ValueError):
+        ozk.compute_split_bits(0, torch.int8, torch.int32)
+    with pytest.raises(KeyError):
+        ozk.compute_split_bits(16, torch.float64, torch.float32)
+
+
+def test_canonicalize_batch_broadcasts_like_matmul():
+    import ozaki_triton_amd as ozk
+    A = torch.zeros(16, 1024, 64, dtype=torch.float64)
+    B = torch.zeros(64, 32, dtype=torch.float64)
+    A3, B3, bs = ozk._canonicalize_batch(A, B)
+    assert tuple(bs) == (16,)
+    assert A3.shape == (16, 1024, 64) and B3.shape == (1, 64, 32)   # B split once
+    A = torch.zeros(2, 1, 5, 6, dtype=torch.float64)
+    B = torch.zeros(3, 6, 7, dtype=torch.float64)
+    A3, B3, bs = ozk._canonicalize_batch(A, B)
+    assert tuple(bs) == (2, 3)
+    assert A3.shape == (6, 5, 6) and B3.shape == (6, 6, 7)
+    assert torch.matmul(A, B).shape == (*bs, 5, 7)
+    # a transposed operand is read in place (no copy)
+    Bt = torch.zeros(32, 64, dtype=torch.float64).T
+    _, B3, _ = ozk._canonicalize_batch(torch.zeros(4, 64, dtype=torch.float64), Bt)
+    assert B3.data_ptr() == Bt.data_ptr()

@@ -1,0 +1,239 @@
+"""GPU parity of the HIP kernels against the CPU oracle.
+
+* split: slices and scales bit-exact for every path (row-resident,
+  column-strip-resident, generic strided) and dtype combination;
+* int8 cross-GEMM and the whole int8 ozaki_matmul: bit-exact;
+* fp16 cross-GEMM: within the a-priori fp32 accumulation bound (the reference's
+  own tl.dot accumulates in fp32 hardware order, which no other machine
+  reproduces bitwise).
+"""
+import numpy as np
+import pytest
+import torch
+
+from tests.helpers import (NAME_OF, assert_bitwise_equal, c3_like, fp16_cross_bound,
+                           oracle_split_batched, to_np)
+
+pytestmark = pytest.mark.gpu
+
+COMBOS = [(torch.float64, torch.int8), (torch.float64, torch.float16),
+          (torch.float32, torch.int8), (torch.float32, torch.float16)]
+
+
+def _alpha(ozk, K, slice_dtype):
+    return ozk.compute_split_bits(K, slice_dtype, ozk._select_dot_accum_dtype(slice_dtype))
+
+
+def _check_split(oracle, ozk, X3_dev, L, slice_dtype, what):
+    K = X3_dev.shape[-1]
+    alpha = _alpha(ozk, K, slice_dtype)
+    sl, sc = ozk.split_matrix(X3_dev, L, alpha, slice_dtype)
+    torch.cuda.synchronize()
+    X3 = to_np(X3_dev.contiguous())
+    osl, osc = oracle_split_batched(oracle, X3, L, alpha, slice_dtype)
+    assert_bitwise_equal(to_np(sc), osc, f"{what} scales")
+    assert_bitwise_equal(to_np(sl), osl, f"{what} slices")
+
+
+# --------------------------------------------------------------------------- #
+# split
+# --------------------------------------------------------------------------- #
+@pytest.mark.parametrize("xdt,sdt", COMBOS)
+@pytest.mark.parametrize("L", [1, 2, 4])
+@pytest.mark.parametrize("rows,K", [(5, 256), (64, 1000), (33, 2048), (7, 8192)])
+def test_split_rows_path(oracle, gpu, xdt, sdt, L, rows, K):
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(rows * K + L)
+    X = torch.randn(2, rows, K, generator=g, dtype=torch.float64)
+    X = X * torch.pow(10.0, torch.empty(2, rows, 1).uniform_(-3, 3, generator=g).double())
+    _check_split(oracle, ozk, X.to(xdt).to(gpu), L, sdt, f"rows {xdt} {sdt} L{L} {rows}x{K}")
+
+
+@pytest.mark.parametrize("xdt,sdt", COMBOS)
+@pytest.mark.parametrize("L", [1, 3, 4])
+@pytest.mark.parametrize("N,K", [(8, 256), (40, 1000), (96, 2048), (24, 8192)])
+def test_split_strip_path(oracle, gpu, xdt, sdt, L, N, K):
+    """B's columns through the transposed view (rows contiguous)."""
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(N * K + L + 1)
+    B = torch.randn(2, K, N, generator=g, dtype=torch.float64)
+    B = B * torch.pow(2.0, torch.randint(-8, 9, (2, 1, N), generator=g).double())
+    Bd = B.to(xdt).to(gpu)
+    _check_split(oracle, ozk, Bd.transpose(-1, -2), L, sdt, f"strip {xdt} {sdt} L{L} {N}x{K}")
+
+
+@pytest.mark.parametrize("xdt,sdt", COMBOS)
+def test_split_generic_path(oracle, gpu, xdt, sdt):
+    """Strides no fast path takes (every other column, odd K) and a K beyond
+    the resident capacity."""
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(5)
+    X = torch.randn(2, 19, 2 * 301, generator=g, dtype=torch.float64).to(xdt).to(gpu)
+    _check_split(oracle, ozk, X[:, :, ::2], 3, sdt, "generic strided")
+    big = 40000 if xdt == torch.float64 else 70000
+    Y = torch.randn(1, 3, big, generator=g, dtype=torch.float64).to(xdt).to(gpu)
+    _check_split(oracle, ozk, Y, 2, sdt, "generic long K")
+
+
+@pytest.mark.parametrize("xdt", [torch.float64, torch.float32])
+def test_split_edge_rows(oracle, gpu, xdt):
+    """Zero rows, power-of-two maxima, the ceil(log2) band, clamped q,
+    subnormal-scale rows and exact ties."""
+    import ozaki_triton_amd as ozk
+    K = 512
+    X = torch.zeros(1, 8, K, dtype=torch.float64)
+    X[0, 1, 7] = 1.0                                        # power of two
+    X[0, 2] = -(2.0 ** -30)                                 # constant power of two
+    k, j = 40, 11                                           # band: J(40) = 11
+    mu = float(np.uint32(((k + 127) << 23) | j).view(np.float32))
+    X[0, 3, 0] = mu
+    X[0, 3, 1:] = torch.linspace(-mu, mu, K - 1, dtype=torch.float64)
+    X[0, 4] = torch.arange(K, dtype=torch.float64) * 0.5 - 100.0    # ties at s = 1
+    X[0, 5] = torch.randn(K, dtype=torch.float64) * 1e-37          # near fp32 underflow
+    X[0, 6, ::3] = 3.0 * 2.0 ** -20
+    X[0, 7] = torch.randn(K, dtype=torch.float64) * 1e30
+    Xd = X.to(xdt).to(gpu)
+    for L in (1, 2, 4):
+        for sdt in (torch.int8, torch.float16):
+            _check_split(oracle, ozk, Xd, L, sdt, f"edge {xdt} {sdt} L{L}")
+            _check_split(oracle, ozk, Xd.transpose(-1, -2).contiguous().transpose(-1, -2), L,
+                         sdt, f"edge strip {xdt} {sdt} L{L}")
+
+
+# --------------------------------------------------------------------------- #
+# cross-GEMM
+# --------------------------------------------------------------------------- #
+def _random_slices(g, B, L, M, N, K, sdt):
+    if sdt == torch.int8:
+        As = torch.randint(-128, 128, (B, L, M, K), generator=g, dtype=torch.int8)
+        BsT = torch.randint(-128, 128, (B, L, N, K), generator=g, dtype=torch.int8)
+    else:
+        As = (torch.rand(B, L, M, K, generator=g) * 2 - 1).mul(64).to(torch.float16)
+        BsT = (torch.rand(B, L, N, K, generator=g) * 2 - 1).mul(64).to(torch.float16)
+    sa = torch.pow(2.0, torch.randint(-20, 5, (B, L, M), generator=g).float())
+    sb = torch.pow(2.0, torch.randint(-20, 5, (B, L, N), generator=g).float())
+    return As, BsT, sa, sb
+
+
+@pytest.mark.parametrize("L", [1, 2, 3, 4])
+@pytest.mark.parametrize("out", [torch.float64, torch.float32])
+@pytest.mark.parametrize("M,N,K", [(64, 64, 128), (100, 72, 1040), (256, 192, 512), (1, 130, 16)])
+def test_cross_gemm_int8_bitexact(oracle, gpu, L, out, M, N, K):
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(M * 7 + N * 3 + K + L)
+    As, BsT, sa, sb = _random_slices(g, 2, L, M, N, K, torch.int8)
+    C = ozk.cross_gemm(As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), L, out)
+    torch.cuda.synchronize()
+    C = to_np(C)
+    for b in range(2):
+        want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[b]), to_np(sa[b]), to_np(sb[b]),
+                                 NAME_OF[out])
+        assert_bitwise_equal(C[b], want, f"int8 cross L{L} {out} {M}x{N}x{K} b{b}")
+
+
+@pytest.mark.parametrize("L", [1, 2, 3, 4])
+@pytest.mark.parametrize("M,N,K", [(64, 64, 128), (100, 72, 1040), (128, 256, 2048)])
+def test_cross_gemm_fp16_within_bound(oracle, gpu, L, M, N, K):
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(M + N + K + L)
+    As, BsT, sa, sb = _random_slices(g, 1, L, M, N, K, torch.float16)
+    C = ozk.cross_gemm(As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), L,
+                       torch.float64)
+    torch.cuda.synchronize()
+    C = to_np(C)[0]
+    a, bT, s_a, s_b = to_np(As[0]), to_np(BsT[0]), to_np(sa[0]), to_np(sb[0])
+    want = oracle.cross_gemm(a, bT, s_a, s_b, "float64")
+    bound = fp16_cross_bound(oracle, a, bT, s_a, s_b)
+    err = np.abs(C - want)
+    assert np.all(err <= bound), float((err / np.maximum(bound, 1e-300)).max())
+
+
+def test_cross_gemm_strided_operands(oracle, gpu):
+    """N-contiguous B slices (how tune.py:60-65 calls cross_gemm) and
+    non-contiguous A slices go through the pack kernel."""
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(9)
+    L, M, N, K = 3, 70, 50, 200
+    As, BsT, sa, sb = _random_slices(g, 1, L, M, N, K, torch.int8)
+    Bs_n = BsT.transpose(-1, -2).contiguous()          # [1, L, K, N], N-contiguous
+    A_wide = torch.zeros(1, L, M, K + 8, dtype=torch.int8)
+    A_wide[..., :K] = As
+    C = ozk.cross_gemm(A_wide.to(gpu)[..., :K], Bs_n.to(gpu), sa.to(gpu), sb.to(gpu), L,
+                       torch.float64)
+    torch.cuda.synchronize()
+    want = oracle.cross_gemm(to_np(As[0]), to_np(BsT[0]), to_np(sa[0]), to_np(sb[0]), "float64")
+    assert_bitwise_equal(to_np(C)[0], want, "strided cross")
+
+
+def test_cross_gemm_zero_splits(gpu):
+    import ozaki_triton_amd as ozk
+    As = torch.zeros(2, 0, 5, 32, dtype=torch.int8, device=gpu)
+    Bs = torch.zeros(2, 0, 32, 7, dtype=torch.int8, device=gpu)
+    sa = torch.zeros(2, 0, 5, device=gpu)
+    sb = torch.zeros(2, 0, 7, device=gpu)
+    C = ozk.cross_gemm(As, Bs, sa, sb, 0, torch.float64)
+    assert C.shape == (2, 5, 7) and bool((C == 0).all())
+
+
+# --------------------------------------------------------------------------- #
+# ozaki_matmul end to end
+# --------------------------------------------------------------------------- #
+@pytest.mark.parametrize("xdt", [torch.float64, torch.float32])
+@pytest.mark.parametrize("L", [1, 2, 3, 4])
+def test_ozaki_matmul_int8_bitexact(oracle, gpu, xdt, L):
+    import ozaki_triton_amd as ozk
+    A, B = c3_like((2, 96, 320), (2, 320, 136), seed=L, dtype=xdt)
+    C = ozk.ozaki_matmul(A.to(gpu), B.to(gpu), L, torch.int8)
+    torch.cuda.synchronize()
+    want = oracle.ozaki_matmul(to_np(A), to_np(B), L, "int8")
+    assert_bitwise_equal(to_np(C), want, f"ozaki int8 {xdt} L{L}")
+
+
+@pytest.mark.parametrize("xdt", [torch.float64, torch.float32])
+def test_ozaki_matmul_broadcast_batch(oracle, gpu, xdt):
+    """torch.matmul batch broadcasting (config 4's pattern, small)."""
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(4)
+    A = torch.randn(3, 1, 40, 128, generator=g, dtype=torch.float64).to(xdt)
+    B = torch.randn(2, 128, 24, generator=g, dtype=torch.float64).to(xdt)
+    C = ozk.ozaki_matmul(A.to(gpu), B.to(gpu), 3, torch.int8)
+    torch.cuda.synchronize()
+    assert C.shape == (3, 2, 40, 24)
+    want = oracle.ozaki_matmul(to_np(A), to_np(B), 3, "int8")
+    assert_bitwise_equal(to_np(C), want, "broadcast")
+    # matches torch.matmul's shape semantics and value to the scheme's accuracy
+    ref = torch.matmul(A.double(), B.double())
+    rel = float((C.cpu().double() - ref).norm() / ref.norm())
+    assert rel < 1e-5
+
+
+@pytest.mark.parametrize("xdt", [torch.float64, torch.float32])
+@pytest.mark.parametrize("L", [2, 3])
+def test_ozaki_matmul_fp16(oracle, gpu, xdt, L):
+    import ozaki_triton_amd as ozk
+    A, B = c3_like((1, 128, 512), (1, 512, 96), seed=10 + L, dtype=xdt)
+    C = ozk.ozaki_matmul(A.to(gpu), B.to(gpu), L, torch.float16)
+    torch.cuda.synchronize()
+    A64, B64 = to_np(A)[0], to_np(B)[0]
+    alpha = ozk.compute_split_bits(512, torch.float16, torch.float32)
+    a_sl, a_sc = oracle.split(A64, L, alpha, "float16")
+    b_sl, b_sc = oracle.split(B64.T, L, alpha, "float16")
+    want = oracle.cross_gemm(a_sl, b_sl, a_sc, b_sc, NAME_OF[xdt])
+    bound = fp16_cross_bound(oracle, a_sl, b_sl, a_sc, b_sc)
+    if xdt == torch.float32:
+        bound = bound + 2.0 ** -23 * np.abs(want)     # output rounding to fp32
+    err = np.abs(to_np(C)[0].astype(np.float64) - want.astype(np.float64))
+    assert np.all(err <= bound)
+
+
+def test_ozaki_matmul_degenerate_shapes(gpu):
+    import ozaki_triton_amd as ozk
+    A = torch.randn(0, 4, 8, dtype=torch.float64, device=gpu)
+    B = torch.randn(8, 3, dtype=torch.float64, device=gpu)
+    assert ozk.ozaki_matmul(A, B, 2, torch.int8).shape == (0, 4, 3)
+    A = torch.randn(4, 8, dtype=torch.float64, device=gpu)
+    C = ozk.ozaki_matmul(A, B, 0, torch.int8)
+    assert C.shape == (4, 3) and bool((C == 0).all())
+    with pytest.raises(ValueError):
+        ozk.ozaki_matmul(torch.randn(4, 0, dtype=torch.float64, device=gpu),
+                         torch.randn(0, 3, dtype=torch.float64, device=gpu), 2, torch.int8)

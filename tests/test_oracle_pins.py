@@ -1,0 +1,308 @@
+"""Pins of the CPU oracle (oracle/ozaki_oracle.c) against facts it does not
+restate: numpy's own float32 log2 / float16 conversion (the primitives the
+Triton interpreter runs for tl.log2 and .to(float16)), an exhaustive fixture,
+exact integer arithmetic, reconstruction invariants, and the relative errors
+the reference publishes in reference/test_results.csv."""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+# --------------------------------------------------------------------------- #
+# alpha rule (ozaki_triton.py:76-98)
+# --------------------------------------------------------------------------- #
+@pytest.mark.parametrize("n,slice_dtype,acc,expected", [
+    (256, "float16", "float32", 7),      # config 1
+    (4096, "float16", "float32", 5),     # config 2
+    (8192, "int8", "int32", 7),          # config 3 (capped by int8's 7 bits)
+    (2048, "float16", "float32", 6),     # config 4
+    (65536, "int8", "int32", 7),         # config 5: floor((31-16)/2) = 7
+    (1 << 20, "int8", "int32", 5),       # (31-20)/2 = 5.5 -> 5
+    (1 << 21, "float16", "float32", 1),  # (23-21)/2 = 1
+    (1, "float32", "float32", 11),       # 23/2 = 11.5 -> 11 < 23
+    (3, "float16", "float32", 10),       # capped by fp16's 10 bits
+])
+def test_alpha_table(oracle, n, slice_dtype, acc, expected):
+    assert oracle.compute_split_bits(n, slice_dtype, acc) == expected
+
+
+def test_alpha_truncates_toward_zero(oracle):
+    # alpha < 0 region: Python int() truncates toward zero, not floor
+    assert oracle.compute_split_bits(1 << 25, "float16", "float32") == -1   # -1.0
+    assert oracle.compute_split_bits(1 << 26, "float16", "float32") == -1   # -1.5 -> -1
+    assert oracle.compute_split_bits(1 << 24, "float16", "float32") == 0    # -0.5 -> 0
+
+
+# --------------------------------------------------------------------------- #
+# exponent rule (ozaki_triton.py:174)
+# --------------------------------------------------------------------------- #
+def test_band_table_matches_exhaustive_fixture(oracle):
+    with open(os.path.join(HERE, "golden", "ceil_log2_band.json")) as f:
+        fx = json.load(f)
+    for k, J in fx["band_J"].items():
+        assert oracle.band_J(int(k)) == J, k
+    assert fx["exp2_inexact"] == [127]
+
+
+def test_ceil_log2_matches_numpy(oracle):
+    rng = np.random.default_rng(0)
+    # every binade: j in [0, 64] (the band lives at j <= 22) plus random mantissas
+    biased = np.arange(1, 255, dtype=np.uint32)          # k = -126 .. 127
+    j = np.concatenate([np.arange(0, 65), rng.integers(0, 1 << 23, 64)]).astype(np.uint32)
+    bits = (biased[:, None] << 23) | j[None, :]
+    x = bits.ravel().view(np.float32)
+    # and uniformly random positive floats >= 1e-38f
+    r = rng.integers(0x006CE3EE, 0x7F7FFFFF, 200000, dtype=np.uint32).view(np.float32)
+    for arr in (x, r):
+        expect = np.ceil(np.log2(arr)).astype(np.int32)
+        got = oracle.ceil_log2_f32(arr)
+        np.testing.assert_array_equal(got, expect)
+
+
+def test_ceil_log2_subnormal_floor(oracle):
+    # mu never drops below 1e-38f (ozaki_triton.py:172), which is subnormal; all of
+    # [1e-38f, 2^-126) has ceil(log2) = -126
+    lo = np.float32(1e-38).view(np.uint32)
+    x = np.arange(lo, 0x00800000, 997, dtype=np.uint32).view(np.float32)
+    np.testing.assert_array_equal(oracle.ceil_log2_f32(x), np.ceil(np.log2(x)).astype(np.int32))
+    assert np.all(oracle.ceil_log2_f32(x) == -126)
+
+
+def test_scale_is_numpy_exp2(oracle):
+    rng = np.random.default_rng(1)
+    mu = rng.integers(0x006CE3EE, 0x7F7FFFFF, 5000, dtype=np.uint32).view(np.float32)
+    for alpha in (1, 5, 7, 10):
+        expect = np.exp2(np.ceil(np.log2(mu)) - np.float32(alpha)).astype(np.float32)
+        got = np.array([oracle.scale_from_max(float(m), alpha) for m in mu], dtype=np.float32)
+        # numpy's float32 exp2(127) is inexact (fixture): only reachable with alpha 1
+        keep = (np.ceil(np.log2(mu)) - alpha) != 127
+        np.testing.assert_array_equal(got[keep], expect[keep])
+
+
+# --------------------------------------------------------------------------- #
+# fp16 rounding: one rounding from the residual dtype (ozaki_triton.py:202)
+# --------------------------------------------------------------------------- #
+def test_f64_to_f16_matches_numpy(oracle):
+    rng = np.random.default_rng(2)
+    x = np.concatenate([
+        rng.standard_normal(100000) * 2.0 ** rng.integers(-30, 20, 100000),
+        # exact ties and near-ties around fp16 grid points (normal and subnormal)
+        (np.arange(-5000, 5000) + 0.5) * 2.0 ** -24,
+        (np.arange(-5000, 5000) + 0.5) * 2.0 ** -10,
+        (np.arange(2048, 4096) + 0.5) * 2.0 ** 5,         # ties near fp16 max
+        np.nextafter((np.arange(1, 3000) + 0.5) * 2.0 ** -14, 0),
+        np.nextafter((np.arange(1, 3000) + 0.5) * 2.0 ** -14, 1),
+        [0.0, -0.0, 65504.0, 65519.99, 65520.0, 1e6, 2.0 ** -25, 2.0 ** -25 * 1.0000001],
+    ])
+    np.testing.assert_array_equal(oracle.f64_to_f16(x).view(np.uint16),
+                                  x.astype(np.float16).view(np.uint16))
+    x32 = x.astype(np.float32)
+    np.testing.assert_array_equal(oracle.f64_to_f16(x32.astype(np.float64)).view(np.uint16),
+                                  x32.astype(np.float16).view(np.uint16))
+
+
+def test_f64_to_f16_is_not_double_rounded(oracle):
+    # a value just above an fp16 tie whose fp32 rounding lands exactly on the tie:
+    # single rounding goes up, fp64 -> fp32 -> fp16 would go to even (down)
+    x = 1.0 + 2.0 ** -11 + 2.0 ** -40
+    assert np.float32(x) == np.float32(1.0 + 2.0 ** -11)
+    assert oracle.f64_to_f16(np.array([x]))[0] == np.float16(1.0 + 2.0 ** -10)
+    assert np.float16(np.float32(x)) == np.float16(1.0)
+
+
+# --------------------------------------------------------------------------- #
+# split invariants (ozaki_triton.py:157-211)
+# --------------------------------------------------------------------------- #
+def _reconstruct(slices, scales):
+    return (slices.astype(np.float64) * scales.astype(np.float64)[:, :, None]).sum(0)
+
+
+@pytest.mark.parametrize("slice_dtype", ["int8", "float16"])
+def test_split_fp32_reconstructs_exactly(oracle, slice_dtype):
+    """fp32 input: every residual is exact in fp32, so sum_l slice_l*s_l plus the
+    final residual is X; the final residual is bounded by s_{L-1}/2 (int8) or
+    half an fp16 ulp of the last slice's magnitude times s."""
+    rng = np.random.default_rng(3)
+    X = (rng.standard_normal((37, 300)) * 10.0 ** rng.uniform(-3, 3, (37, 1))).astype(np.float32)
+    alpha = oracle.compute_split_bits(300, slice_dtype, "int32" if slice_dtype == "int8" else "float32")
+    L = 3
+    sl, sc = oracle.split(X, L, alpha, slice_dtype)
+    rec = _reconstruct(sl, sc)
+    resid = X.astype(np.float64) - rec
+    if slice_dtype == "int8":
+        assert sl.min() >= -128 and sl.max() <= 127
+        # |q| <= 2^alpha, so only q in (127.5, 128] is clamped (slice 127); there
+        # the residual reaches s, elsewhere it is at most s/2
+        s_last = sc[L - 1][:, None]
+        clamped = sl[L - 1] == 127
+        assert np.all(np.abs(resid)[~clamped] <= (s_last * 0.5 * np.ones_like(resid))[~clamped])
+        assert np.all(np.abs(resid) <= s_last)
+    else:
+        assert np.all(np.abs(resid) <= sc[L - 1][:, None] * 2.0 ** alpha * 2.0 ** -11)
+    # scales are powers of two and the first is 2^(ceil(log2 rowmax) - alpha)
+    m, e = np.frexp(sc)
+    assert np.all(m == 0.5)
+    expect0 = np.exp2(np.ceil(np.log2(np.abs(X).max(1))) - alpha).astype(np.float32)
+    np.testing.assert_array_equal(sc[0], expect0)
+    # the residual of level l is what level l+1 splits: slices of X - s_0 A_0 are levels 1..
+    r1 = (X.astype(np.float64) - sl[0].astype(np.float64) * sc[0][:, None]).astype(np.float32)
+    sl1, sc1 = oracle.split(r1, L - 1, alpha, slice_dtype)
+    np.testing.assert_array_equal(sl1, sl[1:])
+    np.testing.assert_array_equal(sc1, sc[1:])
+
+
+def test_split_fp64_residual_is_rounded_to_fp32(oracle):
+    """fp64 input: the reference stores the residual in an fp32 buffer
+    (ozaki_triton.py:233), so level 1 sees fl32(X - s_0 A_0); later levels are
+    exact.  Splitting the rounded residual again must give levels 1.. bit for bit."""
+    rng = np.random.default_rng(4)
+    X = rng.standard_normal((29, 512)) * 2.0 ** rng.integers(-8, 9, (29, 1))
+    alpha, L = 7, 4
+    sl, sc = oracle.split(X, L, alpha, "int8")
+    r1 = (X - sl[0].astype(np.float64) * sc[0].astype(np.float64)[:, None]).astype(np.float32)
+    sl1, sc1 = oracle.split(r1.astype(np.float64), L - 1, alpha, "int8")
+    np.testing.assert_array_equal(sl1, sl[1:])
+    np.testing.assert_array_equal(sc1, sc[1:])
+    # the fp32 rounding is visible: without it level 1 differs somewhere
+    r1x = X - sl[0].astype(np.float64) * sc[0].astype(np.float64)[:, None]
+    sl1x, _ = oracle.split(r1x, L - 1, alpha, "int8")
+    assert not np.array_equal(sl1x, sl[1:])
+
+
+def test_split_int8_rounding_cases(oracle):
+    """int8 rounding is trunc(clip(fl(q +/- 0.5))): halves go away from zero,
+    and in fp32 q = 0.5 - 2^-25 rounds to 1 because fl32(q + 0.5) == 1."""
+    alpha = 7
+    # row max 128 -> E = 7 -> s = 1, so q == x
+    xs = np.array([[128.0, 0.5, -0.5, 1.5, -1.5, 2.5, 0.49999997, -0.49999997, 127.5, -127.5,
+                    0.0, -0.0]], dtype=np.float32)
+    sl, sc = oracle.split(xs, 1, alpha, "int8")
+    assert sc[0, 0] == 1.0
+    assert list(sl[0, 0]) == [127, 1, -1, 2, -2, 3, 1, -1, 127, -128, 0, 0]
+    # the same values in fp64 round half away from zero exactly
+    sl64, _ = oracle.split(xs.astype(np.float64), 1, alpha, "int8")
+    assert list(sl64[0, 0]) == [127, 1, -1, 2, -2, 3, 0, 0, 127, -128, 0, 0]
+
+
+def test_split_zero_and_power_of_two_rows(oracle):
+    X = np.zeros((3, 16), dtype=np.float64)
+    X[1, 3] = 1.0          # power of two: E = 0
+    X[2, :] = -2.0 ** -30
+    sl, sc = oracle.split(X, 2, 7, "int8")
+    assert sc[0, 0] == np.float32(2.0 ** (-126 - 7))    # mu = 1e-38f -> E = -126
+    assert np.all(sl[:, 0] == 0)
+    assert sc[0, 1] == 2.0 ** -7 and sl[0, 1, 3] == 127   # q = 128 -> 128.5 -> 127
+    assert sc[1, 1] == np.float32(2.0 ** (-7 - 7))        # residual 2^-7 -> E = -7
+    assert sc[0, 2] == 2.0 ** -37 and np.all(sl[0, 2] == -128)
+
+
+def test_split_band_exponent(oracle):
+    """A row max just above a power of two inside the band (j <= J(k)) keeps
+    E = k, so q can exceed 2^alpha slightly and the int8 slice clamps."""
+    k, j = 40, 11                          # J(40) = 11
+    mu = np.float32(np.uint32(((k + 127) << 23) | j).view(np.float32))
+    X = np.array([[mu, -mu * np.float32(0.5)]], dtype=np.float32)
+    sl, sc = oracle.split(X, 2, 7, "int8")
+    assert sc[0, 0] == np.float32(2.0 ** (k - 7))
+    assert sl[0, 0, 0] == 127
+    assert int(np.ceil(np.log2(mu))) == k
+
+
+# --------------------------------------------------------------------------- #
+# cross-GEMM (ozaki_triton.py:357-452)
+# --------------------------------------------------------------------------- #
+def test_int8_pair_dots_are_exact(oracle):
+    rng = np.random.default_rng(5)
+    As = rng.integers(-128, 128, (3, 17, 200), dtype=np.int8)
+    Bs = rng.integers(-128, 128, (3, 23, 200), dtype=np.int8)
+    acc = oracle.int8_pair_dots(As, Bs)
+    expect = np.einsum("imk,jnk->ijmn", As.astype(np.int64), Bs.astype(np.int64))
+    np.testing.assert_array_equal(acc, expect)
+
+
+@pytest.mark.parametrize("out", ["float64", "float32"])
+def test_int8_cross_gemm_equals_reconstructed_product(oracle, out):
+    """C = sum_ij s_i s_j (A_i B_j): with small accumulators every fp32 step is
+    exact, so C equals the fp64 product of the reconstructed operands up to fp64
+    (or fp32) summation rounding."""
+    rng = np.random.default_rng(6)
+    dt = np.float64 if out == "float64" else np.float32
+    A = (rng.standard_normal((33, 256)) * 2.0 ** rng.integers(-8, 9, (33, 1))).astype(dt)
+    B = (rng.standard_normal((256, 41)) * 2.0 ** rng.integers(-8, 9, (1, 41))).astype(dt)
+    L = 4
+    a_sl, a_sc = oracle.split(A, L, 7, "int8")
+    b_sl, b_sc = oracle.split(B.T, L, 7, "int8")
+    C = oracle.cross_gemm(a_sl, b_sl, a_sc, b_sc, out)
+    Ah = _reconstruct(a_sl, a_sc)
+    Bh = _reconstruct(b_sl, b_sc)
+    ref = Ah @ Bh.T
+    tol = 1e-14 if out == "float64" else 1e-6
+    assert np.linalg.norm(C - ref) / np.linalg.norm(ref) < tol
+    # a transposed operand or swapped scales would not come close
+    bad = oracle.cross_gemm(a_sl, b_sl, a_sc, b_sc[::-1].copy(), out)
+    assert np.linalg.norm(bad - ref) / np.linalg.norm(ref) > 1e-3
+
+
+def test_cross_gemm_outer_sum_order(oracle):
+    """The outer accumulation is sequential i-major / j-minor from +0: with
+    terms 1, 2^-60, -1, 2^-60 (i=0: j=0,1; i=1: j=0,1) the fp64 result is 2^-60,
+    not 0 (pairwise) or 2^-59 (exact)."""
+    As = np.zeros((2, 1, 16), np.int8)
+    Bs = np.zeros((2, 1, 16), np.int8)
+    As[0, 0, 0] = 1
+    As[1, 0, 0] = 1
+    Bs[0, 0, 0] = 1
+    Bs[1, 0, 0] = 1
+    sa = np.array([[1.0], [-1.0]], np.float32)        # t_1j = -t_0j ...
+    sb = np.array([[1.0], [2.0 ** -60]], np.float32)
+    # t00 = 1, t01 = 2^-60, t10 = -1, t11 = -2^-60 -> 1 + 2^-60 = 1 ; -1 -> 0 ; -2^-60
+    C = oracle.cross_gemm(As, Bs, sa, sb, "float64")
+    assert C[0, 0] == -(2.0 ** -60)
+
+
+# --------------------------------------------------------------------------- #
+# end to end: the relative errors the reference publishes
+# --------------------------------------------------------------------------- #
+# reference/test_results.csv, shape (B,M,N,K) = (2,512,2048,256), FP64 inputs,
+# rel_error = ||C - a@b||_F / ||a@b||_F with a@b in float64 (test.py:113,128)
+PUBLISHED = {
+    ("int8", 1): 0.01452, ("int8", 2): 5.718e-05, ("int8", 3): 3.26e-07,
+    ("int8", 4): 1.489e-09, ("float16", 1): 0.0002919,
+}
+
+
+@pytest.mark.parametrize("key", sorted(PUBLISHED))
+def test_relative_error_matches_published(oracle, key):
+    """Same input distribution as test.py:104-108 (randn times per-row /
+    per-column 10^U(-2,2)) at (1,512,512,256): the oracle's rel-err must lie
+    within [0.8, 1.25] of the published value (8 seeds measured 0.95-1.11).
+    A wrong alpha, a dropped split level or truncating instead of rounding
+    moves it by 2x or more."""
+    sd, L = key
+    rng = np.random.default_rng(11)
+    M = N = 512
+    K = 256
+    rs = 10 ** ((rng.random(M) * 2 - 1) * 2)
+    cs = 10 ** ((rng.random(N) * 2 - 1) * 2)
+    a = rng.standard_normal((M, K)) * rs[:, None]
+    b = rng.standard_normal((K, N)) * cs
+    C = oracle.ozaki_matmul(a, b, L, sd)
+    ref = a @ b
+    rel = np.linalg.norm(C - ref) / np.linalg.norm(ref)
+    ratio = rel / PUBLISHED[key]
+    assert 0.8 <= ratio <= 1.25, (rel, ratio)
+
+
+def test_broadcast_batch_matches_per_batch(oracle):
+    rng = np.random.default_rng(7)
+    A = rng.standard_normal((3, 20, 64))
+    B = rng.standard_normal((64, 24))
+    C = oracle.ozaki_matmul(A, B, 3, "float16")
+    assert C.shape == (3, 20, 24)
+    for b in range(3):
+        np.testing.assert_array_equal(C[b], oracle.ozaki_matmul(A[b], B, 3, "float16"))
