@@ -16,13 +16,15 @@
 //     holds 128 bytes of K for all L*(BM+BN) rows, staged global -> VGPR ->
 //     LDS with the next stage's loads in flight during the current MFMAs
 //     (double-buffered LDS, one barrier per stage).  16-byte chunks are
-//     XOR-swizzled by (row & 7) so ds_read_b128 / ds_write_b128 are
-//     bank-conflict free.
+//     XOR-swizzled by row so ds_read_b128 / ds_write_b128 are bank-conflict
+//     free.
 //   * int8 products are exact integers, so the order in which K is fed to
 //     the MFMA cannot change acc_ij: the int8 result is bit-identical to the
 //     reference for any tiling.
 //   * Workgroups are remapped so each XCD (own L2) processes a contiguous
 //     range of tiles, grouped GROUP_M tile-rows at a time.
+#include <stdlib.h>
+
 #include "ozk_common.h"
 #include "ozk_internal.h"
 
@@ -78,7 +80,13 @@ template <int L, int MI, int NI> struct GemmShape {
     static_assert((ROWS * kChunks) % 256 == 0, "stage must split evenly over 256 lanes");
 };
 
-OZK_DEV int swz(int row, int chunk) { return row * kRowBytes + ((chunk ^ (row & 7)) << 4); }
+// gfx950's LDS serves a ds_read_b128 16 lanes (256 bytes, all 64 banks) per
+// cycle.  For 128-byte rows, rows r and r + 2 share banks, so the 16-byte
+// chunk is XORed with (r >> 1) & 7: the 16 rows one pass reads land on 16
+// distinct chunk columns.
+OZK_DEV int swz(int row, int chunk) {
+    return row * kRowBytes + ((chunk ^ ((row >> 1) & 7)) << 4);
+}
 
 template <typename ST, int L, int MI, int NI, typename OutT>
 __global__ __launch_bounds__(256, 1) void cross_gemm_kernel(GemmParams p, int group_m) {
@@ -242,6 +250,545 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_kernel(GemmParams p, int gr
 }
 
 // ---------------------------------------------------------------------------
+// Pipelined variant: global -> LDS by buffer_load ... lds (no VGPR staging),
+// a ring of DMA_STAGES LDS stages of 64 bytes of K per row, loads issued
+// DMA_STAGES-1 stages ahead.  Lane i of a DMA instruction writes LDS bytes
+// [16 i, 16 i + 16) of that instruction's 1 KB window, so the XOR swizzle is
+// applied by choosing which 16-byte chunk of global memory each lane fetches.
+// Out-of-range rows and K tails are fetched from a buffer offset beyond
+// num_records, which the hardware returns as zeros.
+// ---------------------------------------------------------------------------
+constexpr int kDmaRowBytes = 64;     // A-direct kernel stage rows
+#ifndef OZK_DMA_ROW
+#define OZK_DMA_ROW 128
+#endif
+constexpr int kDmaRB = OZK_DMA_ROW;  // 2 x 2 DMA kernel stage rows (64 or 128 bytes of K)
+#ifndef OZK_DMA_STAGES
+#define OZK_DMA_STAGES (kDmaRB == 64 ? 4 : 2)
+#endif
+constexpr int kDmaStages = OZK_DMA_STAGES;
+
+template <int L, int MI, int NI> struct DmaShape {
+    static constexpr int BM = 64 * MI;
+    static constexpr int BN = 64 * NI;
+    static constexpr int A_ROWS = L * BM;
+    static constexpr int ROWS = L * (BM + BN);
+    static constexpr int STAGE = ROWS * kDmaRB;
+    static constexpr int LPS = STAGE / (4 * 1024);      // DMA instructions per wave per stage
+    static constexpr int LDS_BYTES = kDmaStages * STAGE;
+    static_assert(STAGE % 4096 == 0, "stage must be a whole number of 1 KB wave windows");
+};
+
+// LDS byte offset of logical 16-byte chunk c of row r inside one stage.
+// gfx950 serves a ds_read_b128 16 lanes (256 bytes = all 64 banks) per pass;
+// the XOR spreads the 16 consecutive rows of one pass over all banks
+// (64-byte rows repeat banks every 4 rows, 128-byte rows every 2).
+template <int RB> OZK_DEV int rswz(int r, int c) {
+    if constexpr (RB == 64) return r * 64 + ((c ^ ((r >> 2) & 3)) << 4);
+    else return r * 128 + ((c ^ ((r >> 1) & 7)) << 4);
+}
+OZK_DEV int dswz(int r, int c) { return rswz<64>(r, c); }
+
+// s_waitcnt with only the vector-memory counter limited to n
+template <int N> OZK_DEV void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup execution barrier without the release fence of __syncthreads()
+// (which would wait for every outstanding global load, i.e. drain the DMA
+// prefetch ring).  Callers make their own DMA writes complete with
+// wait_vmcnt first; the memory clobber keeps the compiler from moving LDS
+// accesses across the barrier.
+OZK_DEV void exec_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+template <typename ST, int L, int MI, int NI, typename OutT>
+__global__ __launch_bounds__(256, 1) void cross_gemm_dma_kernel(GemmParams p, int group_m,
+                                                                uint32_t a_records,
+                                                                uint32_t b_records) {
+    using Sh = DmaShape<L, MI, NI>;
+    using MF = Mfma<ST>;
+    using Acc = typename MF::Acc;
+    using OA = typename OutAcc<OutT>::T;
+    constexpr int BM = Sh::BM, BN = Sh::BN;
+    constexpr int ES = (int)sizeof(ST);
+    constexpr uint32_t kOOB = 0x80000000u;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    // wave index is uniform across the wave; saying so keeps the LDS-DMA
+    // destination (M0) and the A/B choice per instruction scalar
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int h = lane >> 5, lr = lane & 31;
+
+    const int64_t tiles_m = (p.M + BM - 1) / BM;
+    const int64_t tiles_n = (p.N + BN - 1) / BN;
+    const int64_t tiles = tiles_m * tiles_n;
+    const int64_t g = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
+    const int64_t bidx = g / tiles;
+    const int64_t t = g % tiles;
+    const int64_t width = (int64_t)group_m * tiles_n;
+    const int64_t first_m = (t / width) * group_m;
+    const int64_t gsz = (tiles_m - first_m < group_m) ? (tiles_m - first_m) : group_m;
+    const int64_t tm = first_m + (t % width) % gsz;
+    const int64_t tn = (t % width) / gsz;
+#ifdef OZK_EXP_SAME_TILE
+    const int64_t m0 = 0, n0 = 0;   // timing experiment: every workgroup on tile 0
+    (void)tm; (void)tn;
+#else
+    const int64_t m0 = tm * BM, n0 = tn * BN;
+#endif
+
+    const uint32_t kbytes = (uint32_t)(p.K * ES);
+    const int nkb = (int)((kbytes + kDmaRB - 1) / kDmaRB);
+    constexpr int CH = kDmaRB / 16;       // 16-byte chunks per row
+    constexpr int STEPS = kDmaRB / 32;    // 32-byte MFMA K steps per stage
+
+    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const char *)p.A + bidx * p.as_b * ES), (short)0, (int)a_records, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const char *)p.B + bidx * p.bs_b * ES), (short)0, (int)b_records, 0x00020000);
+
+    // Per-lane source offsets (bytes, excluding the stage's K offset) for the
+    // LPS DMA instructions of this wave; kOOB marks rows outside the matrix.
+    // A 1 KB DMA window covers whole rows and A_ROWS is a multiple of 64,
+    // so each instruction reads only A or only B (uniform per wave).
+    uint32_t src[Sh::LPS];
+    int chunk[Sh::LPS];
+#pragma unroll
+    for (int q = 0; q < Sh::LPS; ++q) {
+        const int pos = (wave * Sh::LPS + q) * 64 + lane;   // 16-byte unit in the stage
+        const int r = pos / CH;
+        const int pc = pos % CH;
+        chunk[q] = (kDmaRB == 64) ? (pc ^ ((r >> 2) & 3)) : (pc ^ ((r >> 1) & 7));
+        if (r < Sh::A_ROWS) {
+            const int i = r / BM;
+            const int64_t m = m0 + r % BM;
+            src[q] = (m < p.M) ? (uint32_t)(((int64_t)i * p.as_l + m * p.as_m) * ES) : kOOB;
+        } else {
+            const int rb = r - Sh::A_ROWS;
+            const int j = rb / BN;
+            const int64_t n = n0 + rb % BN;
+            src[q] = (n < p.N) ? (uint32_t)(((int64_t)j * p.bs_l + n * p.bs_n) * ES) : kOOB;
+        }
+    }
+
+    auto issue_one = [&](int kb, int q) {
+        char *dst = smem + (kb % kDmaStages) * Sh::STAGE + wave * Sh::LPS * 1024;
+        const uint32_t kofs = (uint32_t)kb * kDmaRB + chunk[q] * 16;
+        const uint32_t vo = (src[q] == kOOB || kofs >= kbytes) ? kOOB : src[q] + kofs;
+        auto *ldsp = (__attribute__((address_space(3))) void *)(dst + q * 1024);
+        const bool isA = (wave * Sh::LPS + q) * (1024 / kDmaRB) < Sh::A_ROWS;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(isA ? rA : rB, ldsp, 16, vo, 0, 0, 0);
+    };
+    auto issue_stage = [&](int kb) {
+#pragma unroll
+        for (int q = 0; q < Sh::LPS; ++q) issue_one(kb, q);
+    };
+
+    Acc acc[L][L][MI][NI];
+#pragma unroll
+    for (int i = 0; i < L; ++i)
+#pragma unroll
+        for (int j = 0; j < L; ++j)
+#pragma unroll
+            for (int a = 0; a < MI; ++a)
+#pragma unroll
+                for (int c = 0; c < NI; ++c) acc[i][j][a][c] = MF::zero();
+
+#pragma unroll
+    for (int s = 0; s < kDmaStages - 1; ++s)
+        if (s < nkb) issue_stage(s);
+
+    // Fragments of one 32-byte K step: this wave's A rows for every slice i
+    // and B rows for every slice j.  Read r (r < L*MI: A, else B) of step kk.
+    struct Frags {
+        i32x4 a[L][MI];
+        i32x4 b[L][NI];
+    };
+    constexpr int kReads = L * (MI + NI);
+    constexpr int kMfmas = L * L * MI * NI;
+    auto read_one = [&](const char *buf, int kk, int r, Frags &f) {
+        const int ch = 2 * kk + h;
+        if (r < L * MI) {
+            const int i = r / MI, a = r % MI;
+            f.a[i][a] = *(const i32x4 *)(buf + rswz<kDmaRB>(i * BM + wm * 32 * MI + a * 32 + lr, ch));
+        } else {
+            const int j = (r - L * MI) / NI, c = (r - L * MI) % NI;
+            f.b[j][c] = *(const i32x4 *)(buf + rswz<kDmaRB>(Sh::A_ROWS + j * BN + wn * 32 * NI +
+                                                            c * 32 + lr, ch));
+        }
+    };
+    // MFMAs of `cur`, with the reads of the next step's fragments into `nxt`
+    // interleaved one per MFMA, so no MFMA waits on a read issued after the
+    // reads of its own operands and the LDS latency hides under the MFMAs.
+    // dma_kb >= 0: also issue the DMA loads of stage dma_kb, spread over the
+    // MFMAs (one per MFMA from the second on) instead of in one burst.
+    auto step = [&](const Frags &cur, Frags &nxt, const char *nbuf, int nkk, int dma_kb) {
+#pragma unroll
+        for (int q = 0; q < kMfmas; ++q) {
+            const int i = q / (L * MI * NI), j = (q / (MI * NI)) % L;
+            const int a = (q / NI) % MI, c = q % NI;
+            acc[i][j][a][c] = MF::run(cur.a[i][a], cur.b[j][c], acc[i][j][a][c]);
+            if (q < kReads) read_one(nbuf, nkk, q, nxt);
+#ifdef OZK_EXP_SPREAD_DMA
+            if (q >= 1 && q - 1 < Sh::LPS && dma_kb >= 0) issue_one(dma_kb, q - 1);
+#endif
+            __builtin_amdgcn_sched_barrier(0);   // keep this order
+        }
+#pragma unroll
+        for (int q = kMfmas; q < kReads; ++q) read_one(nbuf, nkk, q, nxt);
+#ifdef OZK_EXP_SPREAD_DMA
+#pragma unroll
+        for (int q = kMfmas; q < Sh::LPS + 1; ++q)
+            if (dma_kb >= 0) issue_one(dma_kb, q - 1);
+#endif
+    };
+    // stage kb has landed once at most the loads of the stages issued after it
+    // are outstanding; then the barrier publishes every wave's DMA writes
+    // When stage kb is awaited, stages up to kb + DMA_STAGES - 2 have been
+    // issued (each LPS loads per lane).
+    auto stage_ready = [&](int kb) {
+        const int after = min(kDmaStages - 2, nkb - 1 - kb);
+        static_assert(kDmaStages >= 2 && kDmaStages <= 6, "wait table");
+        // only counts that can occur (after <= DMA_STAGES - 2) are instantiated
+        if constexpr (kDmaStages - 2 >= 4) { if (after == 4) { wait_vmcnt<4 * Sh::LPS>(); goto waited; } }
+        if constexpr (kDmaStages - 2 >= 3) { if (after == 3) { wait_vmcnt<3 * Sh::LPS>(); goto waited; } }
+        if constexpr (kDmaStages - 2 >= 2) { if (after == 2) { wait_vmcnt<2 * Sh::LPS>(); goto waited; } }
+        if constexpr (kDmaStages - 2 >= 1) { if (after == 1) { wait_vmcnt<Sh::LPS>(); goto waited; } }
+        wait_vmcnt<0>();
+    waited:
+        // this wave's reads of the slot refilled after the barrier must have
+        // completed, not only been issued
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0) only
+        exec_barrier();
+    };
+
+    // Software pipeline over 32-byte K steps (two per stage).
+    Frags f0, f1;
+    if (nkb > 0) {
+        stage_ready(0);
+        if (kDmaStages - 1 < nkb) issue_stage(kDmaStages - 1);
+#pragma unroll
+        for (int q = 0; q < kReads; ++q) read_one(smem, 0, q, f0);
+    }
+    for (int kb = 0; kb < nkb; ++kb) {
+        const char *buf = smem + (kb % kDmaStages) * Sh::STAGE;
+        // steps 0 .. STEPS-2 of this stage, each reading the next step's
+        // fragments; f0 / f1 alternate
+#pragma unroll
+        for (int kk = 0; kk + 1 < STEPS; ++kk) {
+            if (kk % 2 == 0) step(f0, f1, buf, kk + 1, -1);
+            else step(f1, f0, buf, kk + 1, -1);
+        }
+        int dma_kb = -1;
+        if (kb + 1 < nkb) {
+            stage_ready(kb + 1);
+            // the ring slot of stage kb + DMA_STAGES is the one of stage kb,
+            // whose reads every wave completed before this barrier
+            if (kb + kDmaStages < nkb) dma_kb = kb + kDmaStages;
+#ifdef OZK_EXP_HALF_DMA
+            if (dma_kb & 1) dma_kb = -1;
+#endif
+#ifdef OZK_EXP_NO_LOOP_LOADS
+            dma_kb = -1;
+#endif
+#ifndef OZK_EXP_SPREAD_DMA
+            if (dma_kb >= 0) issue_stage(dma_kb);
+            dma_kb = -1;
+#endif
+        }
+        // last step: reads the next stage's step-0 fragments (on the last
+        // stage, unused data from a slot that is not being written)
+        if ((STEPS - 1) % 2 == 0) step(f0, f1, smem + ((kb + 1) % kDmaStages) * Sh::STAGE, 0, dma_kb);
+        else step(f1, f0, smem + ((kb + 1) % kDmaStages) * Sh::STAGE, 0, dma_kb);
+        if ((STEPS - 1) % 2 == 0) {   // next stage's step 0 expects its fragments in f0
+#pragma unroll
+            for (int i = 0; i < L; ++i)
+#pragma unroll
+                for (int a = 0; a < MI; ++a) f0.a[i][a] = f1.a[i][a];
+#pragma unroll
+            for (int j = 0; j < L; ++j)
+#pragma unroll
+                for (int c = 0; c < NI; ++c) f0.b[j][c] = f1.b[j][c];
+        }
+    }
+
+#ifdef OZK_EXP_NO_EPILOGUE
+    {   // timing experiment: keep the accumulators alive, store one word per lane
+        int sum = 0;
+#pragma unroll
+        for (int i = 0; i < L; ++i)
+#pragma unroll
+            for (int j = 0; j < L; ++j)
+#pragma unroll
+                for (int a = 0; a < MI; ++a)
+#pragma unroll
+                    for (int c = 0; c < NI; ++c)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) sum += (int)acc[i][j][a][c][r];
+        if (m0 + tid < p.M) ((OutT *)p.C)[(m0 + tid) * p.cs_m + n0] = (OutT)sum;
+        return;
+    }
+#endif
+    // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
+    const float *sab = p.sa + bidx * p.sas_b;
+    const float *sbb = p.sb + bidx * p.sbs_b;
+    OutT *Cb = (OutT *)p.C + bidx * p.cs_b;
+#pragma unroll
+    for (int c = 0; c < NI; ++c) {
+        const int64_t col = n0 + wn * 32 * NI + c * 32 + lr;
+        const bool cok = col < p.N;
+        float sbv[L];
+#pragma unroll
+        for (int j = 0; j < L; ++j) sbv[j] = cok ? sbb[j * p.sbs_l + col * p.sbs_n] : 0.0f;
+#pragma unroll
+        for (int a = 0; a < MI; ++a) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = m0 + wm * 32 * MI + a * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (cok && row < p.M) {
+                    OA out = (OA)0;
+#pragma unroll
+                    for (int i = 0; i < L; ++i) {
+                        const float sai = sab[i * p.sas_l + row * p.sas_m];
+#pragma unroll
+                        for (int j = 0; j < L; ++j) {
+                            const float x = MF::to_f32(acc[i][j][a][c][r]);
+                            const float t1 = x * sai;
+                            const float t2 = t1 * sbv[j];
+                            out = out + (OA)t2;
+                        }
+                    }
+                    Cb[row * p.cs_m + col * p.cs_n] = (OutT)out;
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// A-direct variant.  The four waves are stacked along M (workgroup tile
+// 128 x 32*NI); each wave streams ITS OWN 32 rows of every A slice from global
+// memory straight into VGPRs (no LDS), and only B, which all four waves share,
+// goes through the LDS ring by DMA.  Per 32-byte K step and CU this moves
+// 4 KB (L=4) of DMA writes and 16 KB of ds_read_b128 through the LDS instead
+// of 16 KB + 32 KB for a 2 x 2 wave grid, at the same L2-miss footprint.
+//
+// K order inside a 64-byte stage: lane (row, h) holds A bytes [32h, 32h+32)
+// as two 16-byte registers t = 0, 1; MFMA step t therefore contracts bytes
+// 32h + 16t of A with the same bytes of B (LDS chunk 2h + t).  Both operands
+// use the same map, so the dot products are unchanged (exactly so for int8).
+// ---------------------------------------------------------------------------
+#ifndef OZK_AD_STAGES
+#define OZK_AD_STAGES 4
+#endif
+constexpr int kAdStages = OZK_AD_STAGES;   // B ring depth = A register sets
+
+template <int L, int NI> struct AdShape {
+    static constexpr int BM = 128;
+    static constexpr int BN = 32 * NI;
+    static constexpr int B_ROWS = L * BN;
+    // LDS rows per stage, rounded up to 64 so every wave DMAs whole 1 KB
+    // windows; the padding rows are filled from out-of-range offsets (zeros)
+    // and never read
+    static constexpr int B_ROWS_LDS = (B_ROWS + 63) / 64 * 64;
+    static constexpr int STAGE = B_ROWS_LDS * kDmaRowBytes;   // LDS bytes per stage
+    static constexpr int DPW = STAGE / (4 * 1024);            // B DMA instrs per wave per stage
+    static constexpr int APW = 2 * L;                         // A loads per lane per stage
+    static constexpr int PER_STAGE = DPW + APW;               // vmcnt units per stage
+    static constexpr int LDS_BYTES = kAdStages * STAGE;
+    static_assert(STAGE % 4096 == 0, "B stage must be whole 1 KB windows per wave");
+    static_assert(2 * PER_STAGE * 1 < 64, "vmcnt range");
+};
+
+template <typename ST, int L, int NI, typename OutT>
+__global__ __launch_bounds__(256, 1) void cross_gemm_ad_kernel(GemmParams p, int group_m,
+                                                               uint32_t a_records,
+                                                               uint32_t b_records) {
+    using Sh = AdShape<L, NI>;
+    using MF = Mfma<ST>;
+    using Acc = typename MF::Acc;
+    using OA = typename OutAcc<OutT>::T;
+    constexpr int BM = Sh::BM, BN = Sh::BN;
+    constexpr int ES = (int)sizeof(ST);
+    constexpr uint32_t kOOB = 0x80000000u;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5, lr = lane & 31;
+
+    const int64_t tiles_m = (p.M + BM - 1) / BM;
+    const int64_t tiles_n = (p.N + BN - 1) / BN;
+    const int64_t tiles = tiles_m * tiles_n;
+    const int64_t g = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
+    const int64_t bidx = g / tiles;
+    const int64_t t = g % tiles;
+    const int64_t width = (int64_t)group_m * tiles_n;
+    const int64_t first_m = (t / width) * group_m;
+    const int64_t gsz = (tiles_m - first_m < group_m) ? (tiles_m - first_m) : group_m;
+    const int64_t tm = first_m + (t % width) % gsz;
+    const int64_t tn = (t % width) / gsz;
+    const int64_t m0 = tm * BM, n0 = tn * BN;
+
+    const uint32_t kbytes = (uint32_t)(p.K * ES);
+    const int nkb = (int)((kbytes + kDmaRowBytes - 1) / kDmaRowBytes);
+
+    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const char *)p.A + bidx * p.as_b * ES), (short)0, (int)a_records, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const char *)p.B + bidx * p.bs_b * ES), (short)0, (int)b_records, 0x00020000);
+
+    // A: this lane's row of every slice; kOOB past the last row
+    const int64_t arow = m0 + wave * 32 + lr;
+    uint32_t aoff[L];
+#pragma unroll
+    for (int i = 0; i < L; ++i)
+        aoff[i] = (arow < p.M) ? (uint32_t)(((int64_t)i * p.as_l + arow * p.as_m) * ES) + 32 * h
+                               : kOOB;
+    // B: DMA windows of this wave (16 rows of 64 bytes each)
+    uint32_t bsrc[Sh::DPW];
+    int bchunk[Sh::DPW];
+#pragma unroll
+    for (int q = 0; q < Sh::DPW; ++q) {
+        const int pos = (wave * Sh::DPW + q) * 64 + lane;
+        const int r = pos >> 2;
+        bchunk[q] = (pos & 3) ^ ((r >> 2) & 3);
+        const int j = r / BN;
+        const int64_t n = n0 + r % BN;
+        bsrc[q] = (r < Sh::B_ROWS && n < p.N)
+                      ? (uint32_t)(((int64_t)j * p.bs_l + n * p.bs_n) * ES) : kOOB;
+    }
+
+    i32x4 areg[kAdStages][L][2];
+    auto issue_stage = [&](int kb, i32x4 (&ar)[L][2]) {
+        char *dst = smem + (kb % kAdStages) * Sh::STAGE + wave * Sh::DPW * 1024;
+#pragma unroll
+        for (int q = 0; q < Sh::DPW; ++q) {
+            const uint32_t kofs = (uint32_t)kb * kDmaRowBytes + bchunk[q] * 16;
+            const uint32_t vo = (bsrc[q] == kOOB || kofs >= kbytes) ? kOOB : bsrc[q] + kofs;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rB, (__attribute__((address_space(3))) void *)(dst + q * 1024), 16, vo, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < L; ++i)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const uint32_t kofs = (uint32_t)kb * kDmaRowBytes + 32 * h + 16 * u;
+                const uint32_t vo =
+                    (aoff[i] == kOOB || kofs >= kbytes) ? kOOB : aoff[i] + kofs - 32 * h;
+                ar[i][u] = __builtin_bit_cast(
+                    i32x4, __builtin_amdgcn_raw_buffer_load_b128(rA, vo, 0, 0));
+            }
+    };
+
+    Acc acc[L][L][NI];
+#pragma unroll
+    for (int i = 0; i < L; ++i)
+#pragma unroll
+        for (int j = 0; j < L; ++j)
+#pragma unroll
+            for (int c = 0; c < NI; ++c) acc[i][j][c] = MF::zero();
+
+    // B fragments of one step: rows j*BN + c*32 + lr, chunk 2h + tt
+    struct BFr {
+        i32x4 b[L][NI];
+    };
+    auto read_b = [&](const char *buf, int tt, int r, BFr &f) {
+        const int j = r / NI, c = r % NI;
+        f.b[j][c] = *(const i32x4 *)(buf + dswz(j * BN + c * 32 + lr, 2 * h + tt));
+    };
+    constexpr int kReads = L * NI;
+    constexpr int kMfmas = L * L * NI;
+    auto step = [&](const i32x4 (&ar)[L][2], int tt, const BFr &cur, BFr &nxt,
+                    const char *nbuf, int ntt) {
+#pragma unroll
+        for (int q = 0; q < kMfmas; ++q) {
+            const int i = q / (L * NI), j = (q / NI) % L, c = q % NI;
+            acc[i][j][c] = MF::run(ar[i][tt], cur.b[j][c], acc[i][j][c]);
+            if (q < kReads) read_b(nbuf, ntt, q, nxt);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int q = kMfmas; q < kReads; ++q) read_b(nbuf, ntt, q, nxt);
+    };
+    // The K loop runs a multiple of DEPTH stages: stages past the end load
+    // only out-of-range offsets (zeros), so their MFMAs add nothing, and the
+    // loop body stays free of branches (which keeps the compiler's own wait
+    // counts for the A registers exact).
+    constexpr int D = kAdStages;
+    const int nkb_pad = (nkb + D - 1) / D * D;
+    BFr f0, f1;
+    // One stage: step 0 (its B fragments f0 already in registers) with the
+    // step-1 reads interleaved; wait for this wave's loads of stage kb + 1
+    // (the D - 2 later stages may stay in flight), drain its LDS reads and
+    // synchronise, which publishes every wave's DMA writes of stage kb + 1
+    // and frees the slot of stage kb; step 1 with the reads of stage kb + 1's
+    // step-0 fragments; then refill this stage's LDS slot and A register set
+    // (whose last MFMA was just issued) with stage kb + D.
+    auto stage = [&](int kb, i32x4 (&ar)[L][2]) {
+        step(ar, 0, f0, f1, smem + (kb % D) * Sh::STAGE, 1);
+        wait_vmcnt<(D - 2) * Sh::PER_STAGE>();
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0) only
+        exec_barrier();
+        step(ar, 1, f1, f0, smem + ((kb + 1) % D) * Sh::STAGE, 0);
+        issue_stage(kb + D, ar);
+    };
+
+    if (nkb > 0) {
+#pragma unroll
+        for (int s = 0; s < D; ++s) issue_stage(s, areg[s]);
+        wait_vmcnt<(D - 1) * Sh::PER_STAGE>();
+        exec_barrier();
+#pragma unroll
+        for (int q = 0; q < kReads; ++q) read_b(smem, 0, q, f0);
+    }
+    for (int kb = 0; kb < nkb_pad; kb += D) {
+#pragma unroll
+        for (int s = 0; s < D; ++s) stage(kb + s, areg[s]);
+    }
+    // the last D stages issued only zero loads; let them land before the LDS
+    // is handed to another workgroup
+    wait_vmcnt<0>();
+
+    // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
+    const float *sab = p.sa + bidx * p.sas_b;
+    const float *sbb = p.sb + bidx * p.sbs_b;
+    OutT *Cb = (OutT *)p.C + bidx * p.cs_b;
+#pragma unroll
+    for (int c = 0; c < NI; ++c) {
+        const int64_t col = n0 + c * 32 + lr;
+        const bool cok = col < p.N;
+        float sbv[L];
+#pragma unroll
+        for (int j = 0; j < L; ++j) sbv[j] = cok ? sbb[j * p.sbs_l + col * p.sbs_n] : 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t row = m0 + wave * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (cok && row < p.M) {
+                OA out = (OA)0;
+#pragma unroll
+                for (int i = 0; i < L; ++i) {
+                    const float sai = sab[i * p.sas_l + row * p.sas_m];
+#pragma unroll
+                    for (int j = 0; j < L; ++j) {
+                        const float x = MF::to_f32(acc[i][j][c][r]);
+                        const float t1 = x * sai;
+                        const float t2 = t1 * sbv[j];
+                        out = out + (OA)t2;
+                    }
+                }
+                Cb[row * p.cs_m + col * p.cs_n] = (OutT)out;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Pack kernel: any-stride slices -> K-contiguous, 16-byte padded rows.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void pack_kernel(PackParams p) {
@@ -296,14 +843,15 @@ hipError_t launch_pack(const PackParams &p, hipStream_t st) {
     return hipGetLastError();
 }
 
+static int64_t dma_extent(int64_t s_l, int64_t s_r, int L, int64_t rows, int64_t K, int es);
+
 // ---------------------------------------------------------------------------
 // Tile table (replaces the reference's Optuna search, ozaki_triton.py:263-304):
 // the wave tile is the largest whose L*L accumulators fit the register file
 // (L*L*MI*NI*16 <= 256 per lane), shrunk when the grid would leave CUs idle.
 // ---------------------------------------------------------------------------
 GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype) {
-    (void)slice_dtype;
-    GemmPlan plan{1, 1, 8};
+    GemmPlan plan{1, 1, 8, kGemmStaged};
     int mi = 1, ni = 1;
     if (L <= 1) { mi = 2; ni = 4; }
     else if (L == 2) { mi = 2; ni = 2; }
@@ -318,12 +866,92 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype) {
     }
     plan.mi = mi;
     plan.ni = ni;
+#ifdef OZK_EXP_GROUP_M
+    plan.group_m = OZK_EXP_GROUP_M;
+#else
     plan.group_m = 8;
+#endif
+    const int es = slice_dtype == 4 ? 1 : 2;
+    // OZK_GEMM_STAGED=1 selects the VGPR-staged kernel (the path operands
+    // beyond 2 GiB take), so tests can cover it at small sizes
+    // OZK_GEMM_KERNEL=staged|dma|ad forces a kernel (tests cover every one at
+    // small sizes); by default the 2 x 2 LDS-DMA kernel whenever both operands
+    // fit its 31-bit buffer offsets, else the VGPR-staged kernel
+    const bool fits = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es) >= 0 &&
+                      dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es) >= 0;
+    plan.kind = fits ? kGemmDMA : kGemmStaged;
+    const char *forced = getenv("OZK_GEMM_KERNEL");
+    if (forced && forced[0] == 's') plan.kind = kGemmStaged;
+    else if (forced && forced[0] == 'a' && fits) plan.kind = kGemmAD;
+#ifdef OZK_EXP_KIND
+    plan.kind = OZK_EXP_KIND;
+#endif
+    if (plan.kind == kGemmAD) plan.group_m = 2;
+#ifdef OZK_EXP_GROUP_M
+    plan.group_m = OZK_EXP_GROUP_M;
+#endif
     return plan;
+}
+
+// byte extent [0, bytes) one batch of a slice operand spans, or -1 if it does
+// not fit the 31-bit buffer offsets of the DMA kernel
+static int64_t dma_extent(int64_t s_l, int64_t s_r, int L, int64_t rows, int64_t K, int es) {
+    if (s_l < 0 || s_r < 0) return -1;
+    const int64_t e = ((int64_t)(L - 1) * s_l + (rows - 1) * s_r + K) * es;
+    return (e < ((int64_t)1 << 31) - 64) ? e : -1;
+}
+
+template <typename ST, int L, int MI, int NI, typename OutT>
+static hipError_t launch_dma(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
+    using Sh = DmaShape<L, MI, NI>;
+    auto kern = cross_gemm_dma_kernel<ST, L, MI, NI, OutT>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void *)kern,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           Sh::LDS_BYTES);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const int es = (int)sizeof(ST);
+    const int64_t ea = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es);
+    const int64_t eb = dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es);
+    const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
+    if (tiles == 0) return hipSuccess;
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(256), Sh::LDS_BYTES, st, p,
+                       plan.group_m, (uint32_t)ea, (uint32_t)eb);
+    return hipGetLastError();
+}
+
+template <typename ST, int L, int NI, typename OutT>
+static hipError_t launch_ad(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
+    using Sh = AdShape<L, NI>;
+    auto kern = cross_gemm_ad_kernel<ST, L, NI, OutT>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void *)kern,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           Sh::LDS_BYTES);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const int es = (int)sizeof(ST);
+    const int64_t ea = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es);
+    const int64_t eb = dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es);
+    const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
+    if (tiles == 0) return hipSuccess;
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(256), Sh::LDS_BYTES, st, p,
+                       plan.group_m, (uint32_t)ea, (uint32_t)eb);
+    return hipGetLastError();
 }
 
 template <typename ST, int L, int MI, int NI, typename OutT>
 static hipError_t launch_one(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
+    if (plan.kind == kGemmAD) {
+        constexpr int ANI = (L == 1) ? 8 : (L == 2) ? 4 : 1;
+        return launch_ad<ST, L, ANI, OutT>(p, plan, st);
+    }
+    if (plan.kind == kGemmDMA) return launch_dma<ST, L, MI, NI, OutT>(p, plan, st);
     using Sh = GemmShape<L, MI, NI>;
     auto kern = cross_gemm_kernel<ST, L, MI, NI, OutT>;
     static bool attr_set = false;   // idempotent; a racing second set is harmless

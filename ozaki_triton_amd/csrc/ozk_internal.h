@@ -51,9 +51,15 @@ struct GemmParams {
     int64_t batch, M, N, K;
 };
 
+enum GemmKind {
+    kGemmStaged = 0,  // global -> VGPR -> LDS, 2 x 2 waves (any operand extent)
+    kGemmDMA = 1,     // LDS-DMA ring for A and B, 2 x 2 waves
+    kGemmAD = 2       // A streamed into VGPRs, B by LDS-DMA, 4 x 1 waves
+};
 struct GemmPlan {
-    int mi, ni;       // wave tile = (32*mi) x (32*ni), workgroup tile = 2x2 waves
+    int mi, ni;       // 2 x 2 kernels: wave tile = (32*mi) x (32*ni)
     int group_m;      // tile-row group for L2 reuse
+    int kind;         // GemmKind; the LDS-DMA kernels need 31-bit operand extents
 };
 GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype);
 hipError_t launch_gemm(const GemmParams &p, const GemmPlan &plan, int L, int slice_dtype,

@@ -237,3 +237,20 @@ def test_ozaki_matmul_degenerate_shapes(gpu):
     with pytest.raises(ValueError):
         ozk.ozaki_matmul(torch.randn(4, 0, dtype=torch.float64, device=gpu),
                          torch.randn(0, 3, dtype=torch.float64, device=gpu), 2, torch.int8)
+
+
+@pytest.mark.parametrize("kernel", ["staged", "dma", "ad"])
+@pytest.mark.parametrize("L", [1, 2, 3, 4])
+def test_cross_gemm_each_kernel_bitexact(oracle, gpu, L, kernel, monkeypatch):
+    """Every cross-GEMM kernel, forced: the VGPR-staged one (taken when an
+    operand's extent exceeds the 31-bit buffer offsets of the LDS-DMA kernels),
+    the 2 x 2 LDS-DMA kernel and the A-direct kernel."""
+    import ozaki_triton_amd as ozk
+    monkeypatch.setenv("OZK_GEMM_KERNEL", kernel)
+    g = torch.Generator().manual_seed(77 + L)
+    As, BsT, sa, sb = _random_slices(g, 1, L, 100, 72, 1040, torch.int8)
+    C = ozk.cross_gemm(As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), L,
+                       torch.float64)
+    torch.cuda.synchronize()
+    want = oracle.cross_gemm(to_np(As[0]), to_np(BsT[0]), to_np(sa[0]), to_np(sb[0]), "float64")
+    assert_bitwise_equal(to_np(C)[0], want, f"{kernel} L{L}")
