@@ -110,14 +110,14 @@ int ozk_split_workspace_bytes(int x_dtype, int64_t batch, int64_t rows, int64_t 
     if (num_splits < 0 || num_splits > OZK_MAX_SPLITS) return OZK_ERR_SPLITS;
     if (batch < 0 || rows < 0 || K < 0) return OZK_ERR_SHAPE;
     *bytes_out = 0;
-    if (num_splits <= 1) return OZK_OK;
+    if (num_splits == 0) return OZK_OK;
     // the plan depends on pointer alignment only through 16-byte checks; a
     // 256-byte aligned stand-in pointer gives the plan of any aligned tensor
     ozk::SplitParams p = make_split_params((const void *)256, batch, rows, K, x_strides,
                                            num_splits, 1, (void *)256, slice_strides, nullptr,
                                            x_strides);
     const ozk::SplitPlan plan = ozk::plan_split(p, x_dtype, slice_dtype);
-    if (plan.path == ozk::kSplitGeneric) *bytes_out = (size_t)(batch * rows * K * 4);
+    *bytes_out = ozk::split_workspace_bytes(p, plan, x_dtype);
     return OZK_OK;
 }
 
@@ -136,8 +136,8 @@ int ozk_split(const void *X, int x_dtype, int64_t batch, int64_t rows, int64_t K
     ozk::SplitParams p = make_split_params(X, batch, rows, K, x_strides, num_splits, alpha,
                                            slices, slice_strides, scales, scale_strides);
     const ozk::SplitPlan plan = ozk::plan_split(p, x_dtype, slice_dtype);
-    if (plan.path == ozk::kSplitGeneric && num_splits > 1) {
-        const size_t need = (size_t)(batch * rows * K * 4);
+    const size_t need = ozk::split_workspace_bytes(p, plan, x_dtype);
+    if (need > 0) {
         if (!workspace || workspace_bytes < need) return OZK_ERR_WORKSPACE;
         p.resid = (float *)workspace;
     }

@@ -19,10 +19,11 @@ struct SplitParams {
     int64_t ss_b, ss_l, ss_r, ss_k;
     float *scales;
     int64_t cs_b, cs_l, cs_r;
-    float *resid;  // generic path only: fp32 residual [batch, rows, K]
+    float *resid;  // workspace: fp32 residual [batch, rows, K] (generic path) or the
+                   // transposed operand [batch, rows, K] (transpose + row path)
 };
 
-enum SplitPath { kSplitRows = 0, kSplitStrip = 1, kSplitGeneric = 2 };
+enum SplitPath { kSplitRows = 0, kSplitStrip = 1, kSplitGeneric = 2, kSplitTransposeRows = 3 };
 
 // Chooses the split kernel for p (x_dtype: 0 = f64, 1 = f32; slice: 4 = i8,
 // 2 = f16).  Returns the path and, for the resident paths, the variant index.
@@ -31,6 +32,9 @@ struct SplitPlan {
     int variant;
 };
 SplitPlan plan_split(const SplitParams &p, int x_dtype, int slice_dtype);
+// scratch the plan needs: fp32 residual (generic path, L > 1) or the
+// transposed operand (transpose + row path)
+size_t split_workspace_bytes(const SplitParams &p, const SplitPlan &plan, int x_dtype);
 hipError_t launch_split(const SplitParams &p, const SplitPlan &plan, int x_dtype,
                         int slice_dtype, hipStream_t stream);
 

@@ -364,6 +364,57 @@ __global__ __launch_bounds__(256) void split_generic_kernel(SplitParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// Transpose of a row-contiguous operand (xs_r == 1, the B^T view) into a
+// K-contiguous workspace [batch, rows, K], for K too long for the strip
+// kernel; the row kernel then splits the workspace.  64 x 64 tiles through
+// LDS: loads are 16 bytes per lane along the rows, stores 16 bytes along K.
+// ---------------------------------------------------------------------------
+template <typename XT>
+__global__ __launch_bounds__(256) void transpose_kernel(const XT *__restrict__ X, int64_t batch,
+                                                        int64_t rows, int64_t K, int64_t xs_b,
+                                                        int64_t xs_k, XT *__restrict__ T) {
+    constexpr int TILE = 64;
+    constexpr int VEC = 16 / (int)sizeof(XT);
+    __shared__ XT tile[TILE][TILE + 1];
+    const int64_t tiles_r = (rows + TILE - 1) / TILE;
+    const int64_t tiles_k = (K + TILE - 1) / TILE;
+    const int64_t tb = blockIdx.x;
+    const int64_t b = tb / (tiles_r * tiles_k);
+    const int64_t rem = tb % (tiles_r * tiles_k);
+    const int64_t r0 = (rem % tiles_r) * TILE;
+    const int64_t k0 = (rem / tiles_r) * TILE;
+    const XT *xb = X + b * xs_b;
+    // load: lane covers VEC consecutive rows of one k
+    constexpr int LPR = TILE / VEC;              // lanes per k-row of the tile
+    constexpr int KPP = 256 / LPR;               // k-rows per pass
+    const int lr = threadIdx.x % LPR, lk = threadIdx.x / LPR;
+#pragma unroll
+    for (int kk = 0; kk < TILE; kk += KPP) {
+        const int64_t k = k0 + kk + lk;
+        const int64_t r = r0 + lr * VEC;
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) {
+            XT v = (XT)0;
+            if (k < K && r + u < rows) v = xb[k * xs_k + r + u];
+            tile[kk + lk][lr * VEC + u] = v;
+        }
+    }
+    __syncthreads();
+    // store: lane covers VEC consecutive k of one row
+    XT *tb_out = T + b * rows * K;
+#pragma unroll
+    for (int rr = 0; rr < TILE; rr += KPP) {
+        const int64_t r = r0 + rr + lk;
+        const int64_t k = k0 + lr * VEC;
+        if (r < rows) {
+#pragma unroll
+            for (int u = 0; u < VEC; ++u)
+                if (k + u < K) tb_out[r * K + k + u] = tile[lr * VEC + u][rr + lk];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Planning and launch.
 // Row variants (GW waves per row, RPB rows per block, NC chunks): capacity
 // 4*NC*64*GW elements.  fp64 rows keep at most 32 values per lane.
@@ -418,7 +469,23 @@ SplitPlan plan_split(const SplitParams &p, int x_dtype, int slice_dtype) {
             if (p.K <= (int64_t)c.kpt * c.nt / 2) return {kSplitStrip, i};
         }
     }
+    // row-contiguous operand with a K too long for a resident strip: transpose
+    // into the workspace, then the row kernel (if the row fits)
+    if (k4 && slice_ok && p.xs_r == 1) {
+        for (int i = 0; i < kNumRowCfgs; ++i) {
+            const RowCfg &c = kRowCfgs[i];
+            if (x_dtype == 0 && c.nc > 8) continue;
+            if (p.K <= (int64_t)4 * c.nc * 64 * c.gw) return {kSplitTransposeRows, i};
+        }
+    }
     return {kSplitGeneric, 0};
+}
+
+size_t split_workspace_bytes(const SplitParams &p, const SplitPlan &plan, int x_dtype) {
+    const int64_t n = p.batch * p.rows * p.K;
+    if (plan.path == kSplitTransposeRows) return (size_t)(n * (x_dtype == 0 ? 8 : 4));
+    if (plan.path == kSplitGeneric && p.L > 1) return (size_t)(n * 4);
+    return 0;
 }
 
 template <typename XT, typename ST>
@@ -469,6 +536,20 @@ static hipError_t launch_typed(const SplitParams &p, const SplitPlan &plan, hipS
     switch (plan.path) {
     case kSplitRows: return launch_rows<XT, ST>(p, plan.variant, st);
     case kSplitStrip: return launch_strip<XT, ST>(p, plan.variant, st);
+    case kSplitTransposeRows: {
+        XT *T = (XT *)p.resid;   // workspace [batch, rows, K]
+        const int64_t tiles = p.batch * ((p.rows + 63) / 64) * ((p.K + 63) / 64);
+        hipLaunchKernelGGL((transpose_kernel<XT>), dim3((unsigned)tiles), dim3(256), 0, st,
+                           (const XT *)p.X, p.batch, p.rows, p.K, p.xs_b, p.xs_k, T);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        SplitParams q = p;
+        q.X = T;
+        q.xs_b = p.rows * p.K;
+        q.xs_r = p.K;
+        q.xs_k = 1;
+        return launch_rows<XT, ST>(q, plan.variant, st);
+    }
     default:
         hipLaunchKernelGGL((split_generic_kernel<XT, ST>), dim3((unsigned)(p.batch * p.rows)),
                            dim3(256), 0, st, p);

@@ -103,6 +103,13 @@ def test_split_workspace_zero_on_resident_paths():
     assert L.ozk_split_workspace_bytes(_lib.OZK_F64, 1, N, K, _lib.i64arr([K * N, 1, N]), 4,
                                        _lib.OZK_I8, sl, ctypes.byref(nb)) == 0
     assert nb.value == 0
+    # a column longer than the resident strip holds is transposed into the
+    # workspace first (config 5: fp32, K = 65536)
+    K5, N5 = 65536, 1024
+    sl5 = _lib.i64arr([3 * N5 * K5, N5 * K5, K5, 1])
+    assert L.ozk_split_workspace_bytes(_lib.OZK_F32, 1, N5, K5, _lib.i64arr([K5 * N5, 1, N5]),
+                                       3, _lib.OZK_I8, sl5, ctypes.byref(nb)) == 0
+    assert nb.value == N5 * K5 * 4
 
 
 def test_cross_gemm_abi_checks_and_workspace():

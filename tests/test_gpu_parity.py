@@ -254,3 +254,16 @@ def test_cross_gemm_each_kernel_bitexact(oracle, gpu, L, kernel, monkeypatch):
     torch.cuda.synchronize()
     want = oracle.cross_gemm(to_np(As[0]), to_np(BsT[0]), to_np(sa[0]), to_np(sb[0]), "float64")
     assert_bitwise_equal(to_np(C)[0], want, f"{kernel} L{L}")
+
+
+@pytest.mark.parametrize("xdt,sdt", COMBOS)
+def test_split_transpose_path(oracle, gpu, xdt, sdt):
+    """Column splits (B^T view) whose K exceeds the resident strip: transposed
+    into the workspace, then the row kernel (config 5's B is 65536 long)."""
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(11)
+    K = 20000 if xdt == torch.float64 else 65536
+    B = torch.randn(1, K, 40, generator=g, dtype=torch.float64)
+    B[torch.rand(1, K, 40, generator=g) < 0.01] *= 1e4
+    Bd = B.to(xdt).to(gpu)
+    _check_split(oracle, ozk, Bd.transpose(-1, -2), 3, sdt, f"transpose {xdt} {sdt}")
