@@ -104,6 +104,22 @@ def cpu_torch_matmul(A_cpu, B_cpu, reps):
     return flops / t / 1e12, ncores, torch.get_num_threads()
 
 
+def measured_traffic(config: str, kernel_prefix: str):
+    """HBM-side bytes per launch of a kernel, from the rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes summarised in profiles/ (scaled by the copy-kernel
+    calibration recorded there), or None when that config was not measured."""
+    path = os.path.join(ROOT, "profiles", "cross_gemm_traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+    except (OSError, ValueError):
+        return None
+    for name, rec in data.get("configs", {}).get(config, {}).items():
+        if name.startswith(kernel_prefix):
+            return int(rec["traffic_bytes"])
+    return None
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -246,7 +262,7 @@ def main():
             "peak": peak,
             "unit": unit_c,
             "frac": round(achieved / peak, 4),
-            "traffic": None,
+            "traffic": measured_traffic(args.config, "ozk::cross_gemm_dma_kernel"),
             "avg_ms": round(t_cross, 4),
         },
         "split": {

@@ -259,14 +259,8 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_kernel(GemmParams p, int gr
 // num_records, which the hardware returns as zeros.
 // ---------------------------------------------------------------------------
 constexpr int kDmaRowBytes = 64;     // A-direct kernel stage rows
-#ifndef OZK_DMA_ROW
-#define OZK_DMA_ROW 128
-#endif
-constexpr int kDmaRB = OZK_DMA_ROW;  // 2 x 2 DMA kernel stage rows (64 or 128 bytes of K)
-#ifndef OZK_DMA_STAGES
-#define OZK_DMA_STAGES (kDmaRB == 64 ? 4 : 2)
-#endif
-constexpr int kDmaStages = OZK_DMA_STAGES;
+constexpr int kDmaRB = 128;          // 2 x 2 DMA kernel stage rows (bytes of K; 64 also works)
+constexpr int kDmaStages = (kDmaRB == 64) ? 4 : 2;   // LDS ring slots
 
 template <int L, int MI, int NI> struct DmaShape {
     static constexpr int BM = 64 * MI;
@@ -334,12 +328,7 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_dma_kernel(GemmParams p, in
     const int64_t gsz = (tiles_m - first_m < group_m) ? (tiles_m - first_m) : group_m;
     const int64_t tm = first_m + (t % width) % gsz;
     const int64_t tn = (t % width) / gsz;
-#ifdef OZK_EXP_SAME_TILE
-    const int64_t m0 = 0, n0 = 0;   // timing experiment: every workgroup on tile 0
-    (void)tm; (void)tn;
-#else
     const int64_t m0 = tm * BM, n0 = tn * BN;
-#endif
 
     const uint32_t kbytes = (uint32_t)(p.K * ES);
     const int nkb = (int)((kbytes + kDmaRB - 1) / kDmaRB);
@@ -424,27 +413,17 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_dma_kernel(GemmParams p, in
     // MFMAs of `cur`, with the reads of the next step's fragments into `nxt`
     // interleaved one per MFMA, so no MFMA waits on a read issued after the
     // reads of its own operands and the LDS latency hides under the MFMAs.
-    // dma_kb >= 0: also issue the DMA loads of stage dma_kb, spread over the
-    // MFMAs (one per MFMA from the second on) instead of in one burst.
-    auto step = [&](const Frags &cur, Frags &nxt, const char *nbuf, int nkk, int dma_kb) {
+    auto step = [&](const Frags &cur, Frags &nxt, const char *nbuf, int nkk) {
 #pragma unroll
         for (int q = 0; q < kMfmas; ++q) {
             const int i = q / (L * MI * NI), j = (q / (MI * NI)) % L;
             const int a = (q / NI) % MI, c = q % NI;
             acc[i][j][a][c] = MF::run(cur.a[i][a], cur.b[j][c], acc[i][j][a][c]);
             if (q < kReads) read_one(nbuf, nkk, q, nxt);
-#ifdef OZK_EXP_SPREAD_DMA
-            if (q >= 1 && q - 1 < Sh::LPS && dma_kb >= 0) issue_one(dma_kb, q - 1);
-#endif
             __builtin_amdgcn_sched_barrier(0);   // keep this order
         }
 #pragma unroll
         for (int q = kMfmas; q < kReads; ++q) read_one(nbuf, nkk, q, nxt);
-#ifdef OZK_EXP_SPREAD_DMA
-#pragma unroll
-        for (int q = kMfmas; q < Sh::LPS + 1; ++q)
-            if (dma_kb >= 0) issue_one(dma_kb, q - 1);
-#endif
     };
     // stage kb has landed once at most the loads of the stages issued after it
     // are outstanding; then the barrier publishes every wave's DMA writes
@@ -480,30 +459,19 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_dma_kernel(GemmParams p, in
         // fragments; f0 / f1 alternate
 #pragma unroll
         for (int kk = 0; kk + 1 < STEPS; ++kk) {
-            if (kk % 2 == 0) step(f0, f1, buf, kk + 1, -1);
-            else step(f1, f0, buf, kk + 1, -1);
+            if (kk % 2 == 0) step(f0, f1, buf, kk + 1);
+            else step(f1, f0, buf, kk + 1);
         }
-        int dma_kb = -1;
         if (kb + 1 < nkb) {
             stage_ready(kb + 1);
             // the ring slot of stage kb + DMA_STAGES is the one of stage kb,
             // whose reads every wave completed before this barrier
-            if (kb + kDmaStages < nkb) dma_kb = kb + kDmaStages;
-#ifdef OZK_EXP_HALF_DMA
-            if (dma_kb & 1) dma_kb = -1;
-#endif
-#ifdef OZK_EXP_NO_LOOP_LOADS
-            dma_kb = -1;
-#endif
-#ifndef OZK_EXP_SPREAD_DMA
-            if (dma_kb >= 0) issue_stage(dma_kb);
-            dma_kb = -1;
-#endif
+            if (kb + kDmaStages < nkb) issue_stage(kb + kDmaStages);
         }
         // last step: reads the next stage's step-0 fragments (on the last
         // stage, unused data from a slot that is not being written)
-        if ((STEPS - 1) % 2 == 0) step(f0, f1, smem + ((kb + 1) % kDmaStages) * Sh::STAGE, 0, dma_kb);
-        else step(f1, f0, smem + ((kb + 1) % kDmaStages) * Sh::STAGE, 0, dma_kb);
+        if ((STEPS - 1) % 2 == 0) step(f0, f1, smem + ((kb + 1) % kDmaStages) * Sh::STAGE, 0);
+        else step(f1, f0, smem + ((kb + 1) % kDmaStages) * Sh::STAGE, 0);
         if ((STEPS - 1) % 2 == 0) {   // next stage's step 0 expects its fragments in f0
 #pragma unroll
             for (int i = 0; i < L; ++i)
@@ -516,23 +484,6 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_dma_kernel(GemmParams p, in
         }
     }
 
-#ifdef OZK_EXP_NO_EPILOGUE
-    {   // timing experiment: keep the accumulators alive, store one word per lane
-        int sum = 0;
-#pragma unroll
-        for (int i = 0; i < L; ++i)
-#pragma unroll
-            for (int j = 0; j < L; ++j)
-#pragma unroll
-                for (int a = 0; a < MI; ++a)
-#pragma unroll
-                    for (int c = 0; c < NI; ++c)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) sum += (int)acc[i][j][a][c][r];
-        if (m0 + tid < p.M) ((OutT *)p.C)[(m0 + tid) * p.cs_m + n0] = (OutT)sum;
-        return;
-    }
-#endif
     // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
     const float *sab = p.sa + bidx * p.sas_b;
     const float *sbb = p.sb + bidx * p.sbs_b;
@@ -582,10 +533,7 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_dma_kernel(GemmParams p, in
 // 32h + 16t of A with the same bytes of B (LDS chunk 2h + t).  Both operands
 // use the same map, so the dot products are unchanged (exactly so for int8).
 // ---------------------------------------------------------------------------
-#ifndef OZK_AD_STAGES
-#define OZK_AD_STAGES 4
-#endif
-constexpr int kAdStages = OZK_AD_STAGES;   // B ring depth = A register sets
+constexpr int kAdStages = 4;        // B ring depth = A register sets
 
 template <int L, int NI> struct AdShape {
     static constexpr int BM = 128;
@@ -866,11 +814,7 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype) {
     }
     plan.mi = mi;
     plan.ni = ni;
-#ifdef OZK_EXP_GROUP_M
-    plan.group_m = OZK_EXP_GROUP_M;
-#else
     plan.group_m = 8;
-#endif
     const int es = slice_dtype == 4 ? 1 : 2;
     // OZK_GEMM_STAGED=1 selects the VGPR-staged kernel (the path operands
     // beyond 2 GiB take), so tests can cover it at small sizes
@@ -883,13 +827,7 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype) {
     const char *forced = getenv("OZK_GEMM_KERNEL");
     if (forced && forced[0] == 's') plan.kind = kGemmStaged;
     else if (forced && forced[0] == 'a' && fits) plan.kind = kGemmAD;
-#ifdef OZK_EXP_KIND
-    plan.kind = OZK_EXP_KIND;
-#endif
     if (plan.kind == kGemmAD) plan.group_m = 2;
-#ifdef OZK_EXP_GROUP_M
-    plan.group_m = OZK_EXP_GROUP_M;
-#endif
     return plan;
 }
 
