@@ -98,6 +98,20 @@ OZK_DEV int quant_i8(float q) {
     return (int)t;
 }
 
+// Round half away from zero of an fp32 value q with |q| <= 2^8 (an exact
+// function of q): trunc(q) +/- 1 when |q - trunc(q)| >= 0.5.  This equals
+// trunc(fl64(q +/- 0.5)) for every fp32 q: q has at most 24 significant bits
+// and |q| < 2^9, so q +/- 0.5 is exact in binary64.  The result is returned
+// as an integer value in float, already limited to 127 from above (q never
+// goes below -2^alpha (1 + 2^-18), whose rounding is -128 anyway).
+OZK_DEV float round_away_exact(float q) {
+    const float t = truncf(q);
+    const float d = q - t;   // exact
+    float r = t;
+    if (fabsf(d) >= 0.5f) r = t + copysignf(1.0f, q);
+    return fminf(r, 127.0f);
+}
+
 // Single round-to-nearest-even conversions to binary16 (bit patterns), written
 // with integer arithmetic so the result does not depend on the denormal mode.
 OZK_DEV uint32_t f64_to_f16_bits(double x) {

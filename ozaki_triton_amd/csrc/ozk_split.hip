@@ -1,5 +1,4 @@
-// ozk_split.hip -- the split of ozaki_triton.py:137-211 as bandwidth-bound
-// gfx950 kernels.
+// ozk_split.hip -- the split of ozaki_triton.py:137-211 as gfx950 kernels.
 //
 // For every operand row (a row of A, or a column of B seen through B^T) and
 // every level l < L:
@@ -9,15 +8,38 @@
 //   slice = int8: trunc(clamp(fl(q +/- 0.5), -128, 127));  fp16: RN(q)
 //   src <- fl32(src - slice * s)   (the reference's fp32 residual buffer)
 //
+// Arithmetic per element (bit-identical to the above, fewer instructions):
+//   level 0, fp64 input   q = x * 2^(alpha-E) and t = fl64(q +/- 0.5) in fp64;
+//                         residual fma(-slice, s, x) rounded to fp64 then fp32
+//                         (the product is exact, so this is fl32(fl64(x - slice*s))).
+//   level >= 1, fp64 input: src is an fp32 residual r.  q = r * 2^(alpha-E)
+//                         is exact in fp32 (or below 2^-126, where the slice
+//                         is 0 either way), so q is computed with ldexp in
+//                         fp32; fl64(q +/- 0.5) is exact, and trunc of it
+//                         equals trunc(fl32(q +/- c)) with c = 0.5 - 2^-25
+//                         for every fp32 q (c keeps q = 0.5 - 2^-25 from
+//                         rounding up to 1; for |q| >= 0.5 subtracting 2^-25
+//                         moves no sum across an integer).  The residual
+//                         r - slice*s is exact in fp32 (for |q| >= 0.5 it is a
+//                         multiple of ulp(r) not above |r|; else it is r), so
+//                         one fp32 fma gives it.
+//   fp32 input (RES = fp32): q = ldexp(x, alpha-E) is the correctly rounded
+//                         quotient; t = fl32(q +/- 0.5) as in the reference;
+//                         residual fma(-slice, s, x) = fl32(x - fl32(slice*s))
+//                         because slice*s is exact.
+//   fp16 slices: RN(q) from fp64 at level 0 of fp64 input (integer rounding);
+//                elsewhere q is an fp32 value and the hardware RNE conversion
+//                rounds it once; slice*s is exact in fp32 in every case.
+//
 // Three kernels:
 //   split_rows_kernel   row-resident, for K-contiguous rows (A).  A group of
 //                       64*GW lanes owns one row; the row stays in VGPRs across
 //                       all levels, so X is read from HBM once and each slice
 //                       written once.
 //   split_strip_kernel  column-strip-resident, for row-contiguous operands
-//                       (the B^T view).  A workgroup owns W adjacent columns of
-//                       B for all K; loads are 16 B per lane along N, and each
-//                       lane holds 4 consecutive k per column so that int8 /
+//                       (the B^T view).  A workgroup owns the VEC adjacent
+//                       columns one 16-byte load covers, for all K; each lane
+//                       holds 4 consecutive k of every column so that int8 /
 //                       fp16 slices leave as 4-/8-byte stores along K.
 //   split_generic_kernel any strides and any K: one workgroup per row,
 //                       multi-pass over K with an fp32 residual in workspace
@@ -30,59 +52,98 @@ namespace ozk {
 typedef double dbl2 __attribute__((ext_vector_type(2)));
 typedef float flt4 __attribute__((ext_vector_type(4)));
 
-template <typename XT> struct ResOf;
-template <> struct ResOf<double> { using R = double; };
-template <> struct ResOf<float> { using R = float; };
+// ---------------------------------------------------------------------------
+// Per-level constants from the row maximum m (wave-uniform).
+// ---------------------------------------------------------------------------
+struct LevelScale {
+    float s;       // 2^(E - alpha), the stored scale
+    int up;        // alpha - E
+    double s64;    // s as double
+    double inv64;  // 2^(alpha - E) as double (always a normal double)
+};
+OZK_DEV LevelScale level_scale(float m, int alpha) {
+    const float mu = fmaxf(1e-38f, m);
+    const int ema = ceil_log2_f32(mu) - alpha;
+    LevelScale c;
+    c.s = pow2f(ema);
+    c.up = -ema;
+    c.s64 = (double)c.s;
+    c.inv64 = pow2d(-ema);
+    return c;
+}
 
-OZK_DEV ScaleF64 make_scale(int e_minus_alpha, double) { return make_scale_f64(e_minus_alpha); }
-OZK_DEV ScaleF32 make_scale(int e_minus_alpha, float) { return make_scale_f32(e_minus_alpha); }
+// Quantisation of one value at one level.  MODE: kQF64 = level 0 of fp64
+// input; kQExact = level >= 1 of fp64 input (fp32 residuals, exact fp32
+// arithmetic); kQF32 = every level of fp32 input.  Returns the slice bits
+// (int8 value in the low byte, or fp16 bits) and writes the fp32 residual.
+enum { kQF64 = 0, kQExact = 1, kQF32 = 2 };
+template <typename ST, int MODE> struct Quant;
 
-// Quantise one value.  Returns the slice bit pattern (int8 in the low byte or
-// fp16 bits) and writes the dequantised slice value (exact in R) to *deq.
-template <typename ST> struct Quant;
-template <> struct Quant<int8_t> {
-    template <typename R> OZK_DEV static uint32_t run(R q, R *deq) {
-        int v = quant_i8(q);
-        *deq = (R)v;
-        return (uint32_t)v & 0xFFu;
+template <> struct Quant<int8_t, kQF64> {
+    OZK_DEV static uint32_t run(double x, const LevelScale &c, float *res) {
+        const double q = x * c.inv64;
+        // |q| <= 2^7 (1 + 2^-18): the sum stays above -129, so truncation
+        // alone gives the reference's lower clamp
+        const double t = fmin(q + __builtin_copysign(0.5, q), 127.0);
+        const int k = (int)t;
+        *res = (float)__builtin_fma(-(double)k, c.s64, x);
+        return (uint32_t)k;
     }
 };
-template <> struct Quant<_Float16> {
-    OZK_DEV static uint32_t run(double q, double *deq) {
-        uint32_t h = f64_to_f16_bits(q);
-        *deq = (double)f16_bits_to_f32(h);
-        return h;
+template <> struct Quant<int8_t, kQExact> {
+    OZK_DEV static uint32_t run(float r, const LevelScale &c, float *res) {
+        const float q = __builtin_ldexpf(r, c.up);
+        const float t = fminf(__builtin_truncf(q + __builtin_copysignf(0x1.fffffep-2f, q)), 127.0f);
+        *res = __builtin_fmaf(-t, c.s, r);
+        return (uint32_t)(int)t;
     }
-    OZK_DEV static uint32_t run(float q, float *deq) {
-        uint32_t h = f32_to_f16_bits(q);
-        *deq = f16_bits_to_f32(h);
+};
+template <> struct Quant<int8_t, kQF32> {
+    OZK_DEV static uint32_t run(float x, const LevelScale &c, float *res) {
+        const float q = __builtin_ldexpf(x, c.up);
+        const float t = __builtin_truncf(
+            __builtin_amdgcn_fmed3f(q + __builtin_copysignf(0.5f, q), -128.0f, 127.0f));
+        *res = __builtin_fmaf(-t, c.s, x);
+        return (uint32_t)(int)t;
+    }
+};
+template <> struct Quant<_Float16, kQF64> {
+    OZK_DEV static uint32_t run(double x, const LevelScale &c, float *res) {
+        const double q = x * c.inv64;
+        const uint32_t h = f64_to_f16_bits(q);
+        const double d = (double)f16_bits_to_f32(h);
+        *res = (float)__builtin_fma(-d, c.s64, x);
         return h;
     }
 };
+template <int MODE> struct QuantF16F32 {
+    OZK_DEV static uint32_t run(float x, const LevelScale &c, float *res) {
+        const float q = __builtin_ldexpf(x, c.up);
+        const _Float16 h = (_Float16)q;
+        *res = __builtin_fmaf(-(float)h, c.s, x);
+        return (uint32_t)__builtin_bit_cast(uint16_t, h);
+    }
+};
+template <> struct Quant<_Float16, kQExact> : QuantF16F32<kQExact> {};
+template <> struct Quant<_Float16, kQF32> : QuantF16F32<kQF32> {};
 
-// fl32(src - deq * s) evaluated in R, then widened back to R.
-OZK_DEV double next_residual(double src, double deq, float s) {
-    double prod = deq * (double)s;
-    return (double)(float)(src - prod);
-}
-OZK_DEV float next_residual(float src, float deq, float s) {
-    float prod = deq * s;
-    return src - prod;
-}
+template <typename XT> struct Modes;
+template <> struct Modes<double> { static constexpr int first = kQF64, rest = kQExact; };
+template <> struct Modes<float> { static constexpr int first = kQF32, rest = kQF32; };
 
 // Store 4 consecutive slice values (k .. k+3) of one row.
 template <typename ST> struct Store4;
 template <> struct Store4<int8_t> {
     OZK_DEV static void run(void *base, int64_t off, const uint32_t v[4]) {
-        uint32_t w = v[0] | (v[1] << 8) | (v[2] << 16) | (v[3] << 24);
+        const uint32_t w = __builtin_amdgcn_perm(v[1], v[0], 0x0c0c0400u) |
+                           __builtin_amdgcn_perm(v[3], v[2], 0x04000c0cu);
         *(uint32_t *)((int8_t *)base + off) = w;
     }
 };
 template <> struct Store4<_Float16> {
     OZK_DEV static void run(void *base, int64_t off, const uint32_t v[4]) {
-        uint64_t w = (uint64_t)v[0] | ((uint64_t)v[1] << 16) | ((uint64_t)v[2] << 32) |
-                     ((uint64_t)v[3] << 48);
-        *(uint64_t *)((_Float16 *)base + off) = w;
+        const uint32_t lo = v[0] | (v[1] << 16), hi = v[2] | (v[3] << 16);
+        *(uint64_t *)((_Float16 *)base + off) = (uint64_t)lo | ((uint64_t)hi << 32);
     }
 };
 template <typename ST> OZK_DEV void store1(void *base, int64_t off, uint32_t v) {
@@ -111,10 +172,32 @@ OZK_DEV void loadvec(const float *p, float v[4]) {
     v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
 }
 
-OZK_DEV float wave_max(float m) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    return m;
+OZK_DEV float absf(double x) { return (float)fabs(x); }   // fl32(|x|)
+OZK_DEV float absf(float x) { return fabsf(x); }
+
+// Maximum of non-negative values over the 64 lanes of a wave, returned
+// wave-uniform.  DPP row reductions, then the row broadcasts of GFX9.
+template <int CTRL, int ROWS> OZK_DEV float dpp_max(float v) {
+    const int o = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROWS,
+                                              0xF, false);
+    return fmaxf(v, __int_as_float(o));
+}
+OZK_DEV float wave_max(float v) {
+    v = dpp_max<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
+    v = dpp_max<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
+    v = dpp_max<0x141, 0xF>(v);   // row_half_mirror
+    v = dpp_max<0x140, 0xF>(v);   // row_mirror: every lane holds its row's max
+    v = dpp_max<0x142, 0xA>(v);   // row_bcast15 into rows 1 and 3
+    v = dpp_max<0x143, 0xC>(v);   // row_bcast31 into rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Workgroup barrier for LDS exchanges: completes this wave's LDS accesses,
+// then s_barrier.  Unlike __syncthreads() it does not wait for outstanding
+// global stores (the previous level's slices).
+OZK_DEV void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
 }
 
 // ---------------------------------------------------------------------------
@@ -122,13 +205,27 @@ OZK_DEV float wave_max(float m) {
 // global row blockIdx.x*RPB + g.  Lane t of a group holds elements
 // (c*G + t)*4 + {0..3} for c < NC, so each wave load covers 1 KB (fp64: 2 KB)
 // of contiguous row and each wave store 256 B (int8) of contiguous slice.
+// Level 0 quantises the input values; levels >= 1 the fp32 residuals.
 // Requirements (checked on the host): xs_k == 1, ss_k == 1, K % 4 == 0, X rows
 // 16-byte aligned, slice rows 4-byte (int8) / 8-byte (fp16) aligned,
 // K <= 4 * NC * G.
 // ---------------------------------------------------------------------------
+template <int GW, int RPB>
+OZK_DEV float row_max(float m, float (*red)[RPB][GW], int buf, int grp, int t) {
+    m = wave_max(m);
+    if constexpr (GW > 1) {
+        if ((t & 63) == 0) red[buf][grp][t / 64] = m;
+        lds_barrier();
+        float r = red[buf][grp][0];
+#pragma unroll
+        for (int w = 1; w < GW; ++w) r = fmaxf(r, red[buf][grp][w]);
+        m = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(r)));
+    }
+    return m;
+}
+
 template <typename XT, typename ST, int GW, int RPB, int NC>
 __global__ __launch_bounds__(64 * GW * RPB) void split_rows_kernel(SplitParams p) {
-    using R = typename ResOf<XT>::R;
     constexpr int G = 64 * GW;
     constexpr int NE = 4 * NC;
     __shared__ float red[2][RPB][GW];
@@ -136,7 +233,6 @@ __global__ __launch_bounds__(64 * GW * RPB) void split_rows_kernel(SplitParams p
     const int tid = threadIdx.x;
     const int grp = tid / G;
     const int t = tid % G;
-    const int wave = t / 64;
     const int64_t nrows = p.batch * p.rows;
     const int64_t grow = (int64_t)blockIdx.x * RPB + grp;
     const bool active = grow < nrows;
@@ -145,8 +241,9 @@ __global__ __launch_bounds__(64 * GW * RPB) void split_rows_kernel(SplitParams p
 
     const XT *xrow = (const XT *)p.X + b * p.xs_b + r * p.xs_r;
     const int64_t srow = b * p.ss_b + r * p.ss_r;
+    float *srow_scale = p.scales + b * p.cs_b + r * p.cs_r;
 
-    R v[NE];
+    XT v[NE];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         const int64_t e0 = ((int64_t)c * G + t) * 4;
@@ -157,40 +254,41 @@ __global__ __launch_bounds__(64 * GW * RPB) void split_rows_kernel(SplitParams p
             tmp[0] = tmp[1] = tmp[2] = tmp[3] = (XT)0;
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[c * 4 + u] = (R)tmp[u];
+        for (int u = 0; u < 4; ++u) v[c * 4 + u] = tmp[u];
     }
 
-    for (int l = 0; l < p.L; ++l) {
-        // sweep 0: row max
+    // level 0 on the input values
+    float w[NE];
+    {
         float m = 0.0f;
 #pragma unroll
-        for (int e = 0; e < NE; ++e) m = fmaxf(m, (float)fabs(v[e]));
-        m = wave_max(m);
-        if (GW > 1) {
-            if ((t & 63) == 0) red[l & 1][grp][wave] = m;
-            __syncthreads();
+        for (int e = 0; e < NE; ++e) m = fmaxf(m, absf(v[e]));
+        const LevelScale c = level_scale(row_max<GW, RPB>(m, red, 0, grp, t), p.alpha);
+        if (active && t == 0) srow_scale[0] = c.s;
 #pragma unroll
-            for (int w = 0; w < GW; ++w) m = fmaxf(m, red[l & 1][grp][w]);
-        }
-        const float mu = fmaxf(1e-38f, m);
-        const int ema = ceil_log2_f32(mu) - p.alpha;
-        const float s = pow2f(ema);
-        const auto sc = make_scale(ema, R(0));
-        if (active && t == 0) p.scales[b * p.cs_b + l * p.cs_l + r * p.cs_r] = s;
-
-        // sweep 1: quantise, store, residual
-        const bool upd = (l + 1 < p.L);
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            const int64_t e0 = ((int64_t)c * G + t) * 4;
+        for (int ch = 0; ch < NC; ++ch) {
+            const int64_t e0 = ((int64_t)ch * G + t) * 4;
             uint32_t qv[4];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                R deq;
-                const R q = sc.apply(v[c * 4 + u]);
-                qv[u] = Quant<ST>::run(q, &deq);
-                if (upd) v[c * 4 + u] = next_residual(v[c * 4 + u], deq, s);
-            }
+            for (int u = 0; u < 4; ++u)
+                qv[u] = Quant<ST, Modes<XT>::first>::run(v[ch * 4 + u], c, &w[ch * 4 + u]);
+            if (active && e0 < p.K) Store4<ST>::run(p.slices, srow + e0, qv);
+        }
+    }
+    // levels >= 1 on the fp32 residuals (the last level's update is unused)
+    for (int l = 1; l < p.L; ++l) {
+        float m = 0.0f;
+#pragma unroll
+        for (int e = 0; e < NE; ++e) m = fmaxf(m, fabsf(w[e]));
+        const LevelScale c = level_scale(row_max<GW, RPB>(m, red, l & 1, grp, t), p.alpha);
+        if (active && t == 0) srow_scale[l * p.cs_l] = c.s;
+#pragma unroll
+        for (int ch = 0; ch < NC; ++ch) {
+            const int64_t e0 = ((int64_t)ch * G + t) * 4;
+            uint32_t qv[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                qv[u] = Quant<ST, Modes<XT>::rest>::run(w[ch * 4 + u], c, &w[ch * 4 + u]);
             if (active && e0 < p.K) Store4<ST>::run(p.slices, srow + l * p.ss_l + e0, qv);
         }
     }
@@ -199,15 +297,16 @@ __global__ __launch_bounds__(64 * GW * RPB) void split_rows_kernel(SplitParams p
 // ---------------------------------------------------------------------------
 // Column-strip-resident split for operands whose rows are contiguous
 // (xs_r == 1): the B^T view, where a "row" is a column of B.  The workgroup
-// owns W = 2*VEC adjacent columns.  Lane t: column group cg = t % 2 (VEC
-// columns read with one 16-byte load), k-quad kq = t / 2; it holds
-// k = 4*(kq + g*NT/2) + {0..3} for g < KPT/4.  Per-column maxima reduce over
-// lanes of equal cg (xor 2..32) and then over waves through LDS.
-// Strips are mapped to workgroups XCD-aware: the strips sharing a cache line
-// are consecutive on one XCD.
+// owns the VEC = 16 / sizeof(XT) adjacent columns one 16-byte load covers.
+// Lane t holds k = 4*(t + g*NT) + {0..3} for g < KPT/4, all VEC columns, so a
+// wave load reads 64 rows x 16 B and every column's maximum reduces over the
+// whole workgroup.  A strip is at most 128 KB of registers, so two or three
+// workgroups share a CU and one's loads overlap another's arithmetic.
+// Strips are mapped to workgroups XCD-aware: the 8 strips sharing a 128-byte
+// line are consecutive on one XCD.
 // Requirements (host-checked): xs_r == 1, ss_k == 1, rows % VEC == 0, xs_k %
 // VEC == 0, X 16-byte aligned, K % 4 == 0, slice rows 4-/8-byte aligned,
-// K <= KPT * NT / 2.
+// K <= KPT * NT.
 // ---------------------------------------------------------------------------
 OZK_DEV int64_t xcd_remap(int64_t g, int64_t n) {
     // hardware dispatches workgroup g to XCD g % 8; give each XCD a contiguous
@@ -217,47 +316,63 @@ OZK_DEV int64_t xcd_remap(int64_t g, int64_t n) {
     return (g % 8) * q + g / 8;
 }
 
+template <int NW, int VEC>
+OZK_DEV void strip_max(float m[VEC], float (*red)[NW][VEC], int buf, int tid) {
+#pragma unroll
+    for (int u = 0; u < VEC; ++u) m[u] = wave_max(m[u]);
+    if constexpr (NW > 1) {
+        if ((tid & 63) == 0) {
+#pragma unroll
+            for (int u = 0; u < VEC; ++u) red[buf][tid / 64][u] = m[u];
+        }
+        lds_barrier();
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) {
+            float r = red[buf][0][u];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) r = fmaxf(r, red[buf][w][u]);
+            m[u] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(r)));
+        }
+    }
+}
+
 template <typename XT, typename ST, int NT, int KPT>
 __global__ __launch_bounds__(NT) void split_strip_kernel(SplitParams p) {
-    using R = typename ResOf<XT>::R;
     constexpr int VEC = 16 / (int)sizeof(XT);
-    constexpr int W = 2 * VEC;
-    constexpr int NQ = NT / 2;      // k-quads per sweep
     constexpr int NG = KPT / 4;     // k-quads per lane
     constexpr int NW = NT / 64;
-    __shared__ float red[2][NW][W];
+    __shared__ float red[2][NW][VEC];
 
     const int tid = threadIdx.x;
-    const int cg = tid & 1;
-    const int kq = tid >> 1;
-    const int wave = tid / 64;
-    const int64_t strips_per_b = (p.rows + W - 1) / W;
+    const int64_t strips_per_b = p.rows / VEC;
     const int64_t sidx = xcd_remap(blockIdx.x, (int64_t)gridDim.x);
     const int64_t b = sidx / strips_per_b;
-    const int64_t col0 = (sidx % strips_per_b) * W + cg * VEC;
-    const bool colok = col0 < p.rows;   // rows % VEC == 0: whole group valid
+    const int64_t col0 = (sidx % strips_per_b) * VEC;
 
     const XT *xb = (const XT *)p.X + b * p.xs_b + col0;
+    const int64_t sbase = b * p.ss_b + col0 * p.ss_r;
+    float *sc_base = p.scales + b * p.cs_b + col0 * p.cs_r;
 
-    R v[NG][4][VEC];
+    XT v[NG][4][VEC];
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
 #pragma unroll
         for (int dk = 0; dk < 4; ++dk) {
-            const int64_t k = 4 * ((int64_t)kq + (int64_t)g * NQ) + dk;
+            const int64_t k = 4 * ((int64_t)tid + (int64_t)g * NT) + dk;
             XT tmp[VEC];
-            if (colok && k < p.K) {
+            if (k < p.K) {
                 loadvec(xb + k * p.xs_k, tmp);
             } else {
 #pragma unroll
                 for (int u = 0; u < VEC; ++u) tmp[u] = (XT)0;
             }
 #pragma unroll
-            for (int u = 0; u < VEC; ++u) v[g][dk][u] = (R)tmp[u];
+            for (int u = 0; u < VEC; ++u) v[g][dk][u] = tmp[u];
         }
     }
 
-    for (int l = 0; l < p.L; ++l) {
+    float w[NG][4][VEC];
+    {
         float m[VEC];
 #pragma unroll
         for (int u = 0; u < VEC; ++u) m[u] = 0.0f;
@@ -266,54 +381,62 @@ __global__ __launch_bounds__(NT) void split_strip_kernel(SplitParams p) {
 #pragma unroll
             for (int dk = 0; dk < 4; ++dk)
 #pragma unroll
-                for (int u = 0; u < VEC; ++u) m[u] = fmaxf(m[u], (float)fabs(v[g][dk][u]));
+                for (int u = 0; u < VEC; ++u) m[u] = fmaxf(m[u], absf(v[g][dk][u]));
+        strip_max<NW, VEC>(m, red, 0, tid);
+        LevelScale c[VEC];
 #pragma unroll
-        for (int u = 0; u < VEC; ++u) {
+        for (int u = 0; u < VEC; ++u) c[u] = level_scale(m[u], p.alpha);
+        if (tid == 0) {
 #pragma unroll
-            for (int off = 32; off >= 2; off >>= 1) m[u] = fmaxf(m[u], __shfl_xor(m[u], off, 64));
+            for (int u = 0; u < VEC; ++u) sc_base[u * p.cs_r] = c[u].s;
         }
-        if ((tid & 63) < 2) {
-#pragma unroll
-            for (int u = 0; u < VEC; ++u) red[l & 1][wave][cg * VEC + u] = m[u];
-        }
-        __syncthreads();
-        float s[VEC];
-        decltype(make_scale(0, R(0))) sc[VEC];
-#pragma unroll
-        for (int u = 0; u < VEC; ++u) {
-            float mm = 0.0f;
-#pragma unroll
-            for (int w = 0; w < NW; ++w) mm = fmaxf(mm, red[l & 1][w][cg * VEC + u]);
-            const float mu = fmaxf(1e-38f, mm);
-            const int ema = ceil_log2_f32(mu) - p.alpha;
-            s[u] = pow2f(ema);
-            sc[u] = make_scale(ema, R(0));
-        }
-        if (colok && kq == 0) {
-#pragma unroll
-            for (int u = 0; u < VEC; ++u)
-                p.scales[b * p.cs_b + l * p.cs_l + (col0 + u) * p.cs_r] = s[u];
-        }
-        const bool upd = (l + 1 < p.L);
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
-            const int64_t k0 = 4 * ((int64_t)kq + (int64_t)g * NQ);
+            const int64_t k0 = 4 * ((int64_t)tid + (int64_t)g * NT);
             uint32_t qv[VEC][4];
 #pragma unroll
-            for (int dk = 0; dk < 4; ++dk) {
-#pragma unroll
-                for (int u = 0; u < VEC; ++u) {
-                    R deq;
-                    const R q = sc[u].apply(v[g][dk][u]);
-                    qv[u][dk] = Quant<ST>::run(q, &deq);
-                    if (upd) v[g][dk][u] = next_residual(v[g][dk][u], deq, s[u]);
-                }
-            }
-            if (colok && k0 < p.K) {
+            for (int dk = 0; dk < 4; ++dk)
 #pragma unroll
                 for (int u = 0; u < VEC; ++u)
-                    Store4<ST>::run(p.slices, b * p.ss_b + l * p.ss_l + (col0 + u) * p.ss_r + k0,
-                                    qv[u]);
+                    qv[u][dk] = Quant<ST, Modes<XT>::first>::run(v[g][dk][u], c[u], &w[g][dk][u]);
+            if (k0 < p.K) {
+#pragma unroll
+                for (int u = 0; u < VEC; ++u)
+                    Store4<ST>::run(p.slices, sbase + u * p.ss_r + k0, qv[u]);
+            }
+        }
+    }
+    for (int l = 1; l < p.L; ++l) {
+        float m[VEC];
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) m[u] = 0.0f;
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+#pragma unroll
+            for (int dk = 0; dk < 4; ++dk)
+#pragma unroll
+                for (int u = 0; u < VEC; ++u) m[u] = fmaxf(m[u], fabsf(w[g][dk][u]));
+        strip_max<NW, VEC>(m, red, l & 1, tid);
+        LevelScale c[VEC];
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) c[u] = level_scale(m[u], p.alpha);
+        if (tid == 0) {
+#pragma unroll
+            for (int u = 0; u < VEC; ++u) sc_base[l * p.cs_l + u * p.cs_r] = c[u].s;
+        }
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            const int64_t k0 = 4 * ((int64_t)tid + (int64_t)g * NT);
+            uint32_t qv[VEC][4];
+#pragma unroll
+            for (int dk = 0; dk < 4; ++dk)
+#pragma unroll
+                for (int u = 0; u < VEC; ++u)
+                    qv[u][dk] = Quant<ST, Modes<XT>::rest>::run(w[g][dk][u], c[u], &w[g][dk][u]);
+            if (k0 < p.K) {
+#pragma unroll
+                for (int u = 0; u < VEC; ++u)
+                    Store4<ST>::run(p.slices, sbase + l * p.ss_l + u * p.ss_r + k0, qv[u]);
             }
         }
     }
@@ -327,8 +450,7 @@ __global__ __launch_bounds__(NT) void split_strip_kernel(SplitParams p) {
 // ---------------------------------------------------------------------------
 template <typename XT, typename ST>
 __global__ __launch_bounds__(256) void split_generic_kernel(SplitParams p) {
-    using R = typename ResOf<XT>::R;
-    __shared__ float red[2][4];
+    __shared__ float red[2][1][4];
     const int t = threadIdx.x;
     const int64_t grow = blockIdx.x;
     const int64_t b = grow / p.rows;
@@ -336,29 +458,28 @@ __global__ __launch_bounds__(256) void split_generic_kernel(SplitParams p) {
     const XT *xrow = (const XT *)p.X + b * p.xs_b + r * p.xs_r;
     float *res = p.resid + (b * p.rows + r) * p.K;
     const int64_t srow = b * p.ss_b + r * p.ss_r;
+    const bool keep = p.L > 1;
 
-    for (int l = 0; l < p.L; ++l) {
-        float m = 0.0f;
+    float m = 0.0f;
+    for (int64_t k = t; k < p.K; k += 256) m = fmaxf(m, absf(xrow[k * p.xs_k]));
+    LevelScale c = level_scale(row_max<4, 1>(m, red, 0, 0, t), p.alpha);
+    if (t == 0) p.scales[b * p.cs_b + r * p.cs_r] = c.s;
+    for (int64_t k = t; k < p.K; k += 256) {
+        float rr;
+        const uint32_t qv = Quant<ST, Modes<XT>::first>::run(xrow[k * p.xs_k], c, &rr);
+        store1<ST>(p.slices, srow + k * p.ss_k, qv);
+        if (keep) res[k] = rr;
+    }
+    for (int l = 1; l < p.L; ++l) {
+        m = 0.0f;
+        for (int64_t k = t; k < p.K; k += 256) m = fmaxf(m, fabsf(res[k]));
+        c = level_scale(row_max<4, 1>(m, red, l & 1, 0, t), p.alpha);
+        if (t == 0) p.scales[b * p.cs_b + l * p.cs_l + r * p.cs_r] = c.s;
         for (int64_t k = t; k < p.K; k += 256) {
-            const R x = (l == 0) ? (R)xrow[k * p.xs_k] : (R)res[k];
-            m = fmaxf(m, (float)fabs(x));
-        }
-        m = wave_max(m);
-        if ((t & 63) == 0) red[l & 1][t / 64] = m;
-        __syncthreads();
-        m = fmaxf(fmaxf(red[l & 1][0], red[l & 1][1]), fmaxf(red[l & 1][2], red[l & 1][3]));
-        const float mu = fmaxf(1e-38f, m);
-        const int ema = ceil_log2_f32(mu) - p.alpha;
-        const float s = pow2f(ema);
-        const auto sc = make_scale(ema, R(0));
-        if (t == 0) p.scales[b * p.cs_b + l * p.cs_l + r * p.cs_r] = s;
-        const bool upd = (l + 1 < p.L);
-        for (int64_t k = t; k < p.K; k += 256) {
-            const R x = (l == 0) ? (R)xrow[k * p.xs_k] : (R)res[k];
-            R deq;
-            const uint32_t qv = Quant<ST>::run(sc.apply(x), &deq);
+            float rr;
+            const uint32_t qv = Quant<ST, Modes<XT>::rest>::run(res[k], c, &rr);
             store1<ST>(p.slices, srow + l * p.ss_l + k * p.ss_k, qv);
-            if (upd) res[k] = (float)next_residual(x, deq, s);
+            res[k] = rr;
         }
     }
 }
@@ -434,11 +555,16 @@ static const RowCfg kRowCfgs[] = {
 static const int kNumRowCfgs = sizeof(kRowCfgs) / sizeof(kRowCfgs[0]);
 
 struct StripCfg { int nt, kpt; };
+// capacity K <= nt * kpt; a lane holds kpt * VEC values: at most 64 (fp64:
+// VEC = 2, kpt <= 32; fp32: VEC = 4, kpt <= 16)
 static const StripCfg kStripCfgs[] = {
-    {256, 8},     // K <= 1024
-    {512, 8},     // K <= 2048
-    {1024, 8},    // K <= 4096
-    {1024, 16},   // K <= 8192
+    {256, 4},     // K <= 1024
+    {256, 8},     // K <= 2048
+    {256, 16},    // K <= 4096
+    {256, 32},    // K <= 8192  (fp64)
+    {512, 16},    // K <= 8192  (fp32)
+    {512, 32},    // K <= 16384 (fp64)
+    {1024, 16},   // K <= 16384 (fp32)
 };
 static const int kNumStripCfgs = sizeof(kStripCfgs) / sizeof(kStripCfgs[0]);
 
@@ -466,7 +592,8 @@ SplitPlan plan_split(const SplitParams &p, int x_dtype, int slice_dtype) {
         (p.xs_k * xsz) % 16 == 0 && (p.xs_b * xsz) % 16 == 0) {
         for (int i = 0; i < kNumStripCfgs; ++i) {
             const StripCfg &c = kStripCfgs[i];
-            if (p.K <= (int64_t)c.kpt * c.nt / 2) return {kSplitStrip, i};
+            if (c.kpt * vec > 64) continue;
+            if (p.K <= (int64_t)c.kpt * c.nt) return {kSplitStrip, i};
         }
     }
     // row-contiguous operand with a K too long for a resident strip: transpose
@@ -515,16 +642,23 @@ static hipError_t launch_rows(const SplitParams &p, int v, hipStream_t st) {
 
 template <typename XT, typename ST>
 static hipError_t launch_strip(const SplitParams &p, int v, hipStream_t st) {
-    constexpr int W = 2 * (16 / (int)sizeof(XT));
-    const int64_t nstrips = p.batch * ((p.rows + W - 1) / W);
+    constexpr int VEC = 16 / (int)sizeof(XT);
+    const int64_t nstrips = p.batch * (p.rows / VEC);   // rows % VEC == 0
 #define OZK_STRIP(NT, KPT)                                                                  \
     hipLaunchKernelGGL((split_strip_kernel<XT, ST, NT, KPT>), dim3((unsigned)nstrips),      \
                        dim3(NT), 0, st, p)
     switch (v) {
-    case 0: OZK_STRIP(256, 8); break;
-    case 1: OZK_STRIP(512, 8); break;
-    case 2: OZK_STRIP(1024, 8); break;
-    case 3: OZK_STRIP(1024, 16); break;
+    case 0: OZK_STRIP(256, 4); break;
+    case 1: OZK_STRIP(256, 8); break;
+    case 2: OZK_STRIP(256, 16); break;
+    case 3:
+        if constexpr (VEC == 2) { OZK_STRIP(256, 32); } else return hipErrorInvalidValue;
+        break;
+    case 4: OZK_STRIP(512, 16); break;
+    case 5:
+        if constexpr (VEC == 2) { OZK_STRIP(512, 32); } else return hipErrorInvalidValue;
+        break;
+    case 6: OZK_STRIP(1024, 16); break;
     default: return hipErrorInvalidValue;
     }
 #undef OZK_STRIP

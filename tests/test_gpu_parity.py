@@ -51,7 +51,7 @@ def test_split_rows_path(oracle, gpu, xdt, sdt, L, rows, K):
 
 @pytest.mark.parametrize("xdt,sdt", COMBOS)
 @pytest.mark.parametrize("L", [1, 3, 4])
-@pytest.mark.parametrize("N,K", [(8, 256), (40, 1000), (96, 2048), (24, 8192)])
+@pytest.mark.parametrize("N,K", [(8, 256), (40, 1000), (96, 2048), (24, 8192), (16, 16000)])
 def test_split_strip_path(oracle, gpu, xdt, sdt, L, N, K):
     """B's columns through the transposed view (rows contiguous)."""
     import ozaki_triton_amd as ozk
