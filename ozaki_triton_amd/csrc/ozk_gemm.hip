@@ -25,6 +25,8 @@
 //     range of tiles, grouped GROUP_M tile-rows at a time.
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "ozk_common.h"
 #include "ozk_internal.h"
 
@@ -521,6 +523,253 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_dma_kernel(GemmParams p, in
 }
 
 // ---------------------------------------------------------------------------
+// Pair-split variant: 8 waves, two per SIMD.  The 2 x 2 grid of 32 x 32 wave
+// blocks is covered twice: wave group g (0 or 1) accumulates the slice pairs
+// [g*P0, ...) of the i-major / j-minor pair order, P0 = ceil(L*L/2), so a wave
+// holds half the accumulators (128 registers at L = 4) and two waves share a
+// SIMD.  While one waits on its DMA issue, an LDS read or the stage barrier,
+// the other's MFMAs run.  The epilogue keeps the reference's ordered sum:
+// group 0 sums its pairs from +0 and hands the partial to group 1 through
+// LDS; group 1 adds its pairs, in order, and stores C.
+// ---------------------------------------------------------------------------
+template <int L> struct PairSplit {
+    static constexpr int P = L * L;
+    static constexpr int P0 = (P + 1) / 2;
+    static constexpr int first(int g) { return g ? P0 : 0; }
+    static constexpr int count(int g) { return g ? P - P0 : P0; }
+    static constexpr int ilo(int g) { return first(g) / L; }
+    static constexpr int na(int g) { return (first(g) + count(g) - 1) / L - ilo(g) + 1; }
+};
+
+template <int L> struct PairShape {
+    static constexpr int BM = 64, BN = 64;
+    static constexpr int A_ROWS = L * BM;
+    static constexpr int ROWS = L * (BM + BN);
+    static constexpr int STAGE = ROWS * kDmaRB;
+    static constexpr int LPS = STAGE / (8 * 1024);   // DMA instructions per wave per stage
+    static constexpr int LDS_BYTES = kDmaStages * STAGE;
+    static_assert(STAGE % 8192 == 0, "stage must be a whole number of 1 KB windows per wave");
+};
+
+template <typename ST, int L, typename OutT>
+__global__ __launch_bounds__(512, 1) void cross_gemm_pair_kernel(GemmParams p, int group_m,
+                                                                 uint32_t a_records,
+                                                                 uint32_t b_records) {
+    using Sh = PairShape<L>;
+    using PS = PairSplit<L>;
+    using MF = Mfma<ST>;
+    using Acc = typename MF::Acc;
+    using OA = typename OutAcc<OutT>::T;
+    constexpr int BM = Sh::BM, BN = Sh::BN;
+    constexpr int ES = (int)sizeof(ST);
+    constexpr uint32_t kOOB = 0x80000000u;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int blk = wave & 3, grp = wave >> 2;
+    const int wm = blk >> 1, wn = blk & 1;
+    const int h = lane >> 5, lr = lane & 31;
+
+    const int64_t tiles_m = (p.M + BM - 1) / BM;
+    const int64_t tiles_n = (p.N + BN - 1) / BN;
+    const int64_t tiles = tiles_m * tiles_n;
+    const int64_t g = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
+    const int64_t bidx = g / tiles;
+    const int64_t t = g % tiles;
+    const int64_t width = (int64_t)group_m * tiles_n;
+    const int64_t first_m = (t / width) * group_m;
+    const int64_t gsz = (tiles_m - first_m < group_m) ? (tiles_m - first_m) : group_m;
+    const int64_t tm = first_m + (t % width) % gsz;
+    const int64_t tn = (t % width) / gsz;
+    const int64_t m0 = tm * BM, n0 = tn * BN;
+
+    const uint32_t kbytes = (uint32_t)(p.K * ES);
+    const int nkb = (int)((kbytes + kDmaRB - 1) / kDmaRB);
+    constexpr int CH = kDmaRB / 16;
+    constexpr int STEPS = kDmaRB / 32;
+
+    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const char *)p.A + bidx * p.as_b * ES), (short)0, (int)a_records, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const char *)p.B + bidx * p.bs_b * ES), (short)0, (int)b_records, 0x00020000);
+
+    // Per-lane source offsets of this wave's LPS DMA instructions (a 1 KB
+    // window covers 8 whole rows; A_ROWS is a multiple of 8, so each
+    // instruction reads only A or only B).
+    uint32_t src[Sh::LPS];
+    int chunk[Sh::LPS];
+#pragma unroll
+    for (int q = 0; q < Sh::LPS; ++q) {
+        const int pos = (wave * Sh::LPS + q) * 64 + lane;
+        const int r = pos / CH;
+        const int pc = pos % CH;
+        chunk[q] = (kDmaRB == 64) ? (pc ^ ((r >> 2) & 3)) : (pc ^ ((r >> 1) & 7));
+        if (r < Sh::A_ROWS) {
+            const int i = r / BM;
+            const int64_t m = m0 + r % BM;
+            src[q] = (m < p.M) ? (uint32_t)(((int64_t)i * p.as_l + m * p.as_m) * ES) : kOOB;
+        } else {
+            const int rb = r - Sh::A_ROWS;
+            const int j = rb / BN;
+            const int64_t n = n0 + rb % BN;
+            src[q] = (n < p.N) ? (uint32_t)(((int64_t)j * p.bs_l + n * p.bs_n) * ES) : kOOB;
+        }
+    }
+    auto issue_stage = [&](int kb) {
+        char *dst = smem + (kb % kDmaStages) * Sh::STAGE + wave * Sh::LPS * 1024;
+#pragma unroll
+        for (int q = 0; q < Sh::LPS; ++q) {
+            const uint32_t kofs = (uint32_t)kb * kDmaRB + chunk[q] * 16;
+            const uint32_t vo = (src[q] == kOOB || kofs >= kbytes) ? kOOB : src[q] + kofs;
+            auto *ldsp = (__attribute__((address_space(3))) void *)(dst + q * 1024);
+            const bool isA = (wave * Sh::LPS + q) * (1024 / kDmaRB) < Sh::A_ROWS;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(isA ? rA : rB, ldsp, 16, vo, 0, 0, 0);
+        }
+    };
+    // stage kb has landed once at most the loads of the stages issued after
+    // it are outstanding; the barrier then publishes every wave's DMA writes,
+    // and the lgkmcnt wait makes this wave's reads of the slot about to be
+    // refilled complete first
+    auto stage_ready = [&](int kb) {
+        const int after = min(kDmaStages - 2, nkb - 1 - kb);
+        static_assert(kDmaStages >= 2 && kDmaStages <= 6, "wait table");
+        if constexpr (kDmaStages - 2 >= 4) { if (after == 4) { wait_vmcnt<4 * Sh::LPS>(); goto waited; } }
+        if constexpr (kDmaStages - 2 >= 3) { if (after == 3) { wait_vmcnt<3 * Sh::LPS>(); goto waited; } }
+        if constexpr (kDmaStages - 2 >= 2) { if (after == 2) { wait_vmcnt<2 * Sh::LPS>(); goto waited; } }
+        if constexpr (kDmaStages - 2 >= 1) { if (after == 1) { wait_vmcnt<Sh::LPS>(); goto waited; } }
+        wait_vmcnt<0>();
+    waited:
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0) only
+        exec_barrier();
+    };
+
+#pragma unroll
+    for (int s = 0; s < kDmaStages - 1; ++s)
+        if (s < nkb) issue_stage(s);
+
+    const float *sab = p.sa + bidx * p.sas_b;
+    const float *sbb = p.sb + bidx * p.sbs_b;
+    OutT *Cb = (OutT *)p.C + bidx * p.cs_b;
+    OA *part = (OA *)smem;   // epilogue hand-off [4 blocks][16][64 lanes]
+    const int64_t col = n0 + wn * 32 + lr;
+    const bool cok = col < p.N;
+
+    // The main loop and epilogue of wave group G (compile-time pair range).
+    auto body = [&](auto G_) {
+        constexpr int G = decltype(G_)::value;
+        constexpr int F = PS::first(G), NP = PS::count(G), ILO = PS::ilo(G), NA = PS::na(G);
+        constexpr int kReads = NA + L;
+        struct Frags {
+            i32x4 a[NA];
+            i32x4 b[L];
+        };
+        Acc acc[NP];
+#pragma unroll
+        for (int q = 0; q < NP; ++q) acc[q] = MF::zero();
+
+        auto read_one = [&](const char *buf, int kk, int r, Frags &f) {
+            const int ch = 2 * kk + h;
+            if (r < NA) {
+                f.a[r] = *(const i32x4 *)(buf + rswz<kDmaRB>((ILO + r) * BM + wm * 32 + lr, ch));
+            } else {
+                const int j = r - NA;
+                f.b[j] = *(const i32x4 *)(buf + rswz<kDmaRB>(Sh::A_ROWS + j * BN + wn * 32 + lr, ch));
+            }
+        };
+        // MFMAs of `cur` with the next step's reads into `nxt` interleaved
+        auto step = [&](const Frags &cur, Frags &nxt, const char *nbuf, int nkk) {
+#pragma unroll
+            for (int q = 0; q < NP; ++q) {
+                const int i = (F + q) / L, j = (F + q) % L;
+                acc[q] = MF::run(cur.a[i - ILO], cur.b[j], acc[q]);
+                if (q < kReads) read_one(nbuf, nkk, q, nxt);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int q = NP; q < kReads; ++q) read_one(nbuf, nkk, q, nxt);
+        };
+
+        Frags f0, f1;
+        if (nkb > 0) {
+            stage_ready(0);
+            if (kDmaStages - 1 < nkb) issue_stage(kDmaStages - 1);
+#pragma unroll
+            for (int q = 0; q < kReads; ++q) read_one(smem, 0, q, f0);
+        }
+        for (int kb = 0; kb < nkb; ++kb) {
+            const char *buf = smem + (kb % kDmaStages) * Sh::STAGE;
+#pragma unroll
+            for (int kk = 0; kk + 1 < STEPS; ++kk) {
+                if (kk % 2 == 0) step(f0, f1, buf, kk + 1);
+                else step(f1, f0, buf, kk + 1);
+            }
+            if (kb + 1 < nkb) {
+                stage_ready(kb + 1);
+                if (kb + kDmaStages < nkb) issue_stage(kb + kDmaStages);
+            }
+            if ((STEPS - 1) % 2 == 0) step(f0, f1, smem + ((kb + 1) % kDmaStages) * Sh::STAGE, 0);
+            else step(f1, f0, smem + ((kb + 1) % kDmaStages) * Sh::STAGE, 0);
+            if ((STEPS - 1) % 2 == 0) {
+#pragma unroll
+                for (int i = 0; i < NA; ++i) f0.a[i] = f1.a[i];
+#pragma unroll
+                for (int j = 0; j < L; ++j) f0.b[j] = f1.b[j];
+            }
+        }
+
+        // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
+        // every wave is past its last ring read before the ring holds partials
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        exec_barrier();
+        float sbv[L];
+#pragma unroll
+        for (int j = 0; j < L; ++j) sbv[j] = cok ? sbb[j * p.sbs_l + col * p.sbs_n] : 0.0f;
+        // t values of this group's pairs: fl32(fl32(fl32(acc) * sa_i) * sb_j)
+        float tv[NP][16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t row = m0 + wm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            const bool ok = cok && row < p.M;
+            float sai[NA];
+#pragma unroll
+            for (int i = 0; i < NA; ++i) sai[i] = ok ? sab[(ILO + i) * p.sas_l + row * p.sas_m] : 0.0f;
+#pragma unroll
+            for (int q = 0; q < NP; ++q) {
+                const int i = (F + q) / L, j = (F + q) % L;
+                const float x = MF::to_f32(acc[q][r]);
+                const float t1 = x * sai[i - ILO];
+                tv[q][r] = t1 * sbv[j];
+            }
+        }
+        if constexpr (G == 0) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                OA out = (OA)0;
+#pragma unroll
+                for (int q = 0; q < NP; ++q) out = out + (OA)tv[q][r];
+                part[(blk * 16 + r) * 64 + lane] = out;
+            }
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            exec_barrier();
+        } else {
+            exec_barrier();
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = m0 + wm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                OA out = part[(blk * 16 + r) * 64 + lane];
+#pragma unroll
+                for (int q = 0; q < NP; ++q) out = out + (OA)tv[q][r];
+                if (cok && row < p.M) Cb[row * p.cs_m + col * p.cs_n] = (OutT)out;
+            }
+        }
+    };
+    if (grp == 0) body(std::integral_constant<int, 0>{});
+    else body(std::integral_constant<int, 1>{});
+}
+
+// ---------------------------------------------------------------------------
 // A-direct variant.  The four waves are stacked along M (workgroup tile
 // 128 x 32*NI); each wave streams ITS OWN 32 rows of every A slice from global
 // memory straight into VGPRs (no LDS), and only B, which all four waves share,
@@ -816,17 +1065,19 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype) {
     plan.ni = ni;
     plan.group_m = 8;
     const int es = slice_dtype == 4 ? 1 : 2;
-    // OZK_GEMM_STAGED=1 selects the VGPR-staged kernel (the path operands
-    // beyond 2 GiB take), so tests can cover it at small sizes
-    // OZK_GEMM_KERNEL=staged|dma|ad forces a kernel (tests cover every one at
-    // small sizes); by default the 2 x 2 LDS-DMA kernel whenever both operands
-    // fit its 31-bit buffer offsets, else the VGPR-staged kernel
+    // OZK_GEMM_KERNEL=staged|dma|ad|pair forces a kernel (tests cover every
+    // one at small sizes).  By default, when both operands fit the 31-bit
+    // buffer offsets of the LDS-DMA kernels: the pair-split kernel for L >= 3
+    // (its wave tile is 32 x 32 anyway), the 2 x 2 LDS-DMA kernel with its
+    // larger wave tiles for L <= 2; else the VGPR-staged kernel.
     const bool fits = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es) >= 0 &&
                       dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es) >= 0;
-    plan.kind = fits ? kGemmDMA : kGemmStaged;
+    plan.kind = fits ? (L >= 3 ? kGemmPair : kGemmDMA) : kGemmStaged;
     const char *forced = getenv("OZK_GEMM_KERNEL");
     if (forced && forced[0] == 's') plan.kind = kGemmStaged;
     else if (forced && forced[0] == 'a' && fits) plan.kind = kGemmAD;
+    else if (forced && forced[0] == 'd' && fits) plan.kind = kGemmDMA;
+    else if (forced && forced[0] == 'p' && fits) plan.kind = L >= 3 ? kGemmPair : kGemmDMA;
     if (plan.kind == kGemmAD) plan.group_m = 2;
     return plan;
 }
@@ -883,8 +1134,33 @@ static hipError_t launch_ad(const GemmParams &p, const GemmPlan &plan, hipStream
     return hipGetLastError();
 }
 
+template <typename ST, int L, typename OutT>
+static hipError_t launch_pair(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
+    using Sh = PairShape<L>;
+    auto kern = cross_gemm_pair_kernel<ST, L, OutT>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void *)kern,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           Sh::LDS_BYTES);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const int es = (int)sizeof(ST);
+    const int64_t ea = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es);
+    const int64_t eb = dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es);
+    const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
+    if (tiles == 0) return hipSuccess;
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(512), Sh::LDS_BYTES, st, p,
+                       plan.group_m, (uint32_t)ea, (uint32_t)eb);
+    return hipGetLastError();
+}
+
 template <typename ST, int L, int MI, int NI, typename OutT>
 static hipError_t launch_one(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
+    if constexpr (L >= 3) {
+        if (plan.kind == kGemmPair) return launch_pair<ST, L, OutT>(p, plan, st);
+    }
     if (plan.kind == kGemmAD) {
         constexpr int ANI = (L == 1) ? 8 : (L == 2) ? 4 : 1;
         return launch_ad<ST, L, ANI, OutT>(p, plan, st);

@@ -58,7 +58,8 @@ struct GemmParams {
 enum GemmKind {
     kGemmStaged = 0,  // global -> VGPR -> LDS, 2 x 2 waves (any operand extent)
     kGemmDMA = 1,     // LDS-DMA ring for A and B, 2 x 2 waves
-    kGemmAD = 2       // A streamed into VGPRs, B by LDS-DMA, 4 x 1 waves
+    kGemmAD = 2,      // A streamed into VGPRs, B by LDS-DMA, 4 x 1 waves
+    kGemmPair = 3     // LDS-DMA ring, 8 waves: 2 x 2 blocks x 2 halves of the slice pairs
 };
 struct GemmPlan {
     int mi, ni;       // 2 x 2 kernels: wave tile = (32*mi) x (32*ni)

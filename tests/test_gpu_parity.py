@@ -239,12 +239,13 @@ def test_ozaki_matmul_degenerate_shapes(gpu):
                          torch.randn(0, 3, dtype=torch.float64, device=gpu), 2, torch.int8)
 
 
-@pytest.mark.parametrize("kernel", ["staged", "dma", "ad"])
+@pytest.mark.parametrize("kernel", ["staged", "dma", "ad", "pair"])
 @pytest.mark.parametrize("L", [1, 2, 3, 4])
 def test_cross_gemm_each_kernel_bitexact(oracle, gpu, L, kernel, monkeypatch):
     """Every cross-GEMM kernel, forced: the VGPR-staged one (taken when an
     operand's extent exceeds the 31-bit buffer offsets of the LDS-DMA kernels),
-    the 2 x 2 LDS-DMA kernel and the A-direct kernel."""
+    the 2 x 2 LDS-DMA kernel, the A-direct kernel and the pair-split kernel
+    (L >= 3; for L <= 2 the request falls back to the 2 x 2 kernel)."""
     import ozaki_triton_amd as ozk
     monkeypatch.setenv("OZK_GEMM_KERNEL", kernel)
     g = torch.Generator().manual_seed(77 + L)
