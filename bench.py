@@ -219,6 +219,9 @@ def main():
     else:
         peak, unit_c = PEAK_FP16_TFLOPS, "TFLOP/s"
     achieved = cross_ops / (t_cross * 1e-3) / 1e12
+    # the library's default kernel choice (plan_gemm in ozk_gemm.hip): the
+    # pair-split kernel for L >= 3, the 2 x 2 LDS-DMA kernel otherwise
+    gemm_kernel = "cross_gemm_pair_kernel" if L >= 3 else "cross_gemm_dma_kernel"
     # split: read the unique inputs, write the unique slices and scales
     xsz = 8 if xdt == "float64" else 4
     ssz = 1 if sdt == "int8" else 2
@@ -256,17 +259,18 @@ def main():
         },
         "rel_err": rel,
         "roofline": {
-            "kernel": "cross_gemm_kernel",
+            "kernel": gemm_kernel,
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": peak,
             "unit": unit_c,
             "frac": round(achieved / peak, 4),
-            "traffic": measured_traffic(args.config, "ozk::cross_gemm_dma_kernel"),
+            "traffic": measured_traffic(args.config, "ozk::" + gemm_kernel),
             "avg_ms": round(t_cross, 4),
         },
         "split": {
-            "kernels": "split_strip_kernel (B) + split_rows_kernel (A)",
+            "kernels": "split_rows_kernel (A) + split_strip_kernel or transpose_kernel + "
+                       "split_rows_kernel (B)",
             "bound": "hbm",
             "bytes": split_bytes,
             "achieved": round(split_gbs, 1),
