@@ -120,6 +120,45 @@ def measured_traffic(config: str, kernel_prefix: str):
     return None
 
 
+def vendor_probes():
+    """Calibration points for the two rooflines, timed with events: the HBM
+    rate torch's own copy kernel reaches (read + write bytes / time) and the
+    rate of the vendor int8 GEMM (hipBLASLt through torch._int_mm) at C3's
+    size, i.e. ONE of the L*L slice GEMMs the cross-GEMM fuses."""
+    import torch
+    dev = torch.device("cuda:0")
+
+    def time_ms(fn, reps):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    out = {}
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    ms = time_ms(lambda: dst.copy_(src), 10)
+    out["copy_1GiB_ms"] = round(ms, 4)
+    out["copy_GBps_read_plus_write"] = round(2 * n / (ms * 1e-3) / 1e9, 1)
+    del src, dst
+    m = 8192
+    g = torch.Generator(device=dev).manual_seed(0)
+    a = torch.randint(-128, 128, (m, m), dtype=torch.int8, device=dev, generator=g)
+    b = torch.randint(-128, 128, (m, m), dtype=torch.int8, device=dev, generator=g)
+    ms = time_ms(lambda: torch._int_mm(a, b.t()), 5)
+    out["int_mm_8192_ms"] = round(ms, 4)
+    out["int_mm_TOPs"] = round(2.0 * m ** 3 / (ms * 1e-3) / 1e12, 1)
+    print(json.dumps(out), flush=True)
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -142,7 +181,14 @@ def main():
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (3 times): the "
                          "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--vendor-probes", action="store_true",
+                    help="only time two vendor kernels that calibrate the rooflines: torch's "
+                         "device copy of 1 GiB (practical HBM rate) and torch._int_mm "
+                         "(hipBLASLt int8 GEMM) at 8192^3")
     args = ap.parse_args()
+    if args.vendor_probes:
+        vendor_probes()
+        return
     if args.copy_probe_mib:
         import torch
         n = args.copy_probe_mib << 20

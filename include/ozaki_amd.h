@@ -16,7 +16,8 @@
  *     ozk_strerror() names the code.  Argument checks run on the host before
  *     anything is enqueued, so a rejected call has no device side effect.
  *   - No device memory is allocated.  Scratch space comes from the caller
- *     through (workspace, workspace_bytes); *_workspace_bytes() says how much.
+ *     through (workspace, workspace_bytes), 16-byte aligned; *_workspace_bytes() says
+ *     how much.
  *   - No mutable global state: calls are re-entrant and thread-safe.
  */
 #ifndef OZAKI_AMD_H
@@ -47,7 +48,7 @@ enum {
     OZK_ERR_SPLITS = -3,      /* num_splits outside [0, OZK_MAX_SPLITS] */
     OZK_ERR_SHAPE = -4,       /* negative size, or K mismatch */
     OZK_ERR_ALPHA = -5,       /* alpha < 1 (K too large for the accumulator) */
-    OZK_ERR_WORKSPACE = -6,   /* workspace missing or too small */
+    OZK_ERR_WORKSPACE = -6,   /* workspace missing, too small or not 16-byte aligned */
     OZK_ERR_LAUNCH = -7,      /* a HIP launch failed (hipGetLastError) */
     OZK_ERR_ACCUM = -8        /* unsupported dot accumulator dtype */
 };

@@ -71,7 +71,7 @@ const char *ozk_strerror(int status) {
     case OZK_ERR_SPLITS: return "num_splits out of range";
     case OZK_ERR_SHAPE: return "invalid shape";
     case OZK_ERR_ALPHA: return "alpha < 1: K too large to split safely";
-    case OZK_ERR_WORKSPACE: return "workspace missing or too small";
+    case OZK_ERR_WORKSPACE: return "workspace missing, too small or not 16-byte aligned";
     case OZK_ERR_LAUNCH: return "HIP launch failed";
     case OZK_ERR_ACCUM: return "unsupported dot accumulator dtype";
     default: return "unknown status";
@@ -138,7 +138,8 @@ int ozk_split(const void *X, int x_dtype, int64_t batch, int64_t rows, int64_t K
     const ozk::SplitPlan plan = ozk::plan_split(p, x_dtype, slice_dtype);
     const size_t need = ozk::split_workspace_bytes(p, plan, x_dtype);
     if (need > 0) {
-        if (!workspace || workspace_bytes < need) return OZK_ERR_WORKSPACE;
+        if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 16 != 0)
+            return OZK_ERR_WORKSPACE;
         p.resid = (float *)workspace;
     }
     return hip_status(ozk::launch_split(p, plan, x_dtype, slice_dtype, (hipStream_t)stream));
@@ -198,7 +199,8 @@ int ozk_cross_gemm(const void *A_slices, const int64_t a_strides[4], const void 
     const int es = slice_size(slice_dtype);
     const int64_t abytes = pack_bytes(A_slices, a_strides, batch, num_splits, M, K, es, false);
     const int64_t bbytes = pack_bytes(B_slices, b_strides, batch, num_splits, N, K, es, true);
-    if (abytes + bbytes > 0 && (!workspace || workspace_bytes < (size_t)(abytes + bbytes)))
+    if (abytes + bbytes > 0 && (!workspace || workspace_bytes < (size_t)(abytes + bbytes) ||
+                                (uintptr_t)workspace % 16 != 0))
         return OZK_ERR_WORKSPACE;
     const int64_t kp = round_up(K * es, 16) / es;
     char *ws = (char *)workspace;

@@ -493,9 +493,11 @@ __global__ __launch_bounds__(256) void split_generic_kernel(SplitParams p) {
 template <typename XT>
 __global__ __launch_bounds__(256) void transpose_kernel(const XT *__restrict__ X, int64_t batch,
                                                         int64_t rows, int64_t K, int64_t xs_b,
-                                                        int64_t xs_k, XT *__restrict__ T) {
+                                                        int64_t xs_k, XT *__restrict__ T,
+                                                        int vec_loads) {
     constexpr int TILE = 64;
     constexpr int VEC = 16 / (int)sizeof(XT);
+    typedef XT vec_t __attribute__((ext_vector_type(VEC)));
     __shared__ XT tile[TILE][TILE + 1];
     const int64_t tiles_r = (rows + TILE - 1) / TILE;
     const int64_t tiles_k = (K + TILE - 1) / TILE;
@@ -505,7 +507,8 @@ __global__ __launch_bounds__(256) void transpose_kernel(const XT *__restrict__ X
     const int64_t r0 = (rem % tiles_r) * TILE;
     const int64_t k0 = (rem / tiles_r) * TILE;
     const XT *xb = X + b * xs_b;
-    // load: lane covers VEC consecutive rows of one k
+    // load: a lane covers VEC consecutive rows of one k (one 16-byte load when
+    // the host found every such group 16-byte aligned and it lies inside)
     constexpr int LPR = TILE / VEC;              // lanes per k-row of the tile
     constexpr int KPP = 256 / LPR;               // k-rows per pass
     const int lr = threadIdx.x % LPR, lk = threadIdx.x / LPR;
@@ -513,24 +516,32 @@ __global__ __launch_bounds__(256) void transpose_kernel(const XT *__restrict__ X
     for (int kk = 0; kk < TILE; kk += KPP) {
         const int64_t k = k0 + kk + lk;
         const int64_t r = r0 + lr * VEC;
+        XT v[VEC];
+        if (vec_loads && k < K && r + VEC <= rows) {
+            const vec_t w = *(const vec_t *)(xb + k * xs_k + r);
 #pragma unroll
-        for (int u = 0; u < VEC; ++u) {
-            XT v = (XT)0;
-            if (k < K && r + u < rows) v = xb[k * xs_k + r + u];
-            tile[kk + lk][lr * VEC + u] = v;
+            for (int u = 0; u < VEC; ++u) v[u] = w[u];
+        } else {
+#pragma unroll
+            for (int u = 0; u < VEC; ++u)
+                v[u] = (k < K && r + u < rows) ? xb[k * xs_k + r + u] : (XT)0;
         }
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) tile[kk + lk][lr * VEC + u] = v[u];
     }
     __syncthreads();
-    // store: lane covers VEC consecutive k of one row
+    // store: a lane covers VEC consecutive k of one row (K % VEC == 0, checked
+    // on the host, and T rows start 16-byte aligned)
     XT *tb_out = T + b * rows * K;
 #pragma unroll
     for (int rr = 0; rr < TILE; rr += KPP) {
         const int64_t r = r0 + rr + lk;
         const int64_t k = k0 + lr * VEC;
-        if (r < rows) {
+        if (r < rows && k < K) {
+            vec_t w;
 #pragma unroll
-            for (int u = 0; u < VEC; ++u)
-                if (k + u < K) tb_out[r * K + k + u] = tile[lr * VEC + u][rr + lk];
+            for (int u = 0; u < VEC; ++u) w[u] = tile[lr * VEC + u][rr + lk];
+            *(vec_t *)(tb_out + r * K + k) = w;
         }
     }
 }
@@ -673,8 +684,11 @@ static hipError_t launch_typed(const SplitParams &p, const SplitPlan &plan, hipS
     case kSplitTransposeRows: {
         XT *T = (XT *)p.resid;   // workspace [batch, rows, K]
         const int64_t tiles = p.batch * ((p.rows + 63) / 64) * ((p.K + 63) / 64);
+        const int64_t xsz = (int64_t)sizeof(XT);
+        const int vec_loads = aligned(p.X, 16) && (p.xs_k * xsz) % 16 == 0 &&
+                              (p.xs_b * xsz) % 16 == 0;
         hipLaunchKernelGGL((transpose_kernel<XT>), dim3((unsigned)tiles), dim3(256), 0, st,
-                           (const XT *)p.X, p.batch, p.rows, p.K, p.xs_b, p.xs_k, T);
+                           (const XT *)p.X, p.batch, p.rows, p.K, p.xs_b, p.xs_k, T, vec_loads);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         SplitParams q = p;

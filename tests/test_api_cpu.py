@@ -87,6 +87,9 @@ def test_split_abi_rejects_bad_arguments_on_host():
     assert nb.value == 1 * 2 * 3 * 4
     assert L.ozk_split(p, _lib.OZK_F64, 1, 2, 3, xs_bad, 2, 7, _lib.OZK_I8, p, s4, p, s3, null,
                        0, null) == _lib.OZK_ERR_WORKSPACE
+    # a workspace must be 16-byte aligned (checked before anything is enqueued)
+    assert L.ozk_split(p, _lib.OZK_F64, 1, 2, 3, xs_bad, 2, 7, _lib.OZK_I8, p, s4, p, s3,
+                       ctypes.c_void_p(0x2008), 4096, null) == _lib.OZK_ERR_WORKSPACE
 
 
 def test_split_workspace_zero_on_resident_paths():
@@ -144,6 +147,7 @@ def test_cross_gemm_abi_checks_and_workspace():
     assert call(K=-3) == _lib.OZK_ERR_SHAPE
     assert call(C=null) == _lib.OZK_ERR_NULL
     assert call(b=b_ncontig) == _lib.OZK_ERR_WORKSPACE
+    assert call(b=b_ncontig, ws=ctypes.c_void_p(0x2004), wsb=1 << 20) == _lib.OZK_ERR_WORKSPACE
     assert call(B=0) == _lib.OZK_OK
 
 
