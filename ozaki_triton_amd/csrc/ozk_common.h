@@ -49,71 +49,9 @@ OZK_DEV double pow2d(int e) {
     return __longlong_as_double((long long)(e + 1023) << 52);
 }
 
-// q = src / s with s = 2^(E - alpha), computed as an exact scaling.  For fp64
-// the factor 2^(alpha - E) is always a normal double and the product is the
-// correctly rounded quotient.  For fp32: when alpha - E > 0 the scaling is up
-// and exact, done in two normal steps if the factor exceeds 2^64; when
-// alpha - E <= 0 the factor is >= 2^-127 (a normal or subnormal float) and one
-// IEEE multiply gives the correctly rounded quotient.
-struct ScaleF64 {
-    double inv;
-    OZK_DEV double apply(double x) const { return x * inv; }
-};
-struct ScaleF32 {
-    float inv_a, inv_b;
-    bool two;
-    OZK_DEV float apply(float x) const { return two ? (x * inv_a) * inv_b : x * inv_a; }
-};
-OZK_DEV ScaleF64 make_scale_f64(int e_minus_alpha) {
-    ScaleF64 s;
-    s.inv = pow2d(-e_minus_alpha);
-    return s;
-}
-OZK_DEV ScaleF32 make_scale_f32(int e_minus_alpha) {
-    ScaleF32 s;
-    int up = -e_minus_alpha;
-    if (up > 64) {
-        s.two = true;
-        s.inv_a = pow2f(64);
-        s.inv_b = pow2f(up - 64);
-    } else {
-        s.two = false;
-        s.inv_a = pow2f(up);
-        s.inv_b = 1.0f;
-    }
-    return s;
-}
-
-// int8 slice of ozaki_triton.py:199-200 in the residual dtype R:
-// t = fl_R(q + 0.5) if q >= 0 else fl_R(q - 0.5); clamp to [-128, 127];
-// convert toward zero.
-OZK_DEV int quant_i8(double q) {
-    double t = (q >= 0.0) ? q + 0.5 : q - 0.5;
-    t = fmin(fmax(t, -128.0), 127.0);
-    return (int)t;
-}
-OZK_DEV int quant_i8(float q) {
-    float t = (q >= 0.0f) ? q + 0.5f : q - 0.5f;
-    t = fminf(fmaxf(t, -128.0f), 127.0f);
-    return (int)t;
-}
-
-// Round half away from zero of an fp32 value q with |q| <= 2^8 (an exact
-// function of q): trunc(q) +/- 1 when |q - trunc(q)| >= 0.5.  This equals
-// trunc(fl64(q +/- 0.5)) for every fp32 q: q has at most 24 significant bits
-// and |q| < 2^9, so q +/- 0.5 is exact in binary64.  The result is returned
-// as an integer value in float, already limited to 127 from above (q never
-// goes below -2^alpha (1 + 2^-18), whose rounding is -128 anyway).
-OZK_DEV float round_away_exact(float q) {
-    const float t = truncf(q);
-    const float d = q - t;   // exact
-    float r = t;
-    if (fabsf(d) >= 0.5f) r = t + copysignf(1.0f, q);
-    return fminf(r, 127.0f);
-}
-
-// Single round-to-nearest-even conversions to binary16 (bit patterns), written
-// with integer arithmetic so the result does not depend on the denormal mode.
+// Single round-to-nearest-even conversion of a binary64 value to binary16 (bit
+// pattern), written with integer arithmetic: one rounding from fp64, which a
+// conversion through fp32 would not give.
 OZK_DEV uint32_t f64_to_f16_bits(double x) {
     uint64_t u = (uint64_t)__double_as_longlong(x);
     uint32_t s = (uint32_t)((u >> 48) & 0x8000u);
@@ -131,26 +69,6 @@ OZK_DEV uint32_t f64_to_f16_bits(double x) {
     uint64_t half = 1ull << (shift - 1);
     if (rem > half || (rem == half && (n & 1ull))) ++n;
     uint32_t b = (e <= -14) ? (uint32_t)n : (uint32_t)(((e + 14) << 10) + (int)n);
-    if (b >= 0x7C00u) b = 0x7C00u;
-    return s | b;
-}
-OZK_DEV uint32_t f32_to_f16_bits(float x) {
-    uint32_t u = __float_as_uint(x);
-    uint32_t s = (u >> 16) & 0x8000u;
-    int be = (int)((u >> 23) & 0xFFu);
-    uint32_t m = u & 0x7FFFFFu;
-    if (be == 0xFF) return s | (m ? 0x7E00u : 0x7C00u);
-    if (be == 0) return s;
-    uint32_t sig = (1u << 23) | m;
-    int e = be - 127;
-    int qe = (e < -14 ? -14 : e) - 10;
-    int shift = qe - (e - 23);          // >= 13
-    if (shift > 24) return s;           // |x| < 2^(qe-1): rounds to 0
-    uint32_t n = sig >> shift;
-    uint32_t rem = sig & ((1u << shift) - 1u);
-    uint32_t half = 1u << (shift - 1);
-    if (rem > half || (rem == half && (n & 1u))) ++n;
-    uint32_t b = (e <= -14) ? n : (uint32_t)(((e + 14) << 10) + (int)n);
     if (b >= 0x7C00u) b = 0x7C00u;
     return s | b;
 }
