@@ -73,15 +73,19 @@ int ozk_compute_split_bits(int64_t n, int slice_dtype, int dot_accum_dtype, int 
 /*
  * Split -- replaces the launch of split_matrix_kernel in split_matrix
  * (ozaki_triton.py:214-256; kernel 137-211).
- *   X       [batch, rows, K]      x_dtype OZK_F64 or OZK_F32, strides x_strides
- *   slices  [batch, L, rows, K]   slice_dtype OZK_I8 or OZK_F16, strides slice_strides
+ *   X       [batch, rows, K]      x_dtype any of OZK_F64 / F32 / F16 / BF16 / I8
+ *                                 (ozaki_triton.py:42-48), strides x_strides
+ *   slices  [batch, L, rows, K]   slice_dtype OZK_I8 / F16 / BF16 / F32, strides
+ *                                 slice_strides
  *   scales  [batch, L, rows]      fp32, strides scale_strides
  * For each row: L levels of (row max -> power-of-two scale -> quantise ->
- * residual), with the residual rounded to fp32 between levels exactly as the
+ * residual), in fp64 for fp64 input and fp32 otherwise (narrow inputs convert
+ * exactly), with the residual rounded to fp32 between levels exactly as the
  * reference's fp32 residual buffer does.  B is split through its transposed
  * view (rows = columns of B, x_strides = {K*N, 1, N}).
- * Workspace: 0 bytes on the resident fast paths; otherwise
- * ozk_split_workspace_bytes() (an fp32 residual, batch*rows*K*4 bytes).
+ * Workspace: 0 bytes on the resident fast paths (fp64 / fp32 input); otherwise
+ * ozk_split_workspace_bytes(): an fp32 copy of a narrow input, a transposed
+ * copy of a long column operand, or an fp32 residual for odd layouts.
  */
 int ozk_split_workspace_bytes(int x_dtype, int64_t batch, int64_t rows, int64_t K,
                               const int64_t x_strides[3], int num_splits, int slice_dtype,
@@ -101,10 +105,13 @@ int ozk_split(const void *X, int x_dtype, int64_t batch, int64_t rows, int64_t K
  *                              passes a K-contiguous view, b_strides[2] == 1)
  *   A_scales [batch, L, M] fp32, B_scales [batch, L, N] fp32
  *   C        [batch, M, N]  out_dtype OZK_F64 (fp64 outer accumulator) or
- *                           OZK_F32 (fp32 outer accumulator)
+ *                           OZK_F32 / F16 / BF16 / I8 (fp32 outer accumulator,
+ *                           stored rounded to nearest even, or for I8 truncated
+ *                           toward zero and saturated)
  *   C = sum_{i,j} fl32(fl32(fl32(A_i B_j) * sa_i) * sb_j), summed i-major,
  *   j-minor from 0 in the outer accumulator.  int8 slices use an exact int32
- *   dot (MFMA i8), fp16 slices an fp32-accumulated dot (MFMA f16).
+ *   dot (MFMA i8); fp16 / bf16 / fp32 slices an fp32-accumulated dot (MFMA f16,
+ *   bf16, f32).
  * Workspace: 0 bytes when both slice operands are K-contiguous with 16-byte
  * aligned rows; otherwise ozk_cross_gemm_workspace_bytes() for a packed copy.
  */

@@ -16,7 +16,9 @@ front end that mirrors the reference's Python structure:
 
 Pins (see tests/test_oracle_*.py): the exponent rule against numpy's float32
 log2 and the committed exhaustive band table; fp64->fp16 rounding against
-numpy's astype; split invariants (powers-of-two scales, int8 range, exact
+numpy's astype; fp64->bf16 rounding against exact rational rounding and
+torch's fp32->bf16; narrow inputs split as their exact fp32 values; fp32
+slices; the C casts to fp16 / bf16 / int8; split invariants (powers-of-two scales, int8 range, exact
 reconstruction of fp32 inputs, residual bounds); the int8 cross-GEMM against
 numpy's exact int64 matmul and against the fp64 product of the reconstructed
 operands; and the end-to-end relative errors the reference publishes in
@@ -72,6 +74,10 @@ def lib() -> ctypes.CDLL:
         L.ozo_f64_to_f16_array.restype = None
         L.ozo_ceil_log2_f32_array.argtypes = [vp, vp, i64]
         L.ozo_ceil_log2_f32_array.restype = None
+        L.ozo_f64_to_bf16_array.argtypes = [vp, vp, i64]
+        L.ozo_f64_to_bf16_array.restype = None
+        L.ozo_bf16_to_f64_array.argtypes = [vp, vp, i64]
+        L.ozo_bf16_to_f64_array.restype = None
         _lib = L
     return _lib
 
@@ -81,10 +87,15 @@ def _ptr(a: np.ndarray) -> int:
 
 
 def code_of(dtype) -> int:
-    """Map a numpy / torch dtype (or its name) to the shared dtype code."""
+    """Map a numpy / torch dtype (or its name) to the shared dtype code.  numpy
+    has no bfloat16: a uint16 array holds bfloat16 bit patterns."""
     name = str(dtype).replace("torch.", "")
-    return {"float64": F64, "float32": F32, "float16": F16, "bfloat16": BF16,
+    return {"float64": F64, "float32": F32, "float16": F16, "bfloat16": BF16, "uint16": BF16,
             "int8": I8, "int32": I32}[name]
+
+
+# numpy storage of each dtype code (bfloat16 as uint16 bit patterns)
+_NP_OF = {F64: np.float64, F32: np.float32, F16: np.float16, BF16: np.uint16, I8: np.int8}
 
 
 # --------------------------------------------------------------------------- #
@@ -112,6 +123,27 @@ def f64_to_f16(x: np.ndarray) -> np.ndarray:
     return out.view(np.float16)
 
 
+def f64_to_bf16(x: np.ndarray) -> np.ndarray:
+    """Single-rounding binary64 -> bfloat16; returns the uint16 bit patterns."""
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().ozo_f64_to_bf16_array(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def bf16_to_f64(h: np.ndarray) -> np.ndarray:
+    """Exact bfloat16 bit patterns -> binary64 values."""
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, dtype=np.float64)
+    lib().ozo_bf16_to_f64_array(_ptr(h), _ptr(out), h.size)
+    return out
+
+
+def to_f64(a: np.ndarray) -> np.ndarray:
+    """Exact values of an array in any shared dtype (uint16 = bfloat16 bits)."""
+    return bf16_to_f64(a) if a.dtype == np.uint16 else a.astype(np.float64)
+
+
 def scale_from_max(mu: float, alpha: int) -> float:
     return float(lib().ozo_scale_from_max(mu, alpha))
 
@@ -127,8 +159,7 @@ def split(X: np.ndarray, num_splits: int, alpha: int, slice_dtype):
     item = X.itemsize
     sr, sk = X.strides[0] // item, X.strides[1] // item
     # hand the C code the base pointer of the (possibly strided) view
-    np_slice = np.int8 if sd == I8 else np.float16
-    slices = np.empty((num_splits, rows, K), dtype=np_slice)
+    slices = np.empty((num_splits, rows, K), dtype=_NP_OF[sd])
     scales = np.empty((num_splits, rows), dtype=np.float32)
     rc = lib().ozo_split(X.ctypes.data, xd, rows, K, sr, sk, num_splits, alpha, sd,
                          _ptr(slices), _ptr(scales))
@@ -149,7 +180,7 @@ def cross_gemm(As: np.ndarray, Bs_T: np.ndarray, sa: np.ndarray, sb: np.ndarray,
     L2, N, K2 = Bs_T.shape
     assert L == L2 and K == K2
     od = code_of(out_dtype)
-    C = np.empty((M, N), dtype=np.float64 if od == F64 else np.float32)
+    C = np.empty((M, N), dtype=_NP_OF[od])
     rc = lib().ozo_cross_gemm(_ptr(As), _ptr(Bs_T), _ptr(sa), _ptr(sb), M, N, K, L,
                               code_of(As.dtype), _ptr(C), od)
     if rc != 0:
@@ -176,8 +207,8 @@ def ozaki_matmul(A: np.ndarray, B: np.ndarray, num_splits: int, slice_dtype,
                  return_parts: bool = False):
     """numpy restatement of ozaki_matmul (ozaki_triton.py:534-606): broadcast the
     batch dims (504-531), split A rows and B columns (through B^T, 593-595),
-    cross-GEMM per batch, output in the input dtype."""
-    assert A.dtype == B.dtype and A.dtype in (np.float64, np.float32)
+    cross-GEMM per batch, output in the input dtype (bfloat16 as uint16 bits)."""
+    assert A.dtype == B.dtype and code_of(A.dtype) in (F64, F32, F16, BF16, I8)
     M, K = A.shape[-2:]
     K2, N = B.shape[-2:]
     assert K == K2

@@ -19,12 +19,18 @@
  *     ozo_ceil_log2_f32 below.
  *   - q = src / s in RES                          ozaki_triton.py:196
  *   - int8 slice: trunc(clip(fl(q +/- 0.5), -128, 127))  ozaki_triton.py:199-200
- *   - fp16 slice: single round-to-nearest-even from RES   ozaki_triton.py:202
+ *   - fp16 / bf16 / fp32 slice: single round-to-nearest-even from RES
+ *                                                 ozaki_triton.py:202
+ *   - inputs fp16 / bf16 / int8 are converted exactly to the fp32 RES
+ *                                                 ozaki_triton.py:188,190
  *   - residual  r = src - (RES)slice * (RES)s, stored as fp32 for l < L-1
  *                                                 ozaki_triton.py:208-211
  *   - cross-GEMM: acc_ij = A_i . B_j (int32 exact for int8, fp32 hardware for
  *     fp16); t_ij = fl32(fl32(fl32(acc_ij) * sa_i) * sb_j);
- *     out = 0; for i: for j: out = fl_OUTACC(out + t_ij); C = (out dtype) out
+ *     out = 0; for i: for j: out = fl_OUTACC(out + t_ij); C = (out dtype) out,
+ *     where the final cast rounds to nearest even for fp16 / bf16 output and
+ *     truncates toward zero, saturating, for int8 output (the NVIDIA
+ *     float-to-integer conversion the reference's tl.store performs)
  *                                                 ozaki_triton.py:357-452
  *
  * Must be compiled with -ffp-contract=off (no fused multiply-add may merge a
@@ -144,11 +150,59 @@ double ozo_f16_to_f64(uint16_t h)
     return s ? -v : v;
 }
 
+/* Round-to-nearest-even binary64 -> bfloat16 in one step.  bfloat16 has
+ * binary32's exponent range and 8 significant bits: quantum 2^(e-7) for a
+ * normal value, 2^-133 below 2^-126.  Returns the bit pattern.                */
+uint16_t ozo_f64_to_bf16(double x)
+{
+    uint64_t u; memcpy(&u, &x, 8);
+    uint16_t s = (uint16_t)((u >> 48) & 0x8000u);
+    int be = (int)((u >> 52) & 0x7FF);
+    uint64_t m = u & 0xFFFFFFFFFFFFFull;
+    if (be == 0x7FF) return (uint16_t)(s | (m ? 0x7FC0u : 0x7F80u));
+    if (be == 0) return s;
+    uint64_t sig = (1ull << 52) | m;
+    int e = be - 1023;
+    int qe = (e < -126 ? -126 : e) - 7;
+    int shift = qe - (e - 52);                   /* >= 45 */
+    if (shift > 63) return s;
+    uint64_t n = sig >> shift;
+    uint64_t rem = sig & ((1ull << shift) - 1);
+    uint64_t half = 1ull << (shift - 1);
+    if (rem > half || (rem == half && (n & 1u))) ++n;
+    uint32_t b = (e <= -126) ? (uint32_t)n : (uint32_t)(((e + 126) << 7) + n);
+    if (b >= 0x7F80u) b = 0x7F80u;
+    return (uint16_t)(s | b);
+}
+
+double ozo_bf16_to_f64(uint16_t h)
+{
+    int s = h >> 15, be = (h >> 7) & 0xFF, m = h & 0x7F;
+    double v;
+    if (be == 0xFF) v = m ? NAN : INFINITY;
+    else if (be == 0) v = ldexp((double)m, -133);
+    else v = ldexp((double)(128 + m), be - 134);
+    return s ? -v : v;
+}
+
+/* an input element as a double (exact for every input dtype) */
+static inline double load_x(const void *X, int dt, int64_t off)
+{
+    switch (dt) {
+    case OZO_F64: return ((const double *)X)[off];
+    case OZO_F32: return (double)((const float *)X)[off];
+    case OZO_F16: return ozo_f16_to_f64(((const uint16_t *)X)[off]);
+    case OZO_BF16: return ozo_bf16_to_f64(((const uint16_t *)X)[off]);
+    default: return (double)((const int8_t *)X)[off];
+    }
+}
+
 /* ------------------------------------------------------------------------ */
 /* Split one operand.
  * X: logical [rows, K] with element strides (stride_r, stride_k), dtype x_dtype
- *    (OZO_F64 or OZO_F32).
- * slices: [L, rows, K] contiguous, dtype slice_dtype (OZO_I8 or OZO_F16 bits).
+ *    (any input dtype; fp16 / bf16 as bit patterns).
+ * slices: [L, rows, K] contiguous, dtype slice_dtype (int8, fp16 / bf16 bits,
+ *    or fp32).
  * scales: [L, rows] contiguous fp32.
  * Follows ozaki_triton.py:157-211 for one batch.  Returns 0, or -1 on a bad
  * argument, -2 on allocation failure.                                          */
@@ -170,10 +224,18 @@ static void quant_store(void *slices, int slice_dtype, size_t idx, double q, int
         int8_t v = (int8_t)(int)t;
         ((int8_t *)slices)[idx] = v;
         *deq = (double)v;
-    } else {
+    } else if (slice_dtype == OZO_F16) {
         uint16_t h = ozo_f64_to_f16(q);          /* q is exact in double for fp32 RES */
         ((uint16_t *)slices)[idx] = h;
         *deq = ozo_f16_to_f64(h);
+    } else if (slice_dtype == OZO_BF16) {
+        uint16_t h = ozo_f64_to_bf16(q);
+        ((uint16_t *)slices)[idx] = h;
+        *deq = ozo_bf16_to_f64(h);
+    } else {                                     /* OZO_F32 */
+        float f = (float)q;                      /* RNE (exact for fp32 RES) */
+        ((float *)slices)[idx] = f;
+        *deq = (double)f;
     }
 }
 
@@ -181,14 +243,12 @@ int ozo_split(const void *X, int x_dtype, int64_t rows, int64_t K, int64_t strid
               int64_t stride_k, int L, int alpha, int slice_dtype, void *slices,
               float *scales)
 {
-    if ((x_dtype != OZO_F64 && x_dtype != OZO_F32) ||
-        (slice_dtype != OZO_I8 && slice_dtype != OZO_F16) || L < 0 || rows < 0 || K < 0)
+    if (x_dtype < OZO_F64 || x_dtype > OZO_I8 || slice_dtype < OZO_F32 || slice_dtype > OZO_I8 ||
+        L < 0 || rows < 0 || K < 0)
         return -1;
     const int res64 = (x_dtype == OZO_F64);
     float *R = (float *)malloc(sizeof(float) * (size_t)(K > 0 ? K : 1));
     if (!R) return -2;
-    const double *X64 = (const double *)X;
-    const float *X32 = (const float *)X;
     for (int64_t r = 0; r < rows; ++r) {
         for (int l = 0; l < L; ++l) {
             /* sweep 0: row max (ozaki_triton.py:172,192) */
@@ -196,8 +256,7 @@ int ozo_split(const void *X, int x_dtype, int64_t rows, int64_t K, int64_t strid
             for (int64_t k = 0; k < K; ++k) {
                 float a;
                 if (l == 0) {
-                    int64_t off = r * stride_r + k * stride_k;
-                    a = res64 ? (float)fabs(X64[off]) : fabsf(X32[off]);
+                    a = (float)fabs(load_x(X, x_dtype, r * stride_r + k * stride_k));
                 } else {
                     a = fabsf(R[k]);
                 }
@@ -210,7 +269,8 @@ int ozo_split(const void *X, int x_dtype, int64_t rows, int64_t K, int64_t strid
                 size_t idx = ((size_t)l * rows + r) * (size_t)K + k;
                 double deq;
                 if (res64) {
-                    double src = (l == 0) ? X64[r * stride_r + k * stride_k] : (double)R[k];
+                    double src = (l == 0) ? load_x(X, x_dtype, r * stride_r + k * stride_k)
+                                          : (double)R[k];
                     double q = src / (double)s;
                     quant_store(slices, slice_dtype, idx, q, 1, &deq);
                     if (l < L - 1) {
@@ -218,7 +278,8 @@ int ozo_split(const void *X, int x_dtype, int64_t rows, int64_t K, int64_t strid
                         R[k] = (float)rr;
                     }
                 } else {
-                    float src = (l == 0) ? X32[r * stride_r + k * stride_k] : R[k];
+                    float src = (l == 0) ? (float)load_x(X, x_dtype, r * stride_r + k * stride_k)
+                                         : R[k];
                     float q = src / s;
                     quant_store(slices, slice_dtype, idx, (double)q, 0, &deq);
                     if (l < L - 1) {
@@ -252,32 +313,50 @@ int64_t ozo_dot_i8(const int8_t *a, const int8_t *b, int64_t K)
 }
 
 /* ------------------------------------------------------------------------ */
+/* The final cast of the fp32 outer accumulator to a non-fp64 output dtype
+ * (ozaki_triton.py:452).                                                      */
+static void store_out(void *C, int out_dtype, int64_t idx, float out)
+{
+    switch (out_dtype) {
+    case OZO_F32: ((float *)C)[idx] = out; break;
+    case OZO_F16: ((uint16_t *)C)[idx] = ozo_f64_to_f16((double)out); break;
+    case OZO_BF16: ((uint16_t *)C)[idx] = ozo_f64_to_bf16((double)out); break;
+    default: {                                   /* OZO_I8 */
+        float t = isnan(out) ? 0.0f : truncf(out);
+        if (t < -128.0f) t = -128.0f;
+        if (t > 127.0f) t = 127.0f;
+        ((int8_t *)C)[idx] = (int8_t)(int)t;
+    }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* Cross-GEMM for one batch.
  * As: [L, M, K] contiguous slices, Bs: [L, N, K] contiguous slices (B^T per
  * slice: the physical layout ozaki_matmul produces, ozaki_triton.py:593-595).
  * sa: [L, M] fp32, sb: [L, N] fp32.  C: [M, N] contiguous, dtype out_dtype
- * (OZO_F64 or OZO_F32); the outer accumulator is fp64 for fp64 output else fp32
+ * (any input dtype); the outer accumulator is fp64 for fp64 output else fp32
  * (ozaki_triton.py:69-73,474).
  * int8 slices: acc_ij is the exact integer dot product (int32 never overflows
  * under the alpha rule, ozaki_triton.py:95); returns -3 if it would.
- * fp16 slices: acc_ij is the binary64 dot product of the exact fp16 values,
- * i.e. an (almost) exact reference for the fp32 hardware accumulation, which
- * a GPU kernel can only match within a tolerance.                             */
+ * fp16 / bf16 / fp32 slices: acc_ij is the binary64 dot product of the exact
+ * slice values, i.e. an (almost) exact reference for the fp32 hardware
+ * accumulation, which a GPU kernel can only match within a tolerance.         */
 int ozo_cross_gemm(const void *As, const void *Bs, const float *sa, const float *sb,
                    int64_t M, int64_t N, int64_t K, int L, int slice_dtype, void *C,
                    int out_dtype)
 {
-    if ((slice_dtype != OZO_I8 && slice_dtype != OZO_F16) ||
-        (out_dtype != OZO_F64 && out_dtype != OZO_F32) || L < 0)
+    if (slice_dtype < OZO_F32 || slice_dtype > OZO_I8 || out_dtype < OZO_F64 ||
+        out_dtype > OZO_I8 || L < 0)
         return -1;
     const int out64 = (out_dtype == OZO_F64);
     double *Bf = NULL, *Af = NULL;
-    if (slice_dtype == OZO_F16) {
+    if (slice_dtype != OZO_I8) {
         Af = (double *)malloc(sizeof(double) * (size_t)(L * M * K + 1));
         Bf = (double *)malloc(sizeof(double) * (size_t)(L * N * K + 1));
         if (!Af || !Bf) { free(Af); free(Bf); return -2; }
-        for (int64_t t = 0; t < (int64_t)L * M * K; ++t) Af[t] = ozo_f16_to_f64(((const uint16_t *)As)[t]);
-        for (int64_t t = 0; t < (int64_t)L * N * K; ++t) Bf[t] = ozo_f16_to_f64(((const uint16_t *)Bs)[t]);
+        for (int64_t t = 0; t < (int64_t)L * M * K; ++t) Af[t] = load_x(As, slice_dtype, t);
+        for (int64_t t = 0; t < (int64_t)L * N * K; ++t) Bf[t] = load_x(Bs, slice_dtype, t);
     }
     float *acc = (float *)malloc(sizeof(float) * (size_t)(L * L + 1));
     if (!acc) { free(Af); free(Bf); return -2; }
@@ -324,7 +403,7 @@ int ozo_cross_gemm(const void *As, const void *Bs, const float *sa, const float 
                         out = out + t2;
                     }
                 }
-                ((float *)C)[m * N + n] = out;
+                store_out(C, out_dtype, m * N + n, out);
             }
         }
     }
@@ -359,4 +438,15 @@ void ozo_f64_to_f16_array(const double *x, uint16_t *out, int64_t n)
 void ozo_ceil_log2_f32_array(const float *x, int32_t *out, int64_t n)
 {
     for (int64_t t = 0; t < n; ++t) out[t] = ozo_ceil_log2_f32(x[t]);
+}
+
+/* Array forms of the bfloat16 conversions. */
+void ozo_f64_to_bf16_array(const double *x, uint16_t *out, int64_t n)
+{
+    for (int64_t t = 0; t < n; ++t) out[t] = ozo_f64_to_bf16(x[t]);
+}
+
+void ozo_bf16_to_f64_array(const uint16_t *h, double *out, int64_t n)
+{
+    for (int64_t t = 0; t < n; ++t) out[t] = ozo_bf16_to_f64(h[t]);
 }

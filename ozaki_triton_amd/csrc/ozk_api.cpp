@@ -12,9 +12,12 @@
 
 namespace {
 
-bool is_input_dtype(int d) { return d == OZK_F64 || d == OZK_F32; }
-bool is_slice_dtype(int d) { return d == OZK_I8 || d == OZK_F16; }
-int slice_size(int d) { return d == OZK_I8 ? 1 : 2; }
+// the reference's _INPUT_DTYPES and _SLICE_DTYPE_INFO (ozaki_triton.py:35-48)
+bool is_input_dtype(int d) {
+    return d == OZK_F64 || d == OZK_F32 || d == OZK_F16 || d == OZK_BF16 || d == OZK_I8;
+}
+bool is_slice_dtype(int d) { return d == OZK_F32 || d == OZK_F16 || d == OZK_BF16 || d == OZK_I8; }
+int slice_size(int d) { return d == OZK_I8 ? 1 : d == OZK_F32 ? 4 : 2; }
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
 int hip_status(hipError_t e) { return e == hipSuccess ? OZK_OK : OZK_ERR_LAUNCH; }
@@ -117,7 +120,7 @@ int ozk_split_workspace_bytes(int x_dtype, int64_t batch, int64_t rows, int64_t 
                                            num_splits, 1, (void *)256, slice_strides, nullptr,
                                            x_strides);
     const ozk::SplitPlan plan = ozk::plan_split(p, x_dtype, slice_dtype);
-    *bytes_out = ozk::split_workspace_bytes(p, plan, x_dtype);
+    *bytes_out = ozk::split_workspace_bytes(p, plan, x_dtype, slice_dtype);
     return OZK_OK;
 }
 
@@ -136,7 +139,7 @@ int ozk_split(const void *X, int x_dtype, int64_t batch, int64_t rows, int64_t K
     ozk::SplitParams p = make_split_params(X, batch, rows, K, x_strides, num_splits, alpha,
                                            slices, slice_strides, scales, scale_strides);
     const ozk::SplitPlan plan = ozk::plan_split(p, x_dtype, slice_dtype);
-    const size_t need = ozk::split_workspace_bytes(p, plan, x_dtype);
+    const size_t need = ozk::split_workspace_bytes(p, plan, x_dtype, slice_dtype);
     if (need > 0) {
         if (!workspace || workspace_bytes < need || (uintptr_t)workspace % 16 != 0)
             return OZK_ERR_WORKSPACE;
@@ -193,7 +196,8 @@ int ozk_cross_gemm(const void *A_slices, const int64_t a_strides[4], const void 
     p.M = M;
     p.N = N;
     p.K = K;
-    if (num_splits == 0) return hip_status(ozk::launch_zero_c(p, out_dtype, st));
+    p.out_dtype = out_dtype;
+    if (num_splits == 0) return hip_status(ozk::launch_zero_c(p, st));
     if (!A_slices || !B_slices || !A_scales || !B_scales) return OZK_ERR_NULL;
 
     const int es = slice_size(slice_dtype);
@@ -237,7 +241,7 @@ int ozk_cross_gemm(const void *A_slices, const int64_t a_strides[4], const void 
         p.bs_n = b_strides[3];
     }
     const ozk::GemmPlan plan = ozk::plan_gemm(p, num_splits, slice_dtype);
-    return hip_status(ozk::launch_gemm(p, plan, num_splits, slice_dtype, out_dtype, st));
+    return hip_status(ozk::launch_gemm(p, plan, num_splits, slice_dtype, st));
 }
 
 }  // extern "C"

@@ -72,6 +72,38 @@ OZK_DEV uint32_t f64_to_f16_bits(double x) {
     if (b >= 0x7C00u) b = 0x7C00u;
     return s | b;
 }
+// Single round-to-nearest-even conversion of a binary64 value to bfloat16 (bit
+// pattern).  bfloat16 has binary32's exponent range and 8 significant bits:
+// quantum 2^(e-7) for a normal value, 2^-133 below 2^-126.
+OZK_DEV uint32_t f64_to_bf16_bits(double x) {
+    uint64_t u = (uint64_t)__double_as_longlong(x);
+    uint32_t s = (uint32_t)((u >> 48) & 0x8000u);
+    int be = (int)((u >> 52) & 0x7FF);
+    uint64_t m = u & 0xFFFFFFFFFFFFFull;
+    if (be == 0x7FF) return s | (m ? 0x7FC0u : 0x7F80u);
+    if (be == 0) return s;
+    uint64_t sig = (1ull << 52) | m;
+    int e = be - 1023;
+    int qe = (e < -126 ? -126 : e) - 7;
+    int shift = qe - (e - 52);          // >= 45
+    if (shift > 63) return s;
+    uint64_t n = sig >> shift;
+    uint64_t rem = sig & ((1ull << shift) - 1ull);
+    uint64_t half = 1ull << (shift - 1);
+    if (rem > half || (rem == half && (n & 1ull))) ++n;
+    uint32_t b = (e <= -126) ? (uint32_t)n : (uint32_t)(((e + 126) << 7) + (int)n);
+    if (b >= 0x7F80u) b = 0x7F80u;
+    return s | b;
+}
+// Round-to-nearest-even binary32 -> bfloat16 bits for finite x: add half an
+// ulp of the kept part (minus one on even) and drop the low 16 bits; a carry
+// out of the mantissa steps the exponent, up to infinity.
+OZK_DEV uint32_t f32_to_bf16_bits(float x) {
+    const uint32_t u = __float_as_uint(x);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+OZK_DEV float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
 // exact binary16 -> binary32 (every binary16 value is a binary32 value)
 OZK_DEV float f16_bits_to_f32(uint32_t h) {
     uint32_t s = (h & 0x8000u) << 16;

@@ -4,14 +4,17 @@
 //   C[m, n] = sum_{i<L} sum_{j<L} fl32(fl32(fl32(acc_ij[m, n]) * sa_i[m]) * sb_j[n])
 //   acc_ij  = A_i[m, :] . B_j[:, n]        (int8: exact int32, fp16: fp32 MFMA)
 //   the outer sum runs i-major, j-minor from +0 in the output's accumulator
-//   dtype (fp64 for fp64 inputs, fp32 for fp32), exactly as the reference.
+//   dtype (fp64 for fp64 output, fp32 for every other output dtype), exactly as
+//   the reference; kernels are templated on the slice type (int8, fp16, bf16,
+//   fp32) and that accumulator type, and store_c converts to C's dtype.
 //
 // Design (one workgroup = 256 lanes = 4 waves in a 2 x 2 grid):
 //   * Every wave owns a (32*MI) x (32*NI) block of C and ALL L*L slice pairs
 //     for it, so each output element's L*L accumulators live in one lane and
 //     the ordered epilogue needs no cross-wave traffic.
-//   * v_mfma_i32_32x32x32_i8 / v_mfma_f32_32x32x16_f16: 32 bytes of K per row
-//     per instruction, 16 accumulator registers per lane.
+//   * v_mfma_i32_32x32x32_i8 / v_mfma_f32_32x32x16_f16 / _bf16: 32 bytes of K
+//     per row per instruction, 16 accumulator registers per lane (fp32 slices:
+//     four v_mfma_f32_32x32x2_f32 per 32 bytes).
 //   * Both operands are K-contiguous ([L, M, K] and B^T = [L, N, K]); a stage
 //     holds 128 bytes of K for all L*(BM+BN) rows, staged global -> VGPR ->
 //     LDS with the next stage's loads in flight during the current MFMAs
@@ -56,9 +59,52 @@ template <> struct Mfma<_Float16> {
     OZK_DEV static float to_f32(float x) { return x; }
 };
 
-template <typename OutT> struct OutAcc;
-template <> struct OutAcc<double> { using T = double; };
-template <> struct OutAcc<float> { using T = float; };
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+template <> struct Mfma<__bf16> {
+    using Acc = f32x16;
+    OZK_DEV static Acc zero() { return Acc{0.0f}; }
+    OZK_DEV static Acc run(i32x4 a, i32x4 b, Acc c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    }
+    OZK_DEV static float to_f32(float x) { return x; }
+};
+// fp32 slices: a 16-byte fragment is 4 floats; lane (row, h) of the 32x32x2
+// MFMA supplies k = h of that instruction, so MFMA q contracts component q of
+// both operands' fragments (the same k on A and B), 4 MFMAs per fragment.
+// The fragment is bit-cast as a whole: with this compiler, bit-casting the
+// int vector's elements one by one made all four MFMAs read component 0.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+template <> struct Mfma<float> {
+    using Acc = f32x16;
+    OZK_DEV static Acc zero() { return Acc{0.0f}; }
+    OZK_DEV static Acc run(i32x4 a, i32x4 b, Acc c) {
+        const f32x4 fa = __builtin_bit_cast(f32x4, a), fb = __builtin_bit_cast(f32x4, b);
+        c = __builtin_amdgcn_mfma_f32_32x32x2f32(fa.x, fb.x, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x2f32(fa.y, fb.y, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x2f32(fa.z, fb.z, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x2f32(fa.w, fb.w, c, 0, 0, 0);
+        return c;
+    }
+    OZK_DEV static float to_f32(float x) { return x; }
+};
+
+// Final store of the outer accumulator (ozaki_triton.py:452): fp64 output is
+// the fp64 accumulator itself; otherwise the fp32 accumulator is stored as
+// fp32, rounded to nearest even for fp16 / bf16, or truncated toward zero and
+// saturated for int8 (NVIDIA's float-to-integer conversion; NaN -> 0).
+OZK_DEV void store_c(const GemmParams &p, int64_t idx, double v) { ((double *)p.C)[idx] = v; }
+OZK_DEV void store_c(const GemmParams &p, int64_t idx, float v) {
+    switch (p.out_dtype) {
+    case 1: ((float *)p.C)[idx] = v; break;
+    case 2: ((_Float16 *)p.C)[idx] = (_Float16)v; break;
+    case 3: ((uint16_t *)p.C)[idx] = (uint16_t)((v != v) ? 0x7FC0u : f32_to_bf16_bits(v)); break;
+    default: {
+        const float t = (v != v) ? 0.0f : fminf(fmaxf(truncf(v), -128.0f), 127.0f);
+        ((int8_t *)p.C)[idx] = (int8_t)(int)t;
+    }
+    }
+}
 
 OZK_DEV int64_t xcd_remap_gemm(int64_t g, int64_t n) {
     const int64_t q = n / 8;
@@ -90,12 +136,12 @@ OZK_DEV int swz(int row, int chunk) {
     return row * kRowBytes + ((chunk ^ ((row >> 1) & 7)) << 4);
 }
 
-template <typename ST, int L, int MI, int NI, typename OutT>
+template <typename ST, int L, int MI, int NI, typename AccT>
 __global__ __launch_bounds__(256, 1) void cross_gemm_kernel(GemmParams p, int group_m) {
     using Sh = GemmShape<L, MI, NI>;
     using MF = Mfma<ST>;
     using Acc = typename MF::Acc;
-    using OA = typename OutAcc<OutT>::T;
+    using OA = AccT;   // outer accumulator: fp64 for fp64 output, else fp32 (store_c)
     constexpr int BM = Sh::BM, BN = Sh::BN;
     constexpr int ES = (int)sizeof(ST);
     extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -218,7 +264,7 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_kernel(GemmParams p, int gr
     // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
     const float *sab = p.sa + bidx * p.sas_b;
     const float *sbb = p.sb + bidx * p.sbs_b;
-    OutT *Cb = (OutT *)p.C + bidx * p.cs_b;
+    const int64_t cbase = bidx * p.cs_b;
 #pragma unroll
     for (int c = 0; c < NI; ++c) {
         const int64_t col = n0 + wn * 32 * NI + c * 32 + lr;
@@ -244,7 +290,7 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_kernel(GemmParams p, int gr
                             out = out + (OA)t2;
                         }
                     }
-                    Cb[row * p.cs_m + col * p.cs_n] = (OutT)out;
+                    store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
                 }
             }
         }
@@ -298,14 +344,14 @@ template <int N> OZK_DEV void wait_vmcnt() {
 // accesses across the barrier.
 OZK_DEV void exec_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-template <typename ST, int L, int MI, int NI, typename OutT>
+template <typename ST, int L, int MI, int NI, typename AccT>
 __global__ __launch_bounds__(256, 1) void cross_gemm_dma_kernel(GemmParams p, int group_m,
                                                                 uint32_t a_records,
                                                                 uint32_t b_records) {
     using Sh = DmaShape<L, MI, NI>;
     using MF = Mfma<ST>;
     using Acc = typename MF::Acc;
-    using OA = typename OutAcc<OutT>::T;
+    using OA = AccT;   // outer accumulator: fp64 for fp64 output, else fp32 (store_c)
     constexpr int BM = Sh::BM, BN = Sh::BN;
     constexpr int ES = (int)sizeof(ST);
     constexpr uint32_t kOOB = 0x80000000u;
@@ -489,7 +535,7 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_dma_kernel(GemmParams p, in
     // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
     const float *sab = p.sa + bidx * p.sas_b;
     const float *sbb = p.sb + bidx * p.sbs_b;
-    OutT *Cb = (OutT *)p.C + bidx * p.cs_b;
+    const int64_t cbase = bidx * p.cs_b;
 #pragma unroll
     for (int c = 0; c < NI; ++c) {
         const int64_t col = n0 + wn * 32 * NI + c * 32 + lr;
@@ -515,7 +561,7 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_dma_kernel(GemmParams p, in
                             out = out + (OA)t2;
                         }
                     }
-                    Cb[row * p.cs_m + col * p.cs_n] = (OutT)out;
+                    store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
                 }
             }
         }
@@ -551,7 +597,7 @@ template <int L> struct PairShape {
     static_assert(STAGE % 8192 == 0, "stage must be a whole number of 1 KB windows per wave");
 };
 
-template <typename ST, int L, typename OutT>
+template <typename ST, int L, typename AccT>
 __global__ __launch_bounds__(512, 1) void cross_gemm_pair_kernel(GemmParams p, int group_m,
                                                                  uint32_t a_records,
                                                                  uint32_t b_records) {
@@ -559,7 +605,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_pair_kernel(GemmParams p, i
     using PS = PairSplit<L>;
     using MF = Mfma<ST>;
     using Acc = typename MF::Acc;
-    using OA = typename OutAcc<OutT>::T;
+    using OA = AccT;   // outer accumulator: fp64 for fp64 output, else fp32 (store_c)
     constexpr int BM = Sh::BM, BN = Sh::BN;
     constexpr int ES = (int)sizeof(ST);
     constexpr uint32_t kOOB = 0x80000000u;
@@ -651,7 +697,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_pair_kernel(GemmParams p, i
 
     const float *sab = p.sa + bidx * p.sas_b;
     const float *sbb = p.sb + bidx * p.sbs_b;
-    OutT *Cb = (OutT *)p.C + bidx * p.cs_b;
+    const int64_t cbase = bidx * p.cs_b;
     OA *part = (OA *)smem;   // epilogue hand-off [4 blocks][16][64 lanes]
     const int64_t col = n0 + wn * 32 + lr;
     const bool cok = col < p.N;
@@ -761,7 +807,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_pair_kernel(GemmParams p, i
                 OA out = part[(blk * 16 + r) * 64 + lane];
 #pragma unroll
                 for (int q = 0; q < NP; ++q) out = out + (OA)tv[q][r];
-                if (cok && row < p.M) Cb[row * p.cs_m + col * p.cs_n] = (OutT)out;
+                if (cok && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
             }
         }
     };
@@ -801,14 +847,14 @@ template <int L, int NI> struct AdShape {
     static_assert(2 * PER_STAGE * 1 < 64, "vmcnt range");
 };
 
-template <typename ST, int L, int NI, typename OutT>
+template <typename ST, int L, int NI, typename AccT>
 __global__ __launch_bounds__(256, 1) void cross_gemm_ad_kernel(GemmParams p, int group_m,
                                                                uint32_t a_records,
                                                                uint32_t b_records) {
     using Sh = AdShape<L, NI>;
     using MF = Mfma<ST>;
     using Acc = typename MF::Acc;
-    using OA = typename OutAcc<OutT>::T;
+    using OA = AccT;   // outer accumulator: fp64 for fp64 output, else fp32 (store_c)
     constexpr int BM = Sh::BM, BN = Sh::BN;
     constexpr int ES = (int)sizeof(ST);
     constexpr uint32_t kOOB = 0x80000000u;
@@ -955,7 +1001,7 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_ad_kernel(GemmParams p, int
     // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
     const float *sab = p.sa + bidx * p.sas_b;
     const float *sbb = p.sb + bidx * p.sbs_b;
-    OutT *Cb = (OutT *)p.C + bidx * p.cs_b;
+    const int64_t cbase = bidx * p.cs_b;
 #pragma unroll
     for (int c = 0; c < NI; ++c) {
         const int64_t col = n0 + c * 32 + lr;
@@ -979,7 +1025,7 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_ad_kernel(GemmParams p, int
                         out = out + (OA)t2;
                     }
                 }
-                Cb[row * p.cs_m + col * p.cs_n] = (OutT)out;
+                store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
             }
         }
     }
@@ -1001,15 +1047,16 @@ __global__ __launch_bounds__(256) void pack_kernel(PackParams p) {
         const int64_t so = b * p.s_b + l * p.s_l + r * p.s_r + k * p.s_k;
         if (p.esize == 1) {
             ((int8_t *)p.dst)[idx] = (k < p.K) ? ((const int8_t *)p.src)[so] : (int8_t)0;
-        } else {
+        } else if (p.esize == 2) {
             ((uint16_t *)p.dst)[idx] = (k < p.K) ? ((const uint16_t *)p.src)[so] : (uint16_t)0;
+        } else {
+            ((uint32_t *)p.dst)[idx] = (k < p.K) ? ((const uint32_t *)p.src)[so] : 0u;
         }
     }
 }
 
 // num_splits == 0: the reference's kernel stores its zero-initialised outer
 // accumulator (ozaki_triton.py:426,452), so C is all zeros.
-template <typename OutT>
 __global__ __launch_bounds__(256) void zero_c_kernel(GemmParams p) {
     const int64_t total = p.batch * p.M * p.N;
     for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total;
@@ -1017,17 +1064,18 @@ __global__ __launch_bounds__(256) void zero_c_kernel(GemmParams p) {
         const int64_t n = idx % p.N;
         const int64_t m = (idx / p.N) % p.M;
         const int64_t b = idx / (p.N * p.M);
-        ((OutT *)p.C)[b * p.cs_b + m * p.cs_m + n * p.cs_n] = (OutT)0;
+        const int64_t o = b * p.cs_b + m * p.cs_m + n * p.cs_n;
+        if (p.out_dtype == 0) store_c(p, o, 0.0);
+        else store_c(p, o, 0.0f);
     }
 }
 
-hipError_t launch_zero_c(const GemmParams &p, int out_dtype, hipStream_t st) {
+hipError_t launch_zero_c(const GemmParams &p, hipStream_t st) {
     const int64_t total = p.batch * p.M * p.N;
     if (total == 0) return hipSuccess;
     int64_t blocks = (total + 255) / 256;
     if (blocks > 65536) blocks = 65536;
-    if (out_dtype == 0) hipLaunchKernelGGL(zero_c_kernel<double>, dim3((unsigned)blocks), dim3(256), 0, st, p);
-    else hipLaunchKernelGGL(zero_c_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, st, p);
+    hipLaunchKernelGGL(zero_c_kernel, dim3((unsigned)blocks), dim3(256), 0, st, p);
     return hipGetLastError();
 }
 
@@ -1064,7 +1112,7 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype) {
     plan.mi = mi;
     plan.ni = ni;
     plan.group_m = 8;
-    const int es = slice_dtype == 4 ? 1 : 2;
+    const int es = slice_dtype == 4 ? 1 : slice_dtype == 1 ? 4 : 2;
     // OZK_GEMM_KERNEL=staged|dma|ad|pair forces a kernel (tests cover every
     // one at small sizes).  By default, when both operands fit the 31-bit
     // buffer offsets of the LDS-DMA kernels: the pair-split kernel for L >= 3
@@ -1090,10 +1138,10 @@ static int64_t dma_extent(int64_t s_l, int64_t s_r, int L, int64_t rows, int64_t
     return (e < ((int64_t)1 << 31) - 64) ? e : -1;
 }
 
-template <typename ST, int L, int MI, int NI, typename OutT>
+template <typename ST, int L, int MI, int NI, typename AccT>
 static hipError_t launch_dma(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     using Sh = DmaShape<L, MI, NI>;
-    auto kern = cross_gemm_dma_kernel<ST, L, MI, NI, OutT>;
+    auto kern = cross_gemm_dma_kernel<ST, L, MI, NI, AccT>;
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void *)kern,
@@ -1112,10 +1160,10 @@ static hipError_t launch_dma(const GemmParams &p, const GemmPlan &plan, hipStrea
     return hipGetLastError();
 }
 
-template <typename ST, int L, int NI, typename OutT>
+template <typename ST, int L, int NI, typename AccT>
 static hipError_t launch_ad(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     using Sh = AdShape<L, NI>;
-    auto kern = cross_gemm_ad_kernel<ST, L, NI, OutT>;
+    auto kern = cross_gemm_ad_kernel<ST, L, NI, AccT>;
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void *)kern,
@@ -1134,10 +1182,10 @@ static hipError_t launch_ad(const GemmParams &p, const GemmPlan &plan, hipStream
     return hipGetLastError();
 }
 
-template <typename ST, int L, typename OutT>
+template <typename ST, int L, typename AccT>
 static hipError_t launch_pair(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     using Sh = PairShape<L>;
-    auto kern = cross_gemm_pair_kernel<ST, L, OutT>;
+    auto kern = cross_gemm_pair_kernel<ST, L, AccT>;
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void *)kern,
@@ -1156,18 +1204,18 @@ static hipError_t launch_pair(const GemmParams &p, const GemmPlan &plan, hipStre
     return hipGetLastError();
 }
 
-template <typename ST, int L, int MI, int NI, typename OutT>
+template <typename ST, int L, int MI, int NI, typename AccT>
 static hipError_t launch_one(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     if constexpr (L >= 3) {
-        if (plan.kind == kGemmPair) return launch_pair<ST, L, OutT>(p, plan, st);
+        if (plan.kind == kGemmPair) return launch_pair<ST, L, AccT>(p, plan, st);
     }
     if (plan.kind == kGemmAD) {
         constexpr int ANI = (L == 1) ? 8 : (L == 2) ? 4 : 1;
-        return launch_ad<ST, L, ANI, OutT>(p, plan, st);
+        return launch_ad<ST, L, ANI, AccT>(p, plan, st);
     }
-    if (plan.kind == kGemmDMA) return launch_dma<ST, L, MI, NI, OutT>(p, plan, st);
+    if (plan.kind == kGemmDMA) return launch_dma<ST, L, MI, NI, AccT>(p, plan, st);
     using Sh = GemmShape<L, MI, NI>;
-    auto kern = cross_gemm_kernel<ST, L, MI, NI, OutT>;
+    auto kern = cross_gemm_kernel<ST, L, MI, NI, AccT>;
     static bool attr_set = false;   // idempotent; a racing second set is harmless
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void *)kern,
@@ -1183,45 +1231,52 @@ static hipError_t launch_one(const GemmParams &p, const GemmPlan &plan, hipStrea
     return hipGetLastError();
 }
 
-template <typename ST, int L, typename OutT>
+template <typename ST, int L, typename AccT>
 static hipError_t launch_L(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     const int key = plan.mi * 10 + plan.ni;
     if constexpr (L == 1) {
         switch (key) {
-        case 24: return launch_one<ST, 1, 2, 4, OutT>(p, plan, st);
-        case 22: return launch_one<ST, 1, 2, 2, OutT>(p, plan, st);
-        case 12: return launch_one<ST, 1, 1, 2, OutT>(p, plan, st);
-        case 11: return launch_one<ST, 1, 1, 1, OutT>(p, plan, st);
+        case 24: return launch_one<ST, 1, 2, 4, AccT>(p, plan, st);
+        case 22: return launch_one<ST, 1, 2, 2, AccT>(p, plan, st);
+        case 12: return launch_one<ST, 1, 1, 2, AccT>(p, plan, st);
+        case 11: return launch_one<ST, 1, 1, 1, AccT>(p, plan, st);
         }
     } else if constexpr (L == 2) {
         switch (key) {
-        case 22: return launch_one<ST, 2, 2, 2, OutT>(p, plan, st);
-        case 12: return launch_one<ST, 2, 1, 2, OutT>(p, plan, st);
-        case 11: return launch_one<ST, 2, 1, 1, OutT>(p, plan, st);
+        case 22: return launch_one<ST, 2, 2, 2, AccT>(p, plan, st);
+        case 12: return launch_one<ST, 2, 1, 2, AccT>(p, plan, st);
+        case 11: return launch_one<ST, 2, 1, 1, AccT>(p, plan, st);
         }
     } else {
-        if (key == 11) return launch_one<ST, L, 1, 1, OutT>(p, plan, st);
+        if (key == 11) return launch_one<ST, L, 1, 1, AccT>(p, plan, st);
     }
     return hipErrorInvalidValue;
 }
 
-template <typename ST, typename OutT>
+template <typename ST, typename AccT>
 static hipError_t launch_st(const GemmParams &p, const GemmPlan &plan, int L, hipStream_t st) {
     switch (L) {
-    case 1: return launch_L<ST, 1, OutT>(p, plan, st);
-    case 2: return launch_L<ST, 2, OutT>(p, plan, st);
-    case 3: return launch_L<ST, 3, OutT>(p, plan, st);
-    case 4: return launch_L<ST, 4, OutT>(p, plan, st);
+    case 1: return launch_L<ST, 1, AccT>(p, plan, st);
+    case 2: return launch_L<ST, 2, AccT>(p, plan, st);
+    case 3: return launch_L<ST, 3, AccT>(p, plan, st);
+    case 4: return launch_L<ST, 4, AccT>(p, plan, st);
     }
     return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemm(const GemmParams &p, const GemmPlan &plan, int L, int slice_dtype,
-                       int out_dtype, hipStream_t st) {
-    if (slice_dtype == 4 && out_dtype == 0) return launch_st<int8_t, double>(p, plan, L, st);
-    if (slice_dtype == 4 && out_dtype == 1) return launch_st<int8_t, float>(p, plan, L, st);
-    if (slice_dtype == 2 && out_dtype == 0) return launch_st<_Float16, double>(p, plan, L, st);
-    if (slice_dtype == 2 && out_dtype == 1) return launch_st<_Float16, float>(p, plan, L, st);
+                       hipStream_t st) {
+    const bool acc64 = p.out_dtype == 0;
+    switch (slice_dtype) {
+    case 4: return acc64 ? launch_st<int8_t, double>(p, plan, L, st)
+                         : launch_st<int8_t, float>(p, plan, L, st);
+    case 2: return acc64 ? launch_st<_Float16, double>(p, plan, L, st)
+                         : launch_st<_Float16, float>(p, plan, L, st);
+    case 3: return acc64 ? launch_st<__bf16, double>(p, plan, L, st)
+                         : launch_st<__bf16, float>(p, plan, L, st);
+    case 1: return acc64 ? launch_st<float, double>(p, plan, L, st)
+                         : launch_st<float, float>(p, plan, L, st);
+    }
     return hipErrorInvalidValue;
 }
 

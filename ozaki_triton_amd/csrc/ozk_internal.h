@@ -23,10 +23,16 @@ struct SplitParams {
                    // transposed operand [batch, rows, K] (transpose + row path)
 };
 
-enum SplitPath { kSplitRows = 0, kSplitStrip = 1, kSplitGeneric = 2, kSplitTransposeRows = 3 };
+enum SplitPath {
+    kSplitRows = 0,
+    kSplitStrip = 1,
+    kSplitGeneric = 2,
+    kSplitTransposeRows = 3,
+    kSplitConvert = 4   // narrow input: exact fp32 copy in the workspace, then the fp32 plan
+};
 
-// Chooses the split kernel for p (x_dtype: 0 = f64, 1 = f32; slice: 4 = i8,
-// 2 = f16).  Returns the path and, for the resident paths, the variant index.
+// Chooses the split kernel for p (x_dtype: 0 = f64, 1 = f32, 2 = f16,
+// 3 = bf16, 4 = i8; slice: 1 = f32, 2 = f16, 3 = bf16, 4 = i8).  Returns the path and, for the resident paths, the variant index.
 struct SplitPlan {
     SplitPath path;
     int variant;
@@ -34,7 +40,8 @@ struct SplitPlan {
 SplitPlan plan_split(const SplitParams &p, int x_dtype, int slice_dtype);
 // scratch the plan needs: fp32 residual (generic path, L > 1) or the
 // transposed operand (transpose + row path)
-size_t split_workspace_bytes(const SplitParams &p, const SplitPlan &plan, int x_dtype);
+size_t split_workspace_bytes(const SplitParams &p, const SplitPlan &plan, int x_dtype,
+                             int slice_dtype);
 hipError_t launch_split(const SplitParams &p, const SplitPlan &plan, int x_dtype,
                         int slice_dtype, hipStream_t stream);
 
@@ -53,6 +60,8 @@ struct GemmParams {
     void *C;
     int64_t cs_b, cs_m, cs_n;
     int64_t batch, M, N, K;
+    int out_dtype;              // C's dtype code: 0 f64 (fp64 outer accumulator), else
+                                // f32 / f16 / bf16 / i8 (fp32 outer accumulator)
 };
 
 enum GemmKind {
@@ -68,9 +77,9 @@ struct GemmPlan {
 };
 GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype);
 hipError_t launch_gemm(const GemmParams &p, const GemmPlan &plan, int L, int slice_dtype,
-                       int out_dtype, hipStream_t stream);
+                       hipStream_t stream);
 
-hipError_t launch_zero_c(const GemmParams &p, int out_dtype, hipStream_t stream);
+hipError_t launch_zero_c(const GemmParams &p, hipStream_t stream);
 
 // Packs slices [batch, L, rows, K] (any strides) into a K-contiguous buffer
 // [batch, L, rows, Kp] with Kp = K rounded up to 16 bytes and zero padding.

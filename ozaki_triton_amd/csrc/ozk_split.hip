@@ -127,6 +127,47 @@ template <int MODE> struct QuantF16F32 {
 template <> struct Quant<_Float16, kQExact> : QuantF16F32<kQExact> {};
 template <> struct Quant<_Float16, kQF32> : QuantF16F32<kQF32> {};
 
+// bfloat16 slices: one RNE rounding of q to 8 significant bits (integer code
+// from fp64 at level 0 of fp64 input; from the exact fp32 q elsewhere)
+template <> struct Quant<__bf16, kQF64> {
+    OZK_DEV static uint32_t run(double x, const LevelScale &c, float *res) {
+        const double q = x * c.inv64;
+        const uint32_t h = f64_to_bf16_bits(q);
+        const double d = (double)bf16_bits_to_f32(h);
+        *res = (float)__builtin_fma(-d, c.s64, x);
+        return h;
+    }
+};
+template <int MODE> struct QuantBF16F32 {
+    OZK_DEV static uint32_t run(float x, const LevelScale &c, float *res) {
+        const float q = __builtin_ldexpf(x, c.up);
+        const uint32_t h = f32_to_bf16_bits(q);
+        *res = __builtin_fmaf(-bf16_bits_to_f32(h), c.s, x);
+        return h;
+    }
+};
+template <> struct Quant<__bf16, kQExact> : QuantBF16F32<kQExact> {};
+template <> struct Quant<__bf16, kQF32> : QuantBF16F32<kQF32> {};
+
+// fp32 slices: the slice is q rounded once to fp32 (exact when RES is fp32 or
+// at levels >= 1, where q is an fp32 value or below 2^-126 either way)
+template <> struct Quant<float, kQF64> {
+    OZK_DEV static uint32_t run(double x, const LevelScale &c, float *res) {
+        const float q = (float)(x * c.inv64);
+        *res = (float)__builtin_fma(-(double)q, c.s64, x);
+        return __float_as_uint(q);
+    }
+};
+template <int MODE> struct QuantF32F32 {
+    OZK_DEV static uint32_t run(float x, const LevelScale &c, float *res) {
+        const float q = __builtin_ldexpf(x, c.up);
+        *res = __builtin_fmaf(-q, c.s, x);
+        return __float_as_uint(q);
+    }
+};
+template <> struct Quant<float, kQExact> : QuantF32F32<kQExact> {};
+template <> struct Quant<float, kQF32> : QuantF32F32<kQF32> {};
+
 template <typename XT> struct Modes;
 template <> struct Modes<double> { static constexpr int first = kQF64, rest = kQExact; };
 template <> struct Modes<float> { static constexpr int first = kQF32, rest = kQF32; };
@@ -140,15 +181,24 @@ template <> struct Store4<int8_t> {
         *(uint32_t *)((int8_t *)base + off) = w;
     }
 };
-template <> struct Store4<_Float16> {
+struct Store4Half {
     OZK_DEV static void run(void *base, int64_t off, const uint32_t v[4]) {
         const uint32_t lo = v[0] | (v[1] << 16), hi = v[2] | (v[3] << 16);
-        *(uint64_t *)((_Float16 *)base + off) = (uint64_t)lo | ((uint64_t)hi << 32);
+        *(uint64_t *)((uint16_t *)base + off) = (uint64_t)lo | ((uint64_t)hi << 32);
+    }
+};
+template <> struct Store4<_Float16> : Store4Half {};
+template <> struct Store4<__bf16> : Store4Half {};
+template <> struct Store4<float> {
+    OZK_DEV static void run(void *base, int64_t off, const uint32_t v[4]) {
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        *(u32x4 *)((uint32_t *)base + off) = u32x4{v[0], v[1], v[2], v[3]};
     }
 };
 template <typename ST> OZK_DEV void store1(void *base, int64_t off, uint32_t v) {
-    if (sizeof(ST) == 1) ((uint8_t *)base)[off] = (uint8_t)v;
-    else ((uint16_t *)base)[off] = (uint16_t)v;
+    if constexpr (sizeof(ST) == 1) ((uint8_t *)base)[off] = (uint8_t)v;
+    else if constexpr (sizeof(ST) == 2) ((uint16_t *)base)[off] = (uint16_t)v;
+    else ((uint32_t *)base)[off] = v;
 }
 
 // Load 4 consecutive elements (16-byte aligned for float, two 16-byte loads
@@ -547,6 +597,40 @@ __global__ __launch_bounds__(256) void transpose_kernel(const XT *__restrict__ X
 }
 
 // ---------------------------------------------------------------------------
+// Exact conversion of a narrow input (fp16 / bf16 / int8, any strides) into
+// an fp32 copy [batch, rows, K] in the workspace.  A thread converts 4
+// consecutive k of one row; rows run fastest when the operand's rows are
+// contiguous (the B^T view), so loads stay coalesced either way.
+// ---------------------------------------------------------------------------
+template <typename XT>
+__global__ __launch_bounds__(256) void convert_kernel(const XT *__restrict__ X, int64_t batch,
+                                                      int64_t rows, int64_t K, int64_t xs_b,
+                                                      int64_t xs_r, int64_t xs_k,
+                                                      float *__restrict__ T, int rows_fast) {
+    const int64_t kq = (K + 3) / 4;
+    const int64_t total = batch * rows * kq;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * 256) {
+        int64_t r, q;
+        if (rows_fast) {
+            r = i % rows;
+            q = (i / rows) % kq;
+        } else {
+            q = i % kq;
+            r = (i / kq) % rows;
+        }
+        const int64_t b = i / (rows * kq);
+        const XT *src = X + b * xs_b + r * xs_r;
+        float *dst = T + (b * rows + r) * K;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t k = 4 * q + u;
+            if (k < K) dst[k] = (float)src[k * xs_k];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Planning and launch.
 // Row variants (GW waves per row, RPB rows per block, NC chunks): capacity
 // 4*NC*64*GW elements.  fp64 rows keep at most 32 values per lane.
@@ -583,9 +667,32 @@ static bool aligned(const void *ptr, int64_t bytes) {
     return ((uintptr_t)ptr % (uintptr_t)bytes) == 0;
 }
 
+static int dtype_size(int code) {
+    switch (code) {
+    case 0: return 8;           // f64
+    case 1: return 4;           // f32
+    case 2: case 3: return 2;   // f16, bf16
+    default: return 1;          // i8
+    }
+}
+
+// layout of the fp32 copy a narrow input (fp16 / bf16 / int8) is split from
+static SplitParams converted_params(const SplitParams &p) {
+    SplitParams q = p;
+    q.xs_b = p.rows * p.K;
+    q.xs_r = p.K;
+    q.xs_k = 1;
+    return q;
+}
+
 SplitPlan plan_split(const SplitParams &p, int x_dtype, int slice_dtype) {
-    const int xsz = (x_dtype == 0) ? 8 : 4;
-    const int ssz = (slice_dtype == 4) ? 1 : 2;
+    // narrow inputs: the reference loads them into its fp32 RES exactly
+    // (ozaki_triton.py:188), so they are converted into the workspace first and
+    // split as fp32 (X is replaced by the workspace at launch, which is 16-byte
+    // aligned; the plan of the copy is taken with that assumption)
+    if (x_dtype >= 2) return {kSplitConvert, 0};
+    const int xsz = dtype_size(x_dtype);
+    const int ssz = dtype_size(slice_dtype);
     const bool k4 = (p.K % 4) == 0;
     const bool slice_ok = p.ss_k == 1 && aligned(p.slices, 4 * ssz) &&
                           (p.ss_r * ssz) % (4 * ssz) == 0 && (p.ss_l * ssz) % (4 * ssz) == 0 &&
@@ -609,7 +716,7 @@ SplitPlan plan_split(const SplitParams &p, int x_dtype, int slice_dtype) {
     }
     // row-contiguous operand with a K too long for a resident strip: transpose
     // into the workspace, then the row kernel (if the row fits)
-    if (k4 && slice_ok && p.xs_r == 1) {
+    if (k4 && slice_ok && p.xs_r == 1 && (p.K * xsz) % 16 == 0) {
         for (int i = 0; i < kNumRowCfgs; ++i) {
             const RowCfg &c = kRowCfgs[i];
             if (x_dtype == 0 && c.nc > 8) continue;
@@ -619,9 +726,22 @@ SplitPlan plan_split(const SplitParams &p, int x_dtype, int slice_dtype) {
     return {kSplitGeneric, 0};
 }
 
-size_t split_workspace_bytes(const SplitParams &p, const SplitPlan &plan, int x_dtype) {
+// plan of the fp32 copy of a narrow input (its X is the 16-byte aligned
+// workspace: `aligned` in plan_split must see an aligned pointer)
+static SplitPlan converted_plan(const SplitParams &p, int slice_dtype) {
+    SplitParams q = converted_params(p);
+    q.X = (const void *)(uintptr_t)256;
+    return plan_split(q, 1, slice_dtype);
+}
+
+size_t split_workspace_bytes(const SplitParams &p, const SplitPlan &plan, int x_dtype,
+                             int slice_dtype) {
     const int64_t n = p.batch * p.rows * p.K;
-    if (plan.path == kSplitTransposeRows) return (size_t)(n * (x_dtype == 0 ? 8 : 4));
+    if (plan.path == kSplitConvert) {
+        const SplitPlan inner = converted_plan(p, slice_dtype);
+        return (size_t)(n * 4) + split_workspace_bytes(converted_params(p), inner, 1, slice_dtype);
+    }
+    if (plan.path == kSplitTransposeRows) return (size_t)(n * dtype_size(x_dtype));
     if (plan.path == kSplitGeneric && p.L > 1) return (size_t)(n * 4);
     return 0;
 }
@@ -705,13 +825,48 @@ static hipError_t launch_typed(const SplitParams &p, const SplitPlan &plan, hipS
     }
 }
 
+template <typename XT>
+static hipError_t launch_convert(const SplitParams &p, float *T, hipStream_t st) {
+    const int64_t total = p.batch * p.rows * ((p.K + 3) / 4);
+    if (total == 0) return hipSuccess;
+    int64_t blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    const int rows_fast = (p.xs_r == 1 && p.xs_k != 1);
+    hipLaunchKernelGGL((convert_kernel<XT>), dim3((unsigned)blocks), dim3(256), 0, st,
+                       (const XT *)p.X, p.batch, p.rows, p.K, p.xs_b, p.xs_r, p.xs_k, T,
+                       rows_fast);
+    return hipGetLastError();
+}
+
+template <typename ST>
+static hipError_t launch_slice(const SplitParams &p, const SplitPlan &plan, int x_dtype,
+                               int slice_dtype, hipStream_t st) {
+    if (x_dtype == 0) return launch_typed<double, ST>(p, plan, st);
+    if (x_dtype == 1) return launch_typed<float, ST>(p, plan, st);
+    // narrow input: convert into the workspace, then split the fp32 copy (any
+    // scratch that split needs follows the copy)
+    float *T = p.resid;
+    hipError_t e;
+    if (x_dtype == 2) e = launch_convert<_Float16>(p, T, st);
+    else if (x_dtype == 3) e = launch_convert<__bf16>(p, T, st);
+    else e = launch_convert<int8_t>(p, T, st);
+    if (e != hipSuccess) return e;
+    SplitParams q = converted_params(p);
+    q.X = T;
+    q.resid = T + p.batch * p.rows * p.K;
+    const SplitPlan inner = plan_split(q, 1, slice_dtype);
+    return launch_typed<float, ST>(q, inner, st);
+}
+
 hipError_t launch_split(const SplitParams &p, const SplitPlan &plan, int x_dtype,
                         int slice_dtype, hipStream_t st) {
     if (p.batch * p.rows == 0 || p.L == 0) return hipSuccess;
-    if (x_dtype == 0 && slice_dtype == 4) return launch_typed<double, int8_t>(p, plan, st);
-    if (x_dtype == 0 && slice_dtype == 2) return launch_typed<double, _Float16>(p, plan, st);
-    if (x_dtype == 1 && slice_dtype == 4) return launch_typed<float, int8_t>(p, plan, st);
-    if (x_dtype == 1 && slice_dtype == 2) return launch_typed<float, _Float16>(p, plan, st);
+    switch (slice_dtype) {
+    case 4: return launch_slice<int8_t>(p, plan, x_dtype, slice_dtype, st);
+    case 2: return launch_slice<_Float16>(p, plan, x_dtype, slice_dtype, st);
+    case 3: return launch_slice<__bf16>(p, plan, x_dtype, slice_dtype, st);
+    case 1: return launch_slice<float>(p, plan, x_dtype, slice_dtype, st);
+    }
     return hipErrorInvalidValue;
 }
 

@@ -12,8 +12,9 @@ dtype policy and assertion messages):
 
 All arithmetic runs in the HIP kernels of libozaki_amd.so, called through the C
 ABI of include/ozaki_amd.h.  Tensors must live on a ROCm GPU; there is no CPU
-path.  Supported dtype combinations: input float64 / float32 with int8 or
-float16 slices (the others the reference accepts raise NotImplementedError).
+path.  Every dtype combination the reference accepts is supported: inputs
+float64 / float32 / float16 / bfloat16 / int8 with float32 / float16 / bfloat16 /
+int8 slices (ozaki_triton.py:35-48); C has the input dtype.
 
 Differences from the reference that do not change any value:
 * both splits run on the caller's current stream (the reference's two side
@@ -56,8 +57,10 @@ _INPUT_DTYPES = {
 }
 
 # combinations the HIP kernels implement
-_SUPPORTED_INPUTS = (torch.float64, torch.float32)
-_SUPPORTED_SLICES = (torch.int8, torch.float16)
+# dtypes the kernels take: all of the reference's tables (C may also be float32
+# etc. through cross_gemm's output_dtype; int32 output is not an input dtype)
+_SUPPORTED_INPUTS = (torch.float64, torch.float32, torch.float16, torch.bfloat16, torch.int8)
+_SUPPORTED_SLICES = (torch.float32, torch.float16, torch.bfloat16, torch.int8)
 
 _TORCH_TO_OZK = {
     torch.float64: _lib.OZK_F64,
@@ -118,8 +121,9 @@ def _require_gpu(*tensors: torch.Tensor) -> None:
 def _require_supported(input_dtype: torch.dtype, slice_dtype: torch.dtype) -> None:
     if input_dtype not in _SUPPORTED_INPUTS or slice_dtype not in _SUPPORTED_SLICES:
         raise NotImplementedError(
-            f"input {input_dtype} with {slice_dtype} slices is not implemented by the "
-            "MI355X kernels (supported: float64/float32 inputs, int8/float16 slices)")
+            f"input/output {input_dtype} with {slice_dtype} slices is not implemented by the "
+            "MI355X kernels (inputs and outputs: float64, float32, float16, bfloat16, int8; "
+            "slices: float32, float16, bfloat16, int8)")
 
 
 def _stream(dev: torch.device) -> ctypes.c_void_p:

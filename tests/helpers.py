@@ -3,13 +3,25 @@ import numpy as np
 import torch
 
 NP_OF = {torch.float64: np.float64, torch.float32: np.float32, torch.int8: np.int8,
-         torch.float16: np.float16}
+         torch.float16: np.float16, torch.bfloat16: np.uint16}
 NAME_OF = {torch.int8: "int8", torch.float16: "float16", torch.float64: "float64",
-           torch.float32: "float32"}
+           torch.float32: "float32", torch.bfloat16: "bfloat16"}
 
 
 def to_np(t: torch.Tensor) -> np.ndarray:
-    return t.detach().cpu().numpy()
+    """numpy copy of a tensor; bfloat16 (which numpy lacks) as uint16 bit
+    patterns, the oracle's convention."""
+    t = t.detach().cpu()
+    if t.dtype == torch.bfloat16:
+        return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def values(a: np.ndarray) -> np.ndarray:
+    """float64 values of an array (uint16 = bfloat16 bit patterns)."""
+    if a.dtype == np.uint16:
+        return (a.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    return a.astype(np.float64)
 
 
 def oracle_split_batched(oracle, X3: np.ndarray, L: int, alpha: int, slice_dtype):
@@ -40,8 +52,8 @@ def assert_bitwise_equal(got: np.ndarray, want: np.ndarray, what: str = ""):
 
 
 def fp16_cross_bound(oracle_np, A_sl, B_slT, sa, sb):
-    """Error bound for a GPU fp16-slice cross-GEMM against the oracle's (binary64
-    accumulated) result, per output element:
+    """Error bound for a GPU float-slice (fp16 / bf16 / fp32) cross-GEMM against
+    the oracle's (binary64 accumulated) result, per output element:
         sum_ij sa_i sb_j gamma_{K+2} (|A_i| |B_j|^T)  (fp32 dot of K products,
         the fl32 of the accumulator and of the scaled term)
     with gamma_n = n u / (1 - n u), u = 2^-24, plus the rounding of the outer
@@ -49,8 +61,8 @@ def fp16_cross_bound(oracle_np, A_sl, B_slT, sa, sb):
     L, M, K = A_sl.shape
     u = 2.0 ** -24
     g = (K + 2) * u / (1 - (K + 2) * u)
-    Aa = np.abs(A_sl.astype(np.float64))
-    Ba = np.abs(B_slT.astype(np.float64))
+    Aa = np.abs(values(A_sl))
+    Ba = np.abs(values(B_slT))
     bound = np.zeros((M, B_slT.shape[1]))
     mag = np.zeros_like(bound)
     for i in range(L):

@@ -69,8 +69,8 @@ def test_split_abi_rejects_bad_arguments_on_host():
         return L.ozk_split(a["X"], a["xd"], a["B"], a["R"], a["K"], s3, a["L"], a["alpha"],
                            a["sd"], a["S"], s4, a["C"], s3, a["ws"], a["wsb"], null)
 
-    assert call(xd=_lib.OZK_F16) == _lib.OZK_ERR_DTYPE
-    assert call(sd=_lib.OZK_BF16) == _lib.OZK_ERR_DTYPE
+    assert call(xd=_lib.OZK_I32) == _lib.OZK_ERR_DTYPE     # not an input dtype
+    assert call(sd=_lib.OZK_F64) == _lib.OZK_ERR_DTYPE     # not a slice dtype
     assert call(L=5) == _lib.OZK_ERR_SPLITS
     assert call(L=-1) == _lib.OZK_ERR_SPLITS
     assert call(K=-1) == _lib.OZK_ERR_SHAPE
@@ -90,6 +90,32 @@ def test_split_abi_rejects_bad_arguments_on_host():
     # a workspace must be 16-byte aligned (checked before anything is enqueued)
     assert L.ozk_split(p, _lib.OZK_F64, 1, 2, 3, xs_bad, 2, 7, _lib.OZK_I8, p, s4, p, s3,
                        ctypes.c_void_p(0x2008), 4096, null) == _lib.OZK_ERR_WORKSPACE
+
+
+def test_split_workspace_narrow_inputs():
+    """fp16 / bf16 / int8 inputs are split from an exact fp32 copy in the
+    workspace (ozaki_triton.py:188 loads them into the fp32 RES); an odd K
+    adds the generic path's fp32 residual behind the copy."""
+    from ozaki_triton_amd import _lib
+    L = _lib.load()
+    nb = ctypes.c_size_t(0)
+    M, K = 96, 512
+    sl = _lib.i64arr([3 * M * K, M * K, K, 1])
+    for xd in (_lib.OZK_F16, _lib.OZK_BF16, _lib.OZK_I8):
+        for sd in (_lib.OZK_I8, _lib.OZK_F16, _lib.OZK_BF16, _lib.OZK_F32):
+            assert L.ozk_split_workspace_bytes(xd, 1, M, K, _lib.i64arr([M * K, K, 1]), 3, sd, sl,
+                                               ctypes.byref(nb)) == 0
+            assert nb.value == M * K * 4
+    K2 = 510
+    sl2 = _lib.i64arr([3 * M * K2, M * K2, K2, 1])
+    assert L.ozk_split_workspace_bytes(_lib.OZK_F16, 1, M, K2, _lib.i64arr([M * K2, K2, 1]), 3,
+                                       _lib.OZK_I8, sl2, ctypes.byref(nb)) == 0
+    assert nb.value == 2 * M * K2 * 4
+    # fp32 slices are 4 bytes: the resident paths still need no workspace
+    sl4 = _lib.i64arr([2 * M * K, M * K, K, 1])
+    assert L.ozk_split_workspace_bytes(_lib.OZK_F64, 1, M, K, _lib.i64arr([M * K, K, 1]), 2,
+                                       _lib.OZK_F32, sl4, ctypes.byref(nb)) == 0
+    assert nb.value == 0
 
 
 def test_split_workspace_zero_on_resident_paths():
@@ -141,8 +167,8 @@ def test_cross_gemm_abi_checks_and_workspace():
         return L.ozk_cross_gemm(p, a, p, d["b"], p, sc, p, sc, d["B"], M, N, d["K"], d["L"],
                                 d["sd"], d["C"], d["od"], s3, d["ws"], d["wsb"], null)
 
-    assert call(sd=_lib.OZK_F32) == _lib.OZK_ERR_DTYPE
-    assert call(od=_lib.OZK_F16) == _lib.OZK_ERR_DTYPE
+    assert call(sd=_lib.OZK_F64) == _lib.OZK_ERR_DTYPE
+    assert call(od=_lib.OZK_I32) == _lib.OZK_ERR_DTYPE
     assert call(L=5) == _lib.OZK_ERR_SPLITS
     assert call(K=-3) == _lib.OZK_ERR_SHAPE
     assert call(C=null) == _lib.OZK_ERR_NULL
@@ -184,11 +210,13 @@ def test_ozaki_matmul_refuses_cpu_tensors():
 def test_unsupported_combinations_raise():
     import ozaki_triton_amd as ozk
     from ozaki_triton_amd.ozaki import _require_supported
+    # every combination of the reference's tables (ozaki_triton.py:35-48) is taken
+    for x in (torch.float64, torch.float32, torch.float16, torch.bfloat16, torch.int8):
+        for sl in (torch.float32, torch.float16, torch.bfloat16, torch.int8):
+            _require_supported(x, sl)
+    # an int32 C (cross_gemm's output_dtype outside the input dtypes) is not
     with pytest.raises(NotImplementedError):
-        _require_supported(torch.bfloat16, torch.float32)
-    with pytest.raises(NotImplementedError):
-        _require_supported(torch.float64, torch.bfloat16)
-    _require_supported(torch.float64, torch.int8)
+        _require_supported(torch.int32, torch.int8)
     assert ozk.compute_split_bits(8192, torch.int8, torch.int32) == 7
 
 

@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from tests.helpers import (NAME_OF, assert_bitwise_equal, c3_like, fp16_cross_bound,
-                           oracle_split_batched, to_np)
+                           oracle_split_batched, to_np, values)
 
 pytestmark = pytest.mark.gpu
 
@@ -268,3 +268,105 @@ def test_split_transpose_path(oracle, gpu, xdt, sdt):
     B[torch.rand(1, K, 40, generator=g) < 0.01] *= 1e4
     Bd = B.to(xdt).to(gpu)
     _check_split(oracle, ozk, Bd.transpose(-1, -2), 3, sdt, f"transpose {xdt} {sdt}")
+
+
+# --------------------------------------------------------------------------- #
+# the remaining dtypes of the reference's tables (ozaki_triton.py:35-48):
+# fp16 / bf16 / int8 inputs (split in fp32 after an exact conversion), bf16 and
+# fp32 slices, and C in the input dtype
+# --------------------------------------------------------------------------- #
+ALL_INPUTS = [torch.float64, torch.float32, torch.float16, torch.bfloat16, torch.int8]
+ALL_SLICES = [torch.int8, torch.float16, torch.bfloat16, torch.float32]
+NEW_COMBOS = [(x, s) for x in ALL_INPUTS for s in ALL_SLICES if (x, s) not in COMBOS]
+
+
+def _random_input(g, shape, xdt):
+    if xdt == torch.int8:
+        return torch.randint(-128, 128, shape, generator=g, dtype=torch.int8)
+    X = torch.randn(*shape, generator=g, dtype=torch.float64)
+    lo, hi = (-3, 3) if xdt == torch.float16 else (-6, 7)   # keep fp16 products finite
+    X = X * torch.pow(2.0, torch.randint(lo, hi, (*shape[:-1], 1), generator=g).double())
+    return X.to(xdt)
+
+
+@pytest.mark.parametrize("xdt,sdt", NEW_COMBOS)
+@pytest.mark.parametrize("layout", ["rows", "columns", "strided"])
+def test_split_all_dtypes(oracle, gpu, xdt, sdt, layout):
+    """Slices and scales bit-exact for every (input, slice) pair the reference
+    accepts, on K-contiguous rows, on B's columns (transposed view) and on a
+    strided view."""
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(ALL_INPUTS.index(xdt) * 7 + ALL_SLICES.index(sdt))
+    if layout == "rows":
+        X = _random_input(g, (2, 33, 1000), xdt).to(gpu)
+    elif layout == "columns":
+        X = _random_input(g, (2, 1000, 48), xdt).to(gpu).transpose(-1, -2)
+    else:
+        X = _random_input(g, (2, 33, 2 * 300), xdt).to(gpu)[..., ::2]
+    _check_split(oracle, ozk, X, 3, sdt, f"{layout} {xdt} {sdt}")
+
+
+@pytest.mark.parametrize("sdt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("L", [1, 2, 3, 4])
+@pytest.mark.parametrize("M,N,K", [(64, 64, 128), (100, 72, 1040)])
+def test_cross_gemm_bf16_fp32_within_bound(oracle, gpu, sdt, L, M, N, K):
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(M + N + K + L + (7 if sdt == torch.float32 else 0))
+    As = (torch.rand(1, L, M, K, generator=g) * 2 - 1).mul(64).to(sdt)
+    BsT = (torch.rand(1, L, N, K, generator=g) * 2 - 1).mul(64).to(sdt)
+    sa = torch.pow(2.0, torch.randint(-20, 5, (1, L, M), generator=g).float())
+    sb = torch.pow(2.0, torch.randint(-20, 5, (1, L, N), generator=g).float())
+    C = ozk.cross_gemm(As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), L,
+                       torch.float64)
+    torch.cuda.synchronize()
+    a, bT, s_a, s_b = to_np(As[0]), to_np(BsT[0]), to_np(sa[0]), to_np(sb[0])
+    want = oracle.cross_gemm(a, bT, s_a, s_b, "float64")
+    bound = fp16_cross_bound(oracle, a, bT, s_a, s_b)
+    err = np.abs(to_np(C)[0] - want)
+    assert np.all(err <= bound), float((err / np.maximum(bound, 1e-300)).max())
+
+
+@pytest.mark.parametrize("out", [torch.float16, torch.bfloat16, torch.int8])
+@pytest.mark.parametrize("L", [2, 4])
+def test_cross_gemm_output_dtypes_bitexact(oracle, gpu, out, L):
+    """int8 slices make the fp32 outer sum exact to the reference's, so C in
+    fp16 / bf16 (round to nearest even) and int8 (truncate, saturate) is too."""
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(31 + L)
+    As, BsT, sa, sb = _random_slices(g, 1, L, 100, 72, 520, torch.int8)
+    sa = sa * 2.0 ** 12
+    C = ozk.cross_gemm(As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), L, out)
+    torch.cuda.synchronize()
+    want = oracle.cross_gemm(to_np(As[0]), to_np(BsT[0]), to_np(sa[0]), to_np(sb[0]),
+                             NAME_OF[out])
+    assert_bitwise_equal(to_np(C)[0], want, f"out {out} L{L}")
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16, torch.int8])
+@pytest.mark.parametrize("sdt", ALL_SLICES)
+def test_ozaki_matmul_narrow_inputs(oracle, gpu, xdt, sdt):
+    """End to end for the narrow inputs: int8 slices bit-exact; float slices
+    within the fp32 accumulation bound plus one rounding of C's dtype."""
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(ALL_INPUTS.index(xdt) * 5 + ALL_SLICES.index(sdt))
+    A = _random_input(g, (2, 70, 300), xdt)
+    B = _random_input(g, (300, 50), xdt)
+    L = 2
+    C = ozk.ozaki_matmul(A.to(gpu), B.to(gpu), L, sdt)
+    torch.cuda.synchronize()
+    assert C.dtype == xdt and C.shape == (2, 70, 50)
+    want, alpha, parts = oracle.ozaki_matmul(to_np(A), to_np(B), L, NAME_OF[sdt],
+                                             return_parts=True)
+    got = to_np(C)
+    if sdt == torch.int8:
+        assert_bitwise_equal(got, want, f"{xdt} {sdt}")
+        return
+    for b, (a_sl, a_sc, b_sl, b_sc) in enumerate(parts):
+        bound = fp16_cross_bound(oracle, a_sl, b_sl, a_sc, b_sc)
+        gv, wv = values(got[b]), values(want[b])
+        if xdt == torch.int8:
+            slack = 1.0                              # truncation may step by one
+        else:
+            ulp = 2.0 ** -10 if xdt == torch.float16 else 2.0 ** -7
+            slack = ulp * np.abs(wv) + 2.0 ** -24
+        assert np.all(np.abs(gv - wv) <= bound + slack), f"{xdt} {sdt} batch {b}"

@@ -116,6 +116,60 @@ def test_f64_to_f16_is_not_double_rounded(oracle):
 
 
 # --------------------------------------------------------------------------- #
+# bfloat16 rounding: one rounding from RES (ozaki_triton.py:202 with a bf16
+# SLICE_DTYPE); pinned against exact rational rounding and torch's fp32 RNE
+# --------------------------------------------------------------------------- #
+def _bf16_exact(x: float) -> float:
+    """Round-to-nearest-even of x to bfloat16 (8 significant bits, binary32's
+    exponent range, subnormal quantum 2^-133), computed with exact rationals."""
+    from fractions import Fraction
+    if x == 0.0:
+        return x
+    m, e = math.frexp(abs(x))                   # |x| = m 2^e, 0.5 <= m < 1
+    E = max(e - 1, -126)                        # exponent of the leading bit
+    quantum = Fraction(2) ** (E - 7)
+    q = Fraction(abs(x)) / quantum
+    n = math.floor(q)
+    rem = q - n
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    v = float(n * quantum)
+    if v >= 2.0 ** 128:
+        v = math.inf
+    return math.copysign(v, x)
+
+
+def test_f64_to_bf16_matches_exact_rounding(oracle):
+    rng = np.random.default_rng(5)
+    x = np.concatenate([
+        rng.standard_normal(3000) * 2.0 ** rng.integers(-140, 128, 3000).astype(np.float64),
+        (np.arange(-300, 300) + 0.5) * 2.0 ** -133,          # ties in the subnormal range
+        (np.arange(128, 256) + 0.5) * 2.0 ** -7,             # ties at 1..2
+        np.nextafter((np.arange(128, 256) + 0.5) * 2.0 ** -7, 0),
+        np.nextafter((np.arange(128, 256) + 0.5) * 2.0 ** -7, 9),
+        [0.0, -0.0, 2.0 ** 127 * (2 - 2.0 ** -8), 2.0 ** 127 * (2 - 2.0 ** -9), 1e39],
+    ])
+    got = oracle.bf16_to_f64(oracle.f64_to_bf16(x))
+    want = np.array([_bf16_exact(float(v)) for v in x])
+    np.testing.assert_array_equal(got, want)
+
+
+def test_f64_to_bf16_matches_torch_on_fp32_values(oracle):
+    import torch
+    rng = np.random.default_rng(6)
+    x32 = (rng.standard_normal(200000) * 2.0 ** rng.integers(-135, 120, 200000)).astype(np.float32)
+    want = torch.from_numpy(x32).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(oracle.f64_to_bf16(x32.astype(np.float64)), want)
+
+
+def test_f64_to_bf16_is_not_double_rounded(oracle):
+    # just above a bf16 tie; fp64 -> fp32 lands on the tie and would go to even
+    x = 1.0 + 2.0 ** -8 + 2.0 ** -30
+    assert np.float32(x) == np.float32(1.0 + 2.0 ** -8)
+    assert oracle.bf16_to_f64(oracle.f64_to_bf16(np.array([x])))[0] == 1.0 + 2.0 ** -7
+
+
+# --------------------------------------------------------------------------- #
 # split invariants (ozaki_triton.py:157-211)
 # --------------------------------------------------------------------------- #
 def _reconstruct(slices, scales):
@@ -306,3 +360,76 @@ def test_broadcast_batch_matches_per_batch(oracle):
     assert C.shape == (3, 20, 24)
     for b in range(3):
         np.testing.assert_array_equal(C[b], oracle.ozaki_matmul(A[b], B, 3, "float16"))
+
+
+# --------------------------------------------------------------------------- #
+# narrow inputs and fp32 / bf16 slices (ozaki_triton.py:35-48, 188-202, 452)
+# --------------------------------------------------------------------------- #
+@pytest.mark.parametrize("slice_dtype", ["int8", "float16", "bfloat16", "float32"])
+def test_split_narrow_inputs_are_split_as_fp32(oracle, slice_dtype):
+    """fp16 / bf16 / int8 inputs are loaded into the fp32 RES exactly
+    (.to(RESIDUAL_DTYPE), :188), so their split is that of the fp32 values;
+    splitting them in their own precision would round differently."""
+    import torch
+    rng = np.random.default_rng(7)
+    base = rng.standard_normal((13, 200)) * 10.0 ** rng.uniform(-2, 2, (13, 1))
+    alpha = oracle.compute_split_bits(200, slice_dtype,
+                                      "int32" if slice_dtype == "int8" else "float32")
+    x16 = base.astype(np.float16)
+    xb = torch.from_numpy(base).to(torch.bfloat16)
+    xb_bits = xb.view(torch.int16).numpy().view(np.uint16)
+    xi8 = np.clip(np.round(base * 10), -128, 127).astype(np.int8)
+    for narrow, as32 in [(x16, x16.astype(np.float32)),
+                         (xb_bits, xb.to(torch.float32).numpy()),
+                         (xi8, xi8.astype(np.float32))]:
+        sl, sc = oracle.split(narrow, 3, alpha, slice_dtype)
+        sl32, sc32 = oracle.split(as32, 3, alpha, slice_dtype)
+        np.testing.assert_array_equal(sc, sc32)
+        np.testing.assert_array_equal(sl.view(np.uint8), sl32.view(np.uint8))
+
+
+def test_split_fp32_slices(oracle):
+    """fp32 slices of an fp32 input hold q = x / s exactly: level 0 reconstructs
+    X, the residual is 0 and later levels are zero with the floor scale
+    2^(-126 - alpha) of mu = 1e-38f.  For fp64 input the slice is q rounded to
+    fp32 and level 1 splits the fp32 residual fl32(x - slice * s)."""
+    rng = np.random.default_rng(8)
+    X = (rng.standard_normal((9, 64)) * 10.0 ** rng.uniform(-3, 3, (9, 1))).astype(np.float32)
+    alpha = oracle.compute_split_bits(64, "float32", "float32")
+    sl, sc = oracle.split(X, 3, alpha, "float32")
+    np.testing.assert_array_equal(sl[0].astype(np.float64) * sc[0][:, None], X.astype(np.float64))
+    assert np.all(sl[1:] == 0)
+    np.testing.assert_array_equal(sc[1:], np.float32(2.0 ** (-126 - alpha)))
+    X64 = rng.standard_normal((9, 64)) * 10.0 ** rng.uniform(-3, 3, (9, 1))
+    sl, sc = oracle.split(X64, 2, alpha, "float32")
+    q = X64 / sc[0][:, None].astype(np.float64)
+    np.testing.assert_array_equal(sl[0], q.astype(np.float32))
+    r1 = (X64 - sl[0].astype(np.float64) * sc[0][:, None]).astype(np.float32)
+    sl1, sc1 = oracle.split(r1, 1, alpha, "float32")
+    np.testing.assert_array_equal(sl1[0], sl[1])
+
+
+@pytest.mark.parametrize("slice_dtype", ["int8", "float16"])
+def test_cross_gemm_output_conversions(oracle, slice_dtype):
+    """The fp32 outer accumulator is stored rounded to nearest even for fp16 /
+    bf16 output and truncated toward zero, saturating, for int8 output (:452)."""
+    import torch
+    rng = np.random.default_rng(9)
+    L, M, N, K = 2, 7, 5, 64
+    if slice_dtype == "int8":
+        A = rng.integers(-128, 128, (L, M, K)).astype(np.int8)
+        B = rng.integers(-128, 128, (L, N, K)).astype(np.int8)
+    else:
+        A = rng.uniform(-4, 4, (L, M, K)).astype(np.float16)
+        B = rng.uniform(-4, 4, (L, N, K)).astype(np.float16)
+    lo, hi = (-12, 1) if slice_dtype == "int8" else (-4, 4)
+    sa = (2.0 ** rng.integers(lo, hi, (L, M))).astype(np.float32)
+    sb = (2.0 ** rng.integers(lo, hi, (L, N))).astype(np.float32)
+    c32 = oracle.cross_gemm(A, B, sa, sb, "float32")
+    np.testing.assert_array_equal(oracle.cross_gemm(A, B, sa, sb, "float16"),
+                                  c32.astype(np.float16))
+    want_bf = torch.from_numpy(c32).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(oracle.cross_gemm(A, B, sa, sb, "bfloat16"), want_bf)
+    want_i8 = np.clip(np.trunc(c32), -128, 127).astype(np.int8)
+    assert np.abs(c32).max() > 127 and np.abs(c32).min() < 127   # saturating and not
+    np.testing.assert_array_equal(oracle.cross_gemm(A, B, sa, sb, "int8"), want_i8)
