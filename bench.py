@@ -220,31 +220,31 @@ def main():
     print(f"[bench] {args.config}: {xdt}->{sdt} L={L} A{tuple(A.shape)} B{tuple(B.shape)}",
           file=sys.stderr, flush=True)
 
+    # four timing events per step, recorded by the library on the launch
+    # stream between the phases (before the B split, the A split, the
+    # cross-GEMM, and after it); each is recorded once here so that it exists
     phases = ("split_b", "split_a", "cross_gemm", "end")
     events = []
-
-    def marker(step_events):
-        def mark(name):
-            ev = torch.cuda.Event(enable_timing=True)
-            ev.record()
-            step_events[name] = ev
-        return mark
+    for _ in range(args.steps):
+        evs = [torch.cuda.Event(enable_timing=True) for _ in phases]
+        for e in evs:
+            e.record()
+        events.append(evs)
 
     for _ in range(args.warmup):
         _ozaki_matmul_impl(A, B, L, slice_dtype, False, None)
     torch.cuda.synchronize()
 
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        ev = {}
-        C = _ozaki_matmul_impl(A, B, L, slice_dtype, False, marker(ev))
-        events.append(ev)
+    for s in range(args.steps):
+        C = _ozaki_matmul_impl(A, B, L, slice_dtype, False, events[s])
     torch.cuda.synchronize()
     t = time.perf_counter() - t0
     ms = t / args.steps * 1e3
 
     def avg_ms(a, b):
-        return sum(e[a].elapsed_time(e[b]) for e in events) / len(events)
+        ia, ib = phases.index(a), phases.index(b)
+        return sum(e[ia].elapsed_time(e[ib]) for e in events) / len(events)
 
     t_split_b = avg_ms("split_b", "split_a")
     t_split_a = avg_ms("split_a", "cross_gemm")

@@ -129,6 +129,31 @@ int ozk_cross_gemm(const void *A_slices, const int64_t a_strides[4], const void 
                    const int64_t c_strides[3], void *workspace, size_t workspace_bytes,
                    void *stream);
 
+/*
+ * Matmul -- replaces ozaki_matmul below its Python checks (ozaki_triton.py:
+ * 565-606): alpha (compute_split_bits), the split of B through its transposed
+ * view and of A, and the fused cross-GEMM, enqueued on `stream` by one call.
+ *   A [batch, M, K], strides a_strides; B [batch, K, N], strides b_strides;
+ *   a batch stride of 0 broadcasts that operand (it is split once).
+ *   dtype: the input dtype of A and B, which is also C's (any input dtype).
+ *   C [batch, M, N], strides c_strides.
+ * Everything temporary lives in `workspace` (256-byte aligned,
+ * ozk_matmul_workspace_bytes() long), so the call allocates nothing and may be
+ * captured in a HIP graph.  events: NULL, or 4 hipEvent_t (each may be NULL)
+ * recorded on `stream` before the B split, before the A split, before the
+ * cross-GEMM and after it.  Returns OZK_ERR_ALPHA when K is too large for
+ * the slice dtype (the reference asserts) and OZK_ERR_SHAPE for K = 0 (the
+ * reference's log2(0) raises).
+ */
+int ozk_matmul_workspace_bytes(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
+                               const int64_t a_strides[3], const int64_t b_strides[3],
+                               int num_splits, int slice_dtype, size_t *bytes_out);
+
+int ozk_matmul(const void *A, const int64_t a_strides[3], const void *B,
+               const int64_t b_strides[3], int dtype, int64_t batch, int64_t M, int64_t N,
+               int64_t K, int num_splits, int slice_dtype, void *C, const int64_t c_strides[3],
+               void *workspace, size_t workspace_bytes, void *const events[4], void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -33,6 +33,8 @@ EXPORTED = (
     "ozk_split",
     "ozk_cross_gemm_workspace_bytes",
     "ozk_cross_gemm",
+    "ozk_matmul_workspace_bytes",
+    "ozk_matmul",
 )
 
 _lib = None
@@ -75,6 +77,12 @@ def load() -> ctypes.CDLL:
     L.ozk_cross_gemm.argtypes = [vp, p64, vp, p64, vp, p64, vp, p64, i64, i64, i64, i64, i32,
                                  i32, vp, i32, p64, vp, sz, vp]
     L.ozk_cross_gemm.restype = i32
+    L.ozk_matmul_workspace_bytes.argtypes = [i32, i64, i64, i64, i64, p64, p64, i32, i32,
+                                             ctypes.POINTER(ctypes.c_size_t)]
+    L.ozk_matmul_workspace_bytes.restype = i32
+    L.ozk_matmul.argtypes = [vp, p64, vp, p64, i32, i64, i64, i64, i64, i32, i32, vp, p64, vp,
+                             sz, ctypes.POINTER(ctypes.c_void_p), vp]
+    L.ozk_matmul.restype = i32
     _lib = L
     return L
 

@@ -163,7 +163,7 @@ int ozk_cross_gemm_workspace_bytes(int64_t batch, int64_t M, int64_t N, int64_t 
     return OZK_OK;
 }
 
-int ozk_cross_gemm(const void *A_slices, const int64_t a_strides[4], const void *B_slices,
+static int cross_gemm_impl(const void *A_slices, const int64_t a_strides[4], const void *B_slices,
                    const int64_t b_strides[4], const float *A_scales,
                    const int64_t sa_strides[3], const float *B_scales,
                    const int64_t sb_strides[3], int64_t batch, int64_t M, int64_t N, int64_t K,
@@ -242,6 +242,162 @@ int ozk_cross_gemm(const void *A_slices, const int64_t a_strides[4], const void 
     }
     const ozk::GemmPlan plan = ozk::plan_gemm(p, num_splits, slice_dtype);
     return hip_status(ozk::launch_gemm(p, plan, num_splits, slice_dtype, st));
+}
+
+int ozk_cross_gemm(const void *A_slices, const int64_t a_strides[4], const void *B_slices,
+                   const int64_t b_strides[4], const float *A_scales,
+                   const int64_t sa_strides[3], const float *B_scales,
+                   const int64_t sb_strides[3], int64_t batch, int64_t M, int64_t N, int64_t K,
+                   int num_splits, int slice_dtype, void *C, int out_dtype,
+                   const int64_t c_strides[3], void *workspace, size_t workspace_bytes,
+                   void *stream) {
+    return cross_gemm_impl(A_slices, a_strides, B_slices, b_strides, A_scales, sa_strides,
+                           B_scales, sb_strides, batch, M, N, K, num_splits, slice_dtype, C,
+                           out_dtype, c_strides, workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// The whole ozaki_matmul below its Python checks (ozaki_triton.py:565-606):
+// alpha, the split of B through its transposed view and of A, and the
+// cross-GEMM, enqueued on one stream from one call; everything temporary
+// (slices, scales, scratch) lives in the caller's workspace:
+//   [A slices][A scales][B slices][B scales][split scratch][pack scratch],
+// each region 256-byte aligned.  A broadcast operand (batch stride 0) is split
+// once.
+// ---------------------------------------------------------------------------
+namespace {
+
+size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+struct MatmulLayout {
+    int alpha;
+    int64_t bA, bB;                                 // split batches (1 when broadcast)
+    size_t a_sl, a_sc, b_sl, b_sc, scratch, pack;   // byte offsets
+    size_t total;
+    int64_t bt_strides[3];                          // B^T view of B
+    int64_t ga[4], gb[4], gsa[3], gsb[3];           // cross-GEMM strides of the slices
+};
+
+int matmul_layout(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
+                  const int64_t as[3], const int64_t bs[3], int L, int sd, MatmulLayout *o) {
+    if (!is_input_dtype(dtype) || !is_slice_dtype(sd)) return OZK_ERR_DTYPE;
+    if (L < 0 || L > OZK_MAX_SPLITS) return OZK_ERR_SPLITS;
+    if (batch < 0 || M < 0 || N < 0 || K < 0) return OZK_ERR_SHAPE;
+    o->alpha = 0;
+    if (L > 0) {
+        const int st = ozk_compute_split_bits(K, sd, sd == OZK_I8 ? OZK_I32 : OZK_F32, &o->alpha);
+        if (st != OZK_OK) return st;
+    }
+    o->bA = (batch > 1 && as[0] != 0) ? batch : 1;
+    o->bB = (batch > 1 && bs[0] != 0) ? batch : 1;
+    o->bt_strides[0] = bs[0];
+    o->bt_strides[1] = bs[2];
+    o->bt_strides[2] = bs[1];
+    const int64_t ss = slice_size(sd);
+    const int64_t asl[4] = {L * M * K, M * K, K, 1}, bsl[4] = {L * N * K, N * K, K, 1};
+    size_t off = 0;
+    o->a_sl = off; off = align256(off + (size_t)(o->bA * L * M * K * ss));
+    o->a_sc = off; off = align256(off + (size_t)(o->bA * L * M * 4));
+    o->b_sl = off; off = align256(off + (size_t)(o->bB * L * N * K * ss));
+    o->b_sc = off; off = align256(off + (size_t)(o->bB * L * N * 4));
+    size_t scratch = 0;
+    if (L > 0) {
+        const int64_t dummy3[3] = {0, 0, 0};
+        ozk::SplitParams pa = make_split_params((const void *)256, o->bA, M, K, as, L, o->alpha,
+                                                (void *)256, asl, nullptr, dummy3);
+        ozk::SplitParams pb = make_split_params((const void *)256, o->bB, N, K, o->bt_strides,
+                                                L, o->alpha, (void *)256, bsl, nullptr, dummy3);
+        const size_t wa = ozk::split_workspace_bytes(pa, ozk::plan_split(pa, dtype, sd), dtype, sd);
+        const size_t wb = ozk::split_workspace_bytes(pb, ozk::plan_split(pb, dtype, sd), dtype, sd);
+        scratch = wa > wb ? wa : wb;
+    }
+    o->scratch = off; off = align256(off + scratch);
+    // cross-GEMM view of the slices (a batch-1 split is broadcast); they are
+    // K-contiguous from a 256-byte aligned base, so only a row length that is
+    // not a multiple of 16 bytes needs the packed copy
+    const int64_t ga[4] = {o->bA == 1 ? 0 : L * M * K, M * K, K, 1};
+    const int64_t gb[4] = {o->bB == 1 ? 0 : L * N * K, N * K, 1, K};
+    const int64_t gsa[3] = {o->bA == 1 ? 0 : L * M, M, 1};
+    const int64_t gsb[3] = {o->bB == 1 ? 0 : L * N, N, 1};
+    for (int t = 0; t < 4; ++t) { o->ga[t] = ga[t]; o->gb[t] = gb[t]; }
+    for (int t = 0; t < 3; ++t) { o->gsa[t] = gsa[t]; o->gsb[t] = gsb[t]; }
+    const int64_t pk = pack_bytes((const void *)256, ga, batch, L, M, K, (int)ss, false) +
+                       pack_bytes((const void *)256, gb, batch, L, N, K, (int)ss, true);
+    o->pack = off; off = align256(off + (size_t)pk);
+    o->total = off;
+    return OZK_OK;
+}
+
+int record(void *const *events, int i, hipStream_t st) {
+    if (!events || !events[i]) return OZK_OK;
+    return hipEventRecord((hipEvent_t)events[i], st) == hipSuccess ? OZK_OK : OZK_ERR_LAUNCH;
+}
+
+}  // namespace
+
+int ozk_matmul_workspace_bytes(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
+                               const int64_t a_strides[3], const int64_t b_strides[3],
+                               int num_splits, int slice_dtype, size_t *bytes_out) {
+    if (!bytes_out || !a_strides || !b_strides) return OZK_ERR_NULL;
+    MatmulLayout lay;
+    const int st = matmul_layout(dtype, batch, M, N, K, a_strides, b_strides, num_splits,
+                                 slice_dtype, &lay);
+    if (st != OZK_OK) return st;
+    *bytes_out = (batch * M * N == 0 || num_splits == 0) ? 0 : lay.total;
+    return OZK_OK;
+}
+
+int ozk_matmul(const void *A, const int64_t a_strides[3], const void *B,
+               const int64_t b_strides[3], int dtype, int64_t batch, int64_t M, int64_t N,
+               int64_t K, int num_splits, int slice_dtype, void *C, const int64_t c_strides[3],
+               void *workspace, size_t workspace_bytes, void *const events[4], void *stream) {
+    if (!a_strides || !b_strides || !c_strides) return OZK_ERR_NULL;
+    MatmulLayout lay;
+    const int lst = matmul_layout(dtype, batch, M, N, K, a_strides, b_strides, num_splits,
+                                  slice_dtype, &lay);
+    if (lst != OZK_OK) return lst;
+    if (batch * M * N == 0) return OZK_OK;
+    if (!C) return OZK_ERR_NULL;
+    hipStream_t st = (hipStream_t)stream;
+    const int L = num_splits;
+    if (L == 0) {
+        // the reference's kernel stores its zero-initialised accumulator
+        const int64_t z4[4] = {0, 0, 0, 0}, z3[3] = {0, 0, 0};
+        return cross_gemm_impl(nullptr, z4, nullptr, z4, nullptr, z3, nullptr, z3, batch, M, N,
+                               K, 0, slice_dtype, C, dtype, c_strides, nullptr, 0, stream);
+    }
+    if (!A || !B) return OZK_ERR_NULL;
+    if (!workspace || workspace_bytes < lay.total || (uintptr_t)workspace % 256 != 0)
+        return OZK_ERR_WORKSPACE;
+    char *ws = (char *)workspace;
+    const int64_t asl[4] = {L * M * K, M * K, K, 1}, bsl[4] = {L * N * K, N * K, K, 1};
+    const int64_t asc[3] = {L * M, M, 1}, bsc[3] = {L * N, N, 1};
+    int e;
+    // split B through its transposed view, then A (ozaki_triton.py:588-599)
+    if ((e = record(events, 0, st)) != OZK_OK) return e;
+    {
+        ozk::SplitParams p = make_split_params(B, lay.bB, N, K, lay.bt_strides, L, lay.alpha,
+                                               ws + lay.b_sl, bsl, (float *)(ws + lay.b_sc), bsc);
+        const ozk::SplitPlan plan = ozk::plan_split(p, dtype, slice_dtype);
+        p.resid = (float *)(ws + lay.scratch);
+        if (hipError_t he = ozk::launch_split(p, plan, dtype, slice_dtype, st)) return hip_status(he);
+    }
+    if ((e = record(events, 1, st)) != OZK_OK) return e;
+    {
+        ozk::SplitParams p = make_split_params(A, lay.bA, M, K, a_strides, L, lay.alpha,
+                                               ws + lay.a_sl, asl, (float *)(ws + lay.a_sc), asc);
+        const ozk::SplitPlan plan = ozk::plan_split(p, dtype, slice_dtype);
+        p.resid = (float *)(ws + lay.scratch);
+        if (hipError_t he = ozk::launch_split(p, plan, dtype, slice_dtype, st)) return hip_status(he);
+    }
+    if ((e = record(events, 2, st)) != OZK_OK) return e;
+    // cross-GEMM over the K-contiguous slices
+    e = cross_gemm_impl(ws + lay.a_sl, lay.ga, ws + lay.b_sl, lay.gb,
+                        (const float *)(ws + lay.a_sc), lay.gsa, (const float *)(ws + lay.b_sc),
+                        lay.gsb, batch, M, N, K, L, slice_dtype, C, dtype, c_strides,
+                        ws + lay.pack, workspace_bytes - lay.pack, stream);
+    if (e != OZK_OK) return e;
+    return record(events, 3, st);
 }
 
 }  // extern "C"

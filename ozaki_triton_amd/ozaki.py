@@ -305,7 +305,7 @@ def ozaki_matmul(
     return _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, None)
 
 
-def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, mark):
+def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, events):
     """
     Ozaki-scheme matrix product C = A @ B with torch.matmul batch broadcasting.
 
@@ -315,18 +315,19 @@ def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, mark):
        accumulation fused in one MFMA kernel.
 
     Args:
-        A: (..., M, K) float64 / float32 on a ROCm GPU
+        A: (..., M, K) on a ROCm GPU, any of the reference's input dtypes
         B: (..., K, N), same dtype as A
         num_splits: number of slices (<= 4)
-        slice_dtype: torch.int8 or torch.float16
+        slice_dtype: torch.int8, torch.float16, torch.bfloat16 or torch.float32
         verbose: print the chosen parameters
 
     Returns:
         C: (broadcast(...), M, N), dtype of A
 
-    ``mark`` (internal, used by bench.py) is called with a phase name
-    ("split_b", "split_a", "cross_gemm", "end") just before each phase is
-    enqueued, so a caller can record stream events between them.
+    The splits and the cross-GEMM are enqueued by one C call (ozk_matmul) with
+    one workspace holding the slices and scales.  ``events`` (internal, used by
+    bench.py) is None or four torch.cuda.Event objects that the call records
+    before the B split, before the A split, before the cross-GEMM and after it.
     """
     assert A.dtype == B.dtype, f"A/B dtype mismatch: {A.dtype} vs {B.dtype}"
     assert A.dtype in _INPUT_DTYPES, f"unsupported input dtype: {A.dtype}"
@@ -347,8 +348,8 @@ def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, mark):
     if BN == 0:
         return torch.empty(out_shape, dtype=input_dtype, device=A.device)
 
-    alpha = compute_split_bits(K, slice_dtype=slice_dtype, dot_accum_dtype=dot_accum_dtype)
     if verbose:
+        alpha = compute_split_bits(K, slice_dtype=slice_dtype, dot_accum_dtype=dot_accum_dtype)
         print(f"[Ozaki] batch={batch_shape}, M={M}, K={K}, N={N}, "
               f"input={input_dtype}, slice={slice_dtype}, "
               f"dot_accum={dot_accum_dtype}, out_accum={out_accum_dtype}, "
@@ -357,27 +358,31 @@ def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, mark):
     _require_gpu(A, B)
     _require_supported(input_dtype, slice_dtype)
     dev = A.device
-
-    # 2. split: B through its transposed view, so B slices come out [.., N, K]
-    #    (K-contiguous), the layout the MFMA kernel reads
-    if mark:
-        mark("split_b")
-    B_T = B3.transpose(-1, -2)
-    B_slices_T = torch.empty((B3.shape[0], num_splits, N, K), dtype=slice_dtype, device=dev)
-    B_scales = torch.empty((B3.shape[0], num_splits, N), dtype=torch.float32, device=dev)
-    _split_into(B_T, num_splits, alpha, slice_dtype, B_slices_T, B_scales)
-    if mark:
-        mark("split_a")
-    A_slices = torch.empty((A3.shape[0], num_splits, M, K), dtype=slice_dtype, device=dev)
-    A_scales = torch.empty((A3.shape[0], num_splits, M), dtype=torch.float32, device=dev)
-    _split_into(A3, num_splits, alpha, slice_dtype, A_slices, A_scales)
-    B_slices = B_slices_T.transpose(-1, -2)
-
-    # 3. fused cross-GEMM
+    L = _lib.load()
+    xd = _TORCH_TO_OZK[input_dtype]
+    sd = _TORCH_TO_OZK[slice_dtype]
+    # a batch-1 operand of a batched product is broadcast (stride 0): split once
+    a_st = _lib.i64arr((A3.stride(0) if A3.shape[0] > 1 else 0, A3.stride(1), A3.stride(2)))
+    b_st = _lib.i64arr((B3.stride(0) if B3.shape[0] > 1 else 0, B3.stride(1), B3.stride(2)))
+    nbytes = ctypes.c_size_t(0)
+    st = L.ozk_matmul_workspace_bytes(xd, BN, M, N, K, a_st, b_st, num_splits, sd,
+                                      ctypes.byref(nbytes))
+    if st in (_lib.OZK_ERR_ALPHA, _lib.OZK_ERR_SHAPE):
+        # raise exactly what the reference's compute_split_bits raises
+        compute_split_bits(K, slice_dtype=slice_dtype, dot_accum_dtype=dot_accum_dtype)
+    _lib.check("ozk_matmul_workspace_bytes", st)
     C = torch.empty((BN, M, N), dtype=input_dtype, device=dev)
-    if mark:
-        mark("cross_gemm")
-    _cross_gemm_into(A_slices, B_slices, A_scales, B_scales, num_splits, C)
-    if mark:
-        mark("end")
+    ws, wsp = _workspace(int(nbytes.value), dev)
+    ev = None
+    if events is not None:
+        ev = (ctypes.c_void_p * 4)(*[ctypes.c_void_p(e.cuda_event) for e in events])
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev)
+        st = L.ozk_matmul(ctypes.c_void_p(A3.data_ptr()), a_st, ctypes.c_void_p(B3.data_ptr()),
+                          b_st, xd, BN, M, N, K, num_splits, sd, ctypes.c_void_p(C.data_ptr()),
+                          _lib.i64arr(C.stride()), wsp, nbytes.value, ev,
+                          ctypes.c_void_p(stream.cuda_stream))
+    _lib.check("ozk_matmul", st)
+    if ws is not None:
+        ws.record_stream(stream)
     return C.view(out_shape)

@@ -249,3 +249,48 @@ def test_canonicalize_batch_broadcasts_like_matmul():
     Bt = torch.zeros(32, 64, dtype=torch.float64).T
     _, B3, _ = ozk._canonicalize_batch(torch.zeros(4, 64, dtype=torch.float64), Bt)
     assert B3.data_ptr() == Bt.data_ptr()
+
+
+def test_matmul_abi_layout_and_errors():
+    """ozk_matmul (the whole ozaki_matmul below its Python checks): workspace
+    layout = 256-byte aligned [A slices][A scales][B slices][B scales][split
+    scratch][pack]; errors come back before anything is enqueued."""
+    from ozaki_triton_amd import _lib
+    L = _lib.load()
+    nb = ctypes.c_size_t(0)
+    M = N = K = 8192
+    a = _lib.i64arr([M * K, K, 1])
+    b = _lib.i64arr([K * N, N, 1])
+    assert L.ozk_matmul_workspace_bytes(_lib.OZK_F64, 1, M, N, K, a, b, 4, _lib.OZK_I8,
+                                        ctypes.byref(nb)) == 0
+    assert nb.value == 2 * (4 * M * K + 4 * M * 4)          # resident paths: no scratch
+    # broadcast B over a batch of 16 (stride 0): B is split once
+    Mb, Kb, Nb = 1024, 2048, 1024
+    a16 = _lib.i64arr([Mb * Kb, Kb, 1])
+    b0 = _lib.i64arr([0, Nb, 1])
+    assert L.ozk_matmul_workspace_bytes(_lib.OZK_F64, 16, Mb, Nb, Kb, a16, b0, 3, _lib.OZK_F16,
+                                        ctypes.byref(nb)) == 0
+    assert nb.value == 16 * 3 * Mb * Kb * 2 + 16 * 3 * Mb * 4 + 3 * Nb * Kb * 2 + 3 * Nb * 4
+    # errors: alpha < 1, K = 0 (log2(0)), too many splits, bad dtype
+    assert L.ozk_matmul_workspace_bytes(_lib.OZK_F32, 1, 4, 4, 1 << 30, a, b, 2, _lib.OZK_F16,
+                                        ctypes.byref(nb)) == _lib.OZK_ERR_ALPHA
+    assert L.ozk_matmul_workspace_bytes(_lib.OZK_F32, 1, 4, 4, 0, a, b, 2, _lib.OZK_F16,
+                                        ctypes.byref(nb)) == _lib.OZK_ERR_SHAPE
+    assert L.ozk_matmul_workspace_bytes(_lib.OZK_F32, 1, 4, 4, 8, a, b, 5, _lib.OZK_F16,
+                                        ctypes.byref(nb)) == _lib.OZK_ERR_SPLITS
+    assert L.ozk_matmul_workspace_bytes(_lib.OZK_I32, 1, 4, 4, 8, a, b, 2, _lib.OZK_F16,
+                                        ctypes.byref(nb)) == _lib.OZK_ERR_DTYPE
+    p = ctypes.c_void_p(0x1000)
+    null = ctypes.c_void_p(0)
+    c = _lib.i64arr([M * N, N, 1])
+
+    def call(ws, wsb):
+        return L.ozk_matmul(p, a, p, b, _lib.OZK_F64, 1, M, N, K, 4, _lib.OZK_I8, p, c, ws, wsb,
+                            None, null)
+    need = 2 * (4 * M * K + 4 * M * 4)
+    assert call(null, 0) == _lib.OZK_ERR_WORKSPACE
+    assert call(ctypes.c_void_p(0x10000), need - 1) == _lib.OZK_ERR_WORKSPACE
+    assert call(ctypes.c_void_p(0x10010), need) == _lib.OZK_ERR_WORKSPACE   # not 256-aligned
+    # nothing to do: OK without a device call
+    assert L.ozk_matmul(p, a, p, b, _lib.OZK_F64, 0, M, N, K, 4, _lib.OZK_I8, p, c, null, 0,
+                        None, null) == _lib.OZK_OK

@@ -370,3 +370,35 @@ def test_ozaki_matmul_narrow_inputs(oracle, gpu, xdt, sdt):
             ulp = 2.0 ** -10 if xdt == torch.float16 else 2.0 ** -7
             slack = ulp * np.abs(wv) + 2.0 ** -24
         assert np.all(np.abs(gv - wv) <= bound + slack), f"{xdt} {sdt} batch {b}"
+
+
+def test_matmul_c_abi_with_caller_workspace_and_events(oracle, gpu):
+    """ozk_matmul called directly through the C ABI with a caller workspace
+    (no allocation inside) equals the oracle bit for bit, and records the four
+    phase events on the stream."""
+    import ctypes
+    from ozaki_triton_amd import _lib
+    A, B = c3_like((96, 520), (520, 72), seed=41)
+    Ad, Bd = A.to(gpu), B.to(gpu)
+    L = _lib.load()
+    nb = ctypes.c_size_t(0)
+    a = _lib.i64arr([0, 520, 1])
+    b = _lib.i64arr([0, 72, 1])
+    assert L.ozk_matmul_workspace_bytes(_lib.OZK_F64, 1, 96, 72, 520, a, b, 3, _lib.OZK_I8,
+                                        ctypes.byref(nb)) == 0
+    ws = torch.empty(nb.value, dtype=torch.uint8, device=gpu)
+    C = torch.empty(96, 72, dtype=torch.float64, device=gpu)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    for e in evs:
+        e.record()
+    arr = (ctypes.c_void_p * 4)(*[ctypes.c_void_p(e.cuda_event) for e in evs])
+    st = L.ozk_matmul(ctypes.c_void_p(Ad.data_ptr()), a, ctypes.c_void_p(Bd.data_ptr()), b,
+                      _lib.OZK_F64, 1, 96, 72, 520, 3, _lib.OZK_I8, ctypes.c_void_p(C.data_ptr()),
+                      _lib.i64arr([96 * 72, 72, 1]), ctypes.c_void_p(ws.data_ptr()), nb.value,
+                      arr, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert st == 0, _lib.strerror(st)
+    torch.cuda.synchronize()
+    want = oracle.ozaki_matmul(to_np(A), to_np(B), 3, "int8")
+    assert_bitwise_equal(to_np(C), want, "ozk_matmul")
+    phases = [evs[i].elapsed_time(evs[i + 1]) for i in range(3)]
+    assert all(t >= 0 for t in phases) and sum(phases) > 0
