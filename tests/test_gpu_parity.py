@@ -402,3 +402,37 @@ def test_matmul_c_abi_with_caller_workspace_and_events(oracle, gpu):
     assert_bitwise_equal(to_np(C), want, "ozk_matmul")
     phases = [evs[i].elapsed_time(evs[i + 1]) for i in range(3)]
     assert all(t >= 0 for t in phases) and sum(phases) > 0
+
+
+@pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
+def test_ozaki_matmul_graph_capture(gpu, sdt):
+    """ozaki_matmul captured in a HIP graph (torch.cuda.graph): every replay,
+    with eager work and synchronisations between replays and the inputs
+    changed in place, equals the eager result bit for bit."""
+    import ozaki_triton_amd as ozk
+    A, B = c3_like((2, 128, 256), (256, 96), seed=53)
+    Ad, Bd = A.to(gpu), B.to(gpu)
+    L = 3
+    ozk.ozaki_matmul(Ad, Bd, L, sdt)          # warm up outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            C_graph = ozk.ozaki_matmul(Ad, Bd, L, sdt)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    gen = torch.Generator().manual_seed(7)
+    for rep in range(4):
+        if rep:
+            Ad.copy_((A * (1 + rep)).to(gpu))
+            Bd.copy_(torch.roll(B, rep, 0).to(gpu))
+        junk = torch.randn(1000, 1000, generator=gen).to(gpu) @ torch.randn(1000, 1000).to(gpu)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        eager = ozk.ozaki_matmul(Ad, Bd, L, sdt)
+        torch.cuda.synchronize()
+        assert_bitwise_equal(to_np(C_graph), to_np(eager), f"replay {rep}")
+        del junk
