@@ -45,7 +45,8 @@ enum {
     OZK_OK = 0,
     OZK_ERR_NULL = -1,        /* a required pointer is NULL */
     OZK_ERR_DTYPE = -2,       /* dtype combination not supported */
-    OZK_ERR_SPLITS = -3,      /* num_splits outside [0, OZK_MAX_SPLITS] */
+    OZK_ERR_SPLITS = -3,      /* num_splits outside [0, OZK_MAX_SPLITS], or > 4 with a
+                                 cross-GEMM that cannot take it */
     OZK_ERR_SHAPE = -4,       /* negative size, or K mismatch */
     OZK_ERR_ALPHA = -5,       /* alpha < 1 (K too large for the accumulator) */
     OZK_ERR_WORKSPACE = -6,   /* workspace missing, too small or not 16-byte aligned */
@@ -53,7 +54,11 @@ enum {
     OZK_ERR_ACCUM = -8        /* unsupported dot accumulator dtype */
 };
 
-#define OZK_MAX_SPLITS 4
+/* The reference's ozaki_matmul asserts num_splits <= 4 (ozaki_triton.py:563),
+ * a limit of its kernel's hard-coded accumulators.  The calls here take up to
+ * 8 slices; with more than 4, the cross-GEMM needs int8 / fp16 / bf16 slices
+ * and an fp64 C (OZK_ERR_SPLITS otherwise). */
+#define OZK_MAX_SPLITS 8
 
 /* Name of a status code (static string). */
 const char *ozk_strerror(int status);

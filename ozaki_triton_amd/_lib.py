@@ -22,7 +22,7 @@ OZK_ERR_ALPHA = -5
 OZK_ERR_WORKSPACE = -6
 OZK_ERR_LAUNCH = -7
 OZK_ERR_ACCUM = -8
-OZK_MAX_SPLITS = 4
+OZK_MAX_SPLITS = 8
 
 # every symbol include/ozaki_amd.h declares
 EXPORTED = (

@@ -241,6 +241,12 @@ static int cross_gemm_impl(const void *A_slices, const int64_t a_strides[4], con
         p.bs_n = b_strides[3];
     }
     const ozk::GemmPlan plan = ozk::plan_gemm(p, num_splits, slice_dtype);
+    // more than 4 slices: int8 / fp16 / bf16 slices into an fp64 C (the
+    // partial sum stays in C between the i-row launches), operands within the
+    // 31-bit offsets of the LDS-DMA kernel
+    if (num_splits > 4 && (out_dtype != OZK_F64 || slice_dtype == OZK_F32 ||
+                           plan.kind != ozk::kGemmPair))
+        return OZK_ERR_SPLITS;
     return hip_status(ozk::launch_gemm(p, plan, num_splits, slice_dtype, st));
 }
 
@@ -282,6 +288,8 @@ int matmul_layout(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
                   const int64_t as[3], const int64_t bs[3], int L, int sd, MatmulLayout *o) {
     if (!is_input_dtype(dtype) || !is_slice_dtype(sd)) return OZK_ERR_DTYPE;
     if (L < 0 || L > OZK_MAX_SPLITS) return OZK_ERR_SPLITS;
+    // more than 4 slices: the cross-GEMM takes them into an fp64 C only
+    if (L > 4 && (dtype != OZK_F64 || sd == OZK_F32)) return OZK_ERR_SPLITS;
     if (batch < 0 || M < 0 || N < 0 || K < 0) return OZK_ERR_SHAPE;
     o->alpha = 0;
     if (L > 0) {

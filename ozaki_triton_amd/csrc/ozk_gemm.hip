@@ -94,6 +94,9 @@ template <> struct Mfma<float> {
 // fp32, rounded to nearest even for fp16 / bf16, or truncated toward zero and
 // saturated for int8 (NVIDIA's float-to-integer conversion; NaN -> 0).
 OZK_DEV void store_c(const GemmParams &p, int64_t idx, double v) { ((double *)p.C)[idx] = v; }
+// partial of an earlier launch (num_splits > 4 runs with an fp64 or fp32 C)
+OZK_DEV double load_c(const GemmParams &p, int64_t idx, double) { return ((const double *)p.C)[idx]; }
+OZK_DEV float load_c(const GemmParams &p, int64_t idx, float) { return ((const float *)p.C)[idx]; }
 OZK_DEV void store_c(const GemmParams &p, int64_t idx, float v) {
     switch (p.out_dtype) {
     case 1: ((float *)p.C)[idx] = v; break;
@@ -578,8 +581,12 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_dma_kernel(GemmParams p, in
 // group 0 sums its pairs from +0 and hands the partial to group 1 through
 // LDS; group 1 adds its pairs, in order, and stores C.
 // ---------------------------------------------------------------------------
-template <int L> struct PairSplit {
-    static constexpr int P = L * L;
+// The kernel covers the pairs of R consecutive i-rows [i0, i0 + R) of the
+// order (R = L: all of them).  num_splits > 4 runs as several such launches in
+// i-major order, each continuing the sum from C, which holds the partial in
+// the fp64 outer accumulator between launches.
+template <int L, int R> struct PairSplit {
+    static constexpr int P = R * L;
     static constexpr int P0 = (P + 1) / 2;
     static constexpr int first(int g) { return g ? P0 : 0; }
     static constexpr int count(int g) { return g ? P - P0 : P0; }
@@ -587,22 +594,24 @@ template <int L> struct PairSplit {
     static constexpr int na(int g) { return (first(g) + count(g) - 1) / L - ilo(g) + 1; }
 };
 
-template <int L> struct PairShape {
+template <int L, int R> struct PairShape {
     static constexpr int BM = 64, BN = 64;
-    static constexpr int A_ROWS = L * BM;
-    static constexpr int ROWS = L * (BM + BN);
+    static constexpr int A_ROWS = R * BM;
+    static constexpr int ROWS = (R + L) * BM;
     static constexpr int STAGE = ROWS * kDmaRB;
     static constexpr int LPS = STAGE / (8 * 1024);   // DMA instructions per wave per stage
     static constexpr int LDS_BYTES = kDmaStages * STAGE;
     static_assert(STAGE % 8192 == 0, "stage must be a whole number of 1 KB windows per wave");
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS");
 };
 
-template <typename ST, int L, typename AccT>
+template <typename ST, int L, typename AccT, int R>
 __global__ __launch_bounds__(512, 1) void cross_gemm_pair_kernel(GemmParams p, int group_m,
                                                                  uint32_t a_records,
-                                                                 uint32_t b_records) {
-    using Sh = PairShape<L>;
-    using PS = PairSplit<L>;
+                                                                 uint32_t b_records, int i0,
+                                                                 int cont) {
+    using Sh = PairShape<L, R>;
+    using PS = PairSplit<L, R>;
     using MF = Mfma<ST>;
     using Acc = typename MF::Acc;
     using OA = AccT;   // outer accumulator: fp64 for fp64 output, else fp32 (store_c)
@@ -653,7 +662,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_pair_kernel(GemmParams p, i
         const int pc = pos % CH;
         chunk[q] = (kDmaRB == 64) ? (pc ^ ((r >> 2) & 3)) : (pc ^ ((r >> 1) & 7));
         if (r < Sh::A_ROWS) {
-            const int i = r / BM;
+            const int i = i0 + r / BM;
             const int64_t m = m0 + r % BM;
             src[q] = (m < p.M) ? (uint32_t)(((int64_t)i * p.as_l + m * p.as_m) * ES) : kOOB;
         } else {
@@ -780,7 +789,8 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_pair_kernel(GemmParams p, i
             const bool ok = cok && row < p.M;
             float sai[NA];
 #pragma unroll
-            for (int i = 0; i < NA; ++i) sai[i] = ok ? sab[(ILO + i) * p.sas_l + row * p.sas_m] : 0.0f;
+            for (int i = 0; i < NA; ++i)
+                sai[i] = ok ? sab[(int64_t)(i0 + ILO + i) * p.sas_l + row * p.sas_m] : 0.0f;
 #pragma unroll
             for (int q = 0; q < NP; ++q) {
                 const int i = (F + q) / L, j = (F + q) % L;
@@ -792,7 +802,12 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_pair_kernel(GemmParams p, i
         if constexpr (G == 0) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
+                // from +0, or from the partial an earlier launch left in C
                 OA out = (OA)0;
+                if (cont) {
+                    const int64_t row = m0 + wm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (cok && row < p.M) out = load_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
+                }
 #pragma unroll
                 for (int q = 0; q < NP; ++q) out = out + (OA)tv[q][r];
                 part[(blk * 16 + r) * 64 + lane] = out;
@@ -1121,6 +1136,7 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype) {
     const bool fits = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es) >= 0 &&
                       dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es) >= 0;
     plan.kind = fits ? (L >= 3 ? kGemmPair : kGemmDMA) : kGemmStaged;
+    if (L > 4) return plan;   // only the pair-split kernel, launched per i-row range
     const char *forced = getenv("OZK_GEMM_KERNEL");
     if (forced && forced[0] == 's') plan.kind = kGemmStaged;
     else if (forced && forced[0] == 'a' && fits) plan.kind = kGemmAD;
@@ -1182,10 +1198,11 @@ static hipError_t launch_ad(const GemmParams &p, const GemmPlan &plan, hipStream
     return hipGetLastError();
 }
 
-template <typename ST, int L, typename AccT>
-static hipError_t launch_pair(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
-    using Sh = PairShape<L>;
-    auto kern = cross_gemm_pair_kernel<ST, L, AccT>;
+template <typename ST, int L, typename AccT, int R>
+static hipError_t launch_pair(const GemmParams &p, const GemmPlan &plan, hipStream_t st, int i0,
+                              int cont) {
+    using Sh = PairShape<L, R>;
+    auto kern = cross_gemm_pair_kernel<ST, L, AccT, R>;
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void *)kern,
@@ -1200,14 +1217,33 @@ static hipError_t launch_pair(const GemmParams &p, const GemmPlan &plan, hipStre
     const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
     if (tiles == 0) return hipSuccess;
     hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(512), Sh::LDS_BYTES, st, p,
-                       plan.group_m, (uint32_t)ea, (uint32_t)eb);
+                       plan.group_m, (uint32_t)ea, (uint32_t)eb, i0, cont);
     return hipGetLastError();
+}
+
+// num_splits = 5..8: launches over consecutive i-rows (at most 16 pairs each,
+// so a wave group still holds 8 pairs), in i-major order, each continuing the
+// fp64 sum from C.  int8 / fp16 / bf16 slices with an fp64 outer accumulator.
+template <typename ST, int L, typename AccT>
+static hipError_t launch_chunks(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
+    if constexpr (!std::is_same<AccT, double>::value || std::is_same<ST, float>::value) {
+        return hipErrorInvalidValue;
+    } else {
+        constexpr int R = (L == 5) ? 3 : 2;   // rows per launch (16 / L, at least 2)
+        hipError_t e = hipSuccess;
+        for (int i0 = 0; i0 < L && e == hipSuccess; i0 += R) {
+            const int cont = i0 > 0;
+            if (L - i0 >= R) e = launch_pair<ST, L, AccT, R>(p, plan, st, i0, cont);
+            else if constexpr (L % R != 0) e = launch_pair<ST, L, AccT, L % R>(p, plan, st, i0, cont);
+        }
+        return e;
+    }
 }
 
 template <typename ST, int L, int MI, int NI, typename AccT>
 static hipError_t launch_one(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     if constexpr (L >= 3) {
-        if (plan.kind == kGemmPair) return launch_pair<ST, L, AccT>(p, plan, st);
+        if (plan.kind == kGemmPair) return launch_pair<ST, L, AccT, L>(p, plan, st, 0, 0);
     }
     if (plan.kind == kGemmAD) {
         constexpr int ANI = (L == 1) ? 8 : (L == 2) ? 4 : 1;
@@ -1247,8 +1283,10 @@ static hipError_t launch_L(const GemmParams &p, const GemmPlan &plan, hipStream_
         case 12: return launch_one<ST, 2, 1, 2, AccT>(p, plan, st);
         case 11: return launch_one<ST, 2, 1, 1, AccT>(p, plan, st);
         }
-    } else {
+    } else if constexpr (L <= 4) {
         if (key == 11) return launch_one<ST, L, 1, 1, AccT>(p, plan, st);
+    } else {
+        return launch_chunks<ST, L, AccT>(p, plan, st);
     }
     return hipErrorInvalidValue;
 }
@@ -1260,6 +1298,10 @@ static hipError_t launch_st(const GemmParams &p, const GemmPlan &plan, int L, hi
     case 2: return launch_L<ST, 2, AccT>(p, plan, st);
     case 3: return launch_L<ST, 3, AccT>(p, plan, st);
     case 4: return launch_L<ST, 4, AccT>(p, plan, st);
+    case 5: return launch_L<ST, 5, AccT>(p, plan, st);
+    case 6: return launch_L<ST, 6, AccT>(p, plan, st);
+    case 7: return launch_L<ST, 7, AccT>(p, plan, st);
+    case 8: return launch_L<ST, 8, AccT>(p, plan, st);
     }
     return hipErrorInvalidValue;
 }

@@ -71,7 +71,7 @@ def test_split_abi_rejects_bad_arguments_on_host():
 
     assert call(xd=_lib.OZK_I32) == _lib.OZK_ERR_DTYPE     # not an input dtype
     assert call(sd=_lib.OZK_F64) == _lib.OZK_ERR_DTYPE     # not a slice dtype
-    assert call(L=5) == _lib.OZK_ERR_SPLITS
+    assert call(L=9) == _lib.OZK_ERR_SPLITS                # up to 8 slices
     assert call(L=-1) == _lib.OZK_ERR_SPLITS
     assert call(K=-1) == _lib.OZK_ERR_SHAPE
     assert call(alpha=0) == _lib.OZK_ERR_ALPHA
@@ -169,7 +169,10 @@ def test_cross_gemm_abi_checks_and_workspace():
 
     assert call(sd=_lib.OZK_F64) == _lib.OZK_ERR_DTYPE
     assert call(od=_lib.OZK_I32) == _lib.OZK_ERR_DTYPE
-    assert call(L=5) == _lib.OZK_ERR_SPLITS
+    assert call(L=9) == _lib.OZK_ERR_SPLITS
+    # more than 4 slices: only int8 / fp16 / bf16 slices into an fp64 C
+    assert call(L=5, od=_lib.OZK_F32) == _lib.OZK_ERR_SPLITS
+    assert call(L=5, sd=_lib.OZK_F32) == _lib.OZK_ERR_SPLITS
     assert call(K=-3) == _lib.OZK_ERR_SHAPE
     assert call(C=null) == _lib.OZK_ERR_NULL
     assert call(b=b_ncontig) == _lib.OZK_ERR_WORKSPACE
@@ -276,8 +279,15 @@ def test_matmul_abi_layout_and_errors():
                                         ctypes.byref(nb)) == _lib.OZK_ERR_ALPHA
     assert L.ozk_matmul_workspace_bytes(_lib.OZK_F32, 1, 4, 4, 0, a, b, 2, _lib.OZK_F16,
                                         ctypes.byref(nb)) == _lib.OZK_ERR_SHAPE
+    assert L.ozk_matmul_workspace_bytes(_lib.OZK_F64, 1, 4, 4, 8, a, b, 9, _lib.OZK_F16,
+                                        ctypes.byref(nb)) == _lib.OZK_ERR_SPLITS
+    # 5..8 slices: fp64 in and out, int8 / fp16 / bf16 slices
     assert L.ozk_matmul_workspace_bytes(_lib.OZK_F32, 1, 4, 4, 8, a, b, 5, _lib.OZK_F16,
                                         ctypes.byref(nb)) == _lib.OZK_ERR_SPLITS
+    assert L.ozk_matmul_workspace_bytes(_lib.OZK_F64, 1, 4, 4, 8, a, b, 6, _lib.OZK_F32,
+                                        ctypes.byref(nb)) == _lib.OZK_ERR_SPLITS
+    assert L.ozk_matmul_workspace_bytes(_lib.OZK_F64, 1, 4, 4, 8, a, b, 6, _lib.OZK_I8,
+                                        ctypes.byref(nb)) == _lib.OZK_OK
     assert L.ozk_matmul_workspace_bytes(_lib.OZK_I32, 1, 4, 4, 8, a, b, 2, _lib.OZK_F16,
                                         ctypes.byref(nb)) == _lib.OZK_ERR_DTYPE
     p = ctypes.c_void_p(0x1000)

@@ -436,3 +436,74 @@ def test_ozaki_matmul_graph_capture(gpu, sdt):
         torch.cuda.synchronize()
         assert_bitwise_equal(to_np(C_graph), to_np(eager), f"replay {rep}")
         del junk
+
+
+# --------------------------------------------------------------------------- #
+# more than 4 slices: split_matrix and cross_gemm take up to 8 (the reference
+# caps only ozaki_matmul, ozaki_triton.py:563); the cross-GEMM runs over i-row
+# ranges that continue the fp64 sum from C
+# --------------------------------------------------------------------------- #
+@pytest.mark.parametrize("L", [5, 6, 7, 8])
+@pytest.mark.parametrize("M,N,K", [(64, 64, 128), (100, 72, 1040)])
+def test_cross_gemm_more_splits_int8_bitexact(oracle, gpu, L, M, N, K):
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(L * 100 + M)
+    As, BsT, sa, sb = _random_slices(g, 2, L, M, N, K, torch.int8)
+    C = ozk.cross_gemm(As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), L,
+                       torch.float64)
+    torch.cuda.synchronize()
+    for b in range(2):
+        want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[b]), to_np(sa[b]), to_np(sb[b]),
+                                 "float64")
+        assert_bitwise_equal(to_np(C)[b], want, f"L{L} {M}x{N}x{K} b{b}")
+
+
+@pytest.mark.parametrize("sdt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("L", [5, 6])
+def test_cross_gemm_more_splits_float_within_bound(oracle, gpu, sdt, L):
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(L + 17)
+    M, N, K = 100, 72, 1040
+    As = (torch.rand(1, L, M, K, generator=g) * 2 - 1).mul(64).to(sdt)
+    BsT = (torch.rand(1, L, N, K, generator=g) * 2 - 1).mul(64).to(sdt)
+    sa = torch.pow(2.0, torch.randint(-20, 5, (1, L, M), generator=g).float())
+    sb = torch.pow(2.0, torch.randint(-20, 5, (1, L, N), generator=g).float())
+    C = ozk.cross_gemm(As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), L,
+                       torch.float64)
+    torch.cuda.synchronize()
+    a, bT, s_a, s_b = to_np(As[0]), to_np(BsT[0]), to_np(sa[0]), to_np(sb[0])
+    want = oracle.cross_gemm(a, bT, s_a, s_b, "float64")
+    bound = fp16_cross_bound(oracle, a, bT, s_a, s_b)
+    err = np.abs(to_np(C)[0] - want)
+    assert np.all(err <= bound), float((err / np.maximum(bound, 1e-300)).max())
+
+
+def test_six_splits_end_to_end(oracle, gpu):
+    """fp64 -> int8 with 6 slices composed from split_matrix and cross_gemm
+    (as ozaki_matmul would do it): bit-exact against the oracle, and at least
+    as accurate as 4 slices (the fp32 residual buffer bounds the gain)."""
+    import ozaki_triton_amd as ozk
+    A, B = c3_like((96, 1024), (1024, 80), seed=61)
+    Ad, Bd = A.to(gpu), B.to(gpu)
+    K = 1024
+    alpha = ozk.compute_split_bits(K, torch.int8, torch.int32)
+    rel = {}
+    for L in (4, 6):
+        a_sl, a_sc = ozk.split_matrix(Ad.unsqueeze(0), L, alpha, torch.int8)
+        bt_sl, b_sc = ozk.split_matrix(Bd.t().unsqueeze(0), L, alpha, torch.int8)
+        C = ozk.cross_gemm(a_sl, bt_sl.transpose(-1, -2), a_sc, b_sc, L, torch.float64)[0]
+        torch.cuda.synchronize()
+        want = oracle.ozaki_matmul(to_np(A), to_np(B), L, "int8")
+        assert_bitwise_equal(to_np(C), want, f"L{L}")
+        ref = A @ B
+        rel[L] = float((C.cpu() - ref).norm() / ref.norm())
+    assert rel[6] <= rel[4]
+
+
+def test_more_splits_unsupported_combination_raises(gpu):
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(3)
+    As, BsT, sa, sb = _random_slices(g, 1, 5, 64, 64, 128, torch.int8)
+    with pytest.raises(ozk._lib.OzakiLibError):
+        ozk.cross_gemm(As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), 5,
+                       torch.float32)
