@@ -23,6 +23,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -104,18 +105,22 @@ def cpu_torch_matmul(A_cpu, B_cpu, reps):
     return flops / t / 1e12, ncores, torch.get_num_threads()
 
 
-def measured_traffic(config: str, kernel_prefix: str):
+def measured_traffic(config: str, kernel: str):
     """HBM-side bytes per launch of a kernel, from the rocprofv3 FETCH_SIZE /
     WRITE_SIZE passes summarised in profiles/ (scaled by the copy-kernel
-    calibration recorded there), or None when that config was not measured."""
+    calibration recorded there), or None when that config was not measured.
+    Profiled names are demangled ("ozk::cross_gemm_ring_kernel<...>") or, for
+    some template arguments, mangled ("_ZN3ozk22cross_gemm_ring_kernel..."):
+    the kernel's base name is matched as a whole identifier in either."""
     path = os.path.join(ROOT, "profiles", "cross_gemm_traffic.json")
     try:
         with open(path) as f:
             data = json.load(f)
     except (OSError, ValueError):
         return None
+    pat = re.compile(r"(ozk::|ozk\d+)" + re.escape(kernel) + r"(<|I)")
     for name, rec in data.get("configs", {}).get(config, {}).items():
-        if name.startswith(kernel_prefix):
+        if pat.search(name):
             return int(rec["traffic_bytes"])
     return None
 
@@ -266,8 +271,10 @@ def main():
         peak, unit_c = PEAK_FP16_TFLOPS, "TFLOP/s"
     achieved = cross_ops / (t_cross * 1e-3) / 1e12
     # the library's default kernel choice (plan_gemm in ozk_gemm.hip): the
-    # pair-split kernel for L >= 3, the 2 x 2 LDS-DMA kernel otherwise
-    gemm_kernel = "cross_gemm_pair_kernel" if L >= 3 else "cross_gemm_dma_kernel"
+    # five-slot ring kernel for L = 3, 4, the pair-split kernel for L > 4, the
+    # 2 x 2 LDS-DMA kernel for L <= 2
+    gemm_kernel = ("cross_gemm_dma_kernel" if L <= 2 else
+                   "cross_gemm_ring_kernel" if L <= 4 else "cross_gemm_pair_kernel")
     # split: read the unique inputs, write the unique slices and scales
     xsz = 8 if xdt == "float64" else 4
     ssz = 1 if sdt == "int8" else 2
@@ -311,7 +318,7 @@ def main():
             "peak": peak,
             "unit": unit_c,
             "frac": round(achieved / peak, 4),
-            "traffic": measured_traffic(args.config, "ozk::" + gemm_kernel),
+            "traffic": measured_traffic(args.config, gemm_kernel),
             "avg_ms": round(t_cross, 4),
         },
         "split": {

@@ -27,6 +27,7 @@
 //   * Workgroups are remapped so each XCD (own L2) processes a contiguous
 //     range of tiles, grouped GROUP_M tile-rows at a time.
 #include <stdlib.h>
+#include <string.h>
 
 #include <type_traits>
 
@@ -672,16 +673,17 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_pair_kernel(GemmParams p, i
             src[q] = (n < p.N) ? (uint32_t)(((int64_t)j * p.bs_l + n * p.bs_n) * ES) : kOOB;
         }
     }
-    auto issue_stage = [&](int kb) {
+    auto issue_one = [&](int kb, int q) {
         char *dst = smem + (kb % kDmaStages) * Sh::STAGE + wave * Sh::LPS * 1024;
+        const uint32_t kofs = (uint32_t)kb * kDmaRB + chunk[q] * 16;
+        const uint32_t vo = (src[q] == kOOB || kofs >= kbytes) ? kOOB : src[q] + kofs;
+        auto *ldsp = (__attribute__((address_space(3))) void *)(dst + q * 1024);
+        const bool isA = (wave * Sh::LPS + q) * (1024 / kDmaRB) < Sh::A_ROWS;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(isA ? rA : rB, ldsp, 16, vo, 0, 0, 0);
+    };
+    auto issue_stage = [&](int kb) {
 #pragma unroll
-        for (int q = 0; q < Sh::LPS; ++q) {
-            const uint32_t kofs = (uint32_t)kb * kDmaRB + chunk[q] * 16;
-            const uint32_t vo = (src[q] == kOOB || kofs >= kbytes) ? kOOB : src[q] + kofs;
-            auto *ldsp = (__attribute__((address_space(3))) void *)(dst + q * 1024);
-            const bool isA = (wave * Sh::LPS + q) * (1024 / kDmaRB) < Sh::A_ROWS;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(isA ? rA : rB, ldsp, 16, vo, 0, 0, 0);
-        }
+        for (int q = 0; q < Sh::LPS; ++q) issue_one(kb, q);
     };
     // stage kb has landed once at most the loads of the stages issued after
     // it are outstanding; the barrier then publishes every wave's DMA writes,
@@ -746,10 +748,24 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_pair_kernel(GemmParams p, i
             for (int q = NP; q < kReads; ++q) read_one(nbuf, nkk, q, nxt);
         };
 
+        // A stage's DMA is issued in three parts: the first right after its
+        // ring slot is released (stage_ready of the stage before it), the
+        // others before the first two K steps of that stage.  Issued at once,
+        // the 8 waves' instructions overfill the vector-memory queue and each
+        // wave stalls at issue for hundreds of cycles.
+        static_assert(kDmaStages == 2, "the DMA issue schedule assumes a ring of two stages");
+        constexpr int DP1 = (Sh::LPS + 2) / 3, DP2 = (2 * DP1 < Sh::LPS) ? 2 * DP1 : Sh::LPS;
+        auto issue_part = [&](int kb, int part) {
+            const int lo = part == 0 ? 0 : part == 1 ? DP1 : DP2;
+            const int hi = part == 0 ? DP1 : part == 1 ? DP2 : Sh::LPS;
+#pragma unroll
+            for (int q = 0; q < Sh::LPS; ++q)
+                if (q >= lo && q < hi) issue_one(kb, q);
+        };
         Frags f0, f1;
         if (nkb > 0) {
             stage_ready(0);
-            if (kDmaStages - 1 < nkb) issue_stage(kDmaStages - 1);
+            if (1 < nkb) issue_part(1, 0);
 #pragma unroll
             for (int q = 0; q < kReads; ++q) read_one(smem, 0, q, f0);
         }
@@ -757,12 +773,13 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_pair_kernel(GemmParams p, i
             const char *buf = smem + (kb % kDmaStages) * Sh::STAGE;
 #pragma unroll
             for (int kk = 0; kk + 1 < STEPS; ++kk) {
+                if (kk < 2 && kb + 1 < nkb) issue_part(kb + 1, kk + 1);
                 if (kk % 2 == 0) step(f0, f1, buf, kk + 1);
                 else step(f1, f0, buf, kk + 1);
             }
             if (kb + 1 < nkb) {
                 stage_ready(kb + 1);
-                if (kb + kDmaStages < nkb) issue_stage(kb + kDmaStages);
+                if (kb + 2 < nkb) issue_part(kb + 2, 0);
             }
             if ((STEPS - 1) % 2 == 0) step(f0, f1, smem + ((kb + 1) % kDmaStages) * Sh::STAGE, 0);
             else step(f1, f0, smem + ((kb + 1) % kDmaStages) * Sh::STAGE, 0);
@@ -773,11 +790,11 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_pair_kernel(GemmParams p, i
                 for (int j = 0; j < L; ++j) f0.b[j] = f1.b[j];
             }
         }
-
-        // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
         // every wave is past its last ring read before the ring holds partials
         __builtin_amdgcn_s_waitcnt(0xC07F);
         exec_barrier();
+
+        // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
         float sbv[L];
 #pragma unroll
         for (int j = 0; j < L; ++j) sbv[j] = cok ? sbb[j * p.sbs_l + col * p.sbs_n] : 0.0f;
@@ -808,6 +825,257 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_pair_kernel(GemmParams p, i
                     const int64_t row = m0 + wm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
                     if (cok && row < p.M) out = load_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
                 }
+#pragma unroll
+                for (int q = 0; q < NP; ++q) out = out + (OA)tv[q][r];
+                part[(blk * 16 + r) * 64 + lane] = out;
+            }
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            exec_barrier();
+        } else {
+            exec_barrier();
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = m0 + wm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                OA out = part[(blk * 16 + r) * 64 + lane];
+#pragma unroll
+                for (int q = 0; q < NP; ++q) out = out + (OA)tv[q][r];
+                if (cok && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
+            }
+        }
+    };
+    if (grp == 0) body(std::integral_constant<int, 0>{});
+    else body(std::integral_constant<int, 1>{});
+}
+
+// ---------------------------------------------------------------------------
+// Ring variant of the pair-split kernel, for num_splits 3 and 4 (all i-rows in
+// one launch).  Same 8 waves, wave blocks and pair split; what changes is how
+// operands reach the LDS.
+//   * The ring has five slots of half a stage: half stage 2kb holds the A
+//     rows and 2kb + 1 the B rows of stage kb (128 bytes of K), in slot
+//     h % 5.  A(kb + 2) reuses the slot of B(kb - 1), which is free from the
+//     start of stage kb, so it can be fetched two stages ahead; B(kb + 1)
+//     reuses the slot of A(kb - 1) and is fetched one stage ahead.
+//   * The DMA of stage kb's time window (B(kb + 1), then A(kb + 2)) is spread
+//     one instruction at a time between this wave's MFMAs.  The LDS-DMA path
+//     accepts about one 1 KB instruction per 13 cycles per CU; issued in
+//     bursts, the 8 waves' instructions fill the vector-memory queue and each
+//     wave stalls at issue for hundreds of cycles.
+//   * A K step issues all reads of the next step before its MFMAs: under
+//     load an LDS read takes several hundred cycles to return.
+// Per stage each wave issues LPH instructions of B(kb + 1) in K steps 0 and 1
+// and LPH of A(kb + 2) in steps 2 and 3 (the part in step 3 after the stage
+// barrier); the barrier before stage kb + 1 waits for everything but the
+// step-2 part of A(kb + 2).
+// ---------------------------------------------------------------------------
+template <int L> struct RingShape {
+    static constexpr int NW = 8;                       // waves
+    static constexpr int BM = 64, BN = 64;
+    static constexpr int SLOT = L * BM * kDmaRB;       // one half stage (A rows or B rows)
+    static constexpr int NSLOT = 5;
+    static constexpr int LPH = SLOT / (NW * 1024);     // DMA instructions per wave per half stage
+    static constexpr int LDS_BYTES = NSLOT * SLOT;
+    static constexpr int B0 = (LPH + 1) / 2;           // B(kb + 1) instructions in step 0
+    static constexpr int A2 = (LPH + 1) / 2;           // A(kb + 2) instructions in step 2
+    static_assert(SLOT % (NW * 1024) == 0, "a half stage must be whole 1 KB windows per wave");
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS");
+    static_assert(kDmaRB == 128, "the ring assumes 128-byte stage rows");
+};
+template <typename ST, int L, typename AccT>
+__global__ __launch_bounds__(512, 1) void cross_gemm_ring_kernel(GemmParams p, int group_m,
+                                                                 uint32_t a_records,
+                                                                 uint32_t b_records) {
+    using Sh = RingShape<L>;
+    using PS = PairSplit<L, L>;
+    using MF = Mfma<ST>;
+    using Acc = typename MF::Acc;
+    using OA = AccT;
+    constexpr int BM = Sh::BM, BN = Sh::BN;
+    constexpr int ES = (int)sizeof(ST);
+    constexpr uint32_t kOOB = 0x80000000u;
+    constexpr int LPH = Sh::LPH;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int blk = wave & 3, grp = wave >> 2;
+    const int wm = blk >> 1, wn = blk & 1;
+    const int h = lane >> 5, lr = lane & 31;
+
+    const int64_t tiles_m = (p.M + BM - 1) / BM;
+    const int64_t tiles_n = (p.N + BN - 1) / BN;
+    const int64_t tiles = tiles_m * tiles_n;
+    const int64_t g = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
+    const int64_t bidx = g / tiles;
+    const int64_t t = g % tiles;
+    const int64_t width = (int64_t)group_m * tiles_n;
+    const int64_t first_m = (t / width) * group_m;
+    const int64_t gsz = (tiles_m - first_m < group_m) ? (tiles_m - first_m) : group_m;
+    const int64_t tm = first_m + (t % width) % gsz;
+    const int64_t tn = (t % width) / gsz;
+    const int64_t m0 = tm * BM, n0 = tn * BN;
+
+    const uint32_t kbytes = (uint32_t)(p.K * ES);
+    const int nkb = (int)((kbytes + kDmaRB - 1) / kDmaRB);
+    constexpr int STEPS = kDmaRB / 32;
+
+    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const char *)p.A + bidx * p.as_b * ES), (short)0, (int)a_records, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const char *)p.B + bidx * p.bs_b * ES), (short)0, (int)b_records, 0x00020000);
+
+    // Per-lane source offsets of this wave's LPH instructions of an A half
+    // and of a B half (a 1 KB window is 8 whole 128-byte rows).
+    uint32_t srcA[LPH], srcB[LPH];
+    int chA[LPH], chB[LPH];
+#pragma unroll
+    for (int q = 0; q < LPH; ++q) {
+        const int pos = (wave * LPH + q) * 64 + lane;
+        const int r = pos / 8, pc = pos % 8;
+        const int c = pc ^ ((r >> 1) & 7);
+        chA[q] = chB[q] = c;
+        const int64_t m = m0 + r % BM, n = n0 + r % BN;
+        srcA[q] = (m < p.M) ? (uint32_t)(((int64_t)(r / BM) * p.as_l + m * p.as_m) * ES) : kOOB;
+        srcB[q] = (n < p.N) ? (uint32_t)(((int64_t)(r / BN) * p.bs_l + n * p.bs_n) * ES) : kOOB;
+    }
+    auto slot = [&](int hs) { return smem + (hs % Sh::NSLOT) * Sh::SLOT; };
+    auto issue_a = [&](int kb, int q) {
+        const uint32_t kofs = (uint32_t)kb * kDmaRB + chA[q] * 16;
+        const uint32_t vo = (srcA[q] == kOOB || kofs >= kbytes) ? kOOB : srcA[q] + kofs;
+        auto *ldsp = (__attribute__((address_space(3))) void *)(slot(2 * kb) + (wave * LPH + q) * 1024);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, ldsp, 16, vo, 0, 0, 0);
+    };
+    auto issue_b = [&](int kb, int q) {
+        const uint32_t kofs = (uint32_t)kb * kDmaRB + chB[q] * 16;
+        const uint32_t vo = (srcB[q] == kOOB || kofs >= kbytes) ? kOOB : srcB[q] + kofs;
+        auto *ldsp = (__attribute__((address_space(3))) void *)(slot(2 * kb + 1) + (wave * LPH + q) * 1024);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, ldsp, 16, vo, 0, 0, 0);
+    };
+
+    // prologue: stage 0 and A(1); stage 0 must land before the first reads
+#pragma unroll
+    for (int q = 0; q < LPH; ++q) issue_a(0, q);
+#pragma unroll
+    for (int q = 0; q < LPH; ++q) issue_b(0, q);
+    if (nkb > 1) {
+#pragma unroll
+        for (int q = 0; q < LPH; ++q) issue_a(1, q);
+        wait_vmcnt<LPH>();
+    } else {
+        wait_vmcnt<0>();
+    }
+    exec_barrier();
+
+    const float *sab = p.sa + bidx * p.sas_b;
+    const float *sbb = p.sb + bidx * p.sbs_b;
+    const int64_t cbase = bidx * p.cs_b;
+    OA *part = (OA *)smem;   // epilogue hand-off [4 blocks][16][64 lanes]
+    const int64_t col = n0 + wn * 32 + lr;
+    const bool cok = col < p.N;
+
+    auto body = [&](auto G_) {
+        constexpr int G = decltype(G_)::value;
+        constexpr int F = PS::first(G), NP = PS::count(G), ILO = PS::ilo(G), NA = PS::na(G);
+        constexpr int kReads = NA + L;
+        struct Frags {
+            i32x4 a[NA];
+            i32x4 b[L];
+        };
+        Acc acc[NP];
+#pragma unroll
+        for (int q = 0; q < NP; ++q) acc[q] = MF::zero();
+
+        auto read_one = [&](int kb, int kk, int r, Frags &f) {
+            const int ch = 2 * kk + h;
+            if (r < NA) {
+                f.a[r] = *(const i32x4 *)(slot(2 * kb) + rswz<kDmaRB>((ILO + r) * BM + wm * 32 + lr, ch));
+            } else {
+                const int j = r - NA;
+                f.b[j] = *(const i32x4 *)(slot(2 * kb + 1) + rswz<kDmaRB>(j * BN + wn * 32 + lr, ch));
+            }
+        };
+        // One K step: the reads of the next K step (stage rkb, step nkk) into
+        // `nxt`, issued first, then the MFMAs of `cur` with this step's DMA
+        // instructions [lo, hi) of half stage kind (0: none, 1: A, 2: B) of
+        // stage dkb spread between them.
+        auto step = [&](const Frags &cur, Frags &nxt, int rkb, int nkk, int kind, int dkb, int lo,
+                        int hi) {
+            const int cnt = hi - lo;
+#pragma unroll
+            for (int q = 0; q < kReads; ++q) read_one(rkb, nkk, q, nxt);
+#pragma unroll
+            for (int q = 0; q < NP; ++q) {
+                const int i = (F + q) / L, j = (F + q) % L;
+                acc[q] = MF::run(cur.a[i - ILO], cur.b[j], acc[q]);
+#pragma unroll
+                for (int d = 0; d < LPH; ++d) {
+                    // instruction lo + d goes after MFMA (d * NP) / cnt
+                    if (d < cnt && (d * NP) / cnt == q) {
+                        if (kind == 1) issue_a(dkb, lo + d);
+                        else if (kind == 2) issue_b(dkb, lo + d);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+
+        Frags f0, f1;
+        if (nkb > 0) {
+#pragma unroll
+            for (int q = 0; q < kReads; ++q) read_one(0, 0, q, f0);
+        }
+        static_assert(STEPS == 4, "four 32-byte K steps per stage");
+        for (int kb = 0; kb < nkb; ++kb) {
+            const bool nb = kb + 1 < nkb, na = kb + 2 < nkb;
+            step(f0, f1, kb, 1, nb ? 2 : 0, kb + 1, 0, Sh::B0);
+            step(f1, f0, kb, 2, nb ? 2 : 0, kb + 1, Sh::B0, LPH);
+            step(f0, f1, kb, 3, na ? 1 : 0, kb + 2, 0, Sh::A2);
+            if (nb) {
+                // stage kb + 1 has landed once only this wave's first part of
+                // A(kb + 2) may be outstanding; the barrier publishes every
+                // wave's DMA writes, and the lgkmcnt wait makes this wave's
+                // reads of stage kb complete before slots are refilled
+                if (na) wait_vmcnt<Sh::A2>();
+                else wait_vmcnt<0>();
+                __builtin_amdgcn_s_waitcnt(0xC07F);
+                exec_barrier();
+            }
+            // the last step reads stage kb + 1's step 0 (unused past the end)
+            step(f1, f0, kb + 1, 0, na ? 1 : 0, kb + 2, Sh::A2, LPH);
+        }
+
+        // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
+        // every wave is past its last ring read before the ring holds partials
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        exec_barrier();
+        float sbv[L];
+#pragma unroll
+        for (int j = 0; j < L; ++j) sbv[j] = cok ? sbb[j * p.sbs_l + col * p.sbs_n] : 0.0f;
+        auto row_sa = [&](int r, float *sai) {
+            const int64_t row = m0 + wm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            const bool ok = cok && row < p.M;
+#pragma unroll
+            for (int i = 0; i < NA; ++i) sai[i] = ok ? sab[(int64_t)(ILO + i) * p.sas_l + row * p.sas_m] : 0.0f;
+        };
+        // t value of pair q at row r: fl32(fl32(fl32(acc) * sa_i) * sb_j)
+        auto tval = [&](int q, int r, const float *sai) {
+            const int i = (F + q) / L, j = (F + q) % L;
+            const float t1 = MF::to_f32(acc[q][r]) * sai[i - ILO];
+            return t1 * sbv[j];
+        };
+        float tv[NP][16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            float sai[NA];
+            row_sa(r, sai);
+#pragma unroll
+            for (int q = 0; q < NP; ++q) tv[q][r] = tval(q, r, sai);
+        }
+        if constexpr (G == 0) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                OA out = (OA)0;
 #pragma unroll
                 for (int q = 0; q < NP; ++q) out = out + (OA)tv[q][r];
                 part[(blk * 16 + r) * 64 + lane] = out;
@@ -1128,20 +1396,23 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype) {
     plan.ni = ni;
     plan.group_m = 8;
     const int es = slice_dtype == 4 ? 1 : slice_dtype == 1 ? 4 : 2;
-    // OZK_GEMM_KERNEL=staged|dma|ad|pair forces a kernel (tests cover every
-    // one at small sizes).  By default, when both operands fit the 31-bit
-    // buffer offsets of the LDS-DMA kernels: the pair-split kernel for L >= 3
-    // (its wave tile is 32 x 32 anyway), the 2 x 2 LDS-DMA kernel with its
-    // larger wave tiles for L <= 2; else the VGPR-staged kernel.
+    // OZK_GEMM_KERNEL=staged|dma|ad|pair|ring forces a kernel (tests cover
+    // every one at small sizes).  By default, when both operands fit the
+    // 31-bit buffer offsets of the LDS-DMA kernels: the ring kernel for
+    // L = 3, 4 and the pair-split kernel for L > 4 (their wave tile is 32 x 32
+    // anyway), the 2 x 2 LDS-DMA kernel with its larger wave tiles for L <= 2;
+    // else the VGPR-staged kernel.
     const bool fits = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es) >= 0 &&
                       dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es) >= 0;
-    plan.kind = fits ? (L >= 3 ? kGemmPair : kGemmDMA) : kGemmStaged;
+    plan.kind = !fits ? kGemmStaged : L <= 2 ? kGemmDMA : L <= 4 ? kGemmRing : kGemmPair;
     if (L > 4) return plan;   // only the pair-split kernel, launched per i-row range
-    const char *forced = getenv("OZK_GEMM_KERNEL");
-    if (forced && forced[0] == 's') plan.kind = kGemmStaged;
-    else if (forced && forced[0] == 'a' && fits) plan.kind = kGemmAD;
-    else if (forced && forced[0] == 'd' && fits) plan.kind = kGemmDMA;
-    else if (forced && forced[0] == 'p' && fits) plan.kind = L >= 3 ? kGemmPair : kGemmDMA;
+    const char *env = getenv("OZK_GEMM_KERNEL");
+    auto forced = [&](const char *name) { return env && strcmp(env, name) == 0; };
+    if (forced("staged")) plan.kind = kGemmStaged;
+    else if (fits && forced("ad")) plan.kind = kGemmAD;
+    else if (fits && forced("dma")) plan.kind = kGemmDMA;
+    else if (fits && forced("pair")) plan.kind = L >= 3 ? kGemmPair : kGemmDMA;
+    else if (fits && forced("ring")) plan.kind = L >= 3 ? kGemmRing : kGemmDMA;
     if (plan.kind == kGemmAD) plan.group_m = 2;
     return plan;
 }
@@ -1221,6 +1492,28 @@ static hipError_t launch_pair(const GemmParams &p, const GemmPlan &plan, hipStre
     return hipGetLastError();
 }
 
+template <typename ST, int L, typename AccT>
+static hipError_t launch_ring(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
+    using Sh = RingShape<L>;
+    auto kern = cross_gemm_ring_kernel<ST, L, AccT>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void *)kern,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           Sh::LDS_BYTES);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const int es = (int)sizeof(ST);
+    const int64_t ea = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es);
+    const int64_t eb = dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es);
+    const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
+    if (tiles == 0) return hipSuccess;
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(512), Sh::LDS_BYTES, st, p,
+                       plan.group_m, (uint32_t)ea, (uint32_t)eb);
+    return hipGetLastError();
+}
+
 // num_splits = 5..8: launches over consecutive i-rows (at most 16 pairs each,
 // so a wave group still holds 8 pairs), in i-major order, each continuing the
 // fp64 sum from C.  int8 / fp16 / bf16 slices with an fp64 outer accumulator.
@@ -1244,6 +1537,9 @@ template <typename ST, int L, int MI, int NI, typename AccT>
 static hipError_t launch_one(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     if constexpr (L >= 3) {
         if (plan.kind == kGemmPair) return launch_pair<ST, L, AccT, L>(p, plan, st, 0, 0);
+        if constexpr (L <= 4) {
+            if (plan.kind == kGemmRing) return launch_ring<ST, L, AccT>(p, plan, st);
+        }
     }
     if (plan.kind == kGemmAD) {
         constexpr int ANI = (L == 1) ? 8 : (L == 2) ? 4 : 1;

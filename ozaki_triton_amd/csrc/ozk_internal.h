@@ -68,7 +68,9 @@ enum GemmKind {
     kGemmStaged = 0,  // global -> VGPR -> LDS, 2 x 2 waves (any operand extent)
     kGemmDMA = 1,     // LDS-DMA ring for A and B, 2 x 2 waves
     kGemmAD = 2,      // A streamed into VGPRs, B by LDS-DMA, 4 x 1 waves
-    kGemmPair = 3     // LDS-DMA ring, 8 waves: 2 x 2 blocks x 2 halves of the slice pairs
+    kGemmPair = 3,    // LDS-DMA ring, 8 waves: 2 x 2 blocks x 2 halves of the slice pairs
+    kGemmRing = 4     // the pair split over a five-slot ring of half stages, DMA spread
+                      // between the MFMAs (num_splits 3 and 4)
 };
 struct GemmPlan {
     int mi, ni;       // 2 x 2 kernels: wave tile = (32*mi) x (32*ni)

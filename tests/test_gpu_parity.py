@@ -239,13 +239,14 @@ def test_ozaki_matmul_degenerate_shapes(gpu):
                          torch.randn(0, 3, dtype=torch.float64, device=gpu), 2, torch.int8)
 
 
-@pytest.mark.parametrize("kernel", ["staged", "dma", "ad", "pair"])
+@pytest.mark.parametrize("kernel", ["staged", "dma", "ad", "pair", "ring"])
 @pytest.mark.parametrize("L", [1, 2, 3, 4])
 def test_cross_gemm_each_kernel_bitexact(oracle, gpu, L, kernel, monkeypatch):
     """Every cross-GEMM kernel, forced: the VGPR-staged one (taken when an
     operand's extent exceeds the 31-bit buffer offsets of the LDS-DMA kernels),
-    the 2 x 2 LDS-DMA kernel, the A-direct kernel and the pair-split kernel
-    (L >= 3; for L <= 2 the request falls back to the 2 x 2 kernel)."""
+    the 2 x 2 LDS-DMA kernel, the A-direct kernel, the pair-split kernel and
+    its five-slot ring form (L >= 3; for L <= 2 the request falls back to the
+    2 x 2 kernel)."""
     import ozaki_triton_amd as ozk
     monkeypatch.setenv("OZK_GEMM_KERNEL", kernel)
     g = torch.Generator().manual_seed(77 + L)
@@ -255,6 +256,32 @@ def test_cross_gemm_each_kernel_bitexact(oracle, gpu, L, kernel, monkeypatch):
     torch.cuda.synchronize()
     want = oracle.cross_gemm(to_np(As[0]), to_np(BsT[0]), to_np(sa[0]), to_np(sb[0]), "float64")
     assert_bitwise_equal(to_np(C)[0], want, f"{kernel} L{L}")
+
+
+@pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
+@pytest.mark.parametrize("L", [3, 4])
+@pytest.mark.parametrize("K", [16, 128, 200, 300, 520, 1040])
+def test_ring_kernel_stage_counts(oracle, gpu, L, K, sdt, monkeypatch):
+    """The five-slot ring kernel over 1 to 9 stages of 128 bytes of K (the
+    prologue fetches a stage and a half, the loop issues each stage's DMA
+    ahead over the K steps of the stages before): int8 bit-exact against the
+    oracle, fp16 bit-identical to the two-slot pair kernel, which runs the
+    same MFMAs per accumulator in the same order."""
+    kernel = "ring"
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(K * 10 + L)
+    As, BsT, sa, sb = _random_slices(g, 2, L, 130, 72, K, sdt)
+    args = (As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), L, torch.float64)
+    monkeypatch.setenv("OZK_GEMM_KERNEL", kernel)
+    C = to_np(ozk.cross_gemm(*args))
+    if sdt == torch.int8:
+        for b in range(2):
+            want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[b]), to_np(sa[b]), to_np(sb[b]),
+                                     "float64")
+            assert_bitwise_equal(C[b], want, f"{kernel} L{L} K{K} b{b}")
+    else:
+        monkeypatch.setenv("OZK_GEMM_KERNEL", "pair")
+        assert_bitwise_equal(C, to_np(ozk.cross_gemm(*args)), f"{kernel} vs pair fp16 L{L} K{K}")
 
 
 @pytest.mark.parametrize("xdt,sdt", COMBOS)
