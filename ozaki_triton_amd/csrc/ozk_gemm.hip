@@ -953,6 +953,34 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ring_kernel(GemmParams p, i
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, ldsp, 16, vo, 0, 0, 0);
     };
 
+    // The scales of the tile (L x 64 of A's rows, L x 64 of B's columns, 2 KB)
+    // are fetched into a free ring slot by one dword DMA instruction per wave
+    // at the start of the last stage, so the epilogue reads them from the LDS
+    // instead of waiting on global loads.  That slot is the one of A(nkb),
+    // which is never fetched, or, when it is slot 0, the one of B(nkb); the
+    // scales take its last 2 KB, past the epilogue's partial sums, which
+    // start at slot 0 and may run into slot 1 (32 KB of fp64 > a 24 KB slot).
+    static_assert(2 * Sh::SLOT - 2048 >= 4 * 16 * 64 * (int)sizeof(double),
+                  "scales clear of the partial sums");
+    char *const scl = slot((2 * nkb) % Sh::NSLOT != 0 ? 2 * nkb : 2 * nkb + 1) + Sh::SLOT - 2048;
+    auto issue_scales = [&]() {
+        const bool isa = wave < 4;
+        const int s = isa ? wave : wave - 4;           // slice
+        const int64_t rc = (isa ? m0 : n0) + lane;     // row of A / column of B
+        const int64_t ext = isa ? ((int64_t)(L - 1) * p.sas_l + (p.M - 1) * p.sas_m + 1)
+                                : ((int64_t)(L - 1) * p.sbs_l + (p.N - 1) * p.sbs_n + 1);
+        const bool ok = s < L && rc < (isa ? p.M : p.N);
+        const uint32_t vo = ok ? (uint32_t)(((int64_t)s * (isa ? p.sas_l : p.sbs_l) +
+                                             rc * (isa ? p.sas_m : p.sbs_n)) * 4)
+                               : kOOB;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(isa ? p.sa + bidx * p.sas_b : p.sb + bidx * p.sbs_b), (short)0,
+            (int)(ext * 4 < 0x7FFFFFFF ? ext * 4 : 0x7FFFFFFF), 0x00020000);
+        auto *ldsp = (__attribute__((address_space(3))) void *)(scl + (isa ? 0 : 1024) + s * 256);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, ldsp, 4, vo, 0, 0, 0);
+    };
+    const float *sa_lds = (const float *)scl, *sb_lds = (const float *)(scl + 1024);
+
     // prologue: stage 0 and A(1); stage 0 must land before the first reads
 #pragma unroll
     for (int q = 0; q < LPH; ++q) issue_a(0, q);
@@ -1026,8 +1054,11 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ring_kernel(GemmParams p, i
             for (int q = 0; q < kReads; ++q) read_one(0, 0, q, f0);
         }
         static_assert(STEPS == 4, "four 32-byte K steps per stage");
+        if (nkb == 0) issue_scales();
         for (int kb = 0; kb < nkb; ++kb) {
             const bool nb = kb + 1 < nkb, na = kb + 2 < nkb;
+            // no DMA is outstanding in the last stage: its waits are unaffected
+            if (!nb) issue_scales();
             step(f0, f1, kb, 1, nb ? 2 : 0, kb + 1, 0, Sh::B0);
             step(f1, f0, kb, 2, nb ? 2 : 0, kb + 1, Sh::B0, LPH);
             step(f0, f1, kb, 3, na ? 1 : 0, kb + 2, 0, Sh::A2);
@@ -1046,17 +1077,19 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ring_kernel(GemmParams p, i
         }
 
         // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
-        // every wave is past its last ring read before the ring holds partials
+        // every wave is past its last ring read before the ring holds
+        // partials, and every wave's scale DMA has landed
+        wait_vmcnt<0>();
         __builtin_amdgcn_s_waitcnt(0xC07F);
         exec_barrier();
         float sbv[L];
 #pragma unroll
-        for (int j = 0; j < L; ++j) sbv[j] = cok ? sbb[j * p.sbs_l + col * p.sbs_n] : 0.0f;
+        for (int j = 0; j < L; ++j) sbv[j] = cok ? sb_lds[j * 64 + wn * 32 + lr] : 0.0f;
         auto row_sa = [&](int r, float *sai) {
-            const int64_t row = m0 + wm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-            const bool ok = cok && row < p.M;
+            const int rt = wm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            const bool ok = cok && m0 + rt < p.M;
 #pragma unroll
-            for (int i = 0; i < NA; ++i) sai[i] = ok ? sab[(int64_t)(ILO + i) * p.sas_l + row * p.sas_m] : 0.0f;
+            for (int i = 0; i < NA; ++i) sai[i] = ok ? sa_lds[(ILO + i) * 64 + rt] : 0.0f;
         };
         // t value of pair q at row r: fl32(fl32(fl32(acc) * sa_i) * sb_j)
         auto tval = [&](int q, int r, const float *sai) {

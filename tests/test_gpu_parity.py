@@ -260,13 +260,14 @@ def test_cross_gemm_each_kernel_bitexact(oracle, gpu, L, kernel, monkeypatch):
 
 @pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
 @pytest.mark.parametrize("L", [3, 4])
-@pytest.mark.parametrize("K", [16, 128, 200, 300, 520, 1040])
+@pytest.mark.parametrize("K", [16, 128, 200, 300, 520, 1040, 2064])
 def test_ring_kernel_stage_counts(oracle, gpu, L, K, sdt, monkeypatch):
-    """The five-slot ring kernel over 1 to 9 stages of 128 bytes of K (the
+    """The five-slot ring kernel over 1 to 17 stages of 128 bytes of K (the
     prologue fetches a stage and a half, the loop issues each stage's DMA
-    ahead over the K steps of the stages before): int8 bit-exact against the
-    oracle, fp16 bit-identical to the two-slot pair kernel, which runs the
-    same MFMAs per accumulator in the same order."""
+    ahead over the K steps of the stages before, and the last stage fetches
+    the tile's scales into a free slot): int8 bit-exact against the oracle,
+    fp16 bit-identical to the two-slot pair kernel, which runs the same MFMAs
+    per accumulator in the same order."""
     kernel = "ring"
     import ozaki_triton_amd as ozk
     g = torch.Generator().manual_seed(K * 10 + L)
