@@ -868,9 +868,13 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_pair_kernel(GemmParams p, i
 // barrier); the barrier before stage kb + 1 waits for everything but the
 // step-2 part of A(kb + 2).
 // ---------------------------------------------------------------------------
-template <int L> struct RingShape {
+// W = 1 for num_splits 3 and 4: 32 x 32 wave blocks, 64 x 64 tiles.  W = 2
+// for num_splits 2: 64 x 64 wave blocks, 128 x 128 tiles; a wave then holds
+// 2 pairs x 4 blocks, again 128 accumulator registers, and the slot is again
+// 32 KB.
+template <int L, int W> struct RingShape {
     static constexpr int NW = 8;                       // waves
-    static constexpr int BM = 64, BN = 64;
+    static constexpr int BM = 64 * W, BN = 64 * W;
     static constexpr int SLOT = L * BM * kDmaRB;       // one half stage (A rows or B rows)
     static constexpr int NSLOT = 5;
     static constexpr int LPH = SLOT / (NW * 1024);     // DMA instructions per wave per half stage
@@ -879,13 +883,15 @@ template <int L> struct RingShape {
     static constexpr int A2 = (LPH + 1) / 2;           // A(kb + 2) instructions in step 2
     static_assert(SLOT % (NW * 1024) == 0, "a half stage must be whole 1 KB windows per wave");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS");
+    static_assert(L * BM <= 256, "the scales of a tile: one dword per lane of four waves");
     static_assert(kDmaRB == 128, "the ring assumes 128-byte stage rows");
 };
-template <typename ST, int L, typename AccT>
+
+template <typename ST, int L, typename AccT, int W>
 __global__ __launch_bounds__(512, 1) void cross_gemm_ring_kernel(GemmParams p, int group_m,
                                                                  uint32_t a_records,
                                                                  uint32_t b_records) {
-    using Sh = RingShape<L>;
+    using Sh = RingShape<L, W>;
     using PS = PairSplit<L, L>;
     using MF = Mfma<ST>;
     using Acc = typename MF::Acc;
@@ -953,20 +959,18 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ring_kernel(GemmParams p, i
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, ldsp, 16, vo, 0, 0, 0);
     };
 
-    // The scales of the tile (L x 64 of A's rows, L x 64 of B's columns, 2 KB)
-    // are fetched into a free ring slot by one dword DMA instruction per wave
-    // at the start of the last stage, so the epilogue reads them from the LDS
-    // instead of waiting on global loads.  That slot is the one of A(nkb),
-    // which is never fetched, or, when it is slot 0, the one of B(nkb); the
-    // scales take its last 2 KB, past the epilogue's partial sums, which
-    // start at slot 0 and may run into slot 1 (32 KB of fp64 > a 24 KB slot).
-    static_assert(2 * Sh::SLOT - 2048 >= 4 * 16 * 64 * (int)sizeof(double),
-                  "scales clear of the partial sums");
-    char *const scl = slot((2 * nkb) % Sh::NSLOT != 0 ? 2 * nkb : 2 * nkb + 1) + Sh::SLOT - 2048;
+    // The scales of the tile (L x BM of A's rows and L x BN of B's columns,
+    // at most 2 KB) are fetched into a free ring slot by one dword DMA
+    // instruction per wave at the start of the last stage, so the epilogue
+    // reads them from the LDS instead of waiting on global loads.  The slot is
+    // the one of A(nkb), which is never fetched.  Waves 0-3 fetch A's scales
+    // [L][BM] (entry 64 wave + lane), waves 4-7 B's [L][BN].
+    char *const scl = slot(2 * nkb);
     auto issue_scales = [&]() {
         const bool isa = wave < 4;
-        const int s = isa ? wave : wave - 4;           // slice
-        const int64_t rc = (isa ? m0 : n0) + lane;     // row of A / column of B
+        const int e = (isa ? wave : wave - 4) * 64 + lane;
+        const int s = e / BM;                              // slice
+        const int64_t rc = (isa ? m0 : n0) + e % BM;       // row of A / column of B
         const int64_t ext = isa ? ((int64_t)(L - 1) * p.sas_l + (p.M - 1) * p.sas_m + 1)
                                 : ((int64_t)(L - 1) * p.sbs_l + (p.N - 1) * p.sbs_n + 1);
         const bool ok = s < L && rc < (isa ? p.M : p.N);
@@ -976,7 +980,8 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ring_kernel(GemmParams p, i
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
             (void *)(isa ? p.sa + bidx * p.sas_b : p.sb + bidx * p.sbs_b), (short)0,
             (int)(ext * 4 < 0x7FFFFFFF ? ext * 4 : 0x7FFFFFFF), 0x00020000);
-        auto *ldsp = (__attribute__((address_space(3))) void *)(scl + (isa ? 0 : 1024) + s * 256);
+        auto *ldsp = (__attribute__((address_space(3))) void *)(scl + (isa ? 0 : 1024) +
+                                                              (isa ? wave : wave - 4) * 256);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, ldsp, 4, vo, 0, 0, 0);
     };
     const float *sa_lds = (const float *)scl, *sb_lds = (const float *)(scl + 1024);
@@ -995,32 +1000,34 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ring_kernel(GemmParams p, i
     }
     exec_barrier();
 
-    const float *sab = p.sa + bidx * p.sas_b;
-    const float *sbb = p.sb + bidx * p.sbs_b;
     const int64_t cbase = bidx * p.cs_b;
-    OA *part = (OA *)smem;   // epilogue hand-off [4 blocks][16][64 lanes]
-    const int64_t col = n0 + wn * 32 + lr;
-    const bool cok = col < p.N;
+    OA *part = (OA *)smem;   // epilogue hand-off [4 blocks][W * W][16][64 lanes]
 
     auto body = [&](auto G_) {
         constexpr int G = decltype(G_)::value;
         constexpr int F = PS::first(G), NP = PS::count(G), ILO = PS::ilo(G), NA = PS::na(G);
-        constexpr int kReads = NA + L;
+        constexpr int kReads = (NA + L) * W;
+        constexpr int NMF = NP * W * W;   // MFMAs per K step
         struct Frags {
-            i32x4 a[NA];
-            i32x4 b[L];
+            i32x4 a[NA][W];
+            i32x4 b[L][W];
         };
-        Acc acc[NP];
+        Acc acc[NP][W][W];
 #pragma unroll
-        for (int q = 0; q < NP; ++q) acc[q] = MF::zero();
+        for (int q = 0; q < NP; ++q)
+#pragma unroll
+            for (int x = 0; x < W * W; ++x) acc[q][x / W][x % W] = MF::zero();
 
         auto read_one = [&](int kb, int kk, int r, Frags &f) {
             const int ch = 2 * kk + h;
-            if (r < NA) {
-                f.a[r] = *(const i32x4 *)(slot(2 * kb) + rswz<kDmaRB>((ILO + r) * BM + wm * 32 + lr, ch));
+            if (r < NA * W) {
+                const int i = r / W, x = r % W;
+                f.a[i][x] = *(const i32x4 *)(slot(2 * kb) +
+                                             rswz<kDmaRB>((ILO + i) * BM + wm * 32 * W + 32 * x + lr, ch));
             } else {
-                const int j = r - NA;
-                f.b[j] = *(const i32x4 *)(slot(2 * kb + 1) + rswz<kDmaRB>(j * BN + wn * 32 + lr, ch));
+                const int j = (r - NA * W) / W, x = (r - NA * W) % W;
+                f.b[j][x] = *(const i32x4 *)(slot(2 * kb + 1) +
+                                             rswz<kDmaRB>(j * BN + wn * 32 * W + 32 * x + lr, ch));
             }
         };
         // One K step: the reads of the next K step (stage rkb, step nkk) into
@@ -1033,13 +1040,14 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ring_kernel(GemmParams p, i
 #pragma unroll
             for (int q = 0; q < kReads; ++q) read_one(rkb, nkk, q, nxt);
 #pragma unroll
-            for (int q = 0; q < NP; ++q) {
+            for (int n = 0; n < NMF; ++n) {
+                const int q = n / (W * W), x = (n / W) % W, y = n % W;
                 const int i = (F + q) / L, j = (F + q) % L;
-                acc[q] = MF::run(cur.a[i - ILO], cur.b[j], acc[q]);
+                acc[q][x][y] = MF::run(cur.a[i - ILO][x], cur.b[j][y], acc[q][x][y]);
 #pragma unroll
                 for (int d = 0; d < LPH; ++d) {
-                    // instruction lo + d goes after MFMA (d * NP) / cnt
-                    if (d < cnt && (d * NP) / cnt == q) {
+                    // instruction lo + d goes after MFMA (d * NMF) / cnt
+                    if (d < cnt && (d * NMF) / cnt == n) {
                         if (kind == 1) issue_a(dkb, lo + d);
                         else if (kind == 2) issue_b(dkb, lo + d);
                     }
@@ -1077,54 +1085,67 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ring_kernel(GemmParams p, i
         }
 
         // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
-        // every wave is past its last ring read before the ring holds
-        // partials, and every wave's scale DMA has landed
+        // every wave's scale DMA has landed and every wave is past its last
+        // ring read
         wait_vmcnt<0>();
         __builtin_amdgcn_s_waitcnt(0xC07F);
         exec_barrier();
-        float sbv[L];
+        // this wave's scales into registers: sa of its rows, sb of its columns
+        float sbv[W][L], sav[W][16][NA];
 #pragma unroll
-        for (int j = 0; j < L; ++j) sbv[j] = cok ? sb_lds[j * 64 + wn * 32 + lr] : 0.0f;
-        auto row_sa = [&](int r, float *sai) {
-            const int rt = wm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-            const bool ok = cok && m0 + rt < p.M;
+        for (int y = 0; y < W; ++y) {
+            const int ct = wn * 32 * W + 32 * y + lr;
 #pragma unroll
-            for (int i = 0; i < NA; ++i) sai[i] = ok ? sa_lds[(ILO + i) * 64 + rt] : 0.0f;
-        };
-        // t value of pair q at row r: fl32(fl32(fl32(acc) * sa_i) * sb_j)
-        auto tval = [&](int q, int r, const float *sai) {
-            const int i = (F + q) / L, j = (F + q) % L;
-            const float t1 = MF::to_f32(acc[q][r]) * sai[i - ILO];
-            return t1 * sbv[j];
-        };
-        float tv[NP][16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            float sai[NA];
-            row_sa(r, sai);
-#pragma unroll
-            for (int q = 0; q < NP; ++q) tv[q][r] = tval(q, r, sai);
+            for (int j = 0; j < L; ++j) sbv[y][j] = sb_lds[j * BN + ct];
         }
-        if constexpr (G == 0) {
+#pragma unroll
+        for (int x = 0; x < W; ++x)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                OA out = (OA)0;
+                const int rt = wm * 32 * W + 32 * x + 8 * (r >> 2) + 4 * h + (r & 3);
 #pragma unroll
-                for (int q = 0; q < NP; ++q) out = out + (OA)tv[q][r];
-                part[(blk * 16 + r) * 64 + lane] = out;
+                for (int i = 0; i < NA; ++i) sav[x][r][i] = sa_lds[(ILO + i) * BM + rt];
             }
+        // t value of pair q, block (x, y), accumulator row r:
+        // fl32(fl32(fl32(acc) * sa_i) * sb_j)
+        auto tval = [&](int q, int x, int y, int r) {
+            const int i = (F + q) / L, j = (F + q) % L;
+            const float t1 = MF::to_f32(acc[q][x][y][r]) * sav[x][r][i - ILO];
+            return t1 * sbv[y][j];
+        };
+        // the partial sums overwrite the scales: every wave has read them
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        exec_barrier();
+        if constexpr (G == 0) {
+#pragma unroll
+            for (int x = 0; x < W; ++x)
+#pragma unroll
+                for (int y = 0; y < W; ++y)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        OA out = (OA)0;
+#pragma unroll
+                        for (int q = 0; q < NP; ++q) out = out + (OA)tval(q, x, y, r);
+                        part[(((blk * W + x) * W + y) * 16 + r) * 64 + lane] = out;
+                    }
             __builtin_amdgcn_s_waitcnt(0xC07F);
             exec_barrier();
         } else {
             exec_barrier();
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t row = m0 + wm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                OA out = part[(blk * 16 + r) * 64 + lane];
+            for (int x = 0; x < W; ++x)
 #pragma unroll
-                for (int q = 0; q < NP; ++q) out = out + (OA)tv[q][r];
-                if (cok && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
-            }
+                for (int y = 0; y < W; ++y) {
+                    const int64_t col = n0 + wn * 32 * W + 32 * y + lr;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int64_t row = m0 + wm * 32 * W + 32 * x + 8 * (r >> 2) + 4 * h + (r & 3);
+                        OA out = part[(((blk * W + x) * W + y) * 16 + r) * 64 + lane];
+#pragma unroll
+                        for (int q = 0; q < NP; ++q) out = out + (OA)tval(q, x, y, r);
+                        if (col < p.N && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
+                    }
+                }
         }
     };
     if (grp == 0) body(std::integral_constant<int, 0>{});
@@ -1432,12 +1453,16 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype) {
     // OZK_GEMM_KERNEL=staged|dma|ad|pair|ring forces a kernel (tests cover
     // every one at small sizes).  By default, when both operands fit the
     // 31-bit buffer offsets of the LDS-DMA kernels: the ring kernel for
-    // L = 3, 4 and the pair-split kernel for L > 4 (their wave tile is 32 x 32
-    // anyway), the 2 x 2 LDS-DMA kernel with its larger wave tiles for L <= 2;
-    // else the VGPR-staged kernel.
+    // L = 3, 4 (64 x 64 tiles) and for L = 2 when the grid takes 128 x 128
+    // tiles, the pair-split kernel for L > 4, the 2 x 2 LDS-DMA kernel with its
+    // larger wave tiles otherwise; else the VGPR-staged kernel.
     const bool fits = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es) >= 0 &&
                       dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es) >= 0;
-    plan.kind = !fits ? kGemmStaged : L <= 2 ? kGemmDMA : L <= 4 ? kGemmRing : kGemmPair;
+    plan.kind = !fits              ? kGemmStaged
+                : L <= 1           ? kGemmDMA
+                : L == 2           ? ((mi == 2 && ni == 2) ? kGemmRing : kGemmDMA)
+                : L <= 4           ? kGemmRing
+                                   : kGemmPair;
     if (L > 4) return plan;   // only the pair-split kernel, launched per i-row range
     const char *env = getenv("OZK_GEMM_KERNEL");
     auto forced = [&](const char *name) { return env && strcmp(env, name) == 0; };
@@ -1445,7 +1470,7 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype) {
     else if (fits && forced("ad")) plan.kind = kGemmAD;
     else if (fits && forced("dma")) plan.kind = kGemmDMA;
     else if (fits && forced("pair")) plan.kind = L >= 3 ? kGemmPair : kGemmDMA;
-    else if (fits && forced("ring")) plan.kind = L >= 3 ? kGemmRing : kGemmDMA;
+    else if (fits && forced("ring")) plan.kind = L >= 2 ? kGemmRing : kGemmDMA;
     if (plan.kind == kGemmAD) plan.group_m = 2;
     return plan;
 }
@@ -1527,8 +1552,9 @@ static hipError_t launch_pair(const GemmParams &p, const GemmPlan &plan, hipStre
 
 template <typename ST, int L, typename AccT>
 static hipError_t launch_ring(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
-    using Sh = RingShape<L>;
-    auto kern = cross_gemm_ring_kernel<ST, L, AccT>;
+    constexpr int W = (L <= 2) ? 2 : 1;
+    using Sh = RingShape<L, W>;
+    auto kern = cross_gemm_ring_kernel<ST, L, AccT, W>;
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void *)kern,
@@ -1570,9 +1596,9 @@ template <typename ST, int L, int MI, int NI, typename AccT>
 static hipError_t launch_one(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     if constexpr (L >= 3) {
         if (plan.kind == kGemmPair) return launch_pair<ST, L, AccT, L>(p, plan, st, 0, 0);
-        if constexpr (L <= 4) {
-            if (plan.kind == kGemmRing) return launch_ring<ST, L, AccT>(p, plan, st);
-        }
+    }
+    if constexpr (L >= 2 && L <= 4) {
+        if (plan.kind == kGemmRing) return launch_ring<ST, L, AccT>(p, plan, st);
     }
     if (plan.kind == kGemmAD) {
         constexpr int ANI = (L == 1) ? 8 : (L == 2) ? 4 : 1;

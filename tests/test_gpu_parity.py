@@ -259,19 +259,22 @@ def test_cross_gemm_each_kernel_bitexact(oracle, gpu, L, kernel, monkeypatch):
 
 
 @pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
-@pytest.mark.parametrize("L", [3, 4])
+@pytest.mark.parametrize("L", [2, 3, 4])
 @pytest.mark.parametrize("K", [16, 128, 200, 300, 520, 1040, 2064])
 def test_ring_kernel_stage_counts(oracle, gpu, L, K, sdt, monkeypatch):
     """The five-slot ring kernel over 1 to 17 stages of 128 bytes of K (the
     prologue fetches a stage and a half, the loop issues each stage's DMA
     ahead over the K steps of the stages before, and the last stage fetches
-    the tile's scales into a free slot): int8 bit-exact against the oracle,
-    fp16 bit-identical to the two-slot pair kernel, which runs the same MFMAs
-    per accumulator in the same order."""
+    the tile's scales into a free slot), with 64 x 64 tiles (L = 3, 4) and
+    128 x 128 tiles (L = 2; M and N cut a tile): int8 bit-exact against the
+    oracle, fp16 bit-identical to the pair kernel (L >= 3) or the 2 x 2
+    kernel (L = 2), which run the same MFMAs per accumulator in the same
+    order."""
     kernel = "ring"
     import ozaki_triton_amd as ozk
     g = torch.Generator().manual_seed(K * 10 + L)
-    As, BsT, sa, sb = _random_slices(g, 2, L, 130, 72, K, sdt)
+    M, N = (130, 72) if L >= 3 else (200, 136)
+    As, BsT, sa, sb = _random_slices(g, 2, L, M, N, K, sdt)
     args = (As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), L, torch.float64)
     monkeypatch.setenv("OZK_GEMM_KERNEL", kernel)
     C = to_np(ozk.cross_gemm(*args))
@@ -281,7 +284,7 @@ def test_ring_kernel_stage_counts(oracle, gpu, L, K, sdt, monkeypatch):
                                      "float64")
             assert_bitwise_equal(C[b], want, f"{kernel} L{L} K{K} b{b}")
     else:
-        monkeypatch.setenv("OZK_GEMM_KERNEL", "pair")
+        monkeypatch.setenv("OZK_GEMM_KERNEL", "pair" if L >= 3 else "dma")
         assert_bitwise_equal(C, to_np(ozk.cross_gemm(*args)), f"{kernel} vs pair fp16 L{L} K{K}")
 
 
