@@ -880,7 +880,9 @@ template <int L, int W> struct RingShape {
     static constexpr int NW = 8;                       // waves
     static constexpr int BM = 64 * W, BN = 64 * W;
     static constexpr int SLOT = L * BM * kDmaRB;       // one half stage (A rows or B rows)
-    static constexpr int NSLOT = 5;
+    // six slots where they fit (L = 3: 144 KB): then whole stages are fetched
+    // two ahead, B as well as A
+    static constexpr int NSLOT = 6 * SLOT <= 160 * 1024 ? 6 : 5;
     static constexpr int LPH = SLOT / (NW * 1024);     // DMA instructions per wave per half stage
     static constexpr int LDS_BYTES = NSLOT * SLOT;
     static constexpr int B0 = (LPH + 1) / 2;           // B(kb + 1) instructions in step 0
@@ -990,7 +992,8 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ring_kernel(GemmParams p, i
     };
     const float *sa_lds = (const float *)scl, *sb_lds = (const float *)(scl + 1024);
 
-    // prologue: stage 0 and A(1); stage 0 must land before the first reads
+    // prologue: stage 0 and A(1) (six slots: all of stage 1); stage 0 must
+    // land before the first reads
 #pragma unroll
     for (int q = 0; q < LPH; ++q) issue_a(0, q);
 #pragma unroll
@@ -998,7 +1001,13 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ring_kernel(GemmParams p, i
     if (nkb > 1) {
 #pragma unroll
         for (int q = 0; q < LPH; ++q) issue_a(1, q);
-        wait_vmcnt<LPH>();
+        if constexpr (Sh::NSLOT == 6) {
+#pragma unroll
+            for (int q = 0; q < LPH; ++q) issue_b(1, q);
+            wait_vmcnt<2 * LPH>();
+        } else {
+            wait_vmcnt<LPH>();
+        }
     } else {
         wait_vmcnt<0>();
     }
@@ -1071,21 +1080,38 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ring_kernel(GemmParams p, i
             const bool nb = kb + 1 < nkb, na = kb + 2 < nkb;
             // no DMA is outstanding in the last stage: its waits are unaffected
             if (!nb) issue_scales();
-            step(f0, f1, kb, 1, nb ? 2 : 0, kb + 1, 0, Sh::B0);
-            step(f1, f0, kb, 2, nb ? 2 : 0, kb + 1, Sh::B0, LPH);
-            step(f0, f1, kb, 3, na ? 1 : 0, kb + 2, 0, Sh::A2);
-            if (nb) {
-                // stage kb + 1 has landed once only this wave's first part of
-                // A(kb + 2) may be outstanding; the barrier publishes every
-                // wave's DMA writes, and the lgkmcnt wait makes this wave's
-                // reads of stage kb complete before slots are refilled
-                if (na) wait_vmcnt<Sh::A2>();
-                else wait_vmcnt<0>();
-                __builtin_amdgcn_s_waitcnt(0xC07F);
-                exec_barrier();
+            if constexpr (Sh::NSLOT == 6) {
+                // A(kb + 2) and B(kb + 2) take the slots of A(kb - 1) and
+                // B(kb - 1), released by the barrier of stage kb - 1
+                step(f0, f1, kb, 1, na ? 1 : 0, kb + 2, 0, Sh::A2);
+                step(f1, f0, kb, 2, na ? 1 : 0, kb + 2, Sh::A2, LPH);
+                step(f0, f1, kb, 3, na ? 2 : 0, kb + 2, 0, Sh::B0);
+                if (nb) {
+                    // stage kb + 1 has landed once only stage kb + 2's
+                    // instructions issued so far may be outstanding
+                    if (na) wait_vmcnt<LPH + Sh::B0>();
+                    else wait_vmcnt<0>();
+                    __builtin_amdgcn_s_waitcnt(0xC07F);
+                    exec_barrier();
+                }
+                step(f1, f0, kb + 1, 0, na ? 2 : 0, kb + 2, Sh::B0, LPH);
+            } else {
+                step(f0, f1, kb, 1, nb ? 2 : 0, kb + 1, 0, Sh::B0);
+                step(f1, f0, kb, 2, nb ? 2 : 0, kb + 1, Sh::B0, LPH);
+                step(f0, f1, kb, 3, na ? 1 : 0, kb + 2, 0, Sh::A2);
+                if (nb) {
+                    // stage kb + 1 has landed once only this wave's first part
+                    // of A(kb + 2) may be outstanding; the barrier publishes
+                    // every wave's DMA writes, and the lgkmcnt wait makes this
+                    // wave's reads of stage kb complete before slots are refilled
+                    if (na) wait_vmcnt<Sh::A2>();
+                    else wait_vmcnt<0>();
+                    __builtin_amdgcn_s_waitcnt(0xC07F);
+                    exec_barrier();
+                }
+                // the last step reads stage kb + 1's step 0 (unused past the end)
+                step(f1, f0, kb + 1, 0, na ? 1 : 0, kb + 2, Sh::A2, LPH);
             }
-            // the last step reads stage kb + 1's step 0 (unused past the end)
-            step(f1, f0, kb + 1, 0, na ? 1 : 0, kb + 2, Sh::A2, LPH);
         }
 
         // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
