@@ -288,6 +288,39 @@ def test_ring_kernel_stage_counts(oracle, gpu, L, K, sdt, monkeypatch):
         assert_bitwise_equal(C, to_np(ozk.cross_gemm(*args)), f"{kernel} vs pair fp16 L{L} K{K}")
 
 
+@pytest.mark.parametrize("out", [torch.float64, torch.float32, torch.float16, torch.bfloat16,
+                                 torch.int8])
+@pytest.mark.parametrize("sdt", [torch.int8, torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("L", [2, 3, 4])
+def test_ring_kernel_dtypes(oracle, gpu, L, sdt, out, monkeypatch):
+    """The ring kernel for every slice and output dtype, batched, with a
+    broadcast (batch stride 0) B: int8 slices bit-exact against the oracle;
+    float slices bit-identical to the pair kernel (L >= 3) or the 2 x 2 kernel
+    (L = 2), which run the same MFMAs per accumulator and the same epilogue."""
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(L * 41 + ALL_SLICES.index(sdt) * 7 + len(str(out)))
+    M, N, K = (100, 72, 400) if L >= 3 else (150, 136, 400)
+    As, BsT, sa, sb = _random_slices(g, 2, L, M, N, K,
+                                     torch.int8 if sdt == torch.int8 else torch.float16)
+    if sdt != torch.int8:
+        As, BsT = As.to(sdt), BsT.to(sdt)
+    if out in (torch.float16, torch.bfloat16, torch.int8):
+        sa = sa * 2.0 ** (12 if sdt == torch.int8 else 2)
+    Bd = BsT[:1].to(gpu).expand(2, -1, -1, -1).transpose(-1, -2)   # broadcast B
+    sbd = sb[:1].to(gpu).expand(2, -1, -1)
+    args = (As.to(gpu), Bd, sa.to(gpu), sbd, L, out)
+    monkeypatch.setenv("OZK_GEMM_KERNEL", "ring")
+    C = to_np(ozk.cross_gemm(*args))
+    if sdt == torch.int8:
+        for b in range(2):
+            want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[0]), to_np(sa[b]), to_np(sb[0]),
+                                     NAME_OF[out])
+            assert_bitwise_equal(C[b], want, f"ring L{L} {sdt} {out} b{b}")
+    else:
+        monkeypatch.setenv("OZK_GEMM_KERNEL", "pair" if L >= 3 else "dma")
+        assert_bitwise_equal(C, to_np(ozk.cross_gemm(*args)), f"ring vs pair L{L} {sdt} {out}")
+
+
 @pytest.mark.parametrize("xdt,sdt", COMBOS)
 def test_split_transpose_path(oracle, gpu, xdt, sdt):
     """Column splits (B^T view) whose K exceeds the resident strip: transposed
