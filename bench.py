@@ -324,8 +324,8 @@ def main():
             "avg_ms": round(t_cross, 4),
         },
         "split": {
-            "kernels": "split_rows_kernel (A) + split_strip_kernel or transpose_kernel + "
-                       "split_rows_kernel (B)",
+            "kernels": "split_rows_kernel (A) + split_coop_kernel, or transpose_kernel + "
+                       "split_rows_kernel for columns longer than 16384 fp32 / 32768 fp64 (B)",
             "bound": "hbm",
             "bytes": split_bytes,
             "achieved": round(split_gbs, 1),

@@ -88,9 +88,12 @@ int ozk_compute_split_bits(int64_t n, int slice_dtype, int dot_accum_dtype, int 
  * exactly), with the residual rounded to fp32 between levels exactly as the
  * reference's fp32 residual buffer does.  B is split through its transposed
  * view (rows = columns of B, x_strides = {K*N, 1, N}).
- * Workspace: 0 bytes on the resident fast paths (fp64 / fp32 input); otherwise
- * ozk_split_workspace_bytes(): an fp32 copy of a narrow input, a transposed
- * copy of a long column operand, or an fp32 residual for odd layouts.
+ * Workspace (ozk_split_workspace_bytes()): 0 bytes for K-contiguous fp64 /
+ * fp32 rows; for row-contiguous operands (the B^T view) 8 bytes per column
+ * group (128 bytes of a row), level and K chunk of 512 or 1024 rows, through
+ * which the workgroups of a column group exchange their level maxima; an fp32
+ * copy of a narrow input, a transposed copy of a long column operand, or an
+ * fp32 residual for odd layouts.
  */
 int ozk_split_workspace_bytes(int x_dtype, int64_t batch, int64_t rows, int64_t K,
                               const int64_t x_strides[3], int num_splits, int slice_dtype,

@@ -28,7 +28,9 @@ enum SplitPath {
     kSplitStrip = 1,
     kSplitGeneric = 2,
     kSplitTransposeRows = 3,
-    kSplitConvert = 4   // narrow input: exact fp32 copy in the workspace, then the fp32 plan
+    kSplitConvert = 4,  // narrow input: exact fp32 copy in the workspace, then the fp32 plan
+    kSplitCoop = 5      // column strips of 128-byte row segments cut along K, the level
+                        // maxima combined through the workspace
 };
 
 // Chooses the split kernel for p (x_dtype: 0 = f64, 1 = f32, 2 = f16,

@@ -31,21 +31,34 @@
 //                elsewhere q is an fp32 value and the hardware RNE conversion
 //                rounds it once; slice*s is exact in fp32 in every case.
 //
-// Three kernels:
+// Kernels:
 //   split_rows_kernel   row-resident, for K-contiguous rows (A).  A group of
 //                       64*GW lanes owns one row; the row stays in VGPRs across
 //                       all levels, so X is read from HBM once and each slice
 //                       written once.
-//   split_strip_kernel  column-strip-resident, for row-contiguous operands
-//                       (the B^T view).  A workgroup owns the VEC adjacent
-//                       columns one 16-byte load covers, for all K; each lane
-//                       holds 4 consecutive k of every column so that int8 /
-//                       fp16 slices leave as 4-/8-byte stores along K.
+//   split_coop_kernel   column groups of row-contiguous operands (the B^T
+//                       view), 128-byte row segments wide, cut along K over
+//                       several workgroups that exchange the level maxima
+//                       through the workspace; X read once, slices written
+//                       once (the default for columns up to 32 K chunks).
+//   split_strip_kernel  column-strip-resident, for row-contiguous operands.
+//                       A workgroup owns the VEC adjacent columns one 16-byte
+//                       load covers, for all K; each lane holds 4 consecutive
+//                       k of every column so that int8 / fp16 slices leave as
+//                       4-/8-byte stores along K.  Kept as a forced
+//                       alternative (OZK_SPLIT_KERNEL=strip): its 16-byte row
+//                       pieces touch a cache line per 16 bytes read.
+//   transpose_kernel    + split_rows_kernel: columns longer than the
+//                       cooperative kernel takes, transposed into the
+//                       workspace first.
 //   split_generic_kernel any strides and any K: one workgroup per row,
 //                       multi-pass over K with an fp32 residual in workspace
 //                       (the reference's own traffic pattern).
 #include "ozk_common.h"
 #include "ozk_internal.h"
+
+#include <stdlib.h>
+#include <string.h>
 
 namespace ozk {
 
@@ -493,6 +506,223 @@ __global__ __launch_bounds__(NT) void split_strip_kernel(SplitParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// Column split shared by a group of workgroups (row-contiguous operands, the
+// B^T view).  A 16-byte load per lane covers only 16 bytes of a row, so a
+// strip one load wide (split_strip_kernel) touches one cache line per 16
+// bytes read; reads of 128-byte row segments run at copy speed.  A strip of
+// SW = 128 / sizeof(XT) columns over all of K does not fit one CU, so it is
+// cut along K into P chunks of CH rows, one workgroup each, and the level
+// maxima are combined through global memory:
+//   * workgroup g = blockIdx.x is member g % P of column group g / P (batch
+//     b, columns col0 .. col0 + SW); lane t covers the VEC columns
+//     col0 + VEC * (t % 8) + {0..VEC-1} and the rows
+//     member * CH + 4 * (t / 8 + RPP * j) + {0..3}, j < RPL / 4, so a wave
+//     load covers eight full 128-byte row segments and a lane holds 4
+//     consecutive k of each column (4- / 8-byte slice stores along K);
+//   * per level, wave 0 stores the workgroup's column maxima into
+//     slot[group][level][member][SW], one 64-bit word each (the tag 1 in the
+//     high half, the fp32 maximum in the low half), with agent-scope stores,
+//     and polls the P * SW words of its group and level with agent-scope
+//     loads until all carry the tag.  Every word validates itself, so no
+//     fence (no L2 write-back or invalidation) is needed;
+//   * the members of a group are consecutive workgroup ids.  Workgroups are
+//     dispatched in id order, so the group of the oldest resident workgroup
+//     is entirely resident once P + 8 is below the workgroups that fit an
+//     XCD; the planner keeps P <= 128.  A wait that still runs out (about
+//     0.1 s) stores NaN scales instead of hanging.
+// slot must be zero at launch (the launcher clears it first).
+// ---------------------------------------------------------------------------
+constexpr int kCoopNT = 256;
+constexpr int kCoopMaxP = 32;
+constexpr int kCoopSpin = 1 << 16;
+constexpr uint64_t kCoopTag = 1ull << 32;               // high word of a published maximum
+
+__global__ __launch_bounds__(256) void zero_u64_kernel(uint64_t *p, int64_t n) {
+    for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0;
+}
+
+template <typename XT, typename ST, int RPL>
+__global__ __launch_bounds__(kCoopNT) void split_coop_kernel(SplitParams p, uint64_t *slot, int P) {
+    constexpr int NT = kCoopNT, NG = RPL / 4;
+    constexpr int VEC = 16 / (int)sizeof(XT);
+    constexpr int SW = 8 * VEC;          // columns per group
+    constexpr int RPP = NT / 8;          // row quads per pass
+    constexpr int NW = NT / 64;
+    __shared__ float red[NW][8][VEC];
+    __shared__ float fin[SW];
+    __shared__ int bad;
+
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int seg = t & 7, ro = t >> 3;
+    const int64_t g = blockIdx.x;
+    const int member = (int)(g % P);
+    const int64_t grp = g / P;
+    const int64_t nstr = (p.rows + SW - 1) / SW;
+    const int64_t b = grp / nstr;
+    const int64_t col0 = (grp % nstr) * SW;
+    const int64_t mycol = col0 + seg * VEC;
+    const bool cvalid = mycol < p.rows;   // rows % VEC == 0: all VEC columns or none
+    const int64_t kbase = (int64_t)member * (RPP * RPL);
+
+    const XT *xb = (const XT *)p.X + b * p.xs_b + mycol;
+    XT v[NG][4][VEC];
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+#pragma unroll
+        for (int dk = 0; dk < 4; ++dk) {
+            const int64_t k = kbase + 4 * (ro + RPP * j) + dk;
+            XT tmp[VEC];
+            if (cvalid && k < p.K) {
+                loadvec(xb + k * p.xs_k, tmp);
+            } else {
+#pragma unroll
+                for (int u = 0; u < VEC; ++u) tmp[u] = (XT)0;
+            }
+#pragma unroll
+            for (int u = 0; u < VEC; ++u) v[j][dk][u] = tmp[u];
+        }
+    }
+    if (t == 0) bad = 0;
+
+    // maximum over the group of the lane maxima m (fl32 values >= 0), per column
+    auto group_max = [&](float m[VEC], int l) {
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) {
+            m[u] = fmaxf(m[u], __shfl_xor(m[u], 8));
+            m[u] = fmaxf(m[u], __shfl_xor(m[u], 16));
+            m[u] = fmaxf(m[u], __shfl_xor(m[u], 32));
+        }
+        if (lane < 8) {
+#pragma unroll
+            for (int u = 0; u < VEC; ++u) red[wave][lane][u] = m[u];
+        }
+        lds_barrier();
+        float r = 0.0f;
+        if (t < SW) {
+            r = red[0][t / VEC][t % VEC];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) r = fmaxf(r, red[w][t / VEC][t % VEC]);
+        }
+        if (P > 1 && wave == 0) {
+            // publish this member's maxima, then poll until every member's
+            // word of this level carries the tag (words already seen are not
+            // read again)
+            uint64_t *sl = slot + (grp * p.L + l) * (int64_t)P * SW;
+            if (t < SW)
+                __hip_atomic_store(sl + (int64_t)member * SW + t, kCoopTag | __float_as_uint(r),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int nw = P * SW;
+            uint64_t seen = 0;
+            const uint64_t want = (lane < nw) ? (((nw - 1 - lane) / 64 >= 63)
+                                                     ? ~0ull
+                                                     : (2ull << ((nw - 1 - lane) / 64)) - 1)
+                                              : 0;
+            float q = 0.0f;
+            for (int it = 0;; ++it) {
+                for (int n = 0; n < (nw + 63) / 64; ++n) {
+                    const int i = lane + 64 * n;
+                    if (i < nw && !((seen >> n) & 1)) {
+                        const uint64_t w64 =
+                            __hip_atomic_load(sl + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        if ((w64 >> 32) == (kCoopTag >> 32)) {
+                            seen |= 1ull << n;
+                            q = fmaxf(q, __uint_as_float((uint32_t)w64));
+                        }
+                    }
+                }
+                if (__all(seen == want)) break;
+                if (it == kCoopSpin) {
+                    if (lane == 0) bad = 1;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            // lane i holds the maximum of column i % SW over members i / SW + 64 / SW * n
+            r = q;
+#pragma unroll
+            for (int x = SW; x < 64; x *= 2) r = fmaxf(r, __shfl_xor(r, x));
+        }
+        if (t < SW) fin[t] = r;
+        lds_barrier();
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) m[u] = fin[seg * VEC + u];
+    };
+    // scales of level l (member 0 stores them; NaN after a wait that ran out)
+    auto store_scales = [&](int l) {
+        if (member == 0 && t < SW && col0 + t < p.rows) {
+            const LevelScale c = level_scale(fin[t], p.alpha);
+            p.scales[b * p.cs_b + l * p.cs_l + (col0 + t) * p.cs_r] =
+                bad ? __int_as_float(0x7fc00000) : c.s;
+        }
+    };
+    const int64_t sbase = b * p.ss_b + mycol * p.ss_r;
+
+    float w[NG][4][VEC];
+    {
+        float m[VEC];
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) m[u] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NG; ++j)
+#pragma unroll
+            for (int dk = 0; dk < 4; ++dk)
+#pragma unroll
+                for (int u = 0; u < VEC; ++u) m[u] = fmaxf(m[u], absf(v[j][dk][u]));
+        group_max(m, 0);
+        store_scales(0);
+        LevelScale c[VEC];
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) c[u] = level_scale(m[u], p.alpha);
+#pragma unroll
+        for (int j = 0; j < NG; ++j) {
+            const int64_t k0 = kbase + 4 * (ro + RPP * j);
+            uint32_t qv[VEC][4];
+#pragma unroll
+            for (int dk = 0; dk < 4; ++dk)
+#pragma unroll
+                for (int u = 0; u < VEC; ++u)
+                    qv[u][dk] = Quant<ST, Modes<XT>::first>::run(v[j][dk][u], c[u], &w[j][dk][u]);
+            if (cvalid && k0 < p.K) {
+#pragma unroll
+                for (int u = 0; u < VEC; ++u)
+                    Store4<ST>::run(p.slices, sbase + u * p.ss_r + k0, qv[u]);
+            }
+        }
+    }
+    for (int l = 1; l < p.L; ++l) {
+        float m[VEC];
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) m[u] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NG; ++j)
+#pragma unroll
+            for (int dk = 0; dk < 4; ++dk)
+#pragma unroll
+                for (int u = 0; u < VEC; ++u) m[u] = fmaxf(m[u], fabsf(w[j][dk][u]));
+        group_max(m, l);
+        store_scales(l);
+        LevelScale c[VEC];
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) c[u] = level_scale(m[u], p.alpha);
+#pragma unroll
+        for (int j = 0; j < NG; ++j) {
+            const int64_t k0 = kbase + 4 * (ro + RPP * j);
+            uint32_t qv[VEC][4];
+#pragma unroll
+            for (int dk = 0; dk < 4; ++dk)
+#pragma unroll
+                for (int u = 0; u < VEC; ++u)
+                    qv[u][dk] = Quant<ST, Modes<XT>::rest>::run(w[j][dk][u], c[u], &w[j][dk][u]);
+            if (cvalid && k0 < p.K) {
+#pragma unroll
+                for (int u = 0; u < VEC; ++u)
+                    Store4<ST>::run(p.slices, sbase + l * p.ss_l + u * p.ss_r + k0, qv[u]);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Generic split: one workgroup of 256 lanes per row, any strides, any K.
 // Level l reads src (X for l = 0, else the fp32 residual workspace) twice:
 // once for the row max, once to quantise; lane t always touches k = t + 256*i,
@@ -663,6 +893,23 @@ static const StripCfg kStripCfgs[] = {
 };
 static const int kNumStripCfgs = sizeof(kStripCfgs) / sizeof(kStripCfgs[0]);
 
+// rows per lane of split_coop_kernel (fp64 columns longer than 4096 take
+// 32, which halves the workgroups that exchange maxima), the members (K
+// chunks of 32 * rpl rows) of a column group, and the workspace: the
+// published maxima [groups][L][P][SW], 8 bytes each (none for P = 1)
+static int coop_rpl(int64_t K, int xsz) { return (xsz == 8 && K > 4096) ? 32 : 16; }
+static int64_t coop_members(int64_t K, int rpl) {
+    const int64_t ch = (int64_t)kCoopNT / 8 * rpl;
+    return K <= 0 ? 1 : (K + ch - 1) / ch;
+}
+static int64_t coop_slots(const SplitParams &p, int xsz, int rpl) {
+    const int64_t P = coop_members(p.K, rpl);
+    if (P <= 1) return 0;
+    const int64_t sw = 8 * (16 / xsz);
+    const int64_t groups = p.batch * ((p.rows + sw - 1) / sw);
+    return groups * p.L * P * sw;
+}
+
 static bool aligned(const void *ptr, int64_t bytes) {
     return ((uintptr_t)ptr % (uintptr_t)bytes) == 0;
 }
@@ -706,8 +953,16 @@ SplitPlan plan_split(const SplitParams &p, int x_dtype, int slice_dtype) {
         }
     }
     const int vec = 16 / xsz;
-    if (k4 && slice_ok && p.xs_r == 1 && p.rows % vec == 0 && aligned(p.X, 16) &&
-        (p.xs_k * xsz) % 16 == 0 && (p.xs_b * xsz) % 16 == 0) {
+    // OZK_SPLIT_KERNEL=strip|transpose|generic steers column operands off the
+    // default (tests cover every path); a path whose requirements fail is not taken
+    const char *env = getenv("OZK_SPLIT_KERNEL");
+    auto forced = [&](const char *name) { return env && strcmp(env, name) == 0; };
+    const bool cols_ok = k4 && slice_ok && p.xs_r == 1 && p.rows % vec == 0 && aligned(p.X, 16) &&
+                         (p.xs_k * xsz) % 16 == 0 && (p.xs_b * xsz) % 16 == 0;
+    if (cols_ok && !forced("strip") && !forced("transpose") && !forced("generic") &&
+        coop_members(p.K, coop_rpl(p.K, xsz)) <= kCoopMaxP)
+        return {kSplitCoop, coop_rpl(p.K, xsz)};
+    if (cols_ok && !forced("transpose") && !forced("generic")) {
         for (int i = 0; i < kNumStripCfgs; ++i) {
             const StripCfg &c = kStripCfgs[i];
             if (c.kpt * vec > 64) continue;
@@ -716,7 +971,7 @@ SplitPlan plan_split(const SplitParams &p, int x_dtype, int slice_dtype) {
     }
     // row-contiguous operand with a K too long for a resident strip: transpose
     // into the workspace, then the row kernel (if the row fits)
-    if (k4 && slice_ok && p.xs_r == 1 && (p.K * xsz) % 16 == 0) {
+    if (k4 && slice_ok && p.xs_r == 1 && (p.K * xsz) % 16 == 0 && !forced("generic")) {
         for (int i = 0; i < kNumRowCfgs; ++i) {
             const RowCfg &c = kRowCfgs[i];
             if (x_dtype == 0 && c.nc > 8) continue;
@@ -742,6 +997,8 @@ size_t split_workspace_bytes(const SplitParams &p, const SplitPlan &plan, int x_
         return (size_t)(n * 4) + split_workspace_bytes(converted_params(p), inner, 1, slice_dtype);
     }
     if (plan.path == kSplitTransposeRows) return (size_t)(n * dtype_size(x_dtype));
+    if (plan.path == kSplitCoop)
+        return (size_t)coop_slots(p, dtype_size(x_dtype), plan.variant) * 8;
     if (plan.path == kSplitGeneric && p.L > 1) return (size_t)(n * 4);
     return 0;
 }
@@ -801,6 +1058,27 @@ static hipError_t launch_typed(const SplitParams &p, const SplitPlan &plan, hipS
     switch (plan.path) {
     case kSplitRows: return launch_rows<XT, ST>(p, plan.variant, st);
     case kSplitStrip: return launch_strip<XT, ST>(p, plan.variant, st);
+    case kSplitCoop: {
+        constexpr int SW = 8 * (16 / (int)sizeof(XT));
+        const int rpl = plan.variant;
+        const int64_t groups = p.batch * ((p.rows + SW - 1) / SW);
+        const int64_t P = coop_members(p.K, rpl);
+        uint64_t *slot = nullptr;
+        if (P > 1) {
+            slot = (uint64_t *)p.resid;
+            const int64_t n = coop_slots(p, (int)sizeof(XT), rpl);
+            const int64_t zb = (n + 255) / 256 < 2048 ? (n + 255) / 256 : 2048;
+            hipLaunchKernelGGL(zero_u64_kernel, dim3((unsigned)zb), dim3(256), 0, st, slot, n);
+            hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
+        const dim3 grid((unsigned)(groups * P)), block(kCoopNT);
+        if (rpl == 16) hipLaunchKernelGGL((split_coop_kernel<XT, ST, 16>), grid, block, 0, st, p, slot, (int)P);
+        else if constexpr (sizeof(XT) == 8) {
+            hipLaunchKernelGGL((split_coop_kernel<XT, ST, 32>), grid, block, 0, st, p, slot, (int)P);
+        } else return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
     case kSplitTransposeRows: {
         XT *T = (XT *)p.resid;   // workspace [batch, rows, K]
         const int64_t tiles = p.batch * ((p.rows + 63) / 64) * ((p.K + 63) / 64);

@@ -118,19 +118,27 @@ def test_split_workspace_narrow_inputs():
     assert nb.value == 0
 
 
-def test_split_workspace_zero_on_resident_paths():
+def test_split_workspace_per_path():
     from ozaki_triton_amd import _lib
     L = _lib.load()
     nb = ctypes.c_size_t(123)
     K, M, N = 8192, 8192, 8192
     sl = _lib.i64arr([4 * M * K, M * K, K, 1])
-    # A rows (K-contiguous)
+    # A rows (K-contiguous): row-resident, no workspace
     assert L.ozk_split_workspace_bytes(_lib.OZK_F64, 1, M, K, _lib.i64arr([M * K, K, 1]), 4,
                                        _lib.OZK_I8, sl, ctypes.byref(nb)) == 0
     assert nb.value == 0
-    # B^T view (rows contiguous)
+    # B^T view (rows contiguous): column groups of 16 fp64 columns cut into
+    # K chunks of 1024 rows exchange one 8-byte maximum per column, level and
+    # chunk: 512 groups x 4 levels x 8 chunks x 16 columns x 8 bytes
     assert L.ozk_split_workspace_bytes(_lib.OZK_F64, 1, N, K, _lib.i64arr([K * N, 1, N]), 4,
                                        _lib.OZK_I8, sl, ctypes.byref(nb)) == 0
+    assert nb.value == 512 * 4 * 8 * 16 * 8
+    # one chunk (K <= 512 for fp32, 32 columns per group): nothing to exchange
+    Ks = 512
+    sls = _lib.i64arr([2 * N * Ks, N * Ks, Ks, 1])
+    assert L.ozk_split_workspace_bytes(_lib.OZK_F32, 1, N, Ks, _lib.i64arr([Ks * N, 1, N]), 2,
+                                       _lib.OZK_F16, sls, ctypes.byref(nb)) == 0
     assert nb.value == 0
     # a column longer than the resident strip holds is transposed into the
     # workspace first (config 5: fp32, K = 65536)
@@ -266,14 +274,17 @@ def test_matmul_abi_layout_and_errors():
     b = _lib.i64arr([K * N, N, 1])
     assert L.ozk_matmul_workspace_bytes(_lib.OZK_F64, 1, M, N, K, a, b, 4, _lib.OZK_I8,
                                         ctypes.byref(nb)) == 0
-    assert nb.value == 2 * (4 * M * K + 4 * M * 4)          # resident paths: no scratch
+    # the split of B^T exchanges column maxima through the split scratch:
+    # 512 column groups x 4 levels x 8 K chunks x 16 columns x 8 bytes
+    assert nb.value == 2 * (4 * M * K + 4 * M * 4) + 512 * 4 * 8 * 16 * 8
     # broadcast B over a batch of 16 (stride 0): B is split once
     Mb, Kb, Nb = 1024, 2048, 1024
     a16 = _lib.i64arr([Mb * Kb, Kb, 1])
     b0 = _lib.i64arr([0, Nb, 1])
     assert L.ozk_matmul_workspace_bytes(_lib.OZK_F64, 16, Mb, Nb, Kb, a16, b0, 3, _lib.OZK_F16,
                                         ctypes.byref(nb)) == 0
-    assert nb.value == 16 * 3 * Mb * Kb * 2 + 16 * 3 * Mb * 4 + 3 * Nb * Kb * 2 + 3 * Nb * 4
+    assert nb.value == (16 * 3 * Mb * Kb * 2 + 16 * 3 * Mb * 4 + 3 * Nb * Kb * 2 + 3 * Nb * 4
+                        + 64 * 3 * 4 * 16 * 8)      # B: 64 groups x 3 levels x 4 chunks
     # errors: alpha < 1, K = 0 (log2(0)), too many splits, bad dtype
     assert L.ozk_matmul_workspace_bytes(_lib.OZK_F32, 1, 4, 4, 1 << 30, a, b, 2, _lib.OZK_F16,
                                         ctypes.byref(nb)) == _lib.OZK_ERR_ALPHA

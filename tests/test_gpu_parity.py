@@ -52,14 +52,39 @@ def test_split_rows_path(oracle, gpu, xdt, sdt, L, rows, K):
 @pytest.mark.parametrize("xdt,sdt", COMBOS)
 @pytest.mark.parametrize("L", [1, 3, 4])
 @pytest.mark.parametrize("N,K", [(8, 256), (40, 1000), (96, 2048), (24, 8192), (16, 16000)])
-def test_split_strip_path(oracle, gpu, xdt, sdt, L, N, K):
-    """B's columns through the transposed view (rows contiguous)."""
+@pytest.mark.parametrize("kernel", ["coop", "strip"])
+def test_split_strip_path(oracle, gpu, xdt, sdt, L, N, K, kernel, monkeypatch):
+    """B's columns through the transposed view (rows contiguous): the
+    cooperative column-group kernel (the default) and the one-load-wide strip
+    kernel."""
     import ozaki_triton_amd as ozk
+    if kernel != "coop":
+        monkeypatch.setenv("OZK_SPLIT_KERNEL", kernel)
     g = torch.Generator().manual_seed(N * K + L + 1)
     B = torch.randn(2, K, N, generator=g, dtype=torch.float64)
     B = B * torch.pow(2.0, torch.randint(-8, 9, (2, 1, N), generator=g).double())
     Bd = B.to(xdt).to(gpu)
-    _check_split(oracle, ozk, Bd.transpose(-1, -2), L, sdt, f"strip {xdt} {sdt} L{L} {N}x{K}")
+    _check_split(oracle, ozk, Bd.transpose(-1, -2), L, sdt,
+                 f"{kernel} {xdt} {sdt} L{L} {N}x{K}")
+
+
+@pytest.mark.parametrize("xdt,sdt", COMBOS)
+@pytest.mark.parametrize("batch,N,K,L", [(2, 264, 8192, 4), (1, 72, 16384, 3), (1, 40, 32768, 2),
+                                         (3, 48, 4100, 2), (1, 256, 8192, 4), (2, 128, 2048, 3)])
+def test_split_coop_groups(oracle, gpu, xdt, sdt, batch, N, K, L):
+    """The cooperative column split at full length: up to 32 workgroups per
+    column group (the planner's limit: fp64 at K = 32768, fp32 at K = 16384;
+    fp32 at K = 32768 goes to the transpose path), a ragged last group and a
+    ragged last K chunk, batched operands, per-column exponents and
+    outliers."""
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(batch * N * K + L)
+    B = torch.randn(batch, K, N, generator=g, dtype=torch.float64)
+    B = B * torch.pow(2.0, torch.randint(-8, 9, (batch, 1, N), generator=g).double())
+    B[torch.rand(batch, K, N, generator=g) < 0.001] *= 1e4
+    B[:, :, 5] = 0.0                                   # a zero column
+    Bd = B.to(xdt).to(gpu)
+    _check_split(oracle, ozk, Bd.transpose(-1, -2), L, sdt, f"coop {xdt} {sdt} b{batch} {N}x{K}")
 
 
 @pytest.mark.parametrize("xdt,sdt", COMBOS)
@@ -322,10 +347,12 @@ def test_ring_kernel_dtypes(oracle, gpu, L, sdt, out, monkeypatch):
 
 
 @pytest.mark.parametrize("xdt,sdt", COMBOS)
-def test_split_transpose_path(oracle, gpu, xdt, sdt):
-    """Column splits (B^T view) whose K exceeds the resident strip: transposed
-    into the workspace, then the row kernel (config 5's B is 65536 long)."""
+def test_split_transpose_path(oracle, gpu, xdt, sdt, monkeypatch):
+    """Column splits (B^T view) through the transpose into the workspace and
+    the row kernel (the path for columns longer than the cooperative kernel
+    takes)."""
     import ozaki_triton_amd as ozk
+    monkeypatch.setenv("OZK_SPLIT_KERNEL", "transpose")
     g = torch.Generator().manual_seed(11)
     K = 20000 if xdt == torch.float64 else 65536
     B = torch.randn(1, K, 40, generator=g, dtype=torch.float64)
