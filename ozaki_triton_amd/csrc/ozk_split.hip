@@ -40,14 +40,15 @@
 //                       view), 128-byte row segments wide, cut along K over
 //                       several workgroups that exchange the level maxima
 //                       through the workspace; X read once, slices written
-//                       once (the default for columns up to 32 K chunks).
-//   split_strip_kernel  column-strip-resident, for row-contiguous operands.
-//                       A workgroup owns the VEC adjacent columns one 16-byte
-//                       load covers, for all K; each lane holds 4 consecutive
-//                       k of every column so that int8 / fp16 slices leave as
-//                       4-/8-byte stores along K.  Kept as a forced
-//                       alternative (OZK_SPLIT_KERNEL=strip): its 16-byte row
-//                       pieces touch a cache line per 16 bytes read.
+//                       once (the default for columns of 64 KB and more, up
+//                       to 32 K chunks).
+//   split_strip_kernel  column-strip-resident, for row-contiguous operands
+//                       with columns under 64 KB.  A workgroup owns the VEC
+//                       adjacent columns one 16-byte load covers, for all K;
+//                       each lane holds 4 consecutive k of every column so that
+//                       int8 / fp16 slices leave as 4-/8-byte stores along K.
+//                       Its 16-byte row pieces touch a cache line per 16 bytes
+//                       read, which longer columns pay for.
 //   transpose_kernel    + split_rows_kernel: columns longer than the
 //                       cooperative kernel takes, transposed into the
 //                       workspace first.
@@ -534,6 +535,7 @@ __global__ __launch_bounds__(NT) void split_strip_kernel(SplitParams p) {
 // ---------------------------------------------------------------------------
 constexpr int kCoopNT = 256;
 constexpr int kCoopMaxP = 32;
+constexpr int64_t kCoopMinColumnBytes = 64 * 1024;
 constexpr int kCoopSpin = 1 << 16;
 constexpr uint64_t kCoopTag = 1ull << 32;               // high word of a published maximum
 
@@ -893,11 +895,10 @@ static const StripCfg kStripCfgs[] = {
 };
 static const int kNumStripCfgs = sizeof(kStripCfgs) / sizeof(kStripCfgs[0]);
 
-// rows per lane of split_coop_kernel (fp64 columns longer than 4096 take
-// 32, which halves the workgroups that exchange maxima), the members (K
-// chunks of 32 * rpl rows) of a column group, and the workspace: the
-// published maxima [groups][L][P][SW], 8 bytes each (none for P = 1)
-static int coop_rpl(int64_t K, int xsz) { return (xsz == 8 && K > 4096) ? 32 : 16; }
+// rows per lane of split_coop_kernel (64 values per lane: 32 rows of fp64,
+// 16 of fp32), the members (K chunks of 32 * rpl rows) of a column group, and
+// the workspace: the published maxima [groups][L][P][SW], 8 bytes each (none
+// for P = 1)
 static int64_t coop_members(int64_t K, int rpl) {
     const int64_t ch = (int64_t)kCoopNT / 8 * rpl;
     return K <= 0 ? 1 : (K + ch - 1) / ch;
@@ -953,15 +954,21 @@ SplitPlan plan_split(const SplitParams &p, int x_dtype, int slice_dtype) {
         }
     }
     const int vec = 16 / xsz;
-    // OZK_SPLIT_KERNEL=strip|transpose|generic steers column operands off the
-    // default (tests cover every path); a path whose requirements fail is not taken
+    // OZK_SPLIT_KERNEL=coop|strip|transpose|generic steers column operands off
+    // the default (tests cover every path); a path whose requirements fail is
+    // not taken
     const char *env = getenv("OZK_SPLIT_KERNEL");
     auto forced = [&](const char *name) { return env && strcmp(env, name) == 0; };
     const bool cols_ok = k4 && slice_ok && p.xs_r == 1 && p.rows % vec == 0 && aligned(p.X, 16) &&
                          (p.xs_k * xsz) % 16 == 0 && (p.xs_b * xsz) % 16 == 0;
-    if (cols_ok && !forced("strip") && !forced("transpose") && !forced("generic") &&
-        coop_members(p.K, coop_rpl(p.K, xsz)) <= kCoopMaxP)
-        return {kSplitCoop, coop_rpl(p.K, xsz)};
+    // columns of 64 KB and more: the cooperative kernel (the strip kernel's
+    // 16-byte row pieces cost more than the exchange from there on; measured
+    // over K = 1024..16384, N = 1024..8192, fp64 / fp32); OZK_SPLIT_KERNEL=coop
+    // takes it for any length it holds
+    const bool coop_fits = cols_ok && coop_members(p.K, 64 / vec) <= kCoopMaxP;
+    const bool other = forced("strip") || forced("transpose") || forced("generic");
+    if (coop_fits && (forced("coop") || (!other && p.K * xsz >= kCoopMinColumnBytes)))
+        return {kSplitCoop, 64 / vec};
     if (cols_ok && !forced("transpose") && !forced("generic")) {
         for (int i = 0; i < kNumStripCfgs; ++i) {
             const StripCfg &c = kStripCfgs[i];
@@ -1073,10 +1080,9 @@ static hipError_t launch_typed(const SplitParams &p, const SplitPlan &plan, hipS
             if (e != hipSuccess) return e;
         }
         const dim3 grid((unsigned)(groups * P)), block(kCoopNT);
-        if (rpl == 16) hipLaunchKernelGGL((split_coop_kernel<XT, ST, 16>), grid, block, 0, st, p, slot, (int)P);
-        else if constexpr (sizeof(XT) == 8) {
-            hipLaunchKernelGGL((split_coop_kernel<XT, ST, 32>), grid, block, 0, st, p, slot, (int)P);
-        } else return hipErrorInvalidValue;
+        constexpr int RPL = 64 / (16 / (int)sizeof(XT));
+        if (rpl != RPL) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((split_coop_kernel<XT, ST, RPL>), grid, block, 0, st, p, slot, (int)P);
         return hipGetLastError();
     }
     case kSplitTransposeRows: {

@@ -128,13 +128,13 @@ def test_split_workspace_per_path():
     assert L.ozk_split_workspace_bytes(_lib.OZK_F64, 1, M, K, _lib.i64arr([M * K, K, 1]), 4,
                                        _lib.OZK_I8, sl, ctypes.byref(nb)) == 0
     assert nb.value == 0
-    # B^T view (rows contiguous): column groups of 16 fp64 columns cut into
-    # K chunks of 1024 rows exchange one 8-byte maximum per column, level and
-    # chunk: 512 groups x 4 levels x 8 chunks x 16 columns x 8 bytes
+    # B^T view (rows contiguous, 64 KB columns): column groups of 16 fp64
+    # columns cut into K chunks of 1024 rows exchange one 8-byte maximum per
+    # column, level and chunk: 512 groups x 4 levels x 8 chunks x 16 columns x 8 bytes
     assert L.ozk_split_workspace_bytes(_lib.OZK_F64, 1, N, K, _lib.i64arr([K * N, 1, N]), 4,
                                        _lib.OZK_I8, sl, ctypes.byref(nb)) == 0
     assert nb.value == 512 * 4 * 8 * 16 * 8
-    # one chunk (K <= 512 for fp32, 32 columns per group): nothing to exchange
+    # short columns (under 64 KB) take the strip kernel: no workspace
     Ks = 512
     sls = _lib.i64arr([2 * N * Ks, N * Ks, Ks, 1])
     assert L.ozk_split_workspace_bytes(_lib.OZK_F32, 1, N, Ks, _lib.i64arr([Ks * N, 1, N]), 2,
@@ -283,8 +283,7 @@ def test_matmul_abi_layout_and_errors():
     b0 = _lib.i64arr([0, Nb, 1])
     assert L.ozk_matmul_workspace_bytes(_lib.OZK_F64, 16, Mb, Nb, Kb, a16, b0, 3, _lib.OZK_F16,
                                         ctypes.byref(nb)) == 0
-    assert nb.value == (16 * 3 * Mb * Kb * 2 + 16 * 3 * Mb * 4 + 3 * Nb * Kb * 2 + 3 * Nb * 4
-                        + 64 * 3 * 4 * 16 * 8)      # B: 64 groups x 3 levels x 4 chunks
+    assert nb.value == 16 * 3 * Mb * Kb * 2 + 16 * 3 * Mb * 4 + 3 * Nb * Kb * 2 + 3 * Nb * 4
     # errors: alpha < 1, K = 0 (log2(0)), too many splits, bad dtype
     assert L.ozk_matmul_workspace_bytes(_lib.OZK_F32, 1, 4, 4, 1 << 30, a, b, 2, _lib.OZK_F16,
                                         ctypes.byref(nb)) == _lib.OZK_ERR_ALPHA

@@ -55,11 +55,10 @@ def test_split_rows_path(oracle, gpu, xdt, sdt, L, rows, K):
 @pytest.mark.parametrize("kernel", ["coop", "strip"])
 def test_split_strip_path(oracle, gpu, xdt, sdt, L, N, K, kernel, monkeypatch):
     """B's columns through the transposed view (rows contiguous): the
-    cooperative column-group kernel (the default) and the one-load-wide strip
-    kernel."""
+    cooperative column-group kernel and the one-load-wide strip kernel, each
+    forced (the planner picks by column length)."""
     import ozaki_triton_amd as ozk
-    if kernel != "coop":
-        monkeypatch.setenv("OZK_SPLIT_KERNEL", kernel)
+    monkeypatch.setenv("OZK_SPLIT_KERNEL", kernel)
     g = torch.Generator().manual_seed(N * K + L + 1)
     B = torch.randn(2, K, N, generator=g, dtype=torch.float64)
     B = B * torch.pow(2.0, torch.randint(-8, 9, (2, 1, N), generator=g).double())
@@ -71,13 +70,14 @@ def test_split_strip_path(oracle, gpu, xdt, sdt, L, N, K, kernel, monkeypatch):
 @pytest.mark.parametrize("xdt,sdt", COMBOS)
 @pytest.mark.parametrize("batch,N,K,L", [(2, 264, 8192, 4), (1, 72, 16384, 3), (1, 40, 32768, 2),
                                          (3, 48, 4100, 2), (1, 256, 8192, 4), (2, 128, 2048, 3)])
-def test_split_coop_groups(oracle, gpu, xdt, sdt, batch, N, K, L):
-    """The cooperative column split at full length: up to 32 workgroups per
-    column group (the planner's limit: fp64 at K = 32768, fp32 at K = 16384;
-    fp32 at K = 32768 goes to the transpose path), a ragged last group and a
-    ragged last K chunk, batched operands, per-column exponents and
-    outliers."""
+def test_split_coop_groups(oracle, gpu, xdt, sdt, batch, N, K, L, monkeypatch):
+    """The cooperative column split (forced; the default from 64 KB columns)
+    at full length: up to 32 workgroups per column group (its limit: fp64 at
+    K = 32768, fp32 at K = 16384; fp32 at K = 32768 falls to the transpose
+    path), a ragged last group and a ragged last K chunk, batched operands,
+    per-column exponents and outliers."""
     import ozaki_triton_amd as ozk
+    monkeypatch.setenv("OZK_SPLIT_KERNEL", "coop")
     g = torch.Generator().manual_seed(batch * N * K + L)
     B = torch.randn(batch, K, N, generator=g, dtype=torch.float64)
     B = B * torch.pow(2.0, torch.randint(-8, 9, (batch, 1, N), generator=g).double())
