@@ -689,6 +689,12 @@ __global__ __launch_bounds__(kCoopNT) void split_coop_kernel(SplitParams p, uint
                 for (int u = 0; u < VEC; ++u)
                     Store4<ST>::run(p.slices, sbase + u * p.ss_r + k0, qv[u]);
             }
+            // the residuals here, not at their first use (the level-1 maximum):
+            // sunk there, every input and every slice value are live at once
+#pragma unroll
+            for (int dk = 0; dk < 4; ++dk)
+#pragma unroll
+                for (int u = 0; u < VEC; ++u) asm volatile("" : "+v"(w[j][dk][u]));
         }
     }
     for (int l = 1; l < p.L; ++l) {
