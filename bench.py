@@ -44,6 +44,9 @@ CONFIGS = {
     "C3": ("float64", "int8", 4, (8192, 8192), (8192, 8192), 2, "exp8"),
     "C4": ("float64", "float16", 3, (16, 1024, 2048), (2048, 1024), 3, "normal"),
     "C5": ("float32", "int8", 3, (1024, 65536), (65536, 1024), 4, "outliers"),
+    # one GPU's share of C3 on a 2 x 2 output-stationary grid (no exchange:
+    # this GPU's A row-block and B column-block)
+    "C3s": ("float64", "int8", 4, (4096, 8192), (8192, 4096), 2, "exp8"),
 }
 
 
@@ -308,6 +311,8 @@ def main():
                 "C3": "FP64->INT8 num_splits=4, M=N=K=8192, batch 1",
                 "C4": "FP64->FP16 num_splits=3, A[16,1024,2048] x B[2048,1024] (broadcast)",
                 "C5": "FP32->INT8 num_splits=3, M=N=1024, K=65536, 1% outliers x1e4",
+                "C3s": "FP64->INT8 num_splits=4, A[4096,8192] x B[8192,4096]: one GPU's share "
+                       "of C3 on a 2x2 grid",
             }[args.config],
             "input_dtype": xdt, "slice_dtype": sdt, "num_splits": L,
             "M": M, "N": N, "K": K, "batch": batch, "seed": cfg[5],
