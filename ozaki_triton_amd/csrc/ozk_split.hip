@@ -544,7 +544,8 @@ __global__ __launch_bounds__(256) void zero_u64_kernel(uint64_t *p, int64_t n) {
 }
 
 template <typename XT, typename ST, int RPL>
-__global__ __launch_bounds__(kCoopNT) void split_coop_kernel(SplitParams p, uint64_t *slot, int P) {
+__global__ __launch_bounds__(kCoopNT) void split_coop_kernel(SplitParams p, uint64_t *slot, int P,
+                                                             uint32_t want_tag, int spin_limit) {
     constexpr int NT = kCoopNT, NG = RPL / 4;
     constexpr int VEC = 16 / (int)sizeof(XT);
     constexpr int SW = 8 * VEC;          // columns per group
@@ -626,14 +627,14 @@ __global__ __launch_bounds__(kCoopNT) void split_coop_kernel(SplitParams p, uint
                     if (i < nw && !((seen >> n) & 1)) {
                         const uint64_t w64 =
                             __hip_atomic_load(sl + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        if ((w64 >> 32) == (kCoopTag >> 32)) {
+                        if ((uint32_t)(w64 >> 32) == want_tag) {
                             seen |= 1ull << n;
                             q = fmaxf(q, __uint_as_float((uint32_t)w64));
                         }
                     }
                 }
                 if (__all(seen == want)) break;
-                if (it == kCoopSpin) {
+                if (it == spin_limit) {
                     if (lane == 0) bad = 1;
                     break;
                 }
@@ -1088,7 +1089,14 @@ static hipError_t launch_typed(const SplitParams &p, const SplitPlan &plan, hipS
         const dim3 grid((unsigned)(groups * P)), block(kCoopNT);
         constexpr int RPL = 64 / (16 / (int)sizeof(XT));
         if (rpl != RPL) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((split_coop_kernel<XT, ST, RPL>), grid, block, 0, st, p, slot, (int)P);
+        // OZK_SPLIT_COOP_TIMEOUT=1 (tests only): every wait looks for a tag that
+        // is never written and gives up after 8 polls, so the timeout path runs
+        // and the multi-chunk scales come out NaN, with no wait longer than that
+        const char *tmo = getenv("OZK_SPLIT_COOP_TIMEOUT");
+        const bool force_timeout = tmo && strcmp(tmo, "1") == 0;
+        hipLaunchKernelGGL((split_coop_kernel<XT, ST, RPL>), grid, block, 0, st, p, slot, (int)P,
+                           (uint32_t)(kCoopTag >> 32) + (force_timeout ? 1u : 0u),
+                           force_timeout ? 8 : kCoopSpin);
         return hipGetLastError();
     }
     case kSplitTransposeRows: {

@@ -346,6 +346,28 @@ def test_ring_kernel_dtypes(oracle, gpu, L, sdt, out, monkeypatch):
         assert_bitwise_equal(C, to_np(ozk.cross_gemm(*args)), f"ring vs pair L{L} {sdt} {out}")
 
 
+@pytest.mark.parametrize("xdt", [torch.float64, torch.float32])
+def test_split_coop_wait_timeout(oracle, gpu, xdt, monkeypatch):
+    """The cooperative split's bounded wait: forced from the host to look for a
+    tag no member writes (8 polls), every wait runs out, the kernel still
+    finishes, and the scales of the exchanged levels come out NaN instead of
+    the call hanging.  Afterwards the normal path gives the oracle's bits
+    again."""
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(21)
+    K, N, L = 4096, 64, 3
+    B = torch.randn(1, K, N, generator=g, dtype=torch.float64).to(xdt).to(gpu)
+    BT = B.transpose(-1, -2)
+    alpha = _alpha(ozk, K, torch.int8)
+    monkeypatch.setenv("OZK_SPLIT_KERNEL", "coop")
+    monkeypatch.setenv("OZK_SPLIT_COOP_TIMEOUT", "1")
+    sl, sc = ozk.split_matrix(BT, L, alpha, torch.int8)
+    torch.cuda.synchronize()
+    assert torch.isnan(sc).all(), "every exchanged level's scale should be NaN after the timeout"
+    monkeypatch.delenv("OZK_SPLIT_COOP_TIMEOUT")
+    _check_split(oracle, ozk, BT, L, torch.int8, f"coop after timeout {xdt}")
+
+
 @pytest.mark.parametrize("xdt,sdt", COMBOS)
 def test_split_transpose_path(oracle, gpu, xdt, sdt, monkeypatch):
     """Column splits (B^T view) through the transpose into the workspace and
