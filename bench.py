@@ -1,6 +1,6 @@
 """Benchmark of the Ozaki-scheme hot path on one MI355X.
 
-Default workload (BASELINE.json metric, config 3): FP64 -> INT8 slices,
+Default workload (the headline metric, configuration C3): FP64 -> INT8 slices,
 num_splits = 4, M = N = K = 8192, batch 1, A and B entries N(0,1) * 2^e with e
 drawn per row of A / per column of B from Uniform-int[-8, 8]
 (torch.Generator seed 2).  A "step" is one ozaki_matmul call (split B, split A,
@@ -209,7 +209,9 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build has no "
-              "multi-GPU path; the sharding design is described in DESIGN.md", file=sys.stderr)
+              "multi-GPU path (the output shards by blocks of A's rows and B's columns with no "
+              "reduction; --config C3s measures one GPU's share of C3 on a 2x2 grid)",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -74,7 +74,7 @@ def fp16_cross_bound(oracle_np, A_sl, B_slT, sa, sb):
 
 
 def c3_like(shape_a, shape_b, seed, dtype=torch.float64, exp_range=8):
-    """Inputs of BASELINE config 3's distribution: N(0,1) * 2^e with e drawn per
+    """Inputs of the FP64 -> INT8 benchmark's (C3) distribution: N(0,1) * 2^e with e drawn per
     row of A / per column of B from Uniform-int[-exp_range, exp_range]."""
     g = torch.Generator().manual_seed(seed)
     A = torch.randn(*shape_a, generator=g, dtype=torch.float64)

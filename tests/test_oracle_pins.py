@@ -21,7 +21,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
     (4096, "float16", "float32", 5),     # config 2
     (8192, "int8", "int32", 7),          # config 3 (capped by int8's 7 bits)
     (2048, "float16", "float32", 6),     # config 4
-    (65536, "int8", "int32", 7),         # config 5: floor((31-16)/2) = 7 (BASELINE.json)
+    (65536, "int8", "int32", 7),         # config 5: floor((31-16)/2) = 7
     (1 << 20, "int8", "int32", 5),       # (31-20)/2 = 5.5 -> 5
     (1 << 21, "float16", "float32", 1),  # (23-21)/2 = 1
     (1, "float32", "float32", 11),       # 23/2 = 11.5 -> 11 < 23
