@@ -331,8 +331,9 @@ def main():
             "avg_ms": round(t_cross, 4),
         },
         "split": {
-            "kernels": "split_rows_kernel (A) + split_coop_kernel, or transpose_kernel + "
-                       "split_rows_kernel for columns longer than 16384 fp32 / 32768 fp64 (B)",
+            "kernels": "split_rows_kernel, or split_rows_coop_kernel for rows over 16384 (A); "
+                       "split_coop_kernel for columns of 64 KB up to 32 K chunks, "
+                       "split_strip_kernel below, transpose_kernel + a row kernel above (B)",
             "bound": "hbm",
             "bytes": split_bytes,
             "achieved": round(split_gbs, 1),

@@ -36,6 +36,9 @@
 //                       64*GW lanes owns one row; the row stays in VGPRs across
 //                       all levels, so X is read from HBM once and each slice
 //                       written once.
+//   split_rows_coop_kernel  rows longer than 16384: K chunks of a row in
+//                       separate workgroups that exchange the level maxima
+//                       through the workspace.
 //   split_coop_kernel   column groups of row-contiguous operands (the B^T
 //                       view), 128-byte row segments wide, cut along K over
 //                       several workgroups that exchange the level maxima
@@ -49,9 +52,8 @@
 //                       int8 / fp16 slices leave as 4-/8-byte stores along K.
 //                       Its 16-byte row pieces touch a cache line per 16 bytes
 //                       read, which longer columns pay for.
-//   transpose_kernel    + split_rows_kernel: columns longer than the
-//                       cooperative kernel takes, transposed into the
-//                       workspace first.
+//   transpose_kernel    + a row kernel: columns longer than the cooperative
+//                       kernel takes, transposed into the workspace first.
 //   split_generic_kernel any strides and any K: one workgroup per row,
 //                       multi-pass over K with an fp32 residual in workspace
 //                       (the reference's own traffic pattern).
@@ -536,6 +538,11 @@ __global__ __launch_bounds__(NT) void split_strip_kernel(SplitParams p) {
 constexpr int kCoopNT = 256;
 constexpr int kCoopMaxP = 32;
 constexpr int64_t kCoopMinColumnBytes = 64 * 1024;
+// rows kernel shared by workgroups: 256 lanes, 64 (fp32) or 32 (fp64) values
+// per lane, for rows longer than 16384 elements, at most 64 chunks
+constexpr int kRowsCoopVariant = 100;
+constexpr int64_t kRowsCoopMinK = 16384;
+constexpr int kRowsCoopMaxP = 64;
 constexpr int kCoopSpin = 1 << 16;
 constexpr uint64_t kCoopTag = 1ull << 32;               // high word of a published maximum
 
@@ -732,6 +739,130 @@ __global__ __launch_bounds__(kCoopNT) void split_coop_kernel(SplitParams p, uint
 }
 
 // ---------------------------------------------------------------------------
+// Row split shared by workgroups, for K-contiguous rows too long for one
+// workgroup per row to keep a CU busy (rows over 16384 elements: one
+// 1024-lane workgroup per CU, whose loads then never overlap another's
+// arithmetic).  Workgroup g takes K chunk g % P of row g / P: CHR = 4 * NC *
+// 64 * GW elements, laid out per lane as in split_rows_kernel.  Per level the
+// workgroup's row maximum is combined over the P chunks through tagged words as
+// in split_coop_kernel: slot[row][level][P], one word per chunk (lane i of
+// wave 0 polls chunk i's word; P <= 64).
+// ---------------------------------------------------------------------------
+template <typename XT, typename ST, int GW, int NC>
+__global__ __launch_bounds__(64 * GW) void split_rows_coop_kernel(SplitParams p, uint64_t *slot,
+                                                                  int P, uint32_t want_tag,
+                                                                  int spin_limit) {
+    constexpr int G = 64 * GW;
+    constexpr int NE = 4 * NC;
+    constexpr int CHR = NE * G;
+    __shared__ float red[2][1][GW];
+    __shared__ float fin[2];
+    __shared__ int bad;
+
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int64_t g = blockIdx.x;
+    const int member = (int)(g % P);
+    const int64_t grow = g / P;
+    const int64_t b = grow / p.rows, r = grow % p.rows;
+    const int64_t kbase = (int64_t)member * CHR;
+    const int64_t kleft = p.K - kbase;   // this chunk's elements inside the row (> 0)
+    const XT *xrow = (const XT *)p.X + b * p.xs_b + r * p.xs_r + kbase;
+    const int64_t srow = b * p.ss_b + r * p.ss_r + kbase;
+    float *srow_scale = p.scales + b * p.cs_b + r * p.cs_r;
+
+    XT v[NE];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int64_t e0 = ((int64_t)c * G + t) * 4;
+        XT tmp[4];
+        if (e0 < kleft) {
+            load4(xrow + e0, tmp);
+        } else {
+            tmp[0] = tmp[1] = tmp[2] = tmp[3] = (XT)0;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[c * 4 + u] = tmp[u];
+    }
+    if (t == 0) bad = 0;
+
+    // the row's maximum at level l (wave-uniform)
+    auto rmax = [&](float m, int l) {
+        m = row_max<GW, 1>(m, red, l & 1, 0, t);
+        if (P > 1) {
+            if (wave == 0) {
+                uint64_t *sl = slot + (grow * p.L + l) * (int64_t)P;
+                if (lane == 0)
+                    __hip_atomic_store(sl + member, kCoopTag | __float_as_uint(m), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                bool seen = lane >= P;
+                float q = 0.0f;
+                for (int it = 0;; ++it) {
+                    if (!seen) {
+                        const uint64_t w64 =
+                            __hip_atomic_load(sl + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        if ((uint32_t)(w64 >> 32) == want_tag) {
+                            seen = true;
+                            q = __uint_as_float((uint32_t)w64);
+                        }
+                    }
+                    if (__all(seen)) break;
+                    if (it == spin_limit) {
+                        if (lane == 0) bad = 1;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                q = wave_max(q);
+                if (lane == 0) fin[l & 1] = q;
+            }
+            lds_barrier();
+            m = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(fin[l & 1])));
+        }
+        return m;
+    };
+    auto store_scale = [&](int l, const LevelScale &c) {
+        if (member == 0 && t == 0) srow_scale[l * p.cs_l] = bad ? __int_as_float(0x7fc00000) : c.s;
+    };
+
+    float w[NE];
+    {
+        float m = 0.0f;
+#pragma unroll
+        for (int e = 0; e < NE; ++e) m = fmaxf(m, absf(v[e]));
+        const LevelScale c = level_scale(rmax(m, 0), p.alpha);
+        store_scale(0, c);
+#pragma unroll
+        for (int ch = 0; ch < NC; ++ch) {
+            const int64_t e0 = ((int64_t)ch * G + t) * 4;
+            uint32_t qv[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                qv[u] = Quant<ST, Modes<XT>::first>::run(v[ch * 4 + u], c, &w[ch * 4 + u]);
+            if (e0 < kleft) Store4<ST>::run(p.slices, srow + e0, qv);
+            // the residuals here, not at their first use (see split_coop_kernel)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) asm volatile("" : "+v"(w[ch * 4 + u]));
+        }
+    }
+    for (int l = 1; l < p.L; ++l) {
+        float m = 0.0f;
+#pragma unroll
+        for (int e = 0; e < NE; ++e) m = fmaxf(m, fabsf(w[e]));
+        const LevelScale c = level_scale(rmax(m, l), p.alpha);
+        store_scale(l, c);
+#pragma unroll
+        for (int ch = 0; ch < NC; ++ch) {
+            const int64_t e0 = ((int64_t)ch * G + t) * 4;
+            uint32_t qv[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                qv[u] = Quant<ST, Modes<XT>::rest>::run(w[ch * 4 + u], c, &w[ch * 4 + u]);
+            if (e0 < kleft) Store4<ST>::run(p.slices, srow + l * p.ss_l + e0, qv);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Generic split: one workgroup of 256 lanes per row, any strides, any K.
 // Level l reads src (X for l = 0, else the fp32 residual workspace) twice:
 // once for the row max, once to quantise; lane t always touches k = t + 256*i,
@@ -918,6 +1049,16 @@ static int64_t coop_slots(const SplitParams &p, int xsz, int rpl) {
     return groups * p.L * P * sw;
 }
 
+static int64_t rows_coop_chunk(int xsz) { return xsz == 8 ? 4 * 8 * 256 : 4 * 16 * 256; }
+static int64_t rows_coop_members(int64_t K, int xsz) {
+    const int64_t ch = rows_coop_chunk(xsz);
+    return K <= 0 ? 1 : (K + ch - 1) / ch;
+}
+static size_t rows_coop_slot_bytes(const SplitParams &p, int xsz) {
+    const int64_t P = rows_coop_members(p.K, xsz);
+    return P > 1 ? (size_t)(p.batch * p.rows * p.L * P) * 8 : 0;
+}
+
 static bool aligned(const void *ptr, int64_t bytes) {
     return ((uintptr_t)ptr % (uintptr_t)bytes) == 0;
 }
@@ -952,8 +1093,17 @@ SplitPlan plan_split(const SplitParams &p, int x_dtype, int slice_dtype) {
     const bool slice_ok = p.ss_k == 1 && aligned(p.slices, 4 * ssz) &&
                           (p.ss_r * ssz) % (4 * ssz) == 0 && (p.ss_l * ssz) % (4 * ssz) == 0 &&
                           (p.ss_b * ssz) % (4 * ssz) == 0;
+    // OZK_SPLIT_KERNEL=coop|strip|transpose|generic steers column operands off
+    // the default, =rows|rowscoop forces one of the two row kernels (tests
+    // cover every path); a path whose requirements fail is not taken
+    const char *env = getenv("OZK_SPLIT_KERNEL");
+    auto forced = [&](const char *name) { return env && strcmp(env, name) == 0; };
+    // long rows: the row kernel shared by workgroups
+    const bool rows_coop = rows_coop_members(p.K, xsz) <= kRowsCoopMaxP &&
+                           (forced("rowscoop") || (!forced("rows") && p.K > kRowsCoopMinK));
     if (k4 && slice_ok && p.xs_k == 1 && aligned(p.X, 16) && (p.xs_r * xsz) % 16 == 0 &&
-        (p.xs_b * xsz) % 16 == 0) {
+        (p.xs_b * xsz) % 16 == 0 && !forced("generic")) {
+        if (rows_coop) return {kSplitRows, kRowsCoopVariant};
         for (int i = 0; i < kNumRowCfgs; ++i) {
             const RowCfg &c = kRowCfgs[i];
             if (x_dtype == 0 && c.nc > 8) continue;
@@ -961,11 +1111,6 @@ SplitPlan plan_split(const SplitParams &p, int x_dtype, int slice_dtype) {
         }
     }
     const int vec = 16 / xsz;
-    // OZK_SPLIT_KERNEL=coop|strip|transpose|generic steers column operands off
-    // the default (tests cover every path); a path whose requirements fail is
-    // not taken
-    const char *env = getenv("OZK_SPLIT_KERNEL");
-    auto forced = [&](const char *name) { return env && strcmp(env, name) == 0; };
     const bool cols_ok = k4 && slice_ok && p.xs_r == 1 && p.rows % vec == 0 && aligned(p.X, 16) &&
                          (p.xs_k * xsz) % 16 == 0 && (p.xs_b * xsz) % 16 == 0;
     // columns of 64 KB and more: the cooperative kernel (the strip kernel's
@@ -986,6 +1131,7 @@ SplitPlan plan_split(const SplitParams &p, int x_dtype, int slice_dtype) {
     // row-contiguous operand with a K too long for a resident strip: transpose
     // into the workspace, then the row kernel (if the row fits)
     if (k4 && slice_ok && p.xs_r == 1 && (p.K * xsz) % 16 == 0 && !forced("generic")) {
+        if (rows_coop) return {kSplitTransposeRows, kRowsCoopVariant};
         for (int i = 0; i < kNumRowCfgs; ++i) {
             const RowCfg &c = kRowCfgs[i];
             if (x_dtype == 0 && c.nc > 8) continue;
@@ -1010,7 +1156,13 @@ size_t split_workspace_bytes(const SplitParams &p, const SplitPlan &plan, int x_
         const SplitPlan inner = converted_plan(p, slice_dtype);
         return (size_t)(n * 4) + split_workspace_bytes(converted_params(p), inner, 1, slice_dtype);
     }
-    if (plan.path == kSplitTransposeRows) return (size_t)(n * dtype_size(x_dtype));
+    if (plan.path == kSplitTransposeRows) {
+        const size_t tb = (size_t)(n * dtype_size(x_dtype));
+        if (plan.variant != kRowsCoopVariant) return tb;
+        return (tb + 255) / 256 * 256 + rows_coop_slot_bytes(p, dtype_size(x_dtype));
+    }
+    if (plan.path == kSplitRows && plan.variant == kRowsCoopVariant)
+        return rows_coop_slot_bytes(p, dtype_size(x_dtype));
     if (plan.path == kSplitCoop)
         return (size_t)coop_slots(p, dtype_size(x_dtype), plan.variant) * 8;
     if (plan.path == kSplitGeneric && p.L > 1) return (size_t)(n * 4);
@@ -1018,7 +1170,33 @@ size_t split_workspace_bytes(const SplitParams &p, const SplitPlan &plan, int x_
 }
 
 template <typename XT, typename ST>
-static hipError_t launch_rows(const SplitParams &p, int v, hipStream_t st) {
+static hipError_t launch_rows_coop(const SplitParams &p, uint64_t *slot, hipStream_t st) {
+    const int xsz = (int)sizeof(XT);
+    const int64_t P = rows_coop_members(p.K, xsz);
+    if (P > 1) {
+        const int64_t n = p.batch * p.rows * p.L * P;
+        const int64_t zb = (n + 255) / 256 < 2048 ? (n + 255) / 256 : 2048;
+        hipLaunchKernelGGL(zero_u64_kernel, dim3((unsigned)zb), dim3(256), 0, st, slot, n);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    const char *tmo = getenv("OZK_SPLIT_COOP_TIMEOUT");   // tests only, as for the columns
+    const bool force_timeout = tmo && strcmp(tmo, "1") == 0;
+    const uint32_t tag = (uint32_t)(kCoopTag >> 32) + (force_timeout ? 1u : 0u);
+    const int spin = force_timeout ? 8 : kCoopSpin;
+    const dim3 grid((unsigned)(p.batch * p.rows * P)), block(256);
+    if constexpr (sizeof(XT) == 8)
+        hipLaunchKernelGGL((split_rows_coop_kernel<XT, ST, 4, 8>), grid, block, 0, st, p, slot,
+                           (int)P, tag, spin);
+    else
+        hipLaunchKernelGGL((split_rows_coop_kernel<XT, ST, 4, 16>), grid, block, 0, st, p, slot,
+                           (int)P, tag, spin);
+    return hipGetLastError();
+}
+
+template <typename XT, typename ST>
+static hipError_t launch_rows(const SplitParams &p, int v, hipStream_t st, uint64_t *slot) {
+    if (v == kRowsCoopVariant) return launch_rows_coop<XT, ST>(p, slot, st);
     const int64_t nrows = p.batch * p.rows;
 #define OZK_ROWS(GW, RPB, NC)                                                               \
     hipLaunchKernelGGL((split_rows_kernel<XT, ST, GW, RPB, NC>),                            \
@@ -1070,7 +1248,7 @@ static hipError_t launch_strip(const SplitParams &p, int v, hipStream_t st) {
 template <typename XT, typename ST>
 static hipError_t launch_typed(const SplitParams &p, const SplitPlan &plan, hipStream_t st) {
     switch (plan.path) {
-    case kSplitRows: return launch_rows<XT, ST>(p, plan.variant, st);
+    case kSplitRows: return launch_rows<XT, ST>(p, plan.variant, st, (uint64_t *)p.resid);
     case kSplitStrip: return launch_strip<XT, ST>(p, plan.variant, st);
     case kSplitCoop: {
         constexpr int SW = 8 * (16 / (int)sizeof(XT));
@@ -1114,7 +1292,10 @@ static hipError_t launch_typed(const SplitParams &p, const SplitPlan &plan, hipS
         q.xs_b = p.rows * p.K;
         q.xs_r = p.K;
         q.xs_k = 1;
-        return launch_rows<XT, ST>(q, plan.variant, st);
+        // the exchange words of the shared row kernel follow the transposed copy
+        const size_t tb = (size_t)(p.batch * p.rows * p.K) * sizeof(XT);
+        return launch_rows<XT, ST>(q, plan.variant, st,
+                                   (uint64_t *)((char *)p.resid + (tb + 255) / 256 * 256));
     }
     default:
         hipLaunchKernelGGL((split_generic_kernel<XT, ST>), dim3((unsigned)(p.batch * p.rows)),

@@ -140,13 +140,20 @@ def test_split_workspace_per_path():
     assert L.ozk_split_workspace_bytes(_lib.OZK_F32, 1, N, Ks, _lib.i64arr([Ks * N, 1, N]), 2,
                                        _lib.OZK_F16, sls, ctypes.byref(nb)) == 0
     assert nb.value == 0
-    # a column longer than the resident strip holds is transposed into the
-    # workspace first (config 5: fp32, K = 65536)
+    # a column longer than the cooperative column kernel takes is transposed
+    # into the workspace first (config 5: fp32, K = 65536); its rows, longer
+    # than 16384, then go to the row kernel shared by 4 workgroups per row,
+    # whose exchange words follow the transposed copy: 1024 rows x 3 levels x
+    # 4 chunks x 8 bytes
     K5, N5 = 65536, 1024
     sl5 = _lib.i64arr([3 * N5 * K5, N5 * K5, K5, 1])
     assert L.ozk_split_workspace_bytes(_lib.OZK_F32, 1, N5, K5, _lib.i64arr([K5 * N5, 1, N5]),
                                        3, _lib.OZK_I8, sl5, ctypes.byref(nb)) == 0
-    assert nb.value == N5 * K5 * 4
+    assert nb.value == N5 * K5 * 4 + N5 * 3 * 4 * 8
+    # and A's rows of config 5 (K-contiguous) need only the exchange words
+    assert L.ozk_split_workspace_bytes(_lib.OZK_F32, 1, N5, K5, _lib.i64arr([K5 * N5, K5, 1]),
+                                       3, _lib.OZK_I8, sl5, ctypes.byref(nb)) == 0
+    assert nb.value == N5 * 3 * 4 * 8
 
 
 def test_cross_gemm_abi_checks_and_workspace():

@@ -41,12 +41,31 @@ def _check_split(oracle, ozk, X3_dev, L, slice_dtype, what):
 @pytest.mark.parametrize("xdt,sdt", COMBOS)
 @pytest.mark.parametrize("L", [1, 2, 4])
 @pytest.mark.parametrize("rows,K", [(5, 256), (64, 1000), (33, 2048), (7, 8192)])
-def test_split_rows_path(oracle, gpu, xdt, sdt, L, rows, K):
+@pytest.mark.parametrize("kernel", ["rows", "rowscoop"])
+def test_split_rows_path(oracle, gpu, xdt, sdt, L, rows, K, kernel, monkeypatch):
+    """K-contiguous rows: the one-workgroup row kernel and the shared row
+    kernel (here one chunk per row, shorter than the chunk), each forced."""
     import ozaki_triton_amd as ozk
+    monkeypatch.setenv("OZK_SPLIT_KERNEL", kernel)
     g = torch.Generator().manual_seed(rows * K + L)
     X = torch.randn(2, rows, K, generator=g, dtype=torch.float64)
     X = X * torch.pow(10.0, torch.empty(2, rows, 1).uniform_(-3, 3, generator=g).double())
-    _check_split(oracle, ozk, X.to(xdt).to(gpu), L, sdt, f"rows {xdt} {sdt} L{L} {rows}x{K}")
+    _check_split(oracle, ozk, X.to(xdt).to(gpu), L, sdt, f"{kernel} {xdt} {sdt} L{L} {rows}x{K}")
+
+
+@pytest.mark.parametrize("xdt,sdt", COMBOS)
+@pytest.mark.parametrize("batch,rows,K,L", [(2, 3, 40000, 3), (1, 5, 65536, 4), (1, 4, 16388, 2)])
+def test_split_rows_coop_long(oracle, gpu, xdt, sdt, batch, rows, K, L):
+    """Rows longer than 16384 (the default there): 2 to 8 workgroups per row
+    exchanging the level maxima, ragged last chunks, a batch, per-row
+    exponents and outliers."""
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(batch * rows * K + L)
+    X = torch.randn(batch, rows, K, generator=g, dtype=torch.float64)
+    X = X * torch.pow(2.0, torch.randint(-8, 9, (batch, rows, 1), generator=g).double())
+    X[torch.rand(batch, rows, K, generator=g) < 0.001] *= 1e4
+    X[:, 0, :] = 0.0                                   # a zero row
+    _check_split(oracle, ozk, X.to(xdt).to(gpu), L, sdt, f"rowscoop {xdt} {sdt} {rows}x{K}")
 
 
 @pytest.mark.parametrize("xdt,sdt", COMBOS)
@@ -97,7 +116,9 @@ def test_split_generic_path(oracle, gpu, xdt, sdt):
     _check_split(oracle, ozk, X[:, :, ::2], 3, sdt, "generic strided")
     big = 40000 if xdt == torch.float64 else 70000
     Y = torch.randn(1, 3, big, generator=g, dtype=torch.float64).to(xdt).to(gpu)
-    _check_split(oracle, ozk, Y, 2, sdt, "generic long K")
+    with pytest.MonkeyPatch.context() as mp:
+        mp.setenv("OZK_SPLIT_KERNEL", "generic")   # long rows otherwise take the shared row kernel
+        _check_split(oracle, ozk, Y, 2, sdt, "generic long K")
 
 
 @pytest.mark.parametrize("xdt", [torch.float64, torch.float32])
@@ -368,15 +389,34 @@ def test_split_coop_wait_timeout(oracle, gpu, xdt, monkeypatch):
     _check_split(oracle, ozk, BT, L, torch.int8, f"coop after timeout {xdt}")
 
 
+@pytest.mark.parametrize("xdt", [torch.float64, torch.float32])
+def test_split_rows_coop_wait_timeout(oracle, gpu, xdt, monkeypatch):
+    """The shared row kernel's bounded wait, forced to run out as above: the
+    kernel finishes and the scales come out NaN; the normal path is exact
+    again afterwards."""
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(22)
+    X = torch.randn(1, 3, 40000, generator=g, dtype=torch.float64).to(xdt).to(gpu)
+    alpha = _alpha(ozk, 40000, torch.int8)
+    monkeypatch.setenv("OZK_SPLIT_COOP_TIMEOUT", "1")
+    sl, sc = ozk.split_matrix(X, 2, alpha, torch.int8)
+    torch.cuda.synchronize()
+    assert torch.isnan(sc).all(), "every exchanged level's scale should be NaN after the timeout"
+    monkeypatch.delenv("OZK_SPLIT_COOP_TIMEOUT")
+    _check_split(oracle, ozk, X, 2, torch.int8, f"rowscoop after timeout {xdt}")
+
+
 @pytest.mark.parametrize("xdt,sdt", COMBOS)
-def test_split_transpose_path(oracle, gpu, xdt, sdt, monkeypatch):
-    """Column splits (B^T view) through the transpose into the workspace and
-    the row kernel (the path for columns longer than the cooperative kernel
-    takes)."""
+@pytest.mark.parametrize("long", [False, True])
+def test_split_transpose_path(oracle, gpu, xdt, sdt, long, monkeypatch):
+    """Column splits (B^T view) through the transpose into the workspace and a
+    row kernel (the path for columns longer than the cooperative column kernel
+    takes): rows up to 16384 go to the one-workgroup row kernel, longer ones
+    (config 5's B is 65536 long) to the shared row kernel."""
     import ozaki_triton_amd as ozk
     monkeypatch.setenv("OZK_SPLIT_KERNEL", "transpose")
     g = torch.Generator().manual_seed(11)
-    K = 20000 if xdt == torch.float64 else 65536
+    K = (20000 if xdt == torch.float64 else 65536) if long else 12000
     B = torch.randn(1, K, 40, generator=g, dtype=torch.float64)
     B[torch.rand(1, K, 40, generator=g) < 0.01] *= 1e4
     Bd = B.to(xdt).to(gpu)
