@@ -305,7 +305,7 @@ def ozaki_matmul(
     return _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, None)
 
 
-def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, events):
+def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, events, max_splits=4):
     """
     Ozaki-scheme matrix product C = A @ B with torch.matmul batch broadcasting.
 
@@ -328,11 +328,14 @@ def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, events):
     one workspace holding the slices and scales.  ``events`` (internal, used by
     bench.py) is None or four torch.cuda.Event objects that the call records
     before the B split, before the A split, before the cross-GEMM and after it.
+    ``max_splits`` (internal) is the reference's limit of 4 (ozaki_triton.py:563)
+    for the public function; bench.py raises it to the C ABI's OZK_MAX_SPLITS (8)
+    to time more slices.
     """
     assert A.dtype == B.dtype, f"A/B dtype mismatch: {A.dtype} vs {B.dtype}"
     assert A.dtype in _INPUT_DTYPES, f"unsupported input dtype: {A.dtype}"
     assert slice_dtype in _SLICE_DTYPE_INFO, f"unsupported slice dtype: {slice_dtype}"
-    assert num_splits <= 4, f"num_splits must be <= 4, got {num_splits}"
+    assert num_splits <= max_splits, f"num_splits must be <= {max_splits}, got {num_splits}"
 
     input_dtype = A.dtype
     dot_accum_dtype = _select_dot_accum_dtype(slice_dtype)
