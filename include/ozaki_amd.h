@@ -18,7 +18,9 @@
  *   - No device memory is allocated.  Scratch space comes from the caller
  *     through (workspace, workspace_bytes), 16-byte aligned; *_workspace_bytes() says
  *     how much.
- *   - No mutable global state: calls are re-entrant and thread-safe.
+ *   - Calls are re-entrant and thread-safe.  The only process-wide state is,
+ *     per cross-GEMM kernel, an atomic record of the devices on which its
+ *     dynamic-LDS limit has been raised (hipFuncSetAttribute, once per device).
  */
 #ifndef OZAKI_AMD_H
 #define OZAKI_AMD_H

@@ -26,6 +26,7 @@
 //     reference for any tiling.
 //   * Workgroups are remapped so each XCD (own L2) processes a contiguous
 //     range of tiles, grouped GROUP_M tile-rows at a time.
+#include <atomic>
 #include <stdlib.h>
 #include <string.h>
 
@@ -1513,18 +1514,26 @@ static int64_t dma_extent(int64_t s_l, int64_t s_r, int L, int64_t rows, int64_t
     return (e < ((int64_t)1 << 31) - 64) ? e : -1;
 }
 
+// Raise a kernel's dynamic LDS limit (above the 64 KB default) once per
+// device.  `done` is that kernel's bitmask of devices already set (bit d:
+// device d); concurrent first calls may both set it, which is harmless.
+static hipError_t set_lds_limit(const void *kern, int bytes, std::atomic<uint64_t> &done) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = (dev >= 0 && dev < 64) ? (1ull << dev) : 0;
+    if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+    e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_acq_rel);
+    return e;
+}
+
 template <typename ST, int L, int MI, int NI, typename AccT>
 static hipError_t launch_dma(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     using Sh = DmaShape<L, MI, NI>;
     auto kern = cross_gemm_dma_kernel<ST, L, MI, NI, AccT>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)kern,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           Sh::LDS_BYTES);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
+    if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
     const int es = (int)sizeof(ST);
     const int64_t ea = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es);
     const int64_t eb = dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es);
@@ -1539,14 +1548,8 @@ template <typename ST, int L, int NI, typename AccT>
 static hipError_t launch_ad(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     using Sh = AdShape<L, NI>;
     auto kern = cross_gemm_ad_kernel<ST, L, NI, AccT>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)kern,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           Sh::LDS_BYTES);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
+    if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
     const int es = (int)sizeof(ST);
     const int64_t ea = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es);
     const int64_t eb = dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es);
@@ -1562,14 +1565,8 @@ static hipError_t launch_pair(const GemmParams &p, const GemmPlan &plan, hipStre
                               int cont) {
     using Sh = PairShape<L, R>;
     auto kern = cross_gemm_pair_kernel<ST, L, AccT, R>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)kern,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           Sh::LDS_BYTES);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
+    if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
     const int es = (int)sizeof(ST);
     const int64_t ea = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es);
     const int64_t eb = dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es);
@@ -1585,14 +1582,8 @@ static hipError_t launch_ring(const GemmParams &p, const GemmPlan &plan, hipStre
     constexpr int W = (L <= 2) ? 2 : 1;
     using Sh = RingShape<L, W>;
     auto kern = cross_gemm_ring_kernel<ST, L, AccT, W>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)kern,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           Sh::LDS_BYTES);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
+    if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
     const int es = (int)sizeof(ST);
     const int64_t ea = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es);
     const int64_t eb = dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es);
@@ -1637,14 +1628,8 @@ static hipError_t launch_one(const GemmParams &p, const GemmPlan &plan, hipStrea
     if (plan.kind == kGemmDMA) return launch_dma<ST, L, MI, NI, AccT>(p, plan, st);
     using Sh = GemmShape<L, MI, NI>;
     auto kern = cross_gemm_kernel<ST, L, MI, NI, AccT>;
-    static bool attr_set = false;   // idempotent; a racing second set is harmless
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)kern,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           Sh::LDS_BYTES);
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
+    if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
     const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
     if (tiles == 0) return hipSuccess;
     hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(256), Sh::LDS_BYTES, st, p,
