@@ -1472,9 +1472,10 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype) {
         return p.batch * ((p.M + 64 * a - 1) / (64 * a)) * ((p.N + 64 * c - 1) / (64 * c));
     };
     // a grid smaller than two waves of 256 CUs loses more to idle CUs than the
-    // larger tile gains in reuse
+    // larger tile gains in reuse.  Shrinks N while it is the larger, then M:
+    // (2,4) -> (2,2) -> (1,2) -> (1,1), the (mi, ni) pairs launch_L instantiates
     while ((mi > 1 || ni > 1) && nt(mi, ni) < 512) {
-        if (ni >= mi && ni > 1) ni /= 2;
+        if (ni > mi) ni /= 2;
         else mi /= 2;
     }
     plan.mi = mi;

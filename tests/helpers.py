@@ -84,3 +84,32 @@ def c3_like(shape_a, shape_b, seed, dtype=torch.float64, exp_range=8):
     A = A * torch.pow(2.0, ea.double())
     B = B * torch.pow(2.0, eb.double())
     return A.to(dtype), B.to(dtype)
+
+
+def sample_indices(n, k, seed):
+    """k indices of range(n): both ends, a tile boundary and random ones."""
+    rng = np.random.default_rng(seed)
+    fixed = [0, 1, 63, 64, n // 2, n - 1]
+    rest = rng.choice(n, size=k, replace=False)
+    idx = sorted(set(fixed) | set(rest.tolist()))
+    return np.array(idx[:k] if len(idx) > k else idx)
+
+
+def check_block_vs_oracle(oracle, ozk, C_np, A_np, B_np, rows, cols, L, sdt, xdt, what):
+    """C_np[rows][:, cols] against the oracle's result for A_np[rows] and
+    B_np[:, cols] (one batch, full K)."""
+    K = A_np.shape[-1]
+    sd = NAME_OF[sdt]
+    alpha = ozk.compute_split_bits(K, sdt, ozk._select_dot_accum_dtype(sdt))
+    a_sl, a_sc = oracle.split(np.ascontiguousarray(A_np[rows]), L, alpha, sd)
+    b_sl, b_sc = oracle.split(np.ascontiguousarray(B_np[:, cols].T), L, alpha, sd)
+    want = oracle.cross_gemm(a_sl, b_sl, a_sc, b_sc, NAME_OF[xdt])
+    got = np.ascontiguousarray(C_np[np.ix_(rows, cols)])
+    if sdt == torch.int8:
+        assert_bitwise_equal(got, want, what)
+    else:
+        bound = fp16_cross_bound(oracle, a_sl, b_sl, a_sc, b_sc)
+        if xdt == torch.float32:
+            bound = bound + 2.0 ** -23 * np.abs(want.astype(np.float64))   # output rounding
+        err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+        assert np.all(err <= bound), (what, float((err / np.maximum(bound, 1e-300)).max()))

@@ -27,7 +27,8 @@ import numpy as np
 import pytest
 import torch
 
-from tests.helpers import NAME_OF, assert_bitwise_equal, fp16_cross_bound, to_np
+from tests.helpers import (NAME_OF, assert_bitwise_equal, check_block_vs_oracle,
+                           sample_indices, to_np)
 
 pytestmark = pytest.mark.gpu
 
@@ -41,38 +42,9 @@ def bench_mod():
     return bench
 
 
-def _sample(n, k, seed):
-    """k indices of range(n): both ends, a tile boundary and random ones."""
-    rng = np.random.default_rng(seed)
-    fixed = [0, 1, 63, 64, n // 2, n - 1]
-    rest = rng.choice(n, size=k, replace=False)
-    idx = sorted(set(fixed) | set(rest.tolist()))
-    return np.array(idx[:k] if len(idx) > k else idx)
-
-
 def _rel_err(C, A, B):
     ref = torch.matmul(A.double(), B.double())
     return float(torch.linalg.norm(C.double() - ref) / torch.linalg.norm(ref))
-
-
-def _check_block(oracle, ozk, C_np, A_np, B_np, rows, cols, L, sdt, xdt, what):
-    """C_np[rows][:, cols] against the oracle's result for A_np[rows] and
-    B_np[:, cols] (one batch, full K)."""
-    K = A_np.shape[-1]
-    sd = NAME_OF[sdt]
-    alpha = ozk.compute_split_bits(K, sdt, ozk._select_dot_accum_dtype(sdt))
-    a_sl, a_sc = oracle.split(np.ascontiguousarray(A_np[rows]), L, alpha, sd)
-    b_sl, b_sc = oracle.split(np.ascontiguousarray(B_np[:, cols].T), L, alpha, sd)
-    want = oracle.cross_gemm(a_sl, b_sl, a_sc, b_sc, NAME_OF[xdt])
-    got = np.ascontiguousarray(C_np[np.ix_(rows, cols)])
-    if sdt == torch.int8:
-        assert_bitwise_equal(got, want, what)
-    else:
-        bound = fp16_cross_bound(oracle, a_sl, b_sl, a_sc, b_sc)
-        if xdt == torch.float32:
-            bound = bound + 2.0 ** -23 * np.abs(want.astype(np.float64))   # output rounding
-        err = np.abs(got.astype(np.float64) - want.astype(np.float64))
-        assert np.all(err <= bound), (what, float((err / np.maximum(bound, 1e-300)).max()))
 
 
 @pytest.mark.parametrize("name", ["C3", "C2", "C5"])
@@ -96,8 +68,8 @@ def test_full_size_single_gemm(oracle, gpu, bench_mod, name):
     del C, Ad, Bd
     M, N = C_np.shape
     k = 32 if name == "C5" else 64
-    rows, cols = _sample(M, k, seed), _sample(N, k, seed + 1)
-    _check_block(oracle, ozk, C_np, A_np, B_np, rows, cols, L, sdt, xdt, f"{name} block")
+    rows, cols = sample_indices(M, k, seed), sample_indices(N, k, seed + 1)
+    check_block_vs_oracle(oracle, ozk, C_np, A_np, B_np, rows, cols, L, sdt, xdt, f"{name} block")
 
 
 def test_full_size_broadcast_batch(oracle, gpu, bench_mod):
@@ -117,8 +89,8 @@ def test_full_size_broadcast_batch(oracle, gpu, bench_mod):
     assert rel <= REL_ERR_BOUND["C4"], rel
     C_np, A_np, B_np = to_np(C), to_np(A), to_np(B)
     for b in (0, 7, 15):
-        rows, cols = _sample(1024, 48, seed + b), _sample(1024, 48, seed + 100 + b)
-        _check_block(oracle, ozk, C_np[b], A_np[b], B_np, rows, cols, L, sdt, xdt,
+        rows, cols = sample_indices(1024, 48, seed + b), sample_indices(1024, 48, seed + 100 + b)
+        check_block_vs_oracle(oracle, ozk, C_np[b], A_np[b], B_np, rows, cols, L, sdt, xdt,
                      f"C4 batch {b} block")
 
 
@@ -132,7 +104,7 @@ def test_c1_whole_output(oracle, gpu):
     C = ozk.ozaki_matmul(A.to(gpu), B.to(gpu), 2, torch.float16)
     torch.cuda.synchronize()
     rows = cols = np.arange(256)
-    _check_block(oracle, ozk, to_np(C), to_np(A), to_np(B), rows, cols, 2, torch.float16,
+    check_block_vs_oracle(oracle, ozk, to_np(C), to_np(A), to_np(B), rows, cols, 2, torch.float16,
                  torch.float32, "C1")
 
 
@@ -156,7 +128,7 @@ def test_full_size_splits(oracle, gpu, bench_mod, name):
         sc_np = to_np(sc)[0]
         mant, _ = np.frexp(sc_np.astype(np.float64))
         assert np.all(mant == 0.5), f"{name} {what}: a scale is not a power of two"
-        rows = _sample(X.shape[0], 64, seed + 7)
+        rows = sample_indices(X.shape[0], 64, seed + 7)
         idx = torch.as_tensor(rows, device=gpu)
         got_sl = to_np(sl[0][:, idx])
         want_sl, want_sc = oracle.split(np.ascontiguousarray(to_np(X)[rows]), L, alpha,

@@ -11,8 +11,8 @@ import numpy as np
 import pytest
 import torch
 
-from tests.helpers import (NAME_OF, assert_bitwise_equal, c3_like, fp16_cross_bound,
-                           oracle_split_batched, to_np, values)
+from tests.helpers import (NAME_OF, assert_bitwise_equal, c3_like, check_block_vs_oracle,
+                           fp16_cross_bound, oracle_split_batched, sample_indices, to_np, values)
 
 pytestmark = pytest.mark.gpu
 
@@ -663,3 +663,30 @@ def test_more_splits_unsupported_combination_raises(gpu):
     with pytest.raises(ozk._lib.OzakiLibError):
         ozk.cross_gemm(As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), 5,
                        torch.float32)
+
+
+@pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
+@pytest.mark.parametrize("L,batch,M,N", [
+    (1, 1, 4096, 4096),    # 128 x 256 tiles kept (512 of them)
+    (1, 1, 2048, 4096),    # shrunk to 128 x 128
+    (1, 2, 2048, 1024),    # shrunk to 64 x 128 (the reference's published (2, 2048, 1024, 256))
+    (1, 1, 2048, 2048),    # 64 x 128
+    (2, 1, 2048, 2048),    # L = 2: 64 x 128 instead of the ring kernel's 128 x 128
+    (2, 1, 1024, 1024),    # 64 x 64
+])
+def test_tile_table_shrink_steps(oracle, gpu, sdt, L, batch, M, N):
+    """The tile table (plan_gemm) shrinks 128 x 256 tiles for grids under 512
+    workgroups, N first while it is the larger side: every (rows, columns)
+    step it can stop at has a kernel.  (An earlier order stopped at 128 x 64,
+    which no kernel took: the launch failed.)  Sampled blocks against the
+    oracle, K = 256."""
+    import ozaki_triton_amd as ozk
+    K = 256
+    A, B = c3_like((batch, M, K), (batch, K, N), seed=M + N + L, dtype=torch.float32)
+    C = ozk.ozaki_matmul(A.to(gpu), B.to(gpu), L, sdt)
+    torch.cuda.synchronize()
+    C_np, A_np, B_np = to_np(C), to_np(A), to_np(B)
+    for b in range(batch):
+        rows, cols = sample_indices(M, 40, b + 1), sample_indices(N, 40, b + 2)
+        check_block_vs_oracle(oracle, ozk, C_np[b], A_np[b], B_np[b], rows, cols, L, sdt,
+                              torch.float32, f"L{L} {sdt} b{b} {M}x{N}")
