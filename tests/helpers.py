@@ -89,7 +89,7 @@ def c3_like(shape_a, shape_b, seed, dtype=torch.float64, exp_range=8):
 def sample_indices(n, k, seed):
     """k indices of range(n): both ends, a tile boundary and random ones."""
     rng = np.random.default_rng(seed)
-    fixed = [0, 1, 63, 64, n // 2, n - 1]
+    fixed = [i for i in (0, 1, 63, 64, n // 2, n - 1) if i < n]
     rest = rng.choice(n, size=k, replace=False)
     idx = sorted(set(fixed) | set(rest.tolist()))
     return np.array(idx[:k] if len(idx) > k else idx)
