@@ -116,6 +116,12 @@ def _require_gpu(*tensors: torch.Tensor) -> None:
             raise RuntimeError(
                 "ozaki_triton_amd runs only on a ROCm GPU device (got a tensor on "
                 f"{t.device}); there is no CPU path")
+    # the kernels take raw pointers: operands on another GPU would be read
+    # through that device's addresses
+    devs = {t.device for t in tensors}
+    if len(devs) > 1:
+        raise RuntimeError("ozaki_triton_amd: all tensors must be on one device "
+                           f"(got {sorted(map(str, devs))})")
 
 
 def _require_supported(input_dtype: torch.dtype, slice_dtype: torch.dtype) -> None:

@@ -321,3 +321,16 @@ def test_matmul_abi_layout_and_errors():
     # nothing to do: OK without a device call
     assert L.ozk_matmul(p, a, p, b, _lib.OZK_F64, 0, M, N, K, 4, _lib.OZK_I8, p, c, null, 0,
                         None, null) == _lib.OZK_OK
+
+
+def test_operands_on_two_devices_are_refused():
+    """The wrappers hand raw pointers to the kernels, so operands on two GPUs
+    are refused on the host (checked with stand-ins: this container has no
+    GPU)."""
+    import types
+    from ozaki_triton_amd.ozaki import _require_gpu
+    a = types.SimpleNamespace(is_cuda=True, device=torch.device("cuda", 0))
+    b = types.SimpleNamespace(is_cuda=True, device=torch.device("cuda", 1))
+    _require_gpu(a, a)
+    with pytest.raises(RuntimeError, match="one device"):
+        _require_gpu(a, b)
