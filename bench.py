@@ -410,7 +410,7 @@ def main():
         },
         "split": {
             "kernels": "split_rows_kernel, or split_rows_coop_kernel for rows over 16384 (A); "
-                       "split_coop_kernel for columns of 64 KB up to 32 K chunks, "
+                       "split_coop_kernel for columns of 64 KB (fp64 to int8: 32 KB, 2048 columns) up to 32 K chunks, "
                        "split_strip_kernel below, transpose_kernel + a row kernel above (B)",
             "bound": "hbm",
             "bytes": split_bytes,

@@ -1115,12 +1115,17 @@ SplitPlan plan_split(const SplitParams &p, int x_dtype, int slice_dtype) {
                          (p.xs_k * xsz) % 16 == 0 && (p.xs_b * xsz) % 16 == 0;
     // columns of 64 KB and more: the cooperative kernel (the strip kernel's
     // 16-byte row pieces cost more than the exchange from there on; measured
-    // over K = 1024..16384, N = 1024..8192, fp64 / fp32); OZK_SPLIT_KERNEL=coop
-    // takes it for any length it holds
+    // over K = 1024..16384, N = 1024..8192, fp64 / fp32), and fp64 columns of
+    // 32 KB into int8 slices when there are at least 2048 of them (0.90-0.94x
+    // the strip kernel's time at K = 4096, N = 2048..8192; 1.04x at N = 1024;
+    // fp16 slices gain nothing there, fp32 columns below 64 KB lose 1.1-1.3x);
+    // OZK_SPLIT_KERNEL=coop takes it for any length it holds
     const bool coop_fits = cols_ok && coop_members(p.K, 64 / vec) <= kCoopMaxP;
     const bool other = forced("strip") || forced("transpose") || forced("generic");
-    if (coop_fits && (forced("coop") || (!other && p.K * xsz >= kCoopMinColumnBytes)))
-        return {kSplitCoop, 64 / vec};
+    const bool coop_long = p.K * xsz >= kCoopMinColumnBytes ||
+                           (xsz == 8 && ssz == 1 && p.K * xsz >= kCoopMinColumnBytes / 2 &&
+                            p.batch * p.rows >= 2048);
+    if (coop_fits && (forced("coop") || (!other && coop_long))) return {kSplitCoop, 64 / vec};
     if (cols_ok && !forced("transpose") && !forced("generic")) {
         for (int i = 0; i < kNumStripCfgs; ++i) {
             const StripCfg &c = kStripCfgs[i];

@@ -690,3 +690,18 @@ def test_tile_table_shrink_steps(oracle, gpu, sdt, L, batch, M, N):
         rows, cols = sample_indices(M, 40, b + 1), sample_indices(N, 40, b + 2)
         check_block_vs_oracle(oracle, ozk, C_np[b], A_np[b], B_np[b], rows, cols, L, sdt,
                               torch.float32, f"L{L} {sdt} b{b} {M}x{N}")
+
+
+@pytest.mark.parametrize("xdt,sdt", COMBOS)
+@pytest.mark.parametrize("batch,N,K", [(1, 2048, 4096), (2, 1024, 6000), (1, 1024, 4096)])
+def test_split_columns_default_plan(oracle, gpu, xdt, sdt, batch, N, K):
+    """B's columns through the transposed view with the planner's own choice
+    (no kernel forced): fp64 columns from 32 KB into int8 slices, 2048 or more
+    of them, take the cooperative kernel; fewer, fp32 columns or fp16 slices
+    the strip kernel."""
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(batch * N + K)
+    B = torch.randn(batch, K, N, generator=g, dtype=torch.float64)
+    B = B * torch.pow(2.0, torch.randint(-8, 9, (batch, 1, N), generator=g).double())
+    _check_split(oracle, ozk, B.to(xdt).to(gpu).transpose(-1, -2), 4, sdt,
+                 f"default {xdt} {sdt} b{batch} {N}x{K}")
