@@ -1473,8 +1473,12 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype) {
     };
     // a grid smaller than two waves of 256 CUs loses more to idle CUs than the
     // larger tile gains in reuse.  Shrinks N while it is the larger, then M:
-    // (2,4) -> (2,2) -> (1,2) -> (1,1), the (mi, ni) pairs launch_L instantiates
-    while ((mi > 1 || ni > 1) && nt(mi, ni) < 512) {
+    // (2,4) -> (2,2) -> (1,2) -> (1,1), the (mi, ni) pairs launch_L instantiates.
+    // num_splits 2 keeps the ring kernel's 128 x 128 tiles from one wave of
+    // tiles on (256 or more: 0.75-0.86x the LDS-DMA kernel's 64 x 128 tiles at
+    // 256, 0.94-0.97x at 384; 1.8-1.9x slower at 64)
+    const bool ring2 = L == 2 && nt(2, 2) >= 256;
+    while (!ring2 && (mi > 1 || ni > 1) && nt(mi, ni) < 512) {
         if (ni > mi) ni /= 2;
         else mi /= 2;
     }
@@ -1485,7 +1489,7 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype) {
     // OZK_GEMM_KERNEL=staged|dma|ad|pair|ring forces a kernel (tests cover
     // every one at small sizes).  By default, when both operands fit the
     // 31-bit buffer offsets of the LDS-DMA kernels: the ring kernel for
-    // L = 3, 4 (64 x 64 tiles) and for L = 2 when the grid takes 128 x 128
+    // L = 3, 4 (64 x 64 tiles) and for L = 2 on grids of 256 or more 128 x 128
     // tiles, the pair-split kernel for L > 4, the 2 x 2 LDS-DMA kernel with its
     // larger wave tiles otherwise; else the VGPR-staged kernel.
     const bool fits = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es) >= 0 &&

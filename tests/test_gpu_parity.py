@@ -671,8 +671,8 @@ def test_more_splits_unsupported_combination_raises(gpu):
     (1, 1, 2048, 4096),    # shrunk to 128 x 128
     (1, 2, 2048, 1024),    # shrunk to 64 x 128 (the reference's published (2, 2048, 1024, 256))
     (1, 1, 2048, 2048),    # 64 x 128
-    (2, 1, 2048, 2048),    # L = 2: 64 x 128 instead of the ring kernel's 128 x 128
-    (2, 1, 1024, 1024),    # 64 x 64
+    (2, 1, 2048, 2048),    # L = 2: the ring kernel's 128 x 128 tiles (256 of them)
+    (2, 1, 1024, 1024),    # L = 2: 64 x 64 (LDS-DMA kernel)
 ])
 def test_tile_table_shrink_steps(oracle, gpu, sdt, L, batch, M, N):
     """The tile table (plan_gemm) shrinks 128 x 256 tiles for grids under 512
