@@ -1512,10 +1512,16 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype) {
 }
 
 // byte extent [0, bytes) one batch of a slice operand spans, or -1 if it does
-// not fit the 31-bit buffer offsets of the DMA kernel
+// not fit the 31-bit buffer offsets of the DMA kernel.  The last row counts
+// up to its 16-byte boundary: the kernels load 16-byte pieces, and a piece
+// that crosses the buffer's end comes back zeroed as a whole, which would
+// drop the row's last elements.  Those bytes exist and are zero: operands
+// whose rows are not whole 16-byte pieces are the pack kernel's zero-padded
+// copies (K * es is a multiple of 16 for every other operand).
 static int64_t dma_extent(int64_t s_l, int64_t s_r, int L, int64_t rows, int64_t K, int es) {
     if (s_l < 0 || s_r < 0) return -1;
-    const int64_t e = ((int64_t)(L - 1) * s_l + (rows - 1) * s_r + K) * es;
+    const int64_t row_bytes = (K * es + 15) / 16 * 16;
+    const int64_t e = ((int64_t)(L - 1) * s_l + (rows - 1) * s_r) * es + row_bytes;
     return (e < ((int64_t)1 << 31) - 64) ? e : -1;
 }
 

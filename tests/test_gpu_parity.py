@@ -705,3 +705,26 @@ def test_split_columns_default_plan(oracle, gpu, xdt, sdt, batch, N, K):
     B = B * torch.pow(2.0, torch.randint(-8, 9, (batch, 1, N), generator=g).double())
     _check_split(oracle, ozk, B.to(xdt).to(gpu).transpose(-1, -2), 4, sdt,
                  f"default {xdt} {sdt} b{batch} {N}x{K}")
+
+
+@pytest.mark.parametrize("kernel", ["", "dma", "ring", "pair", "ad", "staged"])
+@pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
+@pytest.mark.parametrize("K", [1, 2, 3, 5, 7, 9, 255, 257, 1003])
+def test_packed_rows_last_piece(oracle, gpu, kernel, sdt, K, monkeypatch):
+    """Slice rows that are not whole 16-byte pieces (K * element size) go
+    through the pack kernel's zero-padded copy.  The LDS-DMA kernels load
+    16-byte pieces; the last piece of the operand's last row (the last slice
+    of its last row) crosses the end of the buffer unless the buffer's extent
+    runs to that row's 16-byte boundary, and a crossing piece comes back
+    zeroed.  Full outputs against the oracle, every kernel forced in turn:
+    int8 bit-exact, fp16 within the fp32 accumulation bound."""
+    import ozaki_triton_amd as ozk
+    if kernel:
+        monkeypatch.setenv("OZK_GEMM_KERNEL", kernel)
+    L = 4 if kernel in ("ring", "pair", "ad") else 2
+    A, B = c3_like((1, 33, K), (1, K, 20), seed=K + 100)
+    C = ozk.ozaki_matmul(A.to(gpu), B.to(gpu), L, sdt)
+    torch.cuda.synchronize()
+    rows, cols = np.arange(33), np.arange(20)
+    check_block_vs_oracle(oracle, ozk, to_np(C)[0], to_np(A)[0], to_np(B)[0], rows, cols, L, sdt,
+                          torch.float64, f"K{K} {kernel or 'default'} {sdt}")
