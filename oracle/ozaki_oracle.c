@@ -37,6 +37,7 @@
  * multiply and an add whose intermediate the reference rounds) and without
  * -ffast-math; x86-64 SSE arithmetic gives IEEE binary32/binary64 results.
  */
+#include <float.h>
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -109,9 +110,12 @@ float ozo_pow2f(int e)
     return bits_f32(1u << (e + 149));
 }
 
-/* scale of one row: ozaki_triton.py:174 */
+/* scale of one row: ozaki_triton.py:174.  A row holding +-inf has mu = inf,
+ * where the reference's exp2(ceil(log2(mu)) - alpha) is inf (log2(inf) = inf,
+ * ozaki_triton.py:173-176); the closed form above covers finite mu only. */
 float ozo_scale_from_max(float mu, int alpha)
 {
+    if (!(mu <= FLT_MAX)) return mu;
     return ozo_pow2f(ozo_ceil_log2_f32(mu) - alpha);
 }
 

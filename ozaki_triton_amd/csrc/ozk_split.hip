@@ -85,6 +85,10 @@ OZK_DEV LevelScale level_scale(float m, int alpha) {
     c.up = -ema;
     c.s64 = (double)c.s;
     c.inv64 = pow2d(-ema);
+    // a row with an infinite entry has m = inf, for which the reference's
+    // exp2(ceil(log2(m)) - alpha) is inf: that scale is stored as it is, so
+    // the row's terms in C come out non-finite (its slices carry no meaning)
+    if (!(m <= 3.402823466e38f)) c.s = m;
     return c;
 }
 

@@ -728,3 +728,31 @@ def test_packed_rows_last_piece(oracle, gpu, kernel, sdt, K, monkeypatch):
     rows, cols = np.arange(33), np.arange(20)
     check_block_vs_oracle(oracle, ozk, to_np(C)[0], to_np(A)[0], to_np(B)[0], rows, cols, L, sdt,
                           torch.float64, f"K{K} {kernel or 'default'} {sdt}")
+
+
+@pytest.mark.parametrize("xdt", [torch.float64, torch.float32, torch.float16])
+@pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
+def test_infinite_entries(oracle, gpu, xdt, sdt):
+    """Rows of A and columns of B holding +-inf: their level-0 maximum is inf,
+    and the reference's scale exp2(ceil(log2(inf)) - alpha) is inf, so exactly
+    those rows and columns of C are non-finite, as in the oracle; every other
+    entry is computed from finite slices (int8: bit-exact with the oracle)."""
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(41)
+    A = torch.randn(1, 40, 96, generator=g, dtype=torch.float64).to(xdt)
+    B = torch.randn(1, 96, 30, generator=g, dtype=torch.float64).to(xdt)
+    A[0, 3, 7] = float("inf")
+    A[0, 10, 0] = float("-inf")
+    B[0, 4, 2] = float("inf")
+    C = ozk.ozaki_matmul(A.to(gpu), B.to(gpu), 3, sdt)
+    torch.cuda.synchronize()
+    got = to_np(C)[0].astype(np.float64)
+    want = oracle.ozaki_matmul(to_np(A), to_np(B), 3, NAME_OF[sdt])[0].astype(np.float64)
+    bad = ~np.isfinite(got)
+    expect = np.zeros_like(bad)
+    expect[[3, 10], :] = True
+    expect[:, 2] = True
+    assert np.array_equal(bad, expect)
+    assert np.array_equal(~np.isfinite(want), expect)
+    if sdt == torch.int8:
+        assert_bitwise_equal(got[~bad], want[~bad], f"finite entries {xdt}")

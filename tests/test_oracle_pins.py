@@ -433,3 +433,16 @@ def test_cross_gemm_output_conversions(oracle, slice_dtype):
     want_i8 = np.clip(np.trunc(c32), -128, 127).astype(np.int8)
     assert np.abs(c32).max() > 127 and np.abs(c32).min() < 127   # saturating and not
     np.testing.assert_array_equal(oracle.cross_gemm(A, B, sa, sb, "int8"), want_i8)
+
+
+def test_scale_of_an_infinite_row_is_infinite(oracle):
+    """A row holding +-inf has mu = inf.  The reference's scale
+    exp2(ceil(log2(mu)) - alpha) (ozaki_triton.py:173-176, numpy's log2 / ceil /
+    exp2 in the interpreter) is then inf, which the integer closed form for
+    finite mu does not give by itself."""
+    want = float(np.exp2(np.ceil(np.log2(np.float32(np.inf))) - 7))
+    assert want == np.inf
+    assert oracle.scale_from_max(float("inf"), 7) == want
+    # finite maxima are unchanged, the largest included
+    fmax = float(np.finfo(np.float32).max)
+    assert oracle.scale_from_max(fmax, 7) == float(np.exp2(np.float32(128 - 7)))
