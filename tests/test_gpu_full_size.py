@@ -136,3 +136,25 @@ def test_full_size_splits(oracle, gpu, bench_mod, name):
         assert_bitwise_equal(sc_np[:, rows], want_sc, f"{name} {what} scales")
         assert_bitwise_equal(got_sl, want_sl, f"{name} {what} slices")
         del sl, sc
+
+
+def test_operand_over_2gib_takes_the_staged_kernel(oracle, gpu):
+    """Slice operands the LDS-DMA kernels cannot address (their buffer offsets
+    are 31-bit: over 2 GiB per batch) fall back to the VGPR-staged kernel.
+    int8 slices A [1, 4, 16448, 32768] (2.06 GiB) made on the device, B
+    [1, 4, 64, 32768]: a sampled block bit-exact against the oracle."""
+    import ozaki_triton_amd as ozk
+    L, M, N, K = 4, 16448, 64, 32768
+    g = torch.Generator(device=gpu).manual_seed(5)
+    As = torch.randint(-128, 128, (1, L, M, K), generator=g, dtype=torch.int8, device=gpu)
+    assert As.numel() > 2 ** 31
+    Bs = torch.randint(-128, 128, (1, L, N, K), generator=g, dtype=torch.int8, device=gpu)
+    sa = torch.pow(2.0, torch.randint(-30, -10, (1, L, M), generator=g, device=gpu).float())
+    sb = torch.pow(2.0, torch.randint(-30, -10, (1, L, N), generator=g, device=gpu).float())
+    C = ozk.cross_gemm(As, Bs.transpose(-1, -2), sa, sb, L, torch.float64)
+    torch.cuda.synchronize()
+    rows = sample_indices(M, 24, 1)
+    idx = torch.as_tensor(rows, device=gpu)
+    a = to_np(As[0][:, idx])
+    want = oracle.cross_gemm(a, to_np(Bs[0]), to_np(sa[0][:, idx]), to_np(sb[0]), "float64")
+    assert_bitwise_equal(to_np(C[0][idx]), want, "over-2GiB operand")
