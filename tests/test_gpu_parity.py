@@ -756,3 +756,46 @@ def test_infinite_entries(oracle, gpu, xdt, sdt):
     assert np.array_equal(~np.isfinite(want), expect)
     if sdt == torch.int8:
         assert_bitwise_equal(got[~bad], want[~bad], f"finite entries {xdt}")
+
+
+def test_concurrent_calls_from_threads(gpu):
+    """Four host threads call ozaki_matmul at once, each on its own stream
+    (default priority) with its own inputs, dtype and slice count; ctypes
+    releases the GIL during the C calls.  Every result equals the same call
+    made alone."""
+    import threading
+    import ozaki_triton_amd as ozk
+    cfgs = [((2, 200, 300), (300, 150), torch.float64, torch.int8, 4),
+            ((1, 256, 4096), (4096, 192), torch.float32, torch.float16, 2),
+            ((3, 96, 1000), (1000, 64), torch.float64, torch.bfloat16, 3),
+            ((1, 130, 8192), (8192, 70), torch.float64, torch.int8, 3)]
+    inputs = []
+    for n, (sa, sb, xdt, sdt, L) in enumerate(cfgs):
+        A, B = c3_like(sa, sb, seed=300 + n, dtype=xdt)
+        inputs.append((A.to(gpu), B.to(gpu), sdt, L))
+    alone = [ozk.ozaki_matmul(A, B, L, sdt) for A, B, sdt, L in inputs]
+    torch.cuda.synchronize()
+    got = [[None] * 8 for _ in inputs]
+    errors = []
+
+    def worker(i):
+        try:
+            A, B, sdt, L = inputs[i]
+            s = torch.cuda.Stream(gpu)
+            s.wait_stream(torch.cuda.default_stream(gpu))
+            with torch.cuda.stream(s):
+                for r in range(8):
+                    got[i][r] = ozk.ozaki_matmul(A, B, L, sdt)
+            s.synchronize()
+        except Exception as e:   # reported below, on the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(len(inputs))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for i, ref in enumerate(alone):
+        for r in range(8):
+            assert torch.equal(got[i][r], ref), (i, r)
