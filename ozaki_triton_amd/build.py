@@ -83,5 +83,22 @@ def build(verbose: bool = False) -> str:
     return LIB_PATH
 
 
+def build_c_example(verbose: bool = False) -> str:
+    """Compile tests/c_abi_example.cpp, a plain C++ caller of the C ABI, against
+    the in-tree library (rpath to it, relative to the binary)."""
+    root = os.path.dirname(HERE)
+    src = os.path.join(root, "tests", "c_abi_example.cpp")
+    out = os.path.join(root, "tests", "c_abi_example")
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-O2", "-std=c++17", "-Wall",
+           "-I", os.path.join(root, "include"), src, "-o", out, "-L", HERE, "-lozaki_amd",
+           "-Wl,-rpath,$ORIGIN/../ozaki_triton_amd"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"c_abi_example build failed:\n{res.stdout}")
+    return out
+
+
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))

@@ -799,3 +799,18 @@ def test_concurrent_calls_from_threads(gpu):
     for i, ref in enumerate(alone):
         for r in range(8):
             assert torch.equal(got[i][r], ref), (i, r)
+
+
+def test_c_abi_example_program(gpu):
+    """The C ABI from plain C++, with no Python or torch in the caller:
+    tests/c_abi_example.cpp (built by build()) runs one FP64 -> INT8 product
+    through ozk_matmul and through ozk_split x2 + ozk_cross_gemm, checks that
+    both agree bit for bit and match a CPU fp64 product, and exits 0."""
+    import os
+    import subprocess
+    exe = os.path.join(os.path.dirname(os.path.abspath(__file__)), "c_abi_example")
+    if not os.path.exists(exe):
+        pytest.fail("tests/c_abi_example is not built: run __graft_entry__.build()")
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "c_abi_example ok" in r.stdout, r.stdout
