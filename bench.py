@@ -351,12 +351,15 @@ def main():
     else:
         peak, unit_c = PEAK_FP16_TFLOPS, "TFLOP/s"
     achieved = cross_ops / (t_cross * 1e-3) / 1e12
-    # the library's default kernel choice (plan_gemm in ozk_gemm.hip): the
+    # the library's default kernel choice (plan_gemm in ozk_gemm.hip): for
+    # L = 3 the wide kernel on a grid of at least 512 64 x 128 tiles, the
     # five-slot ring kernel for L = 3, 4 and for L = 2 on a grid of at least 256
     # 128 x 128 tiles, the pair-split kernel for L > 4, the 2 x 2 LDS-DMA kernel
     # otherwise
     big2 = batch * -(-M // 128) * -(-N // 128) >= 256
-    gemm_kernel = ("cross_gemm_ring_kernel" if 3 <= L <= 4 or (L == 2 and big2) else
+    wide3 = batch * -(-M // 64) * -(-N // 128) >= 512
+    gemm_kernel = ("cross_gemm_wide_kernel" if L == 3 and wide3 else
+                   "cross_gemm_ring_kernel" if 3 <= L <= 4 or (L == 2 and big2) else
                    "cross_gemm_pair_kernel" if L > 4 else "cross_gemm_dma_kernel")
     # split: read the unique inputs, write the unique slices and scales
     xsz = 8 if xdt == "float64" else 4

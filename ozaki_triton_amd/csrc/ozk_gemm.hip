@@ -1184,6 +1184,248 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ring_kernel(GemmParams p, i
 }
 
 // ---------------------------------------------------------------------------
+// Wide kernel for num_splits 3: 64 x 128 tiles, 8 waves in a 2 x 4 grid of
+// 32 x 32 blocks, each wave holding all 9 slice pairs of its block (144
+// accumulator registers).  Per 32-byte K step a wave reads 3 A and 3 B
+// fragments for 9 MFMAs (the ring kernel's wave groups read 9 fragments for
+// the 9 MFMAs of two waves), and a stage of 128 bytes of K (24 KB of A rows,
+// 48 KB of B rows) feeds 288 MFMAs (the ring kernel's 48 KB: 144).  Each wave
+// sums its own pairs in the reference's i-major / j-minor order, so the
+// epilogue hands nothing between waves.
+// The LDS holds two whole stages (144 KB; the A and B halves differ in size,
+// so they do not form a ring of equal slots).  Stage kb + 2 is fetched into
+// stage kb's buffer, released by the barrier of stage kb: P1 instructions per
+// wave in the K step after that barrier, the rest in the next K step, and the
+// barrier of stage kb + 1 waits for all of them.
+// ---------------------------------------------------------------------------
+struct WideShape {
+    static constexpr int L = 3;
+    static constexpr int NW = 8;                         // waves
+    static constexpr int BM = 64, BN = 128;
+    static constexpr int A_BYTES = L * BM * kDmaRB;      // 24 KB
+    static constexpr int B_BYTES = L * BN * kDmaRB;      // 48 KB
+    static constexpr int STAGE = A_BYTES + B_BYTES;
+    static constexpr int LA = A_BYTES / (NW * 1024);     // A instructions per wave per stage
+    static constexpr int LB = B_BYTES / (NW * 1024);     // B instructions per wave per stage
+    static constexpr int LPS = LA + LB;
+    static constexpr int P1 = 5;                         // issued in the K step after the barrier
+    static constexpr int LDS_BYTES = 2 * STAGE;
+    static_assert(A_BYTES % (NW * 1024) == 0 && B_BYTES % (NW * 1024) == 0,
+                  "a half stage must be whole 1 KB windows per wave");
+    static_assert(P1 >= LPS - P1 && P1 <= LPS, "the larger part goes first");
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS");
+    static_assert(L * (BM + BN) * 4 <= STAGE, "the tile's scales fit a stage buffer");
+    static_assert(kDmaRB == 128, "128-byte stage rows");
+};
+
+template <typename ST, typename AccT>
+__global__ __launch_bounds__(512, 1) void cross_gemm_wide_kernel(GemmParams p, int group_m,
+                                                                 uint32_t a_records,
+                                                                 uint32_t b_records) {
+    using Sh = WideShape;
+    using MF = Mfma<ST>;
+    using Acc = typename MF::Acc;
+    using OA = AccT;
+    constexpr int L = Sh::L, BM = Sh::BM, BN = Sh::BN;
+    constexpr int ES = (int)sizeof(ST);
+    constexpr uint32_t kOOB = 0x80000000u;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 2, wn = wave & 3;
+    const int h = lane >> 5, lr = lane & 31;
+
+    const int64_t tiles_m = (p.M + BM - 1) / BM;
+    const int64_t tiles_n = (p.N + BN - 1) / BN;
+    const int64_t tiles = tiles_m * tiles_n;
+    const int64_t g = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
+    const int64_t bidx = g / tiles;
+    const int64_t t = g % tiles;
+    const int64_t width = (int64_t)group_m * tiles_n;
+    const int64_t first_m = (t / width) * group_m;
+    const int64_t gsz = (tiles_m - first_m < group_m) ? (tiles_m - first_m) : group_m;
+    const int64_t tm = first_m + (t % width) % gsz;
+    const int64_t tn = (t % width) / gsz;
+    const int64_t m0 = tm * BM, n0 = tn * BN;
+
+    const uint32_t kbytes = (uint32_t)(p.K * ES);
+    const int nkb = (int)((kbytes + kDmaRB - 1) / kDmaRB);
+
+    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const char *)p.A + bidx * p.as_b * ES), (short)0, (int)a_records, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const char *)p.B + bidx * p.bs_b * ES), (short)0, (int)b_records, 0x00020000);
+
+    // This wave's LPS DMA instructions of a stage: q < LA fetch window
+    // wave * LA + q of the A half, the others window wave * LB + q - LA of the
+    // B half (a 1 KB window is 8 whole 128-byte rows; lane -> row lane / 8,
+    // physical chunk lane % 8, which holds logical chunk pc ^ ((r >> 1) & 7);
+    // with r = 8 window + lane / 8 that is c0, or c0 ^ 4 in an odd window).
+    auto window = [&](int q) { return q < Sh::LA ? wave * Sh::LA + q : wave * Sh::LB + q - Sh::LA; };
+    const int c0 = (lane & 7) ^ (lane >> 4);
+    uint32_t src[Sh::LPS];
+#pragma unroll
+    for (int q = 0; q < Sh::LPS; ++q) {
+        const int r = window(q) * 8 + lane / 8;
+        if (q < Sh::LA) {
+            const int64_t m = m0 + r % BM;
+            src[q] = (m < p.M) ? (uint32_t)(((int64_t)(r / BM) * p.as_l + m * p.as_m) * ES) : kOOB;
+        } else {
+            const int64_t n = n0 + r % BN;
+            src[q] = (n < p.N) ? (uint32_t)(((int64_t)(r / BN) * p.bs_l + n * p.bs_n) * ES) : kOOB;
+        }
+    }
+    auto buf = [&](int kb) { return smem + (kb & 1) * Sh::STAGE; };
+    auto issue = [&](int kb, int q) {
+        const int ch = c0 ^ ((window(q) & 1) << 2);
+        const uint32_t kofs = (uint32_t)kb * kDmaRB + ch * 16;
+        const uint32_t vo = (src[q] == kOOB || kofs >= kbytes) ? kOOB : src[q] + kofs;
+        auto *ldsp = (__attribute__((address_space(3))) void *)(
+            buf(kb) + (q < Sh::LA ? 0 : Sh::A_BYTES) + window(q) * 1024);
+        if (q < Sh::LA) __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, ldsp, 16, vo, 0, 0, 0);
+        else __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, ldsp, 16, vo, 0, 0, 0);
+    };
+
+    // The tile's scales (A's [L][BM], then B's [L][BN]: 2304 bytes) are
+    // fetched by dword DMA into the buffer of stage nkb, which holds no stage
+    // the tile still reads, at the start of the last stage: instruction
+    // u < 9 (wave u and wave u - 8) fetches entries 64 u .. 64 u + 63, the
+    // first 3 of A's scales, the next 6 of B's.
+    char *const scl = buf(nkb);
+    auto issue_scales = [&]() {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int u = q * Sh::NW + wave;
+            if (u >= L * (BM + BN) / 64) break;
+            const bool isa = u < L * BM / 64;
+            const int e = (isa ? u : u - L * BM / 64) * 64 + lane;
+            const int s = isa ? e / BM : e / BN;                 // slice
+            const int64_t rc = isa ? m0 + e % BM : n0 + e % BN;  // row of A / column of B
+            const int64_t ext = isa ? ((int64_t)(L - 1) * p.sas_l + (p.M - 1) * p.sas_m + 1)
+                                    : ((int64_t)(L - 1) * p.sbs_l + (p.N - 1) * p.sbs_n + 1);
+            const bool ok = rc < (isa ? p.M : p.N);
+            const uint32_t vo = ok ? (uint32_t)(((int64_t)s * (isa ? p.sas_l : p.sbs_l) +
+                                                 rc * (isa ? p.sas_m : p.sbs_n)) * 4)
+                                   : kOOB;
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)(isa ? p.sa + bidx * p.sas_b : p.sb + bidx * p.sbs_b), (short)0,
+                (int)(ext * 4 < 0x7FFFFFFF ? ext * 4 : 0x7FFFFFFF), 0x00020000);
+            auto *ldsp = (__attribute__((address_space(3))) void *)(scl + u * 256);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, ldsp, 4, vo, 0, 0, 0);
+        }
+    };
+    const float *sa_lds = (const float *)scl, *sb_lds = (const float *)(scl + L * BM * 4);
+
+    // prologue: stages 0 and 1; stage 0 must land before the first reads
+#pragma unroll
+    for (int q = 0; q < Sh::LPS; ++q) issue(0, q);
+    if (nkb > 1) {
+#pragma unroll
+        for (int q = 0; q < Sh::LPS; ++q) issue(1, q);
+        wait_vmcnt<Sh::LPS>();
+    } else {
+        wait_vmcnt<0>();
+    }
+    exec_barrier();
+
+    struct Frags {
+        i32x4 a[L];
+        i32x4 b[L];
+    };
+    Acc acc[L][L];
+#pragma unroll
+    for (int i = 0; i < L; ++i)
+#pragma unroll
+        for (int j = 0; j < L; ++j) acc[i][j] = MF::zero();
+
+    auto read_one = [&](int kb, int kk, int r, Frags &f) {
+        const int c = 2 * kk + h;
+        if (r < L) f.a[r] = *(const i32x4 *)(buf(kb) + rswz<kDmaRB>(r * BM + wm * 32 + lr, c));
+        else
+            f.b[r - L] = *(const i32x4 *)(buf(kb) + Sh::A_BYTES +
+                                          rswz<kDmaRB>((r - L) * BN + wn * 32 + lr, c));
+    };
+    // One K step: the reads of the next K step (stage rkb, step nkk) into
+    // `nxt`, issued first, then the 9 MFMAs of `cur` with, if `on`, DMA
+    // instructions [lo, hi) of stage dkb spread between them (lo and hi are
+    // constants at every call, so the spread folds at compile time).
+    auto step = [&](const Frags &cur, Frags &nxt, int rkb, int nkk, int dkb, bool on, int lo,
+                    int hi) {
+        const int cnt = hi - lo;
+#pragma unroll
+        for (int q = 0; q < 2 * L; ++q) read_one(rkb, nkk, q, nxt);
+#pragma unroll
+        for (int n = 0; n < L * L; ++n) {
+            const int i = n / L, j = n % L;
+            acc[i][j] = MF::run(cur.a[i], cur.b[j], acc[i][j]);
+#pragma unroll
+            for (int d = 0; d < Sh::P1; ++d) {
+                // instruction lo + d goes after MFMA (d * L * L) / cnt
+                if (d < cnt && (d * L * L) / cnt == n && on) issue(dkb, lo + d);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    Frags f0, f1;
+    if (nkb > 0) {
+#pragma unroll
+        for (int q = 0; q < 2 * L; ++q) read_one(0, 0, q, f0);
+    }
+    static_assert(kDmaRB / 32 == 4, "four 32-byte K steps per stage");
+    if (nkb == 0) issue_scales();
+    for (int kb = 0; kb < nkb; ++kb) {
+        const bool nb = kb + 1 < nkb, n2 = kb + 2 < nkb;
+        // no DMA is outstanding in the last stage: its waits are unaffected
+        if (!nb) issue_scales();
+        // the rest of stage kb + 1 (stage 1 went out whole in the prologue)
+        step(f0, f1, kb, 1, kb + 1, nb && kb >= 1, Sh::P1, Sh::LPS);
+        step(f1, f0, kb, 2, kb + 1, false, 0, 0);
+        step(f0, f1, kb, 3, kb + 1, false, 0, 0);
+        if (nb) {
+            // stage kb + 1 is the only DMA outstanding; the barrier publishes
+            // every wave's DMA writes, and the lgkmcnt wait makes this wave's
+            // reads of stage kb complete before its buffer is refilled
+            wait_vmcnt<0>();
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            exec_barrier();
+        }
+        // the last step reads stage kb + 1's step 0 (unused past the end)
+        step(f1, f0, kb + 1, 0, kb + 2, n2, 0, Sh::P1);
+    }
+
+    // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
+    wait_vmcnt<0>();
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    exec_barrier();
+    const int ct = wn * 32 + lr;
+    const int64_t col = n0 + ct;
+    const int64_t cbase = bidx * p.cs_b;
+    float sbv[L];
+#pragma unroll
+    for (int j = 0; j < L; ++j) sbv[j] = sb_lds[j * BN + ct];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int rt = wm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        const int64_t row = m0 + rt;
+        OA out = (OA)0;
+#pragma unroll
+        for (int i = 0; i < L; ++i) {
+            const float sai = sa_lds[i * BM + rt];
+#pragma unroll
+            for (int j = 0; j < L; ++j) {
+                // fl32(fl32(fl32(acc) * sa_i) * sb_j), summed i-major, j-minor
+                const float t1 = MF::to_f32(acc[i][j][r]) * sai;
+                out = out + (OA)(t1 * sbv[j]);
+            }
+        }
+        if (col < p.N && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // A-direct variant.  The four waves are stacked along M (workgroup tile
 // 128 x 32*NI); each wave streams ITS OWN 32 rows of every A slice from global
 // memory straight into VGPRs (no LDS), and only B, which all four waves share,
@@ -1486,17 +1728,24 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype) {
     plan.ni = ni;
     plan.group_m = 8;
     const int es = slice_dtype == 4 ? 1 : slice_dtype == 1 ? 4 : 2;
-    // OZK_GEMM_KERNEL=staged|dma|ad|pair|ring forces a kernel (tests cover
+    // OZK_GEMM_KERNEL=staged|dma|ad|pair|ring|wide forces a kernel (tests cover
     // every one at small sizes).  By default, when both operands fit the
-    // 31-bit buffer offsets of the LDS-DMA kernels: the ring kernel for
-    // L = 3, 4 (64 x 64 tiles) and for L = 2 on grids of 256 or more 128 x 128
-    // tiles, the pair-split kernel for L > 4, the 2 x 2 LDS-DMA kernel with its
-    // larger wave tiles otherwise; else the VGPR-staged kernel.
+    // 31-bit buffer offsets of the LDS-DMA kernels: for L = 3 the wide kernel
+    // on grids of 512 or more 64 x 128 tiles, the ring kernel for L = 3, 4
+    // (64 x 64 tiles) and for L = 2 on grids of 256 or more 128 x 128 tiles,
+    // the pair-split kernel for L > 4, the 2 x 2 LDS-DMA kernel with its larger
+    // wave tiles otherwise; else the VGPR-staged kernel.
+    // Wide vs ring at L = 3, cross-GEMM alone, M = N, batch 1: 0.65x / 0.78x
+    // the ring's rate at 32 / 128 wide tiles, 1.11-1.24x from 512 up (int8
+    // K = 8192 and fp16 K = 4096, M up to 8192; fp16 batch 16, 1024 x 1024,
+    // K = 2048: 1.16x).
     const bool fits = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es) >= 0 &&
                       dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es) >= 0;
+    const int64_t wide_tiles = p.batch * ((p.M + 63) / 64) * ((p.N + 127) / 128);
     plan.kind = !fits              ? kGemmStaged
                 : L <= 1           ? kGemmDMA
                 : L == 2           ? ((mi == 2 && ni == 2) ? kGemmRing : kGemmDMA)
+                : L == 3 && wide_tiles >= 512 ? kGemmWide
                 : L <= 4           ? kGemmRing
                                    : kGemmPair;
     if (L > 4) return plan;   // only the pair-split kernel, launched per i-row range
@@ -1507,6 +1756,7 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype) {
     else if (fits && forced("dma")) plan.kind = kGemmDMA;
     else if (fits && forced("pair")) plan.kind = L >= 3 ? kGemmPair : kGemmDMA;
     else if (fits && forced("ring")) plan.kind = L >= 2 ? kGemmRing : kGemmDMA;
+    else if (fits && forced("wide")) plan.kind = L == 3 ? kGemmWide : plan.kind;
     if (plan.kind == kGemmAD) plan.group_m = 2;
     return plan;
 }
@@ -1605,6 +1855,22 @@ static hipError_t launch_ring(const GemmParams &p, const GemmPlan &plan, hipStre
     return hipGetLastError();
 }
 
+template <typename ST, typename AccT>
+static hipError_t launch_wide(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
+    using Sh = WideShape;
+    auto kern = cross_gemm_wide_kernel<ST, AccT>;
+    static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
+    if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
+    const int es = (int)sizeof(ST);
+    const int64_t ea = dma_extent(p.as_l, p.as_m, Sh::L, p.M, p.K, es);
+    const int64_t eb = dma_extent(p.bs_l, p.bs_n, Sh::L, p.N, p.K, es);
+    const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
+    if (tiles == 0) return hipSuccess;
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(512), Sh::LDS_BYTES, st, p,
+                       plan.group_m, (uint32_t)ea, (uint32_t)eb);
+    return hipGetLastError();
+}
+
 // num_splits = 5..8: launches over consecutive i-rows (at most 16 pairs each,
 // so a wave group still holds 8 pairs), in i-major order, each continuing the
 // fp64 sum from C.  int8 / fp16 / bf16 slices with an fp64 outer accumulator.
@@ -1628,6 +1894,9 @@ template <typename ST, int L, int MI, int NI, typename AccT>
 static hipError_t launch_one(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     if constexpr (L >= 3) {
         if (plan.kind == kGemmPair) return launch_pair<ST, L, AccT, L>(p, plan, st, 0, 0);
+    }
+    if constexpr (L == 3) {
+        if (plan.kind == kGemmWide) return launch_wide<ST, AccT>(p, plan, st);
     }
     if constexpr (L >= 2 && L <= 4) {
         if (plan.kind == kGemmRing) return launch_ring<ST, L, AccT>(p, plan, st);

@@ -71,8 +71,10 @@ enum GemmKind {
     kGemmDMA = 1,     // LDS-DMA ring for A and B, 2 x 2 waves
     kGemmAD = 2,      // A streamed into VGPRs, B by LDS-DMA, 4 x 1 waves
     kGemmPair = 3,    // LDS-DMA ring, 8 waves: 2 x 2 blocks x 2 halves of the slice pairs
-    kGemmRing = 4     // the pair split over a five-slot ring of half stages, DMA spread
+    kGemmRing = 4,    // the pair split over a five-slot ring of half stages, DMA spread
                       // between the MFMAs (num_splits 3 and 4)
+    kGemmWide = 5     // num_splits 3: 64 x 128 tiles, 8 waves each holding all 9 pairs
+                      // of a 32 x 32 block, two whole stages in the LDS
 };
 struct GemmPlan {
     int mi, ni;       // 2 x 2 kernels: wave tile = (32*mi) x (32*ni)

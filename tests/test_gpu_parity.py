@@ -285,14 +285,14 @@ def test_ozaki_matmul_degenerate_shapes(gpu):
                          torch.randn(0, 3, dtype=torch.float64, device=gpu), 2, torch.int8)
 
 
-@pytest.mark.parametrize("kernel", ["staged", "dma", "ad", "pair", "ring"])
+@pytest.mark.parametrize("kernel", ["staged", "dma", "ad", "pair", "ring", "wide"])
 @pytest.mark.parametrize("L", [1, 2, 3, 4])
 def test_cross_gemm_each_kernel_bitexact(oracle, gpu, L, kernel, monkeypatch):
     """Every cross-GEMM kernel, forced: the VGPR-staged one (taken when an
     operand's extent exceeds the 31-bit buffer offsets of the LDS-DMA kernels),
-    the 2 x 2 LDS-DMA kernel, the A-direct kernel, the pair-split kernel and
-    its five-slot ring form (L >= 3; for L <= 2 the request falls back to the
-    2 x 2 kernel)."""
+    the 2 x 2 LDS-DMA kernel, the A-direct kernel, the pair-split kernel, its
+    five-slot ring form (L >= 3; for L <= 2 the request falls back to the
+    2 x 2 kernel) and the wide kernel (L = 3; otherwise the default kernel)."""
     import ozaki_triton_amd as ozk
     monkeypatch.setenv("OZK_GEMM_KERNEL", kernel)
     g = torch.Generator().manual_seed(77 + L)
@@ -332,6 +332,66 @@ def test_ring_kernel_stage_counts(oracle, gpu, L, K, sdt, monkeypatch):
     else:
         monkeypatch.setenv("OZK_GEMM_KERNEL", "pair" if L >= 3 else "dma")
         assert_bitwise_equal(C, to_np(ozk.cross_gemm(*args)), f"{kernel} vs pair fp16 L{L} K{K}")
+
+
+@pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
+@pytest.mark.parametrize("MN", [(130, 200), (64, 128), (200, 136), (1, 300)])
+@pytest.mark.parametrize("K", [16, 128, 200, 300, 520, 1040, 2064])
+def test_wide_kernel_stage_counts(oracle, gpu, K, MN, sdt, monkeypatch):
+    """The num_splits 3 wide kernel (64 x 128 tiles, every wave holding all 9
+    pairs of its 32 x 32 block, two whole stages in the LDS) over 1 to 17
+    stages of 128 bytes of K (the prologue fetches stages 0 and 1, the loop
+    fetches stage kb + 2 after the barrier of stage kb, the last stage fetches
+    the tile's scales into the free buffer), with M and N cutting tiles, and
+    batch 2: int8 bit-exact against the oracle, fp16 bit-identical to the pair
+    kernel, which runs the same MFMAs per accumulator in the same order."""
+    import ozaki_triton_amd as ozk
+    L, (M, N) = 3, MN
+    g = torch.Generator().manual_seed(K * 10 + M + N)
+    As, BsT, sa, sb = _random_slices(g, 2, L, M, N, K, sdt)
+    args = (As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), L, torch.float64)
+    monkeypatch.setenv("OZK_GEMM_KERNEL", "wide")
+    C = to_np(ozk.cross_gemm(*args))
+    if sdt == torch.int8:
+        for b in range(2):
+            want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[b]), to_np(sa[b]), to_np(sb[b]),
+                                     "float64")
+            assert_bitwise_equal(C[b], want, f"wide K{K} M{M} N{N} b{b}")
+    else:
+        monkeypatch.setenv("OZK_GEMM_KERNEL", "pair")
+        assert_bitwise_equal(C, to_np(ozk.cross_gemm(*args)), f"wide vs pair fp16 K{K} M{M} N{N}")
+
+
+@pytest.mark.parametrize("out", [torch.float64, torch.float32, torch.float16, torch.bfloat16,
+                                 torch.int8])
+@pytest.mark.parametrize("sdt", [torch.int8, torch.float16, torch.bfloat16, torch.float32])
+def test_wide_kernel_dtypes(oracle, gpu, sdt, out, monkeypatch):
+    """The wide kernel for every slice and output dtype, batched, with a
+    broadcast (batch stride 0) B: int8 slices bit-exact against the oracle;
+    float slices bit-identical to the pair kernel."""
+    import ozaki_triton_amd as ozk
+    L = 3
+    g = torch.Generator().manual_seed(ALL_SLICES.index(sdt) * 7 + len(str(out)) + 500)
+    M, N, K = 100, 150, 400
+    As, BsT, sa, sb = _random_slices(g, 2, L, M, N, K,
+                                     torch.int8 if sdt == torch.int8 else torch.float16)
+    if sdt != torch.int8:
+        As, BsT = As.to(sdt), BsT.to(sdt)
+    if out in (torch.float16, torch.bfloat16, torch.int8):
+        sa = sa * 2.0 ** (12 if sdt == torch.int8 else 2)
+    Bd = BsT[:1].to(gpu).expand(2, -1, -1, -1).transpose(-1, -2)   # broadcast B
+    sbd = sb[:1].to(gpu).expand(2, -1, -1)
+    args = (As.to(gpu), Bd, sa.to(gpu), sbd, L, out)
+    monkeypatch.setenv("OZK_GEMM_KERNEL", "wide")
+    C = to_np(ozk.cross_gemm(*args))
+    if sdt == torch.int8:
+        for b in range(2):
+            want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[0]), to_np(sa[b]), to_np(sb[0]),
+                                     NAME_OF[out])
+            assert_bitwise_equal(C[b], want, f"wide {sdt} {out} b{b}")
+    else:
+        monkeypatch.setenv("OZK_GEMM_KERNEL", "pair")
+        assert_bitwise_equal(C, to_np(ozk.cross_gemm(*args)), f"wide vs pair {sdt} {out}")
 
 
 @pytest.mark.parametrize("out", [torch.float64, torch.float32, torch.float16, torch.bfloat16,
@@ -673,13 +733,16 @@ def test_more_splits_unsupported_combination_raises(gpu):
     (1, 1, 2048, 2048),    # 64 x 128
     (2, 1, 2048, 2048),    # L = 2: the ring kernel's 128 x 128 tiles (256 of them)
     (2, 1, 1024, 1024),    # L = 2: 64 x 64 (LDS-DMA kernel)
+    (3, 1, 2048, 2048),    # L = 3: the wide kernel's 64 x 128 tiles (512 of them)
+    (3, 1, 2048, 1920),    # L = 3: 480 wide tiles, so the ring kernel's 64 x 64
 ])
 def test_tile_table_shrink_steps(oracle, gpu, sdt, L, batch, M, N):
     """The tile table (plan_gemm) shrinks 128 x 256 tiles for grids under 512
     workgroups, N first while it is the larger side: every (rows, columns)
     step it can stop at has a kernel.  (An earlier order stopped at 128 x 64,
-    which no kernel took: the launch failed.)  Sampled blocks against the
-    oracle, K = 256."""
+    which no kernel took: the launch failed.)  At num_splits 3 it takes the
+    wide kernel from 512 of its tiles on.  Sampled blocks against the oracle,
+    K = 256."""
     import ozaki_triton_amd as ozk
     K = 256
     A, B = c3_like((batch, M, K), (batch, K, N), seed=M + N + L, dtype=torch.float32)
@@ -707,7 +770,7 @@ def test_split_columns_default_plan(oracle, gpu, xdt, sdt, batch, N, K):
                  f"default {xdt} {sdt} b{batch} {N}x{K}")
 
 
-@pytest.mark.parametrize("kernel", ["", "dma", "ring", "pair", "ad", "staged"])
+@pytest.mark.parametrize("kernel", ["", "dma", "ring", "pair", "ad", "staged", "wide"])
 @pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
 @pytest.mark.parametrize("K", [1, 2, 3, 5, 7, 9, 255, 257, 1003])
 def test_packed_rows_last_piece(oracle, gpu, kernel, sdt, K, monkeypatch):
@@ -721,7 +784,7 @@ def test_packed_rows_last_piece(oracle, gpu, kernel, sdt, K, monkeypatch):
     import ozaki_triton_amd as ozk
     if kernel:
         monkeypatch.setenv("OZK_GEMM_KERNEL", kernel)
-    L = 4 if kernel in ("ring", "pair", "ad") else 2
+    L = 3 if kernel == "wide" else 4 if kernel in ("ring", "pair", "ad") else 2
     A, B = c3_like((1, 33, K), (1, K, 20), seed=K + 100)
     C = ozk.ozaki_matmul(A.to(gpu), B.to(gpu), L, sdt)
     torch.cuda.synchronize()
