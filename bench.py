@@ -352,12 +352,13 @@ def main():
         peak, unit_c = PEAK_FP16_TFLOPS, "TFLOP/s"
     achieved = cross_ops / (t_cross * 1e-3) / 1e12
     # the library's default kernel choice (plan_gemm in ozk_gemm.hip): for
-    # L = 3 the wide kernel on a grid of at least 512 64 x 128 tiles, the
-    # five-slot ring kernel for L = 3, 4 and for L = 2 on a grid of at least 256
-    # 128 x 128 tiles, the pair-split kernel for L > 4, the 2 x 2 LDS-DMA kernel
-    # otherwise
+    # L = 3 the wide kernel where its rounds of 256 workgroups take less time
+    # (12 / 7 of a ring round each), the five-slot ring kernel for L = 3, 4
+    # and for L = 2 on a grid of at least 256 128 x 128 tiles, the pair-split
+    # kernel for L > 4, the 2 x 2 LDS-DMA kernel otherwise
     big2 = batch * -(-M // 128) * -(-N // 128) >= 256
-    wide3 = batch * -(-M // 64) * -(-N // 128) >= 512
+    wide3 = (12 * -(-(batch * -(-M // 64) * -(-N // 128)) // 256)
+             < 7 * -(-(batch * -(-M // 64) * -(-N // 64)) // 256))
     gemm_kernel = ("cross_gemm_wide_kernel" if L == 3 and wide3 else
                    "cross_gemm_ring_kernel" if 3 <= L <= 4 or (L == 2 and big2) else
                    "cross_gemm_pair_kernel" if L > 4 else "cross_gemm_dma_kernel")

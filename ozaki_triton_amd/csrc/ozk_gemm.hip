@@ -1731,21 +1731,28 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype) {
     // OZK_GEMM_KERNEL=staged|dma|ad|pair|ring|wide forces a kernel (tests cover
     // every one at small sizes).  By default, when both operands fit the
     // 31-bit buffer offsets of the LDS-DMA kernels: for L = 3 the wide kernel
-    // on grids of 512 or more 64 x 128 tiles, the ring kernel for L = 3, 4
+    // where it finishes its grid sooner (below), the ring kernel for L = 3, 4
     // (64 x 64 tiles) and for L = 2 on grids of 256 or more 128 x 128 tiles,
     // the pair-split kernel for L > 4, the 2 x 2 LDS-DMA kernel with its larger
     // wave tiles otherwise; else the VGPR-staged kernel.
-    // Wide vs ring at L = 3, cross-GEMM alone, M = N, batch 1: 0.65x / 0.78x
-    // the ring's rate at 32 / 128 wide tiles, 1.11-1.24x from 512 up (int8
-    // K = 8192 and fp16 K = 4096, M up to 8192; fp16 batch 16, 1024 x 1024,
-    // K = 2048: 1.16x).
     const bool fits = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es) >= 0 &&
                       dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es) >= 0;
-    const int64_t wide_tiles = p.batch * ((p.M + 63) / 64) * ((p.N + 127) / 128);
+    // Both L = 3 kernels run one workgroup per CU (144 KB of LDS each), so a
+    // grid takes ceil(tiles / 256) rounds.  A wide tile (64 x 128) does twice
+    // a ring tile's (64 x 64) work at 1.11-1.24x its rate: about 12/7 of its
+    // time.  Measured (cross-GEMM alone, int8 K = 8192 and fp16 K = 4096),
+    // wide / ring rate by wide tiles: 32: 0.65, 128: 0.78, 200: 1.20,
+    // 256: 1.14, 288: 0.95, 384: 1.01-1.03, 480: 1.16-1.18, 512 to 8192:
+    // 1.11-1.24; the rule below picks the faster one at each of these except
+    // 384 (within 3%).
+    constexpr int64_t kCUs = 256;
+    const int64_t wide_rounds = (p.batch * ((p.M + 63) / 64) * ((p.N + 127) / 128) + kCUs - 1) / kCUs;
+    const int64_t ring_rounds = (nt(1, 1) + kCUs - 1) / kCUs;
+    const bool wide3 = L == 3 && 12 * wide_rounds < 7 * ring_rounds;
     plan.kind = !fits              ? kGemmStaged
                 : L <= 1           ? kGemmDMA
                 : L == 2           ? ((mi == 2 && ni == 2) ? kGemmRing : kGemmDMA)
-                : L == 3 && wide_tiles >= 512 ? kGemmWide
+                : wide3            ? kGemmWide
                 : L <= 4           ? kGemmRing
                                    : kGemmPair;
     if (L > 4) return plan;   // only the pair-split kernel, launched per i-row range

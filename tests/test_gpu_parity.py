@@ -734,15 +734,17 @@ def test_more_splits_unsupported_combination_raises(gpu):
     (2, 1, 2048, 2048),    # L = 2: the ring kernel's 128 x 128 tiles (256 of them)
     (2, 1, 1024, 1024),    # L = 2: 64 x 64 (LDS-DMA kernel)
     (3, 1, 2048, 2048),    # L = 3: the wide kernel's 64 x 128 tiles (512 of them)
-    (3, 1, 2048, 1920),    # L = 3: 480 wide tiles, so the ring kernel's 64 x 64
+    (3, 1, 1280, 1280),    # L = 3: wide (200 tiles, one round against the ring's two)
+    (3, 1, 1536, 1536),    # L = 3: ring (288 wide tiles take two rounds, 576 ring tiles three)
+    (3, 2, 1024, 1000),    # L = 3: wide, batch 2, N cutting a tile
 ])
 def test_tile_table_shrink_steps(oracle, gpu, sdt, L, batch, M, N):
     """The tile table (plan_gemm) shrinks 128 x 256 tiles for grids under 512
     workgroups, N first while it is the larger side: every (rows, columns)
     step it can stop at has a kernel.  (An earlier order stopped at 128 x 64,
     which no kernel took: the launch failed.)  At num_splits 3 it takes the
-    wide kernel from 512 of its tiles on.  Sampled blocks against the oracle,
-    K = 256."""
+    wide kernel where its rounds of 256 tiles finish sooner than the ring
+    kernel's.  Sampled blocks against the oracle, K = 256."""
     import ozaki_triton_amd as ozk
     K = 256
     A, B = c3_like((batch, M, K), (batch, K, N), seed=M + N + L, dtype=torch.float32)
