@@ -20,7 +20,9 @@
  *     how much.
  *   - Calls are re-entrant and thread-safe.  The only process-wide state is,
  *     per cross-GEMM kernel, an atomic record of the devices on which its
- *     dynamic-LDS limit has been raised (hipFuncSetAttribute, once per device).
+ *     dynamic-LDS limit has been raised (hipFuncSetAttribute, once per device),
+ *     each device's compute-unit count (asked once), and the sticky device
+ *     status word (ozk_device_status).
  */
 #ifndef OZAKI_AMD_H
 #define OZAKI_AMD_H
@@ -53,7 +55,10 @@ enum {
     OZK_ERR_ALPHA = -5,       /* alpha < 1 (K too large for the accumulator) */
     OZK_ERR_WORKSPACE = -6,   /* workspace missing, too small or not 16-byte aligned */
     OZK_ERR_LAUNCH = -7,      /* a HIP launch failed (hipGetLastError) */
-    OZK_ERR_ACCUM = -8        /* unsupported dot accumulator dtype */
+    OZK_ERR_ACCUM = -8,       /* unsupported dot accumulator dtype */
+    OZK_ERR_DEVICE_WAIT = -9  /* (ozk_device_status) a cooperative split wait on the
+                                 device gave up; that split's scales, and so the C
+                                 computed from them, are NaN */
 };
 
 /* The reference's ozaki_matmul asserts num_splits <= 4 (ozaki_triton.py:563),
@@ -67,6 +72,19 @@ const char *ozk_strerror(int status);
 
 /* ABI version: major * 10000 + minor * 100 + patch. */
 int ozk_version(void);
+
+/*
+ * Sticky device status -- no counterpart in the reference, whose kernels have
+ * no bounded waits.  The cooperative split kernels (long columns of B, long
+ * rows of A) combine their level maxima across workgroups with waits bounded
+ * at 2 s.  A wait that gives up makes every scale of that split NaN (so C is
+ * NaN, never silently wrong) and sets a per-device status word.  This call
+ * waits for `stream`, reads the current device's word into *status_out
+ * (OZK_OK or OZK_ERR_DEVICE_WAIT) and clears it when `clear` is non-zero.
+ * Calls are asynchronous, so a failure is seen by the first status read
+ * after the call that failed.
+ */
+int ozk_device_status(int clear, int *status_out, void *stream);
 
 /*
  * compute_split_bits -- replaces ozaki_triton.py:76-98.
@@ -91,11 +109,13 @@ int ozk_compute_split_bits(int64_t n, int slice_dtype, int dot_accum_dtype, int 
  * reference's fp32 residual buffer does.  B is split through its transposed
  * view (rows = columns of B, x_strides = {K*N, 1, N}).
  * Workspace (ozk_split_workspace_bytes()): 0 bytes for K-contiguous fp64 /
- * fp32 rows; for row-contiguous operands (the B^T view) 8 bytes per column
- * group (128 bytes of a row), level and K chunk of 512 or 1024 rows, through
- * which the workgroups of a column group exchange their level maxima; an fp32
- * copy of a narrow input, a transposed copy of a long column operand, or an
- * fp32 residual for odd layouts.
+ * fp32 rows up to 16384 long and for odd layouts; for row-contiguous operands
+ * (the B^T view) 8 bytes per column group (128 bytes of a row), level and K
+ * chunk of 512 or 1024 rows, through which the workgroups of a column group
+ * exchange their level maxima (likewise per row, level and chunk for longer
+ * rows), plus a status word; an fp32 copy of a narrow input, or a transposed
+ * copy of a long column operand.  The query sees no pointers: it sizes for
+ * 16-byte aligned X and slices, and a call with other pointers needs no more.
  */
 int ozk_split_workspace_bytes(int x_dtype, int64_t batch, int64_t rows, int64_t K,
                               const int64_t x_strides[3], int num_splits, int slice_dtype,

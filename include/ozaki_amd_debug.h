@@ -1,0 +1,72 @@
+/*
+ * ozaki_amd_debug.h -- test hooks of libozaki_amd.so.
+ *
+ * None of these has a counterpart in the reference (WhFanatic/Ozaki_triton):
+ * its kernels are chosen by an autotuner and it has no bounded waits.  They
+ * exist so that tests can run every kernel and every error path, and so that
+ * tools can name the kernel a call would use.  Product code never needs them.
+ *
+ * The force settings live in thread-local storage: they apply to calls made
+ * from the host thread that set them, and to nothing else.  The library reads
+ * no environment variable.
+ */
+#ifndef OZAKI_AMD_DEBUG_H
+#define OZAKI_AMD_DEBUG_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * Force the cross-GEMM kernel of later calls on this thread: one of "staged",
+ * "dma", "ad", "pair", "ring", "wide", or NULL / "" for the planner's
+ * choice.  A kernel that cannot take a call (operand extents, slice count) is
+ * not used for it.  Returns OZK_ERR_DTYPE for an unknown name.
+ */
+int ozk_debug_force_gemm_kernel(const char *name);
+
+/*
+ * Force the split kernel of later calls on this thread: "coop", "strip",
+ * "transpose", "generic" (column operands), "rows", "rowscoop" (row
+ * operands), or NULL / "" for the planner's choice.  A path whose layout
+ * requirements fail is not taken.  Returns OZK_ERR_DTYPE for an unknown name.
+ */
+int ozk_debug_force_split_kernel(const char *name);
+
+/*
+ * on != 0: every cooperative split wait of later calls on this thread gives
+ * up at its first check (it looks for a tag that is never written), so the
+ * timeout path runs: the split's scales become NaN and the sticky device
+ * status is set (ozk_device_status).  No kernel waits longer than one poll.
+ */
+int ozk_debug_force_coop_timeout(int on);
+
+/*
+ * The cross-GEMM kernel the planner would choose for K-contiguous,
+ * 16-byte aligned slice operands of this shape, as a name ("dma", "ring",
+ * "wide", "pair", "staged", "ad") written to *name_out (a static
+ * string).  cus: compute units to plan for (0: those of the current device).
+ */
+int ozk_debug_gemm_kernel(int64_t batch, int64_t M, int64_t N, int64_t K, int num_splits,
+                          int slice_dtype, int cus, const char **name_out);
+
+/*
+ * The split path the planner would choose for an operand described as in
+ * ozk_split (X and slices are only inspected for their alignment, never
+ * read), as a name ("rows", "rowscoop", "coop", "strip", "transpose",
+ * "transposerowscoop", "generic", "convert") written to *name_out (a static
+ * string), and the workspace bytes that plan needs to *bytes_out.
+ */
+int ozk_debug_split_kernel(const void *X, int x_dtype, int64_t batch, int64_t rows, int64_t K,
+                           const int64_t x_strides[3], int num_splits, int slice_dtype,
+                           const void *slices, const int64_t slice_strides[4],
+                           const char **name_out, size_t *bytes_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OZAKI_AMD_DEBUG_H */

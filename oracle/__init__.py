@@ -68,6 +68,8 @@ def lib() -> ctypes.CDLL:
         L.ozo_split.restype = i32
         L.ozo_cross_gemm.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, i32, vp, i32]
         L.ozo_cross_gemm.restype = i32
+        L.ozo_cross_gemm_skip.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, i32, vp, i32, i32]
+        L.ozo_cross_gemm_skip.restype = i32
         L.ozo_int8_pair_dots.argtypes = [vp, vp, i64, i64, i64, i32, vp]
         L.ozo_int8_pair_dots.restype = i32
         L.ozo_f64_to_f16_array.argtypes = [vp, vp, i64]
@@ -169,9 +171,11 @@ def split(X: np.ndarray, num_splits: int, alpha: int, slice_dtype):
 
 
 def cross_gemm(As: np.ndarray, Bs_T: np.ndarray, sa: np.ndarray, sb: np.ndarray,
-               out_dtype) -> np.ndarray:
+               out_dtype, skip_pair: int = -1) -> np.ndarray:
     """As [L, M, K], Bs_T [L, N, K] (B slices stored K-contiguous), sa [L, M],
-    sb [L, N] -> C [M, N] (ozaki_triton.py:357-452)."""
+    sb [L, N] -> C [M, N] (ozaki_triton.py:357-452).  skip_pair = i * L + j
+    leaves that pair's term out: a planted mistake for tests that must show
+    their checks catch a dropped pair (never used as a reference)."""
     As = np.ascontiguousarray(As)
     Bs_T = np.ascontiguousarray(Bs_T)
     sa = np.ascontiguousarray(sa, dtype=np.float32)
@@ -181,8 +185,8 @@ def cross_gemm(As: np.ndarray, Bs_T: np.ndarray, sa: np.ndarray, sb: np.ndarray,
     assert L == L2 and K == K2
     od = code_of(out_dtype)
     C = np.empty((M, N), dtype=_NP_OF[od])
-    rc = lib().ozo_cross_gemm(_ptr(As), _ptr(Bs_T), _ptr(sa), _ptr(sb), M, N, K, L,
-                              code_of(As.dtype), _ptr(C), od)
+    rc = lib().ozo_cross_gemm_skip(_ptr(As), _ptr(Bs_T), _ptr(sa), _ptr(sb), M, N, K, L,
+                                   code_of(As.dtype), _ptr(C), od, int(skip_pair))
     if rc != 0:
         raise RuntimeError(f"ozo_cross_gemm failed: {rc}")
     return C

@@ -222,7 +222,11 @@ static void quant_store(void *slices, int slice_dtype, size_t idx, double q, int
             float tf = (qf >= 0) ? qf + 0.5f : qf - 0.5f;
             t = tf;
         }
-        /* tl.clamp(x, -128, 127) then cast to int8 (fptosi: toward zero) */
+        /* tl.clamp(x, -128, 127) then cast to int8 (fptosi: toward zero).
+         * A NaN input quantises to 0: the Triton interpreter's np.clip keeps
+         * the NaN and its astype(int8) gives 0 on x86-64; what a GPU build of
+         * the reference gives is not pinned by any of its tests.            */
+        if (t != t) t = 0.0;
         if (t < -128.0) t = -128.0;
         if (t > 127.0) t = 127.0;
         int8_t v = (int8_t)(int)t;
@@ -346,9 +350,23 @@ static void store_out(void *C, int out_dtype, int64_t idx, float out)
  * fp16 / bf16 / fp32 slices: acc_ij is the binary64 dot product of the exact
  * slice values, i.e. an (almost) exact reference for the fp32 hardware
  * accumulation, which a GPU kernel can only match within a tolerance.         */
+int ozo_cross_gemm_skip(const void *As, const void *Bs, const float *sa, const float *sb,
+                        int64_t M, int64_t N, int64_t K, int L, int slice_dtype, void *C,
+                        int out_dtype, int skip_pair);
+
 int ozo_cross_gemm(const void *As, const void *Bs, const float *sa, const float *sb,
                    int64_t M, int64_t N, int64_t K, int L, int slice_dtype, void *C,
                    int out_dtype)
+{
+    return ozo_cross_gemm_skip(As, Bs, sa, sb, M, N, K, L, slice_dtype, C, out_dtype, -1);
+}
+
+/* The same with the term of pair i * L + j == skip_pair left out of the outer
+ * sum: a deliberately wrong result, which tests use to show that their checks
+ * catch a dropped slice pair (skip_pair = -1: the correct result).            */
+int ozo_cross_gemm_skip(const void *As, const void *Bs, const float *sa, const float *sb,
+                        int64_t M, int64_t N, int64_t K, int L, int slice_dtype, void *C,
+                        int out_dtype, int skip_pair)
 {
     if (slice_dtype < OZO_F32 || slice_dtype > OZO_I8 || out_dtype < OZO_F64 ||
         out_dtype > OZO_I8 || L < 0)
@@ -391,6 +409,7 @@ int ozo_cross_gemm(const void *As, const void *Bs, const float *sa, const float 
                 for (int i = 0; i < L; ++i) {
                     float si = sa[(size_t)i * M + m];
                     for (int j = 0; j < L; ++j) {
+                        if (i * L + j == skip_pair) continue;
                         float t1 = acc[i * L + j] * si;
                         float t2 = t1 * sb[(size_t)j * N + n];
                         out = out + (double)t2;
@@ -402,6 +421,7 @@ int ozo_cross_gemm(const void *As, const void *Bs, const float *sa, const float 
                 for (int i = 0; i < L; ++i) {
                     float si = sa[(size_t)i * M + m];
                     for (int j = 0; j < L; ++j) {
+                        if (i * L + j == skip_pair) continue;
                         float t1 = acc[i * L + j] * si;
                         float t2 = t1 * sb[(size_t)j * N + n];
                         out = out + t2;

@@ -13,6 +13,7 @@ from .ozaki import (  # noqa: F401
     _select_out_accum_dtype,
     compute_split_bits,
     cross_gemm,
+    device_status,
     ozaki_matmul,
     split_matrix,
 )

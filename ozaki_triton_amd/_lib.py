@@ -22,12 +22,14 @@ OZK_ERR_ALPHA = -5
 OZK_ERR_WORKSPACE = -6
 OZK_ERR_LAUNCH = -7
 OZK_ERR_ACCUM = -8
+OZK_ERR_DEVICE_WAIT = -9
 OZK_MAX_SPLITS = 8
 
 # every symbol include/ozaki_amd.h declares
 EXPORTED = (
     "ozk_strerror",
     "ozk_version",
+    "ozk_device_status",
     "ozk_compute_split_bits",
     "ozk_split_workspace_bytes",
     "ozk_split",
@@ -35,6 +37,15 @@ EXPORTED = (
     "ozk_cross_gemm",
     "ozk_matmul_workspace_bytes",
     "ozk_matmul",
+)
+
+# the test hooks of include/ozaki_amd_debug.h
+EXPORTED_DEBUG = (
+    "ozk_debug_force_gemm_kernel",
+    "ozk_debug_force_split_kernel",
+    "ozk_debug_force_coop_timeout",
+    "ozk_debug_gemm_kernel",
+    "ozk_debug_split_kernel",
 )
 
 _lib = None
@@ -63,6 +74,8 @@ def load() -> ctypes.CDLL:
     L.ozk_strerror.restype = ctypes.c_char_p
     L.ozk_version.argtypes = []
     L.ozk_version.restype = i32
+    L.ozk_device_status.argtypes = [i32, ctypes.POINTER(ctypes.c_int), vp]
+    L.ozk_device_status.restype = i32
     L.ozk_compute_split_bits.argtypes = [i64, i32, i32, ctypes.POINTER(ctypes.c_int)]
     L.ozk_compute_split_bits.restype = i32
     L.ozk_split_workspace_bytes.argtypes = [i32, i64, i64, i64, p64, i32, i32, p64,
@@ -83,6 +96,19 @@ def load() -> ctypes.CDLL:
     L.ozk_matmul.argtypes = [vp, p64, vp, p64, i32, i64, i64, i64, i64, i32, i32, vp, p64, vp,
                              sz, ctypes.POINTER(ctypes.c_void_p), vp]
     L.ozk_matmul.restype = i32
+    cp = ctypes.c_char_p
+    L.ozk_debug_force_gemm_kernel.argtypes = [cp]
+    L.ozk_debug_force_gemm_kernel.restype = i32
+    L.ozk_debug_force_split_kernel.argtypes = [cp]
+    L.ozk_debug_force_split_kernel.restype = i32
+    L.ozk_debug_force_coop_timeout.argtypes = [i32]
+    L.ozk_debug_force_coop_timeout.restype = i32
+    L.ozk_debug_gemm_kernel.argtypes = [i64, i64, i64, i64, i32, i32, i32,
+                                        ctypes.POINTER(ctypes.c_char_p)]
+    L.ozk_debug_gemm_kernel.restype = i32
+    L.ozk_debug_split_kernel.argtypes = [vp, i32, i64, i64, i64, p64, i32, i32, vp, p64,
+                                         ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(sz)]
+    L.ozk_debug_split_kernel.restype = i32
     _lib = L
     return L
 
@@ -99,3 +125,43 @@ def i64arr(vals) -> ctypes.Array:
 def check(fn: str, status: int) -> None:
     if status != OZK_OK:
         raise OzakiLibError(fn, status)
+
+
+def device_status(clear: bool = True, stream=None) -> int:
+    """Wait for `stream` (a hipStream_t as int, or None for the null stream)
+    and return the sticky device status of the current device: OZK_OK, or
+    OZK_ERR_DEVICE_WAIT if a cooperative split wait gave up since the last
+    clear (the scales of that split, and the C computed from them, are NaN)."""
+    st = ctypes.c_int(0)
+    check("ozk_device_status", load().ozk_device_status(int(bool(clear)), ctypes.byref(st),
+                                                         ctypes.c_void_p(stream or 0)))
+    return int(st.value)
+
+
+class forced_kernels:
+    """Context manager for tests: force the cross-GEMM kernel (`gemm`: "staged",
+    "dma", "ad", "pair", "ring", "wide") and / or the split kernel (`split`:
+    "coop", "strip", "transpose", "generic", "rows", "rowscoop") of the calls
+    this host thread makes inside it, and optionally make every cooperative
+    split wait give up at once (`coop_timeout`).  Restores the defaults on exit."""
+
+    def __init__(self, gemm=None, split=None, coop_timeout=False):
+        self.gemm, self.split, self.coop_timeout = gemm, split, coop_timeout
+
+    def __enter__(self):
+        L = load()
+        if self.gemm is not None:
+            check("ozk_debug_force_gemm_kernel", L.ozk_debug_force_gemm_kernel(self.gemm.encode()))
+        if self.split is not None:
+            check("ozk_debug_force_split_kernel",
+                  L.ozk_debug_force_split_kernel(self.split.encode()))
+        if self.coop_timeout:
+            L.ozk_debug_force_coop_timeout(1)
+        return self
+
+    def __exit__(self, *exc):
+        L = load()
+        L.ozk_debug_force_gemm_kernel(None)
+        L.ozk_debug_force_split_kernel(None)
+        L.ozk_debug_force_coop_timeout(0)
+        return False

@@ -7,8 +7,18 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <string.h>
+
 #include "../../include/ozaki_amd.h"
+#include "../../include/ozaki_amd_debug.h"
 #include "ozk_internal.h"
+
+namespace ozk {
+DebugOverrides &debug_overrides() {
+    static thread_local DebugOverrides d;
+    return d;
+}
+}  // namespace ozk
 
 namespace {
 
@@ -77,11 +87,22 @@ const char *ozk_strerror(int status) {
     case OZK_ERR_WORKSPACE: return "workspace missing, too small or not 16-byte aligned";
     case OZK_ERR_LAUNCH: return "HIP launch failed";
     case OZK_ERR_ACCUM: return "unsupported dot accumulator dtype";
+    case OZK_ERR_DEVICE_WAIT:
+        return "a cooperative split wait gave up on the device (its scales and C are NaN)";
     default: return "unknown status";
     }
 }
 
-int ozk_version(void) { return 100; }
+int ozk_version(void) { return 200; }
+
+int ozk_device_status(int clear, int *status_out, void *stream) {
+    if (!status_out) return OZK_ERR_NULL;
+    unsigned v = 0;
+    if (ozk::read_device_status(&v, clear != 0, (hipStream_t)stream) != hipSuccess)
+        return OZK_ERR_LAUNCH;
+    *status_out = v ? OZK_ERR_DEVICE_WAIT : OZK_OK;
+    return OZK_OK;
+}
 
 int ozk_compute_split_bits(int64_t n, int slice_dtype, int dot_accum_dtype, int *alpha_out) {
     if (!alpha_out) return OZK_ERR_NULL;
@@ -279,6 +300,7 @@ struct MatmulLayout {
     int alpha;
     int64_t bA, bB;                                 // split batches (1 when broadcast)
     size_t a_sl, a_sc, b_sl, b_sc, scratch, pack;   // byte offsets
+    size_t scratch_bytes;                           // split scratch reserved
     size_t total;
     int64_t bt_strides[3];                          // B^T view of B
     int64_t ga[4], gb[4], gsa[3], gsb[3];           // cross-GEMM strides of the slices
@@ -287,15 +309,18 @@ struct MatmulLayout {
 int matmul_layout(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
                   const int64_t as[3], const int64_t bs[3], int L, int sd, MatmulLayout *o) {
     if (!is_input_dtype(dtype) || !is_slice_dtype(sd)) return OZK_ERR_DTYPE;
-    if (L < 0 || L > OZK_MAX_SPLITS) return OZK_ERR_SPLITS;
-    // more than 4 slices: the cross-GEMM takes them into an fp64 C only
-    if (L > 4 && (dtype != OZK_F64 || sd == OZK_F32)) return OZK_ERR_SPLITS;
     if (batch < 0 || M < 0 || N < 0 || K < 0) return OZK_ERR_SHAPE;
+    // alpha for every num_splits, 0 included: the reference calls
+    // compute_split_bits before splitting (ozaki_triton.py:580), so K = 0
+    // (log2(0)) and alpha < 1 fail whatever the slice count
     o->alpha = 0;
-    if (L > 0) {
+    {
         const int st = ozk_compute_split_bits(K, sd, sd == OZK_I8 ? OZK_I32 : OZK_F32, &o->alpha);
         if (st != OZK_OK) return st;
     }
+    if (L < 0 || L > OZK_MAX_SPLITS) return OZK_ERR_SPLITS;
+    // more than 4 slices: the cross-GEMM takes them into an fp64 C only
+    if (L > 4 && (dtype != OZK_F64 || sd == OZK_F32)) return OZK_ERR_SPLITS;
     o->bA = (batch > 1 && as[0] != 0) ? batch : 1;
     o->bB = (batch > 1 && bs[0] != 0) ? batch : 1;
     o->bt_strides[0] = bs[0];
@@ -308,6 +333,8 @@ int matmul_layout(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
     o->a_sc = off; off = align256(off + (size_t)(o->bA * L * M * 4));
     o->b_sl = off; off = align256(off + (size_t)(o->bB * L * N * K * ss));
     o->b_sc = off; off = align256(off + (size_t)(o->bB * L * N * 4));
+    // the split scratch is sized for 256-byte aligned operands; plan_split
+    // keeps the plan of any other pointer within that (ozk_matmul checks it)
     size_t scratch = 0;
     if (L > 0) {
         const int64_t dummy3[3] = {0, 0, 0};
@@ -320,6 +347,7 @@ int matmul_layout(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
         scratch = wa > wb ? wa : wb;
     }
     o->scratch = off; off = align256(off + scratch);
+    o->scratch_bytes = scratch;
     // cross-GEMM view of the slices (a batch-1 split is broadcast); they are
     // K-contiguous from a 256-byte aligned base, so only a row length that is
     // not a multiple of 16 bytes needs the packed copy
@@ -387,6 +415,8 @@ int ozk_matmul(const void *A, const int64_t a_strides[3], const void *B,
         ozk::SplitParams p = make_split_params(B, lay.bB, N, K, lay.bt_strides, L, lay.alpha,
                                                ws + lay.b_sl, bsl, (float *)(ws + lay.b_sc), bsc);
         const ozk::SplitPlan plan = ozk::plan_split(p, dtype, slice_dtype);
+        if (ozk::split_workspace_bytes(p, plan, dtype, slice_dtype) > lay.scratch_bytes)
+            return OZK_ERR_WORKSPACE;
         p.resid = (float *)(ws + lay.scratch);
         if (hipError_t he = ozk::launch_split(p, plan, dtype, slice_dtype, st)) return hip_status(he);
     }
@@ -395,6 +425,8 @@ int ozk_matmul(const void *A, const int64_t a_strides[3], const void *B,
         ozk::SplitParams p = make_split_params(A, lay.bA, M, K, a_strides, L, lay.alpha,
                                                ws + lay.a_sl, asl, (float *)(ws + lay.a_sc), asc);
         const ozk::SplitPlan plan = ozk::plan_split(p, dtype, slice_dtype);
+        if (ozk::split_workspace_bytes(p, plan, dtype, slice_dtype) > lay.scratch_bytes)
+            return OZK_ERR_WORKSPACE;
         p.resid = (float *)(ws + lay.scratch);
         if (hipError_t he = ozk::launch_split(p, plan, dtype, slice_dtype, st)) return hip_status(he);
     }
@@ -406,6 +438,111 @@ int ozk_matmul(const void *A, const int64_t a_strides[3], const void *B,
                         ws + lay.pack, workspace_bytes - lay.pack, stream);
     if (e != OZK_OK) return e;
     return record(events, 3, st);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Test hooks (include/ozaki_amd_debug.h)
+// ---------------------------------------------------------------------------
+namespace {
+struct Named {
+    const char *name;
+    int code;
+};
+const Named kGemmNames[] = {{"staged", ozk::kGemmStaged}, {"dma", ozk::kGemmDMA},
+                            {"ad", ozk::kGemmAD},         {"pair", ozk::kGemmPair},
+                            {"ring", ozk::kGemmRing},     {"wide", ozk::kGemmWide}};
+const Named kSplitNames[] = {{"coop", ozk::kForceSplitCoop},
+                             {"strip", ozk::kForceSplitStrip},
+                             {"transpose", ozk::kForceSplitTranspose},
+                             {"generic", ozk::kForceSplitGeneric},
+                             {"rows", ozk::kForceSplitRows},
+                             {"rowscoop", ozk::kForceSplitRowsCoop}};
+template <size_t N> int lookup(const Named (&t)[N], const char *name, int none, int *out) {
+    if (!name || !*name) {
+        *out = none;
+        return OZK_OK;
+    }
+    for (size_t i = 0; i < N; ++i)
+        if (strcmp(t[i].name, name) == 0) {
+            *out = t[i].code;
+            return OZK_OK;
+        }
+    return OZK_ERR_DTYPE;
+}
+template <size_t N> const char *name_of(const Named (&t)[N], int code) {
+    for (size_t i = 0; i < N; ++i)
+        if (t[i].code == code) return t[i].name;
+    return "?";
+}
+}  // namespace
+
+extern "C" {
+
+int ozk_debug_force_gemm_kernel(const char *name) {
+    return lookup(kGemmNames, name, ozk::kForceGemmNone, &ozk::debug_overrides().gemm);
+}
+
+int ozk_debug_force_split_kernel(const char *name) {
+    return lookup(kSplitNames, name, ozk::kForceSplitNone, &ozk::debug_overrides().split);
+}
+
+int ozk_debug_force_coop_timeout(int on) {
+    ozk::debug_overrides().coop_timeout = on != 0;
+    return OZK_OK;
+}
+
+int ozk_debug_gemm_kernel(int64_t batch, int64_t M, int64_t N, int64_t K, int num_splits,
+                          int slice_dtype, int cus, const char **name_out) {
+    if (!name_out) return OZK_ERR_NULL;
+    if (!is_slice_dtype(slice_dtype)) return OZK_ERR_DTYPE;
+    if (num_splits < 1 || num_splits > OZK_MAX_SPLITS) return OZK_ERR_SPLITS;
+    if (batch < 0 || M < 0 || N < 0 || K < 0) return OZK_ERR_SHAPE;
+    ozk::GemmParams p{};
+    const int64_t es = slice_size(slice_dtype);
+    const int64_t kp = round_up(K * es, 16) / es;
+    p.A = p.B = (const void *)(uintptr_t)256;
+    p.as_m = kp;
+    p.as_l = M * kp;
+    p.as_b = num_splits * M * kp;
+    p.bs_n = kp;
+    p.bs_l = N * kp;
+    p.bs_b = num_splits * N * kp;
+    p.batch = batch;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.out_dtype = OZK_F64;
+    *name_out = name_of(kGemmNames, ozk::plan_gemm(p, num_splits, slice_dtype, cus).kind);
+    return OZK_OK;
+}
+
+int ozk_debug_split_kernel(const void *X, int x_dtype, int64_t batch, int64_t rows, int64_t K,
+                           const int64_t x_strides[3], int num_splits, int slice_dtype,
+                           const void *slices, const int64_t slice_strides[4],
+                           const char **name_out, size_t *bytes_out) {
+    if (!name_out || !bytes_out || !x_strides || !slice_strides) return OZK_ERR_NULL;
+    if (!is_input_dtype(x_dtype) || !is_slice_dtype(slice_dtype)) return OZK_ERR_DTYPE;
+    if (num_splits < 1 || num_splits > OZK_MAX_SPLITS) return OZK_ERR_SPLITS;
+    if (batch < 0 || rows < 0 || K < 0) return OZK_ERR_SHAPE;
+    const int64_t dummy3[3] = {0, 0, 0};
+    ozk::SplitParams p = make_split_params(X, batch, rows, K, x_strides, num_splits, 1,
+                                           const_cast<void *>(slices), slice_strides, nullptr,
+                                           dummy3);
+    const ozk::SplitPlan plan = ozk::plan_split(p, x_dtype, slice_dtype);
+    *bytes_out = ozk::split_workspace_bytes(p, plan, x_dtype, slice_dtype);
+    switch (plan.path) {
+    case ozk::kSplitRows: *name_out = plan.variant == 100 ? "rowscoop" : "rows"; break;
+    case ozk::kSplitStrip: *name_out = "strip"; break;
+    case ozk::kSplitCoop: *name_out = "coop"; break;
+    case ozk::kSplitTransposeRows:
+        *name_out = plan.variant == 100 ? "transposerowscoop" : "transpose";
+        break;
+    case ozk::kSplitConvert: *name_out = "convert"; break;
+    default: *name_out = "generic";
+    }
+    return OZK_OK;
 }
 
 }  // extern "C"

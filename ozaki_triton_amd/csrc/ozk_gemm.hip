@@ -1705,7 +1705,21 @@ static int64_t dma_extent(int64_t s_l, int64_t s_r, int L, int64_t rows, int64_t
 // the wave tile is the largest whose L*L accumulators fit the register file
 // (L*L*MI*NI*16 <= 256 per lane), shrunk when the grid would leave CUs idle.
 // ---------------------------------------------------------------------------
-GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype) {
+// Compute units of the current device, asked once per device (256 on MI355X;
+// fewer on a partitioned device).
+static int device_cus() {
+    static std::atomic<int> cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
+        c = 256;
+    cached[dev].store(c, std::memory_order_relaxed);
+    return c;
+}
+
+GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
     GemmPlan plan{1, 1, 8, kGemmStaged};
     int mi = 1, ni = 1;
     if (L <= 1) { mi = 2; ni = 4; }
@@ -1728,7 +1742,7 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype) {
     plan.ni = ni;
     plan.group_m = 8;
     const int es = slice_dtype == 4 ? 1 : slice_dtype == 1 ? 4 : 2;
-    // OZK_GEMM_KERNEL=staged|dma|ad|pair|ring|wide forces a kernel (tests cover
+    // The test hooks (include/ozaki_amd_debug.h) force a kernel (tests cover
     // every one at small sizes).  By default, when both operands fit the
     // 31-bit buffer offsets of the LDS-DMA kernels: for L = 3 the wide kernel
     // where it finishes its grid sooner (below), the ring kernel for L = 3, 4
@@ -1745,7 +1759,7 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype) {
     // 256: 1.14, 288: 0.95, 384: 1.01-1.03, 480: 1.16-1.18, 512 to 8192:
     // 1.11-1.24; the rule below picks the faster one at each of these except
     // 384 (within 3%).
-    constexpr int64_t kCUs = 256;
+    const int64_t kCUs = cus > 0 ? cus : device_cus();
     const int64_t wide_rounds = (p.batch * ((p.M + 63) / 64) * ((p.N + 127) / 128) + kCUs - 1) / kCUs;
     const int64_t ring_rounds = (nt(1, 1) + kCUs - 1) / kCUs;
     const bool wide3 = L == 3 && 12 * wide_rounds < 7 * ring_rounds;
@@ -1756,14 +1770,14 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype) {
                 : L <= 4           ? kGemmRing
                                    : kGemmPair;
     if (L > 4) return plan;   // only the pair-split kernel, launched per i-row range
-    const char *env = getenv("OZK_GEMM_KERNEL");
-    auto forced = [&](const char *name) { return env && strcmp(env, name) == 0; };
-    if (forced("staged")) plan.kind = kGemmStaged;
-    else if (fits && forced("ad")) plan.kind = kGemmAD;
-    else if (fits && forced("dma")) plan.kind = kGemmDMA;
-    else if (fits && forced("pair")) plan.kind = L >= 3 ? kGemmPair : kGemmDMA;
-    else if (fits && forced("ring")) plan.kind = L >= 2 ? kGemmRing : kGemmDMA;
-    else if (fits && forced("wide")) plan.kind = L == 3 ? kGemmWide : plan.kind;
+    const int force = debug_overrides().gemm;
+    auto forced = [&](int kind) { return force == kind; };
+    if (forced(kGemmStaged)) plan.kind = kGemmStaged;
+    else if (fits && forced(kGemmAD)) plan.kind = kGemmAD;
+    else if (fits && forced(kGemmDMA)) plan.kind = kGemmDMA;
+    else if (fits && forced(kGemmPair)) plan.kind = L >= 3 ? kGemmPair : kGemmDMA;
+    else if (fits && forced(kGemmRing)) plan.kind = L >= 2 ? kGemmRing : kGemmDMA;
+    else if (fits && forced(kGemmWide)) plan.kind = L == 3 ? kGemmWide : plan.kind;
     if (plan.kind == kGemmAD) plan.group_m = 2;
     return plan;
 }

@@ -8,6 +8,28 @@
 
 namespace ozk {
 
+constexpr int kMaxLevels = 8;   // most slices a split or cross-GEMM takes (OZK_MAX_SPLITS)
+
+// Kernel choices forced by the test hooks of include/ozaki_amd_debug.h.  They
+// live in thread-local storage: a setting applies to calls made from the host
+// thread that set it, and nothing else (no environment variable is read).
+enum ForceGemm { kForceGemmNone = -1 };   // else a GemmKind
+enum ForceSplit {
+    kForceSplitNone = -1,
+    kForceSplitCoop = 0,
+    kForceSplitStrip = 1,
+    kForceSplitTranspose = 2,
+    kForceSplitGeneric = 3,
+    kForceSplitRows = 4,
+    kForceSplitRowsCoop = 5
+};
+struct DebugOverrides {
+    int gemm = kForceGemmNone;
+    int split = kForceSplitNone;
+    int coop_timeout = 0;   // 1: every cooperative wait gives up at once (its timeout path)
+};
+DebugOverrides &debug_overrides();
+
 // One split launch: X [batch, rows, K] -> slices [batch, L, rows, K] and
 // scales [batch, L, rows].  All strides in elements.
 struct SplitParams {
@@ -19,8 +41,9 @@ struct SplitParams {
     int64_t ss_b, ss_l, ss_r, ss_k;
     float *scales;
     int64_t cs_b, cs_l, cs_r;
-    float *resid;  // workspace: fp32 residual [batch, rows, K] (generic path) or the
-                   // transposed operand [batch, rows, K] (transpose + row path)
+    float *resid;  // workspace: exchange words of the cooperative kernels, the
+                   // transposed operand [batch, rows, K] (transpose + row path) or
+                   // the fp32 copy of a narrow input
 };
 
 enum SplitPath {
@@ -39,13 +62,23 @@ struct SplitPlan {
     SplitPath path;
     int variant;
 };
+// The plan depends on the pointers X and slices only through alignment.  The
+// workspace queries see no pointers and size for 256-byte aligned ones; a plan
+// for other pointers never needs more scratch than that (it falls back to the
+// generic kernel, which needs none).
 SplitPlan plan_split(const SplitParams &p, int x_dtype, int slice_dtype);
-// scratch the plan needs: fp32 residual (generic path, L > 1) or the
-// transposed operand (transpose + row path)
+// scratch the plan needs: the exchange words of the cooperative kernels and
+// their status word, the transposed operand (transpose + row path), the fp32
+// copy of a narrow input (none for the row, strip and generic kernels)
 size_t split_workspace_bytes(const SplitParams &p, const SplitPlan &plan, int x_dtype,
                              int slice_dtype);
 hipError_t launch_split(const SplitParams &p, const SplitPlan &plan, int x_dtype,
                         int slice_dtype, hipStream_t stream);
+
+// Sticky device status (per device): bit 0 is set when a cooperative split
+// wait gave up (the split's scales are then NaN).  read_device_status waits
+// for `stream`, reads the word of the current device and clears it if asked.
+hipError_t read_device_status(unsigned *out, bool clear, hipStream_t stream);
 
 // One cross-GEMM launch.  A slices [batch, L, M, K] and B slices presented as
 // [batch, L, N, K] (K-contiguous rows of B^T).  Strides in elements of the
@@ -81,7 +114,8 @@ struct GemmPlan {
     int group_m;      // tile-row group for L2 reuse
     int kind;         // GemmKind; the LDS-DMA kernels need 31-bit operand extents
 };
-GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype);
+// cus: compute units of the device (0: ask the current device, once per device)
+GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus = 0);
 hipError_t launch_gemm(const GemmParams &p, const GemmPlan &plan, int L, int slice_dtype,
                        hipStream_t stream);
 

@@ -55,8 +55,8 @@
 //   transpose_kernel    + a row kernel: columns longer than the cooperative
 //                       kernel takes, transposed into the workspace first.
 //   split_generic_kernel any strides and any K: one workgroup per row,
-//                       multi-pass over K with an fp32 residual in workspace
-//                       (the reference's own traffic pattern).
+//                       multi-pass over K, each level's residual recomputed
+//                       from the input (no workspace).
 #include "ozk_common.h"
 #include "ozk_internal.h"
 
@@ -104,7 +104,8 @@ template <> struct Quant<int8_t, kQF64> {
         const double q = x * c.inv64;
         // |q| <= 2^7 (1 + 2^-18): the sum stays above -129, so truncation
         // alone gives the reference's lower clamp
-        const double t = fmin(q + __builtin_copysign(0.5, q), 127.0);
+        double t = fmin(q + __builtin_copysign(0.5, q), 127.0);
+        t = (q == q) ? t : 0.0;   // NaN quantises to 0
         const int k = (int)t;
         *res = (float)__builtin_fma(-(double)k, c.s64, x);
         return (uint32_t)k;
@@ -113,7 +114,8 @@ template <> struct Quant<int8_t, kQF64> {
 template <> struct Quant<int8_t, kQExact> {
     OZK_DEV static uint32_t run(float r, const LevelScale &c, float *res) {
         const float q = __builtin_ldexpf(r, c.up);
-        const float t = fminf(__builtin_truncf(q + __builtin_copysignf(0x1.fffffep-2f, q)), 127.0f);
+        float t = fminf(__builtin_truncf(q + __builtin_copysignf(0x1.fffffep-2f, q)), 127.0f);
+        t = (q == q) ? t : 0.0f;   // NaN quantises to 0
         *res = __builtin_fmaf(-t, c.s, r);
         return (uint32_t)(int)t;
     }
@@ -121,8 +123,9 @@ template <> struct Quant<int8_t, kQExact> {
 template <> struct Quant<int8_t, kQF32> {
     OZK_DEV static uint32_t run(float x, const LevelScale &c, float *res) {
         const float q = __builtin_ldexpf(x, c.up);
-        const float t = __builtin_truncf(
+        float t = __builtin_truncf(
             __builtin_amdgcn_fmed3f(q + __builtin_copysignf(0.5f, q), -128.0f, 127.0f));
+        t = (q == q) ? t : 0.0f;   // NaN quantises to 0
         *res = __builtin_fmaf(-t, c.s, x);
         return (uint32_t)(int)t;
     }
@@ -535,9 +538,13 @@ __global__ __launch_bounds__(NT) void split_strip_kernel(SplitParams p) {
 //   * the members of a group are consecutive workgroup ids.  Workgroups are
 //     dispatched in id order, so the group of the oldest resident workgroup
 //     is entirely resident once P + 8 is below the workgroups that fit an
-//     XCD; the planner keeps P <= 128.  A wait that still runs out (about
-//     0.1 s) stores NaN scales instead of hanging.
-// slot must be zero at launch (the launcher clears it first).
+//     XCD; the planner keeps P <= 64.  A wait is still bounded (2 s of the
+//     100 MHz real-time counter): a member that gives up sets the launch's
+//     status word, member 0 stores NaN scales, and the poison kernel that
+//     follows the launch makes every scale of the split NaN and records the
+//     failure in the sticky device status (ozk_device_status).
+// slot and the status word after it must be zero at launch (the launcher
+// clears them first).
 // ---------------------------------------------------------------------------
 constexpr int kCoopNT = 256;
 constexpr int kCoopMaxP = 32;
@@ -547,16 +554,40 @@ constexpr int64_t kCoopMinColumnBytes = 64 * 1024;
 constexpr int kRowsCoopVariant = 100;
 constexpr int64_t kRowsCoopMinK = 16384;
 constexpr int kRowsCoopMaxP = 64;
-constexpr int kCoopSpin = 1 << 16;
+constexpr uint64_t kCoopTickLimit = 200000000ull;   // 2 s of the 100 MHz counter
 constexpr uint64_t kCoopTag = 1ull << 32;               // high word of a published maximum
 
 __global__ __launch_bounds__(256) void zero_u64_kernel(uint64_t *p, int64_t n) {
     for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0;
 }
 
+// Sticky device status: bit 0 = a cooperative wait gave up since the last
+// clear (read and cleared by read_device_status).
+__device__ uint32_t g_device_status = 0;
+
+// After a cooperative launch: if any member gave up its wait (status != 0),
+// every scale of the split becomes NaN, so no entry of C computed from it can
+// pass for a valid result, and the sticky device status records it.
+__global__ __launch_bounds__(256) void poison_scales_kernel(const uint32_t *status, float *scales,
+                                                            int64_t batch, int L, int64_t rows,
+                                                            int64_t cs_b, int64_t cs_l,
+                                                            int64_t cs_r) {
+    if (*status == 0) return;
+    const int64_t n = batch * L * rows;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * 256) {
+        const int64_t r = i % rows, l = (i / rows) % L, b = i / (rows * L);
+        scales[b * cs_b + l * cs_l + r * cs_r] = __int_as_float(0x7fc00000);
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0)
+        __hip_atomic_fetch_or(&g_device_status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 template <typename XT, typename ST, int RPL>
 __global__ __launch_bounds__(kCoopNT) void split_coop_kernel(SplitParams p, uint64_t *slot, int P,
-                                                             uint32_t want_tag, int spin_limit) {
+                                                             uint32_t want_tag,
+                                                             uint64_t tick_limit,
+                                                             uint32_t *status) {
     constexpr int NT = kCoopNT, NG = RPL / 4;
     constexpr int VEC = 16 / (int)sizeof(XT);
     constexpr int SW = 8 * VEC;          // columns per group
@@ -632,7 +663,8 @@ __global__ __launch_bounds__(kCoopNT) void split_coop_kernel(SplitParams p, uint
                                                      : (2ull << ((nw - 1 - lane) / 64)) - 1)
                                               : 0;
             float q = 0.0f;
-            for (int it = 0;; ++it) {
+            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+            for (;;) {
                 for (int n = 0; n < (nw + 63) / 64; ++n) {
                     const int i = lane + 64 * n;
                     if (i < nw && !((seen >> n) & 1)) {
@@ -645,8 +677,12 @@ __global__ __launch_bounds__(kCoopNT) void split_coop_kernel(SplitParams p, uint
                     }
                 }
                 if (__all(seen == want)) break;
-                if (it == spin_limit) {
-                    if (lane == 0) bad = 1;
+                if (__builtin_amdgcn_s_memrealtime() - t0 >= tick_limit) {
+                    if (lane == 0) {
+                        bad = 1;
+                        __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+                    }
                     break;
                 }
                 __builtin_amdgcn_s_sleep(1);
@@ -755,7 +791,8 @@ __global__ __launch_bounds__(kCoopNT) void split_coop_kernel(SplitParams p, uint
 template <typename XT, typename ST, int GW, int NC>
 __global__ __launch_bounds__(64 * GW) void split_rows_coop_kernel(SplitParams p, uint64_t *slot,
                                                                   int P, uint32_t want_tag,
-                                                                  int spin_limit) {
+                                                                  uint64_t tick_limit,
+                                                                  uint32_t *status) {
     constexpr int G = 64 * GW;
     constexpr int NE = 4 * NC;
     constexpr int CHR = NE * G;
@@ -800,7 +837,8 @@ __global__ __launch_bounds__(64 * GW) void split_rows_coop_kernel(SplitParams p,
                                        __HIP_MEMORY_SCOPE_AGENT);
                 bool seen = lane >= P;
                 float q = 0.0f;
-                for (int it = 0;; ++it) {
+                const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+                for (;;) {
                     if (!seen) {
                         const uint64_t w64 =
                             __hip_atomic_load(sl + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -810,8 +848,12 @@ __global__ __launch_bounds__(64 * GW) void split_rows_coop_kernel(SplitParams p,
                         }
                     }
                     if (__all(seen)) break;
-                    if (it == spin_limit) {
-                        if (lane == 0) bad = 1;
+                    if (__builtin_amdgcn_s_memrealtime() - t0 >= tick_limit) {
+                        if (lane == 0) {
+                            bad = 1;
+                            __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+                        }
                         break;
                     }
                     __builtin_amdgcn_s_sleep(1);
@@ -867,43 +909,49 @@ __global__ __launch_bounds__(64 * GW) void split_rows_coop_kernel(SplitParams p,
 }
 
 // ---------------------------------------------------------------------------
-// Generic split: one workgroup of 256 lanes per row, any strides, any K.
-// Level l reads src (X for l = 0, else the fp32 residual workspace) twice:
-// once for the row max, once to quantise; lane t always touches k = t + 256*i,
-// so a lane re-reads only residuals it wrote itself.
+// Generic split: one workgroup of 256 lanes per row, any strides, any K, no
+// workspace.  Level l sweeps the row twice (maximum, then quantise).  The
+// level-l source of an element is recomputed from the input with the scales
+// of levels < l, kept in LDS: the same chain of quantisations as the
+// reference's residual buffer (ozaki_triton.py:208-211), so the same bits,
+// with L(L+1) reads of the input instead of a residual written and re-read.
 // ---------------------------------------------------------------------------
 template <typename XT, typename ST>
 __global__ __launch_bounds__(256) void split_generic_kernel(SplitParams p) {
     __shared__ float red[2][1][4];
+    __shared__ LevelScale cs[kMaxLevels];
     const int t = threadIdx.x;
     const int64_t grow = blockIdx.x;
     const int64_t b = grow / p.rows;
     const int64_t r = grow % p.rows;
     const XT *xrow = (const XT *)p.X + b * p.xs_b + r * p.xs_r;
-    float *res = p.resid + (b * p.rows + r) * p.K;
     const int64_t srow = b * p.ss_b + r * p.ss_r;
-    const bool keep = p.L > 1;
 
-    float m = 0.0f;
-    for (int64_t k = t; k < p.K; k += 256) m = fmaxf(m, absf(xrow[k * p.xs_k]));
-    LevelScale c = level_scale(row_max<4, 1>(m, red, 0, 0, t), p.alpha);
-    if (t == 0) p.scales[b * p.cs_b + r * p.cs_r] = c.s;
-    for (int64_t k = t; k < p.K; k += 256) {
+    // the fp32 residual entering level l >= 1 of input value x
+    auto resid = [&](XT x, int l) {
         float rr;
-        const uint32_t qv = Quant<ST, Modes<XT>::first>::run(xrow[k * p.xs_k], c, &rr);
-        store1<ST>(p.slices, srow + k * p.ss_k, qv);
-        if (keep) res[k] = rr;
-    }
-    for (int l = 1; l < p.L; ++l) {
-        m = 0.0f;
-        for (int64_t k = t; k < p.K; k += 256) m = fmaxf(m, fabsf(res[k]));
-        c = level_scale(row_max<4, 1>(m, red, l & 1, 0, t), p.alpha);
-        if (t == 0) p.scales[b * p.cs_b + l * p.cs_l + r * p.cs_r] = c.s;
+        (void)Quant<ST, Modes<XT>::first>::run(x, cs[0], &rr);
+        for (int j = 1; j < l; ++j) (void)Quant<ST, Modes<XT>::rest>::run(rr, cs[j], &rr);
+        return rr;
+    };
+    for (int l = 0; l < p.L; ++l) {
+        float m = 0.0f;
         for (int64_t k = t; k < p.K; k += 256) {
+            const XT x = xrow[k * p.xs_k];
+            m = fmaxf(m, l == 0 ? absf(x) : fabsf(resid(x, l)));
+        }
+        const LevelScale c = level_scale(row_max<4, 1>(m, red, l & 1, 0, t), p.alpha);
+        if (t == 0) {
+            cs[l] = c;
+            p.scales[b * p.cs_b + l * p.cs_l + r * p.cs_r] = c.s;
+        }
+        __syncthreads();
+        for (int64_t k = t; k < p.K; k += 256) {
+            const XT x = xrow[k * p.xs_k];
             float rr;
-            const uint32_t qv = Quant<ST, Modes<XT>::rest>::run(res[k], c, &rr);
+            const uint32_t qv = (l == 0) ? Quant<ST, Modes<XT>::first>::run(x, c, &rr)
+                                         : Quant<ST, Modes<XT>::rest>::run(resid(x, l), c, &rr);
             store1<ST>(p.slices, srow + l * p.ss_l + k * p.ss_k, qv);
-            res[k] = rr;
         }
     }
 }
@@ -1058,10 +1106,16 @@ static int64_t rows_coop_members(int64_t K, int xsz) {
     const int64_t ch = rows_coop_chunk(xsz);
     return K <= 0 ? 1 : (K + ch - 1) / ch;
 }
-static size_t rows_coop_slot_bytes(const SplitParams &p, int xsz) {
+static int64_t rows_coop_slots(const SplitParams &p, int xsz) {
     const int64_t P = rows_coop_members(p.K, xsz);
-    return P > 1 ? (size_t)(p.batch * p.rows * p.L * P) * 8 : 0;
+    return P > 1 ? p.batch * p.rows * p.L * P : 0;
 }
+// exchange words plus the launch's status word (none without an exchange)
+static size_t slot_bytes(int64_t nslots) { return nslots > 0 ? (size_t)(nslots + 1) * 8 : 0; }
+static size_t rows_coop_slot_bytes(const SplitParams &p, int xsz) {
+    return slot_bytes(rows_coop_slots(p, xsz));
+}
+static size_t round256(size_t x) { return (x + 255) / 256 * 256; }
 
 static bool aligned(const void *ptr, int64_t bytes) {
     return ((uintptr_t)ptr % (uintptr_t)bytes) == 0;
@@ -1085,7 +1139,7 @@ static SplitParams converted_params(const SplitParams &p) {
     return q;
 }
 
-SplitPlan plan_split(const SplitParams &p, int x_dtype, int slice_dtype) {
+static SplitPlan plan_split_raw(const SplitParams &p, int x_dtype, int slice_dtype) {
     // narrow inputs: the reference loads them into its fp32 RES exactly
     // (ozaki_triton.py:188), so they are converted into the workspace first and
     // split as fp32 (X is replaced by the workspace at launch, which is 16-byte
@@ -1097,16 +1151,16 @@ SplitPlan plan_split(const SplitParams &p, int x_dtype, int slice_dtype) {
     const bool slice_ok = p.ss_k == 1 && aligned(p.slices, 4 * ssz) &&
                           (p.ss_r * ssz) % (4 * ssz) == 0 && (p.ss_l * ssz) % (4 * ssz) == 0 &&
                           (p.ss_b * ssz) % (4 * ssz) == 0;
-    // OZK_SPLIT_KERNEL=coop|strip|transpose|generic steers column operands off
-    // the default, =rows|rowscoop forces one of the two row kernels (tests
-    // cover every path); a path whose requirements fail is not taken
-    const char *env = getenv("OZK_SPLIT_KERNEL");
-    auto forced = [&](const char *name) { return env && strcmp(env, name) == 0; };
+    // the test hooks (include/ozaki_amd_debug.h) steer column operands to the
+    // coop / strip / transpose / generic path, or force one of the two row
+    // kernels; a path whose requirements fail is not taken
+    const int force = debug_overrides().split;
+    auto forced = [&](int which) { return force == which; };
     // long rows: the row kernel shared by workgroups
     const bool rows_coop = rows_coop_members(p.K, xsz) <= kRowsCoopMaxP &&
-                           (forced("rowscoop") || (!forced("rows") && p.K > kRowsCoopMinK));
+                           (forced(kForceSplitRowsCoop) || (!forced(kForceSplitRows) && p.K > kRowsCoopMinK));
     if (k4 && slice_ok && p.xs_k == 1 && aligned(p.X, 16) && (p.xs_r * xsz) % 16 == 0 &&
-        (p.xs_b * xsz) % 16 == 0 && !forced("generic")) {
+        (p.xs_b * xsz) % 16 == 0 && !forced(kForceSplitGeneric)) {
         if (rows_coop) return {kSplitRows, kRowsCoopVariant};
         for (int i = 0; i < kNumRowCfgs; ++i) {
             const RowCfg &c = kRowCfgs[i];
@@ -1123,14 +1177,14 @@ SplitPlan plan_split(const SplitParams &p, int x_dtype, int slice_dtype) {
     // 32 KB into int8 slices when there are at least 2048 of them (0.90-0.94x
     // the strip kernel's time at K = 4096, N = 2048..8192; 1.04x at N = 1024;
     // fp16 slices gain nothing there, fp32 columns below 64 KB lose 1.1-1.3x);
-    // OZK_SPLIT_KERNEL=coop takes it for any length it holds
+    // a forced coop takes it for any length it holds
     const bool coop_fits = cols_ok && coop_members(p.K, 64 / vec) <= kCoopMaxP;
-    const bool other = forced("strip") || forced("transpose") || forced("generic");
+    const bool other = forced(kForceSplitStrip) || forced(kForceSplitTranspose) || forced(kForceSplitGeneric);
     const bool coop_long = p.K * xsz >= kCoopMinColumnBytes ||
                            (xsz == 8 && ssz == 1 && p.K * xsz >= kCoopMinColumnBytes / 2 &&
                             p.batch * p.rows >= 2048);
-    if (coop_fits && (forced("coop") || (!other && coop_long))) return {kSplitCoop, 64 / vec};
-    if (cols_ok && !forced("transpose") && !forced("generic")) {
+    if (coop_fits && (forced(kForceSplitCoop) || (!other && coop_long))) return {kSplitCoop, 64 / vec};
+    if (cols_ok && !forced(kForceSplitTranspose) && !forced(kForceSplitGeneric)) {
         for (int i = 0; i < kNumStripCfgs; ++i) {
             const StripCfg &c = kStripCfgs[i];
             if (c.kpt * vec > 64) continue;
@@ -1139,7 +1193,7 @@ SplitPlan plan_split(const SplitParams &p, int x_dtype, int slice_dtype) {
     }
     // row-contiguous operand with a K too long for a resident strip: transpose
     // into the workspace, then the row kernel (if the row fits)
-    if (k4 && slice_ok && p.xs_r == 1 && (p.K * xsz) % 16 == 0 && !forced("generic")) {
+    if (k4 && slice_ok && p.xs_r == 1 && (p.K * xsz) % 16 == 0 && !forced(kForceSplitGeneric)) {
         if (rows_coop) return {kSplitTransposeRows, kRowsCoopVariant};
         for (int i = 0; i < kNumRowCfgs; ++i) {
             const RowCfg &c = kRowCfgs[i];
@@ -1148,6 +1202,22 @@ SplitPlan plan_split(const SplitParams &p, int x_dtype, int slice_dtype) {
         }
     }
     return {kSplitGeneric, 0};
+}
+
+
+SplitPlan plan_split(const SplitParams &p, int x_dtype, int slice_dtype) {
+    const SplitPlan plan = plan_split_raw(p, x_dtype, slice_dtype);
+    if (aligned(p.X, 16) && aligned(p.slices, 16)) return plan;   // the aligned plan
+    // other pointers: no more scratch than the workspace queries reserve for
+    // aligned ones, which see no pointers (the generic kernel needs none)
+    SplitParams q = p;
+    q.X = (const void *)(uintptr_t)256;
+    q.slices = (void *)(uintptr_t)256;
+    const SplitPlan ref = plan_split_raw(q, x_dtype, slice_dtype);
+    if (split_workspace_bytes(p, plan, x_dtype, slice_dtype) >
+        split_workspace_bytes(q, ref, x_dtype, slice_dtype))
+        return {kSplitGeneric, 0};
+    return plan;
 }
 
 // plan of the fp32 copy of a narrow input (its X is the 16-byte aligned
@@ -1163,44 +1233,70 @@ size_t split_workspace_bytes(const SplitParams &p, const SplitPlan &plan, int x_
     const int64_t n = p.batch * p.rows * p.K;
     if (plan.path == kSplitConvert) {
         const SplitPlan inner = converted_plan(p, slice_dtype);
-        return (size_t)(n * 4) + split_workspace_bytes(converted_params(p), inner, 1, slice_dtype);
+        const size_t in = split_workspace_bytes(converted_params(p), inner, 1, slice_dtype);
+        return in ? round256((size_t)(n * 4)) + in : (size_t)(n * 4);
     }
     if (plan.path == kSplitTransposeRows) {
         const size_t tb = (size_t)(n * dtype_size(x_dtype));
         if (plan.variant != kRowsCoopVariant) return tb;
-        return (tb + 255) / 256 * 256 + rows_coop_slot_bytes(p, dtype_size(x_dtype));
+        return round256(tb) + rows_coop_slot_bytes(p, dtype_size(x_dtype));
     }
     if (plan.path == kSplitRows && plan.variant == kRowsCoopVariant)
         return rows_coop_slot_bytes(p, dtype_size(x_dtype));
-    if (plan.path == kSplitCoop)
-        return (size_t)coop_slots(p, dtype_size(x_dtype), plan.variant) * 8;
-    if (plan.path == kSplitGeneric && p.L > 1) return (size_t)(n * 4);
+    if (plan.path == kSplitCoop) return slot_bytes(coop_slots(p, dtype_size(x_dtype), plan.variant));
     return 0;
+}
+
+// Clears n exchange words and the status word after them.
+static hipError_t clear_slots(uint64_t *slot, int64_t n, hipStream_t st) {
+    const int64_t zb = (n + 256) / 256 < 2048 ? (n + 256) / 256 : 2048;
+    hipLaunchKernelGGL(zero_u64_kernel, dim3((unsigned)zb), dim3(256), 0, st, slot, n + 1);
+    return hipGetLastError();
+}
+
+// Follows a cooperative launch whose status word is `status` (see
+// poison_scales_kernel).
+static hipError_t launch_poison(const SplitParams &p, const uint64_t *status, hipStream_t st) {
+    const int64_t n = p.batch * p.L * p.rows;
+    const int64_t nb = (n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024;
+    hipLaunchKernelGGL(poison_scales_kernel, dim3((unsigned)nb), dim3(256), 0, st,
+                       (const uint32_t *)status, p.scales, p.batch, p.L, p.rows, p.cs_b, p.cs_l,
+                       p.cs_r);
+    return hipGetLastError();
+}
+
+// The tag a wait looks for and its time limit: the test hook makes every wait
+// look for a tag that is never written and give up at its first check, so
+// the timeout path runs with no wait longer than one poll.
+struct WaitRule {
+    uint32_t tag;
+    uint64_t ticks;
+};
+static WaitRule wait_rule() {
+    const bool force = debug_overrides().coop_timeout != 0;
+    return {(uint32_t)(kCoopTag >> 32) + (force ? 1u : 0u), force ? 0ull : kCoopTickLimit};
 }
 
 template <typename XT, typename ST>
 static hipError_t launch_rows_coop(const SplitParams &p, uint64_t *slot, hipStream_t st) {
     const int xsz = (int)sizeof(XT);
     const int64_t P = rows_coop_members(p.K, xsz);
+    const int64_t n = rows_coop_slots(p, xsz);
+    uint32_t *status = nullptr;
     if (P > 1) {
-        const int64_t n = p.batch * p.rows * p.L * P;
-        const int64_t zb = (n + 255) / 256 < 2048 ? (n + 255) / 256 : 2048;
-        hipLaunchKernelGGL(zero_u64_kernel, dim3((unsigned)zb), dim3(256), 0, st, slot, n);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
+        if (hipError_t e = clear_slots(slot, n, st)) return e;
+        status = (uint32_t *)(slot + n);
     }
-    const char *tmo = getenv("OZK_SPLIT_COOP_TIMEOUT");   // tests only, as for the columns
-    const bool force_timeout = tmo && strcmp(tmo, "1") == 0;
-    const uint32_t tag = (uint32_t)(kCoopTag >> 32) + (force_timeout ? 1u : 0u);
-    const int spin = force_timeout ? 8 : kCoopSpin;
+    const WaitRule w = wait_rule();
     const dim3 grid((unsigned)(p.batch * p.rows * P)), block(256);
     if constexpr (sizeof(XT) == 8)
         hipLaunchKernelGGL((split_rows_coop_kernel<XT, ST, 4, 8>), grid, block, 0, st, p, slot,
-                           (int)P, tag, spin);
+                           (int)P, w.tag, w.ticks, status);
     else
         hipLaunchKernelGGL((split_rows_coop_kernel<XT, ST, 4, 16>), grid, block, 0, st, p, slot,
-                           (int)P, tag, spin);
-    return hipGetLastError();
+                           (int)P, w.tag, w.ticks, status);
+    if (hipError_t e = hipGetLastError()) return e;
+    return P > 1 ? launch_poison(p, slot + n, st) : hipSuccess;
 }
 
 template <typename XT, typename ST>
@@ -1265,26 +1361,21 @@ static hipError_t launch_typed(const SplitParams &p, const SplitPlan &plan, hipS
         const int64_t groups = p.batch * ((p.rows + SW - 1) / SW);
         const int64_t P = coop_members(p.K, rpl);
         uint64_t *slot = nullptr;
+        uint32_t *status = nullptr;
+        const int64_t n = coop_slots(p, (int)sizeof(XT), rpl);
         if (P > 1) {
             slot = (uint64_t *)p.resid;
-            const int64_t n = coop_slots(p, (int)sizeof(XT), rpl);
-            const int64_t zb = (n + 255) / 256 < 2048 ? (n + 255) / 256 : 2048;
-            hipLaunchKernelGGL(zero_u64_kernel, dim3((unsigned)zb), dim3(256), 0, st, slot, n);
-            hipError_t e = hipGetLastError();
-            if (e != hipSuccess) return e;
+            if (hipError_t e = clear_slots(slot, n, st)) return e;
+            status = (uint32_t *)(slot + n);
         }
         const dim3 grid((unsigned)(groups * P)), block(kCoopNT);
         constexpr int RPL = 64 / (16 / (int)sizeof(XT));
         if (rpl != RPL) return hipErrorInvalidValue;
-        // OZK_SPLIT_COOP_TIMEOUT=1 (tests only): every wait looks for a tag that
-        // is never written and gives up after 8 polls, so the timeout path runs
-        // and the multi-chunk scales come out NaN, with no wait longer than that
-        const char *tmo = getenv("OZK_SPLIT_COOP_TIMEOUT");
-        const bool force_timeout = tmo && strcmp(tmo, "1") == 0;
+        const WaitRule w = wait_rule();
         hipLaunchKernelGGL((split_coop_kernel<XT, ST, RPL>), grid, block, 0, st, p, slot, (int)P,
-                           (uint32_t)(kCoopTag >> 32) + (force_timeout ? 1u : 0u),
-                           force_timeout ? 8 : kCoopSpin);
-        return hipGetLastError();
+                           w.tag, w.ticks, status);
+        if (hipError_t e = hipGetLastError()) return e;
+        return P > 1 ? launch_poison(p, slot + n, st) : hipSuccess;
     }
     case kSplitTransposeRows: {
         XT *T = (XT *)p.resid;   // workspace [batch, rows, K]
@@ -1303,8 +1394,7 @@ static hipError_t launch_typed(const SplitParams &p, const SplitPlan &plan, hipS
         q.xs_k = 1;
         // the exchange words of the shared row kernel follow the transposed copy
         const size_t tb = (size_t)(p.batch * p.rows * p.K) * sizeof(XT);
-        return launch_rows<XT, ST>(q, plan.variant, st,
-                                   (uint64_t *)((char *)p.resid + (tb + 255) / 256 * 256));
+        return launch_rows<XT, ST>(q, plan.variant, st, (uint64_t *)((char *)p.resid + round256(tb)));
     }
     default:
         hipLaunchKernelGGL((split_generic_kernel<XT, ST>), dim3((unsigned)(p.batch * p.rows)),
@@ -1341,7 +1431,7 @@ static hipError_t launch_slice(const SplitParams &p, const SplitPlan &plan, int 
     if (e != hipSuccess) return e;
     SplitParams q = converted_params(p);
     q.X = T;
-    q.resid = T + p.batch * p.rows * p.K;
+    q.resid = (float *)((char *)T + round256((size_t)(p.batch * p.rows * p.K) * 4));
     const SplitPlan inner = plan_split(q, 1, slice_dtype);
     return launch_typed<float, ST>(q, inner, st);
 }
@@ -1356,6 +1446,21 @@ hipError_t launch_split(const SplitParams &p, const SplitPlan &plan, int x_dtype
     case 1: return launch_slice<float>(p, plan, x_dtype, slice_dtype, st);
     }
     return hipErrorInvalidValue;
+}
+
+hipError_t read_device_status(unsigned *out, bool clear, hipStream_t st) {
+    uint32_t v = 0;
+    hipError_t e = hipMemcpyFromSymbolAsync(&v, HIP_SYMBOL(g_device_status), sizeof(v), 0,
+                                            hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e == hipSuccess && clear && v != 0) {
+        const uint32_t zero = 0;
+        e = hipMemcpyToSymbolAsync(HIP_SYMBOL(g_device_status), &zero, sizeof(zero), 0,
+                                   hipMemcpyHostToDevice, st);
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+    }
+    *out = v;
+    return e;
 }
 
 }  // namespace ozk

@@ -110,6 +110,17 @@ def compute_split_bits(n: int, slice_dtype: torch.dtype = torch.float16,
 # helpers
 # ============================================================
 
+def device_status(clear: bool = True) -> None:
+    """Raise if a cooperative split wait gave up on the current device since
+    the last check (no counterpart in the reference, whose kernels have no
+    bounded waits).  Such a split's scales, and every C computed from them,
+    are NaN.  Waits for the current stream; ``clear`` resets the status."""
+    stream = torch.cuda.current_stream().cuda_stream
+    st = _lib.device_status(clear, stream)
+    if st != _lib.OZK_OK:
+        raise _lib.OzakiLibError("ozk_device_status", st)
+
+
 def _require_gpu(*tensors: torch.Tensor) -> None:
     for t in tensors:
         if not t.is_cuda:
@@ -357,8 +368,11 @@ def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, events, max_split
     if BN == 0:
         return torch.empty(out_shape, dtype=input_dtype, device=A.device)
 
+    # before anything touches the device, for every num_splits, as the
+    # reference (ozaki_triton.py:580): K = 0 raises ValueError, alpha < 1
+    # AssertionError
+    alpha = compute_split_bits(K, slice_dtype=slice_dtype, dot_accum_dtype=dot_accum_dtype)
     if verbose:
-        alpha = compute_split_bits(K, slice_dtype=slice_dtype, dot_accum_dtype=dot_accum_dtype)
         print(f"[Ozaki] batch={batch_shape}, M={M}, K={K}, N={N}, "
               f"input={input_dtype}, slice={slice_dtype}, "
               f"dot_accum={dot_accum_dtype}, out_accum={out_accum_dtype}, "
@@ -376,9 +390,6 @@ def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, events, max_split
     nbytes = ctypes.c_size_t(0)
     st = L.ozk_matmul_workspace_bytes(xd, BN, M, N, K, a_st, b_st, num_splits, sd,
                                       ctypes.byref(nbytes))
-    if st in (_lib.OZK_ERR_ALPHA, _lib.OZK_ERR_SHAPE):
-        # raise exactly what the reference's compute_split_bits raises
-        compute_split_bits(K, slice_dtype=slice_dtype, dot_accum_dtype=dot_accum_dtype)
     _lib.check("ozk_matmul_workspace_bytes", st)
     C = torch.empty((BN, M, N), dtype=input_dtype, device=dev)
     ws, wsp = _workspace(int(nbytes.value), dev)

@@ -25,3 +25,26 @@ def gpu():
     if not torch.cuda.is_available():
         pytest.fail("GPU test selected but torch.cuda.is_available() is False")
     return torch.device("cuda:0")
+
+
+@pytest.fixture
+def force():
+    """force(gemm=..., split=..., coop_timeout=...) forces kernels through the
+    library's thread-local test hooks (include/ozaki_amd_debug.h) for the rest
+    of the test; the defaults come back at teardown."""
+    from ozaki_triton_amd import _lib
+    L = _lib.load()
+
+    def set_(gemm=None, split=None, coop_timeout=None):
+        if gemm is not None:
+            _lib.check("ozk_debug_force_gemm_kernel", L.ozk_debug_force_gemm_kernel(gemm.encode()))
+        if split is not None:
+            _lib.check("ozk_debug_force_split_kernel",
+                       L.ozk_debug_force_split_kernel(split.encode()))
+        if coop_timeout is not None:
+            L.ozk_debug_force_coop_timeout(1 if coop_timeout else 0)
+
+    yield set_
+    L.ozk_debug_force_gemm_kernel(None)
+    L.ozk_debug_force_split_kernel(None)
+    L.ozk_debug_force_coop_timeout(0)

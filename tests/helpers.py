@@ -113,3 +113,20 @@ def check_block_vs_oracle(oracle, ozk, C_np, A_np, B_np, rows, cols, L, sdt, xdt
             bound = bound + 2.0 ** -23 * np.abs(want.astype(np.float64))   # output rounding
         err = np.abs(got.astype(np.float64) - want.astype(np.float64))
         assert np.all(err <= bound), (what, float((err / np.maximum(bound, 1e-300)).max()))
+
+
+def int_valued_slices(g, B, L, M, N, K, sdt, vmax=32, exp_range=(-20, 5)):
+    """Float slices (float16 / bfloat16 / float32) holding integers in
+    [-vmax, vmax] and power-of-two scales 2^[lo, hi).  With K * vmax^2 <= 2^24
+    every product and every partial dot sum is an integer that fp32 holds
+    exactly, so an fp32-accumulating kernel gives the exact dot in whatever
+    order it adds, and its C must equal the oracle's (exact dot, then the
+    reference's epilogue) bit for bit: a dropped slice pair, a misplaced
+    fragment or a wrong scale shows."""
+    assert K * vmax * vmax <= 1 << 24
+    As = torch.randint(-vmax, vmax + 1, (B, L, M, K), generator=g).to(sdt)
+    BsT = torch.randint(-vmax, vmax + 1, (B, L, N, K), generator=g).to(sdt)
+    lo, hi = exp_range
+    sa = torch.pow(2.0, torch.randint(lo, hi, (B, L, M), generator=g).float())
+    sb = torch.pow(2.0, torch.randint(lo, hi, (B, L, N), generator=g).float())
+    return As, BsT, sa, sb

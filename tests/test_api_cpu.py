@@ -11,8 +11,8 @@ import torch
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def _declared_symbols():
-    with open(os.path.join(ROOT, "include", "ozaki_amd.h")) as f:
+def _declared_symbols(header):
+    with open(os.path.join(ROOT, "include", header)) as f:
         text = f.read()
     return sorted(set(re.findall(r"^\w[\w\s\*]*?\b(ozk_\w+)\s*\(", text, re.M)))
 
@@ -20,16 +20,18 @@ def _declared_symbols():
 def test_library_exports_every_declared_symbol():
     from ozaki_triton_amd import _lib
     L = _lib.load()
-    declared = _declared_symbols()
-    assert declared == sorted(_lib.EXPORTED)
-    for name in declared:
+    headers = sorted(f for f in os.listdir(os.path.join(ROOT, "include")) if f.endswith(".h"))
+    assert headers == ["ozaki_amd.h", "ozaki_amd_debug.h"]
+    assert _declared_symbols("ozaki_amd.h") == sorted(_lib.EXPORTED)
+    assert _declared_symbols("ozaki_amd_debug.h") == sorted(_lib.EXPORTED_DEBUG)
+    for name in _lib.EXPORTED + _lib.EXPORTED_DEBUG:
         assert hasattr(L, name), name
-    assert L.ozk_version() >= 100
+    assert L.ozk_version() >= 200
 
 
 def test_strerror_names_every_code():
     from ozaki_triton_amd import _lib
-    for code in range(0, -9, -1):
+    for code in range(0, -10, -1):
         assert _lib.strerror(code) != "unknown status"
     assert _lib.strerror(-99) == "unknown status"
 
@@ -79,23 +81,33 @@ def test_split_abi_rejects_bad_arguments_on_host():
     # nothing to do: returns OK without any device call
     assert call(B=0) == _lib.OZK_OK
     assert call(L=0) == _lib.OZK_OK
-    # the generic (strided) path needs a residual workspace
-    nb = ctypes.c_size_t(0)
+    # the generic (strided) path recomputes each level's residual from the
+    # input: no workspace
+    nb = ctypes.c_size_t(123)
     xs_bad = _lib.i64arr([6, 3, 2])
     assert L.ozk_split_workspace_bytes(_lib.OZK_F64, 1, 2, 3, xs_bad, 2, _lib.OZK_I8, s4,
                                        ctypes.byref(nb)) == 0
-    assert nb.value == 1 * 2 * 3 * 4
-    assert L.ozk_split(p, _lib.OZK_F64, 1, 2, 3, xs_bad, 2, 7, _lib.OZK_I8, p, s4, p, s3, null,
+    assert nb.value == 0
+    # the cooperative column path needs its exchange words: refused without
+    # them, or with a workspace that is not 16-byte aligned (before anything
+    # is enqueued)
+    K, N = 8192, 16
+    xs_c = _lib.i64arr([K * N, 1, N])
+    sl_c = _lib.i64arr([2 * N * K, N * K, K, 1])
+    sc_c = _lib.i64arr([2 * N, N, 1])
+    assert L.ozk_split_workspace_bytes(_lib.OZK_F64, 1, N, K, xs_c, 2, _lib.OZK_I8, sl_c,
+                                       ctypes.byref(nb)) == 0
+    assert nb.value == 1 * 2 * 8 * 16 * 8 + 8
+    assert L.ozk_split(p, _lib.OZK_F64, 1, N, K, xs_c, 2, 7, _lib.OZK_I8, p, sl_c, p, sc_c, null,
                        0, null) == _lib.OZK_ERR_WORKSPACE
-    # a workspace must be 16-byte aligned (checked before anything is enqueued)
-    assert L.ozk_split(p, _lib.OZK_F64, 1, 2, 3, xs_bad, 2, 7, _lib.OZK_I8, p, s4, p, s3,
-                       ctypes.c_void_p(0x2008), 4096, null) == _lib.OZK_ERR_WORKSPACE
+    assert L.ozk_split(p, _lib.OZK_F64, 1, N, K, xs_c, 2, 7, _lib.OZK_I8, p, sl_c, p, sc_c,
+                       ctypes.c_void_p(0x2008), 1 << 20, null) == _lib.OZK_ERR_WORKSPACE
 
 
 def test_split_workspace_narrow_inputs():
     """fp16 / bf16 / int8 inputs are split from an exact fp32 copy in the
     workspace (ozaki_triton.py:188 loads them into the fp32 RES); an odd K
-    adds the generic path's fp32 residual behind the copy."""
+    takes the generic kernel, which needs nothing behind the copy."""
     from ozaki_triton_amd import _lib
     L = _lib.load()
     nb = ctypes.c_size_t(0)
@@ -110,7 +122,7 @@ def test_split_workspace_narrow_inputs():
     sl2 = _lib.i64arr([3 * M * K2, M * K2, K2, 1])
     assert L.ozk_split_workspace_bytes(_lib.OZK_F16, 1, M, K2, _lib.i64arr([M * K2, K2, 1]), 3,
                                        _lib.OZK_I8, sl2, ctypes.byref(nb)) == 0
-    assert nb.value == 2 * M * K2 * 4
+    assert nb.value == M * K2 * 4
     # fp32 slices are 4 bytes: the resident paths still need no workspace
     sl4 = _lib.i64arr([2 * M * K, M * K, K, 1])
     assert L.ozk_split_workspace_bytes(_lib.OZK_F64, 1, M, K, _lib.i64arr([M * K, K, 1]), 2,
@@ -130,10 +142,11 @@ def test_split_workspace_per_path():
     assert nb.value == 0
     # B^T view (rows contiguous, 64 KB columns): column groups of 16 fp64
     # columns cut into K chunks of 1024 rows exchange one 8-byte maximum per
-    # column, level and chunk: 512 groups x 4 levels x 8 chunks x 16 columns x 8 bytes
+    # column, level and chunk: 512 groups x 4 levels x 8 chunks x 16 columns x 8 bytes,
+    # plus the launch's status word
     assert L.ozk_split_workspace_bytes(_lib.OZK_F64, 1, N, K, _lib.i64arr([K * N, 1, N]), 4,
                                        _lib.OZK_I8, sl, ctypes.byref(nb)) == 0
-    assert nb.value == 512 * 4 * 8 * 16 * 8
+    assert nb.value == 512 * 4 * 8 * 16 * 8 + 8
     # short columns (under 64 KB) take the strip kernel: no workspace
     Ks = 512
     sls = _lib.i64arr([2 * N * Ks, N * Ks, Ks, 1])
@@ -144,16 +157,16 @@ def test_split_workspace_per_path():
     # into the workspace first (config 5: fp32, K = 65536); its rows, longer
     # than 16384, then go to the row kernel shared by 4 workgroups per row,
     # whose exchange words follow the transposed copy: 1024 rows x 3 levels x
-    # 4 chunks x 8 bytes
+    # 4 chunks x 8 bytes, and a status word
     K5, N5 = 65536, 1024
     sl5 = _lib.i64arr([3 * N5 * K5, N5 * K5, K5, 1])
     assert L.ozk_split_workspace_bytes(_lib.OZK_F32, 1, N5, K5, _lib.i64arr([K5 * N5, 1, N5]),
                                        3, _lib.OZK_I8, sl5, ctypes.byref(nb)) == 0
-    assert nb.value == N5 * K5 * 4 + N5 * 3 * 4 * 8
+    assert nb.value == N5 * K5 * 4 + N5 * 3 * 4 * 8 + 8
     # and A's rows of config 5 (K-contiguous) need only the exchange words
     assert L.ozk_split_workspace_bytes(_lib.OZK_F32, 1, N5, K5, _lib.i64arr([K5 * N5, K5, 1]),
                                        3, _lib.OZK_I8, sl5, ctypes.byref(nb)) == 0
-    assert nb.value == N5 * 3 * 4 * 8
+    assert nb.value == N5 * 3 * 4 * 8 + 8
 
 
 def test_cross_gemm_abi_checks_and_workspace():
@@ -282,8 +295,9 @@ def test_matmul_abi_layout_and_errors():
     assert L.ozk_matmul_workspace_bytes(_lib.OZK_F64, 1, M, N, K, a, b, 4, _lib.OZK_I8,
                                         ctypes.byref(nb)) == 0
     # the split of B^T exchanges column maxima through the split scratch:
-    # 512 column groups x 4 levels x 8 K chunks x 16 columns x 8 bytes
-    assert nb.value == 2 * (4 * M * K + 4 * M * 4) + 512 * 4 * 8 * 16 * 8
+    # 512 column groups x 4 levels x 8 K chunks x 16 columns x 8 bytes and a
+    # status word, the region rounded to 256 bytes
+    assert nb.value == 2 * (4 * M * K + 4 * M * 4) + 512 * 4 * 8 * 16 * 8 + 256
     # broadcast B over a batch of 16 (stride 0): B is split once
     Mb, Kb, Nb = 1024, 2048, 1024
     a16 = _lib.i64arr([Mb * Kb, Kb, 1])
@@ -334,3 +348,134 @@ def test_operands_on_two_devices_are_refused():
     _require_gpu(a, a)
     with pytest.raises(RuntimeError, match="one device"):
         _require_gpu(a, b)
+
+
+# --------------------------------------------------------------------------- #
+# Workspace sizing does not depend on pointer alignment
+# --------------------------------------------------------------------------- #
+def _split_plan(L, X, xd, batch, rows, K, xs, nsp, sd, S, ss):
+    from ozaki_triton_amd import _lib
+    name = ctypes.c_char_p()
+    nb = ctypes.c_size_t(0)
+    assert L.ozk_debug_split_kernel(ctypes.c_void_p(X), xd, batch, rows, K, _lib.i64arr(xs), nsp,
+                                    sd, ctypes.c_void_p(S), _lib.i64arr(ss), ctypes.byref(name),
+                                    ctypes.byref(nb)) == 0
+    return name.value.decode(), nb.value
+
+
+@pytest.mark.parametrize("xd", [0, 1])          # OZK_F64, OZK_F32
+@pytest.mark.parametrize("sd", [4, 2])          # OZK_I8, OZK_F16
+@pytest.mark.parametrize("K,rows", [(8192, 8192), (4096, 2048), (65536, 1024), (1000, 64),
+                                    (40000, 3)])
+def test_split_plan_for_unaligned_pointers_fits_the_query(xd, sd, K, rows):
+    """The *_workspace_bytes queries see no pointers and size for aligned ones.
+    An operand whose data pointer is 8 (or 4) mod 16 -- e.g. torch.empty(1 +
+    M * K)[1:].view(M, K) -- must get a plan that needs no more scratch: the
+    query must cover it for A's rows and for B's columns (the B^T view)."""
+    from ozaki_triton_amd import _lib
+    L = _lib.load()
+    nsp = 3
+    ss = [nsp * rows * K, rows * K, K, 1]
+    for xs in ([rows * K, K, 1], [K * rows, 1, rows]):      # A rows, B^T view
+        nb = ctypes.c_size_t(0)
+        assert L.ozk_split_workspace_bytes(xd, 1, rows, K, _lib.i64arr(xs), nsp, sd,
+                                           _lib.i64arr(ss), ctypes.byref(nb)) == 0
+        name_al, need_al = _split_plan(L, 0x10000, xd, 1, rows, K, xs, nsp, sd, 0x20000, ss)
+        assert need_al == nb.value, (name_al, need_al, nb.value)
+        for off in (8, 4) if xd == 1 else (8,):
+            name, need = _split_plan(L, 0x10000 + off, xd, 1, rows, K, xs, nsp, sd, 0x20000, ss)
+            assert need <= nb.value, (xs, off, name, need, nb.value)
+        # slices at an odd address: the fast paths need aligned slice rows
+        name, need = _split_plan(L, 0x10000, xd, 1, rows, K, xs, nsp, sd, 0x20001, ss)
+        assert need <= nb.value and name == "generic", (name, need)
+
+
+def test_matmul_workspace_covers_unaligned_operands():
+    """ozk_matmul carves the split scratch from the size its query returned;
+    with unaligned operands the plans still fit (checked again in ozk_matmul,
+    which returns OZK_ERR_WORKSPACE rather than write past the region)."""
+    from ozaki_triton_amd import _lib
+    L = _lib.load()
+    for xd in (0, 1):
+        M = N = K = 8192
+        nb = ctypes.c_size_t(0)
+        assert L.ozk_matmul_workspace_bytes(xd, 1, M, N, K, _lib.i64arr([M * K, K, 1]),
+                                            _lib.i64arr([K * N, N, 1]), 4, 4,
+                                            ctypes.byref(nb)) == 0
+        slices = 2 * (4 * M * K + 4 * M * 4)
+        scratch = nb.value - slices
+        for xs in ([M * K, K, 1], [K * N, 1, N]):
+            name, need = _split_plan(L, 0x10008, xd, 1, M, K, xs, 4, 4, 0x100000,
+                                     [4 * M * K, M * K, K, 1])
+            assert need <= scratch, (name, need, scratch)
+
+
+# --------------------------------------------------------------------------- #
+# Error parity: compute_split_bits runs for every num_splits, 0 included
+# --------------------------------------------------------------------------- #
+def test_zero_splits_still_checks_alpha_like_the_reference():
+    """ozaki_triton.py:580 calls compute_split_bits before splitting, whatever
+    num_splits is: K = 0 raises ValueError (log2(0)) and alpha < 1 the alpha
+    assertion, before any device work (here: before the CPU-tensor check)."""
+    import ozaki_triton_amd as ozk
+    from ozaki_triton_amd import _lib
+    with pytest.raises(ValueError):
+        ozk.ozaki_matmul(torch.zeros(4, 0, dtype=torch.float64),
+                         torch.zeros(0, 3, dtype=torch.float64), 0, torch.int8)
+    big = torch.zeros(2, 1 << 22, dtype=torch.float32)   # fp16 slices: alpha = int(0.5) = 0
+    with pytest.raises(AssertionError, match="alpha="):
+        ozk.ozaki_matmul(big, big.T, 0, torch.float16)
+    L = _lib.load()
+    nb = ctypes.c_size_t(0)
+    a = _lib.i64arr([0, 1, 1])
+    assert L.ozk_matmul_workspace_bytes(_lib.OZK_F64, 1, 4, 3, 0, a, a, 0, _lib.OZK_I8,
+                                        ctypes.byref(nb)) == _lib.OZK_ERR_SHAPE
+    assert L.ozk_matmul_workspace_bytes(_lib.OZK_F32, 1, 4, 3, 1 << 30, a, a, 0, _lib.OZK_F16,
+                                        ctypes.byref(nb)) == _lib.OZK_ERR_ALPHA
+
+
+# --------------------------------------------------------------------------- #
+# Test hooks and the planner's kernel choice
+# --------------------------------------------------------------------------- #
+def test_debug_hooks_reject_unknown_names():
+    from ozaki_triton_amd import _lib
+    L = _lib.load()
+    assert L.ozk_debug_force_gemm_kernel(b"fastest") == _lib.OZK_ERR_DTYPE
+    assert L.ozk_debug_force_split_kernel(b"fastest") == _lib.OZK_ERR_DTYPE
+    for k in (b"staged", b"dma", b"ad", b"pair", b"ring", b"wide", b"", None):
+        assert L.ozk_debug_force_gemm_kernel(k) == 0
+    for k in (b"coop", b"strip", b"transpose", b"generic", b"rows", b"rowscoop", None):
+        assert L.ozk_debug_force_split_kernel(k) == 0
+
+
+def _gemm_kernel(L, batch, M, N, K, nsp, sd, cus):
+    name = ctypes.c_char_p()
+    assert L.ozk_debug_gemm_kernel(batch, M, N, K, nsp, sd, cus, ctypes.byref(name)) == 0
+    return name.value.decode()
+
+
+def test_planner_kernel_choice():
+    """num_splits 3: the wide kernel where its rounds of one workgroup per CU
+    finish sooner (12 * wide rounds < 7 * ring rounds), measured crossovers at
+    200 / 288 / 384 / 480 / 512 wide tiles on 256 CUs; the rule follows the
+    device's compute-unit count (a 32-CU partition)."""
+    from ozaki_triton_amd import _lib
+    L = _lib.load()
+    I8 = _lib.OZK_I8
+    # wide tiles = (M / 64) * (N / 128)
+    assert _gemm_kernel(L, 1, 640, 2560, 4096, 3, I8, 256) == "wide"      # 200 tiles
+    assert _gemm_kernel(L, 1, 1024, 2304, 4096, 3, I8, 256) == "ring"     # 288
+    assert _gemm_kernel(L, 1, 1024, 3072, 4096, 3, I8, 256) == "ring"     # 384
+    assert _gemm_kernel(L, 1, 1024, 3840, 4096, 3, I8, 256) == "wide"     # 480
+    assert _gemm_kernel(L, 1, 1024, 4096, 4096, 3, I8, 256) == "wide"     # 512
+    assert _gemm_kernel(L, 16, 1024, 1024, 2048, 3, _lib.OZK_F16, 256) == "wide"   # config 4
+    assert _gemm_kernel(L, 1, 1024, 1024, 65536, 3, I8, 256) == "ring"    # config 5: 128 tiles
+    # 200 wide tiles on 32 CUs: 7 rounds against 13 -> 84 < 91: wide; 288: 9 vs 18 -> wide
+    assert _gemm_kernel(L, 1, 640, 2560, 4096, 3, I8, 32) == "wide"
+    assert _gemm_kernel(L, 1, 1024, 2304, 4096, 3, I8, 32) == "wide"
+    # other slice counts
+    assert _gemm_kernel(L, 1, 8192, 8192, 8192, 4, I8, 256) == "ring"     # config 3
+    assert _gemm_kernel(L, 1, 4096, 4096, 4096, 2, _lib.OZK_F16, 256) == "ring"   # config 2
+    assert _gemm_kernel(L, 1, 256, 256, 256, 2, _lib.OZK_F16, 256) == "dma"       # config 1
+    assert _gemm_kernel(L, 1, 2048, 2048, 2048, 1, I8, 256) == "dma"
+    assert _gemm_kernel(L, 1, 1024, 1024, 1024, 5, I8, 256) == "pair"

@@ -12,7 +12,8 @@ import pytest
 import torch
 
 from tests.helpers import (NAME_OF, assert_bitwise_equal, c3_like, check_block_vs_oracle,
-                           fp16_cross_bound, oracle_split_batched, sample_indices, to_np, values)
+                           fp16_cross_bound, int_valued_slices, oracle_split_batched,
+                           sample_indices, to_np, values)
 
 pytestmark = pytest.mark.gpu
 
@@ -42,11 +43,11 @@ def _check_split(oracle, ozk, X3_dev, L, slice_dtype, what):
 @pytest.mark.parametrize("L", [1, 2, 4])
 @pytest.mark.parametrize("rows,K", [(5, 256), (64, 1000), (33, 2048), (7, 8192)])
 @pytest.mark.parametrize("kernel", ["rows", "rowscoop"])
-def test_split_rows_path(oracle, gpu, xdt, sdt, L, rows, K, kernel, monkeypatch):
+def test_split_rows_path(oracle, gpu, xdt, sdt, L, rows, K, kernel, force):
     """K-contiguous rows: the one-workgroup row kernel and the shared row
     kernel (here one chunk per row, shorter than the chunk), each forced."""
     import ozaki_triton_amd as ozk
-    monkeypatch.setenv("OZK_SPLIT_KERNEL", kernel)
+    force(split=kernel)
     g = torch.Generator().manual_seed(rows * K + L)
     X = torch.randn(2, rows, K, generator=g, dtype=torch.float64)
     X = X * torch.pow(10.0, torch.empty(2, rows, 1).uniform_(-3, 3, generator=g).double())
@@ -72,12 +73,12 @@ def test_split_rows_coop_long(oracle, gpu, xdt, sdt, batch, rows, K, L):
 @pytest.mark.parametrize("L", [1, 3, 4])
 @pytest.mark.parametrize("N,K", [(8, 256), (40, 1000), (96, 2048), (24, 8192), (16, 16000)])
 @pytest.mark.parametrize("kernel", ["coop", "strip"])
-def test_split_strip_path(oracle, gpu, xdt, sdt, L, N, K, kernel, monkeypatch):
+def test_split_strip_path(oracle, gpu, xdt, sdt, L, N, K, kernel, force):
     """B's columns through the transposed view (rows contiguous): the
     cooperative column-group kernel and the one-load-wide strip kernel, each
     forced (the planner picks by column length)."""
     import ozaki_triton_amd as ozk
-    monkeypatch.setenv("OZK_SPLIT_KERNEL", kernel)
+    force(split=kernel)
     g = torch.Generator().manual_seed(N * K + L + 1)
     B = torch.randn(2, K, N, generator=g, dtype=torch.float64)
     B = B * torch.pow(2.0, torch.randint(-8, 9, (2, 1, N), generator=g).double())
@@ -89,14 +90,14 @@ def test_split_strip_path(oracle, gpu, xdt, sdt, L, N, K, kernel, monkeypatch):
 @pytest.mark.parametrize("xdt,sdt", COMBOS)
 @pytest.mark.parametrize("batch,N,K,L", [(2, 264, 8192, 4), (1, 72, 16384, 3), (1, 40, 32768, 2),
                                          (3, 48, 4100, 2), (1, 256, 8192, 4), (2, 128, 2048, 3)])
-def test_split_coop_groups(oracle, gpu, xdt, sdt, batch, N, K, L, monkeypatch):
+def test_split_coop_groups(oracle, gpu, xdt, sdt, batch, N, K, L, force):
     """The cooperative column split (forced; the default from 64 KB columns)
     at full length: up to 32 workgroups per column group (its limit: fp64 at
     K = 32768, fp32 at K = 16384; fp32 at K = 32768 falls to the transpose
     path), a ragged last group and a ragged last K chunk, batched operands,
     per-column exponents and outliers."""
     import ozaki_triton_amd as ozk
-    monkeypatch.setenv("OZK_SPLIT_KERNEL", "coop")
+    force(split="coop")
     g = torch.Generator().manual_seed(batch * N * K + L)
     B = torch.randn(batch, K, N, generator=g, dtype=torch.float64)
     B = B * torch.pow(2.0, torch.randint(-8, 9, (batch, 1, N), generator=g).double())
@@ -116,8 +117,8 @@ def test_split_generic_path(oracle, gpu, xdt, sdt):
     _check_split(oracle, ozk, X[:, :, ::2], 3, sdt, "generic strided")
     big = 40000 if xdt == torch.float64 else 70000
     Y = torch.randn(1, 3, big, generator=g, dtype=torch.float64).to(xdt).to(gpu)
-    with pytest.MonkeyPatch.context() as mp:
-        mp.setenv("OZK_SPLIT_KERNEL", "generic")   # long rows otherwise take the shared row kernel
+    from ozaki_triton_amd import _lib
+    with _lib.forced_kernels(split="generic"):   # long rows otherwise take the shared row kernel
         _check_split(oracle, ozk, Y, 2, sdt, "generic long K")
 
 
@@ -159,6 +160,14 @@ def _random_slices(g, B, L, M, N, K, sdt):
     sa = torch.pow(2.0, torch.randint(-20, 5, (B, L, M), generator=g).float())
     sb = torch.pow(2.0, torch.randint(-20, 5, (B, L, N), generator=g).float())
     return As, BsT, sa, sb
+
+
+def _slices_for(g, B, L, M, N, K, sdt):
+    """int8: random slices; float dtypes: integer-valued ones, for which the
+    fp32-accumulated kernels are exact and must match the oracle bit for bit."""
+    if sdt == torch.int8:
+        return _random_slices(g, B, L, M, N, K, sdt)
+    return int_valued_slices(g, B, L, M, N, K, sdt)
 
 
 @pytest.mark.parametrize("L", [1, 2, 3, 4])
@@ -287,14 +296,14 @@ def test_ozaki_matmul_degenerate_shapes(gpu):
 
 @pytest.mark.parametrize("kernel", ["staged", "dma", "ad", "pair", "ring", "wide"])
 @pytest.mark.parametrize("L", [1, 2, 3, 4])
-def test_cross_gemm_each_kernel_bitexact(oracle, gpu, L, kernel, monkeypatch):
+def test_cross_gemm_each_kernel_bitexact(oracle, gpu, L, kernel, force):
     """Every cross-GEMM kernel, forced: the VGPR-staged one (taken when an
     operand's extent exceeds the 31-bit buffer offsets of the LDS-DMA kernels),
     the 2 x 2 LDS-DMA kernel, the A-direct kernel, the pair-split kernel, its
     five-slot ring form (L >= 3; for L <= 2 the request falls back to the
     2 x 2 kernel) and the wide kernel (L = 3; otherwise the default kernel)."""
     import ozaki_triton_amd as ozk
-    monkeypatch.setenv("OZK_GEMM_KERNEL", kernel)
+    force(gemm=kernel)
     g = torch.Generator().manual_seed(77 + L)
     As, BsT, sa, sb = _random_slices(g, 1, L, 100, 72, 1040, torch.int8)
     C = ozk.cross_gemm(As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), L,
@@ -304,177 +313,203 @@ def test_cross_gemm_each_kernel_bitexact(oracle, gpu, L, kernel, monkeypatch):
     assert_bitwise_equal(to_np(C)[0], want, f"{kernel} L{L}")
 
 
+@pytest.mark.parametrize("sdt", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("kernel,L,M,N,K", [
+    ("ring", 2, 256, 384, 4096),    # config 2's kernel: 128 x 128 tiles, K = 4096
+    ("wide", 3, 128, 256, 2048),    # config 4's kernel: 64 x 128 tiles, K = 2048
+    ("ring", 4, 128, 192, 8192),    # config 3's kernel shape: 64 x 64 tiles, K = 8192
+    ("ring", 3, 130, 72, 4096),
+    ("pair", 3, 100, 72, 1040),
+    ("pair", 4, 100, 72, 1040),
+    ("dma", 1, 130, 260, 1040),
+    ("dma", 2, 130, 136, 1040),
+    ("staged", 2, 100, 72, 1040),
+    ("staged", 4, 100, 72, 520),
+    ("ad", 3, 100, 72, 1040),
+])
+def test_float_slice_kernels_bitexact(oracle, gpu, kernel, L, M, N, K, sdt, force):
+    """Every cross-GEMM kernel with float slices, at the tile shapes and K of
+    the BASELINE configurations it serves: on integer-valued slices the
+    fp32-accumulated dot is exact in any order, so C must equal the oracle bit
+    for bit.  Unlike a tolerance, this fails for a kernel that drops any one
+    slice pair (test_oracle_pins.py:test_int_valued_check_catches_a_dropped_pair)."""
+    import ozaki_triton_amd as ozk
+    force(gemm=kernel)
+    g = torch.Generator().manual_seed(M * 3 + N + K + L)
+    As, BsT, sa, sb = int_valued_slices(g, 1, L, M, N, K, sdt)
+    C = ozk.cross_gemm(As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), L,
+                       torch.float64)
+    torch.cuda.synchronize()
+    want = oracle.cross_gemm(to_np(As[0]), to_np(BsT[0]), to_np(sa[0]), to_np(sb[0]), "float64")
+    assert_bitwise_equal(to_np(C)[0], want, f"{kernel} L{L} {sdt} {M}x{N}x{K}")
+
+
 @pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
 @pytest.mark.parametrize("L", [2, 3, 4])
 @pytest.mark.parametrize("K", [16, 128, 200, 300, 520, 1040, 2064])
-def test_ring_kernel_stage_counts(oracle, gpu, L, K, sdt, monkeypatch):
+def test_ring_kernel_stage_counts(oracle, gpu, L, K, sdt, force):
     """The five-slot ring kernel over 1 to 17 stages of 128 bytes of K (the
     prologue fetches a stage and a half, the loop issues each stage's DMA
     ahead over the K steps of the stages before, and the last stage fetches
     the tile's scales into a free slot), with 64 x 64 tiles (L = 3, 4) and
-    128 x 128 tiles (L = 2; M and N cut a tile): int8 bit-exact against the
-    oracle, fp16 bit-identical to the pair kernel (L >= 3) or the 2 x 2
-    kernel (L = 2), which run the same MFMAs per accumulator in the same
-    order."""
+    128 x 128 tiles (L = 2; M and N cut a tile): int8 and integer-valued fp16
+    slices bit-exact against the oracle."""
     kernel = "ring"
     import ozaki_triton_amd as ozk
     g = torch.Generator().manual_seed(K * 10 + L)
     M, N = (130, 72) if L >= 3 else (200, 136)
-    As, BsT, sa, sb = _random_slices(g, 2, L, M, N, K, sdt)
+    As, BsT, sa, sb = _slices_for(g, 2, L, M, N, K, sdt)
     args = (As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), L, torch.float64)
-    monkeypatch.setenv("OZK_GEMM_KERNEL", kernel)
+    force(gemm=kernel)
     C = to_np(ozk.cross_gemm(*args))
-    if sdt == torch.int8:
-        for b in range(2):
-            want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[b]), to_np(sa[b]), to_np(sb[b]),
-                                     "float64")
-            assert_bitwise_equal(C[b], want, f"{kernel} L{L} K{K} b{b}")
-    else:
-        monkeypatch.setenv("OZK_GEMM_KERNEL", "pair" if L >= 3 else "dma")
-        assert_bitwise_equal(C, to_np(ozk.cross_gemm(*args)), f"{kernel} vs pair fp16 L{L} K{K}")
+    for b in range(2):
+        want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[b]), to_np(sa[b]), to_np(sb[b]),
+                                 "float64")
+        assert_bitwise_equal(C[b], want, f"{kernel} {sdt} L{L} K{K} b{b}")
 
 
 @pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
 @pytest.mark.parametrize("MN", [(130, 200), (64, 128), (200, 136), (1, 300)])
 @pytest.mark.parametrize("K", [16, 128, 200, 300, 520, 1040, 2064])
-def test_wide_kernel_stage_counts(oracle, gpu, K, MN, sdt, monkeypatch):
+def test_wide_kernel_stage_counts(oracle, gpu, K, MN, sdt, force):
     """The num_splits 3 wide kernel (64 x 128 tiles, every wave holding all 9
     pairs of its 32 x 32 block, two whole stages in the LDS) over 1 to 17
     stages of 128 bytes of K (the prologue fetches stages 0 and 1, the loop
     fetches stage kb + 2 after the barrier of stage kb, the last stage fetches
     the tile's scales into the free buffer), with M and N cutting tiles, and
-    batch 2: int8 bit-exact against the oracle, fp16 bit-identical to the pair
-    kernel, which runs the same MFMAs per accumulator in the same order."""
+    batch 2: int8 and integer-valued fp16 slices bit-exact against the
+    oracle."""
     import ozaki_triton_amd as ozk
     L, (M, N) = 3, MN
     g = torch.Generator().manual_seed(K * 10 + M + N)
-    As, BsT, sa, sb = _random_slices(g, 2, L, M, N, K, sdt)
+    As, BsT, sa, sb = _slices_for(g, 2, L, M, N, K, sdt)
     args = (As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), L, torch.float64)
-    monkeypatch.setenv("OZK_GEMM_KERNEL", "wide")
+    force(gemm="wide")
     C = to_np(ozk.cross_gemm(*args))
-    if sdt == torch.int8:
-        for b in range(2):
-            want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[b]), to_np(sa[b]), to_np(sb[b]),
-                                     "float64")
-            assert_bitwise_equal(C[b], want, f"wide K{K} M{M} N{N} b{b}")
-    else:
-        monkeypatch.setenv("OZK_GEMM_KERNEL", "pair")
-        assert_bitwise_equal(C, to_np(ozk.cross_gemm(*args)), f"wide vs pair fp16 K{K} M{M} N{N}")
+    for b in range(2):
+        want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[b]), to_np(sa[b]), to_np(sb[b]),
+                                 "float64")
+        assert_bitwise_equal(C[b], want, f"wide {sdt} K{K} M{M} N{N} b{b}")
 
 
 @pytest.mark.parametrize("out", [torch.float64, torch.float32, torch.float16, torch.bfloat16,
                                  torch.int8])
 @pytest.mark.parametrize("sdt", [torch.int8, torch.float16, torch.bfloat16, torch.float32])
-def test_wide_kernel_dtypes(oracle, gpu, sdt, out, monkeypatch):
+def test_wide_kernel_dtypes(oracle, gpu, sdt, out, force):
     """The wide kernel for every slice and output dtype, batched, with a
-    broadcast (batch stride 0) B: int8 slices bit-exact against the oracle;
-    float slices bit-identical to the pair kernel."""
+    broadcast (batch stride 0) B: int8 and integer-valued float slices
+    bit-exact against the oracle."""
     import ozaki_triton_amd as ozk
     L = 3
     g = torch.Generator().manual_seed(ALL_SLICES.index(sdt) * 7 + len(str(out)) + 500)
     M, N, K = 100, 150, 400
-    As, BsT, sa, sb = _random_slices(g, 2, L, M, N, K,
-                                     torch.int8 if sdt == torch.int8 else torch.float16)
-    if sdt != torch.int8:
-        As, BsT = As.to(sdt), BsT.to(sdt)
+    As, BsT, sa, sb = _slices_for(g, 2, L, M, N, K, sdt)
     if out in (torch.float16, torch.bfloat16, torch.int8):
-        sa = sa * 2.0 ** (12 if sdt == torch.int8 else 2)
+        sa = sa * 2.0 ** (12 if sdt == torch.int8 else 0)
     Bd = BsT[:1].to(gpu).expand(2, -1, -1, -1).transpose(-1, -2)   # broadcast B
     sbd = sb[:1].to(gpu).expand(2, -1, -1)
     args = (As.to(gpu), Bd, sa.to(gpu), sbd, L, out)
-    monkeypatch.setenv("OZK_GEMM_KERNEL", "wide")
+    force(gemm="wide")
     C = to_np(ozk.cross_gemm(*args))
-    if sdt == torch.int8:
-        for b in range(2):
-            want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[0]), to_np(sa[b]), to_np(sb[0]),
-                                     NAME_OF[out])
-            assert_bitwise_equal(C[b], want, f"wide {sdt} {out} b{b}")
-    else:
-        monkeypatch.setenv("OZK_GEMM_KERNEL", "pair")
-        assert_bitwise_equal(C, to_np(ozk.cross_gemm(*args)), f"wide vs pair {sdt} {out}")
+    for b in range(2):
+        want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[0]), to_np(sa[b]), to_np(sb[0]),
+                                 NAME_OF[out])
+        assert_bitwise_equal(C[b], want, f"wide {sdt} {out} b{b}")
 
 
 @pytest.mark.parametrize("out", [torch.float64, torch.float32, torch.float16, torch.bfloat16,
                                  torch.int8])
 @pytest.mark.parametrize("sdt", [torch.int8, torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("L", [2, 3, 4])
-def test_ring_kernel_dtypes(oracle, gpu, L, sdt, out, monkeypatch):
+def test_ring_kernel_dtypes(oracle, gpu, L, sdt, out, force):
     """The ring kernel for every slice and output dtype, batched, with a
-    broadcast (batch stride 0) B: int8 slices bit-exact against the oracle;
-    float slices bit-identical to the pair kernel (L >= 3) or the 2 x 2 kernel
-    (L = 2), which run the same MFMAs per accumulator and the same epilogue."""
+    broadcast (batch stride 0) B: int8 and integer-valued float slices
+    bit-exact against the oracle."""
     import ozaki_triton_amd as ozk
     g = torch.Generator().manual_seed(L * 41 + ALL_SLICES.index(sdt) * 7 + len(str(out)))
     M, N, K = (100, 72, 400) if L >= 3 else (150, 136, 400)
-    As, BsT, sa, sb = _random_slices(g, 2, L, M, N, K,
-                                     torch.int8 if sdt == torch.int8 else torch.float16)
-    if sdt != torch.int8:
-        As, BsT = As.to(sdt), BsT.to(sdt)
+    As, BsT, sa, sb = _slices_for(g, 2, L, M, N, K, sdt)
     if out in (torch.float16, torch.bfloat16, torch.int8):
-        sa = sa * 2.0 ** (12 if sdt == torch.int8 else 2)
+        sa = sa * 2.0 ** (12 if sdt == torch.int8 else 0)
     Bd = BsT[:1].to(gpu).expand(2, -1, -1, -1).transpose(-1, -2)   # broadcast B
     sbd = sb[:1].to(gpu).expand(2, -1, -1)
     args = (As.to(gpu), Bd, sa.to(gpu), sbd, L, out)
-    monkeypatch.setenv("OZK_GEMM_KERNEL", "ring")
+    force(gemm="ring")
     C = to_np(ozk.cross_gemm(*args))
-    if sdt == torch.int8:
-        for b in range(2):
-            want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[0]), to_np(sa[b]), to_np(sb[0]),
-                                     NAME_OF[out])
-            assert_bitwise_equal(C[b], want, f"ring L{L} {sdt} {out} b{b}")
-    else:
-        monkeypatch.setenv("OZK_GEMM_KERNEL", "pair" if L >= 3 else "dma")
-        assert_bitwise_equal(C, to_np(ozk.cross_gemm(*args)), f"ring vs pair L{L} {sdt} {out}")
+    for b in range(2):
+        want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[0]), to_np(sa[b]), to_np(sb[0]),
+                                 NAME_OF[out])
+        assert_bitwise_equal(C[b], want, f"ring L{L} {sdt} {out} b{b}")
 
 
 @pytest.mark.parametrize("xdt", [torch.float64, torch.float32])
-def test_split_coop_wait_timeout(oracle, gpu, xdt, monkeypatch):
+def test_split_coop_wait_timeout(oracle, gpu, xdt, force):
     """The cooperative split's bounded wait: forced from the host to look for a
-    tag no member writes (8 polls), every wait runs out, the kernel still
-    finishes, and the scales of the exchanged levels come out NaN instead of
-    the call hanging.  Afterwards the normal path gives the oracle's bits
-    again."""
+    tag no member writes and to give up at its first check, every wait runs
+    out, the kernel still finishes, every scale of the split comes out NaN
+    and the sticky device status reports OZK_ERR_DEVICE_WAIT (once: reading
+    clears it).  Through ozaki_matmul the whole C is NaN.  Afterwards the
+    normal path gives the oracle's bits again and sets no status."""
     import ozaki_triton_amd as ozk
     g = torch.Generator().manual_seed(21)
     K, N, L = 4096, 64, 3
     B = torch.randn(1, K, N, generator=g, dtype=torch.float64).to(xdt).to(gpu)
     BT = B.transpose(-1, -2)
     alpha = _alpha(ozk, K, torch.int8)
-    monkeypatch.setenv("OZK_SPLIT_KERNEL", "coop")
-    monkeypatch.setenv("OZK_SPLIT_COOP_TIMEOUT", "1")
+    from ozaki_triton_amd import _lib
+    ozk.device_status()                       # clear anything older
+    force(split="coop")
+    force(coop_timeout=True)
     sl, sc = ozk.split_matrix(BT, L, alpha, torch.int8)
     torch.cuda.synchronize()
-    assert torch.isnan(sc).all(), "every exchanged level's scale should be NaN after the timeout"
-    monkeypatch.delenv("OZK_SPLIT_COOP_TIMEOUT")
+    assert torch.isnan(sc).all(), "every scale of the split should be NaN after the timeout"
+    with pytest.raises(_lib.OzakiLibError) as e:
+        ozk.device_status()
+    assert e.value.status == _lib.OZK_ERR_DEVICE_WAIT
+    ozk.device_status()                       # cleared by the read above
+    # through ozaki_matmul: C is NaN everywhere (B's scales are), and flagged
+    A = torch.randn(1, 40, K, dtype=torch.float64).to(xdt).to(gpu)
+    C = ozk.ozaki_matmul(A, B, L, torch.int8)
+    torch.cuda.synchronize()
+    assert torch.isnan(C).all()
+    with pytest.raises(_lib.OzakiLibError):
+        ozk.device_status()
+    force(coop_timeout=False)
     _check_split(oracle, ozk, BT, L, torch.int8, f"coop after timeout {xdt}")
+    ozk.device_status()                       # the normal path sets nothing
 
 
 @pytest.mark.parametrize("xdt", [torch.float64, torch.float32])
-def test_split_rows_coop_wait_timeout(oracle, gpu, xdt, monkeypatch):
+def test_split_rows_coop_wait_timeout(oracle, gpu, xdt, force):
     """The shared row kernel's bounded wait, forced to run out as above: the
-    kernel finishes and the scales come out NaN; the normal path is exact
-    again afterwards."""
+    kernel finishes, the scales come out NaN and the device status is set;
+    the normal path is exact again afterwards."""
     import ozaki_triton_amd as ozk
     g = torch.Generator().manual_seed(22)
     X = torch.randn(1, 3, 40000, generator=g, dtype=torch.float64).to(xdt).to(gpu)
     alpha = _alpha(ozk, 40000, torch.int8)
-    monkeypatch.setenv("OZK_SPLIT_COOP_TIMEOUT", "1")
+    from ozaki_triton_amd import _lib
+    ozk.device_status()
+    force(coop_timeout=True)
     sl, sc = ozk.split_matrix(X, 2, alpha, torch.int8)
     torch.cuda.synchronize()
-    assert torch.isnan(sc).all(), "every exchanged level's scale should be NaN after the timeout"
-    monkeypatch.delenv("OZK_SPLIT_COOP_TIMEOUT")
+    assert torch.isnan(sc).all(), "every scale of the split should be NaN after the timeout"
+    with pytest.raises(_lib.OzakiLibError):
+        ozk.device_status()
+    force(coop_timeout=False)
     _check_split(oracle, ozk, X, 2, torch.int8, f"rowscoop after timeout {xdt}")
+    ozk.device_status()
 
 
 @pytest.mark.parametrize("xdt,sdt", COMBOS)
 @pytest.mark.parametrize("long", [False, True])
-def test_split_transpose_path(oracle, gpu, xdt, sdt, long, monkeypatch):
+def test_split_transpose_path(oracle, gpu, xdt, sdt, long, force):
     """Column splits (B^T view) through the transpose into the workspace and a
     row kernel (the path for columns longer than the cooperative column kernel
     takes): rows up to 16384 go to the one-workgroup row kernel, longer ones
     (config 5's B is 65536 long) to the shared row kernel."""
     import ozaki_triton_amd as ozk
-    monkeypatch.setenv("OZK_SPLIT_KERNEL", "transpose")
+    force(split="transpose")
     g = torch.Generator().manual_seed(11)
     K = (20000 if xdt == torch.float64 else 65536) if long else 12000
     B = torch.randn(1, K, 40, generator=g, dtype=torch.float64)
@@ -617,16 +652,34 @@ def test_matmul_c_abi_with_caller_workspace_and_events(oracle, gpu):
     assert all(t >= 0 for t in phases) and sum(phases) > 0
 
 
+def _int_valued_inputs(shape_a, shape_b, seed):
+    """A and B holding integers in [-32, 32], every row of A and column of B
+    reaching 32, times 2^e per row of A / column of B.  Their level-0 slices
+    are the integers themselves (fp16 or int8, scaled by powers of two), the
+    residuals are 0, and every dot is an integer below 2^24: the fp16 path is
+    then exact and equals the oracle bit for bit, like the int8 path."""
+    g = torch.Generator().manual_seed(seed)
+    A = torch.randint(-32, 33, shape_a, generator=g).double()
+    B = torch.randint(-32, 33, shape_b, generator=g).double()
+    A[..., 0] = 32.0
+    B[..., 0, :] = -32.0
+    A = A * torch.pow(2.0, torch.randint(-8, 9, (*shape_a[:-1], 1), generator=g).double())
+    B = B * torch.pow(2.0, torch.randint(-8, 9, (*shape_b[:-2], 1, shape_b[-1]),
+                                         generator=g).double())
+    return A, B
+
+
 @pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
 @pytest.mark.parametrize("sa,sb", [((2, 128, 256), (256, 96)), ((1, 64, 8192), (8192, 96))])
-def test_ozaki_matmul_graph_capture(gpu, sdt, sa, sb):
+def test_ozaki_matmul_graph_capture(oracle, gpu, sdt, sa, sb):
     """ozaki_matmul captured in a HIP graph (torch.cuda.graph): every replay,
     with eager work and synchronisations between replays and the inputs
-    changed in place, equals the eager result bit for bit.  At K = 8192 the
-    B split is the cooperative kernel, whose exchange words a fill kernel
-    clears on every replay."""
+    changed in place, equals the oracle bit for bit (inputs for which the fp16
+    path is exact too) and the eager call.  At K = 8192 the B split is the
+    cooperative kernel, whose exchange words a fill kernel clears on every
+    replay."""
     import ozaki_triton_amd as ozk
-    A, B = c3_like(sa, sb, seed=53)
+    A, B = _int_valued_inputs(sa, sb, seed=53)
     Ad, Bd = A.to(gpu), B.to(gpu)
     L = 3
     ozk.ozaki_matmul(Ad, Bd, L, sdt)          # warm up outside the capture
@@ -641,16 +694,19 @@ def test_ozaki_matmul_graph_capture(gpu, sdt, sa, sb):
     torch.cuda.synchronize()
     gen = torch.Generator().manual_seed(7)
     for rep in range(4):
+        An, Bn = A * 2.0 ** rep, torch.roll(B, rep, -2)
         if rep:
-            Ad.copy_((A * (1 + rep)).to(gpu))
-            Bd.copy_(torch.roll(B, rep, 0).to(gpu))
+            Ad.copy_(An.to(gpu))
+            Bd.copy_(Bn.to(gpu))
         junk = torch.randn(1000, 1000, generator=gen).to(gpu) @ torch.randn(1000, 1000).to(gpu)
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
+        want = oracle.ozaki_matmul(to_np(An), to_np(Bn), L, NAME_OF[sdt])
+        assert_bitwise_equal(to_np(C_graph), want, f"replay {rep} vs oracle")
         eager = ozk.ozaki_matmul(Ad, Bd, L, sdt)
         torch.cuda.synchronize()
-        assert_bitwise_equal(to_np(C_graph), to_np(eager), f"replay {rep}")
+        assert_bitwise_equal(to_np(C_graph), to_np(eager), f"replay {rep} vs eager")
         del junk
 
 
@@ -676,22 +732,18 @@ def test_cross_gemm_more_splits_int8_bitexact(oracle, gpu, L, M, N, K):
 
 @pytest.mark.parametrize("sdt", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("L", [5, 6])
-def test_cross_gemm_more_splits_float_within_bound(oracle, gpu, sdt, L):
+def test_cross_gemm_more_splits_float_bitexact(oracle, gpu, sdt, L):
+    """5 and 6 float slices on integer-valued slices: bit-exact against the
+    oracle."""
     import ozaki_triton_amd as ozk
     g = torch.Generator().manual_seed(L + 17)
     M, N, K = 100, 72, 1040
-    As = (torch.rand(1, L, M, K, generator=g) * 2 - 1).mul(64).to(sdt)
-    BsT = (torch.rand(1, L, N, K, generator=g) * 2 - 1).mul(64).to(sdt)
-    sa = torch.pow(2.0, torch.randint(-20, 5, (1, L, M), generator=g).float())
-    sb = torch.pow(2.0, torch.randint(-20, 5, (1, L, N), generator=g).float())
+    As, BsT, sa, sb = int_valued_slices(g, 1, L, M, N, K, sdt)
     C = ozk.cross_gemm(As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), L,
                        torch.float64)
     torch.cuda.synchronize()
-    a, bT, s_a, s_b = to_np(As[0]), to_np(BsT[0]), to_np(sa[0]), to_np(sb[0])
-    want = oracle.cross_gemm(a, bT, s_a, s_b, "float64")
-    bound = fp16_cross_bound(oracle, a, bT, s_a, s_b)
-    err = np.abs(to_np(C)[0] - want)
-    assert np.all(err <= bound), float((err / np.maximum(bound, 1e-300)).max())
+    want = oracle.cross_gemm(to_np(As[0]), to_np(BsT[0]), to_np(sa[0]), to_np(sb[0]), "float64")
+    assert_bitwise_equal(to_np(C)[0], want, f"L{L} {sdt}")
 
 
 def test_six_splits_end_to_end(oracle, gpu):
@@ -775,7 +827,7 @@ def test_split_columns_default_plan(oracle, gpu, xdt, sdt, batch, N, K):
 @pytest.mark.parametrize("kernel", ["", "dma", "ring", "pair", "ad", "staged", "wide"])
 @pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
 @pytest.mark.parametrize("K", [1, 2, 3, 5, 7, 9, 255, 257, 1003])
-def test_packed_rows_last_piece(oracle, gpu, kernel, sdt, K, monkeypatch):
+def test_packed_rows_last_piece(oracle, gpu, kernel, sdt, K, force):
     """Slice rows that are not whole 16-byte pieces (K * element size) go
     through the pack kernel's zero-padded copy.  The LDS-DMA kernels load
     16-byte pieces; the last piece of the operand's last row (the last slice
@@ -785,7 +837,7 @@ def test_packed_rows_last_piece(oracle, gpu, kernel, sdt, K, monkeypatch):
     int8 bit-exact, fp16 within the fp32 accumulation bound."""
     import ozaki_triton_amd as ozk
     if kernel:
-        monkeypatch.setenv("OZK_GEMM_KERNEL", kernel)
+        force(gemm=kernel)
     L = 3 if kernel == "wide" else 4 if kernel in ("ring", "pair", "ad") else 2
     A, B = c3_like((1, 33, K), (1, K, 20), seed=K + 100)
     C = ozk.ozaki_matmul(A.to(gpu), B.to(gpu), L, sdt)
@@ -879,3 +931,27 @@ def test_c_abi_example_program(gpu):
     r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "c_abi_example ok" in r.stdout, r.stdout
+
+
+@pytest.mark.parametrize("xdt,off", [(torch.float64, 1), (torch.float32, 1), (torch.float32, 2)])
+@pytest.mark.parametrize("K", [8192, 40000])
+def test_unaligned_operands(oracle, gpu, xdt, off, K):
+    """Operands whose data pointer is not 16-byte aligned (a view starting
+    `off` elements into its storage): the workspace query sees no pointers
+    and sizes for aligned ones, so the split plans for these pointers must
+    need no more (they take the generic kernel, or the transpose path when
+    the aligned plan does too).  C bit-exact against the oracle, for A's rows
+    and for B's columns at lengths whose aligned plans take the cooperative
+    kernels."""
+    import ozaki_triton_amd as ozk
+    M, N, L = 48, 40, 3
+    A, B = c3_like((M, K), (K, N), seed=K + off, dtype=xdt)
+    Ad = torch.empty(off + M * K, dtype=xdt, device=gpu)[off:].view(M, K)
+    Bd = torch.empty(off + K * N, dtype=xdt, device=gpu)[off:].view(K, N)
+    Ad.copy_(A.to(gpu))
+    Bd.copy_(B.to(gpu))
+    assert Ad.data_ptr() % 16 != 0 and Bd.data_ptr() % 16 != 0
+    C = ozk.ozaki_matmul(Ad, Bd, L, torch.int8)
+    torch.cuda.synchronize()
+    want = oracle.ozaki_matmul(to_np(A), to_np(B), L, "int8")
+    assert_bitwise_equal(to_np(C), want, f"unaligned {xdt} +{off} K{K}")

@@ -446,3 +446,131 @@ def test_scale_of_an_infinite_row_is_infinite(oracle):
     # finite maxima are unchanged, the largest included
     fmax = float(np.finfo(np.float32).max)
     assert oracle.scale_from_max(fmax, 7) == float(np.exp2(np.float32(128 - 7)))
+
+
+# --------------------------------------------------------------------------- #
+# NaN entries (not pinned by the reference's tests: documented choice)
+# --------------------------------------------------------------------------- #
+@pytest.mark.parametrize("xdt", [np.float64, np.float32])
+def test_split_nan_entries(oracle, xdt):
+    """The row maximum ignores NaN (Triton's maximum without NaN propagation).
+    An int8 slice of a NaN is 0 at every level, so the split equals the split of
+    the row with the NaN replaced by 0; a float slice keeps the NaN at every
+    level (the residual stays NaN), with every other entry unchanged."""
+    rng = np.random.default_rng(3)
+    X = rng.standard_normal((4, 300)) * np.array([[1.0], [1e3], [1e-3], [1.0]])
+    X[1, 17] = np.nan
+    X[2, [0, 299]] = np.nan
+    X[3, :] = np.nan
+    nan = np.isnan(X)
+    Xz = np.where(nan, 0.0, X)
+    for L in (1, 3):
+        sl, sc = oracle.split(X.astype(xdt), L, 7, "int8")
+        slz, scz = oracle.split(Xz.astype(xdt), L, 7, "int8")
+        np.testing.assert_array_equal(sl, slz)
+        np.testing.assert_array_equal(sc, scz)
+        fl, fc = oracle.split(X.astype(xdt), L, 5, "float16")
+        flz, fcz = oracle.split(Xz.astype(xdt), L, 5, "float16")
+        np.testing.assert_array_equal(fc, fcz)
+        for lv in range(L):
+            got = fl[lv].view(np.float16)
+            assert np.array_equal(np.isnan(got), nan)
+            np.testing.assert_array_equal(fl[lv][~nan], flz[lv][~nan])
+
+
+# --------------------------------------------------------------------------- #
+# float-slice cross-GEMM (ozaki_triton.py:403-418, :427-447)
+# --------------------------------------------------------------------------- #
+@pytest.mark.parametrize("slice_dtype", ["float16", "bfloat16", "float32"])
+@pytest.mark.parametrize("L", [1, 2, 4])
+def test_float_cross_gemm_equals_numpy_matmul_when_exact(oracle, slice_dtype, L):
+    """Integer-valued slices (|v| <= 32, K = 4096) and scales 2^[0, 3]: every
+    dot is an integer below 2^24, every scaled term and the fp64 sum are
+    integers below 2^53, so C is exact whatever the order.  The oracle must
+    then equal numpy's float64 matmul of the slice values bit for bit, which
+    pins its dot (operands, transposition, which pair goes with which scales)
+    independently of its own code."""
+    import torch
+    from tests.helpers import int_valued_slices, values
+    g = torch.Generator().manual_seed(40 + L)
+    sdt = {"float16": torch.float16, "bfloat16": torch.bfloat16, "float32": torch.float32}[slice_dtype]
+    M, N, K = 24, 20, 4096
+    As, BsT, sa, sb = int_valued_slices(g, 1, L, M, N, K, sdt, exp_range=(0, 4))
+    to = {torch.bfloat16: lambda t: t.view(torch.int16).numpy().view(np.uint16)}.get(
+        sdt, lambda t: t.numpy())
+    a, b = to(As[0]), to(BsT[0])
+    s_a, s_b = sa[0].numpy(), sb[0].numpy()
+    got = oracle.cross_gemm(a, b, s_a, s_b, "float64")
+    want = np.zeros((M, N))
+    for i in range(L):
+        for j in range(L):
+            want += (values(a[i]) @ values(b[j]).T) * s_a[i][:, None] * s_b[j][None, :]
+    np.testing.assert_array_equal(got, want)
+
+
+def test_float_cross_gemm_matches_numpy_on_general_slices(oracle):
+    """fp16 slices with general values and a wide scale range: the oracle's
+    binary64 dot, rounded to fp32 per the reference's epilogue, stays within
+    a few fp32 ulps of each term of numpy's float64 product."""
+    rng = np.random.default_rng(12)
+    L, M, N, K = 3, 16, 12, 2048
+    a = rng.uniform(-64, 64, (L, M, K)).astype(np.float16)
+    b = rng.uniform(-64, 64, (L, N, K)).astype(np.float16)
+    s_a = (2.0 ** rng.integers(-20, 5, (L, M))).astype(np.float32)
+    s_b = (2.0 ** rng.integers(-20, 5, (L, N))).astype(np.float32)
+    got = oracle.cross_gemm(a, b, s_a, s_b, "float64")
+    want = np.zeros((M, N))
+    mag = np.zeros((M, N))
+    for i in range(L):
+        for j in range(L):
+            t = (a[i].astype(np.float64) @ b[j].astype(np.float64).T) * s_a[i][:, None] * s_b[j][None, :]
+            want += t
+            mag += np.abs(t)
+    assert np.all(np.abs(got - want) <= 4 * 2.0 ** -24 * mag)
+
+
+@pytest.mark.parametrize("slice_dtype,L,K", [("float16", 2, 4096), ("bfloat16", 3, 2048),
+                                             ("float32", 4, 1024), ("float16", 4, 8192)])
+def test_int_valued_check_catches_a_dropped_pair(oracle, slice_dtype, L, K):
+    """The bit-exact check of the GPU float-slice kernels (integer-valued
+    slices, tests/helpers.py:int_valued_slices) must fail for a kernel that
+    leaves out any one slice pair: the oracle with that pair's term planted
+    out differs from the full result in almost every entry."""
+    import torch
+    from tests.helpers import bits, int_valued_slices
+    g = torch.Generator().manual_seed(K + L)
+    sdt = {"float16": torch.float16, "bfloat16": torch.bfloat16, "float32": torch.float32}[slice_dtype]
+    As, BsT, sa, sb = int_valued_slices(g, 1, L, 32, 24, K, sdt)
+    to = {torch.bfloat16: lambda t: t.view(torch.int16).numpy().view(np.uint16)}.get(
+        sdt, lambda t: t.numpy())
+    a, b, s_a, s_b = to(As[0]), to(BsT[0]), sa[0].numpy(), sb[0].numpy()
+    full = bits(oracle.cross_gemm(a, b, s_a, s_b, "float64"))
+    for p in range(L * L):
+        dropped = bits(oracle.cross_gemm(a, b, s_a, s_b, "float64", skip_pair=p))
+        assert (dropped != full).mean() > 0.9, (p, (dropped != full).mean())
+
+
+@pytest.mark.parametrize("value,want", [
+    (-2.75, -2), (2.75, 2), (127.875, 127), (300.0, 127), (-129.5, -128), (-128.5, -128),
+    (float("nan"), 0), (float("inf"), 127), (float("-inf"), -128), (-0.5, 0)])
+def test_int8_output_truncates_and_saturates(oracle, value, want):
+    """int8 C (ozaki_triton.py:452 stores out.to(int8)): the reference's GPU
+    conversion is PTX cvt.rzi.s8.f32, which rounds toward zero, clamps to the
+    destination range and maps NaN to 0 (PTX ISA, cvt: float-to-integer
+    conversions saturate).  Each expected value here is written from that rule
+    by hand; the mistakes it excludes are floor for negatives (-2.75 -> -3),
+    rounding (2.75 -> 3) and wrap-around (300 -> 44).  One 1 x 1 x 1 product
+    per case: acc = a * b, t = acc * sa * sb exactly."""
+    cases = {-2.75: (-11, 1, 0.25), 2.75: (11, 1, 0.25), 127.875: (31, 33, 0.125),
+             300.0: (75, 4, 1.0), -129.5: (-37, 7, 0.5), -128.5: (-1, 1, 128.5),
+             -0.5: (-1, 1, 0.5)}
+    if math.isnan(value) or math.isinf(value):
+        a, b, s = 1, 1, value
+    else:
+        a, b, s = cases[value]
+    A = np.array([[[a]]], dtype=np.int8)
+    B = np.array([[[b]]], dtype=np.int8)
+    sa = np.array([[s]], dtype=np.float32)
+    sb = np.array([[1.0]], dtype=np.float32)
+    assert float(oracle.cross_gemm(A, B, sa, sb, "float32")[0, 0]) == pytest.approx(value, nan_ok=True)
+    assert int(oracle.cross_gemm(A, B, sa, sb, "int8")[0, 0]) == want
