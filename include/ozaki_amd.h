@@ -56,9 +56,11 @@ enum {
     OZK_ERR_WORKSPACE = -6,   /* workspace missing, too small or not 16-byte aligned */
     OZK_ERR_LAUNCH = -7,      /* a HIP launch failed (hipGetLastError) */
     OZK_ERR_ACCUM = -8,       /* unsupported dot accumulator dtype */
-    OZK_ERR_DEVICE_WAIT = -9  /* (ozk_device_status) a cooperative split wait on the
+    OZK_ERR_DEVICE_WAIT = -9, /* (ozk_device_status) a cooperative split wait on the
                                  device gave up; that split's scales, and so the C
                                  computed from them, are NaN */
+    OZK_ERR_TOO_LARGE = -10   /* (ozk_matmul_static) the call needs more scratch than
+                                 OZK_STATIC_SCRATCH_BYTES */
 };
 
 /* The reference's ozaki_matmul asserts num_splits <= 4 (ozaki_triton.py:563),
@@ -183,6 +185,25 @@ int ozk_matmul(const void *A, const int64_t a_strides[3], const void *B,
                const int64_t b_strides[3], int dtype, int64_t batch, int64_t M, int64_t N,
                int64_t K, int num_splits, int slice_dtype, void *C, const int64_t c_strides[3],
                void *workspace, size_t workspace_bytes, void *const events[4], void *stream);
+
+/*
+ * Matmul without a workspace -- no counterpart in the reference.  For callers
+ * that cannot allocate device memory at all (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc): ozk_matmul with its
+ * workspace taken from a library-owned device array of OZK_STATIC_SCRATCH_BYTES,
+ * one per device, held until the process ends.  The caller still passes the
+ * inputs and C.  A call whose ozk_matmul_workspace_bytes() exceeds that
+ * returns OZK_ERR_TOO_LARGE before anything is enqueued.  The call allocates
+ * nothing (no hipMalloc, hipFree or allocating library routine).  All calls on
+ * one device share its array: calls that overlap on one device (other streams
+ * or threads, without ordering between them) race and give wrong results.
+ */
+#define OZK_STATIC_SCRATCH_BYTES ((size_t)64 << 20)
+
+int ozk_matmul_static(const void *A, const int64_t a_strides[3], const void *B,
+                      const int64_t b_strides[3], int dtype, int64_t batch, int64_t M,
+                      int64_t N, int64_t K, int num_splits, int slice_dtype, void *C,
+                      const int64_t c_strides[3], void *const events[4], void *stream);
 
 #ifdef __cplusplus
 }

@@ -23,6 +23,8 @@ OZK_ERR_WORKSPACE = -6
 OZK_ERR_LAUNCH = -7
 OZK_ERR_ACCUM = -8
 OZK_ERR_DEVICE_WAIT = -9
+OZK_ERR_TOO_LARGE = -10
+OZK_STATIC_SCRATCH_BYTES = 64 << 20
 OZK_MAX_SPLITS = 8
 
 # every symbol include/ozaki_amd.h declares
@@ -37,6 +39,7 @@ EXPORTED = (
     "ozk_cross_gemm",
     "ozk_matmul_workspace_bytes",
     "ozk_matmul",
+    "ozk_matmul_static",
 )
 
 # the test hooks of include/ozaki_amd_debug.h
@@ -96,6 +99,9 @@ def load() -> ctypes.CDLL:
     L.ozk_matmul.argtypes = [vp, p64, vp, p64, i32, i64, i64, i64, i64, i32, i32, vp, p64, vp,
                              sz, ctypes.POINTER(ctypes.c_void_p), vp]
     L.ozk_matmul.restype = i32
+    L.ozk_matmul_static.argtypes = [vp, p64, vp, p64, i32, i64, i64, i64, i64, i32, i32, vp,
+                                    p64, ctypes.POINTER(ctypes.c_void_p), vp]
+    L.ozk_matmul_static.restype = i32
     cp = ctypes.c_char_p
     L.ozk_debug_force_gemm_kernel.argtypes = [cp]
     L.ozk_debug_force_gemm_kernel.restype = i32

@@ -9,6 +9,8 @@
 
 #include <string.h>
 
+#include <atomic>
+
 #include "../../include/ozaki_amd.h"
 #include "../../include/ozaki_amd_debug.h"
 #include "ozk_internal.h"
@@ -89,6 +91,7 @@ const char *ozk_strerror(int status) {
     case OZK_ERR_ACCUM: return "unsupported dot accumulator dtype";
     case OZK_ERR_DEVICE_WAIT:
         return "a cooperative split wait gave up on the device (its scales and C are NaN)";
+    case OZK_ERR_TOO_LARGE: return "the call needs more scratch than OZK_STATIC_SCRATCH_BYTES";
     default: return "unknown status";
     }
 }
@@ -441,6 +444,58 @@ int ozk_matmul(const void *A, const int64_t a_strides[3], const void *B,
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// ozk_matmul_static: ozk_matmul on a library-owned scratch buffer, for callers
+// that cannot allocate.  `scratch` is a file-scope device array; every device
+// holds its own copy at its own address.  In host code the array's name is
+// only a stand-in for the symbol, so its device address is asked once per
+// device (hipGetSymbolAddress, with that device current) and only that
+// address is handed to the kernels.  Every region the kernels read is written
+// by the same call first, and the exchange words of the cooperative splits
+// are cleared by a fill kernel at each launch, so nothing depends on what an
+// earlier call left in the array.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) char scratch[OZK_STATIC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<void *> g_scratch_ptr[kMaxDevices];   // device address of `scratch`, per device
+
+int static_scratch(void **out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return OZK_ERR_LAUNCH;
+    void *ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (!ptr) {
+        // first call on this device (concurrent first calls store the same address)
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr)
+            return OZK_ERR_LAUNCH;
+        g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+    }
+    *out = ptr;
+    return OZK_OK;
+}
+}  // namespace
+
+extern "C" int ozk_matmul_static(const void *A, const int64_t a_strides[3], const void *B,
+                                 const int64_t b_strides[3], int dtype, int64_t batch,
+                                 int64_t M, int64_t N, int64_t K, int num_splits,
+                                 int slice_dtype, void *C, const int64_t c_strides[3],
+                                 void *const events[4], void *stream) {
+    if (!a_strides || !b_strides || !c_strides) return OZK_ERR_NULL;
+    MatmulLayout lay;
+    const int lst = matmul_layout(dtype, batch, M, N, K, a_strides, b_strides, num_splits,
+                                  slice_dtype, &lay);
+    if (lst != OZK_OK) return lst;
+    if (batch * M * N == 0 || num_splits == 0)   // no workspace used
+        return ozk_matmul(A, a_strides, B, b_strides, dtype, batch, M, N, K, num_splits,
+                          slice_dtype, C, c_strides, nullptr, 0, events, stream);
+    if (lay.total > OZK_STATIC_SCRATCH_BYTES) return OZK_ERR_TOO_LARGE;
+    void *ws = nullptr;
+    if (const int e = static_scratch(&ws)) return e;
+    return ozk_matmul(A, a_strides, B, b_strides, dtype, batch, M, N, K, num_splits,
+                      slice_dtype, C, c_strides, ws, OZK_STATIC_SCRATCH_BYTES, events, stream);
+}
 
 // ---------------------------------------------------------------------------
 // Test hooks (include/ozaki_amd_debug.h)

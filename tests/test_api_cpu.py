@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_strerror_names_every_code():
     from ozaki_triton_amd import _lib
-    for code in range(0, -10, -1):
+    for code in range(0, -11, -1):
         assert _lib.strerror(code) != "unknown status"
     assert _lib.strerror(-99) == "unknown status"
 
