@@ -507,7 +507,8 @@ struct Named {
 };
 const Named kGemmNames[] = {{"staged", ozk::kGemmStaged}, {"dma", ozk::kGemmDMA},
                             {"ad", ozk::kGemmAD},         {"pair", ozk::kGemmPair},
-                            {"ring", ozk::kGemmRing},     {"wide", ozk::kGemmWide}};
+                            {"ring", ozk::kGemmRing},     {"wide", ozk::kGemmWide},
+                            {"wide4", ozk::kGemmWide4}};
 const Named kSplitNames[] = {{"coop", ozk::kForceSplitCoop},
                              {"strip", ozk::kForceSplitStrip},
                              {"transpose", ozk::kForceSplitTranspose},

@@ -1426,6 +1426,356 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide_kernel(GemmParams p, i
 }
 
 // ---------------------------------------------------------------------------
+// Wide kernel for num_splits 4: 96 x 64 tiles (row blocks x = 0..2, column
+// blocks y = 0..1 of 32 x 32), 8 waves of 12 accumulator tiles each, so that
+// every wave reads 3 A and 4 B fragments per 32-byte K step for 12 MFMAs
+// (0.58 fragment reads per MFMA; the ring kernel's 64 x 64 tiles: 0.75) and a
+// stage of 128 bytes of K (48 KB of A rows, 32 KB of B rows) feeds 384 MFMAs
+// (0.21 KB of DMA per MFMA; ring: 0.25).
+//   * waves 0..5 (x = wave / 2, y = wave % 2) hold the pairs i = 0..2, j = 0..3
+//     of block (x, y): A fragments (slice u, rows of x), u = 0..2;
+//   * waves 6, 7 (y = wave - 6) hold the pairs i = 3, j = 0..3 of the blocks
+//     (0..2, y): A fragments (slice 3, rows of block u), u = 0..2;
+//   * every wave: B fragments (slice j, columns of y), j = 0..3, and
+//     acc[u][j] += A_u . B_j.
+// The reference's sum runs i-major, so the i = 3 pairs come last: a wave of
+// the first kind sums its 12 pairs in order from +0 and hands the partial to
+// the wave of its y through the LDS, which adds its 4 pairs in order and
+// stores C.  The second kind converts its accumulators to the fp32 t values
+// before the hand-off barrier, so only the additions follow it.
+// 12 accumulator tiles are 192 registers of the 256 a wave has at two waves
+// per SIMD, so only the A fragments are double-buffered: the B fragments of
+// the next K step are read one by one as the MFMAs of the current step
+// release them (j-outer order), 9 MFMAs before their first use.
+// The LDS holds two whole stages (160 KB); stage kb + 2 is fetched into stage
+// kb's buffer after the barrier of stage kb, P1 instructions per wave in the
+// K step after that barrier and the rest in the next.
+// ---------------------------------------------------------------------------
+struct Wide4Shape {
+    static constexpr int L = 4;
+    static constexpr int NW = 8;                         // waves
+    static constexpr int BM = 96, BN = 64;
+    static constexpr int A_BYTES = L * BM * kDmaRB;      // 48 KB
+    static constexpr int B_BYTES = L * BN * kDmaRB;      // 32 KB
+    static constexpr int STAGE = A_BYTES + B_BYTES;
+    static constexpr int LA = A_BYTES / (NW * 1024);     // A instructions per wave per stage
+    static constexpr int LB = B_BYTES / (NW * 1024);     // B instructions per wave per stage
+    static constexpr int LPS = LA + LB;
+    static constexpr int P1 = 6;                         // issued in the K step after the barrier
+    static constexpr int LDS_BYTES = 2 * STAGE;
+    static constexpr int NSC = L * (BM + BN) / 64;       // scale instructions (64 entries each)
+    static_assert(A_BYTES % (NW * 1024) == 0 && B_BYTES % (NW * 1024) == 0,
+                  "a half stage must be whole 1 KB windows per wave");
+    static_assert(P1 >= LPS - P1 && P1 <= LPS, "the larger part goes first");
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS");
+    static_assert(NSC <= 2 * NW, "two scale instructions per wave at most");
+    static_assert(kDmaRB == 128, "128-byte stage rows");
+};
+
+template <typename ST, typename AccT>
+__global__ __launch_bounds__(512, 1) void cross_gemm_wide4_kernel(GemmParams p, int group_m,
+                                                                  uint32_t a_records,
+                                                                  uint32_t b_records) {
+    using Sh = Wide4Shape;
+    using MF = Mfma<ST>;
+    using Acc = typename MF::Acc;
+    using OA = AccT;
+    constexpr int L = Sh::L, BM = Sh::BM, BN = Sh::BN;
+    constexpr int ES = (int)sizeof(ST);
+    constexpr uint32_t kOOB = 0x80000000u;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool last_i = wave >= 6;                 // holds the pairs i = 3
+    const int wy = last_i ? wave - 6 : (wave & 1);
+    const int wx = last_i ? 0 : (wave >> 1);
+    // A fragment u: LDS row a_row0 + u * a_rstep (+ lane row)
+    const int a_row0 = last_i ? 3 * BM : wx * 32;
+    const int a_rstep = last_i ? 32 : BM;
+    const int h = lane >> 5, lr = lane & 31;
+
+    const int64_t tiles_m = (p.M + BM - 1) / BM;
+    const int64_t tiles_n = (p.N + BN - 1) / BN;
+    const int64_t tiles = tiles_m * tiles_n;
+    const int64_t g = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
+    const int64_t bidx = g / tiles;
+    const int64_t t = g % tiles;
+    const int64_t width = (int64_t)group_m * tiles_n;
+    const int64_t first_m = (t / width) * group_m;
+    const int64_t gsz = (tiles_m - first_m < group_m) ? (tiles_m - first_m) : group_m;
+    const int64_t tm = first_m + (t % width) % gsz;
+    const int64_t tn = (t % width) / gsz;
+    const int64_t m0 = tm * BM, n0 = tn * BN;
+
+    const uint32_t kbytes = (uint32_t)(p.K * ES);
+    const int nkb = (int)((kbytes + kDmaRB - 1) / kDmaRB);
+
+    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const char *)p.A + bidx * p.as_b * ES), (short)0, (int)a_records, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const char *)p.B + bidx * p.bs_b * ES), (short)0, (int)b_records, 0x00020000);
+
+    // This wave's LPS DMA instructions of a stage: q < LA fetch window
+    // wave * LA + q of the A half, the others window wave * LB + q - LA of the
+    // B half (a 1 KB window is 8 whole 128-byte rows; lane -> row lane / 8,
+    // physical chunk lane % 8, which holds logical chunk pc ^ ((r >> 1) & 7);
+    // with r = 8 window + lane / 8 that is c0, or c0 ^ 4 in an odd window).
+    // A window (8 rows) never straddles a slice (96 or 64 rows = 12 or 8
+    // windows), so an instruction's source offset is a wave-uniform part (slice,
+    // first row of the window, K block) plus one of four per-lane parts (lane
+    // row lane / 8 and chunk, for A or B and even or odd windows).  The uniform
+    // part goes through readfirstlane at each use, so the compiler keeps just
+    // the four lane parts in registers instead of one sum per instruction.
+    auto window = [&](int q) { return q < Sh::LA ? wave * Sh::LA + q : wave * Sh::LB + q - Sh::LA; };
+    const int lrow = lane >> 3;
+    const int c0 = (lane & 7) ^ (lane >> 4);
+    const uint32_t ch16[2] = {(uint32_t)c0 * 16, (uint32_t)(c0 ^ 4) * 16};
+    const uint32_t a_lp[2] = {(uint32_t)(lrow * p.as_m * ES) + ch16[0],
+                              (uint32_t)(lrow * p.as_m * ES) + ch16[1]};
+    const uint32_t b_lp[2] = {(uint32_t)(lrow * p.bs_n * ES) + ch16[0],
+                              (uint32_t)(lrow * p.bs_n * ES) + ch16[1]};
+    auto buf = [&](int kb) { return smem + (kb & 1) * Sh::STAGE; };
+    auto issue = [&](int kb, int q) {
+        const int w = window(q);
+        const int par = w & 1;
+        int64_t first, rows;
+        int64_t ubase;
+        if (q < Sh::LA) {
+            first = m0 + (w % (BM / 8)) * 8;
+            rows = p.M;
+            ubase = ((int64_t)(w / (BM / 8)) * p.as_l + first * p.as_m) * ES;
+        } else {
+            first = n0 + (w % (BN / 8)) * 8;
+            rows = p.N;
+            ubase = ((int64_t)(w / (BN / 8)) * p.bs_l + first * p.bs_n) * ES;
+        }
+        const int rows_left = (int)(rows - first < 8 ? rows - first : 8);   // may be <= 0
+        const int kleft = (int)kbytes - kb * kDmaRB;                       // > 0
+        const uint32_t ub = (uint32_t)__builtin_amdgcn_readfirstlane((int)(ubase + kb * kDmaRB));
+        const bool ok = lrow < rows_left && (int)ch16[par] < kleft;
+        const uint32_t vo = ok ? (q < Sh::LA ? a_lp[par] : b_lp[par]) + ub : kOOB;
+        auto *ldsp = (__attribute__((address_space(3))) void *)(
+            buf(kb) + (q < Sh::LA ? 0 : Sh::A_BYTES) + w * 1024);
+        if (q < Sh::LA) __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, ldsp, 16, vo, 0, 0, 0);
+        else __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, ldsp, 16, vo, 0, 0, 0);
+    };
+
+    // The tile's scales (A's [L][BM], then B's [L][BN]: 2560 bytes) are
+    // fetched by dword DMA into the buffer of stage nkb, which holds no stage
+    // the tile still reads, at the start of the last stage: instruction
+    // u < NSC (wave u and wave u - 8) fetches entries 64 u .. 64 u + 63.
+    char *const scl = buf(nkb);
+    auto issue_scales = [&]() {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int u = q * Sh::NW + wave;
+            if (u >= Sh::NSC) break;
+            const bool isa = u < L * BM / 64;
+            const int e = (isa ? u : u - L * BM / 64) * 64 + lane;
+            const int s = isa ? e / BM : e / BN;                 // slice
+            const int64_t rc = isa ? m0 + e % BM : n0 + e % BN;  // row of A / column of B
+            const int64_t ext = isa ? ((int64_t)(L - 1) * p.sas_l + (p.M - 1) * p.sas_m + 1)
+                                    : ((int64_t)(L - 1) * p.sbs_l + (p.N - 1) * p.sbs_n + 1);
+            const bool ok = rc < (isa ? p.M : p.N);
+            const uint32_t vo = ok ? (uint32_t)(((int64_t)s * (isa ? p.sas_l : p.sbs_l) +
+                                                 rc * (isa ? p.sas_m : p.sbs_n)) * 4)
+                                   : kOOB;
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)(isa ? p.sa + bidx * p.sas_b : p.sb + bidx * p.sbs_b), (short)0,
+                (int)(ext * 4 < 0x7FFFFFFF ? ext * 4 : 0x7FFFFFFF), 0x00020000);
+            auto *ldsp = (__attribute__((address_space(3))) void *)(scl + u * 256);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, ldsp, 4, vo, 0, 0, 0);
+        }
+    };
+    const float *sa_lds = (const float *)scl, *sb_lds = (const float *)(scl + L * BM * 4);
+
+    // prologue: stages 0 and 1; stage 0 must land before the first reads
+#pragma unroll
+    for (int q = 0; q < Sh::LPS; ++q) issue(0, q);
+    if (nkb > 1) {
+#pragma unroll
+        for (int q = 0; q < Sh::LPS; ++q) issue(1, q);
+        wait_vmcnt<Sh::LPS>();
+    } else {
+        wait_vmcnt<0>();
+    }
+    exec_barrier();
+
+    struct FragsA {
+        i32x4 a[3];
+    };
+    i32x4 fb[L];   // B fragments, single-buffered
+    Acc acc[3][L];
+#pragma unroll
+    for (int u = 0; u < 3; ++u)
+#pragma unroll
+        for (int j = 0; j < L; ++j) acc[u][j] = MF::zero();
+
+    // Fragment rows start at multiples of 32, so the swizzle key of a lane's
+    // row, ((row >> 1) & 7), is that of lr for every fragment: the address is
+    // a wave-uniform row offset plus one of four per-lane offsets (one per
+    // K step of a stage), rswz<kDmaRB> with its terms regrouped.
+    // The uniform part (buffer, first row) goes through readfirstlane at each
+    // use, so only the four per-lane offsets stay in registers.
+    const int key = (lr >> 1) & 7;
+    int lane_rd[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) lane_rd[kk] = lr * kDmaRB + (((2 * kk + h) ^ key) << 4);
+    const int smem_base = (int)(uintptr_t)(__attribute__((address_space(3))) char *)smem;
+    auto lds_at = [&](int uniform, int kk) {
+        const int u = __builtin_amdgcn_readfirstlane(uniform);
+        return (const __attribute__((address_space(3))) i32x4 *)(uintptr_t)(u + lane_rd[kk]);
+    };
+    auto read_a = [&](int kb, int kk, int u, FragsA &f) {
+        f.a[u] = *lds_at(smem_base + (kb & 1) * Sh::STAGE + (a_row0 + u * a_rstep) * kDmaRB, kk);
+    };
+    auto read_b = [&](int kb, int kk, int j) {
+        fb[j] = *lds_at(smem_base + (kb & 1) * Sh::STAGE + Sh::A_BYTES + (j * BN + wy * 32) * kDmaRB, kk);
+    };
+    // One K step: the A reads of the next K step (stage rkb, step nkk) into
+    // `nxt`, issued first; then the 12 MFMAs of `cur` and the current B
+    // fragments, j-outer, each B fragment re-read for the next step after its
+    // last MFMA; with, if `on`, DMA instructions [lo, hi) of stage dkb spread
+    // between them (lo and hi are constants at every call, so the spread
+    // folds at compile time).
+    auto step = [&](const FragsA &cur, FragsA &nxt, int rkb, int nkk, int dkb, bool on, int lo,
+                    int hi) {
+        const int cnt = hi - lo;
+#pragma unroll
+        for (int u = 0; u < 3; ++u) read_a(rkb, nkk, u, nxt);
+#pragma unroll
+        for (int n = 0; n < 3 * L; ++n) {
+            const int j = n / 3, u = n % 3;
+            acc[u][j] = MF::run(cur.a[u], fb[j], acc[u][j]);
+            if (u == 2) read_b(rkb, nkk, j);
+#pragma unroll
+            for (int d = 0; d < Sh::P1; ++d) {
+                // instruction lo + d goes after MFMA (d * 12) / cnt
+                if (d < cnt && (d * 3 * L) / cnt == n && on) issue(dkb, lo + d);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    FragsA f0, f1;
+    if (nkb > 0) {
+#pragma unroll
+        for (int u = 0; u < 3; ++u) read_a(0, 0, u, f0);
+#pragma unroll
+        for (int j = 0; j < L; ++j) read_b(0, 0, j);
+    }
+    static_assert(kDmaRB / 32 == 4, "four 32-byte K steps per stage");
+    if (nkb == 0) issue_scales();
+    for (int kb = 0; kb < nkb; ++kb) {
+        const bool nb = kb + 1 < nkb, n2 = kb + 2 < nkb;
+        // no DMA is outstanding in the last stage: its waits are unaffected
+        if (!nb) issue_scales();
+        // the rest of stage kb + 1 (stage 1 went out whole in the prologue)
+        step(f0, f1, kb, 1, kb + 1, nb && kb >= 1, Sh::P1, Sh::LPS);
+        step(f1, f0, kb, 2, kb + 1, false, 0, 0);
+        step(f0, f1, kb, 3, kb + 1, false, 0, 0);
+        if (nb) {
+            // stage kb + 1 is the only DMA outstanding; the barrier publishes
+            // every wave's DMA writes, and the lgkmcnt wait makes this wave's
+            // reads of stage kb complete before its buffer is refilled
+            wait_vmcnt<0>();
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            exec_barrier();
+        }
+        // the last step reads stage kb + 1's step 0 (unused past the end)
+        step(f1, f0, kb + 1, 0, kb + 2, n2, 0, Sh::P1);
+    }
+
+    // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
+    wait_vmcnt<0>();
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    exec_barrier();
+    const int ct = wy * 32 + lr;
+    const int64_t col = n0 + ct;
+    const int64_t cbase = bidx * p.cs_b;
+    float sbv[L];
+#pragma unroll
+    for (int j = 0; j < L; ++j) sbv[j] = sb_lds[j * BN + ct];
+    // rows of accumulator registers 4 q .. 4 q + 3 of A fragment u, inside the
+    // tile, start at row4(u, q): their 4 scales are one 16-byte LDS read
+    auto row4 = [&](int u, int q) { return (last_i ? u * 32 : wx * 32) + 8 * q + 4 * h; };
+    auto sa4 = [&](int i, int u, int q) {
+        return *(const f32x4 *)(sa_lds + i * BM + row4(u, q));
+    };
+    // the i = 3 waves: t values fl32(fl32(fl32(acc) * sa_3) * sb_j) in place
+    // of their accumulators, before the hand-off (one block at a time, each
+    // behind a scheduling barrier: the scale reads are not hoisted).  The
+    // accumulator vectors are bit-cast whole: with this compiler a bit-cast of
+    // single elements of a vector reads element 0.
+    if (last_i) {
+#pragma unroll
+        for (int u = 0; u < 3; ++u) {
+            f32x4 s4[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) s4[q] = sa4(3, u, q);
+#pragma unroll
+            for (int j = 0; j < L; ++j) {
+                f32x16 tv;
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    tv[r] = (MF::to_f32(acc[u][j][r]) * s4[r >> 2][r & 3]) * sbv[j];
+                acc[u][j] = __builtin_bit_cast(Acc, tv);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // the partial sums go to the buffer of the last stage, which every wave
+    // has finished reading (the scales sit in the other one)
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    exec_barrier();
+    OA *part = (OA *)buf(nkb + 1);   // [6 blocks][16][64 lanes]
+    static_assert(6 * 16 * 64 * sizeof(OA) <= Sh::STAGE, "the partials fit a stage buffer");
+    if (!last_i) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            f32x4 s4[3];
+#pragma unroll
+            for (int i = 0; i < 3; ++i) s4[i] = sa4(i, 0, q);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = 4 * q + e;
+                OA out = (OA)0;
+#pragma unroll
+                for (int i = 0; i < 3; ++i)
+#pragma unroll
+                    for (int j = 0; j < L; ++j) {
+                        // fl32(fl32(fl32(acc) * sa_i) * sb_j), summed i-major, j-minor
+                        const float t1 = MF::to_f32(acc[i][j][r]) * s4[i][e];
+                        out = out + (OA)(t1 * sbv[j]);
+                    }
+                part[(wave * 16 + r) * 64 + lane] = out;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        exec_barrier();
+    } else {
+        exec_barrier();
+#pragma unroll
+        for (int u = 0; u < 3; ++u) {
+            f32x16 tv[L];
+#pragma unroll
+            for (int j = 0; j < L; ++j) tv[j] = __builtin_bit_cast(f32x16, acc[u][j]);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = m0 + row4(u, r >> 2) + (r & 3);
+                OA out = part[((u * 2 + wy) * 16 + r) * 64 + lane];
+#pragma unroll
+                for (int j = 0; j < L; ++j) out = out + (OA)tv[j][r];
+                if (col < p.N && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // A-direct variant.  The four waves are stacked along M (workgroup tile
 // 128 x 32*NI); each wave streams ITS OWN 32 rows of every A slice from global
 // memory straight into VGPRs (no LDS), and only B, which all four waves share,
@@ -1763,10 +2113,18 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
     const int64_t wide_rounds = (p.batch * ((p.M + 63) / 64) * ((p.N + 127) / 128) + kCUs - 1) / kCUs;
     const int64_t ring_rounds = (nt(1, 1) + kCUs - 1) / kCUs;
     const bool wide3 = L == 3 && 12 * wide_rounds < 7 * ring_rounds;
+    // L = 4: the 96 x 64 wide kernel (one workgroup per CU, like the ring
+    // kernel) does 1.5 ring tiles of work per tile at 1.04-1.14x the ring's
+    // rate, about 1.45 ring tiles' time (measured: 8192^3 43 rounds against
+    // 64, 0.965x the ring's time; 4096^2 x 8192 11 / 16, 0.875x; 2048^2 x
+    // 8192 3 / 4, 0.99x; 1024^2 x 65536 1 / 1, 1.10x)
+    const int64_t wide4_rounds = (p.batch * ((p.M + 95) / 96) * ((p.N + 63) / 64) + kCUs - 1) / kCUs;
+    const bool wide4 = L == 4 && 29 * wide4_rounds < 20 * ring_rounds;
     plan.kind = !fits              ? kGemmStaged
                 : L <= 1           ? kGemmDMA
                 : L == 2           ? ((mi == 2 && ni == 2) ? kGemmRing : kGemmDMA)
                 : wide3            ? kGemmWide
+                : wide4            ? kGemmWide4
                 : L <= 4           ? kGemmRing
                                    : kGemmPair;
     if (L > 4) return plan;   // only the pair-split kernel, launched per i-row range
@@ -1778,6 +2136,7 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
     else if (fits && forced(kGemmPair)) plan.kind = L >= 3 ? kGemmPair : kGemmDMA;
     else if (fits && forced(kGemmRing)) plan.kind = L >= 2 ? kGemmRing : kGemmDMA;
     else if (fits && forced(kGemmWide)) plan.kind = L == 3 ? kGemmWide : plan.kind;
+    else if (fits && forced(kGemmWide4)) plan.kind = L == 4 ? kGemmWide4 : plan.kind;
     if (plan.kind == kGemmAD) plan.group_m = 2;
     return plan;
 }
@@ -1892,6 +2251,22 @@ static hipError_t launch_wide(const GemmParams &p, const GemmPlan &plan, hipStre
     return hipGetLastError();
 }
 
+template <typename ST, typename AccT>
+static hipError_t launch_wide4(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
+    using Sh = Wide4Shape;
+    auto kern = cross_gemm_wide4_kernel<ST, AccT>;
+    static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
+    if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
+    const int es = (int)sizeof(ST);
+    const int64_t ea = dma_extent(p.as_l, p.as_m, Sh::L, p.M, p.K, es);
+    const int64_t eb = dma_extent(p.bs_l, p.bs_n, Sh::L, p.N, p.K, es);
+    const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
+    if (tiles == 0) return hipSuccess;
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(512), Sh::LDS_BYTES, st, p,
+                       plan.group_m, (uint32_t)ea, (uint32_t)eb);
+    return hipGetLastError();
+}
+
 // num_splits = 5..8: launches over consecutive i-rows (at most 16 pairs each,
 // so a wave group still holds 8 pairs), in i-major order, each continuing the
 // fp64 sum from C.  int8 / fp16 / bf16 slices with an fp64 outer accumulator.
@@ -1918,6 +2293,9 @@ static hipError_t launch_one(const GemmParams &p, const GemmPlan &plan, hipStrea
     }
     if constexpr (L == 3) {
         if (plan.kind == kGemmWide) return launch_wide<ST, AccT>(p, plan, st);
+    }
+    if constexpr (L == 4) {
+        if (plan.kind == kGemmWide4) return launch_wide4<ST, AccT>(p, plan, st);
     }
     if constexpr (L >= 2 && L <= 4) {
         if (plan.kind == kGemmRing) return launch_ring<ST, L, AccT>(p, plan, st);

@@ -106,8 +106,10 @@ enum GemmKind {
     kGemmPair = 3,    // LDS-DMA ring, 8 waves: 2 x 2 blocks x 2 halves of the slice pairs
     kGemmRing = 4,    // the pair split over a five-slot ring of half stages, DMA spread
                       // between the MFMAs (num_splits 3 and 4)
-    kGemmWide = 5     // num_splits 3: 64 x 128 tiles, 8 waves each holding all 9 pairs
+    kGemmWide = 5,    // num_splits 3: 64 x 128 tiles, 8 waves each holding all 9 pairs
                       // of a 32 x 32 block, two whole stages in the LDS
+    kGemmWide4 = 6    // num_splits 4: 96 x 64 tiles, 8 waves of 12 accumulator tiles
+                      // (3 A x 4 B fragments), two whole stages in the LDS
 };
 struct GemmPlan {
     int mi, ni;       // 2 x 2 kernels: wave tile = (32*mi) x (32*ni)

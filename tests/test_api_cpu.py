@@ -442,7 +442,7 @@ def test_debug_hooks_reject_unknown_names():
     L = _lib.load()
     assert L.ozk_debug_force_gemm_kernel(b"fastest") == _lib.OZK_ERR_DTYPE
     assert L.ozk_debug_force_split_kernel(b"fastest") == _lib.OZK_ERR_DTYPE
-    for k in (b"staged", b"dma", b"ad", b"pair", b"ring", b"wide", b"", None):
+    for k in (b"staged", b"dma", b"ad", b"pair", b"ring", b"wide", b"wide4", b"", None):
         assert L.ozk_debug_force_gemm_kernel(k) == 0
     for k in (b"coop", b"strip", b"transpose", b"generic", b"rows", b"rowscoop", None):
         assert L.ozk_debug_force_split_kernel(k) == 0
@@ -474,7 +474,12 @@ def test_planner_kernel_choice():
     assert _gemm_kernel(L, 1, 640, 2560, 4096, 3, I8, 32) == "wide"
     assert _gemm_kernel(L, 1, 1024, 2304, 4096, 3, I8, 32) == "wide"
     # other slice counts
-    assert _gemm_kernel(L, 1, 8192, 8192, 8192, 4, I8, 256) == "ring"     # config 3
+    # num_splits 4: the 96 x 64 wide kernel where 1.45 x its rounds are fewer
+    # than the ring kernel's (29 * wide4 rounds < 20 * ring rounds)
+    assert _gemm_kernel(L, 1, 8192, 8192, 8192, 4, I8, 256) == "wide4"    # config 3: 43 vs 64
+    assert _gemm_kernel(L, 1, 4096, 4096, 8192, 4, I8, 256) == "wide4"    # 11 vs 16
+    assert _gemm_kernel(L, 1, 2048, 2048, 8192, 4, I8, 256) == "ring"     # 3 vs 4
+    assert _gemm_kernel(L, 1, 1024, 1024, 65536, 4, I8, 256) == "ring"    # 1 vs 1
     assert _gemm_kernel(L, 1, 4096, 4096, 4096, 2, _lib.OZK_F16, 256) == "ring"   # config 2
     assert _gemm_kernel(L, 1, 256, 256, 256, 2, _lib.OZK_F16, 256) == "dma"       # config 1
     assert _gemm_kernel(L, 1, 2048, 2048, 2048, 1, I8, 256) == "dma"

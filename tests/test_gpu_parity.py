@@ -294,14 +294,15 @@ def test_ozaki_matmul_degenerate_shapes(gpu):
                          torch.randn(0, 3, dtype=torch.float64, device=gpu), 2, torch.int8)
 
 
-@pytest.mark.parametrize("kernel", ["staged", "dma", "ad", "pair", "ring", "wide"])
+@pytest.mark.parametrize("kernel", ["staged", "dma", "ad", "pair", "ring", "wide", "wide4"])
 @pytest.mark.parametrize("L", [1, 2, 3, 4])
 def test_cross_gemm_each_kernel_bitexact(oracle, gpu, L, kernel, force):
     """Every cross-GEMM kernel, forced: the VGPR-staged one (taken when an
     operand's extent exceeds the 31-bit buffer offsets of the LDS-DMA kernels),
     the 2 x 2 LDS-DMA kernel, the A-direct kernel, the pair-split kernel, its
     five-slot ring form (L >= 3; for L <= 2 the request falls back to the
-    2 x 2 kernel) and the wide kernel (L = 3; otherwise the default kernel)."""
+    2 x 2 kernel), the wide kernel (L = 3) and the 96 x 64 wide kernel (L = 4;
+    otherwise the default kernel)."""
     import ozaki_triton_amd as ozk
     force(gemm=kernel)
     g = torch.Generator().manual_seed(77 + L)
@@ -317,7 +318,9 @@ def test_cross_gemm_each_kernel_bitexact(oracle, gpu, L, kernel, force):
 @pytest.mark.parametrize("kernel,L,M,N,K", [
     ("ring", 2, 256, 384, 4096),    # config 2's kernel: 128 x 128 tiles, K = 4096
     ("wide", 3, 128, 256, 2048),    # config 4's kernel: 64 x 128 tiles, K = 2048
-    ("ring", 4, 128, 192, 8192),    # config 3's kernel shape: 64 x 64 tiles, K = 8192
+    ("ring", 4, 128, 192, 8192),    # 64 x 64 tiles, K = 8192
+    ("wide4", 4, 192, 128, 8192),   # config 3's kernel: 96 x 64 tiles, K = 8192
+    ("wide4", 4, 100, 72, 1040),
     ("ring", 3, 130, 72, 4096),
     ("pair", 3, 100, 72, 1040),
     ("pair", 4, 100, 72, 1040),
@@ -390,6 +393,54 @@ def test_wide_kernel_stage_counts(oracle, gpu, K, MN, sdt, force):
         want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[b]), to_np(sa[b]), to_np(sb[b]),
                                  "float64")
         assert_bitwise_equal(C[b], want, f"wide {sdt} K{K} M{M} N{N} b{b}")
+
+
+@pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
+@pytest.mark.parametrize("MN", [(200, 130), (96, 64), (97, 65), (1, 300), (300, 1)])
+@pytest.mark.parametrize("K", [16, 128, 200, 300, 520, 1040, 2064])
+def test_wide4_kernel_stage_counts(oracle, gpu, K, MN, sdt, force):
+    """The num_splits 4 wide kernel (96 x 64 tiles; waves holding pairs
+    i = 0..2 of one 32 x 32 block or pairs i = 3 of three blocks, one partial
+    hand-off through the LDS; two whole stages of 80 KB) over 1 to 17 stages
+    of 128 bytes of K (prologue, the loop's two DMA parts, the last stage's
+    scale fetch), with M and N cutting tiles and batch 2: int8 and
+    integer-valued fp16 slices bit-exact against the oracle."""
+    import ozaki_triton_amd as ozk
+    L, (M, N) = 4, MN
+    g = torch.Generator().manual_seed(K * 10 + M + 3 * N)
+    As, BsT, sa, sb = _slices_for(g, 2, L, M, N, K, sdt)
+    args = (As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), L, torch.float64)
+    force(gemm="wide4")
+    C = to_np(ozk.cross_gemm(*args))
+    for b in range(2):
+        want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[b]), to_np(sa[b]), to_np(sb[b]),
+                                 "float64")
+        assert_bitwise_equal(C[b], want, f"wide4 {sdt} K{K} M{M} N{N} b{b}")
+
+
+@pytest.mark.parametrize("out", [torch.float64, torch.float32, torch.float16, torch.bfloat16,
+                                 torch.int8])
+@pytest.mark.parametrize("sdt", [torch.int8, torch.float16, torch.bfloat16, torch.float32])
+def test_wide4_kernel_dtypes(oracle, gpu, sdt, out, force):
+    """The num_splits 4 wide kernel for every slice and output dtype, batched,
+    with a broadcast (batch stride 0) B: int8 and integer-valued float slices
+    bit-exact against the oracle."""
+    import ozaki_triton_amd as ozk
+    L = 4
+    g = torch.Generator().manual_seed(ALL_SLICES.index(sdt) * 11 + len(str(out)) + 900)
+    M, N, K = 150, 100, 400
+    As, BsT, sa, sb = _slices_for(g, 2, L, M, N, K, sdt)
+    if out in (torch.float16, torch.bfloat16, torch.int8):
+        sa = sa * 2.0 ** (12 if sdt == torch.int8 else 0)
+    Bd = BsT[:1].to(gpu).expand(2, -1, -1, -1).transpose(-1, -2)   # broadcast B
+    sbd = sb[:1].to(gpu).expand(2, -1, -1)
+    args = (As.to(gpu), Bd, sa.to(gpu), sbd, L, out)
+    force(gemm="wide4")
+    C = to_np(ozk.cross_gemm(*args))
+    for b in range(2):
+        want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[0]), to_np(sa[b]), to_np(sb[0]),
+                                 NAME_OF[out])
+        assert_bitwise_equal(C[b], want, f"wide4 {sdt} {out} b{b}")
 
 
 @pytest.mark.parametrize("out", [torch.float64, torch.float32, torch.float16, torch.bfloat16,
@@ -824,7 +875,7 @@ def test_split_columns_default_plan(oracle, gpu, xdt, sdt, batch, N, K):
                  f"default {xdt} {sdt} b{batch} {N}x{K}")
 
 
-@pytest.mark.parametrize("kernel", ["", "dma", "ring", "pair", "ad", "staged", "wide"])
+@pytest.mark.parametrize("kernel", ["", "dma", "ring", "pair", "ad", "staged", "wide", "wide4"])
 @pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
 @pytest.mark.parametrize("K", [1, 2, 3, 5, 7, 9, 255, 257, 1003])
 def test_packed_rows_last_piece(oracle, gpu, kernel, sdt, K, force):
@@ -838,7 +889,7 @@ def test_packed_rows_last_piece(oracle, gpu, kernel, sdt, K, force):
     import ozaki_triton_amd as ozk
     if kernel:
         force(gemm=kernel)
-    L = 3 if kernel == "wide" else 4 if kernel in ("ring", "pair", "ad") else 2
+    L = 3 if kernel == "wide" else 4 if kernel in ("ring", "pair", "ad", "wide4") else 2
     A, B = c3_like((1, 33, K), (1, K, 20), seed=K + 100)
     C = ozk.ozaki_matmul(A.to(gpu), B.to(gpu), L, sdt)
     torch.cuda.synchronize()
