@@ -65,8 +65,8 @@ enum {
 
 /* The reference's ozaki_matmul asserts num_splits <= 4 (ozaki_triton.py:563),
  * a limit of its kernel's hard-coded accumulators.  The calls here take up to
- * 8 slices; with more than 4, the cross-GEMM needs int8 / fp16 / bf16 slices
- * and an fp64 C (OZK_ERR_SPLITS otherwise). */
+ * 8 slices; with more than 4, the cross-GEMM needs int8 / fp16 / bf16 slices,
+ * and with more than 5 an fp64 C (OZK_ERR_SPLITS otherwise). */
 #define OZK_MAX_SPLITS 8
 
 /* Name of a status code (static string). */

@@ -22,7 +22,7 @@ extern "C" {
 
 /*
  * Force the cross-GEMM kernel of later calls on this thread: one of "staged",
- * "dma", "ad", "pair", "ring", "wide", "wide4", or NULL / "" for the planner's
+ * "dma", "ad", "pair", "ring", "wide", "wide4", "solo5", or NULL / "" for the planner's
  * choice.  A kernel that cannot take a call (operand extents, slice count) is
  * not used for it.  Returns OZK_ERR_DTYPE for an unknown name.
  */
@@ -47,7 +47,7 @@ int ozk_debug_force_coop_timeout(int on);
 /*
  * The cross-GEMM kernel the planner would choose for K-contiguous,
  * 16-byte aligned slice operands of this shape, as a name ("dma", "ring",
- * "wide", "wide4", "pair", "staged", "ad") written to *name_out (a static
+ * "wide", "wide4", "solo5", "pair", "staged", "ad") written to *name_out (a static
  * string).  cus: compute units to plan for (0: those of the current device).
  */
 int ozk_debug_gemm_kernel(int64_t batch, int64_t M, int64_t N, int64_t K, int num_splits,

@@ -265,12 +265,16 @@ static int cross_gemm_impl(const void *A_slices, const int64_t a_strides[4], con
         p.bs_n = b_strides[3];
     }
     const ozk::GemmPlan plan = ozk::plan_gemm(p, num_splits, slice_dtype);
-    // more than 4 slices: int8 / fp16 / bf16 slices into an fp64 C (the
-    // partial sum stays in C between the i-row launches), operands within the
-    // 31-bit offsets of the LDS-DMA kernel
-    if (num_splits > 4 && (out_dtype != OZK_F64 || slice_dtype == OZK_F32 ||
-                           plan.kind != ozk::kGemmPair))
-        return OZK_ERR_SPLITS;
+    // more than 4 slices, operands within the 31-bit offsets of the LDS-DMA
+    // kernels: 5 int8 / fp16 / bf16 slices in one launch (any C dtype); 6 to
+    // 8 (or a forced pair-split kernel) into an fp64 C, which holds the
+    // partial sum between the i-row launches
+    if (num_splits > 4) {
+        const bool solo = plan.kind == ozk::kGemmSolo5;
+        const bool pair = plan.kind == ozk::kGemmPair && out_dtype == OZK_F64 &&
+                          slice_dtype != OZK_F32;
+        if (!solo && !pair) return OZK_ERR_SPLITS;
+    }
     return hip_status(ozk::launch_gemm(p, plan, num_splits, slice_dtype, st));
 }
 
@@ -322,8 +326,20 @@ int matmul_layout(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
         if (st != OZK_OK) return st;
     }
     if (L < 0 || L > OZK_MAX_SPLITS) return OZK_ERR_SPLITS;
-    // more than 4 slices: the cross-GEMM takes them into an fp64 C only
-    if (L > 4 && (dtype != OZK_F64 || sd == OZK_F32)) return OZK_ERR_SPLITS;
+    // more than 4 slices: 5 int8 / fp16 / bf16 slices into any C; 6 to 8 into
+    // an fp64 C only
+    if (L > 4 && (sd == OZK_F32 || (L > 5 && dtype != OZK_F64))) return OZK_ERR_SPLITS;
+    if (L > 4) {
+        // and a kernel that takes them (the LDS-DMA kernels' 31-bit operand
+        // extents), known before anything is enqueued
+        const int64_t es = slice_size(sd), kp = (K * es + 15) / 16 * 16 / es;
+        ozk::GemmParams gp{};
+        gp.as_l = M * kp; gp.as_m = kp; gp.bs_l = N * kp; gp.bs_n = kp;
+        gp.batch = batch; gp.M = M; gp.N = N; gp.K = K; gp.out_dtype = dtype;
+        const int kind = ozk::plan_gemm(gp, L, sd, 256).kind;
+        if (kind != ozk::kGemmSolo5 && !(kind == ozk::kGemmPair && dtype == OZK_F64))
+            return OZK_ERR_SPLITS;
+    }
     o->bA = (batch > 1 && as[0] != 0) ? batch : 1;
     o->bB = (batch > 1 && bs[0] != 0) ? batch : 1;
     o->bt_strides[0] = bs[0];
@@ -508,7 +524,7 @@ struct Named {
 const Named kGemmNames[] = {{"staged", ozk::kGemmStaged}, {"dma", ozk::kGemmDMA},
                             {"ad", ozk::kGemmAD},         {"pair", ozk::kGemmPair},
                             {"ring", ozk::kGemmRing},     {"wide", ozk::kGemmWide},
-                            {"wide4", ozk::kGemmWide4}};
+                            {"wide4", ozk::kGemmWide4},   {"solo5", ozk::kGemmSolo5}};
 const Named kSplitNames[] = {{"coop", ozk::kForceSplitCoop},
                              {"strip", ozk::kForceSplitStrip},
                              {"transpose", ozk::kForceSplitTranspose},

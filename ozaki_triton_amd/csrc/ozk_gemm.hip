@@ -1776,6 +1776,308 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide4_kernel(GemmParams p, 
 }
 
 // ---------------------------------------------------------------------------
+// num_splits 5: one wave per SIMD, each holding all 25 slice pairs of one
+// 32 x 32 block ("solo" kernel).  4 waves of 512 registers cover a 64 x 64
+// tile: wave (x, y) = (w / 2, w % 2) reads 5 A fragments (slice u, rows of
+// x) and 5 B fragments (slice j, columns of y) per 32-byte K step for 25
+// MFMAs (0.4 fragment reads per MFMA), and sums its own pairs in the
+// reference's i-major order: one launch, no hand-off, C written once.
+// The 25 accumulator tiles take 400 registers, more than either register
+// file holds (256 each), so each MFMA is written out with its accumulator
+// placed explicitly: tiles 0..15 in AGPRs, 16..24 in VGPRs (the compiler
+// does not split a kernel's MFMA accumulators between the two files by
+// itself).  The fragments are double-buffered: a K step's 10 reads are
+// issued one whole K step ahead.  A lone wave issues independent MFMAs at
+// 92-95% of the rate two waves reach (measured with 12 accumulators).
+// Hazards of the hand-placed MFMAs that the compiler cannot see: their
+// results are read by other instructions only in the epilogue, after 64 wait
+// states; an accumulator is first read as srcC after its zero fill and the
+// prologue's barrier; each one is accumulated again only 25 MFMAs later.
+// The LDS holds two whole stages of 128 bytes of K (2 x 80 KB); stage kb + 2
+// is fetched into stage kb's buffer after the barrier of stage kb, spread
+// over the two K steps that follow it.
+// ---------------------------------------------------------------------------
+struct Solo5Shape {
+    static constexpr int L = 5, BM = 64, BN = 64;
+    static constexpr int NW = 4;                         // waves
+    static constexpr int A_BYTES = L * BM * kDmaRB;      // 40 KB
+    static constexpr int B_BYTES = L * BN * kDmaRB;      // 40 KB
+    static constexpr int STAGE = A_BYTES + B_BYTES;
+    static constexpr int LA = A_BYTES / (NW * 1024);     // A instructions per wave per stage
+    static constexpr int LB = B_BYTES / (NW * 1024);
+    static constexpr int LPS = LA + LB;
+    static constexpr int P1 = LPS / 2;                   // issued in the K step after the barrier
+    static constexpr int LDS_BYTES = 2 * STAGE;
+    static constexpr int NSC = L * (BM + BN) / 64;       // scale instructions (64 entries each)
+    static constexpr int SCQ = (NSC + NW - 1) / NW;
+    static constexpr int NAGPR = 16;                     // accumulator tiles in AGPRs
+    static_assert(A_BYTES % (NW * 1024) == 0 && B_BYTES % (NW * 1024) == 0,
+                  "a half stage must be whole 1 KB windows per wave");
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS");
+    static_assert(kDmaRB == 128, "128-byte stage rows");
+};
+
+// one MFMA with its accumulator in AGPRs (AG) or VGPRs
+template <typename ST, bool AG> struct HandMfma;
+template <bool AG> struct HandMfma<int8_t, AG> {
+    OZK_DEV static void run(i32x16 &c, i32x4 a, i32x4 b) {
+        if constexpr (AG) asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+        else asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+    }
+};
+template <bool AG> struct HandMfma<_Float16, AG> {
+    OZK_DEV static void run(f32x16 &c, i32x4 a, i32x4 b) {
+        if constexpr (AG) asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+        else asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+    }
+};
+template <bool AG> struct HandMfma<__bf16, AG> {
+    OZK_DEV static void run(f32x16 &c, i32x4 a, i32x4 b) {
+        if constexpr (AG) asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+        else asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+    }
+};
+
+template <int N, typename F> OZK_DEV void static_for(F &&f) {
+    if constexpr (N > 0) {
+        static_for<N - 1>(f);
+        f(std::integral_constant<int, N - 1>{});
+    }
+}
+
+template <typename ST, typename AccT>
+__global__ __launch_bounds__(256, 1) void cross_gemm_solo5_kernel(GemmParams p, int group_m,
+                                                                  uint32_t a_records,
+                                                                  uint32_t b_records) {
+    using Sh = Solo5Shape;
+    using MF = Mfma<ST>;
+    using Acc = typename MF::Acc;
+    using OA = AccT;
+    constexpr int L = Sh::L, BM = Sh::BM, BN = Sh::BN;
+    constexpr int ES = (int)sizeof(ST);
+    constexpr uint32_t kOOB = 0x80000000u;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wx = wave >> 1, wy = wave & 1;
+    const int h = lane >> 5, lr = lane & 31;
+
+    const int64_t tiles_m = (p.M + BM - 1) / BM;
+    const int64_t tiles_n = (p.N + BN - 1) / BN;
+    const int64_t tiles = tiles_m * tiles_n;
+    const int64_t g = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
+    const int64_t bidx = g / tiles;
+    const int64_t t = g % tiles;
+    const int64_t width = (int64_t)group_m * tiles_n;
+    const int64_t first_m = (t / width) * group_m;
+    const int64_t gsz = (tiles_m - first_m < group_m) ? (tiles_m - first_m) : group_m;
+    const int64_t tm = first_m + (t % width) % gsz;
+    const int64_t tn = (t % width) / gsz;
+    const int64_t m0 = tm * BM, n0 = tn * BN;
+
+    const uint32_t kbytes = (uint32_t)(p.K * ES);
+    const int nkb = (int)((kbytes + kDmaRB - 1) / kDmaRB);
+
+    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const char *)p.A + bidx * p.as_b * ES), (short)0, (int)a_records, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const char *)p.B + bidx * p.bs_b * ES), (short)0, (int)b_records, 0x00020000);
+
+    // DMA: window wave * LA + q of the A half (q < LA), else wave * LB + q - LA
+    // of the B half; a 1 KB window is 8 whole 128-byte rows of one slice
+    // (lane -> row lane / 8, physical chunk lane % 8, holding logical chunk
+    // (lane % 8) ^ (lane / 16) ^ (4 in an odd window)).  The source offset is
+    // a uniform part, through readfirstlane at each use, plus one of four lane
+    // parts.
+    auto window = [&](int q) { return q < Sh::LA ? wave * Sh::LA + q : wave * Sh::LB + q - Sh::LA; };
+    const int lrow = lane >> 3;
+    const int c0 = (lane & 7) ^ (lane >> 4);
+    const uint32_t ch16[2] = {(uint32_t)c0 * 16, (uint32_t)(c0 ^ 4) * 16};
+    const uint32_t a_lp[2] = {(uint32_t)(lrow * p.as_m * ES) + ch16[0],
+                              (uint32_t)(lrow * p.as_m * ES) + ch16[1]};
+    const uint32_t b_lp[2] = {(uint32_t)(lrow * p.bs_n * ES) + ch16[0],
+                              (uint32_t)(lrow * p.bs_n * ES) + ch16[1]};
+    auto buf = [&](int kb) { return smem + (kb & 1) * Sh::STAGE; };
+    auto issue = [&](int kb, int q) {
+        const int w = window(q);
+        const int par = w & 1;
+        int64_t first, rows, ubase;
+        if (q < Sh::LA) {
+            first = m0 + (w % (BM / 8)) * 8;
+            rows = p.M;
+            ubase = ((int64_t)(w / (BM / 8)) * p.as_l + first * p.as_m) * ES;
+        } else {
+            first = n0 + (w % (BN / 8)) * 8;
+            rows = p.N;
+            ubase = ((int64_t)(w / (BN / 8)) * p.bs_l + first * p.bs_n) * ES;
+        }
+        const int rows_left = (int)(rows - first < 8 ? rows - first : 8);   // may be <= 0
+        const int kleft = (int)kbytes - kb * kDmaRB;                       // > 0
+        const uint32_t ub = (uint32_t)__builtin_amdgcn_readfirstlane((int)(ubase + kb * kDmaRB));
+        const bool ok = lrow < rows_left && (int)ch16[par] < kleft;
+        const uint32_t vo = ok ? (q < Sh::LA ? a_lp[par] : b_lp[par]) + ub : kOOB;
+        auto *ldsp = (__attribute__((address_space(3))) void *)(
+            buf(kb) + (q < Sh::LA ? 0 : Sh::A_BYTES) + w * 1024);
+        if (q < Sh::LA) __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, ldsp, 16, vo, 0, 0, 0);
+        else __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, ldsp, 16, vo, 0, 0, 0);
+    };
+
+    // The tile's scales (A's [L][BM], then B's [L][BN]: 2560 bytes) come by
+    // dword DMA into the buffer of stage nkb, which holds no stage the tile
+    // still reads, at the start of the last stage: instruction u (wave u % 4)
+    // fetches entries 64 u .. 64 u + 63.
+    char *const scl = buf(nkb);
+    auto issue_scales = [&]() {
+#pragma unroll
+        for (int q = 0; q < Sh::SCQ; ++q) {
+            const int u = q * Sh::NW + wave;
+            if (u >= Sh::NSC) break;
+            const bool isa = u < L * BM / 64;
+            const int e = (isa ? u : u - L * BM / 64) * 64 + lane;
+            const int s = isa ? e / BM : e / BN;                 // slice
+            const int64_t rc = isa ? m0 + e % BM : n0 + e % BN;  // row of A / column of B
+            const int64_t ext = isa ? ((int64_t)(L - 1) * p.sas_l + (p.M - 1) * p.sas_m + 1)
+                                    : ((int64_t)(L - 1) * p.sbs_l + (p.N - 1) * p.sbs_n + 1);
+            const bool ok = rc < (isa ? p.M : p.N);
+            const uint32_t vo = ok ? (uint32_t)(((int64_t)s * (isa ? p.sas_l : p.sbs_l) +
+                                                 rc * (isa ? p.sas_m : p.sbs_n)) * 4)
+                                   : kOOB;
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)(isa ? p.sa + bidx * p.sas_b : p.sb + bidx * p.sbs_b), (short)0,
+                (int)(ext * 4 < 0x7FFFFFFF ? ext * 4 : 0x7FFFFFFF), 0x00020000);
+            auto *ldsp = (__attribute__((address_space(3))) void *)(scl + u * 256);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, ldsp, 4, vo, 0, 0, 0);
+        }
+    };
+    const float *sa_lds = (const float *)scl, *sb_lds = (const float *)(scl + L * BM * 4);
+
+    Acc acc[L][L];
+#pragma unroll
+    for (int u = 0; u < L; ++u)
+#pragma unroll
+        for (int j = 0; j < L; ++j) acc[u][j] = MF::zero();
+
+    // prologue: stages 0 and 1; stage 0 must land before the first reads
+#pragma unroll
+    for (int q = 0; q < Sh::LPS; ++q) issue(0, q);
+    if (nkb > 1) {
+#pragma unroll
+        for (int q = 0; q < Sh::LPS; ++q) issue(1, q);
+        wait_vmcnt<Sh::LPS>();
+    } else {
+        wait_vmcnt<0>();
+    }
+    exec_barrier();
+
+    struct Frags {
+        i32x4 a[L];
+        i32x4 b[L];
+    };
+    // Fragment rows start at multiples of 32, so a lane's swizzle key is that
+    // of lr for every fragment: the address is a uniform row offset (through
+    // readfirstlane) plus one of four per-lane offsets, one per K step.
+    const int key = (lr >> 1) & 7;
+    int lane_rd[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) lane_rd[kk] = lr * kDmaRB + (((2 * kk + h) ^ key) << 4);
+    const int smem_base = (int)(uintptr_t)(__attribute__((address_space(3))) char *)smem;
+    auto lds_at = [&](int uniform, int kk) {
+        const int u = __builtin_amdgcn_readfirstlane(uniform);
+        return (const __attribute__((address_space(3))) i32x4 *)(uintptr_t)(u + lane_rd[kk]);
+    };
+    auto read_all = [&](int kb, int kk, Frags &f) {
+        const int base = smem_base + (kb & 1) * Sh::STAGE;
+#pragma unroll
+        for (int u = 0; u < L; ++u) f.a[u] = *lds_at(base + (u * BM + wx * 32) * kDmaRB, kk);
+#pragma unroll
+        for (int j = 0; j < L; ++j)
+            f.b[j] = *lds_at(base + Sh::A_BYTES + (j * BN + wy * 32) * kDmaRB, kk);
+    };
+    // One K step: all reads of the next K step (stage rkb, step nkk) into
+    // `nxt`, issued first, then the 25 MFMAs of `cur`, with, if `on`, DMA
+    // instructions [lo, hi) of stage dkb spread between them.
+    auto step = [&](const Frags &cur, Frags &nxt, int rkb, int nkk, int dkb, bool on, int lo,
+                    int hi) {
+        constexpr int NMF = L * L;
+        const int cnt = hi - lo;
+        read_all(rkb, nkk, nxt);
+        static_for<NMF>([&](auto n_) {
+            constexpr int n = decltype(n_)::value;
+            constexpr int u = n / L, j = n % L;
+            HandMfma<ST, (n < Sh::NAGPR)>::run(acc[u][j], cur.a[u], cur.b[j]);
+#pragma unroll
+            for (int d = 0; d < Sh::LPS; ++d) {
+                // instruction lo + d goes after MFMA (d * NMF) / cnt
+                if (d < cnt && (d * NMF) / cnt == n && on) issue(dkb, lo + d);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+
+    Frags f0, f1;
+    if (nkb > 0) read_all(0, 0, f0);
+    static_assert(kDmaRB / 32 == 4, "four 32-byte K steps per stage");
+    if (nkb == 0) issue_scales();
+    for (int kb = 0; kb < nkb; ++kb) {
+        const bool nb = kb + 1 < nkb, n2 = kb + 2 < nkb;
+        // no DMA is outstanding in the last stage: its waits are unaffected
+        if (!nb) issue_scales();
+        // the rest of stage kb + 1 (stage 1 went out whole in the prologue)
+        step(f0, f1, kb, 1, kb + 1, nb && kb >= 1, Sh::P1, Sh::LPS);
+        step(f1, f0, kb, 2, kb + 1, false, 0, 0);
+        step(f0, f1, kb, 3, kb + 1, false, 0, 0);
+        if (nb) {
+            // stage kb + 1 is the only DMA outstanding; the barrier publishes
+            // every wave's DMA writes, and the lgkmcnt wait makes this wave's
+            // reads of stage kb complete before its buffer is refilled
+            wait_vmcnt<0>();
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            exec_barrier();
+        }
+        // the last step reads stage kb + 1's step 0 (unused past the end)
+        step(f1, f0, kb + 1, 0, kb + 2, n2, 0, Sh::P1);
+    }
+    // the hand-placed MFMAs' results are read below: 64 wait states first
+    asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory");
+
+    // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
+    wait_vmcnt<0>();
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    exec_barrier();
+    const int ct = wy * 32 + lr;
+    const int64_t col = n0 + ct;
+    const int64_t cbase = bidx * p.cs_b;
+    float sbv[L];
+#pragma unroll
+    for (int j = 0; j < L; ++j) sbv[j] = sb_lds[j * BN + ct];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        // scales of accumulator registers 4 q .. 4 q + 3: one 16-byte read per slice
+        f32x4 s4[L];
+#pragma unroll
+        for (int i = 0; i < L; ++i) s4[i] = *(const f32x4 *)(sa_lds + i * BM + wx * 32 + 8 * q + 4 * h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int r = 4 * q + e;
+            const int64_t row = m0 + wx * 32 + 8 * q + 4 * h + e;
+            OA out = (OA)0;
+#pragma unroll
+            for (int i = 0; i < L; ++i)
+#pragma unroll
+                for (int j = 0; j < L; ++j) {
+                    // fl32(fl32(fl32(acc) * sa_i) * sb_j), summed i-major, j-minor
+                    const float t1 = MF::to_f32(acc[i][j][r]) * s4[i][e];
+                    out = out + (OA)(t1 * sbv[j]);
+                }
+            if (col < p.N && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // A-direct variant.  The four waves are stacked along M (workgroup tile
 // 128 x 32*NI); each wave streams ITS OWN 32 rows of every A slice from global
 // memory straight into VGPRs (no LDS), and only B, which all four waves share,
@@ -2097,8 +2399,9 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
     // 31-bit buffer offsets of the LDS-DMA kernels: for L = 3 the wide kernel
     // where it finishes its grid sooner (below), the ring kernel for L = 3, 4
     // (64 x 64 tiles) and for L = 2 on grids of 256 or more 128 x 128 tiles,
-    // the pair-split kernel for L > 4, the 2 x 2 LDS-DMA kernel with its larger
-    // wave tiles otherwise; else the VGPR-staged kernel.
+    // the pair-split kernel for L > 5, the 2 x 2 LDS-DMA kernel with its larger
+    // wave tiles otherwise; for L = 5 the one-wave-per-SIMD kernel; else the
+    // VGPR-staged kernel.
     const bool fits = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es) >= 0 &&
                       dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es) >= 0;
     // Both L = 3 kernels run one workgroup per CU (144 KB of LDS each), so a
@@ -2120,16 +2423,25 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
     // 8192 3 / 4, 0.99x; 1024^2 x 65536 1 / 1, 1.10x)
     const int64_t wide4_rounds = (p.batch * ((p.M + 95) / 96) * ((p.N + 63) / 64) + kCUs - 1) / kCUs;
     const bool wide4 = L == 4 && 29 * wide4_rounds < 20 * ring_rounds;
+    // L = 5: the one-wave-per-SIMD kernel (one launch; int8 / fp16 / bf16
+    // slices); L = 6..8 and fp32 slices: the pair-split kernel per i-row range
+    const bool solo5 = L == 5 && slice_dtype != 1;
     plan.kind = !fits              ? kGemmStaged
                 : L <= 1           ? kGemmDMA
                 : L == 2           ? ((mi == 2 && ni == 2) ? kGemmRing : kGemmDMA)
                 : wide3            ? kGemmWide
                 : wide4            ? kGemmWide4
                 : L <= 4           ? kGemmRing
+                : solo5            ? kGemmSolo5
                                    : kGemmPair;
-    if (L > 4) return plan;   // only the pair-split kernel, launched per i-row range
     const int force = debug_overrides().gemm;
     auto forced = [&](int kind) { return force == kind; };
+    if (L > 4) {
+        // the pair-split kernel keeps its partial sums in an fp64 C
+        if (fits && forced(kGemmPair) && p.out_dtype == 0 && slice_dtype != 1)
+            plan.kind = kGemmPair;
+        return plan;
+    }
     if (forced(kGemmStaged)) plan.kind = kGemmStaged;
     else if (fits && forced(kGemmAD)) plan.kind = kGemmAD;
     else if (fits && forced(kGemmDMA)) plan.kind = kGemmDMA;
@@ -2138,6 +2450,9 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
     else if (fits && forced(kGemmWide)) plan.kind = L == 3 ? kGemmWide : plan.kind;
     else if (fits && forced(kGemmWide4)) plan.kind = L == 4 ? kGemmWide4 : plan.kind;
     if (plan.kind == kGemmAD) plan.group_m = 2;
+    // 96 x 64 tiles: groups of 4 tile rows (C3: 7.12-7.16 ms against 7.21-7.23
+    // with 8, 7.33-7.35 with 16; cross-GEMM alone, one box)
+    if (plan.kind == kGemmWide4) plan.group_m = 4;
     return plan;
 }
 
@@ -2267,6 +2582,26 @@ static hipError_t launch_wide4(const GemmParams &p, const GemmPlan &plan, hipStr
     return hipGetLastError();
 }
 
+template <typename ST, typename AccT>
+static hipError_t launch_solo5(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
+    if constexpr (std::is_same<ST, float>::value) {
+        return hipErrorInvalidValue;   // no fp32-slice form
+    } else {
+        using Sh = Solo5Shape;
+        auto kern = cross_gemm_solo5_kernel<ST, AccT>;
+        static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
+        if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
+        const int es = (int)sizeof(ST);
+        const int64_t ea = dma_extent(p.as_l, p.as_m, Sh::L, p.M, p.K, es);
+        const int64_t eb = dma_extent(p.bs_l, p.bs_n, Sh::L, p.N, p.K, es);
+        const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
+        if (tiles == 0) return hipSuccess;
+        hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(256), Sh::LDS_BYTES, st, p,
+                           plan.group_m, (uint32_t)ea, (uint32_t)eb);
+        return hipGetLastError();
+    }
+}
+
 // num_splits = 5..8: launches over consecutive i-rows (at most 16 pairs each,
 // so a wave group still holds 8 pairs), in i-major order, each continuing the
 // fp64 sum from C.  int8 / fp16 / bf16 slices with an fp64 outer accumulator.
@@ -2335,6 +2670,9 @@ static hipError_t launch_L(const GemmParams &p, const GemmPlan &plan, hipStream_
     } else if constexpr (L <= 4) {
         if (key == 11) return launch_one<ST, L, 1, 1, AccT>(p, plan, st);
     } else {
+        if constexpr (L == 5) {
+            if (plan.kind == kGemmSolo5) return launch_solo5<ST, AccT>(p, plan, st);
+        }
         return launch_chunks<ST, L, AccT>(p, plan, st);
     }
     return hipErrorInvalidValue;

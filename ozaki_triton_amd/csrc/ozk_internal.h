@@ -108,8 +108,10 @@ enum GemmKind {
                       // between the MFMAs (num_splits 3 and 4)
     kGemmWide = 5,    // num_splits 3: 64 x 128 tiles, 8 waves each holding all 9 pairs
                       // of a 32 x 32 block, two whole stages in the LDS
-    kGemmWide4 = 6    // num_splits 4: 96 x 64 tiles, 8 waves of 12 accumulator tiles
+    kGemmWide4 = 6,   // num_splits 4: 96 x 64 tiles, 8 waves of 12 accumulator tiles
                       // (3 A x 4 B fragments), two whole stages in the LDS
+    kGemmSolo5 = 7    // num_splits 5: 64 x 64 tiles, 4 waves (one per SIMD) each holding
+                      // all 25 pairs of a 32 x 32 block, two whole stages in the LDS
 };
 struct GemmPlan {
     int mi, ni;       // 2 x 2 kernels: wave tile = (32*mi) x (32*ni)

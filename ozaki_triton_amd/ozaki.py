@@ -317,9 +317,19 @@ def ozaki_matmul(
     num_splits: int = 3,
     slice_dtype: torch.dtype = torch.float16,
     verbose: bool = False,
+    *,
+    max_splits: int = 4,
 ) -> torch.Tensor:
-    """Ozaki-scheme C = A @ B (ozaki_triton.py:534-606); see _ozaki_matmul_impl."""
-    return _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, None)
+    """Ozaki-scheme C = A @ B (ozaki_triton.py:534-606); see _ozaki_matmul_impl.
+
+    ``max_splits`` (keyword only, not in the reference) raises the reference's
+    limit of 4 slices (ozaki_triton.py:563) up to OZK_MAX_SPLITS (8): fp64
+    accuracy needs 5 or more int8 slices.  5 int8 / fp16 / bf16 slices run in
+    one cross-GEMM launch for any input dtype; 6 to 8 need fp64 inputs.
+    """
+    if max_splits > _lib.OZK_MAX_SPLITS:
+        raise ValueError(f"max_splits must be <= {_lib.OZK_MAX_SPLITS}, got {max_splits}")
+    return _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, None, max_splits)
 
 
 def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, events, max_splits=4):
@@ -334,7 +344,7 @@ def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, events, max_split
     Args:
         A: (..., M, K) on a ROCm GPU, any of the reference's input dtypes
         B: (..., K, N), same dtype as A
-        num_splits: number of slices (<= 4)
+        num_splits: number of slices (<= max_splits)
         slice_dtype: torch.int8, torch.float16, torch.bfloat16 or torch.float32
         verbose: print the chosen parameters
 
@@ -345,9 +355,8 @@ def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, events, max_split
     one workspace holding the slices and scales.  ``events`` (internal, used by
     bench.py) is None or four torch.cuda.Event objects that the call records
     before the B split, before the A split, before the cross-GEMM and after it.
-    ``max_splits`` (internal) is the reference's limit of 4 (ozaki_triton.py:563)
-    for the public function; bench.py raises it to the C ABI's OZK_MAX_SPLITS (8)
-    to time more slices.
+    ``max_splits`` is the reference's limit of 4 (ozaki_triton.py:563) unless
+    the caller raises it, up to the C ABI's OZK_MAX_SPLITS (8).
     """
     assert A.dtype == B.dtype, f"A/B dtype mismatch: {A.dtype} vs {B.dtype}"
     assert A.dtype in _INPUT_DTYPES, f"unsupported input dtype: {A.dtype}"

@@ -198,9 +198,10 @@ def test_cross_gemm_abi_checks_and_workspace():
     assert call(sd=_lib.OZK_F64) == _lib.OZK_ERR_DTYPE
     assert call(od=_lib.OZK_I32) == _lib.OZK_ERR_DTYPE
     assert call(L=9) == _lib.OZK_ERR_SPLITS
-    # more than 4 slices: only int8 / fp16 / bf16 slices into an fp64 C
-    assert call(L=5, od=_lib.OZK_F32) == _lib.OZK_ERR_SPLITS
+    # more than 4 slices: int8 / fp16 / bf16 slices only, and beyond 5 an fp64 C
+    assert call(L=6, od=_lib.OZK_F32) == _lib.OZK_ERR_SPLITS
     assert call(L=5, sd=_lib.OZK_F32) == _lib.OZK_ERR_SPLITS
+    assert call(L=5, od=_lib.OZK_F32, B=0) == _lib.OZK_OK
     assert call(K=-3) == _lib.OZK_ERR_SHAPE
     assert call(C=null) == _lib.OZK_ERR_NULL
     assert call(b=b_ncontig) == _lib.OZK_ERR_WORKSPACE
@@ -223,6 +224,11 @@ def test_ozaki_matmul_assertions():
         ozk.ozaki_matmul(a64, a64.T, slice_dtype=torch.float64)
     with pytest.raises(AssertionError, match="num_splits must be <= 4, got 5"):
         ozk.ozaki_matmul(a64, a64.T, num_splits=5)
+    # the keyword-only max_splits raises the limit up to OZK_MAX_SPLITS (8)
+    with pytest.raises(AssertionError, match="num_splits must be <= 5, got 6"):
+        ozk.ozaki_matmul(a64, a64.T, num_splits=6, max_splits=5)
+    with pytest.raises(ValueError, match="max_splits must be <= 8"):
+        ozk.ozaki_matmul(a64, a64.T, num_splits=5, max_splits=9)
     with pytest.raises(AssertionError, match="contraction dim mismatch: A K=8, B K=4"):
         ozk.ozaki_matmul(a64, a64)
     # a 1-D operand fails unpacking A.shape[-2:] before any assert, as in the
@@ -312,13 +318,25 @@ def test_matmul_abi_layout_and_errors():
                                         ctypes.byref(nb)) == _lib.OZK_ERR_SHAPE
     assert L.ozk_matmul_workspace_bytes(_lib.OZK_F64, 1, 4, 4, 8, a, b, 9, _lib.OZK_F16,
                                         ctypes.byref(nb)) == _lib.OZK_ERR_SPLITS
-    # 5..8 slices: fp64 in and out, int8 / fp16 / bf16 slices
+    # 5 slices: int8 / fp16 / bf16 slices, any input; 6..8: fp64 in and out
     assert L.ozk_matmul_workspace_bytes(_lib.OZK_F32, 1, 4, 4, 8, a, b, 5, _lib.OZK_F16,
+                                        ctypes.byref(nb)) == _lib.OZK_OK
+    assert L.ozk_matmul_workspace_bytes(_lib.OZK_F32, 1, 4, 4, 8, a, b, 5, _lib.OZK_F32,
+                                        ctypes.byref(nb)) == _lib.OZK_ERR_SPLITS
+    assert L.ozk_matmul_workspace_bytes(_lib.OZK_F32, 1, 4, 4, 8, a, b, 6, _lib.OZK_F16,
                                         ctypes.byref(nb)) == _lib.OZK_ERR_SPLITS
     assert L.ozk_matmul_workspace_bytes(_lib.OZK_F64, 1, 4, 4, 8, a, b, 6, _lib.OZK_F32,
                                         ctypes.byref(nb)) == _lib.OZK_ERR_SPLITS
     assert L.ozk_matmul_workspace_bytes(_lib.OZK_F64, 1, 4, 4, 8, a, b, 6, _lib.OZK_I8,
                                         ctypes.byref(nb)) == _lib.OZK_OK
+    # ... and slices within the 31-bit extents of the kernels that take them
+    # (5 x 32768 x 32768 int8 slices of A are 5 GiB), refused before any launch
+    big = _lib.i64arr([32768 * 32768, 32768, 1])
+    for dt in (_lib.OZK_F64, _lib.OZK_F32):
+        assert L.ozk_matmul_workspace_bytes(dt, 1, 32768, 64, 32768, big, b, 5, _lib.OZK_I8,
+                                            ctypes.byref(nb)) == _lib.OZK_ERR_SPLITS
+        assert L.ozk_matmul_workspace_bytes(dt, 1, 8192, 64, 32768, big, b, 5, _lib.OZK_I8,
+                                            ctypes.byref(nb)) == _lib.OZK_OK
     assert L.ozk_matmul_workspace_bytes(_lib.OZK_I32, 1, 4, 4, 8, a, b, 2, _lib.OZK_F16,
                                         ctypes.byref(nb)) == _lib.OZK_ERR_DTYPE
     p = ctypes.c_void_p(0x1000)
@@ -442,7 +460,8 @@ def test_debug_hooks_reject_unknown_names():
     L = _lib.load()
     assert L.ozk_debug_force_gemm_kernel(b"fastest") == _lib.OZK_ERR_DTYPE
     assert L.ozk_debug_force_split_kernel(b"fastest") == _lib.OZK_ERR_DTYPE
-    for k in (b"staged", b"dma", b"ad", b"pair", b"ring", b"wide", b"wide4", b"", None):
+    for k in (b"staged", b"dma", b"ad", b"pair", b"ring", b"wide", b"wide4", b"solo5", b"",
+              None):
         assert L.ozk_debug_force_gemm_kernel(k) == 0
     for k in (b"coop", b"strip", b"transpose", b"generic", b"rows", b"rowscoop", None):
         assert L.ozk_debug_force_split_kernel(k) == 0
@@ -483,4 +502,10 @@ def test_planner_kernel_choice():
     assert _gemm_kernel(L, 1, 4096, 4096, 4096, 2, _lib.OZK_F16, 256) == "ring"   # config 2
     assert _gemm_kernel(L, 1, 256, 256, 256, 2, _lib.OZK_F16, 256) == "dma"       # config 1
     assert _gemm_kernel(L, 1, 2048, 2048, 2048, 1, I8, 256) == "dma"
-    assert _gemm_kernel(L, 1, 1024, 1024, 1024, 5, I8, 256) == "pair"
+    # num_splits 5: the one-wave-per-SIMD kernel, in one launch, for int8 /
+    # fp16 / bf16 slices; fp32 slices and 6 to 8 slices: the pair-split kernel
+    assert _gemm_kernel(L, 1, 1024, 1024, 1024, 5, I8, 256) == "solo5"
+    assert _gemm_kernel(L, 1, 8192, 8192, 8192, 5, I8, 256) == "solo5"
+    assert _gemm_kernel(L, 1, 4096, 4096, 4096, 5, _lib.OZK_BF16, 256) == "solo5"
+    assert _gemm_kernel(L, 1, 1024, 1024, 1024, 5, _lib.OZK_F32, 256) == "pair"
+    assert _gemm_kernel(L, 1, 1024, 1024, 1024, 6, I8, 256) == "pair"

@@ -162,6 +162,18 @@ def _random_slices(g, B, L, M, N, K, sdt):
     return As, BsT, sa, sb
 
 
+def _planned(batch, M, N, K, L, sdt):
+    """The cross-GEMM kernel the planner picks for K-contiguous slices on this
+    device (ozk_debug_gemm_kernel)."""
+    import ctypes
+    from ozaki_triton_amd import _lib
+    from ozaki_triton_amd.ozaki import _TORCH_TO_OZK
+    name = ctypes.c_char_p()
+    _lib.check("ozk_debug_gemm_kernel", _lib.load().ozk_debug_gemm_kernel(
+        batch, M, N, K, L, _TORCH_TO_OZK[sdt], 0, ctypes.byref(name)))
+    return name.value.decode()
+
+
 def _slices_for(g, B, L, M, N, K, sdt):
     """int8: random slices; float dtypes: integer-valued ones, for which the
     fp32-accumulated kernels are exact and must match the oracle bit for bit."""
@@ -441,6 +453,78 @@ def test_wide4_kernel_dtypes(oracle, gpu, sdt, out, force):
         want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[0]), to_np(sa[b]), to_np(sb[0]),
                                  NAME_OF[out])
         assert_bitwise_equal(C[b], want, f"wide4 {sdt} {out} b{b}")
+
+
+@pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
+@pytest.mark.parametrize("MN", [(130, 200), (64, 64), (65, 63), (1, 300), (300, 1)])
+@pytest.mark.parametrize("K", [16, 128, 200, 300, 520, 1040, 2064])
+def test_solo5_kernel_stage_counts(oracle, gpu, K, MN, sdt):
+    """The num_splits 5 kernel (64 x 64 tiles, one wave per SIMD holding all 25
+    pairs of its 32 x 32 block, 16 accumulator tiles in AGPRs and 9 in VGPRs,
+    two whole stages of 80 KB) over 1 to 17 stages of 128 bytes of K
+    (prologue, the loop's two DMA parts, the last stage's scale fetch), with M
+    and N cutting tiles and batch 2, chosen by the planner: int8 and
+    integer-valued fp16 slices bit-exact against the oracle."""
+    import ozaki_triton_amd as ozk
+    L, (M, N) = 5, MN
+    assert _planned(1, M, N, K, L, sdt) == "solo5"
+    g = torch.Generator().manual_seed(K * 10 + 7 * M + N)
+    As, BsT, sa, sb = _slices_for(g, 2, L, M, N, K, sdt)
+    args = (As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), L, torch.float64)
+    C = to_np(ozk.cross_gemm(*args))
+    for b in range(2):
+        want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[b]), to_np(sa[b]), to_np(sb[b]),
+                                 "float64")
+        assert_bitwise_equal(C[b], want, f"solo5 {sdt} K{K} M{M} N{N} b{b}")
+
+
+@pytest.mark.parametrize("out", [torch.float64, torch.float32, torch.float16, torch.bfloat16,
+                                 torch.int8])
+@pytest.mark.parametrize("sdt", [torch.int8, torch.float16, torch.bfloat16])
+def test_solo5_kernel_dtypes(oracle, gpu, sdt, out):
+    """The num_splits 5 kernel for every slice dtype it takes and every output
+    dtype (an fp32 outer accumulator for all but fp64), batched, with a
+    broadcast (batch stride 0) B: int8 and integer-valued float slices
+    bit-exact against the oracle."""
+    import ozaki_triton_amd as ozk
+    L = 5
+    g = torch.Generator().manual_seed(ALL_SLICES.index(sdt) * 13 + len(str(out)) + 1900)
+    M, N, K = 150, 100, 400
+    As, BsT, sa, sb = _slices_for(g, 2, L, M, N, K, sdt)
+    if out in (torch.float16, torch.bfloat16, torch.int8):
+        sa = sa * 2.0 ** (12 if sdt == torch.int8 else 0)
+    Bd = BsT[:1].to(gpu).expand(2, -1, -1, -1).transpose(-1, -2)   # broadcast B
+    sbd = sb[:1].to(gpu).expand(2, -1, -1)
+    C = to_np(ozk.cross_gemm(As.to(gpu), Bd, sa.to(gpu), sbd, L, out))
+    for b in range(2):
+        want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[0]), to_np(sa[b]), to_np(sb[0]),
+                                 NAME_OF[out])
+        assert_bitwise_equal(C[b], want, f"solo5 {sdt} {out} b{b}")
+
+
+@pytest.mark.parametrize("xdt,sdt", [(torch.float64, torch.int8), (torch.float32, torch.int8),
+                                     (torch.float64, torch.bfloat16)])
+def test_ozaki_matmul_five_splits(oracle, gpu, xdt, sdt):
+    """The public ozaki_matmul with max_splits raised to 5 (the reference stops
+    at 4, ozaki_triton.py:563): splits and the one-launch num_splits 5
+    cross-GEMM, bit-exact against the oracle (int8 slices) or within the fp32
+    accumulation bound (bf16 slices); for fp64 inputs with int8 slices the
+    result is closer to the exact product than with 4 slices."""
+    import ozaki_triton_amd as ozk
+    A, B = c3_like((2, 96, 1040), (1040, 80), seed=555, dtype=xdt)
+    Ad, Bd = A.to(gpu), B.to(gpu)
+    C5 = ozk.ozaki_matmul(Ad, Bd, 5, sdt, max_splits=5)
+    torch.cuda.synchronize()
+    C_np, A_np, B_np = to_np(C5), to_np(A), to_np(B)
+    rows, cols = np.arange(96), np.arange(80)
+    for b in range(2):
+        check_block_vs_oracle(oracle, ozk, C_np[b], A_np[b], B_np, rows, cols, 5, sdt, xdt,
+                              f"L5 {xdt} {sdt} b{b}")
+    if xdt == torch.float64 and sdt == torch.int8:
+        C4 = ozk.ozaki_matmul(Ad, Bd, 4, sdt)
+        ref = A @ B
+        rel = lambda C: float((C.cpu() - ref).norm() / ref.norm())
+        assert rel(C5) < rel(C4)
 
 
 @pytest.mark.parametrize("out", [torch.float64, torch.float32, torch.float16, torch.bfloat16,
@@ -766,10 +850,16 @@ def test_ozaki_matmul_graph_capture(oracle, gpu, sdt, sa, sb):
 # caps only ozaki_matmul, ozaki_triton.py:563); the cross-GEMM runs over i-row
 # ranges that continue the fp64 sum from C
 # --------------------------------------------------------------------------- #
+@pytest.mark.parametrize("kernel", ["", "pair"])
 @pytest.mark.parametrize("L", [5, 6, 7, 8])
 @pytest.mark.parametrize("M,N,K", [(64, 64, 128), (100, 72, 1040)])
-def test_cross_gemm_more_splits_int8_bitexact(oracle, gpu, L, M, N, K):
+def test_cross_gemm_more_splits_int8_bitexact(oracle, gpu, L, M, N, K, kernel, force):
+    """5 to 8 slices, the planner's kernel (one launch for 5) and the
+    pair-split kernel forced (launched per i-row range, the fp64 sum carried
+    in C)."""
     import ozaki_triton_amd as ozk
+    if kernel:
+        force(gemm=kernel)
     g = torch.Generator().manual_seed(L * 100 + M)
     As, BsT, sa, sb = _random_slices(g, 2, L, M, N, K, torch.int8)
     C = ozk.cross_gemm(As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), L,
@@ -781,12 +871,15 @@ def test_cross_gemm_more_splits_int8_bitexact(oracle, gpu, L, M, N, K):
         assert_bitwise_equal(to_np(C)[b], want, f"L{L} {M}x{N}x{K} b{b}")
 
 
+@pytest.mark.parametrize("kernel", ["", "pair"])
 @pytest.mark.parametrize("sdt", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("L", [5, 6])
-def test_cross_gemm_more_splits_float_bitexact(oracle, gpu, sdt, L):
-    """5 and 6 float slices on integer-valued slices: bit-exact against the
-    oracle."""
+def test_cross_gemm_more_splits_float_bitexact(oracle, gpu, sdt, L, kernel, force):
+    """5 and 6 float slices on integer-valued slices, the planner's kernel and
+    the pair-split kernel forced: bit-exact against the oracle."""
     import ozaki_triton_amd as ozk
+    if kernel:
+        force(gemm=kernel)
     g = torch.Generator().manual_seed(L + 17)
     M, N, K = 100, 72, 1040
     As, BsT, sa, sb = int_valued_slices(g, 1, L, M, N, K, sdt)
@@ -820,12 +913,18 @@ def test_six_splits_end_to_end(oracle, gpu):
 
 
 def test_more_splits_unsupported_combination_raises(gpu):
+    """6 to 8 slices need an fp64 C (the pair-split kernel carries its partial
+    sums there); 5 fp32 slices have no kernel but the pair-split one."""
     import ozaki_triton_amd as ozk
     g = torch.Generator().manual_seed(3)
-    As, BsT, sa, sb = _random_slices(g, 1, 5, 64, 64, 128, torch.int8)
+    As, BsT, sa, sb = _random_slices(g, 1, 6, 64, 64, 128, torch.int8)
     with pytest.raises(ozk._lib.OzakiLibError):
-        ozk.cross_gemm(As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), 5,
+        ozk.cross_gemm(As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), 6,
                        torch.float32)
+    As32, Bs32 = As[:, :5].float(), BsT[:, :5].float()
+    with pytest.raises(ozk._lib.OzakiLibError):
+        ozk.cross_gemm(As32.to(gpu), Bs32.to(gpu).transpose(-1, -2), sa[:, :5].to(gpu),
+                       sb[:, :5].to(gpu), 5, torch.float32)
 
 
 @pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
@@ -875,7 +974,8 @@ def test_split_columns_default_plan(oracle, gpu, xdt, sdt, batch, N, K):
                  f"default {xdt} {sdt} b{batch} {N}x{K}")
 
 
-@pytest.mark.parametrize("kernel", ["", "dma", "ring", "pair", "ad", "staged", "wide", "wide4"])
+@pytest.mark.parametrize("kernel", ["", "dma", "ring", "pair", "ad", "staged", "wide", "wide4",
+                                    "solo5"])
 @pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
 @pytest.mark.parametrize("K", [1, 2, 3, 5, 7, 9, 255, 257, 1003])
 def test_packed_rows_last_piece(oracle, gpu, kernel, sdt, K, force):
@@ -889,9 +989,10 @@ def test_packed_rows_last_piece(oracle, gpu, kernel, sdt, K, force):
     import ozaki_triton_amd as ozk
     if kernel:
         force(gemm=kernel)
-    L = 3 if kernel == "wide" else 4 if kernel in ("ring", "pair", "ad", "wide4") else 2
+    L = (3 if kernel == "wide" else 4 if kernel in ("ring", "pair", "ad", "wide4")
+         else 5 if kernel == "solo5" else 2)
     A, B = c3_like((1, 33, K), (1, K, 20), seed=K + 100)
-    C = ozk.ozaki_matmul(A.to(gpu), B.to(gpu), L, sdt)
+    C = ozk.ozaki_matmul(A.to(gpu), B.to(gpu), L, sdt, max_splits=L)
     torch.cuda.synchronize()
     rows, cols = np.arange(33), np.arange(20)
     check_block_vs_oracle(oracle, ozk, to_np(C)[0], to_np(A)[0], to_np(B)[0], rows, cols, L, sdt,
