@@ -290,6 +290,39 @@ def vendor_probes():
     ms = time_ms(lambda: torch._int_mm(a, b.t()), 5)
     out["int_mm_8192_ms"] = round(ms, 4)
     out["int_mm_TOPs"] = round(2.0 * m ** 3 / (ms * 1e-3) / 1e12, 1)
+    # the same GEMM on zero operands: same instructions, same memory traffic,
+    # no operand bits toggling in the multipliers
+    z = torch.zeros_like(a)
+    ms = time_ms(lambda: torch._int_mm(z, z.t()), 5)
+    out["int_mm_zeros_TOPs"] = round(2.0 * m ** 3 / (ms * 1e-3) / 1e12, 1)
+    del a, b, z
+    # the library's cross-GEMM at C3's size (num_splits 4 and 5, the planner's
+    # kernel) on three kinds of int8 slices: those of C3's inputs, uniform
+    # random ones and zeros.  A kernel limited by its own schedule runs all
+    # three at one rate; a rate that rises as fewer operand bits toggle is set
+    # by the chip's power limit (the clock), not by the kernel.
+    import ozaki_triton_amd as ozk
+    A, B = make_inputs(CONFIGS["C3"])
+    A, B = A.to(dev), B.to(dev)
+    K = A.shape[-1]
+    alpha = ozk.compute_split_bits(K, torch.int8, torch.int32)
+    for L in (4, 5):
+        a_sl, a_sc = ozk.split_matrix(A.unsqueeze(0), L, alpha, torch.int8)
+        b_sl, b_sc = ozk.split_matrix(B.t().unsqueeze(0), L, alpha, torch.int8)
+        kinds = {"c3_slices": (a_sl, b_sl),
+                 "uniform_random": (torch.randint(-128, 128, a_sl.shape, dtype=torch.int8,
+                                                  device=dev, generator=g),
+                                    torch.randint(-128, 128, b_sl.shape, dtype=torch.int8,
+                                                  device=dev, generator=g)),
+                 "zeros": (torch.zeros_like(a_sl), torch.zeros_like(b_sl))}
+        res = {"kernel": planned_gemm_kernel(1, m, m, K, L, "int8")}
+        for name, (xa, xb) in kinds.items():
+            ms = time_ms(lambda: ozk.cross_gemm(xa, xb.transpose(-1, -2), a_sc, b_sc, L,
+                                                torch.float64), 5)
+            res[name + "_ms"] = round(ms, 4)
+            res[name + "_TOPs"] = round(2.0 * m * m * K * L * L / (ms * 1e-3) / 1e12, 1)
+        out[f"cross_gemm_L{L}"] = res
+        del a_sl, b_sl, kinds
     print(json.dumps(out), flush=True)
 
 
@@ -319,9 +352,10 @@ def main():
                     help="only run a plain device copy of this many MiB (3 times): the "
                          "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--vendor-probes", action="store_true",
-                    help="only time two vendor kernels that calibrate the rooflines: torch's "
-                         "device copy of 1 GiB (practical HBM rate) and torch._int_mm "
-                         "(hipBLASLt int8 GEMM) at 8192^3")
+                    help="only time the calibration probes of the rooflines: torch's device "
+                         "copy of 1 GiB (practical HBM rate), torch._int_mm (hipBLASLt int8 "
+                         "GEMM) at 8192^3 on random and zero operands, and the library's "
+                         "cross-GEMM at C3's size on C3's, random and zero slices")
     ap.add_argument("--reference-shapes", action="store_true",
                     help="only time ozaki_matmul at the reference's published points "
                          "(test_results.csv: 4 shapes x 4 dtype scenarios x num_splits 1-4)")
