@@ -207,7 +207,8 @@ def planned_gemm_kernel(batch, M, N, K, L, sdt):
     name = ctypes.c_char_p()
     code = {"int8": _lib.OZK_I8, "float16": _lib.OZK_F16}[sdt]
     _lib.check("ozk_debug_gemm_kernel",
-               _lib.load().ozk_debug_gemm_kernel(batch, M, N, K, L, code, 0, ctypes.byref(name)))
+               _lib.load().ozk_debug_gemm_kernel(batch, M, N, K, L, code, 0, ctypes.byref(name),
+                                                 None))
     return name.value.decode()
 
 

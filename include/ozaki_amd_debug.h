@@ -45,13 +45,25 @@ int ozk_debug_force_split_kernel(const char *name);
 int ozk_debug_force_coop_timeout(int on);
 
 /*
+ * Force the split-K ranges of later calls on this thread whose cross-GEMM
+ * runs the ring or the wide kernel: each tile's K is cut into `ranges` (at
+ * most one per 128 bytes of K), one workgroup each, when the call's
+ * workspace holds the split-K buffers (ozk_cross_gemm_workspace_bytes and
+ * ozk_matmul_workspace_bytes size them for the forced count); 0 for the
+ * planner's choice, 1 for none.
+ */
+int ozk_debug_force_gemm_ksplit(int ranges);
+
+/*
  * The cross-GEMM kernel the planner would choose for K-contiguous,
  * 16-byte aligned slice operands of this shape, as a name ("dma", "ring",
- * "wide", "wide4", "solo5", "pair", "staged", "ad") written to *name_out (a static
- * string).  cus: compute units to plan for (0: those of the current device).
+ * "wide", "wide4", "solo5", "pair", "staged", "ad") written to *name_out (a
+ * static string), and its split-K ranges per tile to *ksplit_out (1: none;
+ * may be NULL).  cus: compute units to plan for (0: those of the current
+ * device).
  */
 int ozk_debug_gemm_kernel(int64_t batch, int64_t M, int64_t N, int64_t K, int num_splits,
-                          int slice_dtype, int cus, const char **name_out);
+                          int slice_dtype, int cus, const char **name_out, int *ksplit_out);
 
 /*
  * The split path the planner would choose for an operand described as in

@@ -45,6 +45,7 @@ EXPORTED = (
 # the test hooks of include/ozaki_amd_debug.h
 EXPORTED_DEBUG = (
     "ozk_debug_force_gemm_kernel",
+    "ozk_debug_force_gemm_ksplit",
     "ozk_debug_force_split_kernel",
     "ozk_debug_force_coop_timeout",
     "ozk_debug_gemm_kernel",
@@ -109,8 +110,11 @@ def load() -> ctypes.CDLL:
     L.ozk_debug_force_split_kernel.restype = i32
     L.ozk_debug_force_coop_timeout.argtypes = [i32]
     L.ozk_debug_force_coop_timeout.restype = i32
+    L.ozk_debug_force_gemm_ksplit.argtypes = [i32]
+    L.ozk_debug_force_gemm_ksplit.restype = i32
     L.ozk_debug_gemm_kernel.argtypes = [i64, i64, i64, i64, i32, i32, i32,
-                                        ctypes.POINTER(ctypes.c_char_p)]
+                                        ctypes.POINTER(ctypes.c_char_p),
+                                        ctypes.POINTER(ctypes.c_int)]
     L.ozk_debug_gemm_kernel.restype = i32
     L.ozk_debug_split_kernel.argtypes = [vp, i32, i64, i64, i64, p64, i32, i32, vp, p64,
                                          ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(sz)]
@@ -146,18 +150,23 @@ def device_status(clear: bool = True, stream=None) -> int:
 
 class forced_kernels:
     """Context manager for tests: force the cross-GEMM kernel (`gemm`: "staged",
-    "dma", "ad", "pair", "ring", "wide") and / or the split kernel (`split`:
-    "coop", "strip", "transpose", "generic", "rows", "rowscoop") of the calls
-    this host thread makes inside it, and optionally make every cooperative
-    split wait give up at once (`coop_timeout`).  Restores the defaults on exit."""
+    "dma", "ad", "pair", "ring", "wide", "wide4", "solo5"), its split-K ranges
+    (`ksplit`, ring and wide kernels; 1: none) and / or the split kernel
+    (`split`: "coop", "strip", "transpose", "generic", "rows", "rowscoop") of
+    the calls this host thread makes inside it, and optionally make every
+    cooperative split wait give up at once (`coop_timeout`).  Restores the
+    defaults on exit."""
 
-    def __init__(self, gemm=None, split=None, coop_timeout=False):
+    def __init__(self, gemm=None, split=None, coop_timeout=False, ksplit=None):
         self.gemm, self.split, self.coop_timeout = gemm, split, coop_timeout
+        self.ksplit = ksplit
 
     def __enter__(self):
         L = load()
         if self.gemm is not None:
             check("ozk_debug_force_gemm_kernel", L.ozk_debug_force_gemm_kernel(self.gemm.encode()))
+        if self.ksplit is not None:
+            check("ozk_debug_force_gemm_ksplit", L.ozk_debug_force_gemm_ksplit(int(self.ksplit)))
         if self.split is not None:
             check("ozk_debug_force_split_kernel",
                   L.ozk_debug_force_split_kernel(self.split.encode()))
@@ -168,6 +177,7 @@ class forced_kernels:
     def __exit__(self, *exc):
         L = load()
         L.ozk_debug_force_gemm_kernel(None)
+        L.ozk_debug_force_gemm_ksplit(0)
         L.ozk_debug_force_split_kernel(None)
         L.ozk_debug_force_coop_timeout(0)
         return False

@@ -34,6 +34,26 @@ int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
 int hip_status(hipError_t e) { return e == hipSuccess ? OZK_OK : OZK_ERR_LAUNCH; }
 
+// Split-K buffers (plus 256 bytes of alignment slack) of the cross-GEMM of
+// K-contiguous slice operands with these strides, 0 when the plan has no
+// split-K.  Planned for 256 CUs: a device with fewer plans no more ranges.
+size_t splitk_need(int64_t batch, int64_t M, int64_t N, int64_t K, int L, int sd,
+                   int64_t as_l, int64_t as_m, int64_t bs_l, int64_t bs_n, int out_dtype) {
+    if (L < 1 || L > 4 || batch * M * N == 0) return 0;
+    ozk::GemmParams gp{};
+    gp.as_l = as_l;
+    gp.as_m = as_m;
+    gp.bs_l = bs_l;
+    gp.bs_n = bs_n;
+    gp.batch = batch;
+    gp.M = M;
+    gp.N = N;
+    gp.K = K;
+    gp.out_dtype = out_dtype;
+    const size_t b = ozk::splitk_bytes(gp, ozk::plan_gemm(gp, L, sd, 256), L);
+    return b ? b + 256 : 0;
+}
+
 ozk::SplitParams make_split_params(const void *X, int64_t batch, int64_t rows, int64_t K,
                                    const int64_t xs[3], int L, int alpha, void *slices,
                                    const int64_t ss[4], float *scales, const int64_t cs[3]) {
@@ -183,7 +203,13 @@ int ozk_cross_gemm_workspace_bytes(int64_t batch, int64_t M, int64_t N, int64_t 
     const int es = slice_size(slice_dtype);
     const int64_t a = pack_bytes(A_slices, a_strides, batch, num_splits, M, K, es, false);
     const int64_t b = pack_bytes(B_slices, b_strides, batch, num_splits, N, K, es, true);
-    *bytes_out = (size_t)(a + b);
+    // and, for grids too small to fill the chip, the split-K buffers (the
+    // call runs without split-K when the workspace lacks them)
+    const int64_t kp = round_up(K * es, 16) / es;
+    const size_t sk = splitk_need(batch, M, N, K, num_splits, slice_dtype,
+                                  a ? M * kp : a_strides[1], a ? kp : a_strides[2],
+                                  b ? N * kp : b_strides[1], b ? kp : b_strides[3], OZK_F64);
+    *bytes_out = (size_t)(a + b) + sk;
     return OZK_OK;
 }
 
@@ -264,7 +290,7 @@ static int cross_gemm_impl(const void *A_slices, const int64_t a_strides[4], con
         p.bs_l = b_strides[1];
         p.bs_n = b_strides[3];
     }
-    const ozk::GemmPlan plan = ozk::plan_gemm(p, num_splits, slice_dtype);
+    ozk::GemmPlan plan = ozk::plan_gemm(p, num_splits, slice_dtype);
     // more than 4 slices, operands within the 31-bit offsets of the LDS-DMA
     // kernels: 5 int8 / fp16 / bf16 slices in one launch (any C dtype); 6 to
     // 8 (or a forced pair-split kernel) into an fp64 C, which holds the
@@ -275,6 +301,16 @@ static int cross_gemm_impl(const void *A_slices, const int64_t a_strides[4], con
                           slice_dtype != OZK_F32;
         if (!solo && !pair) return OZK_ERR_SPLITS;
     }
+    // split-K buffers after the packed operands, 256-byte aligned, when the
+    // workspace holds them (else the plan runs without split-K)
+    void *skws = nullptr;
+    if (const size_t skb = ozk::splitk_bytes(p, plan, num_splits)) {
+        const uintptr_t base = (uintptr_t)workspace;
+        const uintptr_t start = (base + (uintptr_t)(abytes + bbytes) + 255) / 256 * 256;
+        if (workspace && start + skb <= base + workspace_bytes) skws = (void *)start;
+        else plan.ksplit = 1;
+    }
+    if (hipError_t e = ozk::setup_splitk(p, plan, num_splits, skws, st)) return hip_status(e);
     return hip_status(ozk::launch_gemm(p, plan, num_splits, slice_dtype, st));
 }
 
@@ -308,6 +344,7 @@ struct MatmulLayout {
     int64_t bA, bB;                                 // split batches (1 when broadcast)
     size_t a_sl, a_sc, b_sl, b_sc, scratch, pack;   // byte offsets
     size_t scratch_bytes;                           // split scratch reserved
+    size_t splitk;                                  // cross-GEMM split-K buffers (after pack)
     size_t total;
     int64_t bt_strides[3];                          // B^T view of B
     int64_t ga[4], gb[4], gsa[3], gsb[3];           // cross-GEMM strides of the slices
@@ -379,7 +416,11 @@ int matmul_layout(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
     const int64_t pk = pack_bytes((const void *)256, ga, batch, L, M, K, (int)ss, false) +
                        pack_bytes((const void *)256, gb, batch, L, N, K, (int)ss, true);
     o->pack = off; off = align256(off + (size_t)pk);
-    o->total = off;
+    // the split-K buffers of a grid too small to fill the chip follow the
+    // pack region (the cross-GEMM runs without them when they are missing)
+    const int64_t kp = round_up(K * ss, 16) / ss;
+    o->splitk = splitk_need(batch, M, N, K, L, sd, M * kp, kp, N * kp, kp, dtype);
+    o->total = off + o->splitk;
     return OZK_OK;
 }
 
@@ -422,7 +463,8 @@ int ozk_matmul(const void *A, const int64_t a_strides[3], const void *B,
                                K, 0, slice_dtype, C, dtype, c_strides, nullptr, 0, stream);
     }
     if (!A || !B) return OZK_ERR_NULL;
-    if (!workspace || workspace_bytes < lay.total || (uintptr_t)workspace % 256 != 0)
+    // the split-K buffers at the end are optional
+    if (!workspace || workspace_bytes < lay.total - lay.splitk || (uintptr_t)workspace % 256 != 0)
         return OZK_ERR_WORKSPACE;
     char *ws = (char *)workspace;
     const int64_t asl[4] = {L * M * K, M * K, K, 1}, bsl[4] = {L * N * K, N * K, K, 1};
@@ -506,7 +548,9 @@ extern "C" int ozk_matmul_static(const void *A, const int64_t a_strides[3], cons
     if (batch * M * N == 0 || num_splits == 0)   // no workspace used
         return ozk_matmul(A, a_strides, B, b_strides, dtype, batch, M, N, K, num_splits,
                           slice_dtype, C, c_strides, nullptr, 0, events, stream);
-    if (lay.total > OZK_STATIC_SCRATCH_BYTES) return OZK_ERR_TOO_LARGE;
+    // split-K buffers are optional: the call needs the rest, and takes them
+    // only if they fit too
+    if (lay.total - lay.splitk > OZK_STATIC_SCRATCH_BYTES) return OZK_ERR_TOO_LARGE;
     void *ws = nullptr;
     if (const int e = static_scratch(&ws)) return e;
     return ozk_matmul(A, a_strides, B, b_strides, dtype, batch, M, N, K, num_splits,
@@ -556,6 +600,12 @@ int ozk_debug_force_gemm_kernel(const char *name) {
     return lookup(kGemmNames, name, ozk::kForceGemmNone, &ozk::debug_overrides().gemm);
 }
 
+int ozk_debug_force_gemm_ksplit(int ranges) {
+    if (ranges < 0) return OZK_ERR_SPLITS;
+    ozk::debug_overrides().ksplit = ranges;
+    return OZK_OK;
+}
+
 int ozk_debug_force_split_kernel(const char *name) {
     return lookup(kSplitNames, name, ozk::kForceSplitNone, &ozk::debug_overrides().split);
 }
@@ -566,7 +616,7 @@ int ozk_debug_force_coop_timeout(int on) {
 }
 
 int ozk_debug_gemm_kernel(int64_t batch, int64_t M, int64_t N, int64_t K, int num_splits,
-                          int slice_dtype, int cus, const char **name_out) {
+                          int slice_dtype, int cus, const char **name_out, int *ksplit_out) {
     if (!name_out) return OZK_ERR_NULL;
     if (!is_slice_dtype(slice_dtype)) return OZK_ERR_DTYPE;
     if (num_splits < 1 || num_splits > OZK_MAX_SPLITS) return OZK_ERR_SPLITS;
@@ -586,7 +636,9 @@ int ozk_debug_gemm_kernel(int64_t batch, int64_t M, int64_t N, int64_t K, int nu
     p.N = N;
     p.K = K;
     p.out_dtype = OZK_F64;
-    *name_out = name_of(kGemmNames, ozk::plan_gemm(p, num_splits, slice_dtype, cus).kind);
+    const ozk::GemmPlan plan = ozk::plan_gemm(p, num_splits, slice_dtype, cus);
+    *name_out = name_of(kGemmNames, plan.kind);
+    if (ksplit_out) *ksplit_out = plan.ksplit;
     return OZK_OK;
 }
 

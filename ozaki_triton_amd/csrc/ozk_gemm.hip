@@ -45,6 +45,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 template <typename ST> struct Mfma;
 template <> struct Mfma<int8_t> {
     using Acc = i32x16;
+    using Elem = int;
     OZK_DEV static Acc zero() { return Acc{0}; }
     OZK_DEV static Acc run(i32x4 a, i32x4 b, Acc c) {
         return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
@@ -53,6 +54,7 @@ template <> struct Mfma<int8_t> {
 };
 template <> struct Mfma<_Float16> {
     using Acc = f32x16;
+    using Elem = float;
     OZK_DEV static Acc zero() { return Acc{0.0f}; }
     OZK_DEV static Acc run(i32x4 a, i32x4 b, Acc c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
@@ -64,6 +66,7 @@ template <> struct Mfma<_Float16> {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 template <> struct Mfma<__bf16> {
     using Acc = f32x16;
+    using Elem = float;
     OZK_DEV static Acc zero() { return Acc{0.0f}; }
     OZK_DEV static Acc run(i32x4 a, i32x4 b, Acc c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
@@ -79,6 +82,7 @@ template <> struct Mfma<__bf16> {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 template <> struct Mfma<float> {
     using Acc = f32x16;
+    using Elem = float;
     OZK_DEV static Acc zero() { return Acc{0.0f}; }
     OZK_DEV static Acc run(i32x4 a, i32x4 b, Acc c) {
         const f32x4 fa = __builtin_bit_cast(f32x4, a), fb = __builtin_bit_cast(f32x4, b);
@@ -348,6 +352,63 @@ template <int N> OZK_DEV void wait_vmcnt() {
 // wait_vmcnt first; the memory clobber keeps the compiler from moving LDS
 // accesses across the barrier.
 OZK_DEV void exec_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// ---------------------------------------------------------------------------
+// Split-K hand-off (ring and wide kernels on grids too small to fill the
+// chip).  A tile's 128-byte K stages are cut into p.ksplit ranges of
+// p.kb_per_split stages, one workgroup each (consecutive workgroup ids).
+// Every range stores its raw accumulators (for int8 slices the exact int32
+// dot products) to p.kpart, lane-contiguous per register, and counts itself
+// in the tile's arrival counter; the range that arrives last reads all
+// ranges' accumulators back, adds them in range order (from zero) and goes
+// on to the epilogue, the others exit.  No workgroup waits for another, and
+// C does not depend on which range arrives last.
+// ---------------------------------------------------------------------------
+constexpr int kSplitKWaves = 8;   // both kernels run 8 waves
+// The lane index read where it is used (an opaque read the compiler cannot
+// hoist), so no split-K address is held in registers through the K loop.
+OZK_DEV int lane_here() {
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+}
+OZK_DEV uint32_t *splitk_slot(const GemmParams &p, int64_t tile, int range, int wave, int regs,
+                              int lane) {
+    return p.kpart + (((tile * p.ksplit + range) * kSplitKWaves + wave) * regs) * 64 + lane;
+}
+// The accumulators go through agent-scope stores and loads, which write
+// through to, and read from, the level every XCD shares: once a store has
+// completed (vmcnt), every later agent-scope load sees it, with no L2
+// write-back or invalidation (a fence here costs a write-back of the whole
+// L2 per wave).
+OZK_DEV void splitk_put(uint32_t *dst, uint32_t v) {
+    __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+OZK_DEV uint32_t splitk_get(const uint32_t *src) {
+    return __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// one accumulator tile (16 registers, 64 words apart): all 16 loads are
+// issued before the first is used
+template <typename Acc> OZK_DEV Acc splitk_get16(const uint32_t *src) {
+    i32x16 u;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) u[r] = (int)splitk_get(src + r * 64);
+    return __builtin_bit_cast(Acc, u);
+}
+// Called by every wave after it stored its accumulators: true in the
+// workgroup that arrived last.  Every wave's stores complete before the
+// barrier, and the counter is incremented after it, so the range that reads
+// ksplit - 1 from the counter finds every range's accumulators in place.
+OZK_DEV bool splitk_arrive(const GemmParams &p, int64_t tile, int *flag) {
+    wait_vmcnt<0>();
+    exec_barrier();
+    if (threadIdx.x == 0)
+        *flag = (int)__hip_atomic_fetch_add(p.kcount + tile, 1u, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // the flag's LDS write
+    exec_barrier();
+    return *flag == p.ksplit - 1;
+}
 
 template <typename ST, int L, int MI, int NI, typename AccT>
 __global__ __launch_bounds__(256, 1) void cross_gemm_dma_kernel(GemmParams p, int group_m,
@@ -919,7 +980,11 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ring_kernel(GemmParams p, i
     const int64_t tiles_m = (p.M + BM - 1) / BM;
     const int64_t tiles_n = (p.N + BN - 1) / BN;
     const int64_t tiles = tiles_m * tiles_n;
-    const int64_t g = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
+    // split-K: workgroup g0 is K range g0 % S of tile g0 / S
+    const int S = p.ksplit > 1 ? p.ksplit : 1;
+    const int64_t g0 = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
+    const int krange = (int)(g0 % S);
+    const int64_t g = g0 / S;
     const int64_t bidx = g / tiles;
     const int64_t t = g % tiles;
     const int64_t width = (int64_t)group_m * tiles_n;
@@ -930,7 +995,10 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ring_kernel(GemmParams p, i
     const int64_t m0 = tm * BM, n0 = tn * BN;
 
     const uint32_t kbytes = (uint32_t)(p.K * ES);
-    const int nkb = (int)((kbytes + kDmaRB - 1) / kDmaRB);
+    const int nkb_all = (int)((kbytes + kDmaRB - 1) / kDmaRB);
+    const int kb0 = S > 1 ? krange * p.kb_per_split : 0;   // this range's first stage
+    const int nkb = S > 1 ? min(p.kb_per_split, nkb_all - kb0) : nkb_all;
+    const uint32_t kbyte0 = (uint32_t)kb0 * kDmaRB;
     constexpr int STEPS = kDmaRB / 32;
 
     const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
@@ -954,13 +1022,13 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ring_kernel(GemmParams p, i
     }
     auto slot = [&](int hs) { return smem + (hs % Sh::NSLOT) * Sh::SLOT; };
     auto issue_a = [&](int kb, int q) {
-        const uint32_t kofs = (uint32_t)kb * kDmaRB + chA[q] * 16;
+        const uint32_t kofs = kbyte0 + (uint32_t)kb * kDmaRB + chA[q] * 16;
         const uint32_t vo = (srcA[q] == kOOB || kofs >= kbytes) ? kOOB : srcA[q] + kofs;
         auto *ldsp = (__attribute__((address_space(3))) void *)(slot(2 * kb) + (wave * LPH + q) * 1024);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, ldsp, 16, vo, 0, 0, 0);
     };
     auto issue_b = [&](int kb, int q) {
-        const uint32_t kofs = (uint32_t)kb * kDmaRB + chB[q] * 16;
+        const uint32_t kofs = kbyte0 + (uint32_t)kb * kDmaRB + chB[q] * 16;
         const uint32_t vo = (srcB[q] == kOOB || kofs >= kbytes) ? kOOB : srcB[q] + kofs;
         auto *ldsp = (__attribute__((address_space(3))) void *)(slot(2 * kb + 1) + (wave * LPH + q) * 1024);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, ldsp, 16, vo, 0, 0, 0);
@@ -1121,6 +1189,40 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ring_kernel(GemmParams p, i
         wait_vmcnt<0>();
         __builtin_amdgcn_s_waitcnt(0xC07F);
         exec_barrier();
+        if (S > 1) {
+            // split-K: the ranges' accumulators into the last range's
+            // registers (the flag word sits in a ring slot no stage used)
+            constexpr int RW = (PS::count(0) > PS::count(1) ? PS::count(0) : PS::count(1)) * W * W * 16;
+            const int ln = lane_here();
+            uint32_t *mine = splitk_slot(p, g, krange, wave, RW, ln);
+#pragma unroll
+            for (int q = 0; q < NP; ++q)
+#pragma unroll
+                for (int x = 0; x < W * W; ++x) {
+                    const i32x16 u = __builtin_bit_cast(i32x16, acc[q][x / W][x % W]);
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) splitk_put(mine + ((q * W * W + x) * 16 + r) * 64, (uint32_t)u[r]);
+                }
+            if (!splitk_arrive(p, g, (int *)slot(2 * nkb + 1))) return;
+            // every range read back in range order: range 0 straight into
+            // the accumulators, then the others added one tile at a time
+            {
+                const uint32_t *src = splitk_slot(p, g, 0, wave, RW, ln);
+#pragma unroll
+                for (int q = 0; q < NP; ++q)
+#pragma unroll
+                    for (int x = 0; x < W * W; ++x)
+                        acc[q][x / W][x % W] = splitk_get16<Acc>(src + (q * W * W + x) * 16 * 64);
+            }
+            for (int s2 = 1; s2 < S; ++s2) {
+                const uint32_t *src = splitk_slot(p, g, s2, wave, RW, ln);
+#pragma unroll
+                for (int q = 0; q < NP; ++q)
+#pragma unroll
+                    for (int x = 0; x < W * W; ++x)
+                        acc[q][x / W][x % W] += splitk_get16<Acc>(src + (q * W * W + x) * 16 * 64);
+            }
+        }
         // this wave's scales into registers: sa of its rows, sb of its columns
         float sbv[W][L], sav[W][16][NA];
 #pragma unroll
@@ -1240,7 +1342,11 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide_kernel(GemmParams p, i
     const int64_t tiles_m = (p.M + BM - 1) / BM;
     const int64_t tiles_n = (p.N + BN - 1) / BN;
     const int64_t tiles = tiles_m * tiles_n;
-    const int64_t g = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
+    // split-K: workgroup g0 is K range g0 % S of tile g0 / S
+    const int S = p.ksplit > 1 ? p.ksplit : 1;
+    const int64_t g0 = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
+    const int krange = (int)(g0 % S);
+    const int64_t g = g0 / S;
     const int64_t bidx = g / tiles;
     const int64_t t = g % tiles;
     const int64_t width = (int64_t)group_m * tiles_n;
@@ -1251,7 +1357,10 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide_kernel(GemmParams p, i
     const int64_t m0 = tm * BM, n0 = tn * BN;
 
     const uint32_t kbytes = (uint32_t)(p.K * ES);
-    const int nkb = (int)((kbytes + kDmaRB - 1) / kDmaRB);
+    const int nkb_all = (int)((kbytes + kDmaRB - 1) / kDmaRB);
+    const int kb0 = S > 1 ? krange * p.kb_per_split : 0;   // this range's first stage
+    const int nkb = S > 1 ? min(p.kb_per_split, nkb_all - kb0) : nkb_all;
+    const uint32_t kbyte0 = (uint32_t)kb0 * kDmaRB;
 
     const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
         (void *)((const char *)p.A + bidx * p.as_b * ES), (short)0, (int)a_records, 0x00020000);
@@ -1280,7 +1389,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide_kernel(GemmParams p, i
     auto buf = [&](int kb) { return smem + (kb & 1) * Sh::STAGE; };
     auto issue = [&](int kb, int q) {
         const int ch = c0 ^ ((window(q) & 1) << 2);
-        const uint32_t kofs = (uint32_t)kb * kDmaRB + ch * 16;
+        const uint32_t kofs = kbyte0 + (uint32_t)kb * kDmaRB + ch * 16;
         const uint32_t vo = (src[q] == kOOB || kofs >= kbytes) ? kOOB : src[q] + kofs;
         auto *ldsp = (__attribute__((address_space(3))) void *)(
             buf(kb) + (q < Sh::LA ? 0 : Sh::A_BYTES) + window(q) * 1024);
@@ -1400,6 +1509,35 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide_kernel(GemmParams p, i
     wait_vmcnt<0>();
     __builtin_amdgcn_s_waitcnt(0xC07F);
     exec_barrier();
+    if (S > 1) {
+        // split-K: the ranges' accumulators into the last range's registers
+        // (the flag word sits in the stage buffer the scales did not use)
+        constexpr int RW = L * L * 16;
+        const int ln = lane_here();
+        uint32_t *mine = splitk_slot(p, g, krange, wave, RW, ln);
+#pragma unroll
+        for (int n = 0; n < L * L; ++n) {
+            const i32x16 u = __builtin_bit_cast(i32x16, acc[n / L][n % L]);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) splitk_put(mine + (n * 16 + r) * 64, (uint32_t)u[r]);
+        }
+        if (!splitk_arrive(p, g, (int *)buf(nkb + 1))) return;
+        // every range read back, this one's too (keeping this range's
+        // registers live through the sum costs the K loop a spill), in
+        // range order: range 0 straight into the accumulators, then the
+        // others added one tile (16 loads in flight) at a time
+        {
+            const uint32_t *src = splitk_slot(p, g, 0, wave, RW, ln);
+#pragma unroll
+            for (int n = 0; n < L * L; ++n) acc[n / L][n % L] = splitk_get16<Acc>(src + n * 16 * 64);
+        }
+        for (int s2 = 1; s2 < S; ++s2) {
+            const uint32_t *src = splitk_slot(p, g, s2, wave, RW, ln);
+#pragma unroll
+            for (int n = 0; n < L * L; ++n)
+                acc[n / L][n % L] += splitk_get16<Acc>(src + n * 16 * 64);
+        }
+    }
     const int ct = wn * 32 + lr;
     const int64_t col = n0 + ct;
     const int64_t cbase = bidx * p.cs_b;
@@ -2372,7 +2510,7 @@ static int device_cus() {
 }
 
 GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
-    GemmPlan plan{1, 1, 8, kGemmStaged};
+    GemmPlan plan{1, 1, 8, kGemmStaged, 1, 0};
     int mi = 1, ni = 1;
     if (L <= 1) { mi = 2; ni = 4; }
     else if (L == 2) { mi = 2; ni = 2; }
@@ -2413,9 +2551,33 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
     // 1.11-1.24; the rule below picks the faster one at each of these except
     // 384 (within 3%).
     const int64_t kCUs = cus > 0 ? cus : device_cus();
-    const int64_t wide_rounds = (p.batch * ((p.M + 63) / 64) * ((p.N + 127) / 128) + kCUs - 1) / kCUs;
-    const int64_t ring_rounds = (nt(1, 1) + kCUs - 1) / kCUs;
-    const bool wide3 = L == 3 && 12 * wide_rounds < 7 * ring_rounds;
+    // Split-K (ring and wide kernels): a grid of fewer tiles than half the
+    // CUs cuts each tile's K stages into S ranges, one workgroup each: S =
+    // CUs / tiles, at most 4 (the last range reads all S ranges'
+    // accumulators back) and at least 16 stages (2 KB of K) per range: the
+    // hand-over costs about as much as 8 to 16 stages of int8 MFMA work
+    // (measured at (1, 128, 2048, 4096), cross-GEMM alone: int8 num_splits 4
+    // 66.7 us unsplit, 61.0 with 2 ranges of 16 stages, 63.4 with 4 of 8;
+    // num_splits 3 47.7 against 54.7 with 4 of 8; fp16 num_splits 4 106.1,
+    // 81.2 with 2 of 32, 73.5 with 4 of 16; C5 wide 899 us unsplit, 572 with
+    // 2 ranges of 256 against the ring kernel's 592).  Sized for at most 256
+    // CUs, so the workspace queries (which plan for 256) cover any gfx950
+    // device.
+    const int nkb_all = (int)((p.K * es + kDmaRB - 1) / kDmaRB);
+    const int64_t cus_k = kCUs < 256 ? kCUs : 256;
+    auto ksplit_for = [&](int64_t ntiles) -> int {
+        if (ntiles <= 0 || 2 * ntiles > cus_k) return 1;
+        int64_t sk = cus_k / ntiles;
+        if (sk > 4) sk = 4;
+        if (sk > nkb_all / 16) sk = nkb_all / 16;
+        return sk >= 2 ? (int)sk : 1;
+    };
+    const int64_t wide_tiles = p.batch * ((p.M + 63) / 64) * ((p.N + 127) / 128);
+    const int sr = ksplit_for(nt(1, 1)), sw = ksplit_for(wide_tiles);
+    const int64_t wide_rounds = (wide_tiles * sw + kCUs - 1) / kCUs;
+    const int64_t ring_rounds = (nt(1, 1) * sr + kCUs - 1) / kCUs;
+    // with split-K a round of S ranges takes 1 / S of a tile's time
+    const bool wide3 = L == 3 && 12 * wide_rounds * sr < 7 * ring_rounds * sw;
     // L = 4: the 96 x 64 wide kernel (one workgroup per CU, like the ring
     // kernel) does 1.5 ring tiles of work per tile at 1.04-1.14x the ring's
     // rate, about 1.45 ring tiles' time (measured: 8192^3 43 rounds against
@@ -2453,7 +2615,67 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
     // 96 x 64 tiles: groups of 4 tile rows (C3: 7.12-7.16 ms against 7.21-7.23
     // with 8, 7.33-7.35 with 16; cross-GEMM alone, one box)
     if (plan.kind == kGemmWide4) plan.group_m = 4;
+    plan.kb_per_split = nkb_all;
+    if (plan.kind == kGemmRing || plan.kind == kGemmWide) {
+        const int64_t tiles_k = plan.kind == kGemmWide ? wide_tiles : L <= 2 ? nt(2, 2) : nt(1, 1);
+        const int fk = debug_overrides().ksplit;
+        int sk = fk > 0 ? fk : ksplit_for(tiles_k);
+        if (sk > nkb_all) sk = nkb_all;
+        if (sk > 1) {
+            // every range holds at least one stage
+            plan.kb_per_split = (nkb_all + sk - 1) / sk;
+            plan.ksplit = (nkb_all + plan.kb_per_split - 1) / plan.kb_per_split;
+        }
+    }
     return plan;
+}
+
+// tiles of a kind's launch and 32-bit accumulator registers per wave that a
+// split-K range hands over
+static void splitk_shape(const GemmParams &p, const GemmPlan &plan, int L, int64_t *tiles,
+                         int *regs) {
+    const int bm = plan.kind == kGemmWide ? 64 : L <= 2 ? 128 : 64;
+    const int bn = plan.kind == kGemmWide ? 128 : L <= 2 ? 128 : 64;
+    *tiles = p.batch * ((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
+    if (plan.kind == kGemmWide) {
+        *regs = 3 * 3 * 16;
+    } else {
+        const int P = L * L, P0 = (L == 3) ? 6 : (P + 1) / 2;   // PairSplit<L, L>
+        const int w = L <= 2 ? 2 : 1;
+        *regs = (P0 > P - P0 ? P0 : P - P0) * w * w * 16;
+    }
+}
+
+static size_t round256(size_t x) { return (x + 255) / 256 * 256; }
+
+size_t splitk_bytes(const GemmParams &p, const GemmPlan &plan, int L) {
+    if (plan.ksplit <= 1) return 0;
+    int64_t tiles;
+    int regs;
+    splitk_shape(p, plan, L, &tiles, &regs);
+    const size_t part = (size_t)(tiles * plan.ksplit * kSplitKWaves * regs) * 64 * 4;
+    return round256(part) + round256((size_t)tiles * 4);
+}
+
+__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t *p, int64_t n) {
+    for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0;
+}
+
+hipError_t setup_splitk(GemmParams &p, const GemmPlan &plan, int L, void *ws, hipStream_t st) {
+    p.ksplit = plan.ksplit;
+    p.kb_per_split = plan.kb_per_split;
+    p.kpart = nullptr;
+    p.kcount = nullptr;
+    if (plan.ksplit <= 1) return hipSuccess;
+    int64_t tiles;
+    int regs;
+    splitk_shape(p, plan, L, &tiles, &regs);
+    const size_t part = (size_t)(tiles * plan.ksplit * kSplitKWaves * regs) * 64 * 4;
+    p.kpart = (uint32_t *)ws;
+    p.kcount = (uint32_t *)((char *)ws + round256(part));
+    const int64_t blocks = (tiles + 255) / 256 < 1024 ? (tiles + 255) / 256 : 1024;
+    hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, st, p.kcount, tiles);
+    return hipGetLastError();
 }
 
 // byte extent [0, bytes) one batch of a slice operand spans, or -1 if it does
@@ -2545,7 +2767,8 @@ static hipError_t launch_ring(const GemmParams &p, const GemmPlan &plan, hipStre
     const int64_t eb = dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es);
     const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
     if (tiles == 0) return hipSuccess;
-    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(512), Sh::LDS_BYTES, st, p,
+    const int64_t ranges = p.ksplit > 1 ? p.ksplit : 1;
+    hipLaunchKernelGGL(kern, dim3((unsigned)(tiles * ranges)), dim3(512), Sh::LDS_BYTES, st, p,
                        plan.group_m, (uint32_t)ea, (uint32_t)eb);
     return hipGetLastError();
 }
@@ -2561,7 +2784,8 @@ static hipError_t launch_wide(const GemmParams &p, const GemmPlan &plan, hipStre
     const int64_t eb = dma_extent(p.bs_l, p.bs_n, Sh::L, p.N, p.K, es);
     const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
     if (tiles == 0) return hipSuccess;
-    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(512), Sh::LDS_BYTES, st, p,
+    const int64_t ranges = p.ksplit > 1 ? p.ksplit : 1;
+    hipLaunchKernelGGL(kern, dim3((unsigned)(tiles * ranges)), dim3(512), Sh::LDS_BYTES, st, p,
                        plan.group_m, (uint32_t)ea, (uint32_t)eb);
     return hipGetLastError();
 }

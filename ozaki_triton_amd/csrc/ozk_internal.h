@@ -27,6 +27,7 @@ struct DebugOverrides {
     int gemm = kForceGemmNone;
     int split = kForceSplitNone;
     int coop_timeout = 0;   // 1: every cooperative wait gives up at once (its timeout path)
+    int ksplit = 0;         // > 0: split-K ranges of the ring and wide kernels (0: the planner's)
 };
 DebugOverrides &debug_overrides();
 
@@ -97,6 +98,14 @@ struct GemmParams {
     int64_t batch, M, N, K;
     int out_dtype;              // C's dtype code: 0 f64 (fp64 outer accumulator), else
                                 // f32 / f16 / bf16 / i8 (fp32 outer accumulator)
+    // split-K (ring and wide kernels): a tile's 128-byte K stages are cut into
+    // ksplit ranges of kb_per_split stages, one workgroup each; ksplit <= 1:
+    // none.  kpart holds the ranges' raw accumulators, kcount one arrival
+    // counter per tile (zero at launch).
+    int ksplit;
+    int kb_per_split;
+    uint32_t *kpart;
+    uint32_t *kcount;
 };
 
 enum GemmKind {
@@ -117,9 +126,17 @@ struct GemmPlan {
     int mi, ni;       // 2 x 2 kernels: wave tile = (32*mi) x (32*ni)
     int group_m;      // tile-row group for L2 reuse
     int kind;         // GemmKind; the LDS-DMA kernels need 31-bit operand extents
+    int ksplit;       // split-K ranges per tile (1: none)
+    int kb_per_split; // 128-byte K stages per range
 };
 // cus: compute units of the device (0: ask the current device, once per device)
 GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus = 0);
+// Workspace of a split-K plan: the ranges' accumulators and the tile counters
+// (0 without split-K), and where they go in it (256-byte aligned offsets).
+size_t splitk_bytes(const GemmParams &p, const GemmPlan &plan, int L);
+// Points p at the split-K buffers in ws and clears the counters (a fill
+// kernel, no memset: the call may be captured in a graph).
+hipError_t setup_splitk(GemmParams &p, const GemmPlan &plan, int L, void *ws, hipStream_t stream);
 hipError_t launch_gemm(const GemmParams &p, const GemmPlan &plan, int L, int slice_dtype,
                        hipStream_t stream);
 

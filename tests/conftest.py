@@ -29,15 +29,17 @@ def gpu():
 
 @pytest.fixture
 def force():
-    """force(gemm=..., split=..., coop_timeout=...) forces kernels through the
-    library's thread-local test hooks (include/ozaki_amd_debug.h) for the rest
-    of the test; the defaults come back at teardown."""
+    """force(gemm=..., split=..., coop_timeout=..., ksplit=...) forces kernels
+    through the library's thread-local test hooks (include/ozaki_amd_debug.h)
+    for the rest of the test; the defaults come back at teardown."""
     from ozaki_triton_amd import _lib
     L = _lib.load()
 
-    def set_(gemm=None, split=None, coop_timeout=None):
+    def set_(gemm=None, split=None, coop_timeout=None, ksplit=None):
         if gemm is not None:
             _lib.check("ozk_debug_force_gemm_kernel", L.ozk_debug_force_gemm_kernel(gemm.encode()))
+        if ksplit is not None:
+            _lib.check("ozk_debug_force_gemm_ksplit", L.ozk_debug_force_gemm_ksplit(int(ksplit)))
         if split is not None:
             _lib.check("ozk_debug_force_split_kernel",
                        L.ozk_debug_force_split_kernel(split.encode()))
@@ -46,5 +48,6 @@ def force():
 
     yield set_
     L.ozk_debug_force_gemm_kernel(None)
+    L.ozk_debug_force_gemm_ksplit(0)
     L.ozk_debug_force_split_kernel(None)
     L.ozk_debug_force_coop_timeout(0)

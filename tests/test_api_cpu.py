@@ -209,6 +209,42 @@ def test_cross_gemm_abi_checks_and_workspace():
     assert call(B=0) == _lib.OZK_OK
 
 
+def test_splitk_workspace():
+    """Grids under half the CUs cut each tile's K into ranges (split-K, planned
+    for 256 CUs in the queries).  The workspace queries add the ranges'
+    accumulators (tiles x ranges x 8 waves x registers x 64 lanes x 4 bytes)
+    and one arrival counter per tile, plus 256 bytes of alignment slack;
+    forcing one range (the test hook) takes them away."""
+    from ozaki_triton_amd import _lib
+    L = _lib.load()
+    nb = ctypes.c_size_t(0)
+    p = ctypes.c_void_p(0x1000)
+    M, N, K, Ls = 128, 2048, 4096, 4
+    a = _lib.i64arr([Ls * M * K, M * K, K, 1])
+    b = _lib.i64arr([Ls * N * K, N * K, 1, K])
+    # ring kernel, L = 4: 64 tiles of 64 x 64, 2 ranges of 16 stages, 8 pairs x
+    # 16 registers per wave
+    splitk = 64 * 2 * 8 * 128 * 64 * 4 + 256 + 256
+    assert L.ozk_cross_gemm_workspace_bytes(1, M, N, K, Ls, _lib.OZK_I8, p, a, p, b,
+                                            ctypes.byref(nb)) == 0
+    assert nb.value == splitk
+    a3, b3 = _lib.i64arr([M * K, K, 1]), _lib.i64arr([K * N, N, 1])
+    assert L.ozk_matmul_workspace_bytes(_lib.OZK_F64, 1, M, N, K, a3, b3, Ls, _lib.OZK_I8,
+                                        ctypes.byref(nb)) == 0
+    with_splitk = nb.value
+    try:
+        assert L.ozk_debug_force_gemm_ksplit(1) == 0
+        assert L.ozk_cross_gemm_workspace_bytes(1, M, N, K, Ls, _lib.OZK_I8, p, a, p, b,
+                                                ctypes.byref(nb)) == 0
+        assert nb.value == 0
+        assert L.ozk_matmul_workspace_bytes(_lib.OZK_F64, 1, M, N, K, a3, b3, Ls, _lib.OZK_I8,
+                                            ctypes.byref(nb)) == 0
+        assert with_splitk - nb.value == splitk
+    finally:
+        L.ozk_debug_force_gemm_ksplit(0)
+    assert L.ozk_debug_force_gemm_ksplit(-1) == _lib.OZK_ERR_SPLITS
+
+
 # --------------------------------------------------------------------------- #
 # Python API: the reference's checks and messages (ozaki_triton.py:97,560-563)
 # --------------------------------------------------------------------------- #
@@ -467,10 +503,12 @@ def test_debug_hooks_reject_unknown_names():
         assert L.ozk_debug_force_split_kernel(k) == 0
 
 
-def _gemm_kernel(L, batch, M, N, K, nsp, sd, cus):
+def _gemm_kernel(L, batch, M, N, K, nsp, sd, cus, with_ksplit=False):
     name = ctypes.c_char_p()
-    assert L.ozk_debug_gemm_kernel(batch, M, N, K, nsp, sd, cus, ctypes.byref(name)) == 0
-    return name.value.decode()
+    ks = ctypes.c_int(0)
+    assert L.ozk_debug_gemm_kernel(batch, M, N, K, nsp, sd, cus, ctypes.byref(name),
+                                   ctypes.byref(ks)) == 0
+    return (name.value.decode(), ks.value) if with_ksplit else name.value.decode()
 
 
 def test_planner_kernel_choice():
@@ -488,7 +526,9 @@ def test_planner_kernel_choice():
     assert _gemm_kernel(L, 1, 1024, 3840, 4096, 3, I8, 256) == "wide"     # 480
     assert _gemm_kernel(L, 1, 1024, 4096, 4096, 3, I8, 256) == "wide"     # 512
     assert _gemm_kernel(L, 16, 1024, 1024, 2048, 3, _lib.OZK_F16, 256) == "wide"   # config 4
-    assert _gemm_kernel(L, 1, 1024, 1024, 65536, 3, I8, 256) == "ring"    # config 5: 128 tiles
+    # config 5: 128 wide tiles with 2 split-K ranges each, one round, against
+    # 256 ring tiles in one round (12 * 1 * 1 < 7 * 1 * 2)
+    assert _gemm_kernel(L, 1, 1024, 1024, 65536, 3, I8, 256) == "wide"
     # 200 wide tiles on 32 CUs: 7 rounds against 13 -> 84 < 91: wide; 288: 9 vs 18 -> wide
     assert _gemm_kernel(L, 1, 640, 2560, 4096, 3, I8, 32) == "wide"
     assert _gemm_kernel(L, 1, 1024, 2304, 4096, 3, I8, 32) == "wide"
@@ -502,6 +542,17 @@ def test_planner_kernel_choice():
     assert _gemm_kernel(L, 1, 4096, 4096, 4096, 2, _lib.OZK_F16, 256) == "ring"   # config 2
     assert _gemm_kernel(L, 1, 256, 256, 256, 2, _lib.OZK_F16, 256) == "dma"       # config 1
     assert _gemm_kernel(L, 1, 2048, 2048, 2048, 1, I8, 256) == "dma"
+    # split-K for grids under half the CUs: S = CUs / tiles, at most 4, at
+    # least 16 stages of 128 bytes of K per range
+    assert _gemm_kernel(L, 1, 128, 2048, 4096, 4, I8, 256, True) == ("ring", 2)      # 64 tiles, 32 stages
+    assert _gemm_kernel(L, 1, 128, 2048, 4096, 4, _lib.OZK_F16, 256, True) == ("ring", 4)
+    assert _gemm_kernel(L, 1, 128, 2048, 4096, 3, I8, 256, True) == ("ring", 2)
+    assert _gemm_kernel(L, 1, 128, 2048, 4096, 4, I8, 64, True) == ("ring", 1)       # 64 CUs
+    assert _gemm_kernel(L, 1, 128, 2048, 2048, 4, I8, 256, True) == ("ring", 1)      # 16 stages
+    assert _gemm_kernel(L, 1, 128, 2048, 8192, 4, I8, 256, True) == ("ring", 4)      # 64 stages
+    assert _gemm_kernel(L, 1, 1024, 1024, 65536, 3, I8, 256, True) == ("wide", 2)    # config 5
+    assert _gemm_kernel(L, 1, 8192, 8192, 8192, 4, I8, 256, True) == ("wide4", 1)    # config 3
+    assert _gemm_kernel(L, 16, 1024, 1024, 2048, 3, _lib.OZK_F16, 256, True) == ("wide", 1)
     # num_splits 5: the one-wave-per-SIMD kernel, in one launch, for int8 /
     # fp16 / bf16 slices; fp32 slices and 6 to 8 slices: the pair-split kernel
     assert _gemm_kernel(L, 1, 1024, 1024, 1024, 5, I8, 256) == "solo5"

@@ -170,7 +170,7 @@ def _planned(batch, M, N, K, L, sdt):
     from ozaki_triton_amd.ozaki import _TORCH_TO_OZK
     name = ctypes.c_char_p()
     _lib.check("ozk_debug_gemm_kernel", _lib.load().ozk_debug_gemm_kernel(
-        batch, M, N, K, L, _TORCH_TO_OZK[sdt], 0, ctypes.byref(name)))
+        batch, M, N, K, L, _TORCH_TO_OZK[sdt], 0, ctypes.byref(name), None))
     return name.value.decode()
 
 
@@ -525,6 +525,101 @@ def test_ozaki_matmul_five_splits(oracle, gpu, xdt, sdt):
         ref = A @ B
         rel = lambda C: float((C.cpu() - ref).norm() / ref.norm())
         assert rel(C5) < rel(C4)
+
+
+def _planned_ksplit(batch, M, N, K, L, sdt):
+    import ctypes
+    from ozaki_triton_amd import _lib
+    from ozaki_triton_amd.ozaki import _TORCH_TO_OZK
+    name, ks = ctypes.c_char_p(), ctypes.c_int(0)
+    _lib.check("ozk_debug_gemm_kernel", _lib.load().ozk_debug_gemm_kernel(
+        batch, M, N, K, L, _TORCH_TO_OZK[sdt], 0, ctypes.byref(name), ctypes.byref(ks)))
+    return name.value.decode(), ks.value
+
+
+@pytest.mark.parametrize("out", [torch.float64, torch.float32])
+@pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
+@pytest.mark.parametrize("kernel,L,ranges,MN,K", [
+    ("ring", 4, 2, (130, 72), 1040),    # int8: 9 stages of 128 bytes, ranges of 5 and 4
+    ("ring", 4, 4, (64, 64), 2064),     # 17 stages: 5, 5, 5, 2
+    ("ring", 3, 3, (65, 200), 520),     # 5 stages: 2, 2, 1
+    ("ring", 2, 2, (200, 136), 1040),   # 128 x 128 tiles
+    ("ring", 4, 8, (1, 300), 1040),     # 9 stages: 8 ranges asked, 5 of 2 stages run
+    ("wide", 3, 2, (130, 200), 1040),
+    ("wide", 3, 4, (64, 128), 4096),
+])
+def test_splitk_bitexact(oracle, gpu, sdt, out, kernel, L, ranges, MN, K, force):
+    """Split-K (ring and wide kernels): every tile's K cut into ranges, one
+    workgroup each; each range stores its raw accumulators, the last to
+    arrive adds all of them in range order and runs the ordered epilogue.
+    Forced range counts, ranges of unequal length, M and N cutting tiles,
+    batch 2 and both outer accumulators: int8 (exact int32 sums) and
+    integer-valued fp16 slices bit-exact against the oracle."""
+    import ozaki_triton_amd as ozk
+    M, N = MN
+    force(gemm=kernel, ksplit=ranges)
+    es = 1 if sdt == torch.int8 else 2
+    nkb = -(-K * es // 128)
+    per = -(-nkb // ranges)
+    assert _planned_ksplit(2, M, N, K, L, sdt) == (kernel, -(-nkb // per))
+    g = torch.Generator().manual_seed(K + 3 * M + N + L + ranges)
+    As, BsT, sa, sb = _slices_for(g, 2, L, M, N, K, sdt)
+    C = to_np(ozk.cross_gemm(As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu),
+                             L, out))
+    for b in range(2):
+        want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[b]), to_np(sa[b]), to_np(sb[b]),
+                                 NAME_OF[out])
+        assert_bitwise_equal(C[b], want, f"{kernel} ksplit {ranges} {sdt} {out} b{b}")
+
+
+def test_splitk_without_workspace_runs_unsplit(oracle, gpu, force):
+    """A call whose workspace lacks the split-K buffers (here: none at all)
+    runs the same kernel without split-K: same bits."""
+    import ctypes
+    import ozaki_triton_amd as ozk
+    from ozaki_triton_amd import _lib
+    L, M, N, K = 4, 64, 128, 2048
+    force(gemm="ring", ksplit=4)
+    g = torch.Generator().manual_seed(99)
+    As, BsT, sa, sb = _random_slices(g, 1, L, M, N, K, torch.int8)
+    Ad, Bd, sad, sbd = As.to(gpu), BsT.to(gpu), sa.to(gpu), sb.to(gpu)
+    C = torch.empty(1, M, N, dtype=torch.float64, device=gpu)
+    a_st = _lib.i64arr([L * M * K, M * K, K, 1])
+    b_st = _lib.i64arr([L * N * K, N * K, 1, K])
+    st = _lib.load().ozk_cross_gemm(
+        ctypes.c_void_p(Ad.data_ptr()), a_st, ctypes.c_void_p(Bd.data_ptr()), b_st,
+        ctypes.c_void_p(sad.data_ptr()), _lib.i64arr([L * M, M, 1]),
+        ctypes.c_void_p(sbd.data_ptr()), _lib.i64arr([L * N, N, 1]), 1, M, N, K, L,
+        _lib.OZK_I8, ctypes.c_void_p(C.data_ptr()), _lib.OZK_F64, _lib.i64arr([M * N, N, 1]),
+        ctypes.c_void_p(0), 0, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert st == 0, _lib.strerror(st)
+    torch.cuda.synchronize()
+    want = oracle.cross_gemm(to_np(As[0]), to_np(BsT[0]), to_np(sa[0]), to_np(sb[0]), "float64")
+    assert_bitwise_equal(to_np(C)[0], want, "no workspace")
+
+
+@pytest.mark.parametrize("xdt,sdt", [(torch.float64, torch.int8), (torch.float32, torch.float16),
+                                     (torch.float64, torch.float16)])
+@pytest.mark.parametrize("L", [3, 4])
+def test_splitk_reference_point(oracle, gpu, xdt, sdt, L):
+    """The reference's published point (1, 128, 2048, 4096)
+    (reference/test_results.csv): 64 tiles of 64 x 64 on 256 CUs, so the
+    planner cuts K into ranges of at least 16 stages (ring kernel): 2 for
+    int8 slices (32 stages), 4 for fp16 (64).  ozaki_matmul end to end,
+    sampled blocks against the oracle (int8 bit-exact, fp16 within the fp32
+    accumulation bound)."""
+    import ozaki_triton_amd as ozk
+    M, N, K = 128, 2048, 4096
+    kern, ks = _planned_ksplit(1, M, N, K, L, sdt)
+    assert kern == "ring"
+    if torch.cuda.get_device_properties(0).multi_processor_count >= 256:
+        assert ks == (2 if sdt == torch.int8 else 4)
+    A, B = c3_like((1, M, K), (1, K, N), seed=L + 17, dtype=xdt)
+    C = ozk.ozaki_matmul(A.to(gpu), B.to(gpu), L, sdt)
+    torch.cuda.synchronize()
+    rows, cols = sample_indices(M, 24, 1), sample_indices(N, 24, 2)
+    check_block_vs_oracle(oracle, ozk, to_np(C)[0], to_np(A)[0], to_np(B)[0], rows, cols, L, sdt,
+                          xdt, f"ref point L{L} {xdt} {sdt}")
 
 
 @pytest.mark.parametrize("out", [torch.float64, torch.float32, torch.float16, torch.bfloat16,
