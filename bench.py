@@ -78,7 +78,9 @@ def reference_shapes(reps: int = 30):
     test.py:104-109 (N(0,1), rows of A and columns of B scaled by 10^U(-2,2);
     seeded here); rel-err against a @ b in the input dtype (test.py:112-128);
     time as triton's do_bench takes it: the GPU time between events around
-    one call, after a cache flush, median over reps.  One JSON line per point,
+    one call, after a cache flush, median over reps; the same for the call
+    replayed from a HIP graph; and the wall-clock time per call of 100 calls
+    (and of 100 graph replays) issued back to back.  One JSON line per point,
     then a summary line.  The reference's figures come from its own NVIDIA
     GPU, so the ratio compares two machines, not two implementations."""
     import statistics
@@ -143,12 +145,25 @@ def reference_shapes(reps: int = 30):
             e1.synchronize()
             gts.append(e0.elapsed_time(e1))
         gms = statistics.median(gts)
+        # back to back, no flush, wall clock per call: what a caller issuing
+        # many small products sees, host costs (Python checks, the workspace,
+        # launches) included -- the cost graph replay removes
+        def per_call_ms(fn, n=100):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(n):
+                fn()
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) / n * 1e3
+        eager_b2b = per_call_ms(lambda: ozk.ozaki_matmul(a, b, num_splits=L, slice_dtype=sdt))
+        graph_b2b = per_call_ms(graph.replay)
         del graph, C_graph
         ratio = r["ozaki_ms"] / ms
         ratios.setdefault(r["scenario"], []).append(ratio)
         print(json.dumps({
             "shape_bmnk": r["shape_bmnk"], "scenario": r["scenario"], "num_splits": L,
             "ms": round(ms, 4), "graph_replay_ms": round(gms, 4),
+            "back_to_back_ms": round(eager_b2b, 4), "graph_back_to_back_ms": round(graph_b2b, 4),
             "graph_equals_eager": same,
             "emulated_tflops": round(2.0 * Bn * M * N * K / (ms * 1e-3) / 1e12, 3),
             "rel_err": rel, "reference_ms": round(r["ozaki_ms"], 4),
