@@ -541,6 +541,9 @@ def main():
         "split": {
             "kernels": {"A": planned_split_kernel(A, xdt, sdt, L, False),
                         "B": planned_split_kernel(B, xdt, sdt, L, True)},
+            # both splits in one launch (split_pair_kernel): the library then
+            # records the B phase's two events at one point, and ms_a covers both
+            "one_launch": t_split_b < 0.02,
             "bound": "hbm",
             "bytes": split_bytes,
             "achieved": round(split_gbs, 1),

@@ -471,25 +471,29 @@ int ozk_matmul(const void *A, const int64_t a_strides[3], const void *B,
     const int64_t asc[3] = {L * M, M, 1}, bsc[3] = {L * N, N, 1};
     int e;
     // split B through its transposed view, then A (ozaki_triton.py:588-599)
+    ozk::SplitParams pb = make_split_params(B, lay.bB, N, K, lay.bt_strides, L, lay.alpha,
+                                            ws + lay.b_sl, bsl, (float *)(ws + lay.b_sc), bsc);
+    const ozk::SplitPlan plan_b = ozk::plan_split(pb, dtype, slice_dtype);
+    ozk::SplitParams pa = make_split_params(A, lay.bA, M, K, a_strides, L, lay.alpha,
+                                            ws + lay.a_sl, asl, (float *)(ws + lay.a_sc), asc);
+    const ozk::SplitPlan plan_a = ozk::plan_split(pa, dtype, slice_dtype);
+    if (ozk::split_workspace_bytes(pb, plan_b, dtype, slice_dtype) > lay.scratch_bytes ||
+        ozk::split_workspace_bytes(pa, plan_a, dtype, slice_dtype) > lay.scratch_bytes)
+        return OZK_ERR_WORKSPACE;
+    pb.resid = pa.resid = (float *)(ws + lay.scratch);
     if ((e = record(events, 0, st)) != OZK_OK) return e;
-    {
-        ozk::SplitParams p = make_split_params(B, lay.bB, N, K, lay.bt_strides, L, lay.alpha,
-                                               ws + lay.b_sl, bsl, (float *)(ws + lay.b_sc), bsc);
-        const ozk::SplitPlan plan = ozk::plan_split(p, dtype, slice_dtype);
-        if (ozk::split_workspace_bytes(p, plan, dtype, slice_dtype) > lay.scratch_bytes)
-            return OZK_ERR_WORKSPACE;
-        p.resid = (float *)(ws + lay.scratch);
-        if (hipError_t he = ozk::launch_split(p, plan, dtype, slice_dtype, st)) return hip_status(he);
-    }
-    if ((e = record(events, 1, st)) != OZK_OK) return e;
-    {
-        ozk::SplitParams p = make_split_params(A, lay.bA, M, K, a_strides, L, lay.alpha,
-                                               ws + lay.a_sl, asl, (float *)(ws + lay.a_sc), asc);
-        const ozk::SplitPlan plan = ozk::plan_split(p, dtype, slice_dtype);
-        if (ozk::split_workspace_bytes(p, plan, dtype, slice_dtype) > lay.scratch_bytes)
-            return OZK_ERR_WORKSPACE;
-        p.resid = (float *)(ws + lay.scratch);
-        if (hipError_t he = ozk::launch_split(p, plan, dtype, slice_dtype, st)) return hip_status(he);
+    if (ozk::split_pair_ok(plan_a, plan_b, dtype)) {
+        // both in one launch; the second event marks the same point (the B
+        // phase then reads as empty, the A phase as both splits)
+        if ((e = record(events, 1, st)) != OZK_OK) return e;
+        if (hipError_t he = ozk::launch_split_pair(pa, plan_a, pb, plan_b, dtype, slice_dtype, st))
+            return hip_status(he);
+    } else {
+        if (hipError_t he = ozk::launch_split(pb, plan_b, dtype, slice_dtype, st))
+            return hip_status(he);
+        if ((e = record(events, 1, st)) != OZK_OK) return e;
+        if (hipError_t he = ozk::launch_split(pa, plan_a, dtype, slice_dtype, st))
+            return hip_status(he);
     }
     if ((e = record(events, 2, st)) != OZK_OK) return e;
     // cross-GEMM over the K-contiguous slices

@@ -75,6 +75,14 @@ size_t split_workspace_bytes(const SplitParams &p, const SplitPlan &plan, int x_
                              int slice_dtype);
 hipError_t launch_split(const SplitParams &p, const SplitPlan &plan, int x_dtype,
                         int slice_dtype, hipStream_t stream);
+// Both splits of a matmul in one launch (split_pair_kernel): A's rows by a
+// 4-wave row configuration and B's columns by the cooperative kernel, fp64
+// input, no split kernel forced by the test hooks.  pb.resid holds B's
+// exchange words (A needs no scratch).
+bool split_pair_ok(const SplitPlan &plan_a, const SplitPlan &plan_b, int x_dtype);
+hipError_t launch_split_pair(const SplitParams &pa, const SplitPlan &plan_a, const SplitParams &pb,
+                             const SplitPlan &plan_b, int x_dtype, int slice_dtype,
+                             hipStream_t stream);
 
 // Sticky device status (per device): bit 0 is set when a cooperative split
 // wait gave up (the split's scales are then NaN).  read_device_status waits

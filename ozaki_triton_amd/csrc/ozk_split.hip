@@ -297,17 +297,18 @@ OZK_DEV float row_max(float m, float (*red)[RPB][GW], int buf, int grp, int t) {
     return m;
 }
 
+// The body of the row kernel for row block `block` (its workgroup, or a
+// workgroup of split_pair_kernel); red: LDS for the row maxima.
 template <typename XT, typename ST, int GW, int RPB, int NC>
-__global__ __launch_bounds__(64 * GW * RPB) void split_rows_kernel(SplitParams p) {
+OZK_DEV void split_rows_body(const SplitParams &p, int64_t block, float (*red)[RPB][GW]) {
     constexpr int G = 64 * GW;
     constexpr int NE = 4 * NC;
-    __shared__ float red[2][RPB][GW];
 
     const int tid = threadIdx.x;
     const int grp = tid / G;
     const int t = tid % G;
     const int64_t nrows = p.batch * p.rows;
-    const int64_t grow = (int64_t)blockIdx.x * RPB + grp;
+    const int64_t grow = block * RPB + grp;
     const bool active = grow < nrows;
     const int64_t b = active ? grow / p.rows : 0;
     const int64_t r = active ? grow % p.rows : 0;
@@ -365,6 +366,12 @@ __global__ __launch_bounds__(64 * GW * RPB) void split_rows_kernel(SplitParams p
             if (active && e0 < p.K) Store4<ST>::run(p.slices, srow + l * p.ss_l + e0, qv);
         }
     }
+}
+
+template <typename XT, typename ST, int GW, int RPB, int NC>
+__global__ __launch_bounds__(64 * GW * RPB) void split_rows_kernel(SplitParams p) {
+    __shared__ float red[2][RPB][GW];
+    split_rows_body<XT, ST, GW, RPB, NC>(p, blockIdx.x, red);
 }
 
 // ---------------------------------------------------------------------------
@@ -522,13 +529,16 @@ __global__ __launch_bounds__(NT) void split_strip_kernel(SplitParams p) {
 // bytes read; reads of 128-byte row segments run at copy speed.  A strip of
 // SW = 128 / sizeof(XT) columns over all of K does not fit one CU, so it is
 // cut along K into P chunks of CH rows, one workgroup each, and the level
-// maxima are combined through global memory:
+// maxima are combined through global memory.  A column group is SEG 16-byte
+// pieces of each row: 128 bytes (SEG = 8), or 32 bytes (SEG = 2, when forced)
+// for columns too long for 32 chunks of those, whose chunks then hold 4x the
+// rows with the same registers (65536-long fp32 columns: 32 chunks of 2048):
 //   * workgroup g = blockIdx.x is member g % P of column group g / P (batch
-//     b, columns col0 .. col0 + SW); lane t covers the VEC columns
-//     col0 + VEC * (t % 8) + {0..VEC-1} and the rows
-//     member * CH + 4 * (t / 8 + RPP * j) + {0..3}, j < RPL / 4, so a wave
-//     load covers eight full 128-byte row segments and a lane holds 4
-//     consecutive k of each column (4- / 8-byte slice stores along K);
+//     b, columns col0 .. col0 + SW, SW = SEG * VEC); lane t covers the VEC
+//     columns col0 + VEC * (t % SEG) + {0..VEC-1} and the rows
+//     member * CH + 4 * (t / SEG + RPP * j) + {0..3}, j < RPL / 4, RPP = 256 /
+//     SEG, so a wave load covers 64 / SEG whole row segments and a lane holds
+//     4 consecutive k of each column (4- / 8-byte slice stores along K);
 //   * per level, wave 0 stores the workgroup's column maxima into
 //     slot[group][level][member][SW], one 64-bit word each (the tag 1 in the
 //     high half, the fp32 maximum in the low half), with agent-scope stores,
@@ -538,7 +548,7 @@ __global__ __launch_bounds__(NT) void split_strip_kernel(SplitParams p) {
 //   * the members of a group are consecutive workgroup ids.  Workgroups are
 //     dispatched in id order, so the group of the oldest resident workgroup
 //     is entirely resident once P + 8 is below the workgroups that fit an
-//     XCD; the planner keeps P <= 64.  A wait is still bounded (2 s of the
+//     XCD (two or three per CU: 64 or more); the planner keeps P <= 32.  A wait is still bounded (2 s of the
 //     100 MHz real-time counter): a member that gives up sets the launch's
 //     status word, member 0 stores NaN scales, and the poison kernel that
 //     follows the launch makes every scale of the split NaN and records the
@@ -583,23 +593,32 @@ __global__ __launch_bounds__(256) void poison_scales_kernel(const uint32_t *stat
         __hip_atomic_fetch_or(&g_device_status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-template <typename XT, typename ST, int RPL>
-__global__ __launch_bounds__(kCoopNT) void split_coop_kernel(SplitParams p, uint64_t *slot, int P,
-                                                             uint32_t want_tag,
-                                                             uint64_t tick_limit,
-                                                             uint32_t *status) {
+// LDS of one cooperative column workgroup
+template <typename XT, int SEG> struct CoopShared {
+    static constexpr int VEC = 16 / (int)sizeof(XT);
+    float red[kCoopNT / 64][SEG][VEC];
+    float fin[SEG * VEC];
+    int bad;
+};
+
+// The body of the cooperative column kernel for logical workgroup g (member
+// g % P of column group g / P): its own workgroup, or one of split_pair_kernel.
+template <typename XT, typename ST, int RPL, int SEG>
+OZK_DEV void split_coop_body(const SplitParams &p, uint64_t *slot, int P, uint32_t want_tag,
+                             uint64_t tick_limit, uint32_t *status, int64_t g,
+                             CoopShared<XT, SEG> &sh) {
     constexpr int NT = kCoopNT, NG = RPL / 4;
     constexpr int VEC = 16 / (int)sizeof(XT);
-    constexpr int SW = 8 * VEC;          // columns per group
-    constexpr int RPP = NT / 8;          // row quads per pass
+    constexpr int SW = SEG * VEC;        // columns per group
+    constexpr int RPP = NT / SEG;        // row quads per pass
     constexpr int NW = NT / 64;
-    __shared__ float red[NW][8][VEC];
-    __shared__ float fin[SW];
-    __shared__ int bad;
+    static_assert(SEG == 8 || SEG == 2, "128- or 32-byte row segments");
+    auto &red = sh.red;
+    auto &fin = sh.fin;
+    int &bad = sh.bad;
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int seg = t & 7, ro = t >> 3;
-    const int64_t g = blockIdx.x;
+    const int seg = t % SEG, ro = t / SEG;
     const int member = (int)(g % P);
     const int64_t grp = g / P;
     const int64_t nstr = (p.rows + SW - 1) / SW;
@@ -632,12 +651,10 @@ __global__ __launch_bounds__(kCoopNT) void split_coop_kernel(SplitParams p, uint
     // maximum over the group of the lane maxima m (fl32 values >= 0), per column
     auto group_max = [&](float m[VEC], int l) {
 #pragma unroll
-        for (int u = 0; u < VEC; ++u) {
-            m[u] = fmaxf(m[u], __shfl_xor(m[u], 8));
-            m[u] = fmaxf(m[u], __shfl_xor(m[u], 16));
-            m[u] = fmaxf(m[u], __shfl_xor(m[u], 32));
-        }
-        if (lane < 8) {
+        for (int u = 0; u < VEC; ++u)
+#pragma unroll
+            for (int x = SEG; x < 64; x *= 2) m[u] = fmaxf(m[u], __shfl_xor(m[u], x));
+        if (lane < SEG) {
 #pragma unroll
             for (int u = 0; u < VEC; ++u) red[wave][lane][u] = m[u];
         }
@@ -775,6 +792,45 @@ __global__ __launch_bounds__(kCoopNT) void split_coop_kernel(SplitParams p, uint
                     Store4<ST>::run(p.slices, sbase + l * p.ss_l + u * p.ss_r + k0, qv[u]);
             }
         }
+    }
+}
+
+template <typename XT, typename ST, int RPL, int SEG>
+__global__ __launch_bounds__(kCoopNT) void split_coop_kernel(SplitParams p, uint64_t *slot, int P,
+                                                             uint32_t want_tag,
+                                                             uint64_t tick_limit,
+                                                             uint32_t *status) {
+    __shared__ CoopShared<XT, SEG> sh;
+    split_coop_body<XT, ST, RPL, SEG>(p, slot, P, want_tag, tick_limit, status, blockIdx.x, sh);
+}
+
+// ---------------------------------------------------------------------------
+// Both splits of a matmul in one launch, where A's rows take a 256-lane row
+// configuration (4 waves per row) and B's columns the cooperative column
+// kernel with 128-byte groups (fp64 operands, 4096 <= K <= 8192: config 3).
+// The grid runs in periods of P + KA workgroups: the P members of one
+// column group of B, then KA row blocks of A.  The row blocks never wait, so
+// they keep CUs busy while column groups wait on their exchanges, and the
+// two splits cost one launch.  The members of a group stay consecutive
+// workgroup ids, which the cooperative kernel's residency argument needs
+// (row blocks between groups retire without waiting).
+// ---------------------------------------------------------------------------
+template <typename XT, typename ST, int RPL, int NC>
+__global__ __launch_bounds__(kCoopNT) void split_pair_kernel(SplitParams pb, uint64_t *slot, int P,
+                                                             uint32_t want_tag,
+                                                             uint64_t tick_limit,
+                                                             uint32_t *status, SplitParams pa,
+                                                             int ka) {
+    __shared__ CoopShared<XT, 8> sh;
+    __shared__ float red[2][1][4];
+    const int64_t period = (int64_t)P + ka;
+    const int64_t q = blockIdx.x / period;
+    const int pos = (int)(blockIdx.x % period);
+    if (pos < P) {
+        split_coop_body<XT, ST, RPL, 8>(pb, slot, P, want_tag, tick_limit, status, q * P + pos, sh);
+    } else {
+        const int64_t ab = q * ka + (pos - P);
+        if (ab < pa.batch * pa.rows) split_rows_body<XT, ST, 4, 1, NC>(pa, ab, red);
     }
 }
 
@@ -1089,14 +1145,15 @@ static const int kNumStripCfgs = sizeof(kStripCfgs) / sizeof(kStripCfgs[0]);
 // 16 of fp32), the members (K chunks of 32 * rpl rows) of a column group, and
 // the workspace: the published maxima [groups][L][P][SW], 8 bytes each (none
 // for P = 1)
-static int64_t coop_members(int64_t K, int rpl) {
-    const int64_t ch = (int64_t)kCoopNT / 8 * rpl;
+static int coop_rpl(int xsz) { return 64 / (16 / xsz); }
+static int64_t coop_members(int64_t K, int xsz, int seg) {
+    const int64_t ch = (int64_t)kCoopNT / seg * coop_rpl(xsz);
     return K <= 0 ? 1 : (K + ch - 1) / ch;
 }
-static int64_t coop_slots(const SplitParams &p, int xsz, int rpl) {
-    const int64_t P = coop_members(p.K, rpl);
+static int64_t coop_slots(const SplitParams &p, int xsz, int seg) {
+    const int64_t P = coop_members(p.K, xsz, seg);
     if (P <= 1) return 0;
-    const int64_t sw = 8 * (16 / xsz);
+    const int64_t sw = seg * (16 / xsz);
     const int64_t groups = p.batch * ((p.rows + sw - 1) / sw);
     return groups * p.L * P * sw;
 }
@@ -1178,12 +1235,20 @@ static SplitPlan plan_split_raw(const SplitParams &p, int x_dtype, int slice_dty
     // the strip kernel's time at K = 4096, N = 2048..8192; 1.04x at N = 1024;
     // fp16 slices gain nothing there, fp32 columns below 64 KB lose 1.1-1.3x);
     // a forced coop takes it for any length it holds
-    const bool coop_fits = cols_ok && coop_members(p.K, 64 / vec) <= kCoopMaxP;
+    const bool coop_fits = cols_ok && coop_members(p.K, xsz, 8) <= kCoopMaxP;
+    // columns too long for 32 chunks of 128-byte groups: 32-byte groups, whose
+    // chunks hold 4x the rows, when the cooperative kernel is forced.  By
+    // default such columns are transposed instead: at config 5 (fp32, K =
+    // 65536, 32 chunks of 2048 rows) the 32-byte groups took 0.255-0.265 ms
+    // against 0.216 ms for the transpose path, the exchange waiting on 32
+    // members per group.
+    const bool coop2_fits = cols_ok && !coop_fits && coop_members(p.K, xsz, 2) <= kCoopMaxP;
     const bool other = forced(kForceSplitStrip) || forced(kForceSplitTranspose) || forced(kForceSplitGeneric);
     const bool coop_long = p.K * xsz >= kCoopMinColumnBytes ||
                            (xsz == 8 && ssz == 1 && p.K * xsz >= kCoopMinColumnBytes / 2 &&
                             p.batch * p.rows >= 2048);
-    if (coop_fits && (forced(kForceSplitCoop) || (!other && coop_long))) return {kSplitCoop, 64 / vec};
+    if (coop_fits && (forced(kForceSplitCoop) || (!other && coop_long))) return {kSplitCoop, 8};
+    if (coop2_fits && forced(kForceSplitCoop)) return {kSplitCoop, 2};
     if (cols_ok && !forced(kForceSplitTranspose) && !forced(kForceSplitGeneric)) {
         for (int i = 0; i < kNumStripCfgs; ++i) {
             const StripCfg &c = kStripCfgs[i];
@@ -1356,13 +1421,13 @@ static hipError_t launch_typed(const SplitParams &p, const SplitPlan &plan, hipS
     case kSplitRows: return launch_rows<XT, ST>(p, plan.variant, st, (uint64_t *)p.resid);
     case kSplitStrip: return launch_strip<XT, ST>(p, plan.variant, st);
     case kSplitCoop: {
-        constexpr int SW = 8 * (16 / (int)sizeof(XT));
-        const int rpl = plan.variant;
-        const int64_t groups = p.batch * ((p.rows + SW - 1) / SW);
-        const int64_t P = coop_members(p.K, rpl);
+        const int seg = plan.variant;   // 16-byte pieces per row of a column group
+        const int64_t sw = seg * (16 / (int)sizeof(XT));
+        const int64_t groups = p.batch * ((p.rows + sw - 1) / sw);
+        const int64_t P = coop_members(p.K, (int)sizeof(XT), seg);
         uint64_t *slot = nullptr;
         uint32_t *status = nullptr;
-        const int64_t n = coop_slots(p, (int)sizeof(XT), rpl);
+        const int64_t n = coop_slots(p, (int)sizeof(XT), seg);
         if (P > 1) {
             slot = (uint64_t *)p.resid;
             if (hipError_t e = clear_slots(slot, n, st)) return e;
@@ -1370,10 +1435,15 @@ static hipError_t launch_typed(const SplitParams &p, const SplitPlan &plan, hipS
         }
         const dim3 grid((unsigned)(groups * P)), block(kCoopNT);
         constexpr int RPL = 64 / (16 / (int)sizeof(XT));
-        if (rpl != RPL) return hipErrorInvalidValue;
         const WaitRule w = wait_rule();
-        hipLaunchKernelGGL((split_coop_kernel<XT, ST, RPL>), grid, block, 0, st, p, slot, (int)P,
-                           w.tag, w.ticks, status);
+        if (seg == 8)
+            hipLaunchKernelGGL((split_coop_kernel<XT, ST, RPL, 8>), grid, block, 0, st, p, slot,
+                               (int)P, w.tag, w.ticks, status);
+        else if (seg == 2)
+            hipLaunchKernelGGL((split_coop_kernel<XT, ST, RPL, 2>), grid, block, 0, st, p, slot,
+                               (int)P, w.tag, w.ticks, status);
+        else
+            return hipErrorInvalidValue;
         if (hipError_t e = hipGetLastError()) return e;
         return P > 1 ? launch_poison(p, slot + n, st) : hipSuccess;
     }
@@ -1444,6 +1514,61 @@ hipError_t launch_split(const SplitParams &p, const SplitPlan &plan, int x_dtype
     case 2: return launch_slice<_Float16>(p, plan, x_dtype, slice_dtype, st);
     case 3: return launch_slice<__bf16>(p, plan, x_dtype, slice_dtype, st);
     case 1: return launch_slice<float>(p, plan, x_dtype, slice_dtype, st);
+    }
+    return hipErrorInvalidValue;
+}
+
+// split_pair_kernel's row configurations: variants 4 and 5 of kRowCfgs (4
+// waves per row, K <= 4096 / 8192)
+static int pair_nc(const SplitPlan &a) {
+    return a.path == kSplitRows ? (a.variant == 4 ? 4 : a.variant == 5 ? 8 : 0) : 0;
+}
+
+bool split_pair_ok(const SplitPlan &plan_a, const SplitPlan &plan_b, int x_dtype) {
+    return x_dtype == 0 && pair_nc(plan_a) != 0 && plan_b.path == kSplitCoop &&
+           plan_b.variant == 8 && debug_overrides().split == kForceSplitNone;
+}
+
+template <typename ST>
+static hipError_t launch_pair_typed(const SplitParams &pa, const SplitPlan &plan_a,
+                                    const SplitParams &pb, hipStream_t st) {
+    using XT = double;
+    constexpr int RPL = 64 / (16 / (int)sizeof(XT));
+    const int64_t sw = 8 * (16 / (int)sizeof(XT));
+    const int64_t groups = pb.batch * ((pb.rows + sw - 1) / sw);
+    const int64_t P = coop_members(pb.K, (int)sizeof(XT), 8);
+    const int64_t n = coop_slots(pb, (int)sizeof(XT), 8);
+    uint64_t *slot = nullptr;
+    uint32_t *status = nullptr;
+    if (P > 1) {
+        slot = (uint64_t *)pb.resid;
+        if (hipError_t e = clear_slots(slot, n, st)) return e;
+        status = (uint32_t *)(slot + n);
+    }
+    const int64_t na = pa.batch * pa.rows;
+    const int64_t ka = groups > 0 ? (na + groups - 1) / groups : 0;
+    const dim3 grid((unsigned)(groups * (P + ka))), block(kCoopNT);
+    const WaitRule w = wait_rule();
+    if (pair_nc(plan_a) == 4)
+        hipLaunchKernelGGL((split_pair_kernel<XT, ST, RPL, 4>), grid, block, 0, st, pb, slot,
+                           (int)P, w.tag, w.ticks, status, pa, (int)ka);
+    else
+        hipLaunchKernelGGL((split_pair_kernel<XT, ST, RPL, 8>), grid, block, 0, st, pb, slot,
+                           (int)P, w.tag, w.ticks, status, pa, (int)ka);
+    if (hipError_t e = hipGetLastError()) return e;
+    return P > 1 ? launch_poison(pb, slot + n, st) : hipSuccess;
+}
+
+hipError_t launch_split_pair(const SplitParams &pa, const SplitPlan &plan_a,
+                             const SplitParams &pb, const SplitPlan &plan_b, int x_dtype,
+                             int slice_dtype, hipStream_t st) {
+    if (!split_pair_ok(plan_a, plan_b, x_dtype)) return hipErrorInvalidValue;
+    if (pa.batch * pa.rows == 0 || pb.batch * pb.rows == 0 || pa.L == 0) return hipSuccess;
+    switch (slice_dtype) {
+    case 4: return launch_pair_typed<int8_t>(pa, plan_a, pb, st);
+    case 2: return launch_pair_typed<_Float16>(pa, plan_a, pb, st);
+    case 3: return launch_pair_typed<__bf16>(pa, plan_a, pb, st);
+    case 1: return launch_pair_typed<float>(pa, plan_a, pb, st);
     }
     return hipErrorInvalidValue;
 }

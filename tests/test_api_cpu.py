@@ -153,11 +153,11 @@ def test_split_workspace_per_path():
     assert L.ozk_split_workspace_bytes(_lib.OZK_F32, 1, N, Ks, _lib.i64arr([Ks * N, 1, N]), 2,
                                        _lib.OZK_F16, sls, ctypes.byref(nb)) == 0
     assert nb.value == 0
-    # a column longer than the cooperative column kernel takes is transposed
-    # into the workspace first (config 5: fp32, K = 65536); its rows, longer
-    # than 16384, then go to the row kernel shared by 4 workgroups per row,
-    # whose exchange words follow the transposed copy: 1024 rows x 3 levels x
-    # 4 chunks x 8 bytes, and a status word
+    # a column longer than the cooperative column kernel's 128-byte groups
+    # take is transposed into the workspace first (config 5: fp32, K = 65536);
+    # its rows, longer than 16384, then go to the row kernel shared by 4
+    # workgroups per row, whose exchange words follow the transposed copy:
+    # 1024 rows x 3 levels x 4 chunks x 8 bytes, and a status word
     K5, N5 = 65536, 1024
     sl5 = _lib.i64arr([3 * N5 * K5, N5 * K5, K5, 1])
     assert L.ozk_split_workspace_bytes(_lib.OZK_F32, 1, N5, K5, _lib.i64arr([K5 * N5, 1, N5]),

@@ -92,10 +92,10 @@ def test_split_strip_path(oracle, gpu, xdt, sdt, L, N, K, kernel, force):
                                          (3, 48, 4100, 2), (1, 256, 8192, 4), (2, 128, 2048, 3)])
 def test_split_coop_groups(oracle, gpu, xdt, sdt, batch, N, K, L, force):
     """The cooperative column split (forced; the default from 64 KB columns)
-    at full length: up to 32 workgroups per column group (its limit: fp64 at
-    K = 32768, fp32 at K = 16384; fp32 at K = 32768 falls to the transpose
-    path), a ragged last group and a ragged last K chunk, batched operands,
-    per-column exponents and outliers."""
+    at full length: up to 32 workgroups per column group of 128-byte row
+    segments (fp64 to K = 32768, fp32 to K = 16384; fp32 at K = 32768 takes
+    32-byte groups), a ragged last group and a ragged last K chunk, batched
+    operands, per-column exponents and outliers."""
     import ozaki_triton_amd as ozk
     force(split="coop")
     g = torch.Generator().manual_seed(batch * N * K + L)
@@ -105,6 +105,75 @@ def test_split_coop_groups(oracle, gpu, xdt, sdt, batch, N, K, L, force):
     B[:, :, 5] = 0.0                                   # a zero column
     Bd = B.to(xdt).to(gpu)
     _check_split(oracle, ozk, Bd.transpose(-1, -2), L, sdt, f"coop {xdt} {sdt} b{batch} {N}x{K}")
+
+
+@pytest.mark.parametrize("xdt,sdt", COMBOS)
+@pytest.mark.parametrize("batch,N,K,L", [(1, 40, 65536, 3), (2, 24, 40000, 2), (1, 12, 65500, 4)])
+def test_split_coop_long_columns(oracle, gpu, xdt, sdt, batch, N, K, L, force):
+    """Columns too long for 32 chunks of 128-byte groups (config 5's B: fp32,
+    K = 65536), with the cooperative kernel forced, take its 32-byte groups,
+    whose chunks hold 4x the rows (2048 fp32 / 4096 fp64): ragged groups and
+    K chunks, batched operands, outliers; bit-exact against the oracle.  (The
+    planner sends such columns to the transpose path, which is faster.)"""
+    import ctypes
+    import ozaki_triton_amd as ozk
+    from ozaki_triton_amd import _lib
+    from ozaki_triton_amd.ozaki import _TORCH_TO_OZK
+    force(split="coop")
+    g = torch.Generator().manual_seed(batch * N * K + L)
+    B = torch.randn(batch, K, N, generator=g, dtype=torch.float64)
+    B = B * torch.pow(2.0, torch.randint(-8, 9, (batch, 1, N), generator=g).double())
+    B[torch.rand(batch, K, N, generator=g) < 0.001] *= 1e4
+    Bd = B.to(xdt).to(gpu)
+    X = Bd.transpose(-1, -2)
+    name, nb = ctypes.c_char_p(), ctypes.c_size_t(0)
+    sl_st = _lib.i64arr([L * N * K, N * K, K, 1])
+    _lib.check("ozk_debug_split_kernel", _lib.load().ozk_debug_split_kernel(
+        ctypes.c_void_p(X.data_ptr()), _TORCH_TO_OZK[xdt], batch, N, K,
+        _lib.i64arr([X.stride(0), X.stride(1), X.stride(2)]), L, _TORCH_TO_OZK[sdt],
+        ctypes.c_void_p(256), sl_st, ctypes.byref(name), ctypes.byref(nb)))
+    assert name.value == b"coop", name.value
+    _check_split(oracle, ozk, X, L, sdt, f"coop32 {xdt} {sdt} b{batch} {N}x{K}")
+
+
+@pytest.mark.parametrize("sdt", [torch.int8, torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("a_shape,b_shape", [((200, 8192), (8192, 2100)),
+                                             ((64, 4096), (4096, 2048)),
+                                             ((2, 96, 8192), (8192, 136))])
+def test_split_pair_one_launch(oracle, gpu, sdt, a_shape, b_shape, force):
+    """ozaki_matmul's two splits in one launch (split_pair_kernel: fp64
+    input, A's rows by the 4-wave row configuration, B's columns by the
+    cooperative kernel; A's row blocks interleaved between B's column
+    groups): the library records the B phase's two events at one point; C
+    equals the two-launch pipeline's (a forced split kernel turns the single
+    launch off) bit for bit, and the oracle's on sampled blocks (int8
+    bit-exact, float slices within the fp32 accumulation bound)."""
+    import ozaki_triton_amd as ozk
+    from ozaki_triton_amd.ozaki import _ozaki_matmul_impl
+    A, B = c3_like(a_shape, b_shape, seed=sum(a_shape) + sum(b_shape))
+    Ad, Bd = A.to(gpu), B.to(gpu)
+    L = 3
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    for e in evs:
+        e.record()
+    C1 = _ozaki_matmul_impl(Ad, Bd, L, sdt, False, evs)
+    torch.cuda.synchronize()
+    if b_shape == (8192, 2100):
+        # B's columns (64 KB each) take the cooperative kernel; split alone they
+        # take tens of microseconds, back-to-back events a few
+        assert evs[0].elapsed_time(evs[1]) < 0.02, "two launches where one was expected"
+    force(split="coop")
+    C2 = ozk.ozaki_matmul(Ad, Bd, L, sdt)
+    torch.cuda.synchronize()
+    assert_bitwise_equal(to_np(C1), to_np(C2), f"one launch vs two {sdt} {a_shape}")
+    C_np, A_np, B_np = to_np(C1), to_np(A), to_np(B)
+    M, N = a_shape[-2], b_shape[-1]
+    rows, cols = sample_indices(M, 24, 3), sample_indices(N, 24, 4)
+    for b in range(C_np.shape[0] if C_np.ndim == 3 else 1):
+        Cb = C_np[b] if C_np.ndim == 3 else C_np
+        Ab = A_np[b] if A_np.ndim == 3 else A_np
+        check_block_vs_oracle(oracle, ozk, Cb, Ab, B_np, rows, cols, L, sdt, torch.float64,
+                              f"pair {sdt} {a_shape} b{b}")
 
 
 @pytest.mark.parametrize("xdt,sdt", COMBOS)
