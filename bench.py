@@ -339,6 +339,35 @@ def vendor_probes():
             res[name + "_TOPs"] = round(2.0 * m * m * K * L * L / (ms * 1e-3) / 1e12, 1)
         out[f"cross_gemm_L{L}"] = res
         del a_sl, b_sl, kinds
+    del A, B
+    # the same for fp16: the vendor fp16 GEMM at 8192^3, and the library's
+    # fp16-slice cross-GEMM at C2's and C4's shapes (uniform random slices of
+    # C2's value range against zeros)
+    a16 = torch.randn(m, m, device=dev, generator=g).half()
+    ms = time_ms(lambda: a16 @ a16.t(), 5)
+    out["matmul_f16_8192_TFLOPs"] = round(2.0 * m ** 3 / (ms * 1e-3) / 1e12, 1)
+    z16 = torch.zeros_like(a16)
+    ms = time_ms(lambda: z16 @ z16.t(), 5)
+    out["matmul_f16_zeros_TFLOPs"] = round(2.0 * m ** 3 / (ms * 1e-3) / 1e12, 1)
+    del a16, z16
+    for name, (L, bt, M, N, K) in (("C2", (2, 1, 4096, 4096, 4096)),
+                                   ("C4", (3, 16, 1024, 1024, 2048))):
+        res = {"kernel": planned_gemm_kernel(bt, M, N, K, L, "float16")}
+        sa = torch.ones(bt, L, M, device=dev)
+        sb = torch.ones(bt, L, N, device=dev)
+        for kind in ("uniform_random", "zeros"):
+            if kind == "zeros":
+                xa = torch.zeros(bt, L, M, K, device=dev, dtype=torch.float16)
+                xb = torch.zeros(bt, L, N, K, device=dev, dtype=torch.float16)
+            else:
+                xa = (torch.rand(bt, L, M, K, device=dev, generator=g) * 2 - 1).half()
+                xb = (torch.rand(bt, L, N, K, device=dev, generator=g) * 2 - 1).half()
+            ms = time_ms(lambda: ozk.cross_gemm(xa, xb.transpose(-1, -2), sa, sb, L,
+                                                torch.float64), 5)
+            res[kind + "_ms"] = round(ms, 4)
+            res[kind + "_TFLOPs"] = round(2.0 * bt * M * N * K * L * L / (ms * 1e-3) / 1e12, 1)
+            del xa, xb
+        out[f"cross_gemm_f16_{name}"] = res
     print(json.dumps(out), flush=True)
 
 
@@ -369,9 +398,10 @@ def main():
                          "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--vendor-probes", action="store_true",
                     help="only time the calibration probes of the rooflines: torch's device "
-                         "copy of 1 GiB (practical HBM rate), torch._int_mm (hipBLASLt int8 "
-                         "GEMM) at 8192^3 on random and zero operands, and the library's "
-                         "cross-GEMM at C3's size on C3's, random and zero slices")
+                         "copy of 1 GiB (practical HBM rate), the vendor int8 and fp16 GEMMs "
+                         "at 8192^3 on random and zero operands, and the library's cross-GEMM "
+                         "at C3's size (int8) and C2's and C4's (fp16) on random and zero "
+                         "slices")
     ap.add_argument("--reference-shapes", action="store_true",
                     help="only time ozaki_matmul at the reference's published points "
                          "(test_results.csv: 4 shapes x 4 dtype scenarios x num_splits 1-4)")
