@@ -2096,6 +2096,17 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_solo5_kernel(GemmParams p, 
     for (int u = 0; u < L; ++u)
 #pragma unroll
         for (int j = 0; j < L; ++j) acc[u][j] = MF::zero();
+    // The MFMAs below are inline assembly, which the compiler's hazard
+    // recogniser does not see into: the zeroed accumulators are pinned in
+    // their register files here, before the prologue, and 8 wait states
+    // separate those writes from any MFMA that reads them.
+    static_for<L * L>([&](auto n_) {
+        constexpr int n = decltype(n_)::value;
+        (void)acc;   // an ordinary use, so that the capture does not hinge on the asm operands
+        if constexpr (n < Sh::NAGPR) asm volatile("" : "+a"(acc[n / L][n % L]));
+        else asm volatile("" : "+v"(acc[n / L][n % L]));
+    });
+    asm volatile("s_nop 7" ::: "memory");
 
     // prologue: stages 0 and 1; stage 0 must land before the first reads
 #pragma unroll
