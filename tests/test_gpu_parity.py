@@ -641,6 +641,26 @@ def test_splitk_bitexact(oracle, gpu, sdt, out, kernel, L, ranges, MN, K, force)
         assert_bitwise_equal(C[b], want, f"{kernel} ksplit {ranges} {sdt} {out} b{b}")
 
 
+@pytest.mark.parametrize("sdt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("kernel,L,ranges,MN,K", [("ring", 4, 3, (100, 72), 1040),
+                                                 ("wide", 3, 2, (130, 200), 1040)])
+def test_splitk_other_slice_dtypes(oracle, gpu, sdt, kernel, L, ranges, MN, K, force):
+    """Split-K with bf16 and fp32 slices (fp32: four MFMAs per fragment),
+    integer-valued so that the fp32 sums are exact: bit-exact against the
+    oracle."""
+    import ozaki_triton_amd as ozk
+    M, N = MN
+    force(gemm=kernel, ksplit=ranges)
+    g = torch.Generator().manual_seed(K + M + N + ranges)
+    As, BsT, sa, sb = int_valued_slices(g, 2, L, M, N, K, sdt)
+    C = to_np(ozk.cross_gemm(As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu),
+                             L, torch.float64))
+    for b in range(2):
+        want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[b]), to_np(sa[b]), to_np(sb[b]),
+                                 "float64")
+        assert_bitwise_equal(C[b], want, f"{kernel} ksplit {ranges} {sdt} b{b}")
+
+
 def test_splitk_without_workspace_runs_unsplit(oracle, gpu, force):
     """A call whose workspace lacks the split-K buffers (here: none at all)
     runs the same kernel without split-K: same bits."""
