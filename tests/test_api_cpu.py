@@ -550,6 +550,9 @@ def test_planner_kernel_choice():
     assert _gemm_kernel(L, 1, 128, 2048, 4096, 4, I8, 64, True) == ("ring", 1)       # 64 CUs
     assert _gemm_kernel(L, 1, 128, 2048, 2048, 4, I8, 256, True) == ("ring", 1)      # 16 stages
     assert _gemm_kernel(L, 1, 128, 2048, 8192, 4, I8, 256, True) == ("ring", 4)      # 64 stages
+    # the K = 8192 shape of test_ozaki_matmul_graph_capture (split-K replayed)
+    assert _gemm_kernel(L, 1, 64, 96, 8192, 3, I8, 256, True) == ("ring", 4)
+    assert _gemm_kernel(L, 1, 64, 96, 8192, 3, _lib.OZK_F16, 256, True) == ("ring", 4)
     assert _gemm_kernel(L, 1, 1024, 1024, 65536, 3, I8, 256, True) == ("wide", 2)    # config 5
     assert _gemm_kernel(L, 1, 8192, 8192, 8192, 4, I8, 256, True) == ("wide4", 1)    # config 3
     assert _gemm_kernel(L, 16, 1024, 1024, 2048, 3, _lib.OZK_F16, 256, True) == ("wide", 1)

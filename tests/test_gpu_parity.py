@@ -995,8 +995,9 @@ def test_ozaki_matmul_graph_capture(oracle, gpu, sdt, sa, sb):
     with eager work and synchronisations between replays and the inputs
     changed in place, equals the oracle bit for bit (inputs for which the fp16
     path is exact too) and the eager call.  At K = 8192 the B split is the
-    cooperative kernel, whose exchange words a fill kernel clears on every
-    replay."""
+    cooperative kernel and the cross-GEMM runs 4 split-K ranges per tile
+    (test_api_cpu checks the plan); a fill kernel clears their exchange words
+    and arrival counters on every replay."""
     import ozaki_triton_amd as ozk
     A, B = _int_valued_inputs(sa, sb, seed=53)
     Ad, Bd = A.to(gpu), B.to(gpu)
