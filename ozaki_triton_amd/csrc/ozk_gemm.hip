@@ -46,6 +46,7 @@ template <typename ST> struct Mfma;
 template <> struct Mfma<int8_t> {
     using Acc = i32x16;
     using Elem = int;
+    static constexpr bool kExactAcc = true;    // int32 sums: exact in any order
     OZK_DEV static Acc zero() { return Acc{0}; }
     OZK_DEV static Acc run(i32x4 a, i32x4 b, Acc c) {
         return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
@@ -55,6 +56,7 @@ template <> struct Mfma<int8_t> {
 template <> struct Mfma<_Float16> {
     using Acc = f32x16;
     using Elem = float;
+    static constexpr bool kExactAcc = false;
     OZK_DEV static Acc zero() { return Acc{0.0f}; }
     OZK_DEV static Acc run(i32x4 a, i32x4 b, Acc c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
@@ -67,6 +69,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 template <> struct Mfma<__bf16> {
     using Acc = f32x16;
     using Elem = float;
+    static constexpr bool kExactAcc = false;
     OZK_DEV static Acc zero() { return Acc{0.0f}; }
     OZK_DEV static Acc run(i32x4 a, i32x4 b, Acc c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
@@ -83,6 +86,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 template <> struct Mfma<float> {
     using Acc = f32x16;
     using Elem = float;
+    static constexpr bool kExactAcc = false;
     OZK_DEV static Acc zero() { return Acc{0.0f}; }
     OZK_DEV static Acc run(i32x4 a, i32x4 b, Acc c) {
         const f32x4 fa = __builtin_bit_cast(f32x4, a), fb = __builtin_bit_cast(f32x4, b);
@@ -1204,6 +1208,19 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ring_kernel(GemmParams p, i
                     for (int r = 0; r < 16; ++r) splitk_put(mine + ((q * W * W + x) * 16 + r) * 64, (uint32_t)u[r]);
                 }
             if (!splitk_arrive(p, g, (int *)slot(2 * nkb + 1))) return;
+            if constexpr (MF::kExactAcc) {
+                // int32 sums are exact in any order: this range's
+                // accumulators stay, the other ranges are added
+                for (int s2 = 0; s2 < S; ++s2) {
+                    if (s2 == krange) continue;
+                    const uint32_t *src = splitk_slot(p, g, s2, wave, RW, ln);
+#pragma unroll
+                    for (int q = 0; q < NP; ++q)
+#pragma unroll
+                        for (int x = 0; x < W * W; ++x)
+                            acc[q][x / W][x % W] += splitk_get16<Acc>(src + (q * W * W + x) * 16 * 64);
+                }
+            } else {
             // every range read back in range order: range 0 straight into
             // the accumulators, then the others added one tile at a time
             {
@@ -1221,6 +1238,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ring_kernel(GemmParams p, i
 #pragma unroll
                     for (int x = 0; x < W * W; ++x)
                         acc[q][x / W][x % W] += splitk_get16<Acc>(src + (q * W * W + x) * 16 * 64);
+            }
             }
         }
         // this wave's scales into registers: sa of its rows, sb of its columns
@@ -1522,20 +1540,31 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide_kernel(GemmParams p, i
             for (int r = 0; r < 16; ++r) splitk_put(mine + (n * 16 + r) * 64, (uint32_t)u[r]);
         }
         if (!splitk_arrive(p, g, (int *)buf(nkb + 1))) return;
-        // every range read back, this one's too (keeping this range's
-        // registers live through the sum costs the K loop a spill), in
-        // range order: range 0 straight into the accumulators, then the
-        // others added one tile (16 loads in flight) at a time
-        {
-            const uint32_t *src = splitk_slot(p, g, 0, wave, RW, ln);
+        if constexpr (MF::kExactAcc) {
+            // int32 sums are exact in any order: this range's accumulators
+            // stay, the other ranges are added one tile (16 loads in
+            // flight) at a time
+            for (int s2 = 0; s2 < S; ++s2) {
+                if (s2 == krange) continue;
+                const uint32_t *src = splitk_slot(p, g, s2, wave, RW, ln);
 #pragma unroll
-            for (int n = 0; n < L * L; ++n) acc[n / L][n % L] = splitk_get16<Acc>(src + n * 16 * 64);
-        }
-        for (int s2 = 1; s2 < S; ++s2) {
-            const uint32_t *src = splitk_slot(p, g, s2, wave, RW, ln);
+                for (int n = 0; n < L * L; ++n)
+                    acc[n / L][n % L] += splitk_get16<Acc>(src + n * 16 * 64);
+            }
+        } else {
+            // every range read back, this one's too, in range order: range
+            // 0 straight into the accumulators, then the others added
+            {
+                const uint32_t *src = splitk_slot(p, g, 0, wave, RW, ln);
 #pragma unroll
-            for (int n = 0; n < L * L; ++n)
-                acc[n / L][n % L] += splitk_get16<Acc>(src + n * 16 * 64);
+                for (int n = 0; n < L * L; ++n) acc[n / L][n % L] = splitk_get16<Acc>(src + n * 16 * 64);
+            }
+            for (int s2 = 1; s2 < S; ++s2) {
+                const uint32_t *src = splitk_slot(p, g, s2, wave, RW, ln);
+#pragma unroll
+                for (int n = 0; n < L * L; ++n)
+                    acc[n / L][n % L] += splitk_get16<Acc>(src + n * 16 * 64);
+            }
         }
     }
     const int ct = wn * 32 + lr;
