@@ -572,7 +572,8 @@ struct Named {
 const Named kGemmNames[] = {{"staged", ozk::kGemmStaged}, {"dma", ozk::kGemmDMA},
                             {"ad", ozk::kGemmAD},         {"pair", ozk::kGemmPair},
                             {"ring", ozk::kGemmRing},     {"wide", ozk::kGemmWide},
-                            {"wide4", ozk::kGemmWide4},   {"solo5", ozk::kGemmSolo5}};
+                            {"wide4", ozk::kGemmWide4},   {"solo5", ozk::kGemmSolo5},
+                            {"kstep", ozk::kGemmKStep}};
 const Named kSplitNames[] = {{"coop", ozk::kForceSplitCoop},
                              {"strip", ozk::kForceSplitStrip},
                              {"transpose", ozk::kForceSplitTranspose},

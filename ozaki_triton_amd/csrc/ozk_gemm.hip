@@ -638,6 +638,326 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_dma_kernel(GemmParams p, in
     }
 }
 
+// one MFMA with its accumulator in AGPRs (AG) or VGPRs
+template <typename ST, bool AG> struct HandMfma;
+template <bool AG> struct HandMfma<int8_t, AG> {
+    OZK_DEV static void run(i32x16 &c, i32x4 a, i32x4 b) {
+        if constexpr (AG) asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+        else asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+    }
+};
+template <bool AG> struct HandMfma<_Float16, AG> {
+    OZK_DEV static void run(f32x16 &c, i32x4 a, i32x4 b) {
+        if constexpr (AG) asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+        else asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+    }
+};
+template <bool AG> struct HandMfma<__bf16, AG> {
+    OZK_DEV static void run(f32x16 &c, i32x4 a, i32x4 b) {
+        if constexpr (AG) asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+        else asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+    }
+};
+
+template <int N, typename F> OZK_DEV void static_for(F &&f) {
+    if constexpr (N > 0) {
+        static_for<N - 1>(f);
+        f(std::integral_constant<int, N - 1>{});
+    }
+}
+
+// ---------------------------------------------------------------------------
+// K-step kernel for grids too small to fill the chip with 64 x 64 tiles (tall
+// or skinny C, large K).  32 x 32 tiles, 4 waves (one per SIMD).  Wave w
+// takes the 32-byte K step w of every 128-byte stage and all L x L slice
+// pairs on it, so per stage it reads L A and L B fragments for L^2 MFMAs (8
+// reads for 16 MFMAs at L = 4) and no tile's K is split across workgroups.
+//   * Stages of 2L x 32 rows x 128 bytes are fetched by LDS-DMA into a ring
+//     of NST slots; stage kb + NST reuses the slot of stage kb after the
+//     barrier that follows every wave's reads of it, and the fragments of
+//     stage kb + 1 are read while the MFMAs of stage kb run.
+//   * Epilogue: the four waves' accumulators of each pair are summed through
+//     the LDS in wave order (int32: exact; fp32: the same order every call),
+//     groups of up to 4 pairs at a time, one pair per wave; that wave turns
+//     the sum into t_ij = fl32(fl32(fl32(acc) * sa_i) * sb_j) in the LDS.
+//     Then each wave sums, for a quarter of the tile, the t values of all
+//     pairs in the i-major / j-minor order from +0 (ozaki_triton.py:420-452)
+//     and stores C.
+// ---------------------------------------------------------------------------
+template <int L> struct KStepShape {
+    static constexpr int BM = 32, BN = 32;
+    static constexpr int ROWS = 2 * L * 32;                   // A rows then B rows
+    static constexpr int STAGE = ROWS * kDmaRB;
+    static constexpr int LPS = STAGE / (4 * 1024);            // DMA instructions per wave per stage
+    static constexpr int NST = (160 * 1024 / STAGE) < 6 ? (160 * 1024 / STAGE) : 6;
+    static constexpr int NP = L * L;                          // slice pairs
+    static constexpr int PR = NP < 4 ? NP : 4;                // pairs per epilogue group
+    static constexpr int T_BYTES = NP * 16 * 64 * 4;          // t values [pair][reg][lane]
+    static constexpr int R_BYTES = 4 * PR * 16 * 64 * 4;      // [wave][pair][reg][lane]
+    static constexpr int S_BYTES = 2 * L * 32 * 4;            // sa [L][32], sb [L][32]
+    static constexpr int EPI_BYTES = T_BYTES + R_BYTES + S_BYTES;
+    static constexpr int LDS_BYTES = NST * STAGE > EPI_BYTES ? NST * STAGE : EPI_BYTES;
+    static constexpr bool kHand = L == 4;   // accumulators in AGPRs, hand-placed MFMAs
+    static_assert(STAGE % 4096 == 0, "a stage is whole 1 KB windows per wave");
+    static_assert(NST >= 3, "stages in flight");
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS");
+    static_assert(kDmaRB == 128 && L * 32 <= 128, "four K steps per stage; scales one per lane");
+};
+
+template <typename ST, int L, typename AccT>
+__global__ __launch_bounds__(256, 1) void cross_gemm_kstep_kernel(GemmParams p, int group_m,
+                                                                  uint32_t a_records,
+                                                                  uint32_t b_records) {
+    using Sh = KStepShape<L>;
+    using MF = Mfma<ST>;
+    using Acc = typename MF::Acc;
+    using Elem = typename MF::Elem;
+    using OA = AccT;
+    constexpr int BM = Sh::BM, BN = Sh::BN, LPS = Sh::LPS, NST = Sh::NST;
+    constexpr int ES = (int)sizeof(ST);
+    constexpr uint32_t kOOB = 0x80000000u;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5, lr = lane & 31;
+
+    const int64_t tiles_m = (p.M + BM - 1) / BM;
+    const int64_t tiles_n = (p.N + BN - 1) / BN;
+    const int64_t tiles = tiles_m * tiles_n;
+    const int64_t g = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
+    const int64_t bidx = g / tiles;
+    const int64_t t = g % tiles;
+    const int64_t width = (int64_t)group_m * tiles_n;
+    const int64_t first_m = (t / width) * group_m;
+    const int64_t gsz = (tiles_m - first_m < group_m) ? (tiles_m - first_m) : group_m;
+    const int64_t tm = first_m + (t % width) % gsz;
+    const int64_t tn = (t % width) / gsz;
+    const int64_t m0 = tm * BM, n0 = tn * BN;
+
+    const uint32_t kbytes = (uint32_t)(p.K * ES);
+    const int nkb = (int)((kbytes + kDmaRB - 1) / kDmaRB);
+
+    // this lane's scale of the tile (lanes 0..32L-1: sa [L][32], lanes
+    // 128..128+32L-1: sb [L][32]), loaded first so that its latency passes
+    // under the K loop; the epilogue stores it in the LDS
+    float scl = 0.0f;
+    {
+        const int e = tid & 127, s = e / 32, o = e % 32;
+        if (e < L * 32) {
+            if (tid < 128) {
+                if (m0 + o < p.M) scl = p.sa[bidx * p.sas_b + s * p.sas_l + (m0 + o) * p.sas_m];
+            } else if (n0 + o < p.N) {
+                scl = p.sb[bidx * p.sbs_b + s * p.sbs_l + (n0 + o) * p.sbs_n];
+            }
+        }
+    }
+
+    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const char *)p.A + bidx * p.as_b * ES), (short)0, (int)a_records, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const char *)p.B + bidx * p.bs_b * ES), (short)0, (int)b_records, 0x00020000);
+
+    // per-lane source offsets of this wave's LPS instructions of a stage (a
+    // 1 KB window is 8 whole 128-byte rows, all of A or all of B)
+    uint32_t src[LPS];
+    int chunk[LPS];
+#pragma unroll
+    for (int q = 0; q < LPS; ++q) {
+        const int pos = (wave * LPS + q) * 64 + lane;
+        const int r = pos / 8, pc = pos % 8;
+        chunk[q] = pc ^ ((r >> 1) & 7);
+        if (r < L * BM) {
+            const int64_t m = m0 + r % BM;
+            src[q] = (m < p.M) ? (uint32_t)(((int64_t)(r / BM) * p.as_l + m * p.as_m) * ES) : kOOB;
+        } else {
+            const int rb = r - L * BM;
+            const int64_t n = n0 + rb % BN;
+            src[q] = (n < p.N) ? (uint32_t)(((int64_t)(rb / BN) * p.bs_l + n * p.bs_n) * ES) : kOOB;
+        }
+    }
+    auto issue_one = [&](int kb, int q) {
+        const uint32_t kofs = (uint32_t)kb * kDmaRB + chunk[q] * 16;
+        const uint32_t vo = (src[q] == kOOB || kofs >= kbytes) ? kOOB : src[q] + kofs;
+        auto *ldsp = (__attribute__((address_space(3))) void *)(smem + (kb % NST) * Sh::STAGE +
+                                                              (wave * LPS + q) * 1024);
+        const bool isA = (wave * LPS + q) * 8 < L * BM;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(isA ? rA : rB, ldsp, 16, vo, 0, 0, 0);
+    };
+    auto issue_stage = [&](int kb) {
+#pragma unroll
+        for (int q = 0; q < LPS; ++q) issue_one(kb, q);
+    };
+    // stage s has landed once at most the instructions of the stages issued
+    // after it are outstanding (stages up to s + NST - 2 are issued when s is
+    // awaited); the lgkmcnt wait completes this wave's reads of the slot the
+    // next issue refills, and the barrier publishes every wave's DMA writes
+    auto stage_ready = [&](int s) {
+        const int after = min(NST - 2, nkb - 1 - s);
+        static_assert(NST - 2 <= 4, "wait table");
+        if constexpr (NST - 2 >= 4) { if (after == 4) { wait_vmcnt<4 * LPS>(); goto waited; } }
+        if constexpr (NST - 2 >= 3) { if (after == 3) { wait_vmcnt<3 * LPS>(); goto waited; } }
+        if constexpr (NST - 2 >= 2) { if (after == 2) { wait_vmcnt<2 * LPS>(); goto waited; } }
+        if (after == 1) { wait_vmcnt<LPS>(); goto waited; }
+        wait_vmcnt<0>();
+    waited:
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0) only
+        exec_barrier();
+    };
+
+    Acc acc[L][L];
+#pragma unroll
+    for (int i = 0; i < L; ++i)
+#pragma unroll
+        for (int j = 0; j < L; ++j) acc[i][j] = MF::zero();
+    // At L = 4 the 16 accumulator tiles (256 registers) live in the AGPRs,
+    // through hand-placed MFMAs (left to the compiler, the K loop spills).
+    // The compiler's hazard recogniser does not see into inline assembly: the
+    // zeroed tiles are pinned here, 8 wait states before any MFMA reads them.
+    constexpr bool kHand = Sh::kHand;
+    if constexpr (kHand) {
+        static_for<L * L>([&](auto n_) {
+            constexpr int n = decltype(n_)::value;
+            (void)acc;   // an ordinary use, so that the capture does not hinge on the asm operand
+            asm volatile("" : "+a"(acc[n / L][n % L]));
+        });
+        asm volatile("s_nop 7" ::: "memory");
+    }
+
+    struct Frags {
+        i32x4 a[L];
+        i32x4 b[L];
+    };
+    const int ch = 2 * wave + h;   // this wave's 16-byte chunk of a stage row
+    auto read_frags = [&](int kb, Frags &f) {
+        const char *buf = smem + (kb % NST) * Sh::STAGE;
+#pragma unroll
+        for (int i = 0; i < L; ++i) f.a[i] = *(const i32x4 *)(buf + rswz<kDmaRB>(i * BM + lr, ch));
+#pragma unroll
+        for (int j = 0; j < L; ++j)
+            f.b[j] = *(const i32x4 *)(buf + rswz<kDmaRB>(L * BM + j * BN + lr, ch));
+    };
+    // the L^2 MFMAs of one stage, with the DMA instructions of stage dkb (if
+    // dkb >= 0) spread between them: issued in a burst, the four waves'
+    // instructions fill the vector-memory queue and stall each wave at issue
+    auto mfmas = [&](const Frags &f, int dkb) {
+        constexpr int NMF = L * L;
+        static_for<NMF>([&](auto n_) {
+            constexpr int n = decltype(n_)::value;
+            if constexpr (kHand) HandMfma<ST, true>::run(acc[n / L][n % L], f.a[n / L], f.b[n % L]);
+            else acc[n / L][n % L] = MF::run(f.a[n / L], f.b[n % L], acc[n / L][n % L]);
+            static_for<LPS>([&](auto d_) {
+                constexpr int d = decltype(d_)::value;
+                // instruction d goes after MFMA (d * NMF) / LPS
+                if constexpr ((d * NMF) / LPS == n) {
+                    if (dkb >= 0) issue_one(dkb, d);
+                }
+            });
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+    // stage kb: the next stage's fragments into `nxt` (after its barrier,
+    // which also frees stage kb's slot for stage kb + NST), then the MFMAs of
+    // `cur` with stage kb + NST's DMA between them
+    auto stage = [&](int kb, const Frags &cur, Frags &nxt) {
+        int dkb = -1;
+        if (kb + 1 < nkb) {
+            stage_ready(kb + 1);
+            if (kb + NST < nkb) dkb = kb + NST;
+            read_frags(kb + 1, nxt);
+        }
+        mfmas(cur, dkb);
+    };
+
+    if (nkb > 0) {
+#pragma unroll
+        for (int s = 0; s < NST - 1; ++s)
+            if (s < nkb) issue_stage(s);
+        stage_ready(0);
+        if (NST - 1 < nkb) issue_stage(NST - 1);
+        Frags f0, f1;
+        read_frags(0, f0);
+        int kb = 0;
+        for (; kb + 1 < nkb; kb += 2) {
+            stage(kb, f0, f1);
+            stage(kb + 1, f1, f0);
+        }
+        if (kb < nkb) stage(kb, f0, f1);
+    }
+
+    // the hand-placed MFMAs' results are read below: 64 wait states first
+    if constexpr (kHand) asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory");
+
+    // ---- epilogue ----
+    wait_vmcnt<0>();
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    exec_barrier();   // every wave is past its last read of the ring
+    // LDS: T [pair][4][lane] x 4 t values, R [wave][pair][4][lane] x 4
+    // accumulator values, S the scales; 16-byte pieces, a wave's 64 pieces
+    // contiguous
+    f32x4 *T = (f32x4 *)smem;
+    using E4 = Elem __attribute__((ext_vector_type(4)));
+    E4 *R = (E4 *)(smem + Sh::T_BYTES);
+    float *S = (float *)(smem + Sh::T_BYTES + Sh::R_BYTES);
+    if ((tid & 127) < L * 32) S[(tid < 128 ? 0 : L * 32) + (tid & 127)] = scl;
+    constexpr int NG = (Sh::NP + Sh::PR - 1) / Sh::PR;
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) {
+#pragma unroll
+        for (int pp = 0; pp < Sh::PR; ++pp) {
+            const int pr = gi * Sh::PR + pp;
+            if (pr < Sh::NP) {
+                const Acc v = acc[pr / L][pr % L];
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    R[((wave * Sh::PR + pp) * 4 + c) * 64 + lane] =
+                        E4{v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]};
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        exec_barrier();
+        const int pr = gi * Sh::PR + wave;
+        if (wave < Sh::PR && pr < Sh::NP) {
+            const int i = pr / L, j = pr % L;
+            const float sbj = S[L * 32 + j * 32 + lr];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                E4 v = R[((0 * Sh::PR + wave) * 4 + c) * 64 + lane];
+                v = v + R[((1 * Sh::PR + wave) * 4 + c) * 64 + lane];
+                v = v + R[((2 * Sh::PR + wave) * 4 + c) * 64 + lane];
+                v = v + R[((3 * Sh::PR + wave) * 4 + c) * 64 + lane];
+                // registers 4c .. 4c + 3: rows 8c + 4h + 0..3 of the tile
+                f32x4 tv;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float t1 = MF::to_f32(v[e]) * S[i * 32 + 8 * c + 4 * h + e];
+                    tv[e] = t1 * sbj;
+                }
+                T[(pr * 4 + c) * 64 + lane] = tv;
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        exec_barrier();
+    }
+    // wave w: accumulator registers 4w .. 4w + 3 of every lane, rows
+    // 8w + 4h + 0..3
+    const int64_t col = n0 + lr;
+    const int64_t cbase = bidx * p.cs_b;
+    OA out[4] = {(OA)0, (OA)0, (OA)0, (OA)0};
+#pragma unroll
+    for (int q = 0; q < Sh::NP; ++q) {
+        const f32x4 tv = T[(q * 4 + wave) * 64 + lane];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) out[e] = out[e] + (OA)tv[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int64_t row = m0 + 8 * wave + 4 * h + e;
+        if (col < p.N && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, out[e]);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Pair-split variant: 8 waves, two per SIMD.  The 2 x 2 grid of 32 x 32 wave
 // blocks is covered twice: wave group g (0 or 1) accumulates the slice pairs
@@ -1984,34 +2304,6 @@ struct Solo5Shape {
     static_assert(kDmaRB == 128, "128-byte stage rows");
 };
 
-// one MFMA with its accumulator in AGPRs (AG) or VGPRs
-template <typename ST, bool AG> struct HandMfma;
-template <bool AG> struct HandMfma<int8_t, AG> {
-    OZK_DEV static void run(i32x16 &c, i32x4 a, i32x4 b) {
-        if constexpr (AG) asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
-        else asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
-    }
-};
-template <bool AG> struct HandMfma<_Float16, AG> {
-    OZK_DEV static void run(f32x16 &c, i32x4 a, i32x4 b) {
-        if constexpr (AG) asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
-        else asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
-    }
-};
-template <bool AG> struct HandMfma<__bf16, AG> {
-    OZK_DEV static void run(f32x16 &c, i32x4 a, i32x4 b) {
-        if constexpr (AG) asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
-        else asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
-    }
-};
-
-template <int N, typename F> OZK_DEV void static_for(F &&f) {
-    if constexpr (N > 0) {
-        static_for<N - 1>(f);
-        f(std::integral_constant<int, N - 1>{});
-    }
-}
-
 template <typename ST, typename AccT>
 __global__ __launch_bounds__(256, 1) void cross_gemm_solo5_kernel(GemmParams p, int group_m,
                                                                   uint32_t a_records,
@@ -2628,7 +2920,27 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
     // L = 5: the one-wave-per-SIMD kernel (one launch; int8 / fp16 / bf16
     // slices); L = 6..8 and fp32 slices: the pair-split kernel per i-row range
     const bool solo5 = L == 5 && slice_dtype != 1;
+    // L = 1..4 on grids whose 64 x 64 tiles leave more than half the CUs idle
+    // and whose 32 x 32 tiles fit one round: the K-step kernel.  A workgroup
+    // of it does 1/4 of a 64 x 64 tile over all of K; one of the ring
+    // kernel's S split-K ranges does 1/S of a whole tile, so with S < 4 the
+    // K-step kernel wins, and with S = 4 only when it has as many workgroups.
+    // Measured (kernel trace, int8 unless noted), K-step against the kernel
+    // the planner would take otherwise: (1, 128, 2048, 4096) L = 4 28.9 us
+    // vs 39.4 (ring, S = 2), L = 3 22.5 vs 26.2, L = 2 15.9 vs 23.9 (LDS-DMA),
+    // L = 1 10.6 vs 16.3, fp16 L = 4 48.7 vs 55.5 (S = 4), L = 3 36.3 vs 36.7,
+    // L = 2 25.8 vs 43.8, L = 1 16.9 vs 25.9; 256^2 x 4096 L = 4 25.9 vs 34.0
+    // (S = 2); config 1 (fp16, L = 2) 7.1 vs 9.6; 320^2 x 8192 L = 4 42.8 vs
+    // 41.1 (S = 4, 100 workgroups each); 64 x 96 x 8192 L = 3 33.2 vs 28.2
+    // (S = 4, 6 workgroups against 8); 640^2 x 4096 L = 4, 400 tiles in two
+    // rounds, 53.7 vs 45.0 (S = 2)
+    const int64_t kstep_tiles = p.batch * ((p.M + 31) / 32) * ((p.N + 31) / 32);
+    const int s_ring = L >= 3 ? ksplit_for(nt(1, 1)) : 1;
+    const bool kstep = L <= 4 && !(L == 4 && slice_dtype == 1) && 2 * nt(1, 1) <= kCUs &&
+                       kstep_tiles <= kCUs &&
+                       (s_ring < 4 || kstep_tiles >= nt(1, 1) * s_ring);
     plan.kind = !fits              ? kGemmStaged
+                : kstep            ? kGemmKStep
                 : L <= 1           ? kGemmDMA
                 : L == 2           ? ((mi == 2 && ni == 2) ? kGemmRing : kGemmDMA)
                 : wide3            ? kGemmWide
@@ -2651,6 +2963,7 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
     else if (fits && forced(kGemmRing)) plan.kind = L >= 2 ? kGemmRing : kGemmDMA;
     else if (fits && forced(kGemmWide)) plan.kind = L == 3 ? kGemmWide : plan.kind;
     else if (fits && forced(kGemmWide4)) plan.kind = L == 4 ? kGemmWide4 : plan.kind;
+    else if (fits && forced(kGemmKStep)) plan.kind = (L == 4 && slice_dtype == 1) ? plan.kind : kGemmKStep;
     if (plan.kind == kGemmAD) plan.group_m = 2;
     // 96 x 64 tiles: groups of 4 tile rows (C3: 7.12-7.16 ms against 7.21-7.23
     // with 8, 7.33-7.35 with 16; cross-GEMM alone, one box)
@@ -2750,6 +3063,22 @@ template <typename ST, int L, int MI, int NI, typename AccT>
 static hipError_t launch_dma(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     using Sh = DmaShape<L, MI, NI>;
     auto kern = cross_gemm_dma_kernel<ST, L, MI, NI, AccT>;
+    static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
+    if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
+    const int es = (int)sizeof(ST);
+    const int64_t ea = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es);
+    const int64_t eb = dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es);
+    const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
+    if (tiles == 0) return hipSuccess;
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(256), Sh::LDS_BYTES, st, p,
+                       plan.group_m, (uint32_t)ea, (uint32_t)eb);
+    return hipGetLastError();
+}
+
+template <typename ST, int L, typename AccT>
+static hipError_t launch_kstep(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
+    using Sh = KStepShape<L>;
+    auto kern = cross_gemm_kstep_kernel<ST, L, AccT>;
     static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
     if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
     const int es = (int)sizeof(ST);
@@ -2917,6 +3246,10 @@ static hipError_t launch_one(const GemmParams &p, const GemmPlan &plan, hipStrea
 
 template <typename ST, int L, typename AccT>
 static hipError_t launch_L(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
+    // (fp32 slices at L = 4: no hand-placed MFMA, so no K-step kernel)
+    if constexpr (L <= 4 && !(L == 4 && std::is_same_v<ST, float>)) {
+        if (plan.kind == kGemmKStep) return launch_kstep<ST, L, AccT>(p, plan, st);
+    }
     const int key = plan.mi * 10 + plan.ni;
     if constexpr (L == 1) {
         switch (key) {

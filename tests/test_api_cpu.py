@@ -219,12 +219,12 @@ def test_splitk_workspace():
     L = _lib.load()
     nb = ctypes.c_size_t(0)
     p = ctypes.c_void_p(0x1000)
-    M, N, K, Ls = 128, 2048, 4096, 4
+    M, N, K, Ls = 1024, 1024, 65536, 3
     a = _lib.i64arr([Ls * M * K, M * K, K, 1])
     b = _lib.i64arr([Ls * N * K, N * K, 1, K])
-    # ring kernel, L = 4: 64 tiles of 64 x 64, 2 ranges of 16 stages, 8 pairs x
-    # 16 registers per wave
-    splitk = 64 * 2 * 8 * 128 * 64 * 4 + 256 + 256
+    # config 5's wide kernel, L = 3: 128 tiles of 64 x 128, 2 ranges of 256
+    # stages, 9 pairs x 16 registers per wave; 128 counters (512 bytes)
+    splitk = 128 * 2 * 8 * 144 * 64 * 4 + 512 + 256
     assert L.ozk_cross_gemm_workspace_bytes(1, M, N, K, Ls, _lib.OZK_I8, p, a, p, b,
                                             ctypes.byref(nb)) == 0
     assert nb.value == splitk
@@ -540,19 +540,35 @@ def test_planner_kernel_choice():
     assert _gemm_kernel(L, 1, 2048, 2048, 8192, 4, I8, 256) == "ring"     # 3 vs 4
     assert _gemm_kernel(L, 1, 1024, 1024, 65536, 4, I8, 256) == "ring"    # 1 vs 1
     assert _gemm_kernel(L, 1, 4096, 4096, 4096, 2, _lib.OZK_F16, 256) == "ring"   # config 2
-    assert _gemm_kernel(L, 1, 256, 256, 256, 2, _lib.OZK_F16, 256) == "dma"       # config 1
+    assert _gemm_kernel(L, 1, 256, 256, 256, 2, _lib.OZK_F16, 256) == "kstep"     # config 1
     assert _gemm_kernel(L, 1, 2048, 2048, 2048, 1, I8, 256) == "dma"
-    # split-K for grids under half the CUs: S = CUs / tiles, at most 4, at
-    # least 16 stages of 128 bytes of K per range
-    assert _gemm_kernel(L, 1, 128, 2048, 4096, 4, I8, 256, True) == ("ring", 2)      # 64 tiles, 32 stages
-    assert _gemm_kernel(L, 1, 128, 2048, 4096, 4, _lib.OZK_F16, 256, True) == ("ring", 4)
-    assert _gemm_kernel(L, 1, 128, 2048, 4096, 3, I8, 256, True) == ("ring", 2)
+    # grids whose 64 x 64 tiles leave more than half the CUs idle: the K-step
+    # kernel's 32 x 32 tiles when they fit one round (the reference's
+    # (1, 128, 2048, 4096) point: 256 of them), else split-K of the ring or
+    # wide kernel, S = CUs / tiles, at most 4, at least 16 stages of 128 bytes
+    # of K per range
+    for nsp in (1, 2, 3, 4):
+        for sd in (I8, _lib.OZK_F16):
+            assert _gemm_kernel(L, 1, 128, 2048, 4096, nsp, sd, 256, True) == ("kstep", 1)
+    assert _gemm_kernel(L, 1, 128, 2048, 4096, 4, _lib.OZK_F32, 256) == "ring"     # fp32 slices
     assert _gemm_kernel(L, 1, 128, 2048, 4096, 4, I8, 64, True) == ("ring", 1)       # 64 CUs
-    assert _gemm_kernel(L, 1, 128, 2048, 2048, 4, I8, 256, True) == ("ring", 1)      # 16 stages
-    assert _gemm_kernel(L, 1, 128, 2048, 8192, 4, I8, 256, True) == ("ring", 4)      # 64 stages
-    # the K = 8192 shape of test_ozaki_matmul_graph_capture (split-K replayed)
+    # the shapes of test_ozaki_matmul_graph_capture: the K-step kernel, and at
+    # K = 8192 the ring kernel with 4 ranges (6 K-step tiles against 8)
+    assert _gemm_kernel(L, 2, 128, 96, 256, 3, I8, 256, True) == ("kstep", 1)
     assert _gemm_kernel(L, 1, 64, 96, 8192, 3, I8, 256, True) == ("ring", 4)
     assert _gemm_kernel(L, 1, 64, 96, 8192, 3, _lib.OZK_F16, 256, True) == ("ring", 4)
+    assert _gemm_kernel(L, 1, 32, 32, 4096, 4, I8, 256, True) == ("kstep", 1)        # S = 2
+    assert _gemm_kernel(L, 1, 512, 2048, 4096, 4, I8, 256, True) == ("ring", 1)      # 256 tiles
+    assert _gemm_kernel(L, 1, 640, 640, 4096, 4, I8, 256, True) == ("ring", 2)       # 100 tiles, 400
+    assert _gemm_kernel(L, 1, 640, 640, 2048, 4, I8, 256, True) == ("ring", 1)       # 16 stages
+    assert _gemm_kernel(L, 1, 640, 640, 8192, 4, I8, 256, True) == ("ring", 2)
+    assert _gemm_kernel(L, 1, 320, 320, 8192, 4, I8, 256, True) == ("kstep", 1)      # 100 = 25 x 4
+    assert _gemm_kernel(L, 1, 288, 320, 8192, 4, I8, 256, True) == ("ring", 4)       # 90 < 25 x 4
+    with _lib.forced_kernels(gemm="ring"):
+        # the reference point with the ring kernel forced: split-K
+        assert _gemm_kernel(L, 1, 128, 2048, 4096, 4, I8, 256, True) == ("ring", 2)
+        assert _gemm_kernel(L, 1, 128, 2048, 4096, 4, _lib.OZK_F16, 256, True) == ("ring", 4)
+        assert _gemm_kernel(L, 1, 128, 2048, 8192, 4, I8, 256, True) == ("ring", 4)
     assert _gemm_kernel(L, 1, 1024, 1024, 65536, 3, I8, 256, True) == ("wide", 2)    # config 5
     assert _gemm_kernel(L, 1, 8192, 8192, 8192, 4, I8, 256, True) == ("wide4", 1)    # config 3
     assert _gemm_kernel(L, 16, 1024, 1024, 2048, 3, _lib.OZK_F16, 256, True) == ("wide", 1)

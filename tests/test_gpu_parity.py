@@ -375,15 +375,16 @@ def test_ozaki_matmul_degenerate_shapes(gpu):
                          torch.randn(0, 3, dtype=torch.float64, device=gpu), 2, torch.int8)
 
 
-@pytest.mark.parametrize("kernel", ["staged", "dma", "ad", "pair", "ring", "wide", "wide4"])
+@pytest.mark.parametrize("kernel", ["staged", "dma", "ad", "pair", "ring", "wide", "wide4",
+                                    "kstep"])
 @pytest.mark.parametrize("L", [1, 2, 3, 4])
 def test_cross_gemm_each_kernel_bitexact(oracle, gpu, L, kernel, force):
     """Every cross-GEMM kernel, forced: the VGPR-staged one (taken when an
     operand's extent exceeds the 31-bit buffer offsets of the LDS-DMA kernels),
     the 2 x 2 LDS-DMA kernel, the A-direct kernel, the pair-split kernel, its
     five-slot ring form (L >= 3; for L <= 2 the request falls back to the
-    2 x 2 kernel), the wide kernel (L = 3) and the 96 x 64 wide kernel (L = 4;
-    otherwise the default kernel)."""
+    2 x 2 kernel), the wide kernel (L = 3), the 96 x 64 wide kernel (L = 4;
+    otherwise the default kernel) and the K-step kernel (32 x 32 tiles)."""
     import ozaki_triton_amd as ozk
     force(gemm=kernel)
     g = torch.Generator().manual_seed(77 + L)
@@ -410,6 +411,10 @@ def test_cross_gemm_each_kernel_bitexact(oracle, gpu, L, kernel, force):
     ("staged", 2, 100, 72, 1040),
     ("staged", 4, 100, 72, 520),
     ("ad", 3, 100, 72, 1040),
+    ("kstep", 4, 100, 72, 1040),    # (fp32 slices at L = 4: the planner's kernel)
+    ("kstep", 3, 130, 72, 4096),
+    ("kstep", 2, 64, 96, 2064),
+    ("kstep", 1, 40, 200, 1040),
 ])
 def test_float_slice_kernels_bitexact(oracle, gpu, kernel, L, M, N, K, sdt, force):
     """Every cross-GEMM kernel with float slices, at the tile shapes and K of
@@ -450,6 +455,29 @@ def test_ring_kernel_stage_counts(oracle, gpu, L, K, sdt, force):
         want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[b]), to_np(sa[b]), to_np(sb[b]),
                                  "float64")
         assert_bitwise_equal(C[b], want, f"{kernel} {sdt} L{L} K{K} b{b}")
+
+
+@pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
+@pytest.mark.parametrize("L", [1, 2, 3, 4])
+@pytest.mark.parametrize("K", [16, 128, 200, 520, 1040, 2064])
+def test_kstep_kernel_stage_counts(oracle, gpu, L, K, sdt, force):
+    """The K-step kernel (32 x 32 tiles, wave w on K step w of every stage,
+    the waves' accumulators summed through the LDS) over 1 to 17 stages of
+    128 bytes of K against a ring of 5 or 6 stage slots (fewer stages than
+    the prologue would fetch, and more than the ring holds), M and N cutting
+    tiles, batch 2: int8 and integer-valued fp16 slices bit-exact against the
+    oracle."""
+    import ozaki_triton_amd as ozk
+    M, N = 70, 45
+    g = torch.Generator().manual_seed(K * 10 + L + 5)
+    As, BsT, sa, sb = _slices_for(g, 2, L, M, N, K, sdt)
+    args = (As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), L, torch.float64)
+    force(gemm="kstep")
+    C = to_np(ozk.cross_gemm(*args))
+    for b in range(2):
+        want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[b]), to_np(sa[b]), to_np(sb[b]),
+                                 "float64")
+        assert_bitwise_equal(C[b], want, f"kstep {sdt} L{L} K{K} b{b}")
 
 
 @pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
@@ -687,28 +715,36 @@ def test_splitk_without_workspace_runs_unsplit(oracle, gpu, force):
     assert_bitwise_equal(to_np(C)[0], want, "no workspace")
 
 
+@pytest.mark.parametrize("gemm", ["", "ring"])
 @pytest.mark.parametrize("xdt,sdt", [(torch.float64, torch.int8), (torch.float32, torch.float16),
                                      (torch.float64, torch.float16)])
-@pytest.mark.parametrize("L", [3, 4])
-def test_splitk_reference_point(oracle, gpu, xdt, sdt, L):
+@pytest.mark.parametrize("L", [1, 2, 3, 4])
+def test_reference_point_small_grid(oracle, gpu, xdt, sdt, L, gemm, force):
     """The reference's published point (1, 128, 2048, 4096)
-    (reference/test_results.csv): 64 tiles of 64 x 64 on 256 CUs, so the
-    planner cuts K into ranges of at least 16 stages (ring kernel): 2 for
-    int8 slices (32 stages), 4 for fp16 (64).  ozaki_matmul end to end,
-    sampled blocks against the oracle (int8 bit-exact, fp16 within the fp32
-    accumulation bound)."""
+    (reference/test_results.csv): 64 tiles of 64 x 64 on 256 CUs.  The
+    planner takes the K-step kernel's 256 tiles of 32 x 32; with the ring
+    kernel forced (L >= 3) it cuts K into split-K ranges of at least 16
+    stages: 2 for int8 slices (32 stages), 4 for fp16 (64).  ozaki_matmul end
+    to end, sampled blocks against the oracle (int8 bit-exact, fp16 within
+    the fp32 accumulation bound)."""
     import ozaki_triton_amd as ozk
     M, N, K = 128, 2048, 4096
+    if gemm:
+        if L < 3:
+            pytest.skip("the ring kernel serves 3 and 4 slices here")
+        force(gemm=gemm)
     kern, ks = _planned_ksplit(1, M, N, K, L, sdt)
-    assert kern == "ring"
     if torch.cuda.get_device_properties(0).multi_processor_count >= 256:
-        assert ks == (2 if sdt == torch.int8 else 4)
+        if gemm:
+            assert (kern, ks) == ("ring", 2 if sdt == torch.int8 else 4)
+        else:
+            assert (kern, ks) == ("kstep", 1)
     A, B = c3_like((1, M, K), (1, K, N), seed=L + 17, dtype=xdt)
     C = ozk.ozaki_matmul(A.to(gpu), B.to(gpu), L, sdt)
     torch.cuda.synchronize()
     rows, cols = sample_indices(M, 24, 1), sample_indices(N, 24, 2)
     check_block_vs_oracle(oracle, ozk, to_np(C)[0], to_np(A)[0], to_np(B)[0], rows, cols, L, sdt,
-                          xdt, f"ref point L{L} {xdt} {sdt}")
+                          xdt, f"ref point L{L} {xdt} {sdt} {gemm or 'planned'}")
 
 
 @pytest.mark.parametrize("out", [torch.float64, torch.float32, torch.float16, torch.bfloat16,
@@ -988,17 +1024,22 @@ def _int_valued_inputs(shape_a, shape_b, seed):
     return A, B
 
 
+@pytest.mark.parametrize("gemm", ["", "kstep", "ring"])
 @pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
 @pytest.mark.parametrize("sa,sb", [((2, 128, 256), (256, 96)), ((1, 64, 8192), (8192, 96))])
-def test_ozaki_matmul_graph_capture(oracle, gpu, sdt, sa, sb):
+def test_ozaki_matmul_graph_capture(oracle, gpu, sdt, sa, sb, gemm, force):
     """ozaki_matmul captured in a HIP graph (torch.cuda.graph): every replay,
     with eager work and synchronisations between replays and the inputs
     changed in place, equals the oracle bit for bit (inputs for which the fp16
     path is exact too) and the eager call.  At K = 8192 the B split is the
-    cooperative kernel and the cross-GEMM runs 4 split-K ranges per tile
-    (test_api_cpu checks the plan); a fill kernel clears their exchange words
-    and arrival counters on every replay."""
+    cooperative kernel, whose exchange words a fill kernel clears on every
+    replay, and the planner's cross-GEMM is the ring kernel with 4 split-K
+    ranges per tile, whose arrival counters a fill kernel clears too; at
+    K = 256 it is the K-step kernel (test_api_cpu checks both plans).  Each
+    kernel is also forced on both shapes."""
     import ozaki_triton_amd as ozk
+    if gemm:
+        force(gemm=gemm)
     A, B = _int_valued_inputs(sa, sb, seed=53)
     Ad, Bd = A.to(gpu), B.to(gpu)
     L = 3
@@ -1160,7 +1201,7 @@ def test_split_columns_default_plan(oracle, gpu, xdt, sdt, batch, N, K):
 
 
 @pytest.mark.parametrize("kernel", ["", "dma", "ring", "pair", "ad", "staged", "wide", "wide4",
-                                    "solo5"])
+                                    "solo5", "kstep"])
 @pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
 @pytest.mark.parametrize("K", [1, 2, 3, 5, 7, 9, 255, 257, 1003])
 def test_packed_rows_last_piece(oracle, gpu, kernel, sdt, K, force):
@@ -1174,7 +1215,7 @@ def test_packed_rows_last_piece(oracle, gpu, kernel, sdt, K, force):
     import ozaki_triton_amd as ozk
     if kernel:
         force(gemm=kernel)
-    L = (3 if kernel == "wide" else 4 if kernel in ("ring", "pair", "ad", "wide4")
+    L = (3 if kernel == "wide" else 4 if kernel in ("ring", "pair", "ad", "wide4", "kstep")
          else 5 if kernel == "solo5" else 2)
     A, B = c3_like((1, 33, K), (1, K, 20), seed=K + 100)
     C = ozk.ozaki_matmul(A.to(gpu), B.to(gpu), L, sdt, max_splits=L)
