@@ -674,15 +674,17 @@ template <int N, typename F> OZK_DEV void static_for(F &&f) {
 // reads for 16 MFMAs at L = 4) and no tile's K is split across workgroups.
 //   * Stages of 2L x 32 rows x 128 bytes are fetched by LDS-DMA into a ring
 //     of NST slots; stage kb + NST reuses the slot of stage kb after the
-//     barrier that follows every wave's reads of it, and the fragments of
-//     stage kb + 1 are read while the MFMAs of stage kb run.
+//     barrier that follows every wave's reads of it.  The fragments of stage
+//     kb + 1 are read while the MFMAs of stage kb run, with stage kb + NST's
+//     DMA instructions spread between those MFMAs.
 //   * Epilogue: the four waves' accumulators of each pair are summed through
 //     the LDS in wave order (int32: exact; fp32: the same order every call),
-//     groups of up to 4 pairs at a time, one pair per wave; that wave turns
-//     the sum into t_ij = fl32(fl32(fl32(acc) * sa_i) * sb_j) in the LDS.
-//     Then each wave sums, for a quarter of the tile, the t values of all
-//     pairs in the i-major / j-minor order from +0 (ozaki_triton.py:420-452)
-//     and stores C.
+//     in 16-byte pieces, groups of up to 4 pairs at a time, one pair per
+//     wave; that wave turns the sum into t_ij = fl32(fl32(fl32(acc) * sa_i) *
+//     sb_j) in the LDS.  Then each wave sums, for a quarter of the tile, the
+//     t values of all pairs in the i-major / j-minor order from +0
+//     (ozaki_triton.py:420-452) and stores C.  The tile's scales are loaded
+//     at kernel start.
 // ---------------------------------------------------------------------------
 template <int L> struct KStepShape {
     static constexpr int BM = 32, BN = 32;
@@ -692,8 +694,8 @@ template <int L> struct KStepShape {
     static constexpr int NST = (160 * 1024 / STAGE) < 6 ? (160 * 1024 / STAGE) : 6;
     static constexpr int NP = L * L;                          // slice pairs
     static constexpr int PR = NP < 4 ? NP : 4;                // pairs per epilogue group
-    static constexpr int T_BYTES = NP * 16 * 64 * 4;          // t values [pair][reg][lane]
-    static constexpr int R_BYTES = 4 * PR * 16 * 64 * 4;      // [wave][pair][reg][lane]
+    static constexpr int T_BYTES = NP * 16 * 64 * 4;          // t values [pair][reg / 4][lane][4]
+    static constexpr int R_BYTES = 4 * PR * 16 * 64 * 4;      // [wave][pair][reg / 4][lane][4]
     static constexpr int S_BYTES = 2 * L * 32 * 4;            // sa [L][32], sb [L][32]
     static constexpr int EPI_BYTES = T_BYTES + R_BYTES + S_BYTES;
     static constexpr int LDS_BYTES = NST * STAGE > EPI_BYTES ? NST * STAGE : EPI_BYTES;
