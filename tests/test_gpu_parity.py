@@ -457,6 +457,32 @@ def test_ring_kernel_stage_counts(oracle, gpu, L, K, sdt, force):
         assert_bitwise_equal(C[b], want, f"{kernel} {sdt} L{L} K{K} b{b}")
 
 
+@pytest.mark.parametrize("out", [torch.float64, torch.float32, torch.float16, torch.bfloat16,
+                                 torch.int8])
+@pytest.mark.parametrize("sdt", [torch.int8, torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("L", [1, 3, 4])
+def test_kstep_kernel_dtypes(oracle, gpu, L, sdt, out, force):
+    """The K-step kernel for every slice and output dtype, batched, with a
+    broadcast (batch stride 0) B: int8 and integer-valued float slices
+    bit-exact against the oracle (fp32 slices at L = 4 take the planner's
+    kernel)."""
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(ALL_SLICES.index(sdt) * 11 + len(str(out)) + 40 * L)
+    M, N, K = 70, 100, 400
+    As, BsT, sa, sb = _slices_for(g, 2, L, M, N, K, sdt)
+    if out in (torch.float16, torch.bfloat16, torch.int8):
+        sa = sa * 2.0 ** (12 if sdt == torch.int8 else 0)
+    Bd = BsT[:1].to(gpu).expand(2, -1, -1, -1).transpose(-1, -2)   # broadcast B
+    sbd = sb[:1].to(gpu).expand(2, -1, -1)
+    args = (As.to(gpu), Bd, sa.to(gpu), sbd, L, out)
+    force(gemm="kstep")
+    C = to_np(ozk.cross_gemm(*args))
+    for b in range(2):
+        want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[0]), to_np(sa[b]), to_np(sb[0]),
+                                 NAME_OF[out])
+        assert_bitwise_equal(C[b], want, f"kstep L{L} {sdt} {out} b{b}")
+
+
 @pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
 @pytest.mark.parametrize("L", [1, 2, 3, 4])
 @pytest.mark.parametrize("K", [16, 128, 200, 520, 1040, 2064])
