@@ -490,6 +490,22 @@ def main():
     del flush
     flushed_ms = statistics.median(fts)
 
+    # the HBM rate a plain copy reaches on this box in the same run (torch's
+    # own device copy of 1 GiB, read + write bytes; outside the timed region):
+    # the practical ceiling the split's bytes are compared with below
+    csrc = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+    cdst = torch.empty_like(csrc)
+    for _ in range(3):
+        cdst.copy_(csrc)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        cdst.copy_(csrc)
+    e1.record()
+    e1.synchronize()
+    copy_gbs = 2.0 * csrc.numel() / (e0.elapsed_time(e1) / 10 * 1e-3) / 1e9
+    del csrc, cdst
+
     t_split_b = avg_ms("split_b", "split_a")
     t_split_a = avg_ms("split_a", "cross_gemm")
     t_cross = avg_ms("cross_gemm", "end")
@@ -582,6 +598,8 @@ def main():
             "frac": round(split_gbs / PEAK_HBM_GBS, 4),
             "ms_a": round(t_split_a, 4),
             "ms_b": round(t_split_b, 4),
+            "device_copy_GBps": round(copy_gbs, 1),
+            "of_device_copy": round(split_gbs / copy_gbs, 4),
         },
     }
     if not args.no_cpu:
