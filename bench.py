@@ -40,6 +40,7 @@ PEAK_HBM_GBS = 8000.0         # GB/s HBM3E
 
 CONFIGS = {
     # name: (input dtype, slice dtype, L, A shape, B shape, seed, distribution)
+    "C1": ("float32", "float16", 2, (256, 256), (256, 256), 0, "normal"),
     "C2": ("float32", "float16", 2, (4096, 4096), (4096, 4096), 1, "uniform"),
     "C3": ("float64", "int8", 4, (8192, 8192), (8192, 8192), 2, "exp8"),
     "C4": ("float64", "float16", 3, (16, 1024, 2048), (2048, 1024), 3, "normal"),
@@ -557,6 +558,7 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": {
+                "C1": "FP32->FP16 num_splits=2, M=N=K=256 (the reference's CPU-runnable case)",
                 "C2": "FP32->FP16 num_splits=2, M=N=K=4096",
                 "C3": "FP64->INT8 num_splits=4, M=N=K=8192, batch 1",
                 "C4": "FP64->FP16 num_splits=3, A[16,1024,2048] x B[2048,1024] (broadcast)",
@@ -603,7 +605,7 @@ def main():
         },
     }
     if not args.no_cpu:
-        block = args.cpu_block
+        block = min(args.cpu_block, M, N)
         v, dt = cpu_oracle_baseline(A_cpu, B_cpu, sdt, L, block)
         rec["cpu_baseline"] = {
             "value": round(v, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
