@@ -28,6 +28,7 @@ Differences from the reference that do not change any value:
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import math
 
@@ -144,7 +145,22 @@ def _require_supported(input_dtype: torch.dtype, slice_dtype: torch.dtype) -> No
 
 
 def _stream(dev: torch.device) -> ctypes.c_void_p:
+    """dev's current stream as a raw pointer (torch's direct accessor where it
+    has one: the Stream object costs microseconds per call)."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw is not None:
+        return ctypes.c_void_p(raw(idx))
     return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _on_device(dev: torch.device):
+    """The device context a launch needs: none when dev is already current.
+    Workspaces come from torch's allocator on dev's current stream, the stream
+    the kernels run on, so they need no record_stream."""
+    if dev.index is None or dev.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(dev)
 
 
 def _workspace(nbytes: int, dev: torch.device):
@@ -174,14 +190,13 @@ def _split_into(A: torch.Tensor, num_splits: int, alpha: int, slice_dtype: torch
                L.ozk_split_workspace_bytes(xd, Bn, M, K, xs, num_splits, sd, ss,
                                            ctypes.byref(nbytes)))
     ws, wsp = _workspace(int(nbytes.value), A.device)
-    with torch.cuda.device(A.device):
+    with _on_device(A.device):
         st = L.ozk_split(ctypes.c_void_p(A.data_ptr()), xd, Bn, M, K, xs, num_splits, alpha, sd,
                          ctypes.c_void_p(slices.data_ptr()), ss,
                          ctypes.c_void_p(scales.data_ptr()), cs, wsp, nbytes.value,
                          _stream(A.device))
     _lib.check("ozk_split", st)
-    if ws is not None:
-        ws.record_stream(torch.cuda.current_stream(A.device))
+    del ws
 
 
 def split_matrix(A: torch.Tensor, num_splits: int, alpha: int, slice_dtype: torch.dtype):
@@ -264,14 +279,13 @@ def _cross_gemm_into(A_slices, B_slices, A_scales, B_scales, num_splits, C) -> N
                L.ozk_cross_gemm_workspace_bytes(BN, M, N, K, num_splits, sd, ap, a_st, bp, b_st,
                                                 ctypes.byref(nbytes)))
     ws, wsp = _workspace(int(nbytes.value), C.device)
-    with torch.cuda.device(C.device):
+    with _on_device(C.device):
         st = L.ozk_cross_gemm(ap, a_st, bp, b_st, ctypes.c_void_p(A_scales.data_ptr()), sa_st,
                               ctypes.c_void_p(B_scales.data_ptr()), sb_st, BN, M, N, K,
                               num_splits, sd, ctypes.c_void_p(C.data_ptr()), od, c_st, wsp,
                               nbytes.value, _stream(C.device))
     _lib.check("ozk_cross_gemm", st)
-    if ws is not None:
-        ws.record_stream(torch.cuda.current_stream(C.device))
+    del ws
 
 
 # ============================================================
@@ -281,6 +295,24 @@ def _cross_gemm_into(A_slices, B_slices, A_scales, B_scales, num_splits, C) -> N
 def _last2_ok(t: torch.Tensor) -> bool:
     """True when the kernels can read t's last two dims in place."""
     return t.stride(-1) == 1 or t.stride(-2) == 1
+
+
+def _broadcast_batch(sa, sb) -> torch.Size:
+    """torch.broadcast_shapes(sa, sb) for two batch shapes, without its
+    per-call overhead; shapes that do not broadcast go to torch, which raises
+    its own error."""
+    n = max(len(sa), len(sb))
+    pa = (1,) * (n - len(sa)) + tuple(sa)
+    pb = (1,) * (n - len(sb)) + tuple(sb)
+    out = []
+    for x, y in zip(pa, pb):
+        if x == y or y == 1:
+            out.append(x)
+        elif x == 1:
+            out.append(y)
+        else:
+            return torch.broadcast_shapes(sa, sb)
+    return torch.Size(out)
 
 
 def _canonicalize_batch(A, B):
@@ -296,7 +328,7 @@ def _canonicalize_batch(A, B):
     K2, N = B.shape[-2:]
     assert K == K2, f"contraction dim mismatch: A K={K}, B K={K2}"
 
-    batch_shape = torch.broadcast_shapes(A.shape[:-2], B.shape[:-2])
+    batch_shape = _broadcast_batch(A.shape[:-2], B.shape[:-2])
     BN = math.prod(batch_shape)
 
     def flat(T, rows, cols):
@@ -405,13 +437,10 @@ def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, events, max_split
     ev = None
     if events is not None:
         ev = (ctypes.c_void_p * 4)(*[ctypes.c_void_p(e.cuda_event) for e in events])
-    with torch.cuda.device(dev):
-        stream = torch.cuda.current_stream(dev)
+    with _on_device(dev):
         st = L.ozk_matmul(ctypes.c_void_p(A3.data_ptr()), a_st, ctypes.c_void_p(B3.data_ptr()),
                           b_st, xd, BN, M, N, K, num_splits, sd, ctypes.c_void_p(C.data_ptr()),
-                          _lib.i64arr(C.stride()), wsp, nbytes.value, ev,
-                          ctypes.c_void_p(stream.cuda_stream))
+                          _lib.i64arr(C.stride()), wsp, nbytes.value, ev, _stream(dev))
     _lib.check("ozk_matmul", st)
-    if ws is not None:
-        ws.record_stream(stream)
+    del ws
     return C.view(out_shape)
