@@ -488,6 +488,11 @@ int ozk_matmul(const void *A, const int64_t a_strides[3], const void *B,
         if ((e = record(events, 1, st)) != OZK_OK) return e;
         if (hipError_t he = ozk::launch_split_pair(pa, plan_a, pb, plan_b, dtype, slice_dtype, st))
             return hip_status(he);
+    } else if (ozk::split_duo_ok(plan_a, plan_b, dtype)) {
+        // B's strips and A's row blocks in one launch (the same event rule)
+        if ((e = record(events, 1, st)) != OZK_OK) return e;
+        if (hipError_t he = ozk::launch_split_duo(pa, plan_a, pb, plan_b, dtype, slice_dtype, st))
+            return hip_status(he);
     } else {
         if (hipError_t he = ozk::launch_split(pb, plan_b, dtype, slice_dtype, st))
             return hip_status(he);

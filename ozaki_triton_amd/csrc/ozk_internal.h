@@ -83,6 +83,11 @@ bool split_pair_ok(const SplitPlan &plan_a, const SplitPlan &plan_b, int x_dtype
 hipError_t launch_split_pair(const SplitParams &pa, const SplitPlan &plan_a, const SplitParams &pb,
                              const SplitPlan &plan_b, int x_dtype, int slice_dtype,
                              hipStream_t stream);
+// both splits in one launch where B takes the 256-lane strip kernel and A a
+// 256-lane row configuration
+bool split_duo_ok(const SplitPlan &plan_a, const SplitPlan &plan_b, int x_dtype);
+hipError_t launch_split_duo(const SplitParams &pa, const SplitPlan &plan_a, const SplitParams &pb,
+                            const SplitPlan &plan_b, int x_dtype, int slice_dtype, hipStream_t st);
 
 // Sticky device status (per device): bit 0 is set when a cooperative split
 // wait gave up (the split's scales are then NaN).  read_device_status waits

@@ -417,15 +417,14 @@ OZK_DEV void strip_max(float m[VEC], float (*red)[NW][VEC], int buf, int tid) {
 }
 
 template <typename XT, typename ST, int NT, int KPT>
-__global__ __launch_bounds__(NT) void split_strip_kernel(SplitParams p) {
+OZK_DEV void split_strip_body(const SplitParams &p, int64_t sidx,
+                              float (*red)[NT / 64][16 / sizeof(XT)]) {
     constexpr int VEC = 16 / (int)sizeof(XT);
     constexpr int NG = KPT / 4;     // k-quads per lane
     constexpr int NW = NT / 64;
-    __shared__ float red[2][NW][VEC];
 
     const int tid = threadIdx.x;
     const int64_t strips_per_b = p.rows / VEC;
-    const int64_t sidx = xcd_remap(blockIdx.x, (int64_t)gridDim.x);
     const int64_t b = sidx / strips_per_b;
     const int64_t col0 = (sidx % strips_per_b) * VEC;
 
@@ -520,6 +519,12 @@ __global__ __launch_bounds__(NT) void split_strip_kernel(SplitParams p) {
             }
         }
     }
+}
+
+template <typename XT, typename ST, int NT, int KPT>
+__global__ __launch_bounds__(NT) void split_strip_kernel(SplitParams p) {
+    __shared__ float red[2][NT / 64][16 / sizeof(XT)];
+    split_strip_body<XT, ST, NT, KPT>(p, xcd_remap(blockIdx.x, (int64_t)gridDim.x), red);
 }
 
 // ---------------------------------------------------------------------------
@@ -832,6 +837,26 @@ __global__ __launch_bounds__(kCoopNT) void split_pair_kernel(SplitParams pb, uin
         const int64_t ab = q * ka + (pos - P);
         if (ab < pa.batch * pa.rows) split_rows_body<XT, ST, 4, 1, NC>(pa, ab, red);
     }
+}
+
+// ---------------------------------------------------------------------------
+// Both splits of a matmul in one launch where B's columns take the 256-lane
+// strip kernel and A's rows a 256-lane row configuration (K <= 8192; the
+// shapes where neither split alone fills the chip).  The first nstrips
+// workgroups are B's strips, in the strip kernel's XCD order (hardware puts
+// workgroup g on XCD g % 8 from the first id on), the rest A's row blocks.
+// Neither waits on another workgroup.
+// ---------------------------------------------------------------------------
+template <typename XT, typename ST, int KPT, int GW, int RPB, int NC>
+__global__ __launch_bounds__(256) void split_duo_kernel(SplitParams pb, int64_t nstrips,
+                                                        SplitParams pa) {
+    static_assert(64 * GW * RPB == 256, "a 256-lane row configuration");
+    __shared__ float red_s[2][4][16 / sizeof(XT)];
+    __shared__ float red_r[2][RPB][GW];
+    if ((int64_t)blockIdx.x < nstrips)
+        split_strip_body<XT, ST, 256, KPT>(pb, xcd_remap(blockIdx.x, nstrips), red_s);
+    else
+        split_rows_body<XT, ST, GW, RPB, NC>(pa, (int64_t)blockIdx.x - nstrips, red_r);
 }
 
 // ---------------------------------------------------------------------------
@@ -1571,6 +1596,62 @@ hipError_t launch_split_pair(const SplitParams &pa, const SplitPlan &plan_a,
     case 1: return launch_pair_typed<float>(pa, plan_a, pb, st);
     }
     return hipErrorInvalidValue;
+}
+
+// split_duo_kernel's pairs of strip configuration (kStripCfgs, 256 lanes) and
+// row configuration (kRowCfgs, 256 lanes): the ones plan_split takes for one K
+bool split_duo_ok(const SplitPlan &plan_a, const SplitPlan &plan_b, int x_dtype) {
+    if ((x_dtype != 0 && x_dtype != 1) || debug_overrides().split != kForceSplitNone) return false;
+    if (plan_a.path != kSplitRows || plan_b.path != kSplitStrip) return false;
+    const int s = plan_b.variant, r = plan_a.variant;
+    return (s == 0 && r >= 0 && r <= 2) || (s == 1 && r == 3) || (s == 2 && r == 4) ||
+           (s == 3 && r == 5 && x_dtype == 0);
+}
+
+template <typename XT, typename ST>
+static hipError_t launch_duo_typed(const SplitParams &pa, int r, const SplitParams &pb, int s,
+                                   hipStream_t st) {
+    constexpr int VEC = 16 / (int)sizeof(XT);
+    const int64_t nstrips = pb.batch * (pb.rows / VEC);   // rows % VEC == 0 (strip plan)
+    const int64_t nrows = pa.batch * pa.rows;
+#define OZK_DUO(KPT, GW, RPB, NC)                                                            \
+    hipLaunchKernelGGL((split_duo_kernel<XT, ST, KPT, GW, RPB, NC>),                          \
+                       dim3((unsigned)(nstrips + (nrows + RPB - 1) / RPB)), dim3(256), 0, st, pb, \
+                       nstrips, pa)
+    switch (s * 10 + r) {
+    case 0: OZK_DUO(4, 1, 4, 1); break;
+    case 1: OZK_DUO(4, 1, 4, 2); break;
+    case 2: OZK_DUO(4, 1, 4, 4); break;
+    case 13: OZK_DUO(8, 4, 1, 2); break;
+    case 24: OZK_DUO(16, 4, 1, 4); break;
+    case 35:
+        if constexpr (VEC == 2) { OZK_DUO(32, 4, 1, 8); } else return hipErrorInvalidValue;
+        break;
+    default: return hipErrorInvalidValue;
+    }
+#undef OZK_DUO
+    return hipGetLastError();
+}
+
+template <typename XT>
+static hipError_t launch_duo_x(const SplitParams &pa, int r, const SplitParams &pb, int s,
+                               int slice_dtype, hipStream_t st) {
+    switch (slice_dtype) {
+    case 4: return launch_duo_typed<XT, int8_t>(pa, r, pb, s, st);
+    case 2: return launch_duo_typed<XT, _Float16>(pa, r, pb, s, st);
+    case 3: return launch_duo_typed<XT, __bf16>(pa, r, pb, s, st);
+    case 1: return launch_duo_typed<XT, float>(pa, r, pb, s, st);
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_split_duo(const SplitParams &pa, const SplitPlan &plan_a, const SplitParams &pb,
+                            const SplitPlan &plan_b, int x_dtype, int slice_dtype,
+                            hipStream_t st) {
+    if (!split_duo_ok(plan_a, plan_b, x_dtype)) return hipErrorInvalidValue;
+    if (pa.batch * pa.rows == 0 || pb.batch * pb.rows == 0 || pa.L == 0) return hipSuccess;
+    return x_dtype == 0 ? launch_duo_x<double>(pa, plan_a.variant, pb, plan_b.variant, slice_dtype, st)
+                        : launch_duo_x<float>(pa, plan_a.variant, pb, plan_b.variant, slice_dtype, st);
 }
 
 hipError_t read_device_status(unsigned *out, bool clear, hipStream_t st) {

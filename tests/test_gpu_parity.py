@@ -823,6 +823,50 @@ def test_ring_kernel_dtypes(oracle, gpu, L, sdt, out, force):
         assert_bitwise_equal(C[b], want, f"ring L{L} {sdt} {out} b{b}")
 
 
+@pytest.mark.parametrize("sdt", [torch.int8, torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("xdt", [torch.float64, torch.float32])
+@pytest.mark.parametrize("a_shape,b_shape", [((2, 96, 200), (2, 200, 72)),    # strip 0, rows 0
+                                             ((40, 400), (400, 136)),         # strip 0, rows 1
+                                             ((3, 50, 1000), (1000, 24)),     # strip 0, rows 2
+                                             ((64, 2000), (2000, 48)),        # strip 1, rows 3
+                                             ((33, 4000), (4000, 40)),        # strip 2, rows 4
+                                             ((20, 8000), (8000, 16))])       # strip 3, rows 5
+def test_split_duo_one_launch(oracle, gpu, sdt, xdt, a_shape, b_shape, force):
+    """ozaki_matmul's two splits in one launch (split_duo_kernel: B's columns
+    by the 256-lane strip kernel, A's rows by a 256-lane row configuration,
+    the strips first): the library records the B phase's two events at one
+    point; C equals the two-launch pipeline's (a forced split kernel turns
+    the single launch off) bit for bit, and the oracle's on sampled blocks
+    (int8 bit-exact, float slices within the fp32 accumulation bound).  The
+    pairs of configurations follow K; the last (K <= 8192) is fp64 only."""
+    import ozaki_triton_amd as ozk
+    from ozaki_triton_amd.ozaki import _ozaki_matmul_impl
+    if xdt == torch.float32 and a_shape[-1] > 4096:
+        pytest.skip("fp32 columns over 4096 take the 512-lane strip kernel")
+    A, B = c3_like(a_shape, b_shape, seed=sum(a_shape) + sum(b_shape) + 7, dtype=xdt)
+    Ad, Bd = A.to(gpu), B.to(gpu)
+    L = 3
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    for e in evs:
+        e.record()
+    C1 = _ozaki_matmul_impl(Ad, Bd, L, sdt, False, evs)
+    torch.cuda.synchronize()
+    assert evs[0].elapsed_time(evs[1]) < 0.02, "two launches where one was expected"
+    force(split="strip")
+    C2 = ozk.ozaki_matmul(Ad, Bd, L, sdt)
+    torch.cuda.synchronize()
+    assert_bitwise_equal(to_np(C1), to_np(C2), f"one launch vs two {xdt} {sdt} {a_shape}")
+    C_np, A_np, B_np = to_np(C1), to_np(A), to_np(B)
+    M, N = a_shape[-2], b_shape[-1]
+    rows, cols = sample_indices(M, 16, 5), sample_indices(N, 16, 6)
+    for b in range(C_np.shape[0] if C_np.ndim == 3 else 1):
+        Cb = C_np[b] if C_np.ndim == 3 else C_np
+        Ab = A_np[b] if A_np.ndim == 3 else A_np
+        Bb = B_np[b] if B_np.ndim == 3 else B_np
+        check_block_vs_oracle(oracle, ozk, Cb, Ab, Bb, rows, cols, L, sdt, xdt,
+                              f"duo {xdt} {sdt} {a_shape} b{b}")
+
+
 @pytest.mark.parametrize("xdt", [torch.float64, torch.float32])
 def test_split_coop_wait_timeout(oracle, gpu, xdt, force):
     """The cooperative split's bounded wait: forced from the host to look for a
