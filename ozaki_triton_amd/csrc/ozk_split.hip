@@ -1256,10 +1256,15 @@ static SplitPlan plan_split_raw(const SplitParams &p, int x_dtype, int slice_dty
     // columns of 64 KB and more: the cooperative kernel (the strip kernel's
     // 16-byte row pieces cost more than the exchange from there on; measured
     // over K = 1024..16384, N = 1024..8192, fp64 / fp32), and fp64 columns of
-    // 32 KB into int8 slices when there are at least 2048 of them (0.90-0.94x
-    // the strip kernel's time at K = 4096, N = 2048..8192; 1.04x at N = 1024;
-    // fp16 slices gain nothing there, fp32 columns below 64 KB lose 1.1-1.3x);
-    // a forced coop takes it for any length it holds
+    // 32 KB into 1 or 2 int8 slices when there are at least 2048 of them
+    // (alone, 0.90-0.94x the strip kernel's time at K = 4096, N = 2048..8192;
+    // 1.04x at N = 1024; fp16 slices gain nothing there, fp32 columns below
+    // 64 KB lose 1.1-1.3x).  With 3 or more slices the strip kernel and A's
+    // rows share one launch (split_duo_kernel), and the whole call is faster
+    // that way: at K = 4096, 4 slices, 83.3 / 370.8 / 1163 us against 89.2 /
+    // 394.2 / 1197 for M x N = 128 x 2048, 1024 x 4096, 2048 x 8192, while 1
+    // slice is 7-11% slower and 2 even.  A forced coop takes it for any length
+    // it holds
     const bool coop_fits = cols_ok && coop_members(p.K, xsz, 8) <= kCoopMaxP;
     // columns too long for 32 chunks of 128-byte groups: 32-byte groups, whose
     // chunks hold 4x the rows, when the cooperative kernel is forced.  By
@@ -1270,8 +1275,8 @@ static SplitPlan plan_split_raw(const SplitParams &p, int x_dtype, int slice_dty
     const bool coop2_fits = cols_ok && !coop_fits && coop_members(p.K, xsz, 2) <= kCoopMaxP;
     const bool other = forced(kForceSplitStrip) || forced(kForceSplitTranspose) || forced(kForceSplitGeneric);
     const bool coop_long = p.K * xsz >= kCoopMinColumnBytes ||
-                           (xsz == 8 && ssz == 1 && p.K * xsz >= kCoopMinColumnBytes / 2 &&
-                            p.batch * p.rows >= 2048);
+                           (xsz == 8 && ssz == 1 && p.L <= 2 &&
+                            p.K * xsz >= kCoopMinColumnBytes / 2 && p.batch * p.rows >= 2048);
     if (coop_fits && (forced(kForceSplitCoop) || (!other && coop_long))) return {kSplitCoop, 8};
     if (coop2_fits && forced(kForceSplitCoop)) return {kSplitCoop, 2};
     if (cols_ok && !forced(kForceSplitTranspose) && !forced(kForceSplitGeneric)) {

@@ -444,6 +444,29 @@ def test_split_plan_for_unaligned_pointers_fits_the_query(xd, sd, K, rows):
         assert need <= nb.value and name == "generic", (name, need)
 
 
+def test_column_split_plan_by_length_and_slices():
+    """B's columns (the B^T view) by column length: the cooperative kernel from
+    64 KB; fp64 columns of 32 KB into 1 or 2 int8 slices, 2048 or more of
+    them, too; otherwise (3 or more slices, fewer columns, fp16 slices, fp32)
+    the strip kernel, which then shares a launch with A's rows."""
+    from ozaki_triton_amd import _lib
+    L = _lib.load()
+
+    def plan(xd, sd, N, K, nsp):
+        return _split_plan(L, 0x10000, xd, 1, N, K, [K * N, 1, N], nsp, sd, 0x20000,
+                           [nsp * N * K, N * K, K, 1])[0]
+    F64, F32, I8, F16 = _lib.OZK_F64, _lib.OZK_F32, _lib.OZK_I8, _lib.OZK_F16
+    assert plan(F64, I8, 8192, 8192, 4) == "coop"        # config 3: 64 KB columns
+    assert plan(F64, I8, 2048, 4096, 1) == "coop"        # 32 KB, 2048 columns, 1-2 slices
+    assert plan(F64, I8, 2048, 4096, 2) == "coop"
+    assert plan(F64, I8, 2048, 4096, 3) == "strip"       # 3-4 slices: strip + rows, one launch
+    assert plan(F64, I8, 2048, 4096, 4) == "strip"
+    assert plan(F64, I8, 1024, 4096, 2) == "strip"       # under 2048 columns
+    assert plan(F64, F16, 2048, 4096, 2) == "strip"      # fp16 slices
+    assert plan(F32, I8, 2048, 4096, 2) == "strip"       # 16 KB fp32 columns
+    assert plan(F32, I8, 2048, 16384, 2) == "coop"       # 64 KB fp32 columns
+
+
 def test_matmul_workspace_covers_unaligned_operands():
     """ozk_matmul carves the split scratch from the size its query returned;
     with unaligned operands the plans still fit (checked again in ozk_matmul,

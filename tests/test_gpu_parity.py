@@ -1255,19 +1255,21 @@ def test_tile_table_shrink_steps(oracle, gpu, sdt, L, batch, M, N):
                               torch.float32, f"L{L} {sdt} b{b} {M}x{N}")
 
 
+@pytest.mark.parametrize("L", [2, 4])
 @pytest.mark.parametrize("xdt,sdt", COMBOS)
 @pytest.mark.parametrize("batch,N,K", [(1, 2048, 4096), (2, 1024, 6000), (1, 1024, 4096)])
-def test_split_columns_default_plan(oracle, gpu, xdt, sdt, batch, N, K):
+def test_split_columns_default_plan(oracle, gpu, xdt, sdt, batch, N, K, L):
     """B's columns through the transposed view with the planner's own choice
-    (no kernel forced): fp64 columns from 32 KB into int8 slices, 2048 or more
-    of them, take the cooperative kernel; fewer, fp32 columns or fp16 slices
-    the strip kernel."""
+    (no kernel forced): fp64 columns from 32 KB into 1 or 2 int8 slices, 2048
+    or more of them, take the cooperative kernel; more slices, fewer columns,
+    fp32 columns or fp16 slices the strip kernel (test_api_cpu checks the
+    plans)."""
     import ozaki_triton_amd as ozk
     g = torch.Generator().manual_seed(batch * N + K)
     B = torch.randn(batch, K, N, generator=g, dtype=torch.float64)
     B = B * torch.pow(2.0, torch.randint(-8, 9, (batch, 1, N), generator=g).double())
-    _check_split(oracle, ozk, B.to(xdt).to(gpu).transpose(-1, -2), 4, sdt,
-                 f"default {xdt} {sdt} b{batch} {N}x{K}")
+    _check_split(oracle, ozk, B.to(xdt).to(gpu).transpose(-1, -2), L, sdt,
+                 f"default {xdt} {sdt} b{batch} {N}x{K} L{L}")
 
 
 @pytest.mark.parametrize("kernel", ["", "dma", "ring", "pair", "ad", "staged", "wide", "wide4",
