@@ -173,7 +173,8 @@ int ozk_cross_gemm(const void *A_slices, const int64_t a_strides[4], const void 
  * ozk_matmul_workspace_bytes() long), so the call allocates nothing and may be
  * captured in a HIP graph.  events: NULL, or 4 hipEvent_t (each may be NULL)
  * recorded on `stream` before the B split, before the A split, before the
- * cross-GEMM and after it.  Returns OZK_ERR_ALPHA when K is too large for
+ * cross-GEMM and after it (where both splits run in one launch, the first
+ * two mark the same point).  Returns OZK_ERR_ALPHA when K is too large for
  * the slice dtype (the reference asserts) and OZK_ERR_SHAPE for K = 0 (the
  * reference's log2(0) raises).
  */
