@@ -23,7 +23,10 @@ LIB_NAME = "libozaki_amd.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 ARCH = os.environ.get("OZK_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["ozk_api.cpp", "ozk_split.hip", "ozk_gemm.hip"]
+# the cross-GEMM kernels are instantiated in one unit per slice dtype (the
+# int8 one is the largest), so that they compile in parallel
+SOURCES = ["ozk_gemm_i8.hip", "ozk_gemm_f16.hip", "ozk_gemm_bf16.hip", "ozk_gemm_f32.hip",
+           "ozk_split.hip", "ozk_api.cpp", "ozk_gemm.hip"]
 
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -1,2769 +1,9 @@
-// ozk_gemm.hip -- the fused cross-GEMM of ozaki_triton.py:306-452 as an
-// LDS-staged MFMA kernel for gfx950.
-//
-//   C[m, n] = sum_{i<L} sum_{j<L} fl32(fl32(fl32(acc_ij[m, n]) * sa_i[m]) * sb_j[n])
-//   acc_ij  = A_i[m, :] . B_j[:, n]        (int8: exact int32, fp16: fp32 MFMA)
-//   the outer sum runs i-major, j-minor from +0 in the output's accumulator
-//   dtype (fp64 for fp64 output, fp32 for every other output dtype), exactly as
-//   the reference; kernels are templated on the slice type (int8, fp16, bf16,
-//   fp32) and that accumulator type, and store_c converts to C's dtype.
-//
-// Design (one workgroup = 256 lanes = 4 waves in a 2 x 2 grid):
-//   * Every wave owns a (32*MI) x (32*NI) block of C and ALL L*L slice pairs
-//     for it, so each output element's L*L accumulators live in one lane and
-//     the ordered epilogue needs no cross-wave traffic.
-//   * v_mfma_i32_32x32x32_i8 / v_mfma_f32_32x32x16_f16 / _bf16: 32 bytes of K
-//     per row per instruction, 16 accumulator registers per lane (fp32 slices:
-//     four v_mfma_f32_32x32x2_f32 per 32 bytes).
-//   * Both operands are K-contiguous ([L, M, K] and B^T = [L, N, K]); a stage
-//     holds 128 bytes of K for all L*(BM+BN) rows, staged global -> VGPR ->
-//     LDS with the next stage's loads in flight during the current MFMAs
-//     (double-buffered LDS, one barrier per stage).  16-byte chunks are
-//     XOR-swizzled by row so ds_read_b128 / ds_write_b128 are bank-conflict
-//     free.
-//   * int8 products are exact integers, so the order in which K is fed to
-//     the MFMA cannot change acc_ij: the int8 result is bit-identical to the
-//     reference for any tiling.
-//   * Workgroups are remapped so each XCD (own L2) processes a contiguous
-//     range of tiles, grouped GROUP_M tile-rows at a time.
-#include <atomic>
-#include <stdlib.h>
-#include <string.h>
-
-#include <type_traits>
-
-#include "ozk_common.h"
-#include "ozk_internal.h"
+// ozk_gemm.hip -- cross-GEMM planner (the tile table that replaces the
+// reference's autotuner, ozaki_triton.py:263-304), split-K set-up, the pack
+// and zero kernels, and the dispatch to the per-slice-dtype kernel units.
+#include "ozk_gemm_kernels.h"
 
 namespace ozk {
-
-typedef int i32x4 __attribute__((ext_vector_type(4)));
-typedef int i32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-
-template <typename ST> struct Mfma;
-template <> struct Mfma<int8_t> {
-    using Acc = i32x16;
-    using Elem = int;
-    static constexpr bool kExactAcc = true;    // int32 sums: exact in any order
-    OZK_DEV static Acc zero() { return Acc{0}; }
-    OZK_DEV static Acc run(i32x4 a, i32x4 b, Acc c) {
-        return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
-    }
-    OZK_DEV static float to_f32(int x) { return (float)x; }   // RNE int32 -> fp32
-};
-template <> struct Mfma<_Float16> {
-    using Acc = f32x16;
-    using Elem = float;
-    static constexpr bool kExactAcc = false;
-    OZK_DEV static Acc zero() { return Acc{0.0f}; }
-    OZK_DEV static Acc run(i32x4 a, i32x4 b, Acc c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
-                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-    }
-    OZK_DEV static float to_f32(float x) { return x; }
-};
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-template <> struct Mfma<__bf16> {
-    using Acc = f32x16;
-    using Elem = float;
-    static constexpr bool kExactAcc = false;
-    OZK_DEV static Acc zero() { return Acc{0.0f}; }
-    OZK_DEV static Acc run(i32x4 a, i32x4 b, Acc c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-    }
-    OZK_DEV static float to_f32(float x) { return x; }
-};
-// fp32 slices: a 16-byte fragment is 4 floats; lane (row, h) of the 32x32x2
-// MFMA supplies k = h of that instruction, so MFMA q contracts component q of
-// both operands' fragments (the same k on A and B), 4 MFMAs per fragment.
-// The fragment is bit-cast as a whole: with this compiler, bit-casting the
-// int vector's elements one by one made all four MFMAs read component 0.
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-template <> struct Mfma<float> {
-    using Acc = f32x16;
-    using Elem = float;
-    static constexpr bool kExactAcc = false;
-    OZK_DEV static Acc zero() { return Acc{0.0f}; }
-    OZK_DEV static Acc run(i32x4 a, i32x4 b, Acc c) {
-        const f32x4 fa = __builtin_bit_cast(f32x4, a), fb = __builtin_bit_cast(f32x4, b);
-        c = __builtin_amdgcn_mfma_f32_32x32x2f32(fa.x, fb.x, c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_32x32x2f32(fa.y, fb.y, c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_32x32x2f32(fa.z, fb.z, c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_32x32x2f32(fa.w, fb.w, c, 0, 0, 0);
-        return c;
-    }
-    OZK_DEV static float to_f32(float x) { return x; }
-};
-
-// Final store of the outer accumulator (ozaki_triton.py:452): fp64 output is
-// the fp64 accumulator itself; otherwise the fp32 accumulator is stored as
-// fp32, rounded to nearest even for fp16 / bf16, or truncated toward zero and
-// saturated for int8 (NVIDIA's float-to-integer conversion; NaN -> 0).
-OZK_DEV void store_c(const GemmParams &p, int64_t idx, double v) { ((double *)p.C)[idx] = v; }
-// partial of an earlier launch (num_splits > 4 runs with an fp64 or fp32 C)
-OZK_DEV double load_c(const GemmParams &p, int64_t idx, double) { return ((const double *)p.C)[idx]; }
-OZK_DEV float load_c(const GemmParams &p, int64_t idx, float) { return ((const float *)p.C)[idx]; }
-OZK_DEV void store_c(const GemmParams &p, int64_t idx, float v) {
-    switch (p.out_dtype) {
-    case 1: ((float *)p.C)[idx] = v; break;
-    case 2: ((_Float16 *)p.C)[idx] = (_Float16)v; break;
-    case 3: ((uint16_t *)p.C)[idx] = (uint16_t)((v != v) ? 0x7FC0u : f32_to_bf16_bits(v)); break;
-    default: {
-        const float t = (v != v) ? 0.0f : fminf(fmaxf(truncf(v), -128.0f), 127.0f);
-        ((int8_t *)p.C)[idx] = (int8_t)(int)t;
-    }
-    }
-}
-
-OZK_DEV int64_t xcd_remap_gemm(int64_t g, int64_t n) {
-    const int64_t q = n / 8;
-    if (g >= q * 8) return g;
-    return (g % 8) * q + g / 8;
-}
-
-constexpr int kRowBytes = 128;   // bytes of K per row per stage
-constexpr int kChunks = kRowBytes / 16;
-
-template <int L, int MI, int NI> struct GemmShape {
-    static constexpr int BM = 64 * MI;
-    static constexpr int BN = 64 * NI;
-    static constexpr int A_ROWS = L * BM;
-    static constexpr int B_ROWS = L * BN;
-    static constexpr int ROWS = A_ROWS + B_ROWS;
-    static constexpr int STAGE = ROWS * kRowBytes;
-    static constexpr int LOADS = ROWS * kChunks / 256;   // 16-byte chunks per lane per stage
-    static constexpr int A_LOADS = A_ROWS * kChunks / 256;
-    static constexpr int LDS_BYTES = 2 * STAGE;
-    static_assert((ROWS * kChunks) % 256 == 0, "stage must split evenly over 256 lanes");
-};
-
-// gfx950's LDS serves a ds_read_b128 16 lanes (256 bytes, all 64 banks) per
-// cycle.  For 128-byte rows, rows r and r + 2 share banks, so the 16-byte
-// chunk is XORed with (r >> 1) & 7: the 16 rows one pass reads land on 16
-// distinct chunk columns.
-OZK_DEV int swz(int row, int chunk) {
-    return row * kRowBytes + ((chunk ^ ((row >> 1) & 7)) << 4);
-}
-
-template <typename ST, int L, int MI, int NI, typename AccT>
-__global__ __launch_bounds__(256, 1) void cross_gemm_kernel(GemmParams p, int group_m) {
-    using Sh = GemmShape<L, MI, NI>;
-    using MF = Mfma<ST>;
-    using Acc = typename MF::Acc;
-    using OA = AccT;   // outer accumulator: fp64 for fp64 output, else fp32 (store_c)
-    constexpr int BM = Sh::BM, BN = Sh::BN;
-    constexpr int ES = (int)sizeof(ST);
-    extern __shared__ __attribute__((aligned(16))) char smem[];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int h = lane >> 5, lr = lane & 31;
-
-    // ---- tile coordinates ----
-    const int64_t tiles_m = (p.M + BM - 1) / BM;
-    const int64_t tiles_n = (p.N + BN - 1) / BN;
-    const int64_t tiles = tiles_m * tiles_n;
-    const int64_t g = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
-    const int64_t bidx = g / tiles;
-    const int64_t t = g % tiles;
-    const int64_t width = (int64_t)group_m * tiles_n;
-    const int64_t first_m = (t / width) * group_m;
-    const int64_t gsz = (tiles_m - first_m < group_m) ? (tiles_m - first_m) : group_m;
-    const int64_t tm = first_m + (t % width) % gsz;
-    const int64_t tn = (t % width) / gsz;
-    const int64_t m0 = tm * BM, n0 = tn * BN;
-
-    const int64_t kbytes = p.K * ES;
-    const int nkb = (int)((kbytes + kRowBytes - 1) / kRowBytes);
-
-    // ---- per-lane load descriptors: lane loads chunk (tid % 8) of rows
-    //      tid/8 + 32*u, u < LOADS ----
-    const int lch = tid & 7;
-    const int lrow = tid >> 3;
-    const char *Ab = (const char *)p.A + (bidx * p.as_b) * ES;
-    const char *Bb = (const char *)p.B + (bidx * p.bs_b) * ES;
-
-    auto load_stage = [&](int kb, i32x4 *stg) {
-        const int64_t kofs = (int64_t)kb * kRowBytes + lch * 16;
-        const bool kok = kofs < kbytes;
-#pragma unroll
-        for (int u = 0; u < Sh::LOADS; ++u) {
-            const char *ptr;
-            bool ok;
-            if (u < Sh::A_LOADS) {
-                constexpr int per = BM / 32;
-                const int i = u / per;
-                const int64_t m = m0 + lrow + 32 * (u % per);
-                ok = kok && (m < p.M);
-                ptr = Ab + ((int64_t)i * p.as_l + m * p.as_m) * ES + kofs;
-            } else {
-                constexpr int per = BN / 32;
-                const int ub = u - Sh::A_LOADS;
-                const int j = ub / per;
-                const int64_t n = n0 + lrow + 32 * (ub % per);
-                ok = kok && (n < p.N);
-                ptr = Bb + ((int64_t)j * p.bs_l + n * p.bs_n) * ES + kofs;
-            }
-            stg[u] = ok ? *(const i32x4 *)ptr : i32x4{0, 0, 0, 0};
-        }
-    };
-    auto store_stage = [&](char *buf, const i32x4 *stg) {
-#pragma unroll
-        for (int u = 0; u < Sh::LOADS; ++u) {
-            const int row = lrow + 32 * u;
-            *(i32x4 *)(buf + swz(row, lch)) = stg[u];
-        }
-    };
-
-    Acc acc[L][L][MI][NI];
-#pragma unroll
-    for (int i = 0; i < L; ++i)
-#pragma unroll
-        for (int j = 0; j < L; ++j)
-#pragma unroll
-            for (int a = 0; a < MI; ++a)
-#pragma unroll
-                for (int c = 0; c < NI; ++c) acc[i][j][a][c] = MF::zero();
-
-    i32x4 stg[Sh::LOADS];
-    if (nkb > 0) {
-        load_stage(0, stg);
-        store_stage(smem, stg);
-    }
-    __syncthreads();
-
-    for (int kb = 0; kb < nkb; ++kb) {
-        const bool more = kb + 1 < nkb;
-        if (more) load_stage(kb + 1, stg);
-        const char *buf = smem + (kb & 1) * Sh::STAGE;
-#pragma unroll
-        for (int kk = 0; kk < kChunks / 2; ++kk) {
-            const int ch = 2 * kk + h;
-            i32x4 af[L][MI], bf[L][NI];
-#pragma unroll
-            for (int i = 0; i < L; ++i)
-#pragma unroll
-                for (int a = 0; a < MI; ++a) {
-                    const int row = i * BM + wm * 32 * MI + a * 32 + lr;
-                    af[i][a] = *(const i32x4 *)(buf + swz(row, ch));
-                }
-#pragma unroll
-            for (int j = 0; j < L; ++j)
-#pragma unroll
-                for (int c = 0; c < NI; ++c) {
-                    const int row = Sh::A_ROWS + j * BN + wn * 32 * NI + c * 32 + lr;
-                    bf[j][c] = *(const i32x4 *)(buf + swz(row, ch));
-                }
-#pragma unroll
-            for (int i = 0; i < L; ++i)
-#pragma unroll
-                for (int j = 0; j < L; ++j)
-#pragma unroll
-                    for (int a = 0; a < MI; ++a)
-#pragma unroll
-                        for (int c = 0; c < NI; ++c)
-                            acc[i][j][a][c] = MF::run(af[i][a], bf[j][c], acc[i][j][a][c]);
-        }
-        if (more) store_stage(smem + ((kb + 1) & 1) * Sh::STAGE, stg);
-        __syncthreads();
-    }
-
-    // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
-    const float *sab = p.sa + bidx * p.sas_b;
-    const float *sbb = p.sb + bidx * p.sbs_b;
-    const int64_t cbase = bidx * p.cs_b;
-#pragma unroll
-    for (int c = 0; c < NI; ++c) {
-        const int64_t col = n0 + wn * 32 * NI + c * 32 + lr;
-        const bool cok = col < p.N;
-        float sbv[L];
-#pragma unroll
-        for (int j = 0; j < L; ++j) sbv[j] = cok ? sbb[j * p.sbs_l + col * p.sbs_n] : 0.0f;
-#pragma unroll
-        for (int a = 0; a < MI; ++a) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t row = m0 + wm * 32 * MI + a * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (cok && row < p.M) {
-                    OA out = (OA)0;
-#pragma unroll
-                    for (int i = 0; i < L; ++i) {
-                        const float sai = sab[i * p.sas_l + row * p.sas_m];
-#pragma unroll
-                        for (int j = 0; j < L; ++j) {
-                            const float x = MF::to_f32(acc[i][j][a][c][r]);
-                            const float t1 = x * sai;
-                            const float t2 = t1 * sbv[j];
-                            out = out + (OA)t2;
-                        }
-                    }
-                    store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
-                }
-            }
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Pipelined variant: global -> LDS by buffer_load ... lds (no VGPR staging),
-// a ring of DMA_STAGES LDS stages of 64 bytes of K per row, loads issued
-// DMA_STAGES-1 stages ahead.  Lane i of a DMA instruction writes LDS bytes
-// [16 i, 16 i + 16) of that instruction's 1 KB window, so the XOR swizzle is
-// applied by choosing which 16-byte chunk of global memory each lane fetches.
-// Out-of-range rows and K tails are fetched from a buffer offset beyond
-// num_records, which the hardware returns as zeros.
-// ---------------------------------------------------------------------------
-constexpr int kDmaRowBytes = 64;     // A-direct kernel stage rows
-constexpr int kDmaRB = 128;          // 2 x 2 DMA kernel stage rows (bytes of K; 64 also works)
-constexpr int kDmaStages = (kDmaRB == 64) ? 4 : 2;   // LDS ring slots
-
-template <int L, int MI, int NI> struct DmaShape {
-    static constexpr int BM = 64 * MI;
-    static constexpr int BN = 64 * NI;
-    static constexpr int A_ROWS = L * BM;
-    static constexpr int ROWS = L * (BM + BN);
-    static constexpr int STAGE = ROWS * kDmaRB;
-    static constexpr int LPS = STAGE / (4 * 1024);      // DMA instructions per wave per stage
-    static constexpr int LDS_BYTES = kDmaStages * STAGE;
-    static_assert(STAGE % 4096 == 0, "stage must be a whole number of 1 KB wave windows");
-};
-
-// LDS byte offset of logical 16-byte chunk c of row r inside one stage.
-// gfx950 serves a ds_read_b128 16 lanes (256 bytes = all 64 banks) per pass;
-// the XOR spreads the 16 consecutive rows of one pass over all banks
-// (64-byte rows repeat banks every 4 rows, 128-byte rows every 2).
-template <int RB> OZK_DEV int rswz(int r, int c) {
-    if constexpr (RB == 64) return r * 64 + ((c ^ ((r >> 2) & 3)) << 4);
-    else return r * 128 + ((c ^ ((r >> 1) & 7)) << 4);
-}
-OZK_DEV int dswz(int r, int c) { return rswz<64>(r, c); }
-
-// s_waitcnt with only the vector-memory counter limited to n
-template <int N> OZK_DEV void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
-}
-
-// Workgroup execution barrier without the release fence of __syncthreads()
-// (which would wait for every outstanding global load, i.e. drain the DMA
-// prefetch ring).  Callers make their own DMA writes complete with
-// wait_vmcnt first; the memory clobber keeps the compiler from moving LDS
-// accesses across the barrier.
-OZK_DEV void exec_barrier() { asm volatile("s_barrier" ::: "memory"); }
-
-// ---------------------------------------------------------------------------
-// Split-K hand-off (ring and wide kernels on grids too small to fill the
-// chip).  A tile's 128-byte K stages are cut into p.ksplit ranges of
-// p.kb_per_split stages, one workgroup each (consecutive workgroup ids).
-// Every range stores its raw accumulators (for int8 slices the exact int32
-// dot products) to p.kpart, lane-contiguous per register, and counts itself
-// in the tile's arrival counter; the range that arrives last reads all
-// ranges' accumulators back, adds them in range order (from zero) and goes
-// on to the epilogue, the others exit.  No workgroup waits for another, and
-// C does not depend on which range arrives last.
-// ---------------------------------------------------------------------------
-constexpr int kSplitKWaves = 8;   // both kernels run 8 waves
-// The lane index read where it is used (an opaque read the compiler cannot
-// hoist), so no split-K address is held in registers through the K loop.
-OZK_DEV int lane_here() {
-    int l;
-    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
-    return l;
-}
-OZK_DEV uint32_t *splitk_slot(const GemmParams &p, int64_t tile, int range, int wave, int regs,
-                              int lane) {
-    return p.kpart + (((tile * p.ksplit + range) * kSplitKWaves + wave) * regs) * 64 + lane;
-}
-// The accumulators go through agent-scope stores and loads, which write
-// through to, and read from, the level every XCD shares: once a store has
-// completed (vmcnt), every later agent-scope load sees it, with no L2
-// write-back or invalidation (a fence here costs a write-back of the whole
-// L2 per wave).
-OZK_DEV void splitk_put(uint32_t *dst, uint32_t v) {
-    __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-OZK_DEV uint32_t splitk_get(const uint32_t *src) {
-    return __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// one accumulator tile (16 registers, 64 words apart): all 16 loads are
-// issued before the first is used
-template <typename Acc> OZK_DEV Acc splitk_get16(const uint32_t *src) {
-    i32x16 u;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) u[r] = (int)splitk_get(src + r * 64);
-    return __builtin_bit_cast(Acc, u);
-}
-// Called by every wave after it stored its accumulators: true in the
-// workgroup that arrived last.  Every wave's stores complete before the
-// barrier, and the counter is incremented after it, so the range that reads
-// ksplit - 1 from the counter finds every range's accumulators in place.
-OZK_DEV bool splitk_arrive(const GemmParams &p, int64_t tile, int *flag) {
-    wait_vmcnt<0>();
-    exec_barrier();
-    if (threadIdx.x == 0)
-        *flag = (int)__hip_atomic_fetch_add(p.kcount + tile, 1u, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0xC07F);   // the flag's LDS write
-    exec_barrier();
-    return *flag == p.ksplit - 1;
-}
-
-template <typename ST, int L, int MI, int NI, typename AccT>
-__global__ __launch_bounds__(256, 1) void cross_gemm_dma_kernel(GemmParams p, int group_m,
-                                                                uint32_t a_records,
-                                                                uint32_t b_records) {
-    using Sh = DmaShape<L, MI, NI>;
-    using MF = Mfma<ST>;
-    using Acc = typename MF::Acc;
-    using OA = AccT;   // outer accumulator: fp64 for fp64 output, else fp32 (store_c)
-    constexpr int BM = Sh::BM, BN = Sh::BN;
-    constexpr int ES = (int)sizeof(ST);
-    constexpr uint32_t kOOB = 0x80000000u;
-    extern __shared__ __attribute__((aligned(16))) char smem[];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    // wave index is uniform across the wave; saying so keeps the LDS-DMA
-    // destination (M0) and the A/B choice per instruction scalar
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
-    const int h = lane >> 5, lr = lane & 31;
-
-    const int64_t tiles_m = (p.M + BM - 1) / BM;
-    const int64_t tiles_n = (p.N + BN - 1) / BN;
-    const int64_t tiles = tiles_m * tiles_n;
-    const int64_t g = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
-    const int64_t bidx = g / tiles;
-    const int64_t t = g % tiles;
-    const int64_t width = (int64_t)group_m * tiles_n;
-    const int64_t first_m = (t / width) * group_m;
-    const int64_t gsz = (tiles_m - first_m < group_m) ? (tiles_m - first_m) : group_m;
-    const int64_t tm = first_m + (t % width) % gsz;
-    const int64_t tn = (t % width) / gsz;
-    const int64_t m0 = tm * BM, n0 = tn * BN;
-
-    const uint32_t kbytes = (uint32_t)(p.K * ES);
-    const int nkb = (int)((kbytes + kDmaRB - 1) / kDmaRB);
-    constexpr int CH = kDmaRB / 16;       // 16-byte chunks per row
-    constexpr int STEPS = kDmaRB / 32;    // 32-byte MFMA K steps per stage
-
-    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)((const char *)p.A + bidx * p.as_b * ES), (short)0, (int)a_records, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)((const char *)p.B + bidx * p.bs_b * ES), (short)0, (int)b_records, 0x00020000);
-
-    // Per-lane source offsets (bytes, excluding the stage's K offset) for the
-    // LPS DMA instructions of this wave; kOOB marks rows outside the matrix.
-    // A 1 KB DMA window covers whole rows and A_ROWS is a multiple of 64,
-    // so each instruction reads only A or only B (uniform per wave).
-    uint32_t src[Sh::LPS];
-    int chunk[Sh::LPS];
-#pragma unroll
-    for (int q = 0; q < Sh::LPS; ++q) {
-        const int pos = (wave * Sh::LPS + q) * 64 + lane;   // 16-byte unit in the stage
-        const int r = pos / CH;
-        const int pc = pos % CH;
-        chunk[q] = (kDmaRB == 64) ? (pc ^ ((r >> 2) & 3)) : (pc ^ ((r >> 1) & 7));
-        if (r < Sh::A_ROWS) {
-            const int i = r / BM;
-            const int64_t m = m0 + r % BM;
-            src[q] = (m < p.M) ? (uint32_t)(((int64_t)i * p.as_l + m * p.as_m) * ES) : kOOB;
-        } else {
-            const int rb = r - Sh::A_ROWS;
-            const int j = rb / BN;
-            const int64_t n = n0 + rb % BN;
-            src[q] = (n < p.N) ? (uint32_t)(((int64_t)j * p.bs_l + n * p.bs_n) * ES) : kOOB;
-        }
-    }
-
-    auto issue_one = [&](int kb, int q) {
-        char *dst = smem + (kb % kDmaStages) * Sh::STAGE + wave * Sh::LPS * 1024;
-        const uint32_t kofs = (uint32_t)kb * kDmaRB + chunk[q] * 16;
-        const uint32_t vo = (src[q] == kOOB || kofs >= kbytes) ? kOOB : src[q] + kofs;
-        auto *ldsp = (__attribute__((address_space(3))) void *)(dst + q * 1024);
-        const bool isA = (wave * Sh::LPS + q) * (1024 / kDmaRB) < Sh::A_ROWS;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(isA ? rA : rB, ldsp, 16, vo, 0, 0, 0);
-    };
-    auto issue_stage = [&](int kb) {
-#pragma unroll
-        for (int q = 0; q < Sh::LPS; ++q) issue_one(kb, q);
-    };
-
-    Acc acc[L][L][MI][NI];
-#pragma unroll
-    for (int i = 0; i < L; ++i)
-#pragma unroll
-        for (int j = 0; j < L; ++j)
-#pragma unroll
-            for (int a = 0; a < MI; ++a)
-#pragma unroll
-                for (int c = 0; c < NI; ++c) acc[i][j][a][c] = MF::zero();
-
-#pragma unroll
-    for (int s = 0; s < kDmaStages - 1; ++s)
-        if (s < nkb) issue_stage(s);
-
-    // Fragments of one 32-byte K step: this wave's A rows for every slice i
-    // and B rows for every slice j.  Read r (r < L*MI: A, else B) of step kk.
-    struct Frags {
-        i32x4 a[L][MI];
-        i32x4 b[L][NI];
-    };
-    constexpr int kReads = L * (MI + NI);
-    constexpr int kMfmas = L * L * MI * NI;
-    auto read_one = [&](const char *buf, int kk, int r, Frags &f) {
-        const int ch = 2 * kk + h;
-        if (r < L * MI) {
-            const int i = r / MI, a = r % MI;
-            f.a[i][a] = *(const i32x4 *)(buf + rswz<kDmaRB>(i * BM + wm * 32 * MI + a * 32 + lr, ch));
-        } else {
-            const int j = (r - L * MI) / NI, c = (r - L * MI) % NI;
-            f.b[j][c] = *(const i32x4 *)(buf + rswz<kDmaRB>(Sh::A_ROWS + j * BN + wn * 32 * NI +
-                                                            c * 32 + lr, ch));
-        }
-    };
-    // MFMAs of `cur`, with the reads of the next step's fragments into `nxt`
-    // interleaved one per MFMA, so no MFMA waits on a read issued after the
-    // reads of its own operands and the LDS latency hides under the MFMAs.
-    auto step = [&](const Frags &cur, Frags &nxt, const char *nbuf, int nkk) {
-#pragma unroll
-        for (int q = 0; q < kMfmas; ++q) {
-            const int i = q / (L * MI * NI), j = (q / (MI * NI)) % L;
-            const int a = (q / NI) % MI, c = q % NI;
-            acc[i][j][a][c] = MF::run(cur.a[i][a], cur.b[j][c], acc[i][j][a][c]);
-            if (q < kReads) read_one(nbuf, nkk, q, nxt);
-            __builtin_amdgcn_sched_barrier(0);   // keep this order
-        }
-#pragma unroll
-        for (int q = kMfmas; q < kReads; ++q) read_one(nbuf, nkk, q, nxt);
-    };
-    // stage kb has landed once at most the loads of the stages issued after it
-    // are outstanding; then the barrier publishes every wave's DMA writes
-    // When stage kb is awaited, stages up to kb + DMA_STAGES - 2 have been
-    // issued (each LPS loads per lane).
-    auto stage_ready = [&](int kb) {
-        const int after = min(kDmaStages - 2, nkb - 1 - kb);
-        static_assert(kDmaStages >= 2 && kDmaStages <= 6, "wait table");
-        // only counts that can occur (after <= DMA_STAGES - 2) are instantiated
-        if constexpr (kDmaStages - 2 >= 4) { if (after == 4) { wait_vmcnt<4 * Sh::LPS>(); goto waited; } }
-        if constexpr (kDmaStages - 2 >= 3) { if (after == 3) { wait_vmcnt<3 * Sh::LPS>(); goto waited; } }
-        if constexpr (kDmaStages - 2 >= 2) { if (after == 2) { wait_vmcnt<2 * Sh::LPS>(); goto waited; } }
-        if constexpr (kDmaStages - 2 >= 1) { if (after == 1) { wait_vmcnt<Sh::LPS>(); goto waited; } }
-        wait_vmcnt<0>();
-    waited:
-        // this wave's reads of the slot refilled after the barrier must have
-        // completed, not only been issued
-        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0) only
-        exec_barrier();
-    };
-
-    // Software pipeline over 32-byte K steps (two per stage).
-    Frags f0, f1;
-    if (nkb > 0) {
-        stage_ready(0);
-        if (kDmaStages - 1 < nkb) issue_stage(kDmaStages - 1);
-#pragma unroll
-        for (int q = 0; q < kReads; ++q) read_one(smem, 0, q, f0);
-    }
-    for (int kb = 0; kb < nkb; ++kb) {
-        const char *buf = smem + (kb % kDmaStages) * Sh::STAGE;
-        // steps 0 .. STEPS-2 of this stage, each reading the next step's
-        // fragments; f0 / f1 alternate
-#pragma unroll
-        for (int kk = 0; kk + 1 < STEPS; ++kk) {
-            if (kk % 2 == 0) step(f0, f1, buf, kk + 1);
-            else step(f1, f0, buf, kk + 1);
-        }
-        if (kb + 1 < nkb) {
-            stage_ready(kb + 1);
-            // the ring slot of stage kb + DMA_STAGES is the one of stage kb,
-            // whose reads every wave completed before this barrier
-            if (kb + kDmaStages < nkb) issue_stage(kb + kDmaStages);
-        }
-        // last step: reads the next stage's step-0 fragments (on the last
-        // stage, unused data from a slot that is not being written)
-        if ((STEPS - 1) % 2 == 0) step(f0, f1, smem + ((kb + 1) % kDmaStages) * Sh::STAGE, 0);
-        else step(f1, f0, smem + ((kb + 1) % kDmaStages) * Sh::STAGE, 0);
-        if ((STEPS - 1) % 2 == 0) {   // next stage's step 0 expects its fragments in f0
-#pragma unroll
-            for (int i = 0; i < L; ++i)
-#pragma unroll
-                for (int a = 0; a < MI; ++a) f0.a[i][a] = f1.a[i][a];
-#pragma unroll
-            for (int j = 0; j < L; ++j)
-#pragma unroll
-                for (int c = 0; c < NI; ++c) f0.b[j][c] = f1.b[j][c];
-        }
-    }
-
-    // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
-    const float *sab = p.sa + bidx * p.sas_b;
-    const float *sbb = p.sb + bidx * p.sbs_b;
-    const int64_t cbase = bidx * p.cs_b;
-#pragma unroll
-    for (int c = 0; c < NI; ++c) {
-        const int64_t col = n0 + wn * 32 * NI + c * 32 + lr;
-        const bool cok = col < p.N;
-        float sbv[L];
-#pragma unroll
-        for (int j = 0; j < L; ++j) sbv[j] = cok ? sbb[j * p.sbs_l + col * p.sbs_n] : 0.0f;
-#pragma unroll
-        for (int a = 0; a < MI; ++a) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t row = m0 + wm * 32 * MI + a * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (cok && row < p.M) {
-                    OA out = (OA)0;
-#pragma unroll
-                    for (int i = 0; i < L; ++i) {
-                        const float sai = sab[i * p.sas_l + row * p.sas_m];
-#pragma unroll
-                        for (int j = 0; j < L; ++j) {
-                            const float x = MF::to_f32(acc[i][j][a][c][r]);
-                            const float t1 = x * sai;
-                            const float t2 = t1 * sbv[j];
-                            out = out + (OA)t2;
-                        }
-                    }
-                    store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
-                }
-            }
-        }
-    }
-}
-
-// one MFMA with its accumulator in AGPRs (AG) or VGPRs
-template <typename ST, bool AG> struct HandMfma;
-template <bool AG> struct HandMfma<int8_t, AG> {
-    OZK_DEV static void run(i32x16 &c, i32x4 a, i32x4 b) {
-        if constexpr (AG) asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
-        else asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
-    }
-};
-template <bool AG> struct HandMfma<_Float16, AG> {
-    OZK_DEV static void run(f32x16 &c, i32x4 a, i32x4 b) {
-        if constexpr (AG) asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
-        else asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
-    }
-};
-template <bool AG> struct HandMfma<__bf16, AG> {
-    OZK_DEV static void run(f32x16 &c, i32x4 a, i32x4 b) {
-        if constexpr (AG) asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
-        else asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
-    }
-};
-
-template <int N, typename F> OZK_DEV void static_for(F &&f) {
-    if constexpr (N > 0) {
-        static_for<N - 1>(f);
-        f(std::integral_constant<int, N - 1>{});
-    }
-}
-
-// ---------------------------------------------------------------------------
-// K-step kernel for grids too small to fill the chip with 64 x 64 tiles (tall
-// or skinny C, large K).  32 x 32 tiles, 4 waves (one per SIMD).  Wave w
-// takes the 32-byte K step w of every 128-byte stage and all L x L slice
-// pairs on it, so per stage it reads L A and L B fragments for L^2 MFMAs (8
-// reads for 16 MFMAs at L = 4) and no tile's K is split across workgroups.
-//   * Stages of 2L x 32 rows x 128 bytes are fetched by LDS-DMA into a ring
-//     of NST slots; stage kb + NST reuses the slot of stage kb after the
-//     barrier that follows every wave's reads of it.  The fragments of stage
-//     kb + 1 are read while the MFMAs of stage kb run, with stage kb + NST's
-//     DMA instructions spread between those MFMAs.
-//   * Epilogue: the four waves' accumulators of each pair are summed through
-//     the LDS in wave order (int32: exact; fp32: the same order every call),
-//     in 16-byte pieces, groups of up to 4 pairs at a time, one pair per
-//     wave; that wave turns the sum into t_ij = fl32(fl32(fl32(acc) * sa_i) *
-//     sb_j) in the LDS.  Then each wave sums, for a quarter of the tile, the
-//     t values of all pairs in the i-major / j-minor order from +0
-//     (ozaki_triton.py:420-452) and stores C.  The tile's scales are loaded
-//     at kernel start.
-// ---------------------------------------------------------------------------
-template <int L> struct KStepShape {
-    static constexpr int BM = 32, BN = 32;
-    static constexpr int ROWS = 2 * L * 32;                   // A rows then B rows
-    static constexpr int STAGE = ROWS * kDmaRB;
-    static constexpr int LPS = STAGE / (4 * 1024);            // DMA instructions per wave per stage
-    static constexpr int NST = (160 * 1024 / STAGE) < 6 ? (160 * 1024 / STAGE) : 6;
-    static constexpr int NP = L * L;                          // slice pairs
-    static constexpr int PR = NP < 4 ? NP : 4;                // pairs per epilogue group
-    static constexpr int T_BYTES = NP * 16 * 64 * 4;          // t values [pair][reg / 4][lane][4]
-    static constexpr int R_BYTES = 4 * PR * 16 * 64 * 4;      // [wave][pair][reg / 4][lane][4]
-    static constexpr int S_BYTES = 2 * L * 32 * 4;            // sa [L][32], sb [L][32]
-    static constexpr int EPI_BYTES = T_BYTES + R_BYTES + S_BYTES;
-    static constexpr int LDS_BYTES = NST * STAGE > EPI_BYTES ? NST * STAGE : EPI_BYTES;
-    static constexpr bool kHand = L == 4;   // accumulators in AGPRs, hand-placed MFMAs
-    static_assert(STAGE % 4096 == 0, "a stage is whole 1 KB windows per wave");
-    static_assert(NST >= 3, "stages in flight");
-    static_assert(LDS_BYTES <= 160 * 1024, "LDS");
-    static_assert(kDmaRB == 128 && L * 32 <= 128, "four K steps per stage; scales one per lane");
-};
-
-template <typename ST, int L, typename AccT>
-__global__ __launch_bounds__(256, 1) void cross_gemm_kstep_kernel(GemmParams p, int group_m,
-                                                                  uint32_t a_records,
-                                                                  uint32_t b_records) {
-    using Sh = KStepShape<L>;
-    using MF = Mfma<ST>;
-    using Acc = typename MF::Acc;
-    using Elem = typename MF::Elem;
-    using OA = AccT;
-    constexpr int BM = Sh::BM, BN = Sh::BN, LPS = Sh::LPS, NST = Sh::NST;
-    constexpr int ES = (int)sizeof(ST);
-    constexpr uint32_t kOOB = 0x80000000u;
-    extern __shared__ __attribute__((aligned(16))) char smem[];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int h = lane >> 5, lr = lane & 31;
-
-    const int64_t tiles_m = (p.M + BM - 1) / BM;
-    const int64_t tiles_n = (p.N + BN - 1) / BN;
-    const int64_t tiles = tiles_m * tiles_n;
-    const int64_t g = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
-    const int64_t bidx = g / tiles;
-    const int64_t t = g % tiles;
-    const int64_t width = (int64_t)group_m * tiles_n;
-    const int64_t first_m = (t / width) * group_m;
-    const int64_t gsz = (tiles_m - first_m < group_m) ? (tiles_m - first_m) : group_m;
-    const int64_t tm = first_m + (t % width) % gsz;
-    const int64_t tn = (t % width) / gsz;
-    const int64_t m0 = tm * BM, n0 = tn * BN;
-
-    const uint32_t kbytes = (uint32_t)(p.K * ES);
-    const int nkb = (int)((kbytes + kDmaRB - 1) / kDmaRB);
-
-    // this lane's scale of the tile (lanes 0..32L-1: sa [L][32], lanes
-    // 128..128+32L-1: sb [L][32]), loaded first so that its latency passes
-    // under the K loop; the epilogue stores it in the LDS
-    float scl = 0.0f;
-    {
-        const int e = tid & 127, s = e / 32, o = e % 32;
-        if (e < L * 32) {
-            if (tid < 128) {
-                if (m0 + o < p.M) scl = p.sa[bidx * p.sas_b + s * p.sas_l + (m0 + o) * p.sas_m];
-            } else if (n0 + o < p.N) {
-                scl = p.sb[bidx * p.sbs_b + s * p.sbs_l + (n0 + o) * p.sbs_n];
-            }
-        }
-    }
-
-    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)((const char *)p.A + bidx * p.as_b * ES), (short)0, (int)a_records, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)((const char *)p.B + bidx * p.bs_b * ES), (short)0, (int)b_records, 0x00020000);
-
-    // per-lane source offsets of this wave's LPS instructions of a stage (a
-    // 1 KB window is 8 whole 128-byte rows, all of A or all of B)
-    uint32_t src[LPS];
-    int chunk[LPS];
-#pragma unroll
-    for (int q = 0; q < LPS; ++q) {
-        const int pos = (wave * LPS + q) * 64 + lane;
-        const int r = pos / 8, pc = pos % 8;
-        chunk[q] = pc ^ ((r >> 1) & 7);
-        if (r < L * BM) {
-            const int64_t m = m0 + r % BM;
-            src[q] = (m < p.M) ? (uint32_t)(((int64_t)(r / BM) * p.as_l + m * p.as_m) * ES) : kOOB;
-        } else {
-            const int rb = r - L * BM;
-            const int64_t n = n0 + rb % BN;
-            src[q] = (n < p.N) ? (uint32_t)(((int64_t)(rb / BN) * p.bs_l + n * p.bs_n) * ES) : kOOB;
-        }
-    }
-    auto issue_one = [&](int kb, int q) {
-        const uint32_t kofs = (uint32_t)kb * kDmaRB + chunk[q] * 16;
-        const uint32_t vo = (src[q] == kOOB || kofs >= kbytes) ? kOOB : src[q] + kofs;
-        auto *ldsp = (__attribute__((address_space(3))) void *)(smem + (kb % NST) * Sh::STAGE +
-                                                              (wave * LPS + q) * 1024);
-        const bool isA = (wave * LPS + q) * 8 < L * BM;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(isA ? rA : rB, ldsp, 16, vo, 0, 0, 0);
-    };
-    auto issue_stage = [&](int kb) {
-#pragma unroll
-        for (int q = 0; q < LPS; ++q) issue_one(kb, q);
-    };
-    // stage s has landed once at most the instructions of the stages issued
-    // after it are outstanding (stages up to s + NST - 2 are issued when s is
-    // awaited); the lgkmcnt wait completes this wave's reads of the slot the
-    // next issue refills, and the barrier publishes every wave's DMA writes
-    auto stage_ready = [&](int s) {
-        const int after = min(NST - 2, nkb - 1 - s);
-        static_assert(NST - 2 <= 4, "wait table");
-        if constexpr (NST - 2 >= 4) { if (after == 4) { wait_vmcnt<4 * LPS>(); goto waited; } }
-        if constexpr (NST - 2 >= 3) { if (after == 3) { wait_vmcnt<3 * LPS>(); goto waited; } }
-        if constexpr (NST - 2 >= 2) { if (after == 2) { wait_vmcnt<2 * LPS>(); goto waited; } }
-        if (after == 1) { wait_vmcnt<LPS>(); goto waited; }
-        wait_vmcnt<0>();
-    waited:
-        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0) only
-        exec_barrier();
-    };
-
-    Acc acc[L][L];
-#pragma unroll
-    for (int i = 0; i < L; ++i)
-#pragma unroll
-        for (int j = 0; j < L; ++j) acc[i][j] = MF::zero();
-    // At L = 4 the 16 accumulator tiles (256 registers) live in the AGPRs,
-    // through hand-placed MFMAs (left to the compiler, the K loop spills).
-    // The compiler's hazard recogniser does not see into inline assembly: the
-    // zeroed tiles are pinned here, 8 wait states before any MFMA reads them.
-    constexpr bool kHand = Sh::kHand;
-    if constexpr (kHand) {
-        static_for<L * L>([&](auto n_) {
-            constexpr int n = decltype(n_)::value;
-            (void)acc;   // an ordinary use, so that the capture does not hinge on the asm operand
-            asm volatile("" : "+a"(acc[n / L][n % L]));
-        });
-        asm volatile("s_nop 7" ::: "memory");
-    }
-
-    struct Frags {
-        i32x4 a[L];
-        i32x4 b[L];
-    };
-    const int ch = 2 * wave + h;   // this wave's 16-byte chunk of a stage row
-    auto read_frags = [&](int kb, Frags &f) {
-        const char *buf = smem + (kb % NST) * Sh::STAGE;
-#pragma unroll
-        for (int i = 0; i < L; ++i) f.a[i] = *(const i32x4 *)(buf + rswz<kDmaRB>(i * BM + lr, ch));
-#pragma unroll
-        for (int j = 0; j < L; ++j)
-            f.b[j] = *(const i32x4 *)(buf + rswz<kDmaRB>(L * BM + j * BN + lr, ch));
-    };
-    // the L^2 MFMAs of one stage, with the DMA instructions of stage dkb (if
-    // dkb >= 0) spread between them: issued in a burst, the four waves'
-    // instructions fill the vector-memory queue and stall each wave at issue
-    auto mfmas = [&](const Frags &f, int dkb) {
-        constexpr int NMF = L * L;
-        static_for<NMF>([&](auto n_) {
-            constexpr int n = decltype(n_)::value;
-            if constexpr (kHand) HandMfma<ST, true>::run(acc[n / L][n % L], f.a[n / L], f.b[n % L]);
-            else acc[n / L][n % L] = MF::run(f.a[n / L], f.b[n % L], acc[n / L][n % L]);
-            static_for<LPS>([&](auto d_) {
-                constexpr int d = decltype(d_)::value;
-                // instruction d goes after MFMA (d * NMF) / LPS
-                if constexpr ((d * NMF) / LPS == n) {
-                    if (dkb >= 0) issue_one(dkb, d);
-                }
-            });
-            __builtin_amdgcn_sched_barrier(0);
-        });
-    };
-    // stage kb: the next stage's fragments into `nxt` (after its barrier,
-    // which also frees stage kb's slot for stage kb + NST), then the MFMAs of
-    // `cur` with stage kb + NST's DMA between them
-    auto stage = [&](int kb, const Frags &cur, Frags &nxt) {
-        int dkb = -1;
-        if (kb + 1 < nkb) {
-            stage_ready(kb + 1);
-            if (kb + NST < nkb) dkb = kb + NST;
-            read_frags(kb + 1, nxt);
-        }
-        mfmas(cur, dkb);
-    };
-
-    if (nkb > 0) {
-#pragma unroll
-        for (int s = 0; s < NST - 1; ++s)
-            if (s < nkb) issue_stage(s);
-        stage_ready(0);
-        if (NST - 1 < nkb) issue_stage(NST - 1);
-        Frags f0, f1;
-        read_frags(0, f0);
-        int kb = 0;
-        for (; kb + 1 < nkb; kb += 2) {
-            stage(kb, f0, f1);
-            stage(kb + 1, f1, f0);
-        }
-        if (kb < nkb) stage(kb, f0, f1);
-    }
-
-    // the hand-placed MFMAs' results are read below: 64 wait states first
-    if constexpr (kHand) asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory");
-
-    // ---- epilogue ----
-    wait_vmcnt<0>();
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    exec_barrier();   // every wave is past its last read of the ring
-    // LDS: T [pair][4][lane] x 4 t values, R [wave][pair][4][lane] x 4
-    // accumulator values, S the scales; 16-byte pieces, a wave's 64 pieces
-    // contiguous
-    f32x4 *T = (f32x4 *)smem;
-    using E4 = Elem __attribute__((ext_vector_type(4)));
-    E4 *R = (E4 *)(smem + Sh::T_BYTES);
-    float *S = (float *)(smem + Sh::T_BYTES + Sh::R_BYTES);
-    if ((tid & 127) < L * 32) S[(tid < 128 ? 0 : L * 32) + (tid & 127)] = scl;
-    constexpr int NG = (Sh::NP + Sh::PR - 1) / Sh::PR;
-#pragma unroll
-    for (int gi = 0; gi < NG; ++gi) {
-#pragma unroll
-        for (int pp = 0; pp < Sh::PR; ++pp) {
-            const int pr = gi * Sh::PR + pp;
-            if (pr < Sh::NP) {
-                const Acc v = acc[pr / L][pr % L];
-#pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    R[((wave * Sh::PR + pp) * 4 + c) * 64 + lane] =
-                        E4{v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]};
-            }
-        }
-        __builtin_amdgcn_s_waitcnt(0xC07F);
-        exec_barrier();
-        const int pr = gi * Sh::PR + wave;
-        if (wave < Sh::PR && pr < Sh::NP) {
-            const int i = pr / L, j = pr % L;
-            const float sbj = S[L * 32 + j * 32 + lr];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                E4 v = R[((0 * Sh::PR + wave) * 4 + c) * 64 + lane];
-                v = v + R[((1 * Sh::PR + wave) * 4 + c) * 64 + lane];
-                v = v + R[((2 * Sh::PR + wave) * 4 + c) * 64 + lane];
-                v = v + R[((3 * Sh::PR + wave) * 4 + c) * 64 + lane];
-                // registers 4c .. 4c + 3: rows 8c + 4h + 0..3 of the tile
-                f32x4 tv;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float t1 = MF::to_f32(v[e]) * S[i * 32 + 8 * c + 4 * h + e];
-                    tv[e] = t1 * sbj;
-                }
-                T[(pr * 4 + c) * 64 + lane] = tv;
-            }
-        }
-        __builtin_amdgcn_s_waitcnt(0xC07F);
-        exec_barrier();
-    }
-    // wave w: accumulator registers 4w .. 4w + 3 of every lane, rows
-    // 8w + 4h + 0..3
-    const int64_t col = n0 + lr;
-    const int64_t cbase = bidx * p.cs_b;
-    OA out[4] = {(OA)0, (OA)0, (OA)0, (OA)0};
-#pragma unroll
-    for (int q = 0; q < Sh::NP; ++q) {
-        const f32x4 tv = T[(q * 4 + wave) * 64 + lane];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) out[e] = out[e] + (OA)tv[e];
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int64_t row = m0 + 8 * wave + 4 * h + e;
-        if (col < p.N && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, out[e]);
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Pair-split variant: 8 waves, two per SIMD.  The 2 x 2 grid of 32 x 32 wave
-// blocks is covered twice: wave group g (0 or 1) accumulates the slice pairs
-// [g*P0, ...) of the i-major / j-minor pair order, P0 = ceil(L*L/2) (6 at
-// L = 3), so a wave holds about half the accumulators (128 registers at
-// L = 4) and two waves share a SIMD.  While one waits on its DMA issue, an LDS read or the stage barrier,
-// the other's MFMAs run.  The epilogue keeps the reference's ordered sum:
-// group 0 sums its pairs from +0 and hands the partial to group 1 through
-// LDS; group 1 adds its pairs, in order, and stores C.
-// ---------------------------------------------------------------------------
-// The kernel covers the pairs of R consecutive i-rows [i0, i0 + R) of the
-// order (R = L: all of them).  num_splits > 4 runs as several such launches in
-// i-major order, each continuing the sum from C, which holds the partial in
-// the fp64 outer accumulator between launches.
-// At num_splits 3 group 0 takes the pairs of i-rows 0 and 1 (6 MFMAs from 5
-// fragment reads per K step) and group 1 those of row 2 (3 MFMAs from 4
-// reads): about 6% faster on the fp16 broadcast-batch shape than the 5 / 4
-// split, whose group 1 needs A fragments of two i-rows for 4 MFMAs.
-template <int L, int R> struct PairSplit {
-    static constexpr int P = R * L;
-    static constexpr int P0 = (L == 3 && R == 3) ? 6 : (P + 1) / 2;
-    static constexpr int first(int g) { return g ? P0 : 0; }
-    static constexpr int count(int g) { return g ? P - P0 : P0; }
-    static constexpr int ilo(int g) { return first(g) / L; }
-    static constexpr int na(int g) { return (first(g) + count(g) - 1) / L - ilo(g) + 1; }
-};
-
-template <int L, int R> struct PairShape {
-    static constexpr int BM = 64, BN = 64;
-    static constexpr int A_ROWS = R * BM;
-    static constexpr int ROWS = (R + L) * BM;
-    static constexpr int STAGE = ROWS * kDmaRB;
-    static constexpr int LPS = STAGE / (8 * 1024);   // DMA instructions per wave per stage
-    static constexpr int LDS_BYTES = kDmaStages * STAGE;
-    static_assert(STAGE % 8192 == 0, "stage must be a whole number of 1 KB windows per wave");
-    static_assert(LDS_BYTES <= 160 * 1024, "LDS");
-};
-
-template <typename ST, int L, typename AccT, int R>
-__global__ __launch_bounds__(512, 1) void cross_gemm_pair_kernel(GemmParams p, int group_m,
-                                                                 uint32_t a_records,
-                                                                 uint32_t b_records, int i0,
-                                                                 int cont) {
-    using Sh = PairShape<L, R>;
-    using PS = PairSplit<L, R>;
-    using MF = Mfma<ST>;
-    using Acc = typename MF::Acc;
-    using OA = AccT;   // outer accumulator: fp64 for fp64 output, else fp32 (store_c)
-    constexpr int BM = Sh::BM, BN = Sh::BN;
-    constexpr int ES = (int)sizeof(ST);
-    constexpr uint32_t kOOB = 0x80000000u;
-    extern __shared__ __attribute__((aligned(16))) char smem[];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int blk = wave & 3, grp = wave >> 2;
-    const int wm = blk >> 1, wn = blk & 1;
-    const int h = lane >> 5, lr = lane & 31;
-
-    const int64_t tiles_m = (p.M + BM - 1) / BM;
-    const int64_t tiles_n = (p.N + BN - 1) / BN;
-    const int64_t tiles = tiles_m * tiles_n;
-    const int64_t g = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
-    const int64_t bidx = g / tiles;
-    const int64_t t = g % tiles;
-    const int64_t width = (int64_t)group_m * tiles_n;
-    const int64_t first_m = (t / width) * group_m;
-    const int64_t gsz = (tiles_m - first_m < group_m) ? (tiles_m - first_m) : group_m;
-    const int64_t tm = first_m + (t % width) % gsz;
-    const int64_t tn = (t % width) / gsz;
-    const int64_t m0 = tm * BM, n0 = tn * BN;
-
-    const uint32_t kbytes = (uint32_t)(p.K * ES);
-    const int nkb = (int)((kbytes + kDmaRB - 1) / kDmaRB);
-    constexpr int CH = kDmaRB / 16;
-    constexpr int STEPS = kDmaRB / 32;
-
-    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)((const char *)p.A + bidx * p.as_b * ES), (short)0, (int)a_records, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)((const char *)p.B + bidx * p.bs_b * ES), (short)0, (int)b_records, 0x00020000);
-
-    // Per-lane source offsets of this wave's LPS DMA instructions (a 1 KB
-    // window covers 8 whole rows; A_ROWS is a multiple of 8, so each
-    // instruction reads only A or only B).
-    uint32_t src[Sh::LPS];
-    int chunk[Sh::LPS];
-#pragma unroll
-    for (int q = 0; q < Sh::LPS; ++q) {
-        const int pos = (wave * Sh::LPS + q) * 64 + lane;
-        const int r = pos / CH;
-        const int pc = pos % CH;
-        chunk[q] = (kDmaRB == 64) ? (pc ^ ((r >> 2) & 3)) : (pc ^ ((r >> 1) & 7));
-        if (r < Sh::A_ROWS) {
-            const int i = i0 + r / BM;
-            const int64_t m = m0 + r % BM;
-            src[q] = (m < p.M) ? (uint32_t)(((int64_t)i * p.as_l + m * p.as_m) * ES) : kOOB;
-        } else {
-            const int rb = r - Sh::A_ROWS;
-            const int j = rb / BN;
-            const int64_t n = n0 + rb % BN;
-            src[q] = (n < p.N) ? (uint32_t)(((int64_t)j * p.bs_l + n * p.bs_n) * ES) : kOOB;
-        }
-    }
-    auto issue_one = [&](int kb, int q) {
-        char *dst = smem + (kb % kDmaStages) * Sh::STAGE + wave * Sh::LPS * 1024;
-        const uint32_t kofs = (uint32_t)kb * kDmaRB + chunk[q] * 16;
-        const uint32_t vo = (src[q] == kOOB || kofs >= kbytes) ? kOOB : src[q] + kofs;
-        auto *ldsp = (__attribute__((address_space(3))) void *)(dst + q * 1024);
-        const bool isA = (wave * Sh::LPS + q) * (1024 / kDmaRB) < Sh::A_ROWS;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(isA ? rA : rB, ldsp, 16, vo, 0, 0, 0);
-    };
-    auto issue_stage = [&](int kb) {
-#pragma unroll
-        for (int q = 0; q < Sh::LPS; ++q) issue_one(kb, q);
-    };
-    // stage kb has landed once at most the loads of the stages issued after
-    // it are outstanding; the barrier then publishes every wave's DMA writes,
-    // and the lgkmcnt wait makes this wave's reads of the slot about to be
-    // refilled complete first
-    auto stage_ready = [&](int kb) {
-        const int after = min(kDmaStages - 2, nkb - 1 - kb);
-        static_assert(kDmaStages >= 2 && kDmaStages <= 6, "wait table");
-        if constexpr (kDmaStages - 2 >= 4) { if (after == 4) { wait_vmcnt<4 * Sh::LPS>(); goto waited; } }
-        if constexpr (kDmaStages - 2 >= 3) { if (after == 3) { wait_vmcnt<3 * Sh::LPS>(); goto waited; } }
-        if constexpr (kDmaStages - 2 >= 2) { if (after == 2) { wait_vmcnt<2 * Sh::LPS>(); goto waited; } }
-        if constexpr (kDmaStages - 2 >= 1) { if (after == 1) { wait_vmcnt<Sh::LPS>(); goto waited; } }
-        wait_vmcnt<0>();
-    waited:
-        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0) only
-        exec_barrier();
-    };
-
-#pragma unroll
-    for (int s = 0; s < kDmaStages - 1; ++s)
-        if (s < nkb) issue_stage(s);
-
-    const float *sab = p.sa + bidx * p.sas_b;
-    const float *sbb = p.sb + bidx * p.sbs_b;
-    const int64_t cbase = bidx * p.cs_b;
-    OA *part = (OA *)smem;   // epilogue hand-off [4 blocks][16][64 lanes]
-    const int64_t col = n0 + wn * 32 + lr;
-    const bool cok = col < p.N;
-
-    // The main loop and epilogue of wave group G (compile-time pair range).
-    auto body = [&](auto G_) {
-        constexpr int G = decltype(G_)::value;
-        constexpr int F = PS::first(G), NP = PS::count(G), ILO = PS::ilo(G), NA = PS::na(G);
-        constexpr int kReads = NA + L;
-        struct Frags {
-            i32x4 a[NA];
-            i32x4 b[L];
-        };
-        Acc acc[NP];
-#pragma unroll
-        for (int q = 0; q < NP; ++q) acc[q] = MF::zero();
-
-        auto read_one = [&](const char *buf, int kk, int r, Frags &f) {
-            const int ch = 2 * kk + h;
-            if (r < NA) {
-                f.a[r] = *(const i32x4 *)(buf + rswz<kDmaRB>((ILO + r) * BM + wm * 32 + lr, ch));
-            } else {
-                const int j = r - NA;
-                f.b[j] = *(const i32x4 *)(buf + rswz<kDmaRB>(Sh::A_ROWS + j * BN + wn * 32 + lr, ch));
-            }
-        };
-        // MFMAs of `cur` with the next step's reads into `nxt` interleaved
-        auto step = [&](const Frags &cur, Frags &nxt, const char *nbuf, int nkk) {
-#pragma unroll
-            for (int q = 0; q < NP; ++q) {
-                const int i = (F + q) / L, j = (F + q) % L;
-                acc[q] = MF::run(cur.a[i - ILO], cur.b[j], acc[q]);
-                if (q < kReads) read_one(nbuf, nkk, q, nxt);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-#pragma unroll
-            for (int q = NP; q < kReads; ++q) read_one(nbuf, nkk, q, nxt);
-        };
-
-        // A stage's DMA is issued in three parts: the first right after its
-        // ring slot is released (stage_ready of the stage before it), the
-        // others before the first two K steps of that stage.  Issued at once,
-        // the 8 waves' instructions overfill the vector-memory queue and each
-        // wave stalls at issue for hundreds of cycles.
-        static_assert(kDmaStages == 2, "the DMA issue schedule assumes a ring of two stages");
-        constexpr int DP1 = (Sh::LPS + 2) / 3, DP2 = (2 * DP1 < Sh::LPS) ? 2 * DP1 : Sh::LPS;
-        auto issue_part = [&](int kb, int part) {
-            const int lo = part == 0 ? 0 : part == 1 ? DP1 : DP2;
-            const int hi = part == 0 ? DP1 : part == 1 ? DP2 : Sh::LPS;
-#pragma unroll
-            for (int q = 0; q < Sh::LPS; ++q)
-                if (q >= lo && q < hi) issue_one(kb, q);
-        };
-        Frags f0, f1;
-        if (nkb > 0) {
-            stage_ready(0);
-            if (1 < nkb) issue_part(1, 0);
-#pragma unroll
-            for (int q = 0; q < kReads; ++q) read_one(smem, 0, q, f0);
-        }
-        for (int kb = 0; kb < nkb; ++kb) {
-            const char *buf = smem + (kb % kDmaStages) * Sh::STAGE;
-#pragma unroll
-            for (int kk = 0; kk + 1 < STEPS; ++kk) {
-                if (kk < 2 && kb + 1 < nkb) issue_part(kb + 1, kk + 1);
-                if (kk % 2 == 0) step(f0, f1, buf, kk + 1);
-                else step(f1, f0, buf, kk + 1);
-            }
-            if (kb + 1 < nkb) {
-                stage_ready(kb + 1);
-                if (kb + 2 < nkb) issue_part(kb + 2, 0);
-            }
-            if ((STEPS - 1) % 2 == 0) step(f0, f1, smem + ((kb + 1) % kDmaStages) * Sh::STAGE, 0);
-            else step(f1, f0, smem + ((kb + 1) % kDmaStages) * Sh::STAGE, 0);
-            if ((STEPS - 1) % 2 == 0) {
-#pragma unroll
-                for (int i = 0; i < NA; ++i) f0.a[i] = f1.a[i];
-#pragma unroll
-                for (int j = 0; j < L; ++j) f0.b[j] = f1.b[j];
-            }
-        }
-        // every wave is past its last ring read before the ring holds partials
-        __builtin_amdgcn_s_waitcnt(0xC07F);
-        exec_barrier();
-
-        // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
-        float sbv[L];
-#pragma unroll
-        for (int j = 0; j < L; ++j) sbv[j] = cok ? sbb[j * p.sbs_l + col * p.sbs_n] : 0.0f;
-        // t values of this group's pairs: fl32(fl32(fl32(acc) * sa_i) * sb_j)
-        float tv[NP][16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int64_t row = m0 + wm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-            const bool ok = cok && row < p.M;
-            float sai[NA];
-#pragma unroll
-            for (int i = 0; i < NA; ++i)
-                sai[i] = ok ? sab[(int64_t)(i0 + ILO + i) * p.sas_l + row * p.sas_m] : 0.0f;
-#pragma unroll
-            for (int q = 0; q < NP; ++q) {
-                const int i = (F + q) / L, j = (F + q) % L;
-                const float x = MF::to_f32(acc[q][r]);
-                const float t1 = x * sai[i - ILO];
-                tv[q][r] = t1 * sbv[j];
-            }
-        }
-        if constexpr (G == 0) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                // from +0, or from the partial an earlier launch left in C
-                OA out = (OA)0;
-                if (cont) {
-                    const int64_t row = m0 + wm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                    if (cok && row < p.M) out = load_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
-                }
-#pragma unroll
-                for (int q = 0; q < NP; ++q) out = out + (OA)tv[q][r];
-                part[(blk * 16 + r) * 64 + lane] = out;
-            }
-            __builtin_amdgcn_s_waitcnt(0xC07F);
-            exec_barrier();
-        } else {
-            exec_barrier();
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t row = m0 + wm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                OA out = part[(blk * 16 + r) * 64 + lane];
-#pragma unroll
-                for (int q = 0; q < NP; ++q) out = out + (OA)tv[q][r];
-                if (cok && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
-            }
-        }
-    };
-    if (grp == 0) body(std::integral_constant<int, 0>{});
-    else body(std::integral_constant<int, 1>{});
-}
-
-// ---------------------------------------------------------------------------
-// Ring variant of the pair-split kernel, for num_splits 3 and 4 (all i-rows in
-// one launch).  Same 8 waves, wave blocks and pair split; what changes is how
-// operands reach the LDS.
-//   * The ring has five slots of half a stage: half stage 2kb holds the A
-//     rows and 2kb + 1 the B rows of stage kb (128 bytes of K), in slot
-//     h % 5.  A(kb + 2) reuses the slot of B(kb - 1), which is free from the
-//     start of stage kb, so it can be fetched two stages ahead; B(kb + 1)
-//     reuses the slot of A(kb - 1) and is fetched one stage ahead.
-//   * The DMA of stage kb's time window (B(kb + 1), then A(kb + 2)) is spread
-//     one instruction at a time between this wave's MFMAs.  The LDS-DMA path
-//     accepts about one 1 KB instruction per 13 cycles per CU; issued in
-//     bursts, the 8 waves' instructions fill the vector-memory queue and each
-//     wave stalls at issue for hundreds of cycles.
-//   * A K step issues all reads of the next step before its MFMAs: under
-//     load an LDS read takes several hundred cycles to return.
-// Per stage each wave issues LPH instructions of B(kb + 1) in K steps 0 and 1
-// and LPH of A(kb + 2) in steps 2 and 3 (the part in step 3 after the stage
-// barrier); the barrier before stage kb + 1 waits for everything but the
-// step-2 part of A(kb + 2).
-// ---------------------------------------------------------------------------
-// W = 1 for num_splits 3 and 4: 32 x 32 wave blocks, 64 x 64 tiles.  W = 2
-// for num_splits 2: 64 x 64 wave blocks, 128 x 128 tiles; a wave then holds
-// 2 pairs x 4 blocks, again 128 accumulator registers, and the slot is again
-// 32 KB.
-template <int L, int W> struct RingShape {
-    static constexpr int NW = 8;                       // waves
-    static constexpr int BM = 64 * W, BN = 64 * W;
-    static constexpr int SLOT = L * BM * kDmaRB;       // one half stage (A rows or B rows)
-    // six slots where they fit (L = 3: 144 KB): then whole stages are fetched
-    // two ahead, B as well as A
-    static constexpr int NSLOT = 6 * SLOT <= 160 * 1024 ? 6 : 5;
-    static constexpr int LPH = SLOT / (NW * 1024);     // DMA instructions per wave per half stage
-    static constexpr int LDS_BYTES = NSLOT * SLOT;
-    static constexpr int B0 = (LPH + 1) / 2;           // B(kb + 1) instructions in step 0
-    static constexpr int A2 = (LPH + 1) / 2;           // A(kb + 2) instructions in step 2
-    static_assert(SLOT % (NW * 1024) == 0, "a half stage must be whole 1 KB windows per wave");
-    static_assert(LDS_BYTES <= 160 * 1024, "LDS");
-    static_assert(L * BM <= 256, "the scales of a tile: one dword per lane of four waves");
-    static_assert(kDmaRB == 128, "the ring assumes 128-byte stage rows");
-};
-
-template <typename ST, int L, typename AccT, int W>
-__global__ __launch_bounds__(512, 1) void cross_gemm_ring_kernel(GemmParams p, int group_m,
-                                                                 uint32_t a_records,
-                                                                 uint32_t b_records) {
-    using Sh = RingShape<L, W>;
-    using PS = PairSplit<L, L>;
-    using MF = Mfma<ST>;
-    using Acc = typename MF::Acc;
-    using OA = AccT;
-    constexpr int BM = Sh::BM, BN = Sh::BN;
-    constexpr int ES = (int)sizeof(ST);
-    constexpr uint32_t kOOB = 0x80000000u;
-    constexpr int LPH = Sh::LPH;
-    extern __shared__ __attribute__((aligned(16))) char smem[];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int blk = wave & 3, grp = wave >> 2;
-    const int wm = blk >> 1, wn = blk & 1;
-    const int h = lane >> 5, lr = lane & 31;
-
-    const int64_t tiles_m = (p.M + BM - 1) / BM;
-    const int64_t tiles_n = (p.N + BN - 1) / BN;
-    const int64_t tiles = tiles_m * tiles_n;
-    // split-K: workgroup g0 is K range g0 % S of tile g0 / S
-    const int S = p.ksplit > 1 ? p.ksplit : 1;
-    const int64_t g0 = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
-    const int krange = (int)(g0 % S);
-    const int64_t g = g0 / S;
-    const int64_t bidx = g / tiles;
-    const int64_t t = g % tiles;
-    const int64_t width = (int64_t)group_m * tiles_n;
-    const int64_t first_m = (t / width) * group_m;
-    const int64_t gsz = (tiles_m - first_m < group_m) ? (tiles_m - first_m) : group_m;
-    const int64_t tm = first_m + (t % width) % gsz;
-    const int64_t tn = (t % width) / gsz;
-    const int64_t m0 = tm * BM, n0 = tn * BN;
-
-    const uint32_t kbytes = (uint32_t)(p.K * ES);
-    const int nkb_all = (int)((kbytes + kDmaRB - 1) / kDmaRB);
-    const int kb0 = S > 1 ? krange * p.kb_per_split : 0;   // this range's first stage
-    const int nkb = S > 1 ? min(p.kb_per_split, nkb_all - kb0) : nkb_all;
-    const uint32_t kbyte0 = (uint32_t)kb0 * kDmaRB;
-    constexpr int STEPS = kDmaRB / 32;
-
-    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)((const char *)p.A + bidx * p.as_b * ES), (short)0, (int)a_records, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)((const char *)p.B + bidx * p.bs_b * ES), (short)0, (int)b_records, 0x00020000);
-
-    // Per-lane source offsets of this wave's LPH instructions of an A half
-    // and of a B half (a 1 KB window is 8 whole 128-byte rows).
-    uint32_t srcA[LPH], srcB[LPH];
-    int chA[LPH], chB[LPH];
-#pragma unroll
-    for (int q = 0; q < LPH; ++q) {
-        const int pos = (wave * LPH + q) * 64 + lane;
-        const int r = pos / 8, pc = pos % 8;
-        const int c = pc ^ ((r >> 1) & 7);
-        chA[q] = chB[q] = c;
-        const int64_t m = m0 + r % BM, n = n0 + r % BN;
-        srcA[q] = (m < p.M) ? (uint32_t)(((int64_t)(r / BM) * p.as_l + m * p.as_m) * ES) : kOOB;
-        srcB[q] = (n < p.N) ? (uint32_t)(((int64_t)(r / BN) * p.bs_l + n * p.bs_n) * ES) : kOOB;
-    }
-    auto slot = [&](int hs) { return smem + (hs % Sh::NSLOT) * Sh::SLOT; };
-    auto issue_a = [&](int kb, int q) {
-        const uint32_t kofs = kbyte0 + (uint32_t)kb * kDmaRB + chA[q] * 16;
-        const uint32_t vo = (srcA[q] == kOOB || kofs >= kbytes) ? kOOB : srcA[q] + kofs;
-        auto *ldsp = (__attribute__((address_space(3))) void *)(slot(2 * kb) + (wave * LPH + q) * 1024);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, ldsp, 16, vo, 0, 0, 0);
-    };
-    auto issue_b = [&](int kb, int q) {
-        const uint32_t kofs = kbyte0 + (uint32_t)kb * kDmaRB + chB[q] * 16;
-        const uint32_t vo = (srcB[q] == kOOB || kofs >= kbytes) ? kOOB : srcB[q] + kofs;
-        auto *ldsp = (__attribute__((address_space(3))) void *)(slot(2 * kb + 1) + (wave * LPH + q) * 1024);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, ldsp, 16, vo, 0, 0, 0);
-    };
-
-    // The scales of the tile (L x BM of A's rows and L x BN of B's columns,
-    // at most 2 KB) are fetched into a free ring slot by one dword DMA
-    // instruction per wave at the start of the last stage, so the epilogue
-    // reads them from the LDS instead of waiting on global loads.  The slot is
-    // the one of A(nkb), which is never fetched.  Waves 0-3 fetch A's scales
-    // [L][BM] (entry 64 wave + lane), waves 4-7 B's [L][BN].
-    char *const scl = slot(2 * nkb);
-    auto issue_scales = [&]() {
-        const bool isa = wave < 4;
-        const int e = (isa ? wave : wave - 4) * 64 + lane;
-        const int s = e / BM;                              // slice
-        const int64_t rc = (isa ? m0 : n0) + e % BM;       // row of A / column of B
-        const int64_t ext = isa ? ((int64_t)(L - 1) * p.sas_l + (p.M - 1) * p.sas_m + 1)
-                                : ((int64_t)(L - 1) * p.sbs_l + (p.N - 1) * p.sbs_n + 1);
-        const bool ok = s < L && rc < (isa ? p.M : p.N);
-        const uint32_t vo = ok ? (uint32_t)(((int64_t)s * (isa ? p.sas_l : p.sbs_l) +
-                                             rc * (isa ? p.sas_m : p.sbs_n)) * 4)
-                               : kOOB;
-        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-            (void *)(isa ? p.sa + bidx * p.sas_b : p.sb + bidx * p.sbs_b), (short)0,
-            (int)(ext * 4 < 0x7FFFFFFF ? ext * 4 : 0x7FFFFFFF), 0x00020000);
-        auto *ldsp = (__attribute__((address_space(3))) void *)(scl + (isa ? 0 : 1024) +
-                                                              (isa ? wave : wave - 4) * 256);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, ldsp, 4, vo, 0, 0, 0);
-    };
-    const float *sa_lds = (const float *)scl, *sb_lds = (const float *)(scl + 1024);
-
-    // prologue: stage 0 and A(1) (six slots: all of stage 1); stage 0 must
-    // land before the first reads
-#pragma unroll
-    for (int q = 0; q < LPH; ++q) issue_a(0, q);
-#pragma unroll
-    for (int q = 0; q < LPH; ++q) issue_b(0, q);
-    if (nkb > 1) {
-#pragma unroll
-        for (int q = 0; q < LPH; ++q) issue_a(1, q);
-        if constexpr (Sh::NSLOT == 6) {
-#pragma unroll
-            for (int q = 0; q < LPH; ++q) issue_b(1, q);
-            wait_vmcnt<2 * LPH>();
-        } else {
-            wait_vmcnt<LPH>();
-        }
-    } else {
-        wait_vmcnt<0>();
-    }
-    exec_barrier();
-
-    const int64_t cbase = bidx * p.cs_b;
-    OA *part = (OA *)smem;   // epilogue hand-off [4 blocks][W * W][16][64 lanes]
-
-    auto body = [&](auto G_) {
-        constexpr int G = decltype(G_)::value;
-        constexpr int F = PS::first(G), NP = PS::count(G), ILO = PS::ilo(G), NA = PS::na(G);
-        constexpr int kReads = (NA + L) * W;
-        constexpr int NMF = NP * W * W;   // MFMAs per K step
-        struct Frags {
-            i32x4 a[NA][W];
-            i32x4 b[L][W];
-        };
-        Acc acc[NP][W][W];
-#pragma unroll
-        for (int q = 0; q < NP; ++q)
-#pragma unroll
-            for (int x = 0; x < W * W; ++x) acc[q][x / W][x % W] = MF::zero();
-
-        auto read_one = [&](int kb, int kk, int r, Frags &f) {
-            const int ch = 2 * kk + h;
-            if (r < NA * W) {
-                const int i = r / W, x = r % W;
-                f.a[i][x] = *(const i32x4 *)(slot(2 * kb) +
-                                             rswz<kDmaRB>((ILO + i) * BM + wm * 32 * W + 32 * x + lr, ch));
-            } else {
-                const int j = (r - NA * W) / W, x = (r - NA * W) % W;
-                f.b[j][x] = *(const i32x4 *)(slot(2 * kb + 1) +
-                                             rswz<kDmaRB>(j * BN + wn * 32 * W + 32 * x + lr, ch));
-            }
-        };
-        // One K step: the reads of the next K step (stage rkb, step nkk) into
-        // `nxt`, issued first, then the MFMAs of `cur` with this step's DMA
-        // instructions [lo, hi) of half stage kind (0: none, 1: A, 2: B) of
-        // stage dkb spread between them.
-        auto step = [&](const Frags &cur, Frags &nxt, int rkb, int nkk, int kind, int dkb, int lo,
-                        int hi) {
-            const int cnt = hi - lo;
-#pragma unroll
-            for (int q = 0; q < kReads; ++q) read_one(rkb, nkk, q, nxt);
-#pragma unroll
-            for (int n = 0; n < NMF; ++n) {
-                const int q = n / (W * W), x = (n / W) % W, y = n % W;
-                const int i = (F + q) / L, j = (F + q) % L;
-                acc[q][x][y] = MF::run(cur.a[i - ILO][x], cur.b[j][y], acc[q][x][y]);
-#pragma unroll
-                for (int d = 0; d < LPH; ++d) {
-                    // instruction lo + d goes after MFMA (d * NMF) / cnt
-                    if (d < cnt && (d * NMF) / cnt == n) {
-                        if (kind == 1) issue_a(dkb, lo + d);
-                        else if (kind == 2) issue_b(dkb, lo + d);
-                    }
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        };
-
-        Frags f0, f1;
-        if (nkb > 0) {
-#pragma unroll
-            for (int q = 0; q < kReads; ++q) read_one(0, 0, q, f0);
-        }
-        static_assert(STEPS == 4, "four 32-byte K steps per stage");
-        if (nkb == 0) issue_scales();
-        for (int kb = 0; kb < nkb; ++kb) {
-            const bool nb = kb + 1 < nkb, na = kb + 2 < nkb;
-            // no DMA is outstanding in the last stage: its waits are unaffected
-            if (!nb) issue_scales();
-            if constexpr (Sh::NSLOT == 6) {
-                // A(kb + 2) and B(kb + 2) take the slots of A(kb - 1) and
-                // B(kb - 1), released by the barrier of stage kb - 1
-                step(f0, f1, kb, 1, na ? 1 : 0, kb + 2, 0, Sh::A2);
-                step(f1, f0, kb, 2, na ? 1 : 0, kb + 2, Sh::A2, LPH);
-                step(f0, f1, kb, 3, na ? 2 : 0, kb + 2, 0, Sh::B0);
-                if (nb) {
-                    // stage kb + 1 has landed once only stage kb + 2's
-                    // instructions issued so far may be outstanding
-                    if (na) wait_vmcnt<LPH + Sh::B0>();
-                    else wait_vmcnt<0>();
-                    __builtin_amdgcn_s_waitcnt(0xC07F);
-                    exec_barrier();
-                }
-                step(f1, f0, kb + 1, 0, na ? 2 : 0, kb + 2, Sh::B0, LPH);
-            } else {
-                step(f0, f1, kb, 1, nb ? 2 : 0, kb + 1, 0, Sh::B0);
-                step(f1, f0, kb, 2, nb ? 2 : 0, kb + 1, Sh::B0, LPH);
-                step(f0, f1, kb, 3, na ? 1 : 0, kb + 2, 0, Sh::A2);
-                if (nb) {
-                    // stage kb + 1 has landed once only this wave's first part
-                    // of A(kb + 2) may be outstanding; the barrier publishes
-                    // every wave's DMA writes, and the lgkmcnt wait makes this
-                    // wave's reads of stage kb complete before slots are refilled
-                    if (na) wait_vmcnt<Sh::A2>();
-                    else wait_vmcnt<0>();
-                    __builtin_amdgcn_s_waitcnt(0xC07F);
-                    exec_barrier();
-                }
-                // the last step reads stage kb + 1's step 0 (unused past the end)
-                step(f1, f0, kb + 1, 0, na ? 1 : 0, kb + 2, Sh::A2, LPH);
-            }
-        }
-
-        // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
-        // every wave's scale DMA has landed and every wave is past its last
-        // ring read
-        wait_vmcnt<0>();
-        __builtin_amdgcn_s_waitcnt(0xC07F);
-        exec_barrier();
-        if (S > 1) {
-            // split-K: the ranges' accumulators into the last range's
-            // registers (the flag word sits in a ring slot no stage used)
-            constexpr int RW = (PS::count(0) > PS::count(1) ? PS::count(0) : PS::count(1)) * W * W * 16;
-            const int ln = lane_here();
-            uint32_t *mine = splitk_slot(p, g, krange, wave, RW, ln);
-#pragma unroll
-            for (int q = 0; q < NP; ++q)
-#pragma unroll
-                for (int x = 0; x < W * W; ++x) {
-                    const i32x16 u = __builtin_bit_cast(i32x16, acc[q][x / W][x % W]);
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) splitk_put(mine + ((q * W * W + x) * 16 + r) * 64, (uint32_t)u[r]);
-                }
-            if (!splitk_arrive(p, g, (int *)slot(2 * nkb + 1))) return;
-            if constexpr (MF::kExactAcc) {
-                // int32 sums are exact in any order: this range's
-                // accumulators stay, the other ranges are added
-                for (int s2 = 0; s2 < S; ++s2) {
-                    if (s2 == krange) continue;
-                    const uint32_t *src = splitk_slot(p, g, s2, wave, RW, ln);
-#pragma unroll
-                    for (int q = 0; q < NP; ++q)
-#pragma unroll
-                        for (int x = 0; x < W * W; ++x)
-                            acc[q][x / W][x % W] += splitk_get16<Acc>(src + (q * W * W + x) * 16 * 64);
-                }
-            } else {
-            // every range read back in range order: range 0 straight into
-            // the accumulators, then the others added one tile at a time
-            {
-                const uint32_t *src = splitk_slot(p, g, 0, wave, RW, ln);
-#pragma unroll
-                for (int q = 0; q < NP; ++q)
-#pragma unroll
-                    for (int x = 0; x < W * W; ++x)
-                        acc[q][x / W][x % W] = splitk_get16<Acc>(src + (q * W * W + x) * 16 * 64);
-            }
-            for (int s2 = 1; s2 < S; ++s2) {
-                const uint32_t *src = splitk_slot(p, g, s2, wave, RW, ln);
-#pragma unroll
-                for (int q = 0; q < NP; ++q)
-#pragma unroll
-                    for (int x = 0; x < W * W; ++x)
-                        acc[q][x / W][x % W] += splitk_get16<Acc>(src + (q * W * W + x) * 16 * 64);
-            }
-            }
-        }
-        // this wave's scales into registers: sa of its rows, sb of its columns
-        float sbv[W][L], sav[W][16][NA];
-#pragma unroll
-        for (int y = 0; y < W; ++y) {
-            const int ct = wn * 32 * W + 32 * y + lr;
-#pragma unroll
-            for (int j = 0; j < L; ++j) sbv[y][j] = sb_lds[j * BN + ct];
-        }
-#pragma unroll
-        for (int x = 0; x < W; ++x)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int rt = wm * 32 * W + 32 * x + 8 * (r >> 2) + 4 * h + (r & 3);
-#pragma unroll
-                for (int i = 0; i < NA; ++i) sav[x][r][i] = sa_lds[(ILO + i) * BM + rt];
-            }
-        // t value of pair q, block (x, y), accumulator row r:
-        // fl32(fl32(fl32(acc) * sa_i) * sb_j)
-        auto tval = [&](int q, int x, int y, int r) {
-            const int i = (F + q) / L, j = (F + q) % L;
-            const float t1 = MF::to_f32(acc[q][x][y][r]) * sav[x][r][i - ILO];
-            return t1 * sbv[y][j];
-        };
-        // the partial sums overwrite the scales: every wave has read them
-        __builtin_amdgcn_s_waitcnt(0xC07F);
-        exec_barrier();
-        if constexpr (G == 0) {
-#pragma unroll
-            for (int x = 0; x < W; ++x)
-#pragma unroll
-                for (int y = 0; y < W; ++y)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        OA out = (OA)0;
-#pragma unroll
-                        for (int q = 0; q < NP; ++q) out = out + (OA)tval(q, x, y, r);
-                        part[(((blk * W + x) * W + y) * 16 + r) * 64 + lane] = out;
-                    }
-            __builtin_amdgcn_s_waitcnt(0xC07F);
-            exec_barrier();
-        } else {
-            exec_barrier();
-#pragma unroll
-            for (int x = 0; x < W; ++x)
-#pragma unroll
-                for (int y = 0; y < W; ++y) {
-                    const int64_t col = n0 + wn * 32 * W + 32 * y + lr;
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int64_t row = m0 + wm * 32 * W + 32 * x + 8 * (r >> 2) + 4 * h + (r & 3);
-                        OA out = part[(((blk * W + x) * W + y) * 16 + r) * 64 + lane];
-#pragma unroll
-                        for (int q = 0; q < NP; ++q) out = out + (OA)tval(q, x, y, r);
-                        if (col < p.N && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
-                    }
-                }
-        }
-    };
-    if (grp == 0) body(std::integral_constant<int, 0>{});
-    else body(std::integral_constant<int, 1>{});
-}
-
-// ---------------------------------------------------------------------------
-// Wide kernel for num_splits 3: 64 x 128 tiles, 8 waves in a 2 x 4 grid of
-// 32 x 32 blocks, each wave holding all 9 slice pairs of its block (144
-// accumulator registers).  Per 32-byte K step a wave reads 3 A and 3 B
-// fragments for 9 MFMAs (the ring kernel's wave groups read 9 fragments for
-// the 9 MFMAs of two waves), and a stage of 128 bytes of K (24 KB of A rows,
-// 48 KB of B rows) feeds 288 MFMAs (the ring kernel's 48 KB: 144).  Each wave
-// sums its own pairs in the reference's i-major / j-minor order, so the
-// epilogue hands nothing between waves.
-// The LDS holds two whole stages (144 KB; the A and B halves differ in size,
-// so they do not form a ring of equal slots).  Stage kb + 2 is fetched into
-// stage kb's buffer, released by the barrier of stage kb: P1 instructions per
-// wave in the K step after that barrier, the rest in the next K step, and the
-// barrier of stage kb + 1 waits for all of them.
-// ---------------------------------------------------------------------------
-struct WideShape {
-    static constexpr int L = 3;
-    static constexpr int NW = 8;                         // waves
-    static constexpr int BM = 64, BN = 128;
-    static constexpr int A_BYTES = L * BM * kDmaRB;      // 24 KB
-    static constexpr int B_BYTES = L * BN * kDmaRB;      // 48 KB
-    static constexpr int STAGE = A_BYTES + B_BYTES;
-    static constexpr int LA = A_BYTES / (NW * 1024);     // A instructions per wave per stage
-    static constexpr int LB = B_BYTES / (NW * 1024);     // B instructions per wave per stage
-    static constexpr int LPS = LA + LB;
-    static constexpr int P1 = 5;                         // issued in the K step after the barrier
-    static constexpr int LDS_BYTES = 2 * STAGE;
-    static_assert(A_BYTES % (NW * 1024) == 0 && B_BYTES % (NW * 1024) == 0,
-                  "a half stage must be whole 1 KB windows per wave");
-    static_assert(P1 >= LPS - P1 && P1 <= LPS, "the larger part goes first");
-    static_assert(LDS_BYTES <= 160 * 1024, "LDS");
-    static_assert(L * (BM + BN) * 4 <= STAGE, "the tile's scales fit a stage buffer");
-    static_assert(kDmaRB == 128, "128-byte stage rows");
-};
-
-template <typename ST, typename AccT>
-__global__ __launch_bounds__(512, 1) void cross_gemm_wide_kernel(GemmParams p, int group_m,
-                                                                 uint32_t a_records,
-                                                                 uint32_t b_records) {
-    using Sh = WideShape;
-    using MF = Mfma<ST>;
-    using Acc = typename MF::Acc;
-    using OA = AccT;
-    constexpr int L = Sh::L, BM = Sh::BM, BN = Sh::BN;
-    constexpr int ES = (int)sizeof(ST);
-    constexpr uint32_t kOOB = 0x80000000u;
-    extern __shared__ __attribute__((aligned(16))) char smem[];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 2, wn = wave & 3;
-    const int h = lane >> 5, lr = lane & 31;
-
-    const int64_t tiles_m = (p.M + BM - 1) / BM;
-    const int64_t tiles_n = (p.N + BN - 1) / BN;
-    const int64_t tiles = tiles_m * tiles_n;
-    // split-K: workgroup g0 is K range g0 % S of tile g0 / S
-    const int S = p.ksplit > 1 ? p.ksplit : 1;
-    const int64_t g0 = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
-    const int krange = (int)(g0 % S);
-    const int64_t g = g0 / S;
-    const int64_t bidx = g / tiles;
-    const int64_t t = g % tiles;
-    const int64_t width = (int64_t)group_m * tiles_n;
-    const int64_t first_m = (t / width) * group_m;
-    const int64_t gsz = (tiles_m - first_m < group_m) ? (tiles_m - first_m) : group_m;
-    const int64_t tm = first_m + (t % width) % gsz;
-    const int64_t tn = (t % width) / gsz;
-    const int64_t m0 = tm * BM, n0 = tn * BN;
-
-    const uint32_t kbytes = (uint32_t)(p.K * ES);
-    const int nkb_all = (int)((kbytes + kDmaRB - 1) / kDmaRB);
-    const int kb0 = S > 1 ? krange * p.kb_per_split : 0;   // this range's first stage
-    const int nkb = S > 1 ? min(p.kb_per_split, nkb_all - kb0) : nkb_all;
-    const uint32_t kbyte0 = (uint32_t)kb0 * kDmaRB;
-
-    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)((const char *)p.A + bidx * p.as_b * ES), (short)0, (int)a_records, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)((const char *)p.B + bidx * p.bs_b * ES), (short)0, (int)b_records, 0x00020000);
-
-    // This wave's LPS DMA instructions of a stage: q < LA fetch window
-    // wave * LA + q of the A half, the others window wave * LB + q - LA of the
-    // B half (a 1 KB window is 8 whole 128-byte rows; lane -> row lane / 8,
-    // physical chunk lane % 8, which holds logical chunk pc ^ ((r >> 1) & 7);
-    // with r = 8 window + lane / 8 that is c0, or c0 ^ 4 in an odd window).
-    auto window = [&](int q) { return q < Sh::LA ? wave * Sh::LA + q : wave * Sh::LB + q - Sh::LA; };
-    const int c0 = (lane & 7) ^ (lane >> 4);
-    uint32_t src[Sh::LPS];
-#pragma unroll
-    for (int q = 0; q < Sh::LPS; ++q) {
-        const int r = window(q) * 8 + lane / 8;
-        if (q < Sh::LA) {
-            const int64_t m = m0 + r % BM;
-            src[q] = (m < p.M) ? (uint32_t)(((int64_t)(r / BM) * p.as_l + m * p.as_m) * ES) : kOOB;
-        } else {
-            const int64_t n = n0 + r % BN;
-            src[q] = (n < p.N) ? (uint32_t)(((int64_t)(r / BN) * p.bs_l + n * p.bs_n) * ES) : kOOB;
-        }
-    }
-    auto buf = [&](int kb) { return smem + (kb & 1) * Sh::STAGE; };
-    auto issue = [&](int kb, int q) {
-        const int ch = c0 ^ ((window(q) & 1) << 2);
-        const uint32_t kofs = kbyte0 + (uint32_t)kb * kDmaRB + ch * 16;
-        const uint32_t vo = (src[q] == kOOB || kofs >= kbytes) ? kOOB : src[q] + kofs;
-        auto *ldsp = (__attribute__((address_space(3))) void *)(
-            buf(kb) + (q < Sh::LA ? 0 : Sh::A_BYTES) + window(q) * 1024);
-        if (q < Sh::LA) __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, ldsp, 16, vo, 0, 0, 0);
-        else __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, ldsp, 16, vo, 0, 0, 0);
-    };
-
-    // The tile's scales (A's [L][BM], then B's [L][BN]: 2304 bytes) are
-    // fetched by dword DMA into the buffer of stage nkb, which holds no stage
-    // the tile still reads, at the start of the last stage: instruction
-    // u < 9 (wave u and wave u - 8) fetches entries 64 u .. 64 u + 63, the
-    // first 3 of A's scales, the next 6 of B's.
-    char *const scl = buf(nkb);
-    auto issue_scales = [&]() {
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const int u = q * Sh::NW + wave;
-            if (u >= L * (BM + BN) / 64) break;
-            const bool isa = u < L * BM / 64;
-            const int e = (isa ? u : u - L * BM / 64) * 64 + lane;
-            const int s = isa ? e / BM : e / BN;                 // slice
-            const int64_t rc = isa ? m0 + e % BM : n0 + e % BN;  // row of A / column of B
-            const int64_t ext = isa ? ((int64_t)(L - 1) * p.sas_l + (p.M - 1) * p.sas_m + 1)
-                                    : ((int64_t)(L - 1) * p.sbs_l + (p.N - 1) * p.sbs_n + 1);
-            const bool ok = rc < (isa ? p.M : p.N);
-            const uint32_t vo = ok ? (uint32_t)(((int64_t)s * (isa ? p.sas_l : p.sbs_l) +
-                                                 rc * (isa ? p.sas_m : p.sbs_n)) * 4)
-                                   : kOOB;
-            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-                (void *)(isa ? p.sa + bidx * p.sas_b : p.sb + bidx * p.sbs_b), (short)0,
-                (int)(ext * 4 < 0x7FFFFFFF ? ext * 4 : 0x7FFFFFFF), 0x00020000);
-            auto *ldsp = (__attribute__((address_space(3))) void *)(scl + u * 256);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, ldsp, 4, vo, 0, 0, 0);
-        }
-    };
-    const float *sa_lds = (const float *)scl, *sb_lds = (const float *)(scl + L * BM * 4);
-
-    // prologue: stages 0 and 1; stage 0 must land before the first reads
-#pragma unroll
-    for (int q = 0; q < Sh::LPS; ++q) issue(0, q);
-    if (nkb > 1) {
-#pragma unroll
-        for (int q = 0; q < Sh::LPS; ++q) issue(1, q);
-        wait_vmcnt<Sh::LPS>();
-    } else {
-        wait_vmcnt<0>();
-    }
-    exec_barrier();
-
-    struct Frags {
-        i32x4 a[L];
-        i32x4 b[L];
-    };
-    Acc acc[L][L];
-#pragma unroll
-    for (int i = 0; i < L; ++i)
-#pragma unroll
-        for (int j = 0; j < L; ++j) acc[i][j] = MF::zero();
-
-    auto read_one = [&](int kb, int kk, int r, Frags &f) {
-        const int c = 2 * kk + h;
-        if (r < L) f.a[r] = *(const i32x4 *)(buf(kb) + rswz<kDmaRB>(r * BM + wm * 32 + lr, c));
-        else
-            f.b[r - L] = *(const i32x4 *)(buf(kb) + Sh::A_BYTES +
-                                          rswz<kDmaRB>((r - L) * BN + wn * 32 + lr, c));
-    };
-    // One K step: the reads of the next K step (stage rkb, step nkk) into
-    // `nxt`, issued first, then the 9 MFMAs of `cur` with, if `on`, DMA
-    // instructions [lo, hi) of stage dkb spread between them (lo and hi are
-    // constants at every call, so the spread folds at compile time).
-    auto step = [&](const Frags &cur, Frags &nxt, int rkb, int nkk, int dkb, bool on, int lo,
-                    int hi) {
-        const int cnt = hi - lo;
-#pragma unroll
-        for (int q = 0; q < 2 * L; ++q) read_one(rkb, nkk, q, nxt);
-#pragma unroll
-        for (int n = 0; n < L * L; ++n) {
-            const int i = n / L, j = n % L;
-            acc[i][j] = MF::run(cur.a[i], cur.b[j], acc[i][j]);
-#pragma unroll
-            for (int d = 0; d < Sh::P1; ++d) {
-                // instruction lo + d goes after MFMA (d * L * L) / cnt
-                if (d < cnt && (d * L * L) / cnt == n && on) issue(dkb, lo + d);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
-
-    Frags f0, f1;
-    if (nkb > 0) {
-#pragma unroll
-        for (int q = 0; q < 2 * L; ++q) read_one(0, 0, q, f0);
-    }
-    static_assert(kDmaRB / 32 == 4, "four 32-byte K steps per stage");
-    if (nkb == 0) issue_scales();
-    for (int kb = 0; kb < nkb; ++kb) {
-        const bool nb = kb + 1 < nkb, n2 = kb + 2 < nkb;
-        // no DMA is outstanding in the last stage: its waits are unaffected
-        if (!nb) issue_scales();
-        // the rest of stage kb + 1 (stage 1 went out whole in the prologue)
-        step(f0, f1, kb, 1, kb + 1, nb && kb >= 1, Sh::P1, Sh::LPS);
-        step(f1, f0, kb, 2, kb + 1, false, 0, 0);
-        step(f0, f1, kb, 3, kb + 1, false, 0, 0);
-        if (nb) {
-            // stage kb + 1 is the only DMA outstanding; the barrier publishes
-            // every wave's DMA writes, and the lgkmcnt wait makes this wave's
-            // reads of stage kb complete before its buffer is refilled
-            wait_vmcnt<0>();
-            __builtin_amdgcn_s_waitcnt(0xC07F);
-            exec_barrier();
-        }
-        // the last step reads stage kb + 1's step 0 (unused past the end)
-        step(f1, f0, kb + 1, 0, kb + 2, n2, 0, Sh::P1);
-    }
-
-    // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
-    wait_vmcnt<0>();
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    exec_barrier();
-    if (S > 1) {
-        // split-K: the ranges' accumulators into the last range's registers
-        // (the flag word sits in the stage buffer the scales did not use)
-        constexpr int RW = L * L * 16;
-        const int ln = lane_here();
-        uint32_t *mine = splitk_slot(p, g, krange, wave, RW, ln);
-#pragma unroll
-        for (int n = 0; n < L * L; ++n) {
-            const i32x16 u = __builtin_bit_cast(i32x16, acc[n / L][n % L]);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) splitk_put(mine + (n * 16 + r) * 64, (uint32_t)u[r]);
-        }
-        if (!splitk_arrive(p, g, (int *)buf(nkb + 1))) return;
-        if constexpr (MF::kExactAcc) {
-            // int32 sums are exact in any order: this range's accumulators
-            // stay, the other ranges are added one tile (16 loads in
-            // flight) at a time
-            for (int s2 = 0; s2 < S; ++s2) {
-                if (s2 == krange) continue;
-                const uint32_t *src = splitk_slot(p, g, s2, wave, RW, ln);
-#pragma unroll
-                for (int n = 0; n < L * L; ++n)
-                    acc[n / L][n % L] += splitk_get16<Acc>(src + n * 16 * 64);
-            }
-        } else {
-            // every range read back, this one's too, in range order: range
-            // 0 straight into the accumulators, then the others added
-            {
-                const uint32_t *src = splitk_slot(p, g, 0, wave, RW, ln);
-#pragma unroll
-                for (int n = 0; n < L * L; ++n) acc[n / L][n % L] = splitk_get16<Acc>(src + n * 16 * 64);
-            }
-            for (int s2 = 1; s2 < S; ++s2) {
-                const uint32_t *src = splitk_slot(p, g, s2, wave, RW, ln);
-#pragma unroll
-                for (int n = 0; n < L * L; ++n)
-                    acc[n / L][n % L] += splitk_get16<Acc>(src + n * 16 * 64);
-            }
-        }
-    }
-    const int ct = wn * 32 + lr;
-    const int64_t col = n0 + ct;
-    const int64_t cbase = bidx * p.cs_b;
-    float sbv[L];
-#pragma unroll
-    for (int j = 0; j < L; ++j) sbv[j] = sb_lds[j * BN + ct];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int rt = wm * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-        const int64_t row = m0 + rt;
-        OA out = (OA)0;
-#pragma unroll
-        for (int i = 0; i < L; ++i) {
-            const float sai = sa_lds[i * BM + rt];
-#pragma unroll
-            for (int j = 0; j < L; ++j) {
-                // fl32(fl32(fl32(acc) * sa_i) * sb_j), summed i-major, j-minor
-                const float t1 = MF::to_f32(acc[i][j][r]) * sai;
-                out = out + (OA)(t1 * sbv[j]);
-            }
-        }
-        if (col < p.N && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Wide kernel for num_splits 4: 96 x 64 tiles (row blocks x = 0..2, column
-// blocks y = 0..1 of 32 x 32), 8 waves of 12 accumulator tiles each, so that
-// every wave reads 3 A and 4 B fragments per 32-byte K step for 12 MFMAs
-// (0.58 fragment reads per MFMA; the ring kernel's 64 x 64 tiles: 0.75) and a
-// stage of 128 bytes of K (48 KB of A rows, 32 KB of B rows) feeds 384 MFMAs
-// (0.21 KB of DMA per MFMA; ring: 0.25).
-//   * waves 0..5 (x = wave / 2, y = wave % 2) hold the pairs i = 0..2, j = 0..3
-//     of block (x, y): A fragments (slice u, rows of x), u = 0..2;
-//   * waves 6, 7 (y = wave - 6) hold the pairs i = 3, j = 0..3 of the blocks
-//     (0..2, y): A fragments (slice 3, rows of block u), u = 0..2;
-//   * every wave: B fragments (slice j, columns of y), j = 0..3, and
-//     acc[u][j] += A_u . B_j.
-// The reference's sum runs i-major, so the i = 3 pairs come last: a wave of
-// the first kind sums its 12 pairs in order from +0 and hands the partial to
-// the wave of its y through the LDS, which adds its 4 pairs in order and
-// stores C.  The second kind converts its accumulators to the fp32 t values
-// before the hand-off barrier, so only the additions follow it.
-// 12 accumulator tiles are 192 registers of the 256 a wave has at two waves
-// per SIMD, so only the A fragments are double-buffered: the B fragments of
-// the next K step are read one by one as the MFMAs of the current step
-// release them (j-outer order), 9 MFMAs before their first use.
-// The LDS holds two whole stages (160 KB); stage kb + 2 is fetched into stage
-// kb's buffer after the barrier of stage kb, P1 instructions per wave in the
-// K step after that barrier and the rest in the next.
-// ---------------------------------------------------------------------------
-struct Wide4Shape {
-    static constexpr int L = 4;
-    static constexpr int NW = 8;                         // waves
-    static constexpr int BM = 96, BN = 64;
-    static constexpr int A_BYTES = L * BM * kDmaRB;      // 48 KB
-    static constexpr int B_BYTES = L * BN * kDmaRB;      // 32 KB
-    static constexpr int STAGE = A_BYTES + B_BYTES;
-    static constexpr int LA = A_BYTES / (NW * 1024);     // A instructions per wave per stage
-    static constexpr int LB = B_BYTES / (NW * 1024);     // B instructions per wave per stage
-    static constexpr int LPS = LA + LB;
-    static constexpr int P1 = 6;                         // issued in the K step after the barrier
-    static constexpr int LDS_BYTES = 2 * STAGE;
-    static constexpr int NSC = L * (BM + BN) / 64;       // scale instructions (64 entries each)
-    static_assert(A_BYTES % (NW * 1024) == 0 && B_BYTES % (NW * 1024) == 0,
-                  "a half stage must be whole 1 KB windows per wave");
-    static_assert(P1 >= LPS - P1 && P1 <= LPS, "the larger part goes first");
-    static_assert(LDS_BYTES <= 160 * 1024, "LDS");
-    static_assert(NSC <= 2 * NW, "two scale instructions per wave at most");
-    static_assert(kDmaRB == 128, "128-byte stage rows");
-};
-
-template <typename ST, typename AccT>
-__global__ __launch_bounds__(512, 1) void cross_gemm_wide4_kernel(GemmParams p, int group_m,
-                                                                  uint32_t a_records,
-                                                                  uint32_t b_records) {
-    using Sh = Wide4Shape;
-    using MF = Mfma<ST>;
-    using Acc = typename MF::Acc;
-    using OA = AccT;
-    constexpr int L = Sh::L, BM = Sh::BM, BN = Sh::BN;
-    constexpr int ES = (int)sizeof(ST);
-    constexpr uint32_t kOOB = 0x80000000u;
-    extern __shared__ __attribute__((aligned(16))) char smem[];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const bool last_i = wave >= 6;                 // holds the pairs i = 3
-    const int wy = last_i ? wave - 6 : (wave & 1);
-    const int wx = last_i ? 0 : (wave >> 1);
-    // A fragment u: LDS row a_row0 + u * a_rstep (+ lane row)
-    const int a_row0 = last_i ? 3 * BM : wx * 32;
-    const int a_rstep = last_i ? 32 : BM;
-    const int h = lane >> 5, lr = lane & 31;
-
-    const int64_t tiles_m = (p.M + BM - 1) / BM;
-    const int64_t tiles_n = (p.N + BN - 1) / BN;
-    const int64_t tiles = tiles_m * tiles_n;
-    const int64_t g = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
-    const int64_t bidx = g / tiles;
-    const int64_t t = g % tiles;
-    const int64_t width = (int64_t)group_m * tiles_n;
-    const int64_t first_m = (t / width) * group_m;
-    const int64_t gsz = (tiles_m - first_m < group_m) ? (tiles_m - first_m) : group_m;
-    const int64_t tm = first_m + (t % width) % gsz;
-    const int64_t tn = (t % width) / gsz;
-    const int64_t m0 = tm * BM, n0 = tn * BN;
-
-    const uint32_t kbytes = (uint32_t)(p.K * ES);
-    const int nkb = (int)((kbytes + kDmaRB - 1) / kDmaRB);
-
-    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)((const char *)p.A + bidx * p.as_b * ES), (short)0, (int)a_records, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)((const char *)p.B + bidx * p.bs_b * ES), (short)0, (int)b_records, 0x00020000);
-
-    // This wave's LPS DMA instructions of a stage: q < LA fetch window
-    // wave * LA + q of the A half, the others window wave * LB + q - LA of the
-    // B half (a 1 KB window is 8 whole 128-byte rows; lane -> row lane / 8,
-    // physical chunk lane % 8, which holds logical chunk pc ^ ((r >> 1) & 7);
-    // with r = 8 window + lane / 8 that is c0, or c0 ^ 4 in an odd window).
-    // A window (8 rows) never straddles a slice (96 or 64 rows = 12 or 8
-    // windows), so an instruction's source offset is a wave-uniform part (slice,
-    // first row of the window, K block) plus one of four per-lane parts (lane
-    // row lane / 8 and chunk, for A or B and even or odd windows).  The uniform
-    // part goes through readfirstlane at each use, so the compiler keeps just
-    // the four lane parts in registers instead of one sum per instruction.
-    auto window = [&](int q) { return q < Sh::LA ? wave * Sh::LA + q : wave * Sh::LB + q - Sh::LA; };
-    const int lrow = lane >> 3;
-    const int c0 = (lane & 7) ^ (lane >> 4);
-    const uint32_t ch16[2] = {(uint32_t)c0 * 16, (uint32_t)(c0 ^ 4) * 16};
-    const uint32_t a_lp[2] = {(uint32_t)(lrow * p.as_m * ES) + ch16[0],
-                              (uint32_t)(lrow * p.as_m * ES) + ch16[1]};
-    const uint32_t b_lp[2] = {(uint32_t)(lrow * p.bs_n * ES) + ch16[0],
-                              (uint32_t)(lrow * p.bs_n * ES) + ch16[1]};
-    auto buf = [&](int kb) { return smem + (kb & 1) * Sh::STAGE; };
-    auto issue = [&](int kb, int q) {
-        const int w = window(q);
-        const int par = w & 1;
-        int64_t first, rows;
-        int64_t ubase;
-        if (q < Sh::LA) {
-            first = m0 + (w % (BM / 8)) * 8;
-            rows = p.M;
-            ubase = ((int64_t)(w / (BM / 8)) * p.as_l + first * p.as_m) * ES;
-        } else {
-            first = n0 + (w % (BN / 8)) * 8;
-            rows = p.N;
-            ubase = ((int64_t)(w / (BN / 8)) * p.bs_l + first * p.bs_n) * ES;
-        }
-        const int rows_left = (int)(rows - first < 8 ? rows - first : 8);   // may be <= 0
-        const int kleft = (int)kbytes - kb * kDmaRB;                       // > 0
-        const uint32_t ub = (uint32_t)__builtin_amdgcn_readfirstlane((int)(ubase + kb * kDmaRB));
-        const bool ok = lrow < rows_left && (int)ch16[par] < kleft;
-        const uint32_t vo = ok ? (q < Sh::LA ? a_lp[par] : b_lp[par]) + ub : kOOB;
-        auto *ldsp = (__attribute__((address_space(3))) void *)(
-            buf(kb) + (q < Sh::LA ? 0 : Sh::A_BYTES) + w * 1024);
-        if (q < Sh::LA) __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, ldsp, 16, vo, 0, 0, 0);
-        else __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, ldsp, 16, vo, 0, 0, 0);
-    };
-
-    // The tile's scales (A's [L][BM], then B's [L][BN]: 2560 bytes) are
-    // fetched by dword DMA into the buffer of stage nkb, which holds no stage
-    // the tile still reads, at the start of the last stage: instruction
-    // u < NSC (wave u and wave u - 8) fetches entries 64 u .. 64 u + 63.
-    char *const scl = buf(nkb);
-    auto issue_scales = [&]() {
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const int u = q * Sh::NW + wave;
-            if (u >= Sh::NSC) break;
-            const bool isa = u < L * BM / 64;
-            const int e = (isa ? u : u - L * BM / 64) * 64 + lane;
-            const int s = isa ? e / BM : e / BN;                 // slice
-            const int64_t rc = isa ? m0 + e % BM : n0 + e % BN;  // row of A / column of B
-            const int64_t ext = isa ? ((int64_t)(L - 1) * p.sas_l + (p.M - 1) * p.sas_m + 1)
-                                    : ((int64_t)(L - 1) * p.sbs_l + (p.N - 1) * p.sbs_n + 1);
-            const bool ok = rc < (isa ? p.M : p.N);
-            const uint32_t vo = ok ? (uint32_t)(((int64_t)s * (isa ? p.sas_l : p.sbs_l) +
-                                                 rc * (isa ? p.sas_m : p.sbs_n)) * 4)
-                                   : kOOB;
-            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-                (void *)(isa ? p.sa + bidx * p.sas_b : p.sb + bidx * p.sbs_b), (short)0,
-                (int)(ext * 4 < 0x7FFFFFFF ? ext * 4 : 0x7FFFFFFF), 0x00020000);
-            auto *ldsp = (__attribute__((address_space(3))) void *)(scl + u * 256);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, ldsp, 4, vo, 0, 0, 0);
-        }
-    };
-    const float *sa_lds = (const float *)scl, *sb_lds = (const float *)(scl + L * BM * 4);
-
-    // prologue: stages 0 and 1; stage 0 must land before the first reads
-#pragma unroll
-    for (int q = 0; q < Sh::LPS; ++q) issue(0, q);
-    if (nkb > 1) {
-#pragma unroll
-        for (int q = 0; q < Sh::LPS; ++q) issue(1, q);
-        wait_vmcnt<Sh::LPS>();
-    } else {
-        wait_vmcnt<0>();
-    }
-    exec_barrier();
-
-    struct FragsA {
-        i32x4 a[3];
-    };
-    i32x4 fb[L];   // B fragments, single-buffered
-    Acc acc[3][L];
-#pragma unroll
-    for (int u = 0; u < 3; ++u)
-#pragma unroll
-        for (int j = 0; j < L; ++j) acc[u][j] = MF::zero();
-
-    // Fragment rows start at multiples of 32, so the swizzle key of a lane's
-    // row, ((row >> 1) & 7), is that of lr for every fragment: the address is
-    // a wave-uniform row offset plus one of four per-lane offsets (one per
-    // K step of a stage), rswz<kDmaRB> with its terms regrouped.
-    // The uniform part (buffer, first row) goes through readfirstlane at each
-    // use, so only the four per-lane offsets stay in registers.
-    const int key = (lr >> 1) & 7;
-    int lane_rd[4];
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) lane_rd[kk] = lr * kDmaRB + (((2 * kk + h) ^ key) << 4);
-    const int smem_base = (int)(uintptr_t)(__attribute__((address_space(3))) char *)smem;
-    auto lds_at = [&](int uniform, int kk) {
-        const int u = __builtin_amdgcn_readfirstlane(uniform);
-        return (const __attribute__((address_space(3))) i32x4 *)(uintptr_t)(u + lane_rd[kk]);
-    };
-    auto read_a = [&](int kb, int kk, int u, FragsA &f) {
-        f.a[u] = *lds_at(smem_base + (kb & 1) * Sh::STAGE + (a_row0 + u * a_rstep) * kDmaRB, kk);
-    };
-    auto read_b = [&](int kb, int kk, int j) {
-        fb[j] = *lds_at(smem_base + (kb & 1) * Sh::STAGE + Sh::A_BYTES + (j * BN + wy * 32) * kDmaRB, kk);
-    };
-    // One K step: the A reads of the next K step (stage rkb, step nkk) into
-    // `nxt`, issued first; then the 12 MFMAs of `cur` and the current B
-    // fragments, j-outer, each B fragment re-read for the next step after its
-    // last MFMA; with, if `on`, DMA instructions [lo, hi) of stage dkb spread
-    // between them (lo and hi are constants at every call, so the spread
-    // folds at compile time).
-    auto step = [&](const FragsA &cur, FragsA &nxt, int rkb, int nkk, int dkb, bool on, int lo,
-                    int hi) {
-        const int cnt = hi - lo;
-#pragma unroll
-        for (int u = 0; u < 3; ++u) read_a(rkb, nkk, u, nxt);
-#pragma unroll
-        for (int n = 0; n < 3 * L; ++n) {
-            const int j = n / 3, u = n % 3;
-            acc[u][j] = MF::run(cur.a[u], fb[j], acc[u][j]);
-            if (u == 2) read_b(rkb, nkk, j);
-#pragma unroll
-            for (int d = 0; d < Sh::P1; ++d) {
-                // instruction lo + d goes after MFMA (d * 12) / cnt
-                if (d < cnt && (d * 3 * L) / cnt == n && on) issue(dkb, lo + d);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
-
-    FragsA f0, f1;
-    if (nkb > 0) {
-#pragma unroll
-        for (int u = 0; u < 3; ++u) read_a(0, 0, u, f0);
-#pragma unroll
-        for (int j = 0; j < L; ++j) read_b(0, 0, j);
-    }
-    static_assert(kDmaRB / 32 == 4, "four 32-byte K steps per stage");
-    if (nkb == 0) issue_scales();
-    for (int kb = 0; kb < nkb; ++kb) {
-        const bool nb = kb + 1 < nkb, n2 = kb + 2 < nkb;
-        // no DMA is outstanding in the last stage: its waits are unaffected
-        if (!nb) issue_scales();
-        // the rest of stage kb + 1 (stage 1 went out whole in the prologue)
-        step(f0, f1, kb, 1, kb + 1, nb && kb >= 1, Sh::P1, Sh::LPS);
-        step(f1, f0, kb, 2, kb + 1, false, 0, 0);
-        step(f0, f1, kb, 3, kb + 1, false, 0, 0);
-        if (nb) {
-            // stage kb + 1 is the only DMA outstanding; the barrier publishes
-            // every wave's DMA writes, and the lgkmcnt wait makes this wave's
-            // reads of stage kb complete before its buffer is refilled
-            wait_vmcnt<0>();
-            __builtin_amdgcn_s_waitcnt(0xC07F);
-            exec_barrier();
-        }
-        // the last step reads stage kb + 1's step 0 (unused past the end)
-        step(f1, f0, kb + 1, 0, kb + 2, n2, 0, Sh::P1);
-    }
-
-    // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
-    wait_vmcnt<0>();
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    exec_barrier();
-    const int ct = wy * 32 + lr;
-    const int64_t col = n0 + ct;
-    const int64_t cbase = bidx * p.cs_b;
-    float sbv[L];
-#pragma unroll
-    for (int j = 0; j < L; ++j) sbv[j] = sb_lds[j * BN + ct];
-    // rows of accumulator registers 4 q .. 4 q + 3 of A fragment u, inside the
-    // tile, start at row4(u, q): their 4 scales are one 16-byte LDS read
-    auto row4 = [&](int u, int q) { return (last_i ? u * 32 : wx * 32) + 8 * q + 4 * h; };
-    auto sa4 = [&](int i, int u, int q) {
-        return *(const f32x4 *)(sa_lds + i * BM + row4(u, q));
-    };
-    // the i = 3 waves: t values fl32(fl32(fl32(acc) * sa_3) * sb_j) in place
-    // of their accumulators, before the hand-off (one block at a time, each
-    // behind a scheduling barrier: the scale reads are not hoisted).  The
-    // accumulator vectors are bit-cast whole: with this compiler a bit-cast of
-    // single elements of a vector reads element 0.
-    if (last_i) {
-#pragma unroll
-        for (int u = 0; u < 3; ++u) {
-            f32x4 s4[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) s4[q] = sa4(3, u, q);
-#pragma unroll
-            for (int j = 0; j < L; ++j) {
-                f32x16 tv;
-#pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    tv[r] = (MF::to_f32(acc[u][j][r]) * s4[r >> 2][r & 3]) * sbv[j];
-                acc[u][j] = __builtin_bit_cast(Acc, tv);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-    // the partial sums go to the buffer of the last stage, which every wave
-    // has finished reading (the scales sit in the other one)
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    exec_barrier();
-    OA *part = (OA *)buf(nkb + 1);   // [6 blocks][16][64 lanes]
-    static_assert(6 * 16 * 64 * sizeof(OA) <= Sh::STAGE, "the partials fit a stage buffer");
-    if (!last_i) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            f32x4 s4[3];
-#pragma unroll
-            for (int i = 0; i < 3; ++i) s4[i] = sa4(i, 0, q);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = 4 * q + e;
-                OA out = (OA)0;
-#pragma unroll
-                for (int i = 0; i < 3; ++i)
-#pragma unroll
-                    for (int j = 0; j < L; ++j) {
-                        // fl32(fl32(fl32(acc) * sa_i) * sb_j), summed i-major, j-minor
-                        const float t1 = MF::to_f32(acc[i][j][r]) * s4[i][e];
-                        out = out + (OA)(t1 * sbv[j]);
-                    }
-                part[(wave * 16 + r) * 64 + lane] = out;
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        __builtin_amdgcn_s_waitcnt(0xC07F);
-        exec_barrier();
-    } else {
-        exec_barrier();
-#pragma unroll
-        for (int u = 0; u < 3; ++u) {
-            f32x16 tv[L];
-#pragma unroll
-            for (int j = 0; j < L; ++j) tv[j] = __builtin_bit_cast(f32x16, acc[u][j]);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t row = m0 + row4(u, r >> 2) + (r & 3);
-                OA out = part[((u * 2 + wy) * 16 + r) * 64 + lane];
-#pragma unroll
-                for (int j = 0; j < L; ++j) out = out + (OA)tv[j][r];
-                if (col < p.N && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
-            }
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// num_splits 5: one wave per SIMD, each holding all 25 slice pairs of one
-// 32 x 32 block ("solo" kernel).  4 waves of 512 registers cover a 64 x 64
-// tile: wave (x, y) = (w / 2, w % 2) reads 5 A fragments (slice u, rows of
-// x) and 5 B fragments (slice j, columns of y) per 32-byte K step for 25
-// MFMAs (0.4 fragment reads per MFMA), and sums its own pairs in the
-// reference's i-major order: one launch, no hand-off, C written once.
-// The 25 accumulator tiles take 400 registers, more than either register
-// file holds (256 each), so each MFMA is written out with its accumulator
-// placed explicitly: tiles 0..15 in AGPRs, 16..24 in VGPRs (the compiler
-// does not split a kernel's MFMA accumulators between the two files by
-// itself).  The fragments are double-buffered: a K step's 10 reads are
-// issued one whole K step ahead.  A lone wave issues independent MFMAs at
-// 92-95% of the rate two waves reach (measured with 12 accumulators).
-// Hazards of the hand-placed MFMAs that the compiler cannot see: their
-// results are read by other instructions only in the epilogue, after 64 wait
-// states; an accumulator is first read as srcC after its zero fill and the
-// prologue's barrier; each one is accumulated again only 25 MFMAs later.
-// The LDS holds two whole stages of 128 bytes of K (2 x 80 KB); stage kb + 2
-// is fetched into stage kb's buffer after the barrier of stage kb, spread
-// over the two K steps that follow it.
-// ---------------------------------------------------------------------------
-struct Solo5Shape {
-    static constexpr int L = 5, BM = 64, BN = 64;
-    static constexpr int NW = 4;                         // waves
-    static constexpr int A_BYTES = L * BM * kDmaRB;      // 40 KB
-    static constexpr int B_BYTES = L * BN * kDmaRB;      // 40 KB
-    static constexpr int STAGE = A_BYTES + B_BYTES;
-    static constexpr int LA = A_BYTES / (NW * 1024);     // A instructions per wave per stage
-    static constexpr int LB = B_BYTES / (NW * 1024);
-    static constexpr int LPS = LA + LB;
-    static constexpr int P1 = LPS / 2;                   // issued in the K step after the barrier
-    static constexpr int LDS_BYTES = 2 * STAGE;
-    static constexpr int NSC = L * (BM + BN) / 64;       // scale instructions (64 entries each)
-    static constexpr int SCQ = (NSC + NW - 1) / NW;
-    static constexpr int NAGPR = 16;                     // accumulator tiles in AGPRs
-    static_assert(A_BYTES % (NW * 1024) == 0 && B_BYTES % (NW * 1024) == 0,
-                  "a half stage must be whole 1 KB windows per wave");
-    static_assert(LDS_BYTES <= 160 * 1024, "LDS");
-    static_assert(kDmaRB == 128, "128-byte stage rows");
-};
-
-template <typename ST, typename AccT>
-__global__ __launch_bounds__(256, 1) void cross_gemm_solo5_kernel(GemmParams p, int group_m,
-                                                                  uint32_t a_records,
-                                                                  uint32_t b_records) {
-    using Sh = Solo5Shape;
-    using MF = Mfma<ST>;
-    using Acc = typename MF::Acc;
-    using OA = AccT;
-    constexpr int L = Sh::L, BM = Sh::BM, BN = Sh::BN;
-    constexpr int ES = (int)sizeof(ST);
-    constexpr uint32_t kOOB = 0x80000000u;
-    extern __shared__ __attribute__((aligned(16))) char smem[];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wx = wave >> 1, wy = wave & 1;
-    const int h = lane >> 5, lr = lane & 31;
-
-    const int64_t tiles_m = (p.M + BM - 1) / BM;
-    const int64_t tiles_n = (p.N + BN - 1) / BN;
-    const int64_t tiles = tiles_m * tiles_n;
-    const int64_t g = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
-    const int64_t bidx = g / tiles;
-    const int64_t t = g % tiles;
-    const int64_t width = (int64_t)group_m * tiles_n;
-    const int64_t first_m = (t / width) * group_m;
-    const int64_t gsz = (tiles_m - first_m < group_m) ? (tiles_m - first_m) : group_m;
-    const int64_t tm = first_m + (t % width) % gsz;
-    const int64_t tn = (t % width) / gsz;
-    const int64_t m0 = tm * BM, n0 = tn * BN;
-
-    const uint32_t kbytes = (uint32_t)(p.K * ES);
-    const int nkb = (int)((kbytes + kDmaRB - 1) / kDmaRB);
-
-    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)((const char *)p.A + bidx * p.as_b * ES), (short)0, (int)a_records, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)((const char *)p.B + bidx * p.bs_b * ES), (short)0, (int)b_records, 0x00020000);
-
-    // DMA: window wave * LA + q of the A half (q < LA), else wave * LB + q - LA
-    // of the B half; a 1 KB window is 8 whole 128-byte rows of one slice
-    // (lane -> row lane / 8, physical chunk lane % 8, holding logical chunk
-    // (lane % 8) ^ (lane / 16) ^ (4 in an odd window)).  The source offset is
-    // a uniform part, through readfirstlane at each use, plus one of four lane
-    // parts.
-    auto window = [&](int q) { return q < Sh::LA ? wave * Sh::LA + q : wave * Sh::LB + q - Sh::LA; };
-    const int lrow = lane >> 3;
-    const int c0 = (lane & 7) ^ (lane >> 4);
-    const uint32_t ch16[2] = {(uint32_t)c0 * 16, (uint32_t)(c0 ^ 4) * 16};
-    const uint32_t a_lp[2] = {(uint32_t)(lrow * p.as_m * ES) + ch16[0],
-                              (uint32_t)(lrow * p.as_m * ES) + ch16[1]};
-    const uint32_t b_lp[2] = {(uint32_t)(lrow * p.bs_n * ES) + ch16[0],
-                              (uint32_t)(lrow * p.bs_n * ES) + ch16[1]};
-    auto buf = [&](int kb) { return smem + (kb & 1) * Sh::STAGE; };
-    auto issue = [&](int kb, int q) {
-        const int w = window(q);
-        const int par = w & 1;
-        int64_t first, rows, ubase;
-        if (q < Sh::LA) {
-            first = m0 + (w % (BM / 8)) * 8;
-            rows = p.M;
-            ubase = ((int64_t)(w / (BM / 8)) * p.as_l + first * p.as_m) * ES;
-        } else {
-            first = n0 + (w % (BN / 8)) * 8;
-            rows = p.N;
-            ubase = ((int64_t)(w / (BN / 8)) * p.bs_l + first * p.bs_n) * ES;
-        }
-        const int rows_left = (int)(rows - first < 8 ? rows - first : 8);   // may be <= 0
-        const int kleft = (int)kbytes - kb * kDmaRB;                       // > 0
-        const uint32_t ub = (uint32_t)__builtin_amdgcn_readfirstlane((int)(ubase + kb * kDmaRB));
-        const bool ok = lrow < rows_left && (int)ch16[par] < kleft;
-        const uint32_t vo = ok ? (q < Sh::LA ? a_lp[par] : b_lp[par]) + ub : kOOB;
-        auto *ldsp = (__attribute__((address_space(3))) void *)(
-            buf(kb) + (q < Sh::LA ? 0 : Sh::A_BYTES) + w * 1024);
-        if (q < Sh::LA) __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, ldsp, 16, vo, 0, 0, 0);
-        else __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, ldsp, 16, vo, 0, 0, 0);
-    };
-
-    // The tile's scales (A's [L][BM], then B's [L][BN]: 2560 bytes) come by
-    // dword DMA into the buffer of stage nkb, which holds no stage the tile
-    // still reads, at the start of the last stage: instruction u (wave u % 4)
-    // fetches entries 64 u .. 64 u + 63.
-    char *const scl = buf(nkb);
-    auto issue_scales = [&]() {
-#pragma unroll
-        for (int q = 0; q < Sh::SCQ; ++q) {
-            const int u = q * Sh::NW + wave;
-            if (u >= Sh::NSC) break;
-            const bool isa = u < L * BM / 64;
-            const int e = (isa ? u : u - L * BM / 64) * 64 + lane;
-            const int s = isa ? e / BM : e / BN;                 // slice
-            const int64_t rc = isa ? m0 + e % BM : n0 + e % BN;  // row of A / column of B
-            const int64_t ext = isa ? ((int64_t)(L - 1) * p.sas_l + (p.M - 1) * p.sas_m + 1)
-                                    : ((int64_t)(L - 1) * p.sbs_l + (p.N - 1) * p.sbs_n + 1);
-            const bool ok = rc < (isa ? p.M : p.N);
-            const uint32_t vo = ok ? (uint32_t)(((int64_t)s * (isa ? p.sas_l : p.sbs_l) +
-                                                 rc * (isa ? p.sas_m : p.sbs_n)) * 4)
-                                   : kOOB;
-            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-                (void *)(isa ? p.sa + bidx * p.sas_b : p.sb + bidx * p.sbs_b), (short)0,
-                (int)(ext * 4 < 0x7FFFFFFF ? ext * 4 : 0x7FFFFFFF), 0x00020000);
-            auto *ldsp = (__attribute__((address_space(3))) void *)(scl + u * 256);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, ldsp, 4, vo, 0, 0, 0);
-        }
-    };
-    const float *sa_lds = (const float *)scl, *sb_lds = (const float *)(scl + L * BM * 4);
-
-    Acc acc[L][L];
-#pragma unroll
-    for (int u = 0; u < L; ++u)
-#pragma unroll
-        for (int j = 0; j < L; ++j) acc[u][j] = MF::zero();
-    // The MFMAs below are inline assembly, which the compiler's hazard
-    // recogniser does not see into: the zeroed accumulators are pinned in
-    // their register files here, before the prologue, and 8 wait states
-    // separate those writes from any MFMA that reads them.
-    static_for<L * L>([&](auto n_) {
-        constexpr int n = decltype(n_)::value;
-        (void)acc;   // an ordinary use, so that the capture does not hinge on the asm operands
-        if constexpr (n < Sh::NAGPR) asm volatile("" : "+a"(acc[n / L][n % L]));
-        else asm volatile("" : "+v"(acc[n / L][n % L]));
-    });
-    asm volatile("s_nop 7" ::: "memory");
-
-    // prologue: stages 0 and 1; stage 0 must land before the first reads
-#pragma unroll
-    for (int q = 0; q < Sh::LPS; ++q) issue(0, q);
-    if (nkb > 1) {
-#pragma unroll
-        for (int q = 0; q < Sh::LPS; ++q) issue(1, q);
-        wait_vmcnt<Sh::LPS>();
-    } else {
-        wait_vmcnt<0>();
-    }
-    exec_barrier();
-
-    struct Frags {
-        i32x4 a[L];
-        i32x4 b[L];
-    };
-    // Fragment rows start at multiples of 32, so a lane's swizzle key is that
-    // of lr for every fragment: the address is a uniform row offset (through
-    // readfirstlane) plus one of four per-lane offsets, one per K step.
-    const int key = (lr >> 1) & 7;
-    int lane_rd[4];
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) lane_rd[kk] = lr * kDmaRB + (((2 * kk + h) ^ key) << 4);
-    const int smem_base = (int)(uintptr_t)(__attribute__((address_space(3))) char *)smem;
-    auto lds_at = [&](int uniform, int kk) {
-        const int u = __builtin_amdgcn_readfirstlane(uniform);
-        return (const __attribute__((address_space(3))) i32x4 *)(uintptr_t)(u + lane_rd[kk]);
-    };
-    auto read_all = [&](int kb, int kk, Frags &f) {
-        const int base = smem_base + (kb & 1) * Sh::STAGE;
-#pragma unroll
-        for (int u = 0; u < L; ++u) f.a[u] = *lds_at(base + (u * BM + wx * 32) * kDmaRB, kk);
-#pragma unroll
-        for (int j = 0; j < L; ++j)
-            f.b[j] = *lds_at(base + Sh::A_BYTES + (j * BN + wy * 32) * kDmaRB, kk);
-    };
-    // One K step: all reads of the next K step (stage rkb, step nkk) into
-    // `nxt`, issued first, then the 25 MFMAs of `cur`, with, if `on`, DMA
-    // instructions [lo, hi) of stage dkb spread between them.
-    auto step = [&](const Frags &cur, Frags &nxt, int rkb, int nkk, int dkb, bool on, int lo,
-                    int hi) {
-        constexpr int NMF = L * L;
-        const int cnt = hi - lo;
-        read_all(rkb, nkk, nxt);
-        static_for<NMF>([&](auto n_) {
-            constexpr int n = decltype(n_)::value;
-            constexpr int u = n / L, j = n % L;
-            HandMfma<ST, (n < Sh::NAGPR)>::run(acc[u][j], cur.a[u], cur.b[j]);
-#pragma unroll
-            for (int d = 0; d < Sh::LPS; ++d) {
-                // instruction lo + d goes after MFMA (d * NMF) / cnt
-                if (d < cnt && (d * NMF) / cnt == n && on) issue(dkb, lo + d);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        });
-    };
-
-    Frags f0, f1;
-    if (nkb > 0) read_all(0, 0, f0);
-    static_assert(kDmaRB / 32 == 4, "four 32-byte K steps per stage");
-    if (nkb == 0) issue_scales();
-    for (int kb = 0; kb < nkb; ++kb) {
-        const bool nb = kb + 1 < nkb, n2 = kb + 2 < nkb;
-        // no DMA is outstanding in the last stage: its waits are unaffected
-        if (!nb) issue_scales();
-        // the rest of stage kb + 1 (stage 1 went out whole in the prologue)
-        step(f0, f1, kb, 1, kb + 1, nb && kb >= 1, Sh::P1, Sh::LPS);
-        step(f1, f0, kb, 2, kb + 1, false, 0, 0);
-        step(f0, f1, kb, 3, kb + 1, false, 0, 0);
-        if (nb) {
-            // stage kb + 1 is the only DMA outstanding; the barrier publishes
-            // every wave's DMA writes, and the lgkmcnt wait makes this wave's
-            // reads of stage kb complete before its buffer is refilled
-            wait_vmcnt<0>();
-            __builtin_amdgcn_s_waitcnt(0xC07F);
-            exec_barrier();
-        }
-        // the last step reads stage kb + 1's step 0 (unused past the end)
-        step(f1, f0, kb + 1, 0, kb + 2, n2, 0, Sh::P1);
-    }
-    // the hand-placed MFMAs' results are read below: 64 wait states first
-    asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory");
-
-    // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
-    wait_vmcnt<0>();
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    exec_barrier();
-    const int ct = wy * 32 + lr;
-    const int64_t col = n0 + ct;
-    const int64_t cbase = bidx * p.cs_b;
-    float sbv[L];
-#pragma unroll
-    for (int j = 0; j < L; ++j) sbv[j] = sb_lds[j * BN + ct];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        // scales of accumulator registers 4 q .. 4 q + 3: one 16-byte read per slice
-        f32x4 s4[L];
-#pragma unroll
-        for (int i = 0; i < L; ++i) s4[i] = *(const f32x4 *)(sa_lds + i * BM + wx * 32 + 8 * q + 4 * h);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int r = 4 * q + e;
-            const int64_t row = m0 + wx * 32 + 8 * q + 4 * h + e;
-            OA out = (OA)0;
-#pragma unroll
-            for (int i = 0; i < L; ++i)
-#pragma unroll
-                for (int j = 0; j < L; ++j) {
-                    // fl32(fl32(fl32(acc) * sa_i) * sb_j), summed i-major, j-minor
-                    const float t1 = MF::to_f32(acc[i][j][r]) * s4[i][e];
-                    out = out + (OA)(t1 * sbv[j]);
-                }
-            if (col < p.N && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-    }
-}
-
-// ---------------------------------------------------------------------------
-// A-direct variant.  The four waves are stacked along M (workgroup tile
-// 128 x 32*NI); each wave streams ITS OWN 32 rows of every A slice from global
-// memory straight into VGPRs (no LDS), and only B, which all four waves share,
-// goes through the LDS ring by DMA.  Per 32-byte K step and CU this moves
-// 4 KB (L=4) of DMA writes and 16 KB of ds_read_b128 through the LDS instead
-// of 16 KB + 32 KB for a 2 x 2 wave grid, at the same L2-miss footprint.
-//
-// K order inside a 64-byte stage: lane (row, h) holds A bytes [32h, 32h+32)
-// as two 16-byte registers t = 0, 1; MFMA step t therefore contracts bytes
-// 32h + 16t of A with the same bytes of B (LDS chunk 2h + t).  Both operands
-// use the same map, so the dot products are unchanged (exactly so for int8).
-// ---------------------------------------------------------------------------
-constexpr int kAdStages = 4;        // B ring depth = A register sets
-
-template <int L, int NI> struct AdShape {
-    static constexpr int BM = 128;
-    static constexpr int BN = 32 * NI;
-    static constexpr int B_ROWS = L * BN;
-    // LDS rows per stage, rounded up to 64 so every wave DMAs whole 1 KB
-    // windows; the padding rows are filled from out-of-range offsets (zeros)
-    // and never read
-    static constexpr int B_ROWS_LDS = (B_ROWS + 63) / 64 * 64;
-    static constexpr int STAGE = B_ROWS_LDS * kDmaRowBytes;   // LDS bytes per stage
-    static constexpr int DPW = STAGE / (4 * 1024);            // B DMA instrs per wave per stage
-    static constexpr int APW = 2 * L;                         // A loads per lane per stage
-    static constexpr int PER_STAGE = DPW + APW;               // vmcnt units per stage
-    static constexpr int LDS_BYTES = kAdStages * STAGE;
-    static_assert(STAGE % 4096 == 0, "B stage must be whole 1 KB windows per wave");
-    static_assert(2 * PER_STAGE * 1 < 64, "vmcnt range");
-};
-
-template <typename ST, int L, int NI, typename AccT>
-__global__ __launch_bounds__(256, 1) void cross_gemm_ad_kernel(GemmParams p, int group_m,
-                                                               uint32_t a_records,
-                                                               uint32_t b_records) {
-    using Sh = AdShape<L, NI>;
-    using MF = Mfma<ST>;
-    using Acc = typename MF::Acc;
-    using OA = AccT;   // outer accumulator: fp64 for fp64 output, else fp32 (store_c)
-    constexpr int BM = Sh::BM, BN = Sh::BN;
-    constexpr int ES = (int)sizeof(ST);
-    constexpr uint32_t kOOB = 0x80000000u;
-    extern __shared__ __attribute__((aligned(16))) char smem[];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int h = lane >> 5, lr = lane & 31;
-
-    const int64_t tiles_m = (p.M + BM - 1) / BM;
-    const int64_t tiles_n = (p.N + BN - 1) / BN;
-    const int64_t tiles = tiles_m * tiles_n;
-    const int64_t g = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
-    const int64_t bidx = g / tiles;
-    const int64_t t = g % tiles;
-    const int64_t width = (int64_t)group_m * tiles_n;
-    const int64_t first_m = (t / width) * group_m;
-    const int64_t gsz = (tiles_m - first_m < group_m) ? (tiles_m - first_m) : group_m;
-    const int64_t tm = first_m + (t % width) % gsz;
-    const int64_t tn = (t % width) / gsz;
-    const int64_t m0 = tm * BM, n0 = tn * BN;
-
-    const uint32_t kbytes = (uint32_t)(p.K * ES);
-    const int nkb = (int)((kbytes + kDmaRowBytes - 1) / kDmaRowBytes);
-
-    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)((const char *)p.A + bidx * p.as_b * ES), (short)0, (int)a_records, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)((const char *)p.B + bidx * p.bs_b * ES), (short)0, (int)b_records, 0x00020000);
-
-    // A: this lane's row of every slice; kOOB past the last row
-    const int64_t arow = m0 + wave * 32 + lr;
-    uint32_t aoff[L];
-#pragma unroll
-    for (int i = 0; i < L; ++i)
-        aoff[i] = (arow < p.M) ? (uint32_t)(((int64_t)i * p.as_l + arow * p.as_m) * ES) + 32 * h
-                               : kOOB;
-    // B: DMA windows of this wave (16 rows of 64 bytes each)
-    uint32_t bsrc[Sh::DPW];
-    int bchunk[Sh::DPW];
-#pragma unroll
-    for (int q = 0; q < Sh::DPW; ++q) {
-        const int pos = (wave * Sh::DPW + q) * 64 + lane;
-        const int r = pos >> 2;
-        bchunk[q] = (pos & 3) ^ ((r >> 2) & 3);
-        const int j = r / BN;
-        const int64_t n = n0 + r % BN;
-        bsrc[q] = (r < Sh::B_ROWS && n < p.N)
-                      ? (uint32_t)(((int64_t)j * p.bs_l + n * p.bs_n) * ES) : kOOB;
-    }
-
-    i32x4 areg[kAdStages][L][2];
-    auto issue_stage = [&](int kb, i32x4 (&ar)[L][2]) {
-        char *dst = smem + (kb % kAdStages) * Sh::STAGE + wave * Sh::DPW * 1024;
-#pragma unroll
-        for (int q = 0; q < Sh::DPW; ++q) {
-            const uint32_t kofs = (uint32_t)kb * kDmaRowBytes + bchunk[q] * 16;
-            const uint32_t vo = (bsrc[q] == kOOB || kofs >= kbytes) ? kOOB : bsrc[q] + kofs;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rB, (__attribute__((address_space(3))) void *)(dst + q * 1024), 16, vo, 0, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < L; ++i)
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const uint32_t kofs = (uint32_t)kb * kDmaRowBytes + 32 * h + 16 * u;
-                const uint32_t vo =
-                    (aoff[i] == kOOB || kofs >= kbytes) ? kOOB : aoff[i] + kofs - 32 * h;
-                ar[i][u] = __builtin_bit_cast(
-                    i32x4, __builtin_amdgcn_raw_buffer_load_b128(rA, vo, 0, 0));
-            }
-    };
-
-    Acc acc[L][L][NI];
-#pragma unroll
-    for (int i = 0; i < L; ++i)
-#pragma unroll
-        for (int j = 0; j < L; ++j)
-#pragma unroll
-            for (int c = 0; c < NI; ++c) acc[i][j][c] = MF::zero();
-
-    // B fragments of one step: rows j*BN + c*32 + lr, chunk 2h + tt
-    struct BFr {
-        i32x4 b[L][NI];
-    };
-    auto read_b = [&](const char *buf, int tt, int r, BFr &f) {
-        const int j = r / NI, c = r % NI;
-        f.b[j][c] = *(const i32x4 *)(buf + dswz(j * BN + c * 32 + lr, 2 * h + tt));
-    };
-    constexpr int kReads = L * NI;
-    constexpr int kMfmas = L * L * NI;
-    auto step = [&](const i32x4 (&ar)[L][2], int tt, const BFr &cur, BFr &nxt,
-                    const char *nbuf, int ntt) {
-#pragma unroll
-        for (int q = 0; q < kMfmas; ++q) {
-            const int i = q / (L * NI), j = (q / NI) % L, c = q % NI;
-            acc[i][j][c] = MF::run(ar[i][tt], cur.b[j][c], acc[i][j][c]);
-            if (q < kReads) read_b(nbuf, ntt, q, nxt);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-#pragma unroll
-        for (int q = kMfmas; q < kReads; ++q) read_b(nbuf, ntt, q, nxt);
-    };
-    // The K loop runs a multiple of DEPTH stages: stages past the end load
-    // only out-of-range offsets (zeros), so their MFMAs add nothing, and the
-    // loop body stays free of branches (which keeps the compiler's own wait
-    // counts for the A registers exact).
-    constexpr int D = kAdStages;
-    const int nkb_pad = (nkb + D - 1) / D * D;
-    BFr f0, f1;
-    // One stage: step 0 (its B fragments f0 already in registers) with the
-    // step-1 reads interleaved; wait for this wave's loads of stage kb + 1
-    // (the D - 2 later stages may stay in flight), drain its LDS reads and
-    // synchronise, which publishes every wave's DMA writes of stage kb + 1
-    // and frees the slot of stage kb; step 1 with the reads of stage kb + 1's
-    // step-0 fragments; then refill this stage's LDS slot and A register set
-    // (whose last MFMA was just issued) with stage kb + D.
-    auto stage = [&](int kb, i32x4 (&ar)[L][2]) {
-        step(ar, 0, f0, f1, smem + (kb % D) * Sh::STAGE, 1);
-        wait_vmcnt<(D - 2) * Sh::PER_STAGE>();
-        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0) only
-        exec_barrier();
-        step(ar, 1, f1, f0, smem + ((kb + 1) % D) * Sh::STAGE, 0);
-        issue_stage(kb + D, ar);
-    };
-
-    if (nkb > 0) {
-#pragma unroll
-        for (int s = 0; s < D; ++s) issue_stage(s, areg[s]);
-        wait_vmcnt<(D - 1) * Sh::PER_STAGE>();
-        exec_barrier();
-#pragma unroll
-        for (int q = 0; q < kReads; ++q) read_b(smem, 0, q, f0);
-    }
-    for (int kb = 0; kb < nkb_pad; kb += D) {
-#pragma unroll
-        for (int s = 0; s < D; ++s) stage(kb + s, areg[s]);
-    }
-    // the last D stages issued only zero loads; let them land before the LDS
-    // is handed to another workgroup
-    wait_vmcnt<0>();
-
-    // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
-    const float *sab = p.sa + bidx * p.sas_b;
-    const float *sbb = p.sb + bidx * p.sbs_b;
-    const int64_t cbase = bidx * p.cs_b;
-#pragma unroll
-    for (int c = 0; c < NI; ++c) {
-        const int64_t col = n0 + c * 32 + lr;
-        const bool cok = col < p.N;
-        float sbv[L];
-#pragma unroll
-        for (int j = 0; j < L; ++j) sbv[j] = cok ? sbb[j * p.sbs_l + col * p.sbs_n] : 0.0f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int64_t row = m0 + wave * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-            if (cok && row < p.M) {
-                OA out = (OA)0;
-#pragma unroll
-                for (int i = 0; i < L; ++i) {
-                    const float sai = sab[i * p.sas_l + row * p.sas_m];
-#pragma unroll
-                    for (int j = 0; j < L; ++j) {
-                        const float x = MF::to_f32(acc[i][j][c][r]);
-                        const float t1 = x * sai;
-                        const float t2 = t1 * sbv[j];
-                        out = out + (OA)t2;
-                    }
-                }
-                store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
-            }
-        }
-    }
-}
 
 // ---------------------------------------------------------------------------
 // Pack kernel: any-stride slices -> K-contiguous, 16-byte padded rows.
@@ -2821,8 +61,6 @@ hipError_t launch_pack(const PackParams &p, hipStream_t st) {
     hipLaunchKernelGGL(pack_kernel, dim3((unsigned)blocks), dim3(256), 0, st, p);
     return hipGetLastError();
 }
-
-static int64_t dma_extent(int64_t s_l, int64_t s_r, int L, int64_t rows, int64_t K, int es);
 
 // ---------------------------------------------------------------------------
 // Tile table (replaces the reference's Optuna search, ozaki_triton.py:263-304):
@@ -3033,277 +271,13 @@ hipError_t setup_splitk(GemmParams &p, const GemmPlan &plan, int L, void *ws, hi
     return hipGetLastError();
 }
 
-// byte extent [0, bytes) one batch of a slice operand spans, or -1 if it does
-// not fit the 31-bit buffer offsets of the DMA kernel.  The last row counts
-// up to its 16-byte boundary: the kernels load 16-byte pieces, and a piece
-// that crosses the buffer's end comes back zeroed as a whole, which would
-// drop the row's last elements.  Those bytes exist and are zero: operands
-// whose rows are not whole 16-byte pieces are the pack kernel's zero-padded
-// copies (K * es is a multiple of 16 for every other operand).
-static int64_t dma_extent(int64_t s_l, int64_t s_r, int L, int64_t rows, int64_t K, int es) {
-    if (s_l < 0 || s_r < 0) return -1;
-    const int64_t row_bytes = (K * es + 15) / 16 * 16;
-    const int64_t e = ((int64_t)(L - 1) * s_l + (rows - 1) * s_r) * es + row_bytes;
-    return (e < ((int64_t)1 << 31) - 64) ? e : -1;
-}
-
-// Raise a kernel's dynamic LDS limit (above the 64 KB default) once per
-// device.  `done` is that kernel's bitmask of devices already set (bit d:
-// device d); concurrent first calls may both set it, which is harmless.
-static hipError_t set_lds_limit(const void *kern, int bytes, std::atomic<uint64_t> &done) {
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return e;
-    const uint64_t bit = (dev >= 0 && dev < 64) ? (1ull << dev) : 0;
-    if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
-    e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-    if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_acq_rel);
-    return e;
-}
-
-template <typename ST, int L, int MI, int NI, typename AccT>
-static hipError_t launch_dma(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
-    using Sh = DmaShape<L, MI, NI>;
-    auto kern = cross_gemm_dma_kernel<ST, L, MI, NI, AccT>;
-    static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
-    if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
-    const int es = (int)sizeof(ST);
-    const int64_t ea = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es);
-    const int64_t eb = dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es);
-    const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
-    if (tiles == 0) return hipSuccess;
-    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(256), Sh::LDS_BYTES, st, p,
-                       plan.group_m, (uint32_t)ea, (uint32_t)eb);
-    return hipGetLastError();
-}
-
-template <typename ST, int L, typename AccT>
-static hipError_t launch_kstep(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
-    using Sh = KStepShape<L>;
-    auto kern = cross_gemm_kstep_kernel<ST, L, AccT>;
-    static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
-    if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
-    const int es = (int)sizeof(ST);
-    const int64_t ea = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es);
-    const int64_t eb = dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es);
-    const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
-    if (tiles == 0) return hipSuccess;
-    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(256), Sh::LDS_BYTES, st, p,
-                       plan.group_m, (uint32_t)ea, (uint32_t)eb);
-    return hipGetLastError();
-}
-
-template <typename ST, int L, int NI, typename AccT>
-static hipError_t launch_ad(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
-    using Sh = AdShape<L, NI>;
-    auto kern = cross_gemm_ad_kernel<ST, L, NI, AccT>;
-    static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
-    if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
-    const int es = (int)sizeof(ST);
-    const int64_t ea = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es);
-    const int64_t eb = dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es);
-    const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
-    if (tiles == 0) return hipSuccess;
-    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(256), Sh::LDS_BYTES, st, p,
-                       plan.group_m, (uint32_t)ea, (uint32_t)eb);
-    return hipGetLastError();
-}
-
-template <typename ST, int L, typename AccT, int R>
-static hipError_t launch_pair(const GemmParams &p, const GemmPlan &plan, hipStream_t st, int i0,
-                              int cont) {
-    using Sh = PairShape<L, R>;
-    auto kern = cross_gemm_pair_kernel<ST, L, AccT, R>;
-    static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
-    if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
-    const int es = (int)sizeof(ST);
-    const int64_t ea = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es);
-    const int64_t eb = dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es);
-    const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
-    if (tiles == 0) return hipSuccess;
-    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(512), Sh::LDS_BYTES, st, p,
-                       plan.group_m, (uint32_t)ea, (uint32_t)eb, i0, cont);
-    return hipGetLastError();
-}
-
-template <typename ST, int L, typename AccT>
-static hipError_t launch_ring(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
-    constexpr int W = (L <= 2) ? 2 : 1;
-    using Sh = RingShape<L, W>;
-    auto kern = cross_gemm_ring_kernel<ST, L, AccT, W>;
-    static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
-    if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
-    const int es = (int)sizeof(ST);
-    const int64_t ea = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es);
-    const int64_t eb = dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es);
-    const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
-    if (tiles == 0) return hipSuccess;
-    const int64_t ranges = p.ksplit > 1 ? p.ksplit : 1;
-    hipLaunchKernelGGL(kern, dim3((unsigned)(tiles * ranges)), dim3(512), Sh::LDS_BYTES, st, p,
-                       plan.group_m, (uint32_t)ea, (uint32_t)eb);
-    return hipGetLastError();
-}
-
-template <typename ST, typename AccT>
-static hipError_t launch_wide(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
-    using Sh = WideShape;
-    auto kern = cross_gemm_wide_kernel<ST, AccT>;
-    static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
-    if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
-    const int es = (int)sizeof(ST);
-    const int64_t ea = dma_extent(p.as_l, p.as_m, Sh::L, p.M, p.K, es);
-    const int64_t eb = dma_extent(p.bs_l, p.bs_n, Sh::L, p.N, p.K, es);
-    const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
-    if (tiles == 0) return hipSuccess;
-    const int64_t ranges = p.ksplit > 1 ? p.ksplit : 1;
-    hipLaunchKernelGGL(kern, dim3((unsigned)(tiles * ranges)), dim3(512), Sh::LDS_BYTES, st, p,
-                       plan.group_m, (uint32_t)ea, (uint32_t)eb);
-    return hipGetLastError();
-}
-
-template <typename ST, typename AccT>
-static hipError_t launch_wide4(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
-    using Sh = Wide4Shape;
-    auto kern = cross_gemm_wide4_kernel<ST, AccT>;
-    static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
-    if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
-    const int es = (int)sizeof(ST);
-    const int64_t ea = dma_extent(p.as_l, p.as_m, Sh::L, p.M, p.K, es);
-    const int64_t eb = dma_extent(p.bs_l, p.bs_n, Sh::L, p.N, p.K, es);
-    const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
-    if (tiles == 0) return hipSuccess;
-    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(512), Sh::LDS_BYTES, st, p,
-                       plan.group_m, (uint32_t)ea, (uint32_t)eb);
-    return hipGetLastError();
-}
-
-template <typename ST, typename AccT>
-static hipError_t launch_solo5(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
-    if constexpr (std::is_same<ST, float>::value) {
-        return hipErrorInvalidValue;   // no fp32-slice form
-    } else {
-        using Sh = Solo5Shape;
-        auto kern = cross_gemm_solo5_kernel<ST, AccT>;
-        static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
-        if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
-        const int es = (int)sizeof(ST);
-        const int64_t ea = dma_extent(p.as_l, p.as_m, Sh::L, p.M, p.K, es);
-        const int64_t eb = dma_extent(p.bs_l, p.bs_n, Sh::L, p.N, p.K, es);
-        const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
-        if (tiles == 0) return hipSuccess;
-        hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(256), Sh::LDS_BYTES, st, p,
-                           plan.group_m, (uint32_t)ea, (uint32_t)eb);
-        return hipGetLastError();
-    }
-}
-
-// num_splits = 5..8: launches over consecutive i-rows (at most 16 pairs each,
-// so a wave group still holds 8 pairs), in i-major order, each continuing the
-// fp64 sum from C.  int8 / fp16 / bf16 slices with an fp64 outer accumulator.
-template <typename ST, int L, typename AccT>
-static hipError_t launch_chunks(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
-    if constexpr (!std::is_same<AccT, double>::value || std::is_same<ST, float>::value) {
-        return hipErrorInvalidValue;
-    } else {
-        constexpr int R = (L == 5) ? 3 : 2;   // rows per launch (16 / L, at least 2)
-        hipError_t e = hipSuccess;
-        for (int i0 = 0; i0 < L && e == hipSuccess; i0 += R) {
-            const int cont = i0 > 0;
-            if (L - i0 >= R) e = launch_pair<ST, L, AccT, R>(p, plan, st, i0, cont);
-            else if constexpr (L % R != 0) e = launch_pair<ST, L, AccT, L % R>(p, plan, st, i0, cont);
-        }
-        return e;
-    }
-}
-
-template <typename ST, int L, int MI, int NI, typename AccT>
-static hipError_t launch_one(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
-    if constexpr (L >= 3) {
-        if (plan.kind == kGemmPair) return launch_pair<ST, L, AccT, L>(p, plan, st, 0, 0);
-    }
-    if constexpr (L == 3) {
-        if (plan.kind == kGemmWide) return launch_wide<ST, AccT>(p, plan, st);
-    }
-    if constexpr (L == 4) {
-        if (plan.kind == kGemmWide4) return launch_wide4<ST, AccT>(p, plan, st);
-    }
-    if constexpr (L >= 2 && L <= 4) {
-        if (plan.kind == kGemmRing) return launch_ring<ST, L, AccT>(p, plan, st);
-    }
-    if (plan.kind == kGemmAD) {
-        constexpr int ANI = (L == 1) ? 8 : (L == 2) ? 4 : 1;
-        return launch_ad<ST, L, ANI, AccT>(p, plan, st);
-    }
-    if (plan.kind == kGemmDMA) return launch_dma<ST, L, MI, NI, AccT>(p, plan, st);
-    using Sh = GemmShape<L, MI, NI>;
-    auto kern = cross_gemm_kernel<ST, L, MI, NI, AccT>;
-    static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
-    if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
-    const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
-    if (tiles == 0) return hipSuccess;
-    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(256), Sh::LDS_BYTES, st, p,
-                       plan.group_m);
-    return hipGetLastError();
-}
-
-template <typename ST, int L, typename AccT>
-static hipError_t launch_L(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
-    // (fp32 slices at L = 4: no hand-placed MFMA, so no K-step kernel)
-    if constexpr (L <= 4 && !(L == 4 && std::is_same_v<ST, float>)) {
-        if (plan.kind == kGemmKStep) return launch_kstep<ST, L, AccT>(p, plan, st);
-    }
-    const int key = plan.mi * 10 + plan.ni;
-    if constexpr (L == 1) {
-        switch (key) {
-        case 24: return launch_one<ST, 1, 2, 4, AccT>(p, plan, st);
-        case 22: return launch_one<ST, 1, 2, 2, AccT>(p, plan, st);
-        case 12: return launch_one<ST, 1, 1, 2, AccT>(p, plan, st);
-        case 11: return launch_one<ST, 1, 1, 1, AccT>(p, plan, st);
-        }
-    } else if constexpr (L == 2) {
-        switch (key) {
-        case 22: return launch_one<ST, 2, 2, 2, AccT>(p, plan, st);
-        case 12: return launch_one<ST, 2, 1, 2, AccT>(p, plan, st);
-        case 11: return launch_one<ST, 2, 1, 1, AccT>(p, plan, st);
-        }
-    } else if constexpr (L <= 4) {
-        if (key == 11) return launch_one<ST, L, 1, 1, AccT>(p, plan, st);
-    } else {
-        if constexpr (L == 5) {
-            if (plan.kind == kGemmSolo5) return launch_solo5<ST, AccT>(p, plan, st);
-        }
-        return launch_chunks<ST, L, AccT>(p, plan, st);
-    }
-    return hipErrorInvalidValue;
-}
-
-template <typename ST, typename AccT>
-static hipError_t launch_st(const GemmParams &p, const GemmPlan &plan, int L, hipStream_t st) {
-    switch (L) {
-    case 1: return launch_L<ST, 1, AccT>(p, plan, st);
-    case 2: return launch_L<ST, 2, AccT>(p, plan, st);
-    case 3: return launch_L<ST, 3, AccT>(p, plan, st);
-    case 4: return launch_L<ST, 4, AccT>(p, plan, st);
-    case 5: return launch_L<ST, 5, AccT>(p, plan, st);
-    case 6: return launch_L<ST, 6, AccT>(p, plan, st);
-    case 7: return launch_L<ST, 7, AccT>(p, plan, st);
-    case 8: return launch_L<ST, 8, AccT>(p, plan, st);
-    }
-    return hipErrorInvalidValue;
-}
-
 hipError_t launch_gemm(const GemmParams &p, const GemmPlan &plan, int L, int slice_dtype,
                        hipStream_t st) {
-    const bool acc64 = p.out_dtype == 0;
     switch (slice_dtype) {
-    case 4: return acc64 ? launch_st<int8_t, double>(p, plan, L, st)
-                         : launch_st<int8_t, float>(p, plan, L, st);
-    case 2: return acc64 ? launch_st<_Float16, double>(p, plan, L, st)
-                         : launch_st<_Float16, float>(p, plan, L, st);
-    case 3: return acc64 ? launch_st<__bf16, double>(p, plan, L, st)
-                         : launch_st<__bf16, float>(p, plan, L, st);
-    case 1: return acc64 ? launch_st<float, double>(p, plan, L, st)
-                         : launch_st<float, float>(p, plan, L, st);
+    case 4: return launch_gemm_i8(p, plan, L, st);
+    case 2: return launch_gemm_f16(p, plan, L, st);
+    case 3: return launch_gemm_bf16(p, plan, L, st);
+    case 1: return launch_gemm_f32(p, plan, L, st);
     }
     return hipErrorInvalidValue;
 }

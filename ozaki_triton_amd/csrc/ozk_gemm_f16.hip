@@ -1,0 +1,12 @@
+// ozk_gemm_f16.hip -- cross-GEMM kernels with _Float16 slices (one translation
+// unit per slice dtype, compiled in parallel).
+#include "ozk_gemm_kernels.h"
+
+namespace ozk {
+
+hipError_t launch_gemm_f16(const GemmParams &p, const GemmPlan &plan, int L, hipStream_t st) {
+    return p.out_dtype == 0 ? launch_st<_Float16, double>(p, plan, L, st)
+                            : launch_st<_Float16, float>(p, plan, L, st);
+}
+
+}  // namespace ozk

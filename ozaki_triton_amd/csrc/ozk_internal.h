@@ -154,6 +154,11 @@ size_t splitk_bytes(const GemmParams &p, const GemmPlan &plan, int L);
 hipError_t setup_splitk(GemmParams &p, const GemmPlan &plan, int L, void *ws, hipStream_t stream);
 hipError_t launch_gemm(const GemmParams &p, const GemmPlan &plan, int L, int slice_dtype,
                        hipStream_t stream);
+// the same for one slice dtype (one translation unit each)
+hipError_t launch_gemm_i8(const GemmParams &p, const GemmPlan &plan, int L, hipStream_t stream);
+hipError_t launch_gemm_f16(const GemmParams &p, const GemmPlan &plan, int L, hipStream_t stream);
+hipError_t launch_gemm_bf16(const GemmParams &p, const GemmPlan &plan, int L, hipStream_t stream);
+hipError_t launch_gemm_f32(const GemmParams &p, const GemmPlan &plan, int L, hipStream_t stream);
 
 hipError_t launch_zero_c(const GemmParams &p, hipStream_t stream);
 
