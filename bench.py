@@ -178,7 +178,7 @@ def reference_shapes(reps: int = 30):
                 "one MI355X"}}), flush=True)
 
 
-def cpu_oracle_baseline(A_cpu, B_cpu, slice_dtype, L, block):
+def cpu_oracle_baseline(A_cpu, B_cpu, slice_dtype, L, block, pairs="all"):
     """Time the C oracle on a block x block corner of the output with the full
     K: split `block` rows of A and `block` columns of B, then the L^2 slice
     GEMMs and the ordered epilogue.  Single-threaded."""
@@ -193,7 +193,7 @@ def cpu_oracle_baseline(A_cpu, B_cpu, slice_dtype, L, block):
     t0 = time.perf_counter()
     a_sl, a_sc = oracle.split(a, L, alpha, sd)
     b_sl, b_sc = oracle.split(np.ascontiguousarray(b).T, L, alpha, sd)
-    oracle.cross_gemm(a_sl, b_sl, a_sc, b_sc, str(a.dtype))
+    oracle.cross_gemm(a_sl, b_sl, a_sc, b_sc, str(a.dtype), pairs=pairs)
     dt = time.perf_counter() - t0
     return 2.0 * block * block * K / dt / 1e12, dt
 
@@ -215,16 +215,17 @@ def cpu_torch_matmul(A_cpu, B_cpu, reps):
     return flops / t / 1e12, ncores, torch.get_num_threads()
 
 
-def planned_gemm_kernel(batch, M, N, K, L, sdt):
+def planned_gemm_kernel(batch, M, N, K, L, sdt, pairs="all"):
     """Name of the cross-GEMM kernel the library's planner picks for this call
-    (ozk_debug_gemm_kernel), e.g. "wide4"."""
+    (ozk_debug_gemm_kernel_pairs), e.g. "wide4"."""
     import ctypes
     from ozaki_triton_amd import _lib
     name = ctypes.c_char_p()
     code = {"int8": _lib.OZK_I8, "float16": _lib.OZK_F16}[sdt]
-    _lib.check("ozk_debug_gemm_kernel",
-               _lib.load().ozk_debug_gemm_kernel(batch, M, N, K, L, code, 0, ctypes.byref(name),
-                                                 None))
+    pc = {"all": _lib.OZK_PAIRS_ALL, "triangular": _lib.OZK_PAIRS_TRIANGULAR}[pairs]
+    _lib.check("ozk_debug_gemm_kernel_pairs",
+               _lib.load().ozk_debug_gemm_kernel_pairs(batch, M, N, K, L, code, pc, 0,
+                                                       ctypes.byref(name), None))
     return name.value.decode()
 
 
@@ -394,6 +395,9 @@ def main():
     ap.add_argument("--num-splits", type=int, default=0,
                     help="override the configuration's num_splits (e.g. 5 at C3: the slice count "
                          "whose rel-err meets 1e-9); the line is then not the headline metric")
+    ap.add_argument("--pairs", default="all", choices=["all", "triangular"],
+                    help="slice pairs the cross-GEMM sums: all (the reference's sum, the "
+                         "metric) or triangular (i + j <= num_splits - 1; not in the reference)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (3 times): the "
                          "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -461,12 +465,13 @@ def main():
         events.append(evs)
 
     for _ in range(args.warmup):
-        _ozaki_matmul_impl(A, B, L, slice_dtype, False, None, max_splits=8)
+        _ozaki_matmul_impl(A, B, L, slice_dtype, False, None, max_splits=8, pairs=args.pairs)
     torch.cuda.synchronize()
 
     t0 = time.perf_counter()
     for s in range(args.steps):
-        C = _ozaki_matmul_impl(A, B, L, slice_dtype, False, events[s], max_splits=8)
+        C = _ozaki_matmul_impl(A, B, L, slice_dtype, False, events[s], max_splits=8,
+                               pairs=args.pairs)
     torch.cuda.synchronize()
     t = time.perf_counter() - t0
     ms = t / args.steps * 1e3
@@ -484,7 +489,7 @@ def main():
         flush.zero_()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        _ozaki_matmul_impl(A, B, L, slice_dtype, False, None, max_splits=8)
+        _ozaki_matmul_impl(A, B, L, slice_dtype, False, None, max_splits=8, pairs=args.pairs)
         e1.record()
         e1.synchronize()
         fts.append(e0.elapsed_time(e1))
@@ -519,8 +524,10 @@ def main():
     rel = float((C.double() - C64).norm() / C64.norm())
     del C64
 
-    # dominant kernel: cross-GEMM, L^2 slice GEMMs of 2*M*N*K ops each
-    cross_ops = L * L * 2.0 * M * N * K * batch
+    # dominant kernel: cross-GEMM, one slice GEMM of 2*M*N*K ops per pair
+    # (L^2 pairs, or L (L + 1) / 2 in the triangular set)
+    n_pairs = L * L if args.pairs == "all" else L * (L + 1) // 2
+    cross_ops = n_pairs * 2.0 * M * N * K * batch
     if sdt == "int8":
         peak, unit_c = PEAK_INT8_TOPS, "TOP/s"
     else:
@@ -528,7 +535,7 @@ def main():
     achieved = cross_ops / (t_cross * 1e-3) / 1e12
     # the kernels the library chose, asked from its planner (the test hooks of
     # include/ozaki_amd_debug.h), so the profiled name is the one that ran
-    gemm_kernel = f"cross_gemm_{planned_gemm_kernel(batch, M, N, K, L, sdt)}_kernel"
+    gemm_kernel = f"cross_gemm_{planned_gemm_kernel(batch, M, N, K, L, sdt, args.pairs)}_kernel"
     # split: read the unique inputs, write the unique slices and scales
     xsz = 8 if xdt == "float64" else 4
     ssz = 1 if sdt == "int8" else 2
@@ -541,9 +548,10 @@ def main():
     split_gbs = split_bytes / (split_ms * 1e-3) / 1e9
 
     rec = {
-        "metric": (METRIC if args.config == "C3" and L == default_L else
+        "metric": (METRIC if args.config == "C3" and L == default_L and args.pairs == "all" else
                    f"emulated TFLOP/s (2MNK/t) {args.config}" +
-                   ("" if L == default_L else f" with num_splits={L}")),
+                   ("" if L == default_L else f" with num_splits={L}") +
+                   ("" if args.pairs == "all" else ", triangular pairs")),
         "value": round(value, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -565,8 +573,9 @@ def main():
                 "C5": "FP32->INT8 num_splits=3, M=N=1024, K=65536, 1% outliers x1e4",
                 "C3s": "FP64->INT8 num_splits=4, A[4096,8192] x B[8192,4096]: one GPU's share "
                        "of C3 on a 2x2 grid",
-            }[args.config] + ("" if L == default_L else f"; num_splits overridden to {L}"),
-            "input_dtype": xdt, "slice_dtype": sdt, "num_splits": L,
+            }[args.config] + ("" if L == default_L else f"; num_splits overridden to {L}") +
+            ("" if args.pairs == "all" else "; triangular pair set (i + j <= num_splits - 1)"),
+            "input_dtype": xdt, "slice_dtype": sdt, "num_splits": L, "pairs": args.pairs,
             "M": M, "N": N, "K": K, "batch": batch, "seed": cfg[5],
         },
         "rel_err": rel,
@@ -583,7 +592,8 @@ def main():
             "peak": peak,
             "unit": unit_c,
             "frac": round(achieved / peak, 4),
-            "traffic": measured_traffic(args.config, gemm_kernel) if L == default_L else None,
+            "traffic": (measured_traffic(args.config, gemm_kernel)
+                        if L == default_L and args.pairs == "all" else None),
             "avg_ms": round(t_cross, 4),
         },
         "split": {
@@ -606,7 +616,7 @@ def main():
     }
     if not args.no_cpu:
         block = min(args.cpu_block, M, N)
-        v, dt = cpu_oracle_baseline(A_cpu, B_cpu, sdt, L, block)
+        v, dt = cpu_oracle_baseline(A_cpu, B_cpu, sdt, L, block, args.pairs)
         rec["cpu_baseline"] = {
             "value": round(v, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
             "sample": f"oracle (C, scalar) on a {block}x{block} output block with the full "

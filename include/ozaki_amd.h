@@ -50,7 +50,9 @@ enum {
     OZK_ERR_NULL = -1,        /* a required pointer is NULL */
     OZK_ERR_DTYPE = -2,       /* dtype combination not supported */
     OZK_ERR_SPLITS = -3,      /* num_splits outside [0, OZK_MAX_SPLITS], or > 4 with a
-                                 cross-GEMM that cannot take it */
+                                 cross-GEMM that cannot take it; or (the *_pairs
+                                 calls) an unknown pair set, or the triangular set
+                                 with more than 5 slices */
     OZK_ERR_SHAPE = -4,       /* negative size, or K mismatch */
     OZK_ERR_ALPHA = -5,       /* alpha < 1 (K too large for the accumulator) */
     OZK_ERR_WORKSPACE = -6,   /* workspace missing, too small or not 16-byte aligned */
@@ -162,6 +164,32 @@ int ozk_cross_gemm(const void *A_slices, const int64_t a_strides[4], const void 
                    void *stream);
 
 /*
+ * Pair sets -- no counterpart in the reference, whose cross-GEMM always sums
+ * all L x L slice pairs (ozaki_triton.py:403-447).
+ *   OZK_PAIRS_ALL         every pair (i, j): the reference's sum, bit for bit.
+ *   OZK_PAIRS_TRIANGULAR  only the pairs with i + j <= L - 1, L (L + 1) / 2 of
+ *                         them, summed in the same i-major / j-minor order from
+ *                         the same t_ij.  Pair (i, j) carries about
+ *                         2^(-alpha (i + j)) of C's magnitude, so the terms left
+ *                         out are of the size of the split's own truncation
+ *                         error: 5 int8 slices on 15 pairs reach the accuracy of
+ *                         25 pairs (fp64 inputs, K = 8192: rel-err 4.31e-10
+ *                         against 4.26e-10), with fewer products than 4 slices
+ *                         on all 16 pairs (2.8e-9).  Takes 1 to 5 slices.
+ * The *_pairs calls take the set as an extra argument and are otherwise the
+ * calls above (the same workspace queries cover both sets).
+ */
+enum { OZK_PAIRS_ALL = 0, OZK_PAIRS_TRIANGULAR = 1 };
+
+int ozk_cross_gemm_pairs(const void *A_slices, const int64_t a_strides[4], const void *B_slices,
+                         const int64_t b_strides[4], const float *A_scales,
+                         const int64_t sa_strides[3], const float *B_scales,
+                         const int64_t sb_strides[3], int64_t batch, int64_t M, int64_t N,
+                         int64_t K, int num_splits, int slice_dtype, int pairs, void *C,
+                         int out_dtype, const int64_t c_strides[3], void *workspace,
+                         size_t workspace_bytes, void *stream);
+
+/*
  * Matmul -- replaces ozaki_matmul below its Python checks (ozaki_triton.py:
  * 565-606): alpha (compute_split_bits), the split of B through its transposed
  * view and of A, and the fused cross-GEMM, enqueued on `stream` by one call.
@@ -186,6 +214,14 @@ int ozk_matmul(const void *A, const int64_t a_strides[3], const void *B,
                const int64_t b_strides[3], int dtype, int64_t batch, int64_t M, int64_t N,
                int64_t K, int num_splits, int slice_dtype, void *C, const int64_t c_strides[3],
                void *workspace, size_t workspace_bytes, void *const events[4], void *stream);
+
+/* ozk_matmul with a pair set (OZK_PAIRS_*, above); ozk_matmul_workspace_bytes
+ * sizes its workspace. */
+int ozk_matmul_pairs(const void *A, const int64_t a_strides[3], const void *B,
+                     const int64_t b_strides[3], int dtype, int64_t batch, int64_t M, int64_t N,
+                     int64_t K, int num_splits, int slice_dtype, int pairs, void *C,
+                     const int64_t c_strides[3], void *workspace, size_t workspace_bytes,
+                     void *const events[4], void *stream);
 
 /*
  * Matmul without a workspace -- no counterpart in the reference.  For callers

@@ -66,6 +66,11 @@ int ozk_debug_force_gemm_ksplit(int ranges);
 int ozk_debug_gemm_kernel(int64_t batch, int64_t M, int64_t N, int64_t K, int num_splits,
                           int slice_dtype, int cus, const char **name_out, int *ksplit_out);
 
+/* The same for a pair set (OZK_PAIRS_ALL or OZK_PAIRS_TRIANGULAR). */
+int ozk_debug_gemm_kernel_pairs(int64_t batch, int64_t M, int64_t N, int64_t K, int num_splits,
+                                int slice_dtype, int pairs, int cus, const char **name_out,
+                                int *ksplit_out);
+
 /*
  * The split path the planner would choose for an operand described as in
  * ozk_split (X and slices are only inspected for their alignment, never

@@ -68,8 +68,9 @@ def lib() -> ctypes.CDLL:
         L.ozo_split.restype = i32
         L.ozo_cross_gemm.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, i32, vp, i32]
         L.ozo_cross_gemm.restype = i32
-        L.ozo_cross_gemm_skip.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, i32, vp, i32, i32]
-        L.ozo_cross_gemm_skip.restype = i32
+        L.ozo_cross_gemm_pairs.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, i32, vp, i32,
+                                           i32, i32]
+        L.ozo_cross_gemm_pairs.restype = i32
         L.ozo_int8_pair_dots.argtypes = [vp, vp, i64, i64, i64, i32, vp]
         L.ozo_int8_pair_dots.restype = i32
         L.ozo_f64_to_f16_array.argtypes = [vp, vp, i64]
@@ -170,10 +171,15 @@ def split(X: np.ndarray, num_splits: int, alpha: int, slice_dtype):
     return slices, scales
 
 
+PAIRS = {"all": 0, "triangular": 1}
+
+
 def cross_gemm(As: np.ndarray, Bs_T: np.ndarray, sa: np.ndarray, sb: np.ndarray,
-               out_dtype, skip_pair: int = -1) -> np.ndarray:
+               out_dtype, skip_pair: int = -1, pairs: str = "all") -> np.ndarray:
     """As [L, M, K], Bs_T [L, N, K] (B slices stored K-contiguous), sa [L, M],
-    sb [L, N] -> C [M, N] (ozaki_triton.py:357-452).  skip_pair = i * L + j
+    sb [L, N] -> C [M, N] (ozaki_triton.py:357-452).  pairs = "triangular"
+    sums only the pairs i + j <= L - 1 (not in the reference: the library's
+    OZK_PAIRS_TRIANGULAR), in the same order.  skip_pair = i * L + j
     leaves that pair's term out: a planted mistake for tests that must show
     their checks catch a dropped pair (never used as a reference)."""
     As = np.ascontiguousarray(As)
@@ -185,8 +191,8 @@ def cross_gemm(As: np.ndarray, Bs_T: np.ndarray, sa: np.ndarray, sb: np.ndarray,
     assert L == L2 and K == K2
     od = code_of(out_dtype)
     C = np.empty((M, N), dtype=_NP_OF[od])
-    rc = lib().ozo_cross_gemm_skip(_ptr(As), _ptr(Bs_T), _ptr(sa), _ptr(sb), M, N, K, L,
-                                   code_of(As.dtype), _ptr(C), od, int(skip_pair))
+    rc = lib().ozo_cross_gemm_pairs(_ptr(As), _ptr(Bs_T), _ptr(sa), _ptr(sb), M, N, K, L,
+                                    code_of(As.dtype), _ptr(C), od, PAIRS[pairs], int(skip_pair))
     if rc != 0:
         raise RuntimeError(f"ozo_cross_gemm failed: {rc}")
     return C
@@ -208,7 +214,7 @@ def _slice_dtype_name(slice_dtype) -> str:
 
 
 def ozaki_matmul(A: np.ndarray, B: np.ndarray, num_splits: int, slice_dtype,
-                 return_parts: bool = False):
+                 return_parts: bool = False, pairs: str = "all"):
     """numpy restatement of ozaki_matmul (ozaki_triton.py:534-606): broadcast the
     batch dims (504-531), split A rows and B columns (through B^T, 593-595),
     cross-GEMM per batch, output in the input dtype (bfloat16 as uint16 bits)."""
@@ -230,7 +236,7 @@ def ozaki_matmul(A: np.ndarray, B: np.ndarray, num_splits: int, slice_dtype,
     for b in range(BN):
         a_sl, a_sc = split(A3[b], num_splits, alpha, sdn)
         b_sl, b_sc = split(B3[b].T, num_splits, alpha, sdn)
-        C[b] = cross_gemm(a_sl, b_sl, a_sc, b_sc, A.dtype)
+        C[b] = cross_gemm(a_sl, b_sl, a_sc, b_sc, A.dtype, pairs=pairs)
         if return_parts:
             parts.append((a_sl, a_sc, b_sl, b_sc))
     C = C.reshape(*batch, M, N)

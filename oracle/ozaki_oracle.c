@@ -350,15 +350,15 @@ static void store_out(void *C, int out_dtype, int64_t idx, float out)
  * fp16 / bf16 / fp32 slices: acc_ij is the binary64 dot product of the exact
  * slice values, i.e. an (almost) exact reference for the fp32 hardware
  * accumulation, which a GPU kernel can only match within a tolerance.         */
-int ozo_cross_gemm_skip(const void *As, const void *Bs, const float *sa, const float *sb,
-                        int64_t M, int64_t N, int64_t K, int L, int slice_dtype, void *C,
-                        int out_dtype, int skip_pair);
+int ozo_cross_gemm_pairs(const void *As, const void *Bs, const float *sa, const float *sb,
+                         int64_t M, int64_t N, int64_t K, int L, int slice_dtype, void *C,
+                         int out_dtype, int pairs, int skip_pair);
 
 int ozo_cross_gemm(const void *As, const void *Bs, const float *sa, const float *sb,
                    int64_t M, int64_t N, int64_t K, int L, int slice_dtype, void *C,
                    int out_dtype)
 {
-    return ozo_cross_gemm_skip(As, Bs, sa, sb, M, N, K, L, slice_dtype, C, out_dtype, -1);
+    return ozo_cross_gemm_pairs(As, Bs, sa, sb, M, N, K, L, slice_dtype, C, out_dtype, 0, -1);
 }
 
 /* The same with the term of pair i * L + j == skip_pair left out of the outer
@@ -368,6 +368,19 @@ int ozo_cross_gemm_skip(const void *As, const void *Bs, const float *sa, const f
                         int64_t M, int64_t N, int64_t K, int L, int slice_dtype, void *C,
                         int out_dtype, int skip_pair)
 {
+    return ozo_cross_gemm_pairs(As, Bs, sa, sb, M, N, K, L, slice_dtype, C, out_dtype, 0,
+                                skip_pair);
+}
+
+/* pairs = 0: every pair (i, j), the reference's sum.  pairs = 1: only the
+ * pairs with i + j <= L - 1 (not in the reference: the triangular pair set of
+ * this library's ozk_cross_gemm_pairs / ozk_matmul_pairs), the same terms in
+ * the same i-major / j-minor order with the others left out.                 */
+int ozo_cross_gemm_pairs(const void *As, const void *Bs, const float *sa, const float *sb,
+                         int64_t M, int64_t N, int64_t K, int L, int slice_dtype, void *C,
+                         int out_dtype, int pairs, int skip_pair)
+{
+    if (pairs != 0 && pairs != 1) return -1;
     if (slice_dtype < OZO_F32 || slice_dtype > OZO_I8 || out_dtype < OZO_F64 ||
         out_dtype > OZO_I8 || L < 0)
         return -1;
@@ -409,7 +422,7 @@ int ozo_cross_gemm_skip(const void *As, const void *Bs, const float *sa, const f
                 for (int i = 0; i < L; ++i) {
                     float si = sa[(size_t)i * M + m];
                     for (int j = 0; j < L; ++j) {
-                        if (i * L + j == skip_pair) continue;
+                        if (i * L + j == skip_pair || (pairs == 1 && i + j > L - 1)) continue;
                         float t1 = acc[i * L + j] * si;
                         float t2 = t1 * sb[(size_t)j * N + n];
                         out = out + (double)t2;
@@ -421,7 +434,7 @@ int ozo_cross_gemm_skip(const void *As, const void *Bs, const float *sa, const f
                 for (int i = 0; i < L; ++i) {
                     float si = sa[(size_t)i * M + m];
                     for (int j = 0; j < L; ++j) {
-                        if (i * L + j == skip_pair) continue;
+                        if (i * L + j == skip_pair || (pairs == 1 && i + j > L - 1)) continue;
                         float t1 = acc[i * L + j] * si;
                         float t2 = t1 * sb[(size_t)j * N + n];
                         out = out + t2;

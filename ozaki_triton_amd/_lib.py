@@ -26,6 +26,7 @@ OZK_ERR_DEVICE_WAIT = -9
 OZK_ERR_TOO_LARGE = -10
 OZK_STATIC_SCRATCH_BYTES = 64 << 20
 OZK_MAX_SPLITS = 8
+OZK_PAIRS_ALL, OZK_PAIRS_TRIANGULAR = 0, 1
 
 # every symbol include/ozaki_amd.h declares
 EXPORTED = (
@@ -40,6 +41,8 @@ EXPORTED = (
     "ozk_matmul_workspace_bytes",
     "ozk_matmul",
     "ozk_matmul_static",
+    "ozk_cross_gemm_pairs",
+    "ozk_matmul_pairs",
 )
 
 # the test hooks of include/ozaki_amd_debug.h
@@ -49,6 +52,7 @@ EXPORTED_DEBUG = (
     "ozk_debug_force_split_kernel",
     "ozk_debug_force_coop_timeout",
     "ozk_debug_gemm_kernel",
+    "ozk_debug_gemm_kernel_pairs",
     "ozk_debug_split_kernel",
 )
 
@@ -103,6 +107,12 @@ def load() -> ctypes.CDLL:
     L.ozk_matmul_static.argtypes = [vp, p64, vp, p64, i32, i64, i64, i64, i64, i32, i32, vp,
                                     p64, ctypes.POINTER(ctypes.c_void_p), vp]
     L.ozk_matmul_static.restype = i32
+    L.ozk_cross_gemm_pairs.argtypes = [vp, p64, vp, p64, vp, p64, vp, p64, i64, i64, i64, i64,
+                                       i32, i32, i32, vp, i32, p64, vp, sz, vp]
+    L.ozk_cross_gemm_pairs.restype = i32
+    L.ozk_matmul_pairs.argtypes = [vp, p64, vp, p64, i32, i64, i64, i64, i64, i32, i32, i32, vp,
+                                   p64, vp, sz, ctypes.POINTER(ctypes.c_void_p), vp]
+    L.ozk_matmul_pairs.restype = i32
     cp = ctypes.c_char_p
     L.ozk_debug_force_gemm_kernel.argtypes = [cp]
     L.ozk_debug_force_gemm_kernel.restype = i32
@@ -116,6 +126,10 @@ def load() -> ctypes.CDLL:
                                         ctypes.POINTER(ctypes.c_char_p),
                                         ctypes.POINTER(ctypes.c_int)]
     L.ozk_debug_gemm_kernel.restype = i32
+    L.ozk_debug_gemm_kernel_pairs.argtypes = [i64, i64, i64, i64, i32, i32, i32, i32,
+                                              ctypes.POINTER(ctypes.c_char_p),
+                                              ctypes.POINTER(ctypes.c_int)]
+    L.ozk_debug_gemm_kernel_pairs.restype = i32
     L.ozk_debug_split_kernel.argtypes = [vp, i32, i64, i64, i64, p64, i32, i32, vp, p64,
                                          ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(sz)]
     L.ozk_debug_split_kernel.restype = i32

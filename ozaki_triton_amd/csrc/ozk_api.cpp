@@ -34,9 +34,19 @@ int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
 int hip_status(hipError_t e) { return e == hipSuccess ? OZK_OK : OZK_ERR_LAUNCH; }
 
+// A known pair set; the triangular one for at most 5 slices (no kernel sums
+// it over more: with the reference's fp32 residual buffer a sixth slice adds
+// no accuracy).
+bool pair_set_ok(int pairs, int L) {
+    if (pairs == OZK_PAIRS_ALL) return true;
+    return pairs == OZK_PAIRS_TRIANGULAR && L <= 5;
+}
+
 // Split-K buffers (plus 256 bytes of alignment slack) of the cross-GEMM of
 // K-contiguous slice operands with these strides, 0 when the plan has no
-// split-K.  Planned for 256 CUs: a device with fewer plans no more ranges.
+// split-K; the larger of the two pair sets' plans, so that the workspace
+// queries need no pair set.  Planned for 256 CUs: a device with fewer plans
+// no more ranges.
 size_t splitk_need(int64_t batch, int64_t M, int64_t N, int64_t K, int L, int sd,
                    int64_t as_l, int64_t as_m, int64_t bs_l, int64_t bs_n, int out_dtype) {
     if (L < 1 || L > 4 || batch * M * N == 0) return 0;
@@ -50,7 +60,12 @@ size_t splitk_need(int64_t batch, int64_t M, int64_t N, int64_t K, int L, int sd
     gp.N = N;
     gp.K = K;
     gp.out_dtype = out_dtype;
-    const size_t b = ozk::splitk_bytes(gp, ozk::plan_gemm(gp, L, sd, 256), L);
+    size_t b = 0;
+    for (int tri = 0; tri <= (L >= 2 ? 1 : 0); ++tri) {
+        gp.tri = tri;
+        const size_t bt = ozk::splitk_bytes(gp, ozk::plan_gemm(gp, L, sd, 256), L);
+        if (bt > b) b = bt;
+    }
     return b ? b + 256 : 0;
 }
 
@@ -116,7 +131,7 @@ const char *ozk_strerror(int status) {
     }
 }
 
-int ozk_version(void) { return 200; }
+int ozk_version(void) { return 300; }   // 0.3.0: the *_pairs calls
 
 int ozk_device_status(int clear, int *status_out, void *stream) {
     if (!status_out) return OZK_ERR_NULL;
@@ -217,13 +232,14 @@ static int cross_gemm_impl(const void *A_slices, const int64_t a_strides[4], con
                    const int64_t b_strides[4], const float *A_scales,
                    const int64_t sa_strides[3], const float *B_scales,
                    const int64_t sb_strides[3], int64_t batch, int64_t M, int64_t N, int64_t K,
-                   int num_splits, int slice_dtype, void *C, int out_dtype,
+                   int num_splits, int slice_dtype, int pairs, void *C, int out_dtype,
                    const int64_t c_strides[3], void *workspace, size_t workspace_bytes,
                    void *stream) {
     if (!a_strides || !b_strides || !sa_strides || !sb_strides || !c_strides)
         return OZK_ERR_NULL;
     if (!is_slice_dtype(slice_dtype) || !is_input_dtype(out_dtype)) return OZK_ERR_DTYPE;
-    if (num_splits < 0 || num_splits > OZK_MAX_SPLITS) return OZK_ERR_SPLITS;
+    if (num_splits < 0 || num_splits > OZK_MAX_SPLITS || !pair_set_ok(pairs, num_splits))
+        return OZK_ERR_SPLITS;
     if (batch < 0 || M < 0 || N < 0 || K < 0) return OZK_ERR_SHAPE;
     if (batch * M * N == 0) return OZK_OK;
     if (!C) return OZK_ERR_NULL;
@@ -247,6 +263,8 @@ static int cross_gemm_impl(const void *A_slices, const int64_t a_strides[4], con
     p.N = N;
     p.K = K;
     p.out_dtype = out_dtype;
+    // one slice is one pair in either set
+    p.tri = pairs == OZK_PAIRS_TRIANGULAR && num_splits >= 2;
     if (num_splits == 0) return hip_status(ozk::launch_zero_c(p, st));
     if (!A_slices || !B_slices || !A_scales || !B_scales) return OZK_ERR_NULL;
 
@@ -298,7 +316,7 @@ static int cross_gemm_impl(const void *A_slices, const int64_t a_strides[4], con
     if (num_splits > 4) {
         const bool solo = plan.kind == ozk::kGemmSolo5;
         const bool pair = plan.kind == ozk::kGemmPair && out_dtype == OZK_F64 &&
-                          slice_dtype != OZK_F32;
+                          slice_dtype != OZK_F32 && !p.tri;
         if (!solo && !pair) return OZK_ERR_SPLITS;
     }
     // split-K buffers after the packed operands, 256-byte aligned, when the
@@ -322,8 +340,21 @@ int ozk_cross_gemm(const void *A_slices, const int64_t a_strides[4], const void 
                    const int64_t c_strides[3], void *workspace, size_t workspace_bytes,
                    void *stream) {
     return cross_gemm_impl(A_slices, a_strides, B_slices, b_strides, A_scales, sa_strides,
-                           B_scales, sb_strides, batch, M, N, K, num_splits, slice_dtype, C,
-                           out_dtype, c_strides, workspace, workspace_bytes, stream);
+                           B_scales, sb_strides, batch, M, N, K, num_splits, slice_dtype,
+                           OZK_PAIRS_ALL, C, out_dtype, c_strides, workspace, workspace_bytes,
+                           stream);
+}
+
+int ozk_cross_gemm_pairs(const void *A_slices, const int64_t a_strides[4], const void *B_slices,
+                         const int64_t b_strides[4], const float *A_scales,
+                         const int64_t sa_strides[3], const float *B_scales,
+                         const int64_t sb_strides[3], int64_t batch, int64_t M, int64_t N,
+                         int64_t K, int num_splits, int slice_dtype, int pairs, void *C,
+                         int out_dtype, const int64_t c_strides[3], void *workspace,
+                         size_t workspace_bytes, void *stream) {
+    return cross_gemm_impl(A_slices, a_strides, B_slices, b_strides, A_scales, sa_strides,
+                           B_scales, sb_strides, batch, M, N, K, num_splits, slice_dtype, pairs,
+                           C, out_dtype, c_strides, workspace, workspace_bytes, stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -351,7 +382,8 @@ struct MatmulLayout {
 };
 
 int matmul_layout(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
-                  const int64_t as[3], const int64_t bs[3], int L, int sd, MatmulLayout *o) {
+                  const int64_t as[3], const int64_t bs[3], int L, int sd, int pairs,
+                  MatmulLayout *o) {
     if (!is_input_dtype(dtype) || !is_slice_dtype(sd)) return OZK_ERR_DTYPE;
     if (batch < 0 || M < 0 || N < 0 || K < 0) return OZK_ERR_SHAPE;
     // alpha for every num_splits, 0 included: the reference calls
@@ -362,7 +394,7 @@ int matmul_layout(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
         const int st = ozk_compute_split_bits(K, sd, sd == OZK_I8 ? OZK_I32 : OZK_F32, &o->alpha);
         if (st != OZK_OK) return st;
     }
-    if (L < 0 || L > OZK_MAX_SPLITS) return OZK_ERR_SPLITS;
+    if (L < 0 || L > OZK_MAX_SPLITS || !pair_set_ok(pairs, L)) return OZK_ERR_SPLITS;
     // more than 4 slices: 5 int8 / fp16 / bf16 slices into any C; 6 to 8 into
     // an fp64 C only
     if (L > 4 && (sd == OZK_F32 || (L > 5 && dtype != OZK_F64))) return OZK_ERR_SPLITS;
@@ -373,8 +405,10 @@ int matmul_layout(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
         ozk::GemmParams gp{};
         gp.as_l = M * kp; gp.as_m = kp; gp.bs_l = N * kp; gp.bs_n = kp;
         gp.batch = batch; gp.M = M; gp.N = N; gp.K = K; gp.out_dtype = dtype;
+        gp.tri = pairs == OZK_PAIRS_TRIANGULAR;
         const int kind = ozk::plan_gemm(gp, L, sd, 256).kind;
-        if (kind != ozk::kGemmSolo5 && !(kind == ozk::kGemmPair && dtype == OZK_F64))
+        if (kind != ozk::kGemmSolo5 &&
+            !(kind == ozk::kGemmPair && dtype == OZK_F64 && !gp.tri))
             return OZK_ERR_SPLITS;
     }
     o->bA = (batch > 1 && as[0] != 0) ? batch : 1;
@@ -437,7 +471,7 @@ int ozk_matmul_workspace_bytes(int dtype, int64_t batch, int64_t M, int64_t N, i
     if (!bytes_out || !a_strides || !b_strides) return OZK_ERR_NULL;
     MatmulLayout lay;
     const int st = matmul_layout(dtype, batch, M, N, K, a_strides, b_strides, num_splits,
-                                 slice_dtype, &lay);
+                                 slice_dtype, OZK_PAIRS_ALL, &lay);
     if (st != OZK_OK) return st;
     *bytes_out = (batch * M * N == 0 || num_splits == 0) ? 0 : lay.total;
     return OZK_OK;
@@ -447,10 +481,20 @@ int ozk_matmul(const void *A, const int64_t a_strides[3], const void *B,
                const int64_t b_strides[3], int dtype, int64_t batch, int64_t M, int64_t N,
                int64_t K, int num_splits, int slice_dtype, void *C, const int64_t c_strides[3],
                void *workspace, size_t workspace_bytes, void *const events[4], void *stream) {
+    return ozk_matmul_pairs(A, a_strides, B, b_strides, dtype, batch, M, N, K, num_splits,
+                            slice_dtype, OZK_PAIRS_ALL, C, c_strides, workspace,
+                            workspace_bytes, events, stream);
+}
+
+int ozk_matmul_pairs(const void *A, const int64_t a_strides[3], const void *B,
+                     const int64_t b_strides[3], int dtype, int64_t batch, int64_t M, int64_t N,
+                     int64_t K, int num_splits, int slice_dtype, int pairs, void *C,
+                     const int64_t c_strides[3], void *workspace, size_t workspace_bytes,
+                     void *const events[4], void *stream) {
     if (!a_strides || !b_strides || !c_strides) return OZK_ERR_NULL;
     MatmulLayout lay;
     const int lst = matmul_layout(dtype, batch, M, N, K, a_strides, b_strides, num_splits,
-                                  slice_dtype, &lay);
+                                  slice_dtype, pairs, &lay);
     if (lst != OZK_OK) return lst;
     if (batch * M * N == 0) return OZK_OK;
     if (!C) return OZK_ERR_NULL;
@@ -460,7 +504,8 @@ int ozk_matmul(const void *A, const int64_t a_strides[3], const void *B,
         // the reference's kernel stores its zero-initialised accumulator
         const int64_t z4[4] = {0, 0, 0, 0}, z3[3] = {0, 0, 0};
         return cross_gemm_impl(nullptr, z4, nullptr, z4, nullptr, z3, nullptr, z3, batch, M, N,
-                               K, 0, slice_dtype, C, dtype, c_strides, nullptr, 0, stream);
+                               K, 0, slice_dtype, OZK_PAIRS_ALL, C, dtype, c_strides, nullptr, 0,
+                               stream);
     }
     if (!A || !B) return OZK_ERR_NULL;
     // the split-K buffers at the end are optional
@@ -504,7 +549,7 @@ int ozk_matmul(const void *A, const int64_t a_strides[3], const void *B,
     // cross-GEMM over the K-contiguous slices
     e = cross_gemm_impl(ws + lay.a_sl, lay.ga, ws + lay.b_sl, lay.gb,
                         (const float *)(ws + lay.a_sc), lay.gsa, (const float *)(ws + lay.b_sc),
-                        lay.gsb, batch, M, N, K, L, slice_dtype, C, dtype, c_strides,
+                        lay.gsb, batch, M, N, K, L, slice_dtype, pairs, C, dtype, c_strides,
                         ws + lay.pack, workspace_bytes - lay.pack, stream);
     if (e != OZK_OK) return e;
     return record(events, 3, st);
@@ -552,7 +597,7 @@ extern "C" int ozk_matmul_static(const void *A, const int64_t a_strides[3], cons
     if (!a_strides || !b_strides || !c_strides) return OZK_ERR_NULL;
     MatmulLayout lay;
     const int lst = matmul_layout(dtype, batch, M, N, K, a_strides, b_strides, num_splits,
-                                  slice_dtype, &lay);
+                                  slice_dtype, OZK_PAIRS_ALL, &lay);
     if (lst != OZK_OK) return lst;
     if (batch * M * N == 0 || num_splits == 0)   // no workspace used
         return ozk_matmul(A, a_strides, B, b_strides, dtype, batch, M, N, K, num_splits,
@@ -627,9 +672,17 @@ int ozk_debug_force_coop_timeout(int on) {
 
 int ozk_debug_gemm_kernel(int64_t batch, int64_t M, int64_t N, int64_t K, int num_splits,
                           int slice_dtype, int cus, const char **name_out, int *ksplit_out) {
+    return ozk_debug_gemm_kernel_pairs(batch, M, N, K, num_splits, slice_dtype, OZK_PAIRS_ALL,
+                                       cus, name_out, ksplit_out);
+}
+
+int ozk_debug_gemm_kernel_pairs(int64_t batch, int64_t M, int64_t N, int64_t K, int num_splits,
+                                int slice_dtype, int pairs, int cus, const char **name_out,
+                                int *ksplit_out) {
     if (!name_out) return OZK_ERR_NULL;
     if (!is_slice_dtype(slice_dtype)) return OZK_ERR_DTYPE;
-    if (num_splits < 1 || num_splits > OZK_MAX_SPLITS) return OZK_ERR_SPLITS;
+    if (num_splits < 1 || num_splits > OZK_MAX_SPLITS || !pair_set_ok(pairs, num_splits))
+        return OZK_ERR_SPLITS;
     if (batch < 0 || M < 0 || N < 0 || K < 0) return OZK_ERR_SHAPE;
     ozk::GemmParams p{};
     const int64_t es = slice_size(slice_dtype);
@@ -646,6 +699,7 @@ int ozk_debug_gemm_kernel(int64_t batch, int64_t M, int64_t N, int64_t K, int nu
     p.N = N;
     p.K = K;
     p.out_dtype = OZK_F64;
+    p.tri = pairs == OZK_PAIRS_TRIANGULAR && num_splits >= 2;
     const ozk::GemmPlan plan = ozk::plan_gemm(p, num_splits, slice_dtype, cus);
     *name_out = name_of(kGemmNames, plan.kind);
     if (ksplit_out) *ksplit_out = plan.ksplit;

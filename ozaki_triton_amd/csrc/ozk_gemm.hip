@@ -190,6 +190,41 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
                                    : kGemmPair;
     const int force = debug_overrides().gemm;
     auto forced = [&](int kind) { return force == kind; };
+    if (p.tri && L >= 2) {
+        // The triangular pair set runs on the kernels that hold every pair of
+        // a block in one wave: the K-step kernel where it runs by default,
+        // else the wide kernel at L = 3 (with split-K on small grids), the
+        // one-wave-per-SIMD kernel at L = 5, and the LDS-DMA kernel at L = 2
+        // and 4 (at L = 4 its 10 pairs of a 32 x 32 block take 160
+        // accumulator registers).  L > 5 has none (kGemmPair: the caller
+        // rejects it).
+        plan.kind = !fits     ? kGemmStaged
+                    : kstep   ? kGemmKStep
+                    : L == 3  ? kGemmWide
+                    : L <= 4  ? kGemmDMA
+                    : solo5   ? kGemmSolo5
+                              : kGemmPair;
+        if (L <= 4) {
+            if (forced(kGemmStaged)) plan.kind = kGemmStaged;
+            else if (fits && forced(kGemmAD)) plan.kind = kGemmAD;
+            else if (fits && forced(kGemmDMA)) plan.kind = kGemmDMA;
+            else if (fits && forced(kGemmWide) && L == 3) plan.kind = kGemmWide;
+            else if (fits && forced(kGemmKStep) && !(L == 4 && slice_dtype == 1))
+                plan.kind = kGemmKStep;
+        }
+        if (plan.kind == kGemmAD) plan.group_m = 2;
+        plan.kb_per_split = nkb_all;
+        if (plan.kind == kGemmWide) {
+            const int fk = debug_overrides().ksplit;
+            int sk = fk > 0 ? fk : ksplit_for(wide_tiles);
+            if (sk > nkb_all) sk = nkb_all;
+            if (sk > 1) {
+                plan.kb_per_split = (nkb_all + sk - 1) / sk;
+                plan.ksplit = (nkb_all + plan.kb_per_split - 1) / plan.kb_per_split;
+            }
+        }
+        return plan;
+    }
     if (L > 4) {
         // the pair-split kernel keeps its partial sums in an fp64 C
         if (fits && forced(kGemmPair) && p.out_dtype == 0 && slice_dtype != 1)

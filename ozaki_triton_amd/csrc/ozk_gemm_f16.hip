@@ -5,8 +5,7 @@
 namespace ozk {
 
 hipError_t launch_gemm_f16(const GemmParams &p, const GemmPlan &plan, int L, hipStream_t st) {
-    return p.out_dtype == 0 ? launch_st<_Float16, double>(p, plan, L, st)
-                            : launch_st<_Float16, float>(p, plan, L, st);
+    return launch_typed<_Float16>(p, plan, L, st);
 }
 
 }  // namespace ozk

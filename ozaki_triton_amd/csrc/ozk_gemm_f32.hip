@@ -5,8 +5,7 @@
 namespace ozk {
 
 hipError_t launch_gemm_f32(const GemmParams &p, const GemmPlan &plan, int L, hipStream_t st) {
-    return p.out_dtype == 0 ? launch_st<float, double>(p, plan, L, st)
-                            : launch_st<float, float>(p, plan, L, st);
+    return launch_typed<float>(p, plan, L, st);
 }
 
 }  // namespace ozk

@@ -5,8 +5,7 @@
 namespace ozk {
 
 hipError_t launch_gemm_i8(const GemmParams &p, const GemmPlan &plan, int L, hipStream_t st) {
-    return p.out_dtype == 0 ? launch_st<int8_t, double>(p, plan, L, st)
-                            : launch_st<int8_t, float>(p, plan, L, st);
+    return launch_typed<int8_t>(p, plan, L, st);
 }
 
 }  // namespace ozk

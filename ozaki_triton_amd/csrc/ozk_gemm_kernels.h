@@ -133,6 +133,41 @@ OZK_DEV int64_t xcd_remap_gemm(int64_t g, int64_t n) {
     return (g % 8) * q + g / 8;
 }
 
+template <int N, typename F> OZK_DEV void static_for(F &&f) {
+    if constexpr (N > 0) {
+        static_for<N - 1>(f);
+        f(std::integral_constant<int, N - 1>{});
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Pair sets.  The reference sums all L x L slice pairs (i, j).  With TRI a
+// kernel sums only the triangle i + j <= L - 1, L (L + 1) / 2 pairs: the
+// terms it drops are of the order of the split's own truncation error (pair
+// (i, j) carries about 2^(-alpha (i + j)) of C's magnitude).  Pair n of a set
+// is its n-th pair in i-major, j-minor order, the order of the outer sum, so
+// a kernel that walks n in order sums the reference's terms in the
+// reference's order and only leaves the others out.
+// ---------------------------------------------------------------------------
+template <int L, bool TRI> struct Pairs {
+    static constexpr int N = TRI ? L * (L + 1) / 2 : L * L;
+    __host__ __device__ static constexpr bool kept(int i, int j) { return !TRI || i + j < L; }
+    // index of pair (i, 0)
+    __host__ __device__ static constexpr int first(int i) {
+        return TRI ? i * L - i * (i - 1) / 2 : i * L;
+    }
+    __host__ __device__ static constexpr int i_of(int n) {
+        int i = 0;
+        while (i + 1 < L && first(i + 1) <= n) ++i;
+        return i;
+    }
+    __host__ __device__ static constexpr int j_of(int n) { return n - first(i_of(n)); }
+};
+static_assert(Pairs<5, true>::N == 15 && Pairs<5, true>::i_of(14) == 4 &&
+                  Pairs<5, true>::j_of(14) == 0 && Pairs<5, true>::j_of(4) == 4 &&
+                  Pairs<5, true>::i_of(5) == 1 && Pairs<4, false>::j_of(6) == 2,
+              "pair table");
+
 constexpr int kRowBytes = 128;   // bytes of K per row per stage
 constexpr int kChunks = kRowBytes / 16;
 
@@ -157,8 +192,9 @@ OZK_DEV int swz(int row, int chunk) {
     return row * kRowBytes + ((chunk ^ ((row >> 1) & 7)) << 4);
 }
 
-template <typename ST, int L, int MI, int NI, typename AccT>
+template <typename ST, int L, int MI, int NI, typename AccT, bool TRI>
 __global__ __launch_bounds__(256, 1) void cross_gemm_kernel(GemmParams p, int group_m) {
+    using PS = Pairs<L, TRI>;
     using Sh = GemmShape<L, MI, NI>;
     using MF = Mfma<ST>;
     using Acc = typename MF::Acc;
@@ -276,7 +312,8 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_kernel(GemmParams p, int gr
                     for (int a = 0; a < MI; ++a)
 #pragma unroll
                         for (int c = 0; c < NI; ++c)
-                            acc[i][j][a][c] = MF::run(af[i][a], bf[j][c], acc[i][j][a][c]);
+                            if (PS::kept(i, j))
+                                acc[i][j][a][c] = MF::run(af[i][a], bf[j][c], acc[i][j][a][c]);
         }
         if (more) store_stage(smem + ((kb + 1) & 1) * Sh::STAGE, stg);
         __syncthreads();
@@ -305,6 +342,7 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_kernel(GemmParams p, int gr
                         const float sai = sab[i * p.sas_l + row * p.sas_m];
 #pragma unroll
                         for (int j = 0; j < L; ++j) {
+                            if (!PS::kept(i, j)) continue;
                             const float x = MF::to_f32(acc[i][j][a][c][r]);
                             const float t1 = x * sai;
                             const float t2 = t1 * sbv[j];
@@ -422,7 +460,7 @@ OZK_DEV bool splitk_arrive(const GemmParams &p, int64_t tile, int *flag) {
     return *flag == p.ksplit - 1;
 }
 
-template <typename ST, int L, int MI, int NI, typename AccT>
+template <typename ST, int L, int MI, int NI, typename AccT, bool TRI>
 __global__ __launch_bounds__(256, 1) void cross_gemm_dma_kernel(GemmParams p, int group_m,
                                                                 uint32_t a_records,
                                                                 uint32_t b_records) {
@@ -523,8 +561,9 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_dma_kernel(GemmParams p, in
         i32x4 a[L][MI];
         i32x4 b[L][NI];
     };
+    using PS = Pairs<L, TRI>;
     constexpr int kReads = L * (MI + NI);
-    constexpr int kMfmas = L * L * MI * NI;
+    constexpr int kMfmas = PS::N * MI * NI;
     auto read_one = [&](const char *buf, int kk, int r, Frags &f) {
         const int ch = 2 * kk + h;
         if (r < L * MI) {
@@ -540,14 +579,14 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_dma_kernel(GemmParams p, in
     // interleaved one per MFMA, so no MFMA waits on a read issued after the
     // reads of its own operands and the LDS latency hides under the MFMAs.
     auto step = [&](const Frags &cur, Frags &nxt, const char *nbuf, int nkk) {
-#pragma unroll
-        for (int q = 0; q < kMfmas; ++q) {
-            const int i = q / (L * MI * NI), j = (q / (MI * NI)) % L;
-            const int a = (q / NI) % MI, c = q % NI;
+        static_for<kMfmas>([&](auto q_) {
+            constexpr int q = decltype(q_)::value;
+            constexpr int i = PS::i_of(q / (MI * NI)), j = PS::j_of(q / (MI * NI));
+            constexpr int a = (q / NI) % MI, c = q % NI;
             acc[i][j][a][c] = MF::run(cur.a[i][a], cur.b[j][c], acc[i][j][a][c]);
-            if (q < kReads) read_one(nbuf, nkk, q, nxt);
+            if constexpr (q < kReads) read_one(nbuf, nkk, q, nxt);
             __builtin_amdgcn_sched_barrier(0);   // keep this order
-        }
+        });
 #pragma unroll
         for (int q = kMfmas; q < kReads; ++q) read_one(nbuf, nkk, q, nxt);
     };
@@ -633,6 +672,7 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_dma_kernel(GemmParams p, in
                         const float sai = sab[i * p.sas_l + row * p.sas_m];
 #pragma unroll
                         for (int j = 0; j < L; ++j) {
+                            if (!PS::kept(i, j)) continue;
                             const float x = MF::to_f32(acc[i][j][a][c][r]);
                             const float t1 = x * sai;
                             const float t2 = t1 * sbv[j];
@@ -667,13 +707,6 @@ template <bool AG> struct HandMfma<__bf16, AG> {
     }
 };
 
-template <int N, typename F> OZK_DEV void static_for(F &&f) {
-    if constexpr (N > 0) {
-        static_for<N - 1>(f);
-        f(std::integral_constant<int, N - 1>{});
-    }
-}
-
 // ---------------------------------------------------------------------------
 // K-step kernel for grids too small to fill the chip with 64 x 64 tiles (tall
 // or skinny C, large K).  32 x 32 tiles, 4 waves (one per SIMD).  Wave w
@@ -694,13 +727,13 @@ template <int N, typename F> OZK_DEV void static_for(F &&f) {
 //     (ozaki_triton.py:420-452) and stores C.  The tile's scales are loaded
 //     at kernel start.
 // ---------------------------------------------------------------------------
-template <int L> struct KStepShape {
+template <int L, bool TRI> struct KStepShape {
     static constexpr int BM = 32, BN = 32;
     static constexpr int ROWS = 2 * L * 32;                   // A rows then B rows
     static constexpr int STAGE = ROWS * kDmaRB;
     static constexpr int LPS = STAGE / (4 * 1024);            // DMA instructions per wave per stage
     static constexpr int NST = (160 * 1024 / STAGE) < 6 ? (160 * 1024 / STAGE) : 6;
-    static constexpr int NP = L * L;                          // slice pairs
+    static constexpr int NP = Pairs<L, TRI>::N;               // slice pairs summed
     static constexpr int PR = NP < 4 ? NP : 4;                // pairs per epilogue group
     static constexpr int T_BYTES = NP * 16 * 64 * 4;          // t values [pair][reg / 4][lane][4]
     static constexpr int R_BYTES = 4 * PR * 16 * 64 * 4;      // [wave][pair][reg / 4][lane][4]
@@ -714,11 +747,12 @@ template <int L> struct KStepShape {
     static_assert(kDmaRB == 128 && L * 32 <= 128, "four K steps per stage; scales one per lane");
 };
 
-template <typename ST, int L, typename AccT>
+template <typename ST, int L, typename AccT, bool TRI>
 __global__ __launch_bounds__(256, 1) void cross_gemm_kstep_kernel(GemmParams p, int group_m,
                                                                   uint32_t a_records,
                                                                   uint32_t b_records) {
-    using Sh = KStepShape<L>;
+    using Sh = KStepShape<L, TRI>;
+    using PS = Pairs<L, TRI>;
     using MF = Mfma<ST>;
     using Acc = typename MF::Acc;
     using Elem = typename MF::Elem;
@@ -827,10 +861,10 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_kstep_kernel(GemmParams p, 
     // zeroed tiles are pinned here, 8 wait states before any MFMA reads them.
     constexpr bool kHand = Sh::kHand;
     if constexpr (kHand) {
-        static_for<L * L>([&](auto n_) {
+        static_for<PS::N>([&](auto n_) {
             constexpr int n = decltype(n_)::value;
             (void)acc;   // an ordinary use, so that the capture does not hinge on the asm operand
-            asm volatile("" : "+a"(acc[n / L][n % L]));
+            asm volatile("" : "+a"(acc[PS::i_of(n)][PS::j_of(n)]));
         });
         asm volatile("s_nop 7" ::: "memory");
     }
@@ -852,11 +886,12 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_kstep_kernel(GemmParams p, 
     // dkb >= 0) spread between them: issued in a burst, the four waves'
     // instructions fill the vector-memory queue and stall each wave at issue
     auto mfmas = [&](const Frags &f, int dkb) {
-        constexpr int NMF = L * L;
+        constexpr int NMF = PS::N;
         static_for<NMF>([&](auto n_) {
             constexpr int n = decltype(n_)::value;
-            if constexpr (kHand) HandMfma<ST, true>::run(acc[n / L][n % L], f.a[n / L], f.b[n % L]);
-            else acc[n / L][n % L] = MF::run(f.a[n / L], f.b[n % L], acc[n / L][n % L]);
+            constexpr int i = PS::i_of(n), j = PS::j_of(n);
+            if constexpr (kHand) HandMfma<ST, true>::run(acc[i][j], f.a[i], f.b[j]);
+            else acc[i][j] = MF::run(f.a[i], f.b[j], acc[i][j]);
             static_for<LPS>([&](auto d_) {
                 constexpr int d = decltype(d_)::value;
                 // instruction d goes after MFMA (d * NMF) / LPS
@@ -912,24 +947,24 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_kstep_kernel(GemmParams p, 
     float *S = (float *)(smem + Sh::T_BYTES + Sh::R_BYTES);
     if ((tid & 127) < L * 32) S[(tid < 128 ? 0 : L * 32) + (tid & 127)] = scl;
     constexpr int NG = (Sh::NP + Sh::PR - 1) / Sh::PR;
-#pragma unroll
-    for (int gi = 0; gi < NG; ++gi) {
-#pragma unroll
-        for (int pp = 0; pp < Sh::PR; ++pp) {
-            const int pr = gi * Sh::PR + pp;
-            if (pr < Sh::NP) {
-                const Acc v = acc[pr / L][pr % L];
+    static_for<NG>([&](auto gi_) {
+        constexpr int gi = decltype(gi_)::value;
+        static_for<Sh::PR>([&](auto pp_) {
+            constexpr int pp = decltype(pp_)::value;
+            constexpr int pr = gi * Sh::PR + pp;
+            if constexpr (pr < Sh::NP) {
+                const Acc v = acc[PS::i_of(pr)][PS::j_of(pr)];
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
                     R[((wave * Sh::PR + pp) * 4 + c) * 64 + lane] =
                         E4{v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]};
             }
-        }
+        });
         __builtin_amdgcn_s_waitcnt(0xC07F);
         exec_barrier();
         const int pr = gi * Sh::PR + wave;
         if (wave < Sh::PR && pr < Sh::NP) {
-            const int i = pr / L, j = pr % L;
+            const int i = PS::i_of(pr), j = PS::j_of(pr);
             const float sbj = S[L * 32 + j * 32 + lr];
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
@@ -949,7 +984,7 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_kstep_kernel(GemmParams p, 
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);
         exec_barrier();
-    }
+    });
     // wave w: accumulator registers 4w .. 4w + 3 of every lane, rows
     // 8w + 4h + 0..3
     const int64_t col = n0 + lr;
@@ -1668,7 +1703,7 @@ struct WideShape {
     static_assert(kDmaRB == 128, "128-byte stage rows");
 };
 
-template <typename ST, typename AccT>
+template <typename ST, typename AccT, bool TRI>
 __global__ __launch_bounds__(512, 1) void cross_gemm_wide_kernel(GemmParams p, int group_m,
                                                                  uint32_t a_records,
                                                                  uint32_t b_records) {
@@ -1677,6 +1712,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide_kernel(GemmParams p, i
     using Acc = typename MF::Acc;
     using OA = AccT;
     constexpr int L = Sh::L, BM = Sh::BM, BN = Sh::BN;
+    using PS = Pairs<L, TRI>;
     constexpr int ES = (int)sizeof(ST);
     constexpr uint32_t kOOB = 0x80000000u;
     extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -1813,17 +1849,18 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide_kernel(GemmParams p, i
         const int cnt = hi - lo;
 #pragma unroll
         for (int q = 0; q < 2 * L; ++q) read_one(rkb, nkk, q, nxt);
-#pragma unroll
-        for (int n = 0; n < L * L; ++n) {
-            const int i = n / L, j = n % L;
+        constexpr int NMF = PS::N;
+        static_for<NMF>([&](auto n_) {
+            constexpr int n = decltype(n_)::value;
+            constexpr int i = PS::i_of(n), j = PS::j_of(n);
             acc[i][j] = MF::run(cur.a[i], cur.b[j], acc[i][j]);
 #pragma unroll
             for (int d = 0; d < Sh::P1; ++d) {
-                // instruction lo + d goes after MFMA (d * L * L) / cnt
-                if (d < cnt && (d * L * L) / cnt == n && on) issue(dkb, lo + d);
+                // instruction lo + d goes after MFMA (d * NMF) / cnt
+                if (d < cnt && (d * NMF) / cnt == n && on) issue(dkb, lo + d);
             }
             __builtin_amdgcn_sched_barrier(0);
-        }
+        });
     };
 
     Frags f0, f1;
@@ -1865,6 +1902,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide_kernel(GemmParams p, i
         uint32_t *mine = splitk_slot(p, g, krange, wave, RW, ln);
 #pragma unroll
         for (int n = 0; n < L * L; ++n) {
+            if (!PS::kept(n / L, n % L)) continue;
             const i32x16 u = __builtin_bit_cast(i32x16, acc[n / L][n % L]);
 #pragma unroll
             for (int r = 0; r < 16; ++r) splitk_put(mine + (n * 16 + r) * 64, (uint32_t)u[r]);
@@ -1879,7 +1917,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide_kernel(GemmParams p, i
                 const uint32_t *src = splitk_slot(p, g, s2, wave, RW, ln);
 #pragma unroll
                 for (int n = 0; n < L * L; ++n)
-                    acc[n / L][n % L] += splitk_get16<Acc>(src + n * 16 * 64);
+                    if (PS::kept(n / L, n % L)) acc[n / L][n % L] += splitk_get16<Acc>(src + n * 16 * 64);
             }
         } else {
             // every range read back, this one's too, in range order: range
@@ -1887,13 +1925,14 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide_kernel(GemmParams p, i
             {
                 const uint32_t *src = splitk_slot(p, g, 0, wave, RW, ln);
 #pragma unroll
-                for (int n = 0; n < L * L; ++n) acc[n / L][n % L] = splitk_get16<Acc>(src + n * 16 * 64);
+                for (int n = 0; n < L * L; ++n)
+                    if (PS::kept(n / L, n % L)) acc[n / L][n % L] = splitk_get16<Acc>(src + n * 16 * 64);
             }
             for (int s2 = 1; s2 < S; ++s2) {
                 const uint32_t *src = splitk_slot(p, g, s2, wave, RW, ln);
 #pragma unroll
                 for (int n = 0; n < L * L; ++n)
-                    acc[n / L][n % L] += splitk_get16<Acc>(src + n * 16 * 64);
+                    if (PS::kept(n / L, n % L)) acc[n / L][n % L] += splitk_get16<Acc>(src + n * 16 * 64);
             }
         }
     }
@@ -1913,6 +1952,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide_kernel(GemmParams p, i
             const float sai = sa_lds[i * BM + rt];
 #pragma unroll
             for (int j = 0; j < L; ++j) {
+                if (!PS::kept(i, j)) continue;
                 // fl32(fl32(fl32(acc) * sa_i) * sb_j), summed i-major, j-minor
                 const float t1 = MF::to_f32(acc[i][j][r]) * sai;
                 out = out + (OA)(t1 * sbv[j]);
@@ -2283,13 +2323,16 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide4_kernel(GemmParams p, 
 // file holds (256 each), so each MFMA is written out with its accumulator
 // placed explicitly: tiles 0..15 in AGPRs, 16..24 in VGPRs (the compiler
 // does not split a kernel's MFMA accumulators between the two files by
-// itself).  The fragments are double-buffered: a K step's 10 reads are
+// itself).  With the triangular pair set (TRI) a wave holds the 15 pairs
+// i + j <= 4, all in AGPRs, and runs 15 MFMAs per K step on the same reads.
+// The fragments are double-buffered: a K step's 10 reads are
 // issued one whole K step ahead.  A lone wave issues independent MFMAs at
 // 92-95% of the rate two waves reach (measured with 12 accumulators).
 // Hazards of the hand-placed MFMAs that the compiler cannot see: their
 // results are read by other instructions only in the epilogue, after 64 wait
 // states; an accumulator is first read as srcC after its zero fill and the
-// prologue's barrier; each one is accumulated again only 25 MFMAs later.
+// prologue's barrier; each one is accumulated again only 25 (TRI: 15) MFMAs
+// later.
 // The LDS holds two whole stages of 128 bytes of K (2 x 80 KB); stage kb + 2
 // is fetched into stage kb's buffer after the barrier of stage kb, spread
 // over the two K steps that follow it.
@@ -2314,7 +2357,7 @@ struct Solo5Shape {
     static_assert(kDmaRB == 128, "128-byte stage rows");
 };
 
-template <typename ST, typename AccT>
+template <typename ST, typename AccT, bool TRI>
 __global__ __launch_bounds__(256, 1) void cross_gemm_solo5_kernel(GemmParams p, int group_m,
                                                                   uint32_t a_records,
                                                                   uint32_t b_records) {
@@ -2323,6 +2366,7 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_solo5_kernel(GemmParams p, 
     using Acc = typename MF::Acc;
     using OA = AccT;
     constexpr int L = Sh::L, BM = Sh::BM, BN = Sh::BN;
+    using PS = Pairs<L, TRI>;
     constexpr int ES = (int)sizeof(ST);
     constexpr uint32_t kOOB = 0x80000000u;
     extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -2431,11 +2475,12 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_solo5_kernel(GemmParams p, 
     // recogniser does not see into: the zeroed accumulators are pinned in
     // their register files here, before the prologue, and 8 wait states
     // separate those writes from any MFMA that reads them.
-    static_for<L * L>([&](auto n_) {
+    static_for<PS::N>([&](auto n_) {
         constexpr int n = decltype(n_)::value;
+        constexpr int i = PS::i_of(n), j = PS::j_of(n);
         (void)acc;   // an ordinary use, so that the capture does not hinge on the asm operands
-        if constexpr (n < Sh::NAGPR) asm volatile("" : "+a"(acc[n / L][n % L]));
-        else asm volatile("" : "+v"(acc[n / L][n % L]));
+        if constexpr (n < Sh::NAGPR) asm volatile("" : "+a"(acc[i][j]));
+        else asm volatile("" : "+v"(acc[i][j]));
     });
     asm volatile("s_nop 7" ::: "memory");
 
@@ -2480,12 +2525,12 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_solo5_kernel(GemmParams p, 
     // instructions [lo, hi) of stage dkb spread between them.
     auto step = [&](const Frags &cur, Frags &nxt, int rkb, int nkk, int dkb, bool on, int lo,
                     int hi) {
-        constexpr int NMF = L * L;
+        constexpr int NMF = PS::N;
         const int cnt = hi - lo;
         read_all(rkb, nkk, nxt);
         static_for<NMF>([&](auto n_) {
             constexpr int n = decltype(n_)::value;
-            constexpr int u = n / L, j = n % L;
+            constexpr int u = PS::i_of(n), j = PS::j_of(n);
             HandMfma<ST, (n < Sh::NAGPR)>::run(acc[u][j], cur.a[u], cur.b[j]);
 #pragma unroll
             for (int d = 0; d < Sh::LPS; ++d) {
@@ -2547,6 +2592,7 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_solo5_kernel(GemmParams p, 
             for (int i = 0; i < L; ++i)
 #pragma unroll
                 for (int j = 0; j < L; ++j) {
+                    if (!PS::kept(i, j)) continue;
                     // fl32(fl32(fl32(acc) * sa_i) * sb_j), summed i-major, j-minor
                     const float t1 = MF::to_f32(acc[i][j][r]) * s4[i][e];
                     out = out + (OA)(t1 * sbv[j]);
@@ -2589,11 +2635,12 @@ template <int L, int NI> struct AdShape {
     static_assert(2 * PER_STAGE * 1 < 64, "vmcnt range");
 };
 
-template <typename ST, int L, int NI, typename AccT>
+template <typename ST, int L, int NI, typename AccT, bool TRI>
 __global__ __launch_bounds__(256, 1) void cross_gemm_ad_kernel(GemmParams p, int group_m,
                                                                uint32_t a_records,
                                                                uint32_t b_records) {
     using Sh = AdShape<L, NI>;
+    using PS = Pairs<L, TRI>;
     using MF = Mfma<ST>;
     using Acc = typename MF::Acc;
     using OA = AccT;   // outer accumulator: fp64 for fp64 output, else fp32 (store_c)
@@ -2688,16 +2735,16 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_ad_kernel(GemmParams p, int
         f.b[j][c] = *(const i32x4 *)(buf + dswz(j * BN + c * 32 + lr, 2 * h + tt));
     };
     constexpr int kReads = L * NI;
-    constexpr int kMfmas = L * L * NI;
+    constexpr int kMfmas = PS::N * NI;
     auto step = [&](const i32x4 (&ar)[L][2], int tt, const BFr &cur, BFr &nxt,
                     const char *nbuf, int ntt) {
-#pragma unroll
-        for (int q = 0; q < kMfmas; ++q) {
-            const int i = q / (L * NI), j = (q / NI) % L, c = q % NI;
+        static_for<kMfmas>([&](auto q_) {
+            constexpr int q = decltype(q_)::value;
+            constexpr int i = PS::i_of(q / NI), j = PS::j_of(q / NI), c = q % NI;
             acc[i][j][c] = MF::run(ar[i][tt], cur.b[j][c], acc[i][j][c]);
-            if (q < kReads) read_b(nbuf, ntt, q, nxt);
+            if constexpr (q < kReads) read_b(nbuf, ntt, q, nxt);
             __builtin_amdgcn_sched_barrier(0);
-        }
+        });
 #pragma unroll
         for (int q = kMfmas; q < kReads; ++q) read_b(nbuf, ntt, q, nxt);
     };
@@ -2761,6 +2808,7 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_ad_kernel(GemmParams p, int
                     const float sai = sab[i * p.sas_l + row * p.sas_m];
 #pragma unroll
                     for (int j = 0; j < L; ++j) {
+                        if (!PS::kept(i, j)) continue;
                         const float x = MF::to_f32(acc[i][j][c][r]);
                         const float t1 = x * sai;
                         const float t2 = t1 * sbv[j];
@@ -2805,10 +2853,10 @@ static inline hipError_t set_lds_limit(const void *kern, int bytes, std::atomic<
 }
 
 
-template <typename ST, int L, int MI, int NI, typename AccT>
+template <typename ST, int L, int MI, int NI, typename AccT, bool TRI>
 static hipError_t launch_dma(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     using Sh = DmaShape<L, MI, NI>;
-    auto kern = cross_gemm_dma_kernel<ST, L, MI, NI, AccT>;
+    auto kern = cross_gemm_dma_kernel<ST, L, MI, NI, AccT, TRI>;
     static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
     if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
     const int es = (int)sizeof(ST);
@@ -2821,10 +2869,10 @@ static hipError_t launch_dma(const GemmParams &p, const GemmPlan &plan, hipStrea
     return hipGetLastError();
 }
 
-template <typename ST, int L, typename AccT>
+template <typename ST, int L, typename AccT, bool TRI>
 static hipError_t launch_kstep(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
-    using Sh = KStepShape<L>;
-    auto kern = cross_gemm_kstep_kernel<ST, L, AccT>;
+    using Sh = KStepShape<L, TRI>;
+    auto kern = cross_gemm_kstep_kernel<ST, L, AccT, TRI>;
     static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
     if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
     const int es = (int)sizeof(ST);
@@ -2837,10 +2885,10 @@ static hipError_t launch_kstep(const GemmParams &p, const GemmPlan &plan, hipStr
     return hipGetLastError();
 }
 
-template <typename ST, int L, int NI, typename AccT>
+template <typename ST, int L, int NI, typename AccT, bool TRI>
 static hipError_t launch_ad(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     using Sh = AdShape<L, NI>;
-    auto kern = cross_gemm_ad_kernel<ST, L, NI, AccT>;
+    auto kern = cross_gemm_ad_kernel<ST, L, NI, AccT, TRI>;
     static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
     if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
     const int es = (int)sizeof(ST);
@@ -2888,10 +2936,10 @@ static hipError_t launch_ring(const GemmParams &p, const GemmPlan &plan, hipStre
     return hipGetLastError();
 }
 
-template <typename ST, typename AccT>
+template <typename ST, typename AccT, bool TRI>
 static hipError_t launch_wide(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     using Sh = WideShape;
-    auto kern = cross_gemm_wide_kernel<ST, AccT>;
+    auto kern = cross_gemm_wide_kernel<ST, AccT, TRI>;
     static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
     if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
     const int es = (int)sizeof(ST);
@@ -2921,13 +2969,13 @@ static hipError_t launch_wide4(const GemmParams &p, const GemmPlan &plan, hipStr
     return hipGetLastError();
 }
 
-template <typename ST, typename AccT>
+template <typename ST, typename AccT, bool TRI>
 static hipError_t launch_solo5(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     if constexpr (std::is_same<ST, float>::value) {
         return hipErrorInvalidValue;   // no fp32-slice form
     } else {
         using Sh = Solo5Shape;
-        auto kern = cross_gemm_solo5_kernel<ST, AccT>;
+        auto kern = cross_gemm_solo5_kernel<ST, AccT, TRI>;
         static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
         if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
         const int es = (int)sizeof(ST);
@@ -2960,27 +3008,36 @@ static hipError_t launch_chunks(const GemmParams &p, const GemmPlan &plan, hipSt
     }
 }
 
-template <typename ST, int L, int MI, int NI, typename AccT>
+// TRI: the triangular pair set, which the kernels that hold every pair of a
+// block in one wave sum (staged, dma, ad, kstep, wide, solo5); the pair-split
+// kernels (pair, ring, wide4) are not instantiated for it, and the planner
+// does not choose them.
+template <typename ST, int L, int MI, int NI, typename AccT, bool TRI>
 static hipError_t launch_one(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
-    if constexpr (L >= 3) {
-        if (plan.kind == kGemmPair) return launch_pair<ST, L, AccT, L>(p, plan, st, 0, 0);
+    if constexpr (!TRI) {
+        if constexpr (L >= 3) {
+            if (plan.kind == kGemmPair) return launch_pair<ST, L, AccT, L>(p, plan, st, 0, 0);
+        }
+        if constexpr (L == 4) {
+            if (plan.kind == kGemmWide4) return launch_wide4<ST, AccT>(p, plan, st);
+        }
+        if constexpr (L >= 2 && L <= 4) {
+            if (plan.kind == kGemmRing) return launch_ring<ST, L, AccT>(p, plan, st);
+        }
+    } else {
+        if (plan.kind == kGemmPair || plan.kind == kGemmWide4 || plan.kind == kGemmRing)
+            return hipErrorInvalidValue;
     }
     if constexpr (L == 3) {
-        if (plan.kind == kGemmWide) return launch_wide<ST, AccT>(p, plan, st);
-    }
-    if constexpr (L == 4) {
-        if (plan.kind == kGemmWide4) return launch_wide4<ST, AccT>(p, plan, st);
-    }
-    if constexpr (L >= 2 && L <= 4) {
-        if (plan.kind == kGemmRing) return launch_ring<ST, L, AccT>(p, plan, st);
+        if (plan.kind == kGemmWide) return launch_wide<ST, AccT, TRI>(p, plan, st);
     }
     if (plan.kind == kGemmAD) {
         constexpr int ANI = (L == 1) ? 8 : (L == 2) ? 4 : 1;
-        return launch_ad<ST, L, ANI, AccT>(p, plan, st);
+        return launch_ad<ST, L, ANI, AccT, TRI>(p, plan, st);
     }
-    if (plan.kind == kGemmDMA) return launch_dma<ST, L, MI, NI, AccT>(p, plan, st);
+    if (plan.kind == kGemmDMA) return launch_dma<ST, L, MI, NI, AccT, TRI>(p, plan, st);
     using Sh = GemmShape<L, MI, NI>;
-    auto kern = cross_gemm_kernel<ST, L, MI, NI, AccT>;
+    auto kern = cross_gemm_kernel<ST, L, MI, NI, AccT, TRI>;
     static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
     if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
     const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
@@ -2990,49 +3047,59 @@ static hipError_t launch_one(const GemmParams &p, const GemmPlan &plan, hipStrea
     return hipGetLastError();
 }
 
-template <typename ST, int L, typename AccT>
+template <typename ST, int L, typename AccT, bool TRI>
 static hipError_t launch_L(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     // (fp32 slices at L = 4: no hand-placed MFMA, so no K-step kernel)
     if constexpr (L <= 4 && !(L == 4 && std::is_same_v<ST, float>)) {
-        if (plan.kind == kGemmKStep) return launch_kstep<ST, L, AccT>(p, plan, st);
+        if (plan.kind == kGemmKStep) return launch_kstep<ST, L, AccT, TRI>(p, plan, st);
     }
     const int key = plan.mi * 10 + plan.ni;
     if constexpr (L == 1) {
         switch (key) {
-        case 24: return launch_one<ST, 1, 2, 4, AccT>(p, plan, st);
-        case 22: return launch_one<ST, 1, 2, 2, AccT>(p, plan, st);
-        case 12: return launch_one<ST, 1, 1, 2, AccT>(p, plan, st);
-        case 11: return launch_one<ST, 1, 1, 1, AccT>(p, plan, st);
+        case 24: return launch_one<ST, 1, 2, 4, AccT, TRI>(p, plan, st);
+        case 22: return launch_one<ST, 1, 2, 2, AccT, TRI>(p, plan, st);
+        case 12: return launch_one<ST, 1, 1, 2, AccT, TRI>(p, plan, st);
+        case 11: return launch_one<ST, 1, 1, 1, AccT, TRI>(p, plan, st);
         }
     } else if constexpr (L == 2) {
         switch (key) {
-        case 22: return launch_one<ST, 2, 2, 2, AccT>(p, plan, st);
-        case 12: return launch_one<ST, 2, 1, 2, AccT>(p, plan, st);
-        case 11: return launch_one<ST, 2, 1, 1, AccT>(p, plan, st);
+        case 22: return launch_one<ST, 2, 2, 2, AccT, TRI>(p, plan, st);
+        case 12: return launch_one<ST, 2, 1, 2, AccT, TRI>(p, plan, st);
+        case 11: return launch_one<ST, 2, 1, 1, AccT, TRI>(p, plan, st);
         }
     } else if constexpr (L <= 4) {
-        if (key == 11) return launch_one<ST, L, 1, 1, AccT>(p, plan, st);
-    } else {
-        if constexpr (L == 5) {
-            if (plan.kind == kGemmSolo5) return launch_solo5<ST, AccT>(p, plan, st);
-        }
+        if (key == 11) return launch_one<ST, L, 1, 1, AccT, TRI>(p, plan, st);
+    } else if constexpr (L == 5) {
+        if (plan.kind == kGemmSolo5) return launch_solo5<ST, AccT, TRI>(p, plan, st);
+        if constexpr (!TRI) return launch_chunks<ST, L, AccT>(p, plan, st);
+    } else if constexpr (!TRI) {
         return launch_chunks<ST, L, AccT>(p, plan, st);
     }
     return hipErrorInvalidValue;
 }
 
-template <typename ST, typename AccT>
+template <typename ST, typename AccT, bool TRI>
 static hipError_t launch_st(const GemmParams &p, const GemmPlan &plan, int L, hipStream_t st) {
     switch (L) {
-    case 1: return launch_L<ST, 1, AccT>(p, plan, st);
-    case 2: return launch_L<ST, 2, AccT>(p, plan, st);
-    case 3: return launch_L<ST, 3, AccT>(p, plan, st);
-    case 4: return launch_L<ST, 4, AccT>(p, plan, st);
-    case 5: return launch_L<ST, 5, AccT>(p, plan, st);
-    case 6: return launch_L<ST, 6, AccT>(p, plan, st);
-    case 7: return launch_L<ST, 7, AccT>(p, plan, st);
-    case 8: return launch_L<ST, 8, AccT>(p, plan, st);
+    case 1: return launch_L<ST, 1, AccT, false>(p, plan, st);   // one pair either way
+    case 2: return launch_L<ST, 2, AccT, TRI>(p, plan, st);
+    case 3: return launch_L<ST, 3, AccT, TRI>(p, plan, st);
+    case 4: return launch_L<ST, 4, AccT, TRI>(p, plan, st);
+    case 5: return launch_L<ST, 5, AccT, TRI>(p, plan, st);
+    case 6: return launch_L<ST, 6, AccT, TRI>(p, plan, st);
+    case 7: return launch_L<ST, 7, AccT, TRI>(p, plan, st);
+    case 8: return launch_L<ST, 8, AccT, TRI>(p, plan, st);
     }
     return hipErrorInvalidValue;
+}
+
+// the entry point of one slice dtype's unit (ozk_gemm_<dtype>.hip)
+template <typename ST>
+static hipError_t launch_typed(const GemmParams &p, const GemmPlan &plan, int L, hipStream_t st) {
+    const bool acc64 = p.out_dtype == 0;
+    if (p.tri) return acc64 ? launch_st<ST, double, true>(p, plan, L, st)
+                            : launch_st<ST, float, true>(p, plan, L, st);
+    return acc64 ? launch_st<ST, double, false>(p, plan, L, st)
+                 : launch_st<ST, float, false>(p, plan, L, st);
 }
 }  // namespace ozk

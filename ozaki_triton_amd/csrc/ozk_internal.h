@@ -111,6 +111,7 @@ struct GemmParams {
     int64_t batch, M, N, K;
     int out_dtype;              // C's dtype code: 0 f64 (fp64 outer accumulator), else
                                 // f32 / f16 / bf16 / i8 (fp32 outer accumulator)
+    int tri;                    // 1: sum only the pairs i + j <= L - 1 (OZK_PAIRS_TRIANGULAR)
     // split-K (ring and wide kernels): a tile's 128-byte K stages are cut into
     // ksplit ranges of kb_per_split stages, one workgroup each; ksplit <= 1:
     // none.  kpart holds the ranges' raw accumulators, kcount one arrival

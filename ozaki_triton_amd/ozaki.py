@@ -233,7 +233,18 @@ def _batch_strides(t: torch.Tensor, BN: int):
     return st
 
 
-def cross_gemm(A_slices, B_slices, A_scales, B_scales, num_splits, output_dtype):
+_PAIRS = {"all": 0, "triangular": 1}
+
+
+def _pair_code(pairs: str) -> int:
+    """OZK_PAIRS_* of a pair-set name ("all": the reference's sum)."""
+    if pairs not in _PAIRS:
+        raise ValueError(f"pairs must be 'all' or 'triangular', got {pairs!r}")
+    return _PAIRS[pairs]
+
+
+def cross_gemm(A_slices, B_slices, A_scales, B_scales, num_splits, output_dtype, *,
+               pairs: str = "all"):
     """
     C = sum_{i,j} scale_A_i * scale_B_j * (A_slice_i @ B_slice_j)
     Args:
@@ -244,6 +255,9 @@ def cross_gemm(A_slices, B_slices, A_scales, B_scales, num_splits, output_dtype)
         B_scales: (B, num_splits, N), float32 (a batch of 1 is broadcast)
         num_splits: number of slices
         output_dtype: dtype of C (the original input dtype)
+        pairs (keyword only, not in the reference): "all" (the reference's
+              sum) or "triangular", the pairs i + j <= num_splits - 1 only
+              (OZK_PAIRS_TRIANGULAR: 1 to 5 slices)
     Returns:
         C: (B, M, N), dtype=output_dtype
     """
@@ -256,12 +270,13 @@ def cross_gemm(A_slices, B_slices, A_scales, B_scales, num_splits, output_dtype)
     _require_supported(output_dtype, slice_dtype)
     if B_slices.dtype != slice_dtype:
         raise AssertionError(f"slice dtype mismatch: {slice_dtype} vs {B_slices.dtype}")
+    code = _pair_code(pairs)
     C = torch.empty((BN, M, N), dtype=output_dtype, device=A_slices.device)
-    _cross_gemm_into(A_slices, B_slices, A_scales, B_scales, num_splits, C)
+    _cross_gemm_into(A_slices, B_slices, A_scales, B_scales, num_splits, C, code)
     return C
 
 
-def _cross_gemm_into(A_slices, B_slices, A_scales, B_scales, num_splits, C) -> None:
+def _cross_gemm_into(A_slices, B_slices, A_scales, B_scales, num_splits, C, pairs=0) -> None:
     L = _lib.load()
     BN, _, M, K = A_slices.shape
     N = B_slices.shape[-1]
@@ -280,11 +295,11 @@ def _cross_gemm_into(A_slices, B_slices, A_scales, B_scales, num_splits, C) -> N
                                                 ctypes.byref(nbytes)))
     ws, wsp = _workspace(int(nbytes.value), C.device)
     with _on_device(C.device):
-        st = L.ozk_cross_gemm(ap, a_st, bp, b_st, ctypes.c_void_p(A_scales.data_ptr()), sa_st,
-                              ctypes.c_void_p(B_scales.data_ptr()), sb_st, BN, M, N, K,
-                              num_splits, sd, ctypes.c_void_p(C.data_ptr()), od, c_st, wsp,
-                              nbytes.value, _stream(C.device))
-    _lib.check("ozk_cross_gemm", st)
+        st = L.ozk_cross_gemm_pairs(ap, a_st, bp, b_st, ctypes.c_void_p(A_scales.data_ptr()),
+                                    sa_st, ctypes.c_void_p(B_scales.data_ptr()), sb_st, BN, M,
+                                    N, K, num_splits, sd, pairs, ctypes.c_void_p(C.data_ptr()),
+                                    od, c_st, wsp, nbytes.value, _stream(C.device))
+    _lib.check("ozk_cross_gemm_pairs", st)
     del ws
 
 
@@ -351,6 +366,7 @@ def ozaki_matmul(
     verbose: bool = False,
     *,
     max_splits: int = 4,
+    pairs: str = "all",
 ) -> torch.Tensor:
     """Ozaki-scheme C = A @ B (ozaki_triton.py:534-606); see _ozaki_matmul_impl.
 
@@ -358,13 +374,21 @@ def ozaki_matmul(
     limit of 4 slices (ozaki_triton.py:563) up to OZK_MAX_SPLITS (8): fp64
     accuracy needs 5 or more int8 slices.  5 int8 / fp16 / bf16 slices run in
     one cross-GEMM launch for any input dtype; 6 to 8 need fp64 inputs.
+
+    ``pairs`` (keyword only, not in the reference): "all", the reference's
+    sum over every slice pair, or "triangular", only the pairs i + j <=
+    num_splits - 1 (1 to 5 slices).  The pairs left out carry about
+    2^(-alpha (i + j)) of C, the size of the split's own truncation error:
+    with fp64 inputs 5 int8 slices on their 15 triangular pairs are as
+    accurate as on all 25, with fewer products than 4 slices on all 16.
     """
     if max_splits > _lib.OZK_MAX_SPLITS:
         raise ValueError(f"max_splits must be <= {_lib.OZK_MAX_SPLITS}, got {max_splits}")
-    return _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, None, max_splits)
+    return _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, None, max_splits, pairs)
 
 
-def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, events, max_splits=4):
+def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, events, max_splits=4,
+                       pairs="all"):
     """
     Ozaki-scheme matrix product C = A @ B with torch.matmul batch broadcasting.
 
@@ -394,6 +418,7 @@ def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, events, max_split
     assert A.dtype in _INPUT_DTYPES, f"unsupported input dtype: {A.dtype}"
     assert slice_dtype in _SLICE_DTYPE_INFO, f"unsupported slice dtype: {slice_dtype}"
     assert num_splits <= max_splits, f"num_splits must be <= {max_splits}, got {num_splits}"
+    pair_code = _pair_code(pairs)
 
     input_dtype = A.dtype
     dot_accum_dtype = _select_dot_accum_dtype(slice_dtype)
@@ -438,9 +463,10 @@ def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, events, max_split
     if events is not None:
         ev = (ctypes.c_void_p * 4)(*[ctypes.c_void_p(e.cuda_event) for e in events])
     with _on_device(dev):
-        st = L.ozk_matmul(ctypes.c_void_p(A3.data_ptr()), a_st, ctypes.c_void_p(B3.data_ptr()),
-                          b_st, xd, BN, M, N, K, num_splits, sd, ctypes.c_void_p(C.data_ptr()),
-                          _lib.i64arr(C.stride()), wsp, nbytes.value, ev, _stream(dev))
-    _lib.check("ozk_matmul", st)
+        st = L.ozk_matmul_pairs(ctypes.c_void_p(A3.data_ptr()), a_st,
+                                ctypes.c_void_p(B3.data_ptr()), b_st, xd, BN, M, N, K, num_splits,
+                                sd, pair_code, ctypes.c_void_p(C.data_ptr()),
+                                _lib.i64arr(C.stride()), wsp, nbytes.value, ev, _stream(dev))
+    _lib.check("ozk_matmul_pairs", st)
     del ws
     return C.view(out_shape)

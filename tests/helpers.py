@@ -95,15 +95,16 @@ def sample_indices(n, k, seed):
     return np.array(idx[:k] if len(idx) > k else idx)
 
 
-def check_block_vs_oracle(oracle, ozk, C_np, A_np, B_np, rows, cols, L, sdt, xdt, what):
+def check_block_vs_oracle(oracle, ozk, C_np, A_np, B_np, rows, cols, L, sdt, xdt, what,
+                          pairs="all"):
     """C_np[rows][:, cols] against the oracle's result for A_np[rows] and
-    B_np[:, cols] (one batch, full K)."""
+    B_np[:, cols] (one batch, full K), summed over the pair set `pairs`."""
     K = A_np.shape[-1]
     sd = NAME_OF[sdt]
     alpha = ozk.compute_split_bits(K, sdt, ozk._select_dot_accum_dtype(sdt))
     a_sl, a_sc = oracle.split(np.ascontiguousarray(A_np[rows]), L, alpha, sd)
     b_sl, b_sc = oracle.split(np.ascontiguousarray(B_np[:, cols].T), L, alpha, sd)
-    want = oracle.cross_gemm(a_sl, b_sl, a_sc, b_sc, NAME_OF[xdt])
+    want = oracle.cross_gemm(a_sl, b_sl, a_sc, b_sc, NAME_OF[xdt], pairs=pairs)
     got = np.ascontiguousarray(C_np[np.ix_(rows, cols)])
     if sdt == torch.int8:
         assert_bitwise_equal(got, want, what)

@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     assert _declared_symbols("ozaki_amd_debug.h") == sorted(_lib.EXPORTED_DEBUG)
     for name in _lib.EXPORTED + _lib.EXPORTED_DEBUG:
         assert hasattr(L, name), name
-    assert L.ozk_version() >= 200
+    assert L.ozk_version() >= 300
 
 
 def test_strerror_names_every_code():
@@ -602,3 +602,74 @@ def test_planner_kernel_choice():
     assert _gemm_kernel(L, 1, 4096, 4096, 4096, 5, _lib.OZK_BF16, 256) == "solo5"
     assert _gemm_kernel(L, 1, 1024, 1024, 1024, 5, _lib.OZK_F32, 256) == "pair"
     assert _gemm_kernel(L, 1, 1024, 1024, 1024, 6, I8, 256) == "pair"
+
+
+def _gemm_kernel_pairs(L, batch, M, N, K, nsp, sd, pairs, cus=256):
+    name = ctypes.c_char_p()
+    ks = ctypes.c_int(0)
+    st = L.ozk_debug_gemm_kernel_pairs(batch, M, N, K, nsp, sd, pairs, cus, ctypes.byref(name),
+                                       ctypes.byref(ks))
+    return (name.value.decode(), ks.value) if st == 0 else st
+
+
+def test_triangular_planner():
+    """The triangular pair set runs on the kernels that hold every pair of a
+    block in one wave: the K-step kernel on small grids as for all pairs, else
+    the wide kernel at 3 slices (split-K on small grids), the one-wave-per-SIMD
+    kernel at 5, the LDS-DMA kernel at 2 and 4; one slice plans as all pairs."""
+    from ozaki_triton_amd import _lib
+    L = _lib.load()
+    I8, F16, F32 = _lib.OZK_I8, _lib.OZK_F16, _lib.OZK_F32
+    T, A = _lib.OZK_PAIRS_TRIANGULAR, _lib.OZK_PAIRS_ALL
+    c3 = (1, 8192, 8192, 8192)
+    assert _gemm_kernel_pairs(L, *c3, 5, I8, T) == ("solo5", 1)
+    assert _gemm_kernel_pairs(L, *c3, 4, I8, T) == ("dma", 1)
+    assert _gemm_kernel_pairs(L, *c3, 4, I8, A) == ("wide4", 1)
+    assert _gemm_kernel_pairs(L, *c3, 3, I8, T) == ("wide", 1)
+    assert _gemm_kernel_pairs(L, *c3, 2, I8, T) == ("dma", 1)
+    assert _gemm_kernel_pairs(L, 1, 4096, 4096, 4096, 2, F16, T) == ("dma", 1)
+    assert _gemm_kernel_pairs(L, 1, 1024, 1024, 65536, 3, I8, T) == ("wide", 2)
+    ref_point = (1, 128, 2048, 4096)
+    for nsp in (2, 3, 4):
+        assert _gemm_kernel_pairs(L, *ref_point, nsp, I8, T) == ("kstep", 1)
+    assert _gemm_kernel_pairs(L, *ref_point, 4, F32, T) == ("dma", 1)
+    assert _gemm_kernel_pairs(L, *c3, 1, I8, T) == _gemm_kernel_pairs(L, *c3, 1, I8, A)
+    # no kernel sums the triangle over more than 5 slices; unknown sets
+    assert _gemm_kernel_pairs(L, *c3, 6, I8, T) == _lib.OZK_ERR_SPLITS
+    assert _gemm_kernel_pairs(L, *c3, 4, I8, 2) == _lib.OZK_ERR_SPLITS
+    assert _gemm_kernel_pairs(L, *c3, 4, I8, -1) == _lib.OZK_ERR_SPLITS
+
+
+def test_pair_set_arguments_rejected_before_enqueue():
+    """ozk_matmul_pairs / ozk_cross_gemm_pairs refuse an unknown set and the
+    triangular set beyond 5 slices (or 5 fp32 slices) before anything touches
+    a device: no pointer is read."""
+    from ozaki_triton_amd import _lib
+    L = _lib.load()
+    s3 = _lib.i64arr((0, 256, 1))
+    s4 = _lib.i64arr((0, 0, 256, 1))
+    for nsp, sd, pairs in [(6, _lib.OZK_I8, 1), (4, _lib.OZK_I8, 3), (5, _lib.OZK_F32, 1)]:
+        st = L.ozk_matmul_pairs(None, s3, None, s3, _lib.OZK_F64, 1, 64, 64, 256, nsp, sd, pairs,
+                                None, s3, None, 0, None, None)
+        assert st == _lib.OZK_ERR_SPLITS, (nsp, sd, pairs, st)
+    for nsp, pairs in [(6, 1), (4, 7)]:
+        st = L.ozk_cross_gemm_pairs(None, s4, None, s4, None, s3, None, s3, 1, 64, 64, 256, nsp,
+                                    _lib.OZK_I8, pairs, None, _lib.OZK_F64, s3, None, 0, None)
+        assert st == _lib.OZK_ERR_SPLITS, (nsp, pairs, st)
+
+
+def test_workspace_covers_both_pair_sets():
+    """The workspace queries take no pair set: their split-K part is the larger
+    of the two sets' plans.  At 64 x 96 x 8192 with 3 int8 slices all pairs
+    take the ring kernel with 4 ranges, the triangle the wide kernel with 4."""
+    from ozaki_triton_amd import _lib
+    L = _lib.load()
+    assert _gemm_kernel_pairs(L, 1, 64, 96, 8192, 3, _lib.OZK_I8, 0) == ("ring", 4)
+    assert _gemm_kernel_pairs(L, 1, 64, 96, 8192, 3, _lib.OZK_I8, 1) == ("wide", 4)
+    nb = ctypes.c_size_t(0)
+    st = L.ozk_matmul_workspace_bytes(_lib.OZK_F64, 1, 64, 96, 8192, _lib.i64arr((0, 8192, 1)),
+                                      _lib.i64arr((0, 96, 1)), 3, _lib.OZK_I8, ctypes.byref(nb))
+    assert st == 0
+    # wide split-K: 1 tile x 4 ranges x 8 waves x 144 registers x 64 lanes x 4 bytes
+    wide = 1 * 4 * 8 * 144 * 64 * 4
+    assert nb.value >= wide

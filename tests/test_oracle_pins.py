@@ -574,3 +574,102 @@ def test_int8_output_truncates_and_saturates(oracle, value, want):
     sb = np.array([[1.0]], dtype=np.float32)
     assert float(oracle.cross_gemm(A, B, sa, sb, "float32")[0, 0]) == pytest.approx(value, nan_ok=True)
     assert int(oracle.cross_gemm(A, B, sa, sb, "int8")[0, 0]) == want
+
+
+# --------------------------------------------------------------------------- #
+# the triangular pair set (not in the reference: OZK_PAIRS_TRIANGULAR sums only
+# the pairs i + j <= L - 1, in the reference's order)
+# --------------------------------------------------------------------------- #
+def _int8_terms(oracle, A, B, L):
+    """Slices of A and B^T and every t_ij = fl32(fl32(fl32(acc_ij) sa_i) sb_j),
+    acc_ij from numpy's exact int64 einsum (not the oracle's dot)."""
+    K = A.shape[1]
+    alpha = oracle.compute_split_bits(K, "int8", "int32")
+    a_sl, a_sc = oracle.split(A, L, alpha, "int8")
+    b_sl, b_sc = oracle.split(np.ascontiguousarray(B.T), L, alpha, "int8")
+    acc = np.einsum("imk,jnk->ijmn", a_sl.astype(np.int64), b_sl.astype(np.int64))
+    t = np.empty(acc.shape)
+    for i in range(L):
+        for j in range(L):
+            t1 = (acc[i, j].astype(np.float32) * a_sc[i][:, None]).astype(np.float32)
+            t[i, j] = (t1 * b_sc[j][None, :]).astype(np.float32)
+    return a_sl, a_sc, b_sl, b_sc, t
+
+
+@pytest.mark.parametrize("L", [2, 3, 4, 5])
+def test_triangular_is_full_sum_without_the_other_pairs(oracle, L):
+    """The triangular sum equals the pinned all-pairs sum minus the terms of
+    the pairs i + j >= L (numpy's own t_ij), to fp64 rounding of the two
+    orders; the set i + j <= L (one diagonal more) is far from it."""
+    rng = np.random.default_rng(70 + L)
+    A = rng.standard_normal((24, 512)) * 2.0 ** rng.integers(-8, 9, (24, 1))
+    B = rng.standard_normal((512, 20)) * 2.0 ** rng.integers(-8, 9, (1, 20))
+    a_sl, a_sc, b_sl, b_sc, t = _int8_terms(oracle, A, B, L)
+    full = oracle.cross_gemm(a_sl, b_sl, a_sc, b_sc, "float64")
+    tri = oracle.cross_gemm(a_sl, b_sl, a_sc, b_sc, "float64", pairs="triangular")
+    mag = np.abs(t).sum(axis=(0, 1))
+    tol = 4 * L * L * 2.0 ** -53 * mag
+    drop = lambda d: sum(t[i, j] for i in range(L) for j in range(L) if i + j >= d)
+    assert np.all(np.abs(tri - (full - drop(L))) <= tol)
+    assert np.abs(tri - (full - drop(L + 1))).max() > 1e3 * tol.max()
+
+
+@pytest.mark.parametrize("slice_dtype", ["float16", "bfloat16", "float32"])
+@pytest.mark.parametrize("L", [2, 3, 5])
+def test_triangular_float_cross_gemm_equals_numpy_when_exact(oracle, slice_dtype, L):
+    """Integer-valued slices and power-of-two scales (every step exact, so the
+    order does not matter): the triangular oracle equals numpy's float64
+    matmul summed over exactly the pairs i + j <= L - 1."""
+    import torch
+    from tests.helpers import int_valued_slices, values
+    g = torch.Generator().manual_seed(90 + L)
+    sdt = {"float16": torch.float16, "bfloat16": torch.bfloat16, "float32": torch.float32}[slice_dtype]
+    M, N, K = 24, 20, 4096
+    As, BsT, sa, sb = int_valued_slices(g, 1, L, M, N, K, sdt, exp_range=(0, 4))
+    to = {torch.bfloat16: lambda t: t.view(torch.int16).numpy().view(np.uint16)}.get(
+        sdt, lambda t: t.numpy())
+    a, b = to(As[0]), to(BsT[0])
+    s_a, s_b = sa[0].numpy(), sb[0].numpy()
+    got = oracle.cross_gemm(a, b, s_a, s_b, "float64", pairs="triangular")
+    want = np.zeros((M, N))
+    for i in range(L):
+        for j in range(L - i):
+            want += (values(a[i]) @ values(b[j]).T) * s_a[i][:, None] * s_b[j][None, :]
+    np.testing.assert_array_equal(got, want)
+
+
+def test_triangular_check_catches_a_dropped_or_added_pair(oracle):
+    """The GPU's bit-exact triangular check (integer-valued slices) fails for
+    a kernel that drops a kept pair or sums all pairs."""
+    import torch
+    from tests.helpers import bits, int_valued_slices
+    L = 4
+    g = torch.Generator().manual_seed(3)
+    As, BsT, sa, sb = int_valued_slices(g, 1, L, 32, 24, 1040, torch.float16)
+    a, b, s_a, s_b = As[0].numpy(), BsT[0].numpy(), sa[0].numpy(), sb[0].numpy()
+    tri = bits(oracle.cross_gemm(a, b, s_a, s_b, "float64", pairs="triangular"))
+    assert (bits(oracle.cross_gemm(a, b, s_a, s_b, "float64")) != tri).mean() > 0.9
+    for i in range(L):
+        for j in range(L - i):
+            dropped = bits(oracle.cross_gemm(a, b, s_a, s_b, "float64", skip_pair=i * L + j,
+                                             pairs="triangular"))
+            assert (dropped != tri).mean() > 0.9, (i, j)
+
+
+def test_triangular_accuracy_at_c3_like_data(oracle):
+    """The accuracy claim of the triangular set: fp64 inputs with per-row and
+    per-column exponents (C3's distribution), K = 8192, int8 slices.  5 slices
+    on 15 pairs stay within 5% of 5 slices on all 25 and below 1e-9; 4 slices
+    on 10 pairs are far better than 3 on all 9."""
+    rng = np.random.default_rng(2)
+    M = N = 64
+    K = 8192
+    A = rng.standard_normal((M, K)) * 2.0 ** rng.integers(-8, 9, (M, 1))
+    B = rng.standard_normal((K, N)) * 2.0 ** rng.integers(-8, 9, (1, N))
+    ref = A @ B
+    rel = lambda C: np.linalg.norm(C - ref) / np.linalg.norm(ref)
+    e = {(L, p): rel(oracle.ozaki_matmul(A, B, L, "int8", pairs=p))
+         for L, p in [(3, "all"), (4, "triangular"), (5, "all"), (5, "triangular")]}
+    assert e[(5, "triangular")] < 1e-9
+    assert e[(5, "triangular")] <= 1.05 * e[(5, "all")]
+    assert e[(4, "triangular")] < 0.1 * e[(3, "all")]
