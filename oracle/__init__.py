@@ -13,6 +13,8 @@ front end that mirrors the reference's Python structure:
 * ``split``               <- ozaki_triton.py:137-211 (kernel) and 214-256 (wrapper)
 * ``cross_gemm``          <- ozaki_triton.py:306-452 (kernel) and 455-498 (wrapper)
 * ``ozaki_matmul``        <- ozaki_triton.py:504-606 (broadcast + split B via B^T)
+* ``cross_gemm(..., pairs="triangular")``: not in the reference; the library's
+  OZK_PAIRS_TRIANGULAR, the same sum over the pairs i + j <= L - 1 only
 
 Pins (see tests/test_oracle_*.py): the exponent rule against numpy's float32
 log2 and the committed exhaustive band table; fp64->fp16 rounding against
@@ -21,8 +23,10 @@ torch's fp32->bf16; narrow inputs split as their exact fp32 values; fp32
 slices; the C casts to fp16 / bf16 / int8; split invariants (powers-of-two scales, int8 range, exact
 reconstruction of fp32 inputs, residual bounds); the int8 cross-GEMM against
 numpy's exact int64 matmul and against the fp64 product of the reconstructed
-operands; and the end-to-end relative errors the reference publishes in
-reference/test_results.csv for the same input distribution.
+operands; the triangular sum against the all-pairs sum minus numpy's dropped
+terms and against numpy on exact integer-valued slices; and the end-to-end
+relative errors the reference publishes in reference/test_results.csv for the
+same input distribution.
 """
 from __future__ import annotations
 
