@@ -315,8 +315,9 @@ static int cross_gemm_impl(const void *A_slices, const int64_t a_strides[4], con
     // partial sum between the i-row launches
     if (num_splits > 4) {
         const bool solo = plan.kind == ozk::kGemmSolo5;
-        const bool pair = plan.kind == ozk::kGemmPair && out_dtype == OZK_F64 &&
-                          slice_dtype != OZK_F32 && !p.tri;
+        // (the triangular set sums all its pairs in one launch, so any C)
+        const bool pair = plan.kind == ozk::kGemmPair && slice_dtype != OZK_F32 &&
+                          (out_dtype == OZK_F64 || p.tri);
         if (!solo && !pair) return OZK_ERR_SPLITS;
     }
     // split-K buffers after the packed operands, 256-byte aligned, when the
@@ -408,7 +409,7 @@ int matmul_layout(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
         gp.tri = pairs == OZK_PAIRS_TRIANGULAR;
         const int kind = ozk::plan_gemm(gp, L, sd, 256).kind;
         if (kind != ozk::kGemmSolo5 &&
-            !(kind == ozk::kGemmPair && dtype == OZK_F64 && !gp.tri))
+            !(kind == ozk::kGemmPair && (dtype == OZK_F64 || gp.tri)))
             return OZK_ERR_SPLITS;
     }
     o->bA = (batch > 1 && as[0] != 0) ? batch : 1;

@@ -191,28 +191,39 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
     const int force = debug_overrides().gemm;
     auto forced = [&](int kind) { return force == kind; };
     if (p.tri && L >= 2) {
-        // The triangular pair set runs on the kernels that hold every pair of
-        // a block in one wave: the K-step kernel where it runs by default,
-        // else the wide kernel at L = 3 (with split-K on small grids), the
-        // one-wave-per-SIMD kernel at L = 5, and the LDS-DMA kernel at L = 2
-        // and 4 (at L = 4 its 10 pairs of a 32 x 32 block take 160
-        // accumulator registers).  L > 5 has none (kGemmPair: the caller
-        // rejects it).
+        // The triangular pair set: the K-step kernel where it runs by
+        // default, else the wide kernel at L = 3 (with split-K on small
+        // grids), wide4 at L = 4 where its rounds rule holds, the LDS-DMA
+        // kernel at L = 2 and otherwise at L = 4 (its 10 pairs of a 32 x 32
+        // block take 160 accumulator registers), and at L = 5 the pair-split
+        // kernel over all i-rows: its two waves per SIMD overlap the stage
+        // DMA, which the one-wave-per-SIMD kernel serializes (measured,
+        // cross-GEMM alone, int8, pair / solo5: 8192^3 8.08 / 8.68 ms, 4096^2
+        // x 8192 2.05 / 2.43, 2048^2 x 8192 0.504 / 0.537, 1024^2 x 65536
+        // 1.05 / 1.26).  At L = 4 wide4 against the LDS-DMA kernel: 8192^3
+        // 5.88 / 6.54 ms, 4096^2 x 8192 1.47-1.64 / 1.66-1.81, 2048^2 x 8192
+        // 0.382 / 0.391, 1024^2 x 65536 1.05 / 0.80.  L > 5 has no kernel
+        // (the caller rejects it).
         plan.kind = !fits     ? kGemmStaged
                     : kstep   ? kGemmKStep
                     : L == 3  ? kGemmWide
+                    : wide4   ? kGemmWide4
                     : L <= 4  ? kGemmDMA
-                    : solo5   ? kGemmSolo5
                               : kGemmPair;
         if (L <= 4) {
             if (forced(kGemmStaged)) plan.kind = kGemmStaged;
             else if (fits && forced(kGemmAD)) plan.kind = kGemmAD;
             else if (fits && forced(kGemmDMA)) plan.kind = kGemmDMA;
+            else if (fits && forced(kGemmPair) && L >= 3) plan.kind = kGemmPair;
             else if (fits && forced(kGemmWide) && L == 3) plan.kind = kGemmWide;
+            else if (fits && forced(kGemmWide4) && L == 4) plan.kind = kGemmWide4;
             else if (fits && forced(kGemmKStep) && !(L == 4 && slice_dtype == 1))
                 plan.kind = kGemmKStep;
+        } else if (fits && forced(kGemmSolo5) && solo5) {
+            plan.kind = kGemmSolo5;
         }
         if (plan.kind == kGemmAD) plan.group_m = 2;
+        if (plan.kind == kGemmWide4) plan.group_m = 4;
         plan.kb_per_split = nkb_all;
         if (plan.kind == kGemmWide) {
             const int fk = debug_overrides().ksplit;

@@ -1021,13 +1021,20 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_kstep_kernel(GemmParams p, 
 // fragment reads per K step) and group 1 those of row 2 (3 MFMAs from 4
 // reads): about 6% faster on the fp16 broadcast-batch shape than the 5 / 4
 // split, whose group 1 needs A fragments of two i-rows for 4 MFMAs.
-template <int L, int R> struct PairSplit {
-    static constexpr int P = R * L;
-    static constexpr int P0 = (L == 3 && R == 3) ? 6 : (P + 1) / 2;
+// With the triangular pair set (TRI, all i-rows in one launch: R = L) the
+// order is that of the kept pairs; at num_splits 5 group 0 takes (0, 0..4)
+// and (1, 0..2), group 1 the other 7.
+template <int L, int R, bool TRI = false> struct PairSplit {
+    static_assert(!TRI || R == L, "the triangular set runs all i-rows in one launch");
+    static constexpr int P = TRI ? Pairs<L, true>::N : R * L;
+    static constexpr int P0 = (L == 3 && R == 3 && !TRI) ? 6 : (P + 1) / 2;
     static constexpr int first(int g) { return g ? P0 : 0; }
     static constexpr int count(int g) { return g ? P - P0 : P0; }
-    static constexpr int ilo(int g) { return first(g) / L; }
-    static constexpr int na(int g) { return (first(g) + count(g) - 1) / L - ilo(g) + 1; }
+    // slice pair n of the launch's order (i relative to its first i-row)
+    static constexpr int i_of(int n) { return TRI ? Pairs<L, true>::i_of(n) : n / L; }
+    static constexpr int j_of(int n) { return TRI ? Pairs<L, true>::j_of(n) : n % L; }
+    static constexpr int ilo(int g) { return i_of(first(g)); }
+    static constexpr int na(int g) { return i_of(first(g) + count(g) - 1) - ilo(g) + 1; }
 };
 
 template <int L, int R> struct PairShape {
@@ -1041,13 +1048,13 @@ template <int L, int R> struct PairShape {
     static_assert(LDS_BYTES <= 160 * 1024, "LDS");
 };
 
-template <typename ST, int L, typename AccT, int R>
+template <typename ST, int L, typename AccT, int R, bool TRI>
 __global__ __launch_bounds__(512, 1) void cross_gemm_pair_kernel(GemmParams p, int group_m,
                                                                  uint32_t a_records,
                                                                  uint32_t b_records, int i0,
                                                                  int cont) {
     using Sh = PairShape<L, R>;
-    using PS = PairSplit<L, R>;
+    using PS = PairSplit<L, R, TRI>;
     using MF = Mfma<ST>;
     using Acc = typename MF::Acc;
     using OA = AccT;   // outer accumulator: fp64 for fp64 output, else fp32 (store_c)
@@ -1172,13 +1179,13 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_pair_kernel(GemmParams p, i
         };
         // MFMAs of `cur` with the next step's reads into `nxt` interleaved
         auto step = [&](const Frags &cur, Frags &nxt, const char *nbuf, int nkk) {
-#pragma unroll
-            for (int q = 0; q < NP; ++q) {
-                const int i = (F + q) / L, j = (F + q) % L;
+            static_for<NP>([&](auto q_) {
+                constexpr int q = decltype(q_)::value;
+                constexpr int i = PS::i_of(F + q), j = PS::j_of(F + q);
                 acc[q] = MF::run(cur.a[i - ILO], cur.b[j], acc[q]);
-                if (q < kReads) read_one(nbuf, nkk, q, nxt);
+                if constexpr (q < kReads) read_one(nbuf, nkk, q, nxt);
                 __builtin_amdgcn_sched_barrier(0);
-            }
+            });
 #pragma unroll
             for (int q = NP; q < kReads; ++q) read_one(nbuf, nkk, q, nxt);
         };
@@ -1243,13 +1250,13 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_pair_kernel(GemmParams p, i
 #pragma unroll
             for (int i = 0; i < NA; ++i)
                 sai[i] = ok ? sab[(int64_t)(i0 + ILO + i) * p.sas_l + row * p.sas_m] : 0.0f;
-#pragma unroll
-            for (int q = 0; q < NP; ++q) {
-                const int i = (F + q) / L, j = (F + q) % L;
+            static_for<NP>([&](auto q_) {
+                constexpr int q = decltype(q_)::value;
+                constexpr int i = PS::i_of(F + q), j = PS::j_of(F + q);
                 const float x = MF::to_f32(acc[q][r]);
                 const float t1 = x * sai[i - ILO];
                 tv[q][r] = t1 * sbv[j];
-            }
+            });
         }
         if constexpr (G == 0) {
 #pragma unroll
@@ -1987,6 +1994,10 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide_kernel(GemmParams p, i
 // The LDS holds two whole stages (160 KB); stage kb + 2 is fetched into stage
 // kb's buffer after the barrier of stage kb, P1 instructions per wave in the
 // K step after that barrier and the rest in the next.
+// With the triangular pair set (TRI: i + j <= 3) a wave of the first kind
+// keeps 9 of its 12 pairs and one of the second kind the pair (3, 0) of its 3
+// blocks; the others' MFMAs and terms are left out (a wave-uniform branch on
+// the wave's kind where the two kinds differ).
 // ---------------------------------------------------------------------------
 struct Wide4Shape {
     static constexpr int L = 4;
@@ -2009,7 +2020,7 @@ struct Wide4Shape {
     static_assert(kDmaRB == 128, "128-byte stage rows");
 };
 
-template <typename ST, typename AccT>
+template <typename ST, typename AccT, bool TRI>
 __global__ __launch_bounds__(512, 1) void cross_gemm_wide4_kernel(GemmParams p, int group_m,
                                                                   uint32_t a_records,
                                                                   uint32_t b_records) {
@@ -2185,7 +2196,12 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide4_kernel(GemmParams p, 
 #pragma unroll
         for (int n = 0; n < 3 * L; ++n) {
             const int j = n / 3, u = n % 3;
-            acc[u][j] = MF::run(cur.a[u], fb[j], acc[u][j]);
+            // the pair (u, j) in a wave of the first kind, (3, j) in one of the second
+            const bool first = !TRI || u + j <= L - 1, second = !TRI || j == 0;
+            if (first && second) acc[u][j] = MF::run(cur.a[u], fb[j], acc[u][j]);
+            else if (first || second) {
+                if (first != last_i) acc[u][j] = MF::run(cur.a[u], fb[j], acc[u][j]);
+            }
             if (u == 2) read_b(rkb, nkk, j);
 #pragma unroll
             for (int d = 0; d < Sh::P1; ++d) {
@@ -2253,7 +2269,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide4_kernel(GemmParams p, 
 #pragma unroll
             for (int q = 0; q < 4; ++q) s4[q] = sa4(3, u, q);
 #pragma unroll
-            for (int j = 0; j < L; ++j) {
+            for (int j = 0; j < (TRI ? 1 : L); ++j) {
                 f32x16 tv;
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
@@ -2283,6 +2299,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide4_kernel(GemmParams p, 
                 for (int i = 0; i < 3; ++i)
 #pragma unroll
                     for (int j = 0; j < L; ++j) {
+                        if (TRI && i + j > L - 1) continue;
                         // fl32(fl32(fl32(acc) * sa_i) * sb_j), summed i-major, j-minor
                         const float t1 = MF::to_f32(acc[i][j][r]) * s4[i][e];
                         out = out + (OA)(t1 * sbv[j]);
@@ -2305,7 +2322,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide4_kernel(GemmParams p, 
                 const int64_t row = m0 + row4(u, r >> 2) + (r & 3);
                 OA out = part[((u * 2 + wy) * 16 + r) * 64 + lane];
 #pragma unroll
-                for (int j = 0; j < L; ++j) out = out + (OA)tv[j][r];
+                for (int j = 0; j < (TRI ? 1 : L); ++j) out = out + (OA)tv[j][r];
                 if (col < p.N && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
             }
         }
@@ -2901,11 +2918,11 @@ static hipError_t launch_ad(const GemmParams &p, const GemmPlan &plan, hipStream
     return hipGetLastError();
 }
 
-template <typename ST, int L, typename AccT, int R>
+template <typename ST, int L, typename AccT, int R, bool TRI = false>
 static hipError_t launch_pair(const GemmParams &p, const GemmPlan &plan, hipStream_t st, int i0,
                               int cont) {
     using Sh = PairShape<L, R>;
-    auto kern = cross_gemm_pair_kernel<ST, L, AccT, R>;
+    auto kern = cross_gemm_pair_kernel<ST, L, AccT, R, TRI>;
     static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
     if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
     const int es = (int)sizeof(ST);
@@ -2953,10 +2970,10 @@ static hipError_t launch_wide(const GemmParams &p, const GemmPlan &plan, hipStre
     return hipGetLastError();
 }
 
-template <typename ST, typename AccT>
+template <typename ST, typename AccT, bool TRI>
 static hipError_t launch_wide4(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     using Sh = Wide4Shape;
-    auto kern = cross_gemm_wide4_kernel<ST, AccT>;
+    auto kern = cross_gemm_wide4_kernel<ST, AccT, TRI>;
     static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
     if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
     const int es = (int)sizeof(ST);
@@ -3009,24 +3026,27 @@ static hipError_t launch_chunks(const GemmParams &p, const GemmPlan &plan, hipSt
 }
 
 // TRI: the triangular pair set, which the kernels that hold every pair of a
-// block in one wave sum (staged, dma, ad, kstep, wide, solo5); the pair-split
-// kernels (pair, ring, wide4) are not instantiated for it, and the planner
-// does not choose them.
+// block in one wave sum (staged, dma, ad, kstep, wide, solo5), wide4 and the
+// pair-split kernel over all i-rows in one launch (L = 3..5); the ring kernel
+// is not instantiated for it, and the planner does not choose it.
 template <typename ST, int L, int MI, int NI, typename AccT, bool TRI>
 static hipError_t launch_one(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     if constexpr (!TRI) {
         if constexpr (L >= 3) {
             if (plan.kind == kGemmPair) return launch_pair<ST, L, AccT, L>(p, plan, st, 0, 0);
         }
-        if constexpr (L == 4) {
-            if (plan.kind == kGemmWide4) return launch_wide4<ST, AccT>(p, plan, st);
-        }
         if constexpr (L >= 2 && L <= 4) {
             if (plan.kind == kGemmRing) return launch_ring<ST, L, AccT>(p, plan, st);
         }
     } else {
-        if (plan.kind == kGemmPair || plan.kind == kGemmWide4 || plan.kind == kGemmRing)
-            return hipErrorInvalidValue;
+        if constexpr (L >= 3) {
+            // one launch over the kept pairs of all i-rows
+            if (plan.kind == kGemmPair) return launch_pair<ST, L, AccT, L, true>(p, plan, st, 0, 0);
+        }
+        if (plan.kind == kGemmPair || plan.kind == kGemmRing) return hipErrorInvalidValue;
+    }
+    if constexpr (L == 4) {
+        if (plan.kind == kGemmWide4) return launch_wide4<ST, AccT, TRI>(p, plan, st);
     }
     if constexpr (L == 3) {
         if (plan.kind == kGemmWide) return launch_wide<ST, AccT, TRI>(p, plan, st);
@@ -3072,6 +3092,9 @@ static hipError_t launch_L(const GemmParams &p, const GemmPlan &plan, hipStream_
     } else if constexpr (L == 5) {
         if (plan.kind == kGemmSolo5) return launch_solo5<ST, AccT, TRI>(p, plan, st);
         if constexpr (!TRI) return launch_chunks<ST, L, AccT>(p, plan, st);
+        // the 15 kept pairs split 8 / 7 over the wave groups: one launch
+        else if (plan.kind == kGemmPair && !std::is_same_v<ST, float>)
+            return launch_pair<ST, 5, AccT, 5, true>(p, plan, st, 0, 0);
     } else if constexpr (!TRI) {
         return launch_chunks<ST, L, AccT>(p, plan, st);
     }
