@@ -144,13 +144,15 @@ def _require_supported(input_dtype: torch.dtype, slice_dtype: torch.dtype) -> No
             "slices: float32, float16, bfloat16, int8)")
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(dev: torch.device) -> ctypes.c_void_p:
     """dev's current stream as a raw pointer (torch's direct accessor where it
     has one: the Stream object costs microseconds per call)."""
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
-    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
-    if raw is not None:
-        return ctypes.c_void_p(raw(idx))
+    if _RAW_STREAM is not None:
+        return ctypes.c_void_p(_RAW_STREAM(idx))
     return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 
 
@@ -387,6 +389,43 @@ def ozaki_matmul(
     return _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, None, max_splits, pairs)
 
 
+# Calls that passed every check of _ozaki_matmul_impl, keyed by what those
+# checks and the launch arguments depend on: the operands' shapes, strides,
+# dtypes and devices, num_splits, the slice dtype, max_splits and the pair
+# set.  A repeated call with the same key goes straight to the workspace
+# query, the allocations and the C call (host time of a small call: 25 -> 13
+# us).  Only calls whose operands are read in place are kept (their strides
+# are the cached ones).  The workspace is asked each call: its size depends
+# on the library's test hooks too.
+_CALLS: dict = {}
+_CALLS_MAX = 256
+
+
+def _matmul_cached(hit, A, B, events):
+    xd, sd, pc, BN, M, N, K, L, a_st, b_st, c_st, c_shape, out_shape = hit
+    dev = A.device
+    lib = _lib.load()
+    nb = ctypes.c_size_t(0)
+    _lib.check("ozk_matmul_workspace_bytes",
+               lib.ozk_matmul_workspace_bytes(xd, BN, M, N, K, a_st, b_st, L, sd, ctypes.byref(nb)))
+    nbytes = nb.value
+    C = torch.empty(c_shape, dtype=A.dtype, device=dev)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes else None
+    ev = None
+    if events is not None:
+        ev = (ctypes.c_void_p * 4)(*[ctypes.c_void_p(e.cuda_event) for e in events])
+    args = (A.data_ptr(), a_st, B.data_ptr(), b_st, xd, BN, M, N, K, L, sd, pc, C.data_ptr(),
+            c_st, ws.data_ptr() if ws is not None else None, nbytes, ev)
+    if dev.index is None or dev.index == torch.cuda.current_device():
+        st = lib.ozk_matmul_pairs(*args, _stream(dev))
+    else:
+        with torch.cuda.device(dev):
+            st = lib.ozk_matmul_pairs(*args, _stream(dev))
+    _lib.check("ozk_matmul_pairs", st)
+    del ws
+    return C.view(out_shape)
+
+
 def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, events, max_splits=4,
                        pairs="all"):
     """
@@ -414,6 +453,16 @@ def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, events, max_split
     ``max_splits`` is the reference's limit of 4 (ozaki_triton.py:563) unless
     the caller raises it, up to the C ABI's OZK_MAX_SPLITS (8).
     """
+    key = None
+    if not verbose and type(A) is torch.Tensor and type(B) is torch.Tensor:
+        key = (A.shape, A.stride(), A.dtype, A.device, B.shape, B.stride(), B.dtype, B.device,
+               num_splits, slice_dtype, max_splits, pairs)
+        try:
+            hit = _CALLS.get(key)
+        except TypeError:   # an unhashable argument: the checks below report it
+            key = hit = None
+        if hit is not None:
+            return _matmul_cached(hit, A, B, events)
     assert A.dtype == B.dtype, f"A/B dtype mismatch: {A.dtype} vs {B.dtype}"
     assert A.dtype in _INPUT_DTYPES, f"unsupported input dtype: {A.dtype}"
     assert slice_dtype in _SLICE_DTYPE_INFO, f"unsupported slice dtype: {slice_dtype}"
@@ -462,11 +511,17 @@ def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, events, max_split
     ev = None
     if events is not None:
         ev = (ctypes.c_void_p * 4)(*[ctypes.c_void_p(e.cuda_event) for e in events])
+    c_st = _lib.i64arr(C.stride())
     with _on_device(dev):
         st = L.ozk_matmul_pairs(ctypes.c_void_p(A3.data_ptr()), a_st,
                                 ctypes.c_void_p(B3.data_ptr()), b_st, xd, BN, M, N, K, num_splits,
-                                sd, pair_code, ctypes.c_void_p(C.data_ptr()),
-                                _lib.i64arr(C.stride()), wsp, nbytes.value, ev, _stream(dev))
+                                sd, pair_code, ctypes.c_void_p(C.data_ptr()), c_st, wsp,
+                                nbytes.value, ev, _stream(dev))
     _lib.check("ozk_matmul_pairs", st)
     del ws
+    if key is not None and A3.data_ptr() == A.data_ptr() and B3.data_ptr() == B.data_ptr():
+        if len(_CALLS) >= _CALLS_MAX:
+            _CALLS.clear()
+        _CALLS[key] = (xd, sd, pair_code, BN, M, N, K, num_splits, a_st, b_st, c_st, (BN, M, N),
+                       out_shape)
     return C.view(out_shape)

@@ -1405,3 +1405,38 @@ def test_unaligned_operands(oracle, gpu, xdt, off, K):
     torch.cuda.synchronize()
     want = oracle.ozaki_matmul(to_np(A), to_np(B), L, "int8")
     assert_bitwise_equal(to_np(C), want, f"unaligned {xdt} +{off} K{K}")
+
+
+def test_repeated_call_fast_path(oracle, gpu):
+    """A repeated ozaki_matmul with the same shapes, strides and dtypes skips the
+    Python checks (ozaki._CALLS): the second call, on other data, is still
+    bit-exact; other strides (a transposed B) get their own entry; an operand
+    that needs a copy (neither of its last two dims contiguous) is not cached;
+    the phase events work on a cached call."""
+    import ozaki_triton_amd as ozk
+    from ozaki_triton_amd import ozaki as oz
+    from tests.helpers import c3_like
+    oz._CALLS.clear()
+    A1, B1 = c3_like((2, 96, 1040), (1040, 72), 31)
+    A2, B2 = c3_like((2, 96, 1040), (1040, 72), 32)
+    for A, B in ((A1, B1), (A2, B2)):
+        C = ozk.ozaki_matmul(A.to(gpu), B.to(gpu), 3, torch.int8)
+        assert_bitwise_equal(to_np(C), oracle.ozaki_matmul(to_np(A), to_np(B), 3, "int8"), "cached")
+    assert len(oz._CALLS) == 1
+    Bt = B2.T.contiguous().to(gpu).T          # column-major B: other strides
+    C = ozk.ozaki_matmul(A2.to(gpu), Bt, 3, torch.int8)
+    assert_bitwise_equal(to_np(C), oracle.ozaki_matmul(to_np(A2), to_np(B2), 3, "int8"), "B^T")
+    assert len(oz._CALLS) == 2
+    As = A2.to(gpu).repeat_interleave(2, dim=-1)[..., ::2]   # strided in both last dims
+    C = ozk.ozaki_matmul(As, B2.to(gpu), 3, torch.int8)
+    assert_bitwise_equal(to_np(C), oracle.ozaki_matmul(to_np(A2), to_np(B2), 3, "int8"), "copy")
+    assert len(oz._CALLS) == 2
+    from ozaki_triton_amd.ozaki import _ozaki_matmul_impl
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    for e in evs:   # torch creates an event at its first record
+        e.record()
+    Ad, Bd = A1.to(gpu), B1.to(gpu)
+    C = _ozaki_matmul_impl(Ad, Bd, 3, torch.int8, False, evs)
+    torch.cuda.synchronize()
+    assert evs[0].elapsed_time(evs[3]) > 0
+    assert_bitwise_equal(to_np(C), oracle.ozaki_matmul(to_np(A1), to_np(B1), 3, "int8"), "events")
