@@ -14,7 +14,8 @@
 //   the outer sum runs i-major, j-minor from +0 in the output's accumulator
 //   dtype (fp64 for fp64 output, fp32 for every other output dtype), exactly as
 //   the reference; kernels are templated on the slice type (int8, fp16, bf16,
-//   fp32) and that accumulator type, and store_c converts to C's dtype.
+//   fp32), that accumulator type and the pair set (all pairs, or with TRI the
+//   triangle i + j <= L - 1: Pairs below), and store_c converts to C's dtype.
 //
 // Design (one workgroup = 256 lanes = 4 waves in a 2 x 2 grid):
 //   * Every wave owns a (32*MI) x (32*NI) block of C and ALL L*L slice pairs
@@ -723,9 +724,9 @@ template <bool AG> struct HandMfma<__bf16, AG> {
 //     in 16-byte pieces, groups of up to 4 pairs at a time, one pair per
 //     wave; that wave turns the sum into t_ij = fl32(fl32(fl32(acc) * sa_i) *
 //     sb_j) in the LDS.  Then each wave sums, for a quarter of the tile, the
-//     t values of all pairs in the i-major / j-minor order from +0
-//     (ozaki_triton.py:420-452) and stores C.  The tile's scales are loaded
-//     at kernel start.
+//     t values of the pairs (all L^2, or the triangular set) in the i-major /
+//     j-minor order from +0 (ozaki_triton.py:420-452) and stores C.  The
+//     tile's scales are loaded at kernel start.
 // ---------------------------------------------------------------------------
 template <int L, bool TRI> struct KStepShape {
     static constexpr int BM = 32, BN = 32;
