@@ -624,7 +624,7 @@ const Named kGemmNames[] = {{"staged", ozk::kGemmStaged}, {"dma", ozk::kGemmDMA}
                             {"ad", ozk::kGemmAD},         {"pair", ozk::kGemmPair},
                             {"ring", ozk::kGemmRing},     {"wide", ozk::kGemmWide},
                             {"wide4", ozk::kGemmWide4},   {"solo5", ozk::kGemmSolo5},
-                            {"kstep", ozk::kGemmKStep}};
+                            {"kstep", ozk::kGemmKStep},   {"kstep2", ozk::kGemmKStep2}};
 const Named kSplitNames[] = {{"coop", ozk::kForceSplitCoop},
                              {"strip", ozk::kForceSplitStrip},
                              {"transpose", ozk::kForceSplitTranspose},

@@ -188,6 +188,11 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
                 : L <= 4           ? kGemmRing
                 : solo5            ? kGemmSolo5
                                    : kGemmPair;
+    // two slices or more: the K-step kernel's 8-wave form, two pair groups
+    // whose waves share the SIMDs (the same bits; cross-GEMM alone at
+    // (1, 128, 2048, 4096) and 256^2 x 4096, int8 and fp16, 2-4 slices:
+    // 3-9% faster)
+    if (plan.kind == kGemmKStep && L >= 2) plan.kind = kGemmKStep2;
     const int force = debug_overrides().gemm;
     auto forced = [&](int kind) { return force == kind; };
     if (p.tri && L >= 2) {
@@ -205,7 +210,7 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
         // 0.382 / 0.391, 1024^2 x 65536 1.05 / 0.80.  L > 5 has no kernel
         // (the caller rejects it).
         plan.kind = !fits     ? kGemmStaged
-                    : kstep   ? kGemmKStep
+                    : kstep   ? kGemmKStep2
                     : L == 3  ? kGemmWide
                     : wide4   ? kGemmWide4
                     : L <= 4  ? kGemmDMA
@@ -219,6 +224,7 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
             else if (fits && forced(kGemmWide4) && L == 4) plan.kind = kGemmWide4;
             else if (fits && forced(kGemmKStep) && !(L == 4 && slice_dtype == 1))
                 plan.kind = kGemmKStep;
+            else if (fits && forced(kGemmKStep2) && L >= 2) plan.kind = kGemmKStep2;
         } else if (fits && forced(kGemmSolo5) && solo5) {
             plan.kind = kGemmSolo5;
         }
@@ -250,6 +256,7 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
     else if (fits && forced(kGemmWide)) plan.kind = L == 3 ? kGemmWide : plan.kind;
     else if (fits && forced(kGemmWide4)) plan.kind = L == 4 ? kGemmWide4 : plan.kind;
     else if (fits && forced(kGemmKStep)) plan.kind = (L == 4 && slice_dtype == 1) ? plan.kind : kGemmKStep;
+    else if (fits && forced(kGemmKStep2) && L >= 2) plan.kind = kGemmKStep2;
     if (plan.kind == kGemmAD) plan.group_m = 2;
     // 96 x 64 tiles: groups of 4 tile rows (C3: 7.12-7.16 ms against 7.21-7.23
     // with 8, 7.33-7.35 with 16; cross-GEMM alone, one box)

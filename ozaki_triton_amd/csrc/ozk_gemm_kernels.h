@@ -728,31 +728,55 @@ template <bool AG> struct HandMfma<__bf16, AG> {
 //     j-minor order from +0 (ozaki_triton.py:420-452) and stores C.  The
 //     tile's scales are loaded at kernel start.
 // ---------------------------------------------------------------------------
-template <int L, bool TRI> struct KStepShape {
+template <int L, bool TRI, int G = 1> struct KStepShape {
     static constexpr int BM = 32, BN = 32;
+    static constexpr int NW = 4 * G;                          // waves: K step (w & 3), pair group (w >> 2)
     static constexpr int ROWS = 2 * L * 32;                   // A rows then B rows
     static constexpr int STAGE = ROWS * kDmaRB;
-    static constexpr int LPS = STAGE / (4 * 1024);            // DMA instructions per wave per stage
+    static constexpr int LPS = STAGE / (NW * 1024);           // DMA instructions per wave per stage
     static constexpr int NST = (160 * 1024 / STAGE) < 6 ? (160 * 1024 / STAGE) : 6;
     static constexpr int NP = Pairs<L, TRI>::N;               // slice pairs summed
-    static constexpr int PR = NP < 4 ? NP : 4;                // pairs per epilogue group
+    static constexpr int P0 = (NP + G - 1) / G;               // pairs of group 0
+    static constexpr int first(int g) { return g ? P0 : 0; }
+    static constexpr int count(int g) { return g ? NP - P0 : P0; }
+    static constexpr int PR = G == 1 ? (NP < 4 ? NP : 4) : 2; // pairs per epilogue round and group
+    static constexpr int NG = (P0 + PR - 1) / PR;             // epilogue rounds
     static constexpr int T_BYTES = NP * 16 * 64 * 4;          // t values [pair][reg / 4][lane][4]
-    static constexpr int R_BYTES = 4 * PR * 16 * 64 * 4;      // [wave][pair][reg / 4][lane][4]
+    static constexpr int R_BYTES = NW * PR * 16 * 64 * 4;     // [wave][pair][reg / 4][lane][4]
     static constexpr int S_BYTES = 2 * L * 32 * 4;            // sa [L][32], sb [L][32]
     static constexpr int EPI_BYTES = T_BYTES + R_BYTES + S_BYTES;
     static constexpr int LDS_BYTES = NST * STAGE > EPI_BYTES ? NST * STAGE : EPI_BYTES;
-    static constexpr bool kHand = L == 4;   // accumulators in AGPRs, hand-placed MFMAs
-    static_assert(STAGE % 4096 == 0, "a stage is whole 1 KB windows per wave");
+    static constexpr bool kHand = L == 4 && G == 1;   // accumulators in AGPRs, hand-placed MFMAs
+    static_assert(G == 1 || (G == 2 && NP >= 2), "two pair groups need two pairs");
+    static_assert(STAGE % (NW * 1024) == 0, "a stage is whole 1 KB windows per wave");
     static_assert(NST >= 3, "stages in flight");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS");
     static_assert(kDmaRB == 128 && L * 32 <= 128, "four K steps per stage; scales one per lane");
 };
+// The slices a K-step pair group reads: A slices [ilo, ilo + na), B slices
+// [jlo, jlo + nb) of its pairs [f, f + c) of the pair order.
+template <int L, bool TRI> struct KStepGroup {
+    using PS = Pairs<L, TRI>;
+    static constexpr int ilo(int f, int c) { return PS::i_of(f); }
+    static constexpr int na(int f, int c) { return PS::i_of(f + c - 1) - PS::i_of(f) + 1; }
+    static constexpr int jlo(int f, int c) {
+        int m = L;
+        for (int n = f; n < f + c; ++n) m = PS::j_of(n) < m ? PS::j_of(n) : m;
+        return m;
+    }
+    static constexpr int nb(int f, int c) {
+        int m = 0;
+        for (int n = f; n < f + c; ++n) m = PS::j_of(n) > m ? PS::j_of(n) : m;
+        return m - jlo(f, c) + 1;
+    }
+};
 
-template <typename ST, int L, typename AccT, bool TRI>
-__global__ __launch_bounds__(256, 1) void cross_gemm_kstep_kernel(GemmParams p, int group_m,
-                                                                  uint32_t a_records,
-                                                                  uint32_t b_records) {
-    using Sh = KStepShape<L, TRI>;
+template <typename ST, int L, typename AccT, bool TRI, int G>
+__global__ __launch_bounds__(256 * G, 1) void cross_gemm_kstep_kernel(GemmParams p, int group_m,
+                                                                      uint32_t a_records,
+                                                                      uint32_t b_records) {
+    using Sh = KStepShape<L, TRI, G>;
+    using KG = KStepGroup<L, TRI>;
     using PS = Pairs<L, TRI>;
     using MF = Mfma<ST>;
     using Acc = typename MF::Acc;
@@ -766,6 +790,7 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_kstep_kernel(GemmParams p, 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ks = wave & 3, grp = wave >> 2;   // K step of every stage, pair group
     const int h = lane >> 5, lr = lane & 31;
 
     const int64_t tiles_m = (p.M + BM - 1) / BM;
@@ -790,7 +815,7 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_kstep_kernel(GemmParams p, 
     float scl = 0.0f;
     {
         const int e = tid & 127, s = e / 32, o = e % 32;
-        if (e < L * 32) {
+        if (e < L * 32 && tid < 256) {
             if (tid < 128) {
                 if (m0 + o < p.M) scl = p.sa[bidx * p.sas_b + s * p.sas_l + (m0 + o) * p.sas_m];
             } else if (n0 + o < p.N) {
@@ -851,143 +876,163 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_kstep_kernel(GemmParams p, 
         exec_barrier();
     };
 
-    Acc acc[L][L];
-#pragma unroll
-    for (int i = 0; i < L; ++i)
-#pragma unroll
-        for (int j = 0; j < L; ++j) acc[i][j] = MF::zero();
-    // At L = 4 the 16 accumulator tiles (256 registers) live in the AGPRs,
-    // through hand-placed MFMAs (left to the compiler, the K loop spills).
-    // The compiler's hazard recogniser does not see into inline assembly: the
-    // zeroed tiles are pinned here, 8 wait states before any MFMA reads them.
-    constexpr bool kHand = Sh::kHand;
-    if constexpr (kHand) {
-        static_for<PS::N>([&](auto n_) {
-            constexpr int n = decltype(n_)::value;
-            (void)acc;   // an ordinary use, so that the capture does not hinge on the asm operand
-            asm volatile("" : "+a"(acc[PS::i_of(n)][PS::j_of(n)]));
-        });
-        asm volatile("s_nop 7" ::: "memory");
-    }
-
-    struct Frags {
-        i32x4 a[L];
-        i32x4 b[L];
-    };
-    const int ch = 2 * wave + h;   // this wave's 16-byte chunk of a stage row
-    auto read_frags = [&](int kb, Frags &f) {
-        const char *buf = smem + (kb % NST) * Sh::STAGE;
-#pragma unroll
-        for (int i = 0; i < L; ++i) f.a[i] = *(const i32x4 *)(buf + rswz<kDmaRB>(i * BM + lr, ch));
-#pragma unroll
-        for (int j = 0; j < L; ++j)
-            f.b[j] = *(const i32x4 *)(buf + rswz<kDmaRB>(L * BM + j * BN + lr, ch));
-    };
-    // the L^2 MFMAs of one stage, with the DMA instructions of stage dkb (if
-    // dkb >= 0) spread between them: issued in a burst, the four waves'
-    // instructions fill the vector-memory queue and stall each wave at issue
-    auto mfmas = [&](const Frags &f, int dkb) {
-        constexpr int NMF = PS::N;
-        static_for<NMF>([&](auto n_) {
-            constexpr int n = decltype(n_)::value;
-            constexpr int i = PS::i_of(n), j = PS::j_of(n);
-            if constexpr (kHand) HandMfma<ST, true>::run(acc[i][j], f.a[i], f.b[j]);
-            else acc[i][j] = MF::run(f.a[i], f.b[j], acc[i][j]);
-            static_for<LPS>([&](auto d_) {
-                constexpr int d = decltype(d_)::value;
-                // instruction d goes after MFMA (d * NMF) / LPS
-                if constexpr ((d * NMF) / LPS == n) {
-                    if (dkb >= 0) issue_one(dkb, d);
-                }
-            });
-            __builtin_amdgcn_sched_barrier(0);
-        });
-    };
-    // stage kb: the next stage's fragments into `nxt` (after its barrier,
-    // which also frees stage kb's slot for stage kb + NST), then the MFMAs of
-    // `cur` with stage kb + NST's DMA between them
-    auto stage = [&](int kb, const Frags &cur, Frags &nxt) {
-        int dkb = -1;
-        if (kb + 1 < nkb) {
-            stage_ready(kb + 1);
-            if (kb + NST < nkb) dkb = kb + NST;
-            read_frags(kb + 1, nxt);
-        }
-        mfmas(cur, dkb);
-    };
-
-    if (nkb > 0) {
-#pragma unroll
-        for (int s = 0; s < NST - 1; ++s)
-            if (s < nkb) issue_stage(s);
-        stage_ready(0);
-        if (NST - 1 < nkb) issue_stage(NST - 1);
-        Frags f0, f1;
-        read_frags(0, f0);
-        int kb = 0;
-        for (; kb + 1 < nkb; kb += 2) {
-            stage(kb, f0, f1);
-            stage(kb + 1, f1, f0);
-        }
-        if (kb < nkb) stage(kb, f0, f1);
-    }
-
-    // the hand-placed MFMAs' results are read below: 64 wait states first
-    if constexpr (kHand) asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory");
-
-    // ---- epilogue ----
-    wait_vmcnt<0>();
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    exec_barrier();   // every wave is past its last read of the ring
-    // LDS: T [pair][4][lane] x 4 t values, R [wave][pair][4][lane] x 4
-    // accumulator values, S the scales; 16-byte pieces, a wave's 64 pieces
-    // contiguous
+    // The main loop and the first part of the epilogue of pair group GI
+    // (compile-time pair range; G = 1: every pair).
     f32x4 *T = (f32x4 *)smem;
     using E4 = Elem __attribute__((ext_vector_type(4)));
     E4 *R = (E4 *)(smem + Sh::T_BYTES);
     float *S = (float *)(smem + Sh::T_BYTES + Sh::R_BYTES);
-    if ((tid & 127) < L * 32) S[(tid < 128 ? 0 : L * 32) + (tid & 127)] = scl;
-    constexpr int NG = (Sh::NP + Sh::PR - 1) / Sh::PR;
-    static_for<NG>([&](auto gi_) {
-        constexpr int gi = decltype(gi_)::value;
-        static_for<Sh::PR>([&](auto pp_) {
-            constexpr int pp = decltype(pp_)::value;
-            constexpr int pr = gi * Sh::PR + pp;
-            if constexpr (pr < Sh::NP) {
-                const Acc v = acc[PS::i_of(pr)][PS::j_of(pr)];
+    auto body = [&](auto GI_) {
+        constexpr int GI = decltype(GI_)::value;
+        constexpr int F = Sh::first(GI), NPG = Sh::count(GI);
+        constexpr int ILO = KG::ilo(F, NPG), NA = KG::na(F, NPG);
+        constexpr int JLO = KG::jlo(F, NPG), NB = KG::nb(F, NPG);
+        Acc acc[NPG];
 #pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    R[((wave * Sh::PR + pp) * 4 + c) * 64 + lane] =
-                        E4{v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]};
-            }
-        });
-        __builtin_amdgcn_s_waitcnt(0xC07F);
-        exec_barrier();
-        const int pr = gi * Sh::PR + wave;
-        if (wave < Sh::PR && pr < Sh::NP) {
-            const int i = PS::i_of(pr), j = PS::j_of(pr);
-            const float sbj = S[L * 32 + j * 32 + lr];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                E4 v = R[((0 * Sh::PR + wave) * 4 + c) * 64 + lane];
-                v = v + R[((1 * Sh::PR + wave) * 4 + c) * 64 + lane];
-                v = v + R[((2 * Sh::PR + wave) * 4 + c) * 64 + lane];
-                v = v + R[((3 * Sh::PR + wave) * 4 + c) * 64 + lane];
-                // registers 4c .. 4c + 3: rows 8c + 4h + 0..3 of the tile
-                f32x4 tv;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float t1 = MF::to_f32(v[e]) * S[i * 32 + 8 * c + 4 * h + e];
-                    tv[e] = t1 * sbj;
-                }
-                T[(pr * 4 + c) * 64 + lane] = tv;
-            }
+        for (int n = 0; n < NPG; ++n) acc[n] = MF::zero();
+        // At L = 4 with one pair group the 16 accumulator tiles (256
+        // registers) live in the AGPRs, through hand-placed MFMAs (left to the
+        // compiler, the K loop spills).  The compiler's hazard recogniser does
+        // not see into inline assembly: the zeroed tiles are pinned here, 8
+        // wait states before any MFMA reads them.
+        constexpr bool kHand = Sh::kHand;
+        if constexpr (kHand) {
+            static_for<NPG>([&](auto n_) {
+                constexpr int n = decltype(n_)::value;
+                (void)acc;   // an ordinary use, so that the capture does not hinge on the asm operand
+                asm volatile("" : "+a"(acc[n]));
+            });
+            asm volatile("s_nop 7" ::: "memory");
         }
+
+        struct Frags {
+            i32x4 a[NA];
+            i32x4 b[NB];
+        };
+        const int ch = 2 * ks + h;   // this wave's 16-byte chunk of a stage row
+        auto read_frags = [&](int kb, Frags &f) {
+            const char *buf = smem + (kb % NST) * Sh::STAGE;
+#pragma unroll
+            for (int i = 0; i < NA; ++i)
+                f.a[i] = *(const i32x4 *)(buf + rswz<kDmaRB>((ILO + i) * BM + lr, ch));
+#pragma unroll
+            for (int j = 0; j < NB; ++j)
+                f.b[j] = *(const i32x4 *)(buf + rswz<kDmaRB>(L * BM + (JLO + j) * BN + lr, ch));
+        };
+        // the group's MFMAs of one stage, with the DMA instructions of stage
+        // dkb (if dkb >= 0) spread between them: issued in a burst, the
+        // waves' instructions fill the vector-memory queue and stall each
+        // wave at issue
+        auto mfmas = [&](const Frags &f, int dkb) {
+            static_for<NPG>([&](auto n_) {
+                constexpr int n = decltype(n_)::value;
+                constexpr int i = PS::i_of(F + n) - ILO, j = PS::j_of(F + n) - JLO;
+                if constexpr (kHand) HandMfma<ST, true>::run(acc[n], f.a[i], f.b[j]);
+                else acc[n] = MF::run(f.a[i], f.b[j], acc[n]);
+                static_for<LPS>([&](auto d_) {
+                    constexpr int d = decltype(d_)::value;
+                    // instruction d goes after MFMA (d * NPG) / LPS
+                    if constexpr ((d * NPG) / LPS == n) {
+                        if (dkb >= 0) issue_one(dkb, d);
+                    }
+                });
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        };
+        // stage kb: the next stage's fragments into `nxt` (after its barrier,
+        // which also frees stage kb's slot for stage kb + NST), then the MFMAs
+        // of `cur` with stage kb + NST's DMA between them
+        auto stage = [&](int kb, const Frags &cur, Frags &nxt) {
+            int dkb = -1;
+            if (kb + 1 < nkb) {
+                stage_ready(kb + 1);
+                if (kb + NST < nkb) dkb = kb + NST;
+                read_frags(kb + 1, nxt);
+            }
+            mfmas(cur, dkb);
+        };
+
+        if (nkb > 0) {
+#pragma unroll
+            for (int s = 0; s < NST - 1; ++s)
+                if (s < nkb) issue_stage(s);
+            stage_ready(0);
+            if (NST - 1 < nkb) issue_stage(NST - 1);
+            Frags f0, f1;
+            read_frags(0, f0);
+            int kb = 0;
+            for (; kb + 1 < nkb; kb += 2) {
+                stage(kb, f0, f1);
+                stage(kb + 1, f1, f0);
+            }
+            if (kb < nkb) stage(kb, f0, f1);
+        }
+
+        // the hand-placed MFMAs' results are read below: 64 wait states first
+        if constexpr (kHand) asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory");
+
+        // ---- epilogue ----
+        wait_vmcnt<0>();
         __builtin_amdgcn_s_waitcnt(0xC07F);
-        exec_barrier();
-    });
-    // wave w: accumulator registers 4w .. 4w + 3 of every lane, rows
-    // 8w + 4h + 0..3
+        exec_barrier();   // every wave is past its last read of the ring
+        // LDS: T [pair][4][lane] x 4 t values, R [wave][pair][4][lane] x 4
+        // accumulator values, S the scales; 16-byte pieces, a wave's 64
+        // pieces contiguous.  Round gi takes the group's pairs gi PR .. gi PR
+        // + PR - 1: every wave stores its accumulators of them, then wave
+        // (group, pp) sums pair pp over the group's four K-step waves in
+        // K-step order and turns the sum into t_ij.  Both groups run all
+        // rounds (their barriers are shared).
+        if ((tid & 127) < L * 32 && tid < 256) S[(tid < 128 ? 0 : L * 32) + (tid & 127)] = scl;
+        static_for<Sh::NG>([&](auto gi_) {
+            constexpr int gi = decltype(gi_)::value;
+            static_for<Sh::PR>([&](auto pp_) {
+                constexpr int pp = decltype(pp_)::value;
+                constexpr int n = gi * Sh::PR + pp;
+                if constexpr (n < NPG) {
+                    const Acc v = acc[n];
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        R[((wave * Sh::PR + pp) * 4 + c) * 64 + lane] =
+                            E4{v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]};
+                }
+            });
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            exec_barrier();
+            const int n = gi * Sh::PR + ks;   // this wave's pair of the round
+            if (ks < Sh::PR && n < NPG) {
+                const int pr = F + n;
+                const int i = PS::i_of(pr), j = PS::j_of(pr);
+                const float sbj = S[L * 32 + j * 32 + lr];
+                const int w0 = GI * 4;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    E4 v = R[(((w0 + 0) * Sh::PR + ks) * 4 + c) * 64 + lane];
+                    v = v + R[(((w0 + 1) * Sh::PR + ks) * 4 + c) * 64 + lane];
+                    v = v + R[(((w0 + 2) * Sh::PR + ks) * 4 + c) * 64 + lane];
+                    v = v + R[(((w0 + 3) * Sh::PR + ks) * 4 + c) * 64 + lane];
+                    // registers 4c .. 4c + 3: rows 8c + 4h + 0..3 of the tile
+                    f32x4 tv;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float t1 = MF::to_f32(v[e]) * S[i * 32 + 8 * c + 4 * h + e];
+                        tv[e] = t1 * sbj;
+                    }
+                    T[(pr * 4 + c) * 64 + lane] = tv;
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            exec_barrier();
+        });
+    };
+    if constexpr (G == 1) {
+        body(std::integral_constant<int, 0>{});
+    } else {
+        if (grp == 0) body(std::integral_constant<int, 0>{});
+        else body(std::integral_constant<int, 1>{});
+    }
+    // waves 0..3: accumulator registers 4w .. 4w + 3 of every lane, rows
+    // 8w + 4h + 0..3, summed over every pair in order
+    if (wave >= 4) return;
     const int64_t col = n0 + lr;
     const int64_t cbase = bidx * p.cs_b;
     OA out[4] = {(OA)0, (OA)0, (OA)0, (OA)0};
@@ -1004,7 +1049,6 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_kstep_kernel(GemmParams p, 
     }
 }
 
-// ---------------------------------------------------------------------------
 // Pair-split variant: 8 waves, two per SIMD.  The 2 x 2 grid of 32 x 32 wave
 // blocks is covered twice: wave group g (0 or 1) accumulates the slice pairs
 // [g*P0, ...) of the i-major / j-minor pair order, P0 = ceil(L*L/2) (6 at
@@ -2887,10 +2931,10 @@ static hipError_t launch_dma(const GemmParams &p, const GemmPlan &plan, hipStrea
     return hipGetLastError();
 }
 
-template <typename ST, int L, typename AccT, bool TRI>
+template <typename ST, int L, typename AccT, bool TRI, int G = 1>
 static hipError_t launch_kstep(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
-    using Sh = KStepShape<L, TRI>;
-    auto kern = cross_gemm_kstep_kernel<ST, L, AccT, TRI>;
+    using Sh = KStepShape<L, TRI, G>;
+    auto kern = cross_gemm_kstep_kernel<ST, L, AccT, TRI, G>;
     static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
     if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
     const int es = (int)sizeof(ST);
@@ -2898,7 +2942,7 @@ static hipError_t launch_kstep(const GemmParams &p, const GemmPlan &plan, hipStr
     const int64_t eb = dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es);
     const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
     if (tiles == 0) return hipSuccess;
-    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(256), Sh::LDS_BYTES, st, p,
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(256 * G), Sh::LDS_BYTES, st, p,
                        plan.group_m, (uint32_t)ea, (uint32_t)eb);
     return hipGetLastError();
 }
@@ -3073,6 +3117,9 @@ static hipError_t launch_L(const GemmParams &p, const GemmPlan &plan, hipStream_
     // (fp32 slices at L = 4: no hand-placed MFMA, so no K-step kernel)
     if constexpr (L <= 4 && !(L == 4 && std::is_same_v<ST, float>)) {
         if (plan.kind == kGemmKStep) return launch_kstep<ST, L, AccT, TRI>(p, plan, st);
+    }
+    if constexpr (L >= 2 && L <= 4) {
+        if (plan.kind == kGemmKStep2) return launch_kstep<ST, L, AccT, TRI, 2>(p, plan, st);
     }
     const int key = plan.mi * 10 + plan.ni;
     if constexpr (L == 1) {

@@ -563,29 +563,31 @@ def test_planner_kernel_choice():
     assert _gemm_kernel(L, 1, 2048, 2048, 8192, 4, I8, 256) == "ring"     # 3 vs 4
     assert _gemm_kernel(L, 1, 1024, 1024, 65536, 4, I8, 256) == "ring"    # 1 vs 1
     assert _gemm_kernel(L, 1, 4096, 4096, 4096, 2, _lib.OZK_F16, 256) == "ring"   # config 2
-    assert _gemm_kernel(L, 1, 256, 256, 256, 2, _lib.OZK_F16, 256) == "kstep"     # config 1
+    assert _gemm_kernel(L, 1, 256, 256, 256, 2, _lib.OZK_F16, 256) == "kstep2"    # config 1
     assert _gemm_kernel(L, 1, 2048, 2048, 2048, 1, I8, 256) == "dma"
     # grids whose 64 x 64 tiles leave more than half the CUs idle: the K-step
     # kernel's 32 x 32 tiles when they fit one round (the reference's
     # (1, 128, 2048, 4096) point: 256 of them), else split-K of the ring or
     # wide kernel, S = CUs / tiles, at most 4, at least 16 stages of 128 bytes
     # of K per range
+    # (two slices or more: its 8-wave form with two pair groups, "kstep2")
     for nsp in (1, 2, 3, 4):
         for sd in (I8, _lib.OZK_F16):
-            assert _gemm_kernel(L, 1, 128, 2048, 4096, nsp, sd, 256, True) == ("kstep", 1)
+            want = "kstep" if nsp == 1 else "kstep2"
+            assert _gemm_kernel(L, 1, 128, 2048, 4096, nsp, sd, 256, True) == (want, 1)
     assert _gemm_kernel(L, 1, 128, 2048, 4096, 4, _lib.OZK_F32, 256) == "ring"     # fp32 slices
     assert _gemm_kernel(L, 1, 128, 2048, 4096, 4, I8, 64, True) == ("ring", 1)       # 64 CUs
     # the shapes of test_ozaki_matmul_graph_capture: the K-step kernel, and at
     # K = 8192 the ring kernel with 4 ranges (6 K-step tiles against 8)
-    assert _gemm_kernel(L, 2, 128, 96, 256, 3, I8, 256, True) == ("kstep", 1)
+    assert _gemm_kernel(L, 2, 128, 96, 256, 3, I8, 256, True) == ("kstep2", 1)
     assert _gemm_kernel(L, 1, 64, 96, 8192, 3, I8, 256, True) == ("ring", 4)
     assert _gemm_kernel(L, 1, 64, 96, 8192, 3, _lib.OZK_F16, 256, True) == ("ring", 4)
-    assert _gemm_kernel(L, 1, 32, 32, 4096, 4, I8, 256, True) == ("kstep", 1)        # S = 2
+    assert _gemm_kernel(L, 1, 32, 32, 4096, 4, I8, 256, True) == ("kstep2", 1)       # S = 2
     assert _gemm_kernel(L, 1, 512, 2048, 4096, 4, I8, 256, True) == ("ring", 1)      # 256 tiles
     assert _gemm_kernel(L, 1, 640, 640, 4096, 4, I8, 256, True) == ("ring", 2)       # 100 tiles, 400
     assert _gemm_kernel(L, 1, 640, 640, 2048, 4, I8, 256, True) == ("ring", 1)       # 16 stages
     assert _gemm_kernel(L, 1, 640, 640, 8192, 4, I8, 256, True) == ("ring", 2)
-    assert _gemm_kernel(L, 1, 320, 320, 8192, 4, I8, 256, True) == ("kstep", 1)      # 100 = 25 x 4
+    assert _gemm_kernel(L, 1, 320, 320, 8192, 4, I8, 256, True) == ("kstep2", 1)     # 100 = 25 x 4
     assert _gemm_kernel(L, 1, 288, 320, 8192, 4, I8, 256, True) == ("ring", 4)       # 90 < 25 x 4
     with _lib.forced_kernels(gemm="ring"):
         # the reference point with the ring kernel forced: split-K
@@ -635,7 +637,7 @@ def test_triangular_planner():
     assert _gemm_kernel_pairs(L, 1, 1024, 1024, 65536, 3, I8, T) == ("wide", 2)
     ref_point = (1, 128, 2048, 4096)
     for nsp in (2, 3, 4):
-        assert _gemm_kernel_pairs(L, *ref_point, nsp, I8, T) == ("kstep", 1)
+        assert _gemm_kernel_pairs(L, *ref_point, nsp, I8, T) == ("kstep2", 1)
     assert _gemm_kernel_pairs(L, *ref_point, 4, F32, T) == ("dma", 1)
     assert _gemm_kernel_pairs(L, *c3, 1, I8, T) == _gemm_kernel_pairs(L, *c3, 1, I8, A)
     # no kernel sums the triangle over more than 5 slices; unknown sets

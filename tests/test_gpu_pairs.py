@@ -36,6 +36,7 @@ def _cross(ozk, gpu, As, BsT, sa, sb, L, out, pairs):
 
 TRI_KERNELS = [("staged", 2), ("staged", 3), ("staged", 4), ("dma", 2), ("dma", 3), ("dma", 4),
                ("ad", 2), ("ad", 3), ("ad", 4), ("kstep", 2), ("kstep", 3), ("kstep", 4),
+               ("kstep2", 2), ("kstep2", 3), ("kstep2", 4),
                ("wide", 3), ("wide4", 4), ("pair", 3), ("pair", 4), ("pair", 5), ("solo5", 5)]
 
 

@@ -376,7 +376,7 @@ def test_ozaki_matmul_degenerate_shapes(gpu):
 
 
 @pytest.mark.parametrize("kernel", ["staged", "dma", "ad", "pair", "ring", "wide", "wide4",
-                                    "kstep"])
+                                    "kstep", "kstep2"])
 @pytest.mark.parametrize("L", [1, 2, 3, 4])
 def test_cross_gemm_each_kernel_bitexact(oracle, gpu, L, kernel, force):
     """Every cross-GEMM kernel, forced: the VGPR-staged one (taken when an
@@ -415,6 +415,9 @@ def test_cross_gemm_each_kernel_bitexact(oracle, gpu, L, kernel, force):
     ("kstep", 3, 130, 72, 4096),
     ("kstep", 2, 64, 96, 2064),
     ("kstep", 1, 40, 200, 1040),
+    ("kstep2", 4, 100, 72, 1040),
+    ("kstep2", 3, 130, 72, 4096),
+    ("kstep2", 2, 64, 96, 2064),
 ])
 def test_float_slice_kernels_bitexact(oracle, gpu, kernel, L, M, N, K, sdt, force):
     """Every cross-GEMM kernel with float slices, at the tile shapes and K of
@@ -461,11 +464,13 @@ def test_ring_kernel_stage_counts(oracle, gpu, L, K, sdt, force):
                                  torch.int8])
 @pytest.mark.parametrize("sdt", [torch.int8, torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("L", [1, 3, 4])
-def test_kstep_kernel_dtypes(oracle, gpu, L, sdt, out, force):
-    """The K-step kernel for every slice and output dtype, batched, with a
-    broadcast (batch stride 0) B: int8 and integer-valued float slices
-    bit-exact against the oracle (fp32 slices at L = 4 take the planner's
-    kernel)."""
+@pytest.mark.parametrize("kernel", ["kstep", "kstep2"])
+def test_kstep_kernel_dtypes(oracle, gpu, L, sdt, out, kernel, force):
+    """The K-step kernel, in its 4-wave and its 8-wave (two pair groups)
+    form, for every slice and output dtype, batched, with a broadcast (batch
+    stride 0) B: int8 and integer-valued float slices bit-exact against the
+    oracle (fp32 slices at L = 4 take the planner's kernel for the 4-wave
+    form, and L = 1 the 4-wave form for the 8-wave one)."""
     import ozaki_triton_amd as ozk
     g = torch.Generator().manual_seed(ALL_SLICES.index(sdt) * 11 + len(str(out)) + 40 * L)
     M, N, K = 70, 100, 400
@@ -475,20 +480,22 @@ def test_kstep_kernel_dtypes(oracle, gpu, L, sdt, out, force):
     Bd = BsT[:1].to(gpu).expand(2, -1, -1, -1).transpose(-1, -2)   # broadcast B
     sbd = sb[:1].to(gpu).expand(2, -1, -1)
     args = (As.to(gpu), Bd, sa.to(gpu), sbd, L, out)
-    force(gemm="kstep")
+    force(gemm=kernel)
     C = to_np(ozk.cross_gemm(*args))
     for b in range(2):
         want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[0]), to_np(sa[b]), to_np(sb[0]),
                                  NAME_OF[out])
-        assert_bitwise_equal(C[b], want, f"kstep L{L} {sdt} {out} b{b}")
+        assert_bitwise_equal(C[b], want, f"{kernel} L{L} {sdt} {out} b{b}")
 
 
 @pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
 @pytest.mark.parametrize("L", [1, 2, 3, 4])
 @pytest.mark.parametrize("K", [16, 128, 200, 520, 1040, 2064])
-def test_kstep_kernel_stage_counts(oracle, gpu, L, K, sdt, force):
+@pytest.mark.parametrize("kernel", ["kstep", "kstep2"])
+def test_kstep_kernel_stage_counts(oracle, gpu, L, K, sdt, kernel, force):
     """The K-step kernel (32 x 32 tiles, wave w on K step w of every stage,
-    the waves' accumulators summed through the LDS) over 1 to 17 stages of
+    the waves' accumulators summed through the LDS; with kstep2 two such sets
+    of 4 waves, each holding half the slice pairs) over 1 to 17 stages of
     128 bytes of K against a ring of 5 or 6 stage slots (fewer stages than
     the prologue would fetch, and more than the ring holds), M and N cutting
     tiles, batch 2: int8 and integer-valued fp16 slices bit-exact against the
@@ -498,12 +505,12 @@ def test_kstep_kernel_stage_counts(oracle, gpu, L, K, sdt, force):
     g = torch.Generator().manual_seed(K * 10 + L + 5)
     As, BsT, sa, sb = _slices_for(g, 2, L, M, N, K, sdt)
     args = (As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), L, torch.float64)
-    force(gemm="kstep")
+    force(gemm=kernel)
     C = to_np(ozk.cross_gemm(*args))
     for b in range(2):
         want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[b]), to_np(sa[b]), to_np(sb[b]),
                                  "float64")
-        assert_bitwise_equal(C[b], want, f"kstep {sdt} L{L} K{K} b{b}")
+        assert_bitwise_equal(C[b], want, f"{kernel} {sdt} L{L} K{K} b{b}")
 
 
 @pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
@@ -764,7 +771,7 @@ def test_reference_point_small_grid(oracle, gpu, xdt, sdt, L, gemm, force):
         if gemm:
             assert (kern, ks) == ("ring", 2 if sdt == torch.int8 else 4)
         else:
-            assert (kern, ks) == ("kstep", 1)
+            assert (kern, ks) == ("kstep" if L == 1 else "kstep2", 1)
     A, B = c3_like((1, M, K), (1, K, N), seed=L + 17, dtype=xdt)
     C = ozk.ozaki_matmul(A.to(gpu), B.to(gpu), L, sdt)
     torch.cuda.synchronize()
@@ -1273,7 +1280,7 @@ def test_split_columns_default_plan(oracle, gpu, xdt, sdt, batch, N, K, L):
 
 
 @pytest.mark.parametrize("kernel", ["", "dma", "ring", "pair", "ad", "staged", "wide", "wide4",
-                                    "solo5", "kstep"])
+                                    "solo5", "kstep", "kstep2"])
 @pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
 @pytest.mark.parametrize("K", [1, 2, 3, 5, 7, 9, 255, 257, 1003])
 def test_packed_rows_last_piece(oracle, gpu, kernel, sdt, K, force):
@@ -1287,7 +1294,7 @@ def test_packed_rows_last_piece(oracle, gpu, kernel, sdt, K, force):
     import ozaki_triton_amd as ozk
     if kernel:
         force(gemm=kernel)
-    L = (3 if kernel == "wide" else 4 if kernel in ("ring", "pair", "ad", "wide4", "kstep")
+    L = (3 if kernel == "wide" else 4 if kernel in ("ring", "pair", "ad", "wide4", "kstep", "kstep2")
          else 5 if kernel == "solo5" else 2)
     A, B = c3_like((1, 33, K), (1, K, 20), seed=K + 100)
     C = ozk.ozaki_matmul(A.to(gpu), B.to(gpu), L, sdt, max_splits=L)
