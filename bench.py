@@ -480,8 +480,8 @@ def main():
         ia, ib = phases.index(a), phases.index(b)
         return sum(e[ia].elapsed_time(e[ib]) for e in events) / len(events)
 
-    # the statistic the survey's measurement asks for: the median of 20 single
-    # calls, each after a 512 MiB write that evicts L2 and MALL
+    # the reference benchmark's statistic: the median of 20 single calls, each
+    # after a 512 MiB write that evicts L2 and MALL
     import statistics
     flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
     fts = []
