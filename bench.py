@@ -480,8 +480,9 @@ def main():
         ia, ib = phases.index(a), phases.index(b)
         return sum(e[ia].elapsed_time(e[ib]) for e in events) / len(events)
 
-    # the reference benchmark's statistic: the median of 20 single calls, each
-    # after a 512 MiB write that evicts L2 and MALL
+    # single calls, each after a 512 MiB write that evicts L2 and MALL (as
+    # triton.testing.do_bench, which reference test.py:125 times with, clears
+    # the cache before each call); the median of 20
     import statistics
     flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
     fts = []
