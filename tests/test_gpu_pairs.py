@@ -115,6 +115,24 @@ def test_triangular_ozaki_matmul_bitexact(oracle, gpu, xdt, L):
     assert_bitwise_equal(to_np(C1), oracle.ozaki_matmul(to_np(A), to_np(B), 1, "int8"), "L1")
 
 
+@pytest.mark.parametrize("L", [3, 4, 5])
+def test_triangular_strided_inputs(oracle, gpu, L):
+    """ozaki_matmul(pairs="triangular") on strided operands: A stored K-major
+    (a transposed view of its transpose) and B a column slice of a wider matrix
+    (row stride 200 for N = 136).  The splits read both through their strides;
+    C must equal the oracle's result on contiguous copies bit for bit."""
+    import ozaki_triton_amd as ozk
+    A, Bw = c3_like((2, 96, 1024), (1024, 200), 90 + L, dtype=torch.float64)
+    Ag = A.to(gpu).transpose(-1, -2).contiguous().transpose(-1, -2)
+    Bg = Bw.to(gpu)[:, 8:144]
+    assert Ag.stride()[-2:] == (1, 96) and Bg.stride() == (200, 1)
+    C = ozk.ozaki_matmul(Ag, Bg, L, torch.int8, max_splits=5, pairs="triangular")
+    torch.cuda.synchronize()
+    want = oracle.ozaki_matmul(to_np(A), np.ascontiguousarray(to_np(Bw)[:, 8:144]), L, "int8",
+                               pairs="triangular")
+    assert_bitwise_equal(to_np(C), want, f"strided matmul L{L} triangular")
+
+
 def test_triangular_rejected_beyond_five_slices(gpu):
     import ozaki_triton_amd as ozk
     from ozaki_triton_amd import _lib
