@@ -109,8 +109,15 @@ def reference_shapes(reps: int = 30):
         a, b, c_ref = inputs[key]
         C = ozk.ozaki_matmul(a, b, num_splits=L, slice_dtype=sdt).double()
         rel = float((C - c_ref).norm() / c_ref.norm())
-        for _ in range(5):
+        # warmup as triton.testing.do_bench's default: 25 ms of calls (at
+        # least 5), synchronised every 8 calls so that host time tracks the GPU
+        tw, nw = time.perf_counter(), 0
+        while nw < 5 or time.perf_counter() - tw < 0.025:
             ozk.ozaki_matmul(a, b, num_splits=L, slice_dtype=sdt)
+            nw += 1
+            if nw % 8 == 0:
+                torch.cuda.synchronize()
+        torch.cuda.synchronize()
         ts = []
         for _ in range(reps):
             flush.zero_()
