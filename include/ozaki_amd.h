@@ -60,7 +60,9 @@ enum {
     OZK_ERR_ACCUM = -8,       /* unsupported dot accumulator dtype */
     OZK_ERR_DEVICE_WAIT = -9, /* (ozk_device_status) a cooperative split wait on the
                                  device gave up; that split's scales, and so the C
-                                 computed from them, are NaN */
+                                 computed from them, are NaN -- except in an int8 C,
+                                 whose conversion maps NaN to 0: there C is 0, and
+                                 only this status tells it from a valid result */
     OZK_ERR_TOO_LARGE = -10   /* (ozk_matmul_static) the call needs more scratch than
                                  OZK_STATIC_SCRATCH_BYTES */
 };
@@ -229,8 +231,10 @@ int ozk_matmul_pairs(const void *A, const int64_t a_strides[3], const void *B,
  * tight serving loops, harnesses that forbid hipMalloc): ozk_matmul with its
  * workspace taken from a library-owned device array of OZK_STATIC_SCRATCH_BYTES,
  * one per device, held until the process ends.  The caller still passes the
- * inputs and C.  A call whose ozk_matmul_workspace_bytes() exceeds that
- * returns OZK_ERR_TOO_LARGE before anything is enqueued.  The call allocates
+ * inputs and C.  A call that needs more than that, not counting the optional
+ * split-K buffers (ozk_matmul_workspace_bytes() includes them), returns
+ * OZK_ERR_TOO_LARGE before anything is enqueued; split-K buffers that do not
+ * fit as well are left out (the same bits, from unsplit tiles).  The call allocates
  * nothing (no hipMalloc, hipFree or allocating library routine).  All calls on
  * one device share its array: calls that overlap on one device (other streams
  * or threads, without ordering between them) race and give wrong results.

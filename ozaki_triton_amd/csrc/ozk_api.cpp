@@ -92,6 +92,7 @@ ozk::SplitParams make_split_params(const void *X, int64_t batch, int64_t rows, i
     p.cs_l = cs[1];
     p.cs_r = cs[2];
     p.resid = nullptr;
+    p.fail_out = nullptr;
     return p;
 }
 
@@ -234,7 +235,7 @@ static int cross_gemm_impl(const void *A_slices, const int64_t a_strides[4], con
                    const int64_t sb_strides[3], int64_t batch, int64_t M, int64_t N, int64_t K,
                    int num_splits, int slice_dtype, int pairs, void *C, int out_dtype,
                    const int64_t c_strides[3], void *workspace, size_t workspace_bytes,
-                   void *stream) {
+                   void *stream, const uint32_t *split_fail = nullptr) {
     if (!a_strides || !b_strides || !sa_strides || !sb_strides || !c_strides)
         return OZK_ERR_NULL;
     if (!is_slice_dtype(slice_dtype) || !is_input_dtype(out_dtype)) return OZK_ERR_DTYPE;
@@ -245,7 +246,7 @@ static int cross_gemm_impl(const void *A_slices, const int64_t a_strides[4], con
     if (!C) return OZK_ERR_NULL;
     hipStream_t st = (hipStream_t)stream;
 
-    ozk::GemmParams p;
+    ozk::GemmParams p{};
     p.sa = A_scales;
     p.sb = B_scales;
     p.sas_b = sa_strides[0];
@@ -265,6 +266,10 @@ static int cross_gemm_impl(const void *A_slices, const int64_t a_strides[4], con
     p.out_dtype = out_dtype;
     // one slice is one pair in either set
     p.tri = pairs == OZK_PAIRS_TRIANGULAR && num_splits >= 2;
+    p.split_fail = split_fail;
+    p.dev_status = nullptr;
+    p.failed = 0;
+    if (split_fail && !(p.dev_status = ozk::device_status_word())) return OZK_ERR_LAUNCH;
     if (num_splits == 0) return hip_status(ozk::launch_zero_c(p, st));
     if (!A_slices || !B_slices || !A_scales || !B_scales) return OZK_ERR_NULL;
 
@@ -527,6 +532,18 @@ int ozk_matmul_pairs(const void *A, const int64_t a_strides[3], const void *B,
         ozk::split_workspace_bytes(pa, plan_a, dtype, slice_dtype) > lay.scratch_bytes)
         return OZK_ERR_WORKSPACE;
     pb.resid = pa.resid = (float *)(ws + lay.scratch);
+    // The status word of the last cooperative launch before the cross-GEMM
+    // goes to the cross-GEMM, which stores a NaN C and sets the device status
+    // if a wait gave up, in place of the poison kernel after that launch.
+    // That is B's split when it shares the launch with A's or when A's split
+    // uses no scratch (which would overwrite B's status word), else A's
+    // (B's split then keeps its poison kernel).
+    const uint32_t *split_fail = nullptr;
+    if (ozk::split_pair_ok(plan_a, plan_b, dtype) ||
+        ozk::split_workspace_bytes(pa, plan_a, dtype, slice_dtype) == 0)
+        pb.fail_out = &split_fail;
+    else
+        pa.fail_out = &split_fail;
     if ((e = record(events, 0, st)) != OZK_OK) return e;
     if (ozk::split_pair_ok(plan_a, plan_b, dtype)) {
         // both in one launch; the second event marks the same point (the B
@@ -551,7 +568,7 @@ int ozk_matmul_pairs(const void *A, const int64_t a_strides[3], const void *B,
     e = cross_gemm_impl(ws + lay.a_sl, lay.ga, ws + lay.b_sl, lay.gb,
                         (const float *)(ws + lay.a_sc), lay.gsa, (const float *)(ws + lay.b_sc),
                         lay.gsb, batch, M, N, K, L, slice_dtype, pairs, C, dtype, c_strides,
-                        ws + lay.pack, workspace_bytes - lay.pack, stream);
+                        ws + lay.pack, workspace_bytes - lay.pack, stream, split_fail);
     if (e != OZK_OK) return e;
     return record(events, 3, st);
 }
@@ -621,7 +638,7 @@ struct Named {
     int code;
 };
 const Named kGemmNames[] = {{"staged", ozk::kGemmStaged}, {"dma", ozk::kGemmDMA},
-                            {"ad", ozk::kGemmAD},         {"pair", ozk::kGemmPair},
+                            {"pair", ozk::kGemmPair},
                             {"ring", ozk::kGemmRing},     {"wide", ozk::kGemmWide},
                             {"wide4", ozk::kGemmWide4},   {"solo5", ozk::kGemmSolo5},
                             {"kstep", ozk::kGemmKStep},   {"kstep2", ozk::kGemmKStep2}};

@@ -217,7 +217,6 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
                               : kGemmPair;
         if (L <= 4) {
             if (forced(kGemmStaged)) plan.kind = kGemmStaged;
-            else if (fits && forced(kGemmAD)) plan.kind = kGemmAD;
             else if (fits && forced(kGemmDMA)) plan.kind = kGemmDMA;
             else if (fits && forced(kGemmPair) && L >= 3) plan.kind = kGemmPair;
             else if (fits && forced(kGemmWide) && L == 3) plan.kind = kGemmWide;
@@ -228,7 +227,6 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
         } else if (fits && forced(kGemmSolo5) && solo5) {
             plan.kind = kGemmSolo5;
         }
-        if (plan.kind == kGemmAD) plan.group_m = 2;
         if (plan.kind == kGemmWide4) plan.group_m = 4;
         plan.kb_per_split = nkb_all;
         if (plan.kind == kGemmWide) {
@@ -249,7 +247,6 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
         return plan;
     }
     if (forced(kGemmStaged)) plan.kind = kGemmStaged;
-    else if (fits && forced(kGemmAD)) plan.kind = kGemmAD;
     else if (fits && forced(kGemmDMA)) plan.kind = kGemmDMA;
     else if (fits && forced(kGemmPair)) plan.kind = L >= 3 ? kGemmPair : kGemmDMA;
     else if (fits && forced(kGemmRing)) plan.kind = L >= 2 ? kGemmRing : kGemmDMA;
@@ -257,7 +254,6 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
     else if (fits && forced(kGemmWide4)) plan.kind = L == 4 ? kGemmWide4 : plan.kind;
     else if (fits && forced(kGemmKStep)) plan.kind = (L == 4 && slice_dtype == 1) ? plan.kind : kGemmKStep;
     else if (fits && forced(kGemmKStep2) && L >= 2) plan.kind = kGemmKStep2;
-    if (plan.kind == kGemmAD) plan.group_m = 2;
     // 96 x 64 tiles: groups of 4 tile rows (C3: 7.12-7.16 ms against 7.21-7.23
     // with 8, 7.33-7.35 with 16; cross-GEMM alone, one box)
     if (plan.kind == kGemmWide4) plan.group_m = 4;

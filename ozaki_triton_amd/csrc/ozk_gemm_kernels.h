@@ -112,11 +112,15 @@ template <> struct Mfma<float> {
 // the fp64 accumulator itself; otherwise the fp32 accumulator is stored as
 // fp32, rounded to nearest even for fp16 / bf16, or truncated toward zero and
 // saturated for int8 (NVIDIA's float-to-integer conversion; NaN -> 0).
-OZK_DEV void store_c(const GemmParams &p, int64_t idx, double v) { ((double *)p.C)[idx] = v; }
+// A failed split before the launch (p.failed) makes every entry NaN.
+OZK_DEV void store_c(const GemmParams &p, int64_t idx, double v) {
+    ((double *)p.C)[idx] = p.failed ? __longlong_as_double(0x7ff8000000000000ll) : v;
+}
 // partial of an earlier launch (num_splits > 4 runs with an fp64 or fp32 C)
 OZK_DEV double load_c(const GemmParams &p, int64_t idx, double) { return ((const double *)p.C)[idx]; }
 OZK_DEV float load_c(const GemmParams &p, int64_t idx, float) { return ((const float *)p.C)[idx]; }
 OZK_DEV void store_c(const GemmParams &p, int64_t idx, float v) {
+    if (p.failed) v = __int_as_float(0x7fc00000);
     switch (p.out_dtype) {
     case 1: ((float *)p.C)[idx] = v; break;
     case 2: ((_Float16 *)p.C)[idx] = (_Float16)v; break;
@@ -126,6 +130,19 @@ OZK_DEV void store_c(const GemmParams &p, int64_t idx, float v) {
         ((int8_t *)p.C)[idx] = (int8_t)(int)t;
     }
     }
+}
+
+// Kernel entry: reads the status word of the cooperative split that ran
+// before on the same stream (complete when the kernel starts) into p.failed,
+// and records a failure in the device's sticky status (one lane).
+OZK_DEV void resolve_split_fail(GemmParams &p) {
+    p.failed = 0;
+    if (!p.split_fail) return;
+    // a scalar load (the constant address space): the word does not change
+    // while the kernel runs, and the value stays in a scalar register
+    p.failed = *(const __attribute__((address_space(4))) uint32_t *)(uintptr_t)p.split_fail != 0;
+    if (p.failed && blockIdx.x == 0 && threadIdx.x == 0)
+        __hip_atomic_fetch_or(p.dev_status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 OZK_DEV int64_t xcd_remap_gemm(int64_t g, int64_t n) {
@@ -195,6 +212,7 @@ OZK_DEV int swz(int row, int chunk) {
 
 template <typename ST, int L, int MI, int NI, typename AccT, bool TRI>
 __global__ __launch_bounds__(256, 1) void cross_gemm_kernel(GemmParams p, int group_m) {
+    resolve_split_fail(p);
     using PS = Pairs<L, TRI>;
     using Sh = GemmShape<L, MI, NI>;
     using MF = Mfma<ST>;
@@ -366,7 +384,6 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_kernel(GemmParams p, int gr
 // Out-of-range rows and K tails are fetched from a buffer offset beyond
 // num_records, which the hardware returns as zeros.
 // ---------------------------------------------------------------------------
-constexpr int kDmaRowBytes = 64;     // A-direct kernel stage rows
 constexpr int kDmaRB = 128;          // 2 x 2 DMA kernel stage rows (bytes of K; 64 also works)
 constexpr int kDmaStages = (kDmaRB == 64) ? 4 : 2;   // LDS ring slots
 
@@ -389,7 +406,6 @@ template <int RB> OZK_DEV int rswz(int r, int c) {
     if constexpr (RB == 64) return r * 64 + ((c ^ ((r >> 2) & 3)) << 4);
     else return r * 128 + ((c ^ ((r >> 1) & 7)) << 4);
 }
-OZK_DEV int dswz(int r, int c) { return rswz<64>(r, c); }
 
 // s_waitcnt with only the vector-memory counter limited to n
 template <int N> OZK_DEV void wait_vmcnt() {
@@ -465,6 +481,7 @@ template <typename ST, int L, int MI, int NI, typename AccT, bool TRI>
 __global__ __launch_bounds__(256, 1) void cross_gemm_dma_kernel(GemmParams p, int group_m,
                                                                 uint32_t a_records,
                                                                 uint32_t b_records) {
+    resolve_split_fail(p);
     using Sh = DmaShape<L, MI, NI>;
     using MF = Mfma<ST>;
     using Acc = typename MF::Acc;
@@ -775,6 +792,7 @@ template <typename ST, int L, typename AccT, bool TRI, int G>
 __global__ __launch_bounds__(256 * G, 1) void cross_gemm_kstep_kernel(GemmParams p, int group_m,
                                                                       uint32_t a_records,
                                                                       uint32_t b_records) {
+    resolve_split_fail(p);
     using Sh = KStepShape<L, TRI, G>;
     using KG = KStepGroup<L, TRI>;
     using PS = Pairs<L, TRI>;
@@ -1098,6 +1116,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_pair_kernel(GemmParams p, i
                                                                  uint32_t a_records,
                                                                  uint32_t b_records, int i0,
                                                                  int cont) {
+    resolve_split_fail(p);
     using Sh = PairShape<L, R>;
     using PS = PairSplit<L, R, TRI>;
     using MF = Mfma<ST>;
@@ -1380,6 +1399,7 @@ template <typename ST, int L, typename AccT, int W>
 __global__ __launch_bounds__(512, 1) void cross_gemm_ring_kernel(GemmParams p, int group_m,
                                                                  uint32_t a_records,
                                                                  uint32_t b_records) {
+    resolve_split_fail(p);
     using Sh = RingShape<L, W>;
     using PS = PairSplit<L, L>;
     using MF = Mfma<ST>;
@@ -1759,6 +1779,7 @@ template <typename ST, typename AccT, bool TRI>
 __global__ __launch_bounds__(512, 1) void cross_gemm_wide_kernel(GemmParams p, int group_m,
                                                                  uint32_t a_records,
                                                                  uint32_t b_records) {
+    resolve_split_fail(p);
     using Sh = WideShape;
     using MF = Mfma<ST>;
     using Acc = typename MF::Acc;
@@ -2069,6 +2090,7 @@ template <typename ST, typename AccT, bool TRI>
 __global__ __launch_bounds__(512, 1) void cross_gemm_wide4_kernel(GemmParams p, int group_m,
                                                                   uint32_t a_records,
                                                                   uint32_t b_records) {
+    resolve_split_fail(p);
     using Sh = Wide4Shape;
     using MF = Mfma<ST>;
     using Acc = typename MF::Acc;
@@ -2423,6 +2445,7 @@ template <typename ST, typename AccT, bool TRI>
 __global__ __launch_bounds__(256, 1) void cross_gemm_solo5_kernel(GemmParams p, int group_m,
                                                                   uint32_t a_records,
                                                                   uint32_t b_records) {
+    resolve_split_fail(p);
     using Sh = Solo5Shape;
     using MF = Mfma<ST>;
     using Acc = typename MF::Acc;
@@ -2666,224 +2689,6 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_solo5_kernel(GemmParams p, 
 }
 
 // ---------------------------------------------------------------------------
-// A-direct variant.  The four waves are stacked along M (workgroup tile
-// 128 x 32*NI); each wave streams ITS OWN 32 rows of every A slice from global
-// memory straight into VGPRs (no LDS), and only B, which all four waves share,
-// goes through the LDS ring by DMA.  Per 32-byte K step and CU this moves
-// 4 KB (L=4) of DMA writes and 16 KB of ds_read_b128 through the LDS instead
-// of 16 KB + 32 KB for a 2 x 2 wave grid, at the same L2-miss footprint.
-//
-// K order inside a 64-byte stage: lane (row, h) holds A bytes [32h, 32h+32)
-// as two 16-byte registers t = 0, 1; MFMA step t therefore contracts bytes
-// 32h + 16t of A with the same bytes of B (LDS chunk 2h + t).  Both operands
-// use the same map, so the dot products are unchanged (exactly so for int8).
-// ---------------------------------------------------------------------------
-constexpr int kAdStages = 4;        // B ring depth = A register sets
-
-template <int L, int NI> struct AdShape {
-    static constexpr int BM = 128;
-    static constexpr int BN = 32 * NI;
-    static constexpr int B_ROWS = L * BN;
-    // LDS rows per stage, rounded up to 64 so every wave DMAs whole 1 KB
-    // windows; the padding rows are filled from out-of-range offsets (zeros)
-    // and never read
-    static constexpr int B_ROWS_LDS = (B_ROWS + 63) / 64 * 64;
-    static constexpr int STAGE = B_ROWS_LDS * kDmaRowBytes;   // LDS bytes per stage
-    static constexpr int DPW = STAGE / (4 * 1024);            // B DMA instrs per wave per stage
-    static constexpr int APW = 2 * L;                         // A loads per lane per stage
-    static constexpr int PER_STAGE = DPW + APW;               // vmcnt units per stage
-    static constexpr int LDS_BYTES = kAdStages * STAGE;
-    static_assert(STAGE % 4096 == 0, "B stage must be whole 1 KB windows per wave");
-    static_assert(2 * PER_STAGE * 1 < 64, "vmcnt range");
-};
-
-template <typename ST, int L, int NI, typename AccT, bool TRI>
-__global__ __launch_bounds__(256, 1) void cross_gemm_ad_kernel(GemmParams p, int group_m,
-                                                               uint32_t a_records,
-                                                               uint32_t b_records) {
-    using Sh = AdShape<L, NI>;
-    using PS = Pairs<L, TRI>;
-    using MF = Mfma<ST>;
-    using Acc = typename MF::Acc;
-    using OA = AccT;   // outer accumulator: fp64 for fp64 output, else fp32 (store_c)
-    constexpr int BM = Sh::BM, BN = Sh::BN;
-    constexpr int ES = (int)sizeof(ST);
-    constexpr uint32_t kOOB = 0x80000000u;
-    extern __shared__ __attribute__((aligned(16))) char smem[];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int h = lane >> 5, lr = lane & 31;
-
-    const int64_t tiles_m = (p.M + BM - 1) / BM;
-    const int64_t tiles_n = (p.N + BN - 1) / BN;
-    const int64_t tiles = tiles_m * tiles_n;
-    const int64_t g = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
-    const int64_t bidx = g / tiles;
-    const int64_t t = g % tiles;
-    const int64_t width = (int64_t)group_m * tiles_n;
-    const int64_t first_m = (t / width) * group_m;
-    const int64_t gsz = (tiles_m - first_m < group_m) ? (tiles_m - first_m) : group_m;
-    const int64_t tm = first_m + (t % width) % gsz;
-    const int64_t tn = (t % width) / gsz;
-    const int64_t m0 = tm * BM, n0 = tn * BN;
-
-    const uint32_t kbytes = (uint32_t)(p.K * ES);
-    const int nkb = (int)((kbytes + kDmaRowBytes - 1) / kDmaRowBytes);
-
-    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)((const char *)p.A + bidx * p.as_b * ES), (short)0, (int)a_records, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)((const char *)p.B + bidx * p.bs_b * ES), (short)0, (int)b_records, 0x00020000);
-
-    // A: this lane's row of every slice; kOOB past the last row
-    const int64_t arow = m0 + wave * 32 + lr;
-    uint32_t aoff[L];
-#pragma unroll
-    for (int i = 0; i < L; ++i)
-        aoff[i] = (arow < p.M) ? (uint32_t)(((int64_t)i * p.as_l + arow * p.as_m) * ES) + 32 * h
-                               : kOOB;
-    // B: DMA windows of this wave (16 rows of 64 bytes each)
-    uint32_t bsrc[Sh::DPW];
-    int bchunk[Sh::DPW];
-#pragma unroll
-    for (int q = 0; q < Sh::DPW; ++q) {
-        const int pos = (wave * Sh::DPW + q) * 64 + lane;
-        const int r = pos >> 2;
-        bchunk[q] = (pos & 3) ^ ((r >> 2) & 3);
-        const int j = r / BN;
-        const int64_t n = n0 + r % BN;
-        bsrc[q] = (r < Sh::B_ROWS && n < p.N)
-                      ? (uint32_t)(((int64_t)j * p.bs_l + n * p.bs_n) * ES) : kOOB;
-    }
-
-    i32x4 areg[kAdStages][L][2];
-    auto issue_stage = [&](int kb, i32x4 (&ar)[L][2]) {
-        char *dst = smem + (kb % kAdStages) * Sh::STAGE + wave * Sh::DPW * 1024;
-#pragma unroll
-        for (int q = 0; q < Sh::DPW; ++q) {
-            const uint32_t kofs = (uint32_t)kb * kDmaRowBytes + bchunk[q] * 16;
-            const uint32_t vo = (bsrc[q] == kOOB || kofs >= kbytes) ? kOOB : bsrc[q] + kofs;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rB, (__attribute__((address_space(3))) void *)(dst + q * 1024), 16, vo, 0, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < L; ++i)
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const uint32_t kofs = (uint32_t)kb * kDmaRowBytes + 32 * h + 16 * u;
-                const uint32_t vo =
-                    (aoff[i] == kOOB || kofs >= kbytes) ? kOOB : aoff[i] + kofs - 32 * h;
-                ar[i][u] = __builtin_bit_cast(
-                    i32x4, __builtin_amdgcn_raw_buffer_load_b128(rA, vo, 0, 0));
-            }
-    };
-
-    Acc acc[L][L][NI];
-#pragma unroll
-    for (int i = 0; i < L; ++i)
-#pragma unroll
-        for (int j = 0; j < L; ++j)
-#pragma unroll
-            for (int c = 0; c < NI; ++c) acc[i][j][c] = MF::zero();
-
-    // B fragments of one step: rows j*BN + c*32 + lr, chunk 2h + tt
-    struct BFr {
-        i32x4 b[L][NI];
-    };
-    auto read_b = [&](const char *buf, int tt, int r, BFr &f) {
-        const int j = r / NI, c = r % NI;
-        f.b[j][c] = *(const i32x4 *)(buf + dswz(j * BN + c * 32 + lr, 2 * h + tt));
-    };
-    constexpr int kReads = L * NI;
-    constexpr int kMfmas = PS::N * NI;
-    auto step = [&](const i32x4 (&ar)[L][2], int tt, const BFr &cur, BFr &nxt,
-                    const char *nbuf, int ntt) {
-        static_for<kMfmas>([&](auto q_) {
-            constexpr int q = decltype(q_)::value;
-            constexpr int i = PS::i_of(q / NI), j = PS::j_of(q / NI), c = q % NI;
-            acc[i][j][c] = MF::run(ar[i][tt], cur.b[j][c], acc[i][j][c]);
-            if constexpr (q < kReads) read_b(nbuf, ntt, q, nxt);
-            __builtin_amdgcn_sched_barrier(0);
-        });
-#pragma unroll
-        for (int q = kMfmas; q < kReads; ++q) read_b(nbuf, ntt, q, nxt);
-    };
-    // The K loop runs a multiple of DEPTH stages: stages past the end load
-    // only out-of-range offsets (zeros), so their MFMAs add nothing, and the
-    // loop body stays free of branches (which keeps the compiler's own wait
-    // counts for the A registers exact).
-    constexpr int D = kAdStages;
-    const int nkb_pad = (nkb + D - 1) / D * D;
-    BFr f0, f1;
-    // One stage: step 0 (its B fragments f0 already in registers) with the
-    // step-1 reads interleaved; wait for this wave's loads of stage kb + 1
-    // (the D - 2 later stages may stay in flight), drain its LDS reads and
-    // synchronise, which publishes every wave's DMA writes of stage kb + 1
-    // and frees the slot of stage kb; step 1 with the reads of stage kb + 1's
-    // step-0 fragments; then refill this stage's LDS slot and A register set
-    // (whose last MFMA was just issued) with stage kb + D.
-    auto stage = [&](int kb, i32x4 (&ar)[L][2]) {
-        step(ar, 0, f0, f1, smem + (kb % D) * Sh::STAGE, 1);
-        wait_vmcnt<(D - 2) * Sh::PER_STAGE>();
-        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0) only
-        exec_barrier();
-        step(ar, 1, f1, f0, smem + ((kb + 1) % D) * Sh::STAGE, 0);
-        issue_stage(kb + D, ar);
-    };
-
-    if (nkb > 0) {
-#pragma unroll
-        for (int s = 0; s < D; ++s) issue_stage(s, areg[s]);
-        wait_vmcnt<(D - 1) * Sh::PER_STAGE>();
-        exec_barrier();
-#pragma unroll
-        for (int q = 0; q < kReads; ++q) read_b(smem, 0, q, f0);
-    }
-    for (int kb = 0; kb < nkb_pad; kb += D) {
-#pragma unroll
-        for (int s = 0; s < D; ++s) stage(kb + s, areg[s]);
-    }
-    // the last D stages issued only zero loads; let them land before the LDS
-    // is handed to another workgroup
-    wait_vmcnt<0>();
-
-    // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
-    const float *sab = p.sa + bidx * p.sas_b;
-    const float *sbb = p.sb + bidx * p.sbs_b;
-    const int64_t cbase = bidx * p.cs_b;
-#pragma unroll
-    for (int c = 0; c < NI; ++c) {
-        const int64_t col = n0 + c * 32 + lr;
-        const bool cok = col < p.N;
-        float sbv[L];
-#pragma unroll
-        for (int j = 0; j < L; ++j) sbv[j] = cok ? sbb[j * p.sbs_l + col * p.sbs_n] : 0.0f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int64_t row = m0 + wave * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-            if (cok && row < p.M) {
-                OA out = (OA)0;
-#pragma unroll
-                for (int i = 0; i < L; ++i) {
-                    const float sai = sab[i * p.sas_l + row * p.sas_m];
-#pragma unroll
-                    for (int j = 0; j < L; ++j) {
-                        if (!PS::kept(i, j)) continue;
-                        const float x = MF::to_f32(acc[i][j][c][r]);
-                        const float t1 = x * sai;
-                        const float t2 = t1 * sbv[j];
-                        out = out + (OA)t2;
-                    }
-                }
-                store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
-            }
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
 // Launch templates (host side)
 // ---------------------------------------------------------------------------
 // byte extent [0, bytes) one batch of a slice operand spans, or -1 if it does
@@ -2943,22 +2748,6 @@ static hipError_t launch_kstep(const GemmParams &p, const GemmPlan &plan, hipStr
     const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
     if (tiles == 0) return hipSuccess;
     hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(256 * G), Sh::LDS_BYTES, st, p,
-                       plan.group_m, (uint32_t)ea, (uint32_t)eb);
-    return hipGetLastError();
-}
-
-template <typename ST, int L, int NI, typename AccT, bool TRI>
-static hipError_t launch_ad(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
-    using Sh = AdShape<L, NI>;
-    auto kern = cross_gemm_ad_kernel<ST, L, NI, AccT, TRI>;
-    static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
-    if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
-    const int es = (int)sizeof(ST);
-    const int64_t ea = dma_extent(p.as_l, p.as_m, L, p.M, p.K, es);
-    const int64_t eb = dma_extent(p.bs_l, p.bs_n, L, p.N, p.K, es);
-    const int64_t tiles = p.batch * ((p.M + Sh::BM - 1) / Sh::BM) * ((p.N + Sh::BN - 1) / Sh::BN);
-    if (tiles == 0) return hipSuccess;
-    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(256), Sh::LDS_BYTES, st, p,
                        plan.group_m, (uint32_t)ea, (uint32_t)eb);
     return hipGetLastError();
 }
@@ -3095,10 +2884,6 @@ static hipError_t launch_one(const GemmParams &p, const GemmPlan &plan, hipStrea
     }
     if constexpr (L == 3) {
         if (plan.kind == kGemmWide) return launch_wide<ST, AccT, TRI>(p, plan, st);
-    }
-    if (plan.kind == kGemmAD) {
-        constexpr int ANI = (L == 1) ? 8 : (L == 2) ? 4 : 1;
-        return launch_ad<ST, L, ANI, AccT, TRI>(p, plan, st);
     }
     if (plan.kind == kGemmDMA) return launch_dma<ST, L, MI, NI, AccT, TRI>(p, plan, st);
     using Sh = GemmShape<L, MI, NI>;

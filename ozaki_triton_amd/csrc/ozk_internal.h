@@ -45,6 +45,12 @@ struct SplitParams {
     float *resid;  // workspace: exchange words of the cooperative kernels, the
                    // transposed operand [batch, rows, K] (transpose + row path) or
                    // the fp32 copy of a narrow input
+    // null: a cooperative launch is followed by its poison kernel (NaN scales
+    // and the device status if a wait gave up).  Else the launcher runs no
+    // poison kernel and stores the launch's status word here (left alone if
+    // the plan has no cooperative launch): the cross-GEMM that follows on
+    // the same stream takes the check over (GemmParams::split_fail).
+    const uint32_t **fail_out;
 };
 
 enum SplitPath {
@@ -93,6 +99,9 @@ hipError_t launch_split_duo(const SplitParams &pa, const SplitPlan &plan_a, cons
 // wait gave up (the split's scales are then NaN).  read_device_status waits
 // for `stream`, reads the word of the current device and clears it if asked.
 hipError_t read_device_status(unsigned *out, bool clear, hipStream_t stream);
+// Device address of the current device's sticky status word (asked once per
+// device), for kernels that record a failure themselves; null on error.
+uint32_t *device_status_word();
 
 // One cross-GEMM launch.  A slices [batch, L, M, K] and B slices presented as
 // [batch, L, N, K] (K-contiguous rows of B^T).  Strides in elements of the
@@ -120,12 +129,19 @@ struct GemmParams {
     int kb_per_split;
     uint32_t *kpart;
     uint32_t *kcount;
+    // Status word of the cooperative split that ran before this launch on the
+    // same stream in place of its poison kernel (SplitParams::fail_out), or
+    // null.  Non-zero there: every C entry is stored as NaN (0 in an int8 C)
+    // and workgroup 0 sets bit 0 of *dev_status, the device's sticky status.
+    const uint32_t *split_fail;
+    uint32_t *dev_status;
+    int failed;   // set on the device from *split_fail at kernel entry
 };
 
 enum GemmKind {
     kGemmStaged = 0,  // global -> VGPR -> LDS, 2 x 2 waves (any operand extent)
     kGemmDMA = 1,     // LDS-DMA ring for A and B, 2 x 2 waves
-    kGemmAD = 2,      // A streamed into VGPRs, B by LDS-DMA, 4 x 1 waves
+                      // (2: unused)
     kGemmPair = 3,    // LDS-DMA ring, 8 waves: 2 x 2 blocks x 2 halves of the slice pairs
     kGemmRing = 4,    // the pair split over a five-slot ring of half stages, DMA spread
                       // between the MFMAs (num_splits 3 and 4)

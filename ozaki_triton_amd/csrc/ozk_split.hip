@@ -60,6 +60,7 @@
 #include "ozk_common.h"
 #include "ozk_internal.h"
 
+#include <atomic>
 #include <stdlib.h>
 #include <string.h>
 
@@ -1352,6 +1353,10 @@ static hipError_t clear_slots(uint64_t *slot, int64_t n, hipStream_t st) {
 // Follows a cooperative launch whose status word is `status` (see
 // poison_scales_kernel).
 static hipError_t launch_poison(const SplitParams &p, const uint64_t *status, hipStream_t st) {
+    if (p.fail_out) {   // the cross-GEMM that follows checks the word instead
+        *p.fail_out = (const uint32_t *)status;
+        return hipSuccess;
+    }
     const int64_t n = p.batch * p.L * p.rows;
     const int64_t nb = (n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024;
     hipLaunchKernelGGL(poison_scales_kernel, dim3((unsigned)nb), dim3(256), 0, st,
@@ -1657,6 +1662,20 @@ hipError_t launch_split_duo(const SplitParams &pa, const SplitPlan &plan_a, cons
     if (pa.batch * pa.rows == 0 || pb.batch * pb.rows == 0 || pa.L == 0) return hipSuccess;
     return x_dtype == 0 ? launch_duo_x<double>(pa, plan_a.variant, pb, plan_b.variant, slice_dtype, st)
                         : launch_duo_x<float>(pa, plan_a.variant, pb, plan_b.variant, slice_dtype, st);
+}
+
+uint32_t *device_status_word() {
+    static std::atomic<uint32_t *> cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    uint32_t *ptr = cached[dev].load(std::memory_order_acquire);
+    if (!ptr) {
+        void *addr = nullptr;
+        if (hipGetSymbolAddress(&addr, HIP_SYMBOL(g_device_status)) != hipSuccess) return nullptr;
+        ptr = (uint32_t *)addr;
+        cached[dev].store(ptr, std::memory_order_release);
+    }
+    return ptr;
 }
 
 hipError_t read_device_status(unsigned *out, bool clear, hipStream_t st) {

@@ -519,7 +519,7 @@ def test_debug_hooks_reject_unknown_names():
     L = _lib.load()
     assert L.ozk_debug_force_gemm_kernel(b"fastest") == _lib.OZK_ERR_DTYPE
     assert L.ozk_debug_force_split_kernel(b"fastest") == _lib.OZK_ERR_DTYPE
-    for k in (b"staged", b"dma", b"ad", b"pair", b"ring", b"wide", b"wide4", b"solo5", b"",
+    for k in (b"staged", b"dma", b"pair", b"ring", b"wide", b"wide4", b"solo5", b"",
               None):
         assert L.ozk_debug_force_gemm_kernel(k) == 0
     for k in (b"coop", b"strip", b"transpose", b"generic", b"rows", b"rowscoop", None):

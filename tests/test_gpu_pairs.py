@@ -2,7 +2,7 @@
 cross-GEMM sums every slice pair, ozaki_triton.py:403-447): C sums only the
 pairs i + j <= L - 1, in the reference's i-major / j-minor order.
 
-Every kernel that takes the set (staged, dma, ad, kstep, wide, wide4, pair, solo5) runs it
+Every kernel that takes the set (staged, dma, kstep, wide, wide4, pair, solo5) runs it
 forced and must equal the oracle's triangular sum bit for bit: int8 slices on
 random values, float slices on integer values (exact in fp32 in any order,
 tests/helpers.py:int_valued_slices).  The oracle's triangular sum is pinned on
@@ -35,7 +35,7 @@ def _cross(ozk, gpu, As, BsT, sa, sb, L, out, pairs):
 
 
 TRI_KERNELS = [("staged", 2), ("staged", 3), ("staged", 4), ("dma", 2), ("dma", 3), ("dma", 4),
-               ("ad", 2), ("ad", 3), ("ad", 4), ("kstep", 2), ("kstep", 3), ("kstep", 4),
+               ("kstep", 2), ("kstep", 3), ("kstep", 4),
                ("kstep2", 2), ("kstep2", 3), ("kstep2", 4),
                ("wide", 3), ("wide4", 4), ("pair", 3), ("pair", 4), ("pair", 5), ("solo5", 5)]
 
@@ -163,3 +163,4 @@ def test_triangular_c3_five_slices(oracle, gpu):
     rows, cols = sample_indices(8192, 64, 21), sample_indices(8192, 64, 22)
     check_block_vs_oracle(oracle, ozk, C_np, A_np, B_np, rows, cols, 5, torch.int8,
                           torch.float64, "C3 triangular block", pairs="triangular")
+

@@ -375,13 +375,13 @@ def test_ozaki_matmul_degenerate_shapes(gpu):
                          torch.randn(0, 3, dtype=torch.float64, device=gpu), 2, torch.int8)
 
 
-@pytest.mark.parametrize("kernel", ["staged", "dma", "ad", "pair", "ring", "wide", "wide4",
+@pytest.mark.parametrize("kernel", ["staged", "dma", "pair", "ring", "wide", "wide4",
                                     "kstep", "kstep2"])
 @pytest.mark.parametrize("L", [1, 2, 3, 4])
 def test_cross_gemm_each_kernel_bitexact(oracle, gpu, L, kernel, force):
     """Every cross-GEMM kernel, forced: the VGPR-staged one (taken when an
     operand's extent exceeds the 31-bit buffer offsets of the LDS-DMA kernels),
-    the 2 x 2 LDS-DMA kernel, the A-direct kernel, the pair-split kernel, its
+    the 2 x 2 LDS-DMA kernel, the pair-split kernel, its
     five-slot ring form (L >= 3; for L <= 2 the request falls back to the
     2 x 2 kernel), the wide kernel (L = 3), the 96 x 64 wide kernel (L = 4;
     otherwise the default kernel) and the K-step kernel (32 x 32 tiles)."""
@@ -410,7 +410,6 @@ def test_cross_gemm_each_kernel_bitexact(oracle, gpu, L, kernel, force):
     ("dma", 2, 130, 136, 1040),
     ("staged", 2, 100, 72, 1040),
     ("staged", 4, 100, 72, 520),
-    ("ad", 3, 100, 72, 1040),
     ("kstep", 4, 100, 72, 1040),    # (fp32 slices at L = 4: the planner's kernel)
     ("kstep", 3, 130, 72, 4096),
     ("kstep", 2, 64, 96, 2064),
@@ -1279,7 +1278,7 @@ def test_split_columns_default_plan(oracle, gpu, xdt, sdt, batch, N, K, L):
                  f"default {xdt} {sdt} b{batch} {N}x{K} L{L}")
 
 
-@pytest.mark.parametrize("kernel", ["", "dma", "ring", "pair", "ad", "staged", "wide", "wide4",
+@pytest.mark.parametrize("kernel", ["", "dma", "ring", "pair", "staged", "wide", "wide4",
                                     "solo5", "kstep", "kstep2"])
 @pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
 @pytest.mark.parametrize("K", [1, 2, 3, 5, 7, 9, 255, 257, 1003])
@@ -1294,7 +1293,7 @@ def test_packed_rows_last_piece(oracle, gpu, kernel, sdt, K, force):
     import ozaki_triton_amd as ozk
     if kernel:
         force(gemm=kernel)
-    L = (3 if kernel == "wide" else 4 if kernel in ("ring", "pair", "ad", "wide4", "kstep", "kstep2")
+    L = (3 if kernel == "wide" else 4 if kernel in ("ring", "pair", "wide4", "kstep", "kstep2")
          else 5 if kernel == "solo5" else 2)
     A, B = c3_like((1, 33, K), (1, K, 20), seed=K + 100)
     C = ozk.ozaki_matmul(A.to(gpu), B.to(gpu), L, sdt, max_splits=L)
