@@ -532,7 +532,21 @@ def main():
     e1.record()
     e1.synchronize()
     copy_gbs = 2.0 * csrc.numel() / (e0.elapsed_time(e1) / 10 * 1e-3) / 1e9
-    del csrc, cdst
+    del cdst
+    # the same with the split's own mix of 2 bytes read per byte written (at
+    # C3: 8-byte inputs read, 4 one-byte slices written): torch's elementwise
+    # add of two 512 MiB byte arrays into a third
+    ca, cb = csrc[: 1 << 29], csrc[1 << 29:]
+    cc = torch.empty_like(ca)
+    for _ in range(3):
+        torch.add(ca, cb, out=cc)
+    e0.record()
+    for _ in range(10):
+        torch.add(ca, cb, out=cc)
+    e1.record()
+    e1.synchronize()
+    copy21_gbs = 3.0 * ca.numel() / (e0.elapsed_time(e1) / 10 * 1e-3) / 1e9
+    del csrc, ca, cb, cc
 
     t_split_b = avg_ms("split_b", "split_a")
     t_split_a = avg_ms("split_a", "cross_gemm")
@@ -634,6 +648,8 @@ def main():
             "ms_b": round(t_split_b, 4),
             "device_copy_GBps": round(copy_gbs, 1),
             "of_device_copy": round(split_gbs / copy_gbs, 4),
+            "device_2to1_GBps": round(copy21_gbs, 1),
+            "of_device_2to1": round(split_gbs / copy21_gbs, 4),
         },
     }
     if not args.no_cpu:

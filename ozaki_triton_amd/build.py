@@ -103,5 +103,22 @@ def build_c_example(verbose: bool = False) -> str:
     return out
 
 
+def build_power_probe(verbose: bool = False) -> str:
+    """Compile tests/mfma_power_probe.hip, the MFMA rate / clock probe that the
+    cross-GEMM's roofline discussion is measured with (test tool, not part of
+    the library)."""
+    root = os.path.dirname(HERE)
+    src = os.path.join(root, "tests", "mfma_power_probe.hip")
+    out = os.path.join(root, "tests", "mfma_power_probe")
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-Wall",
+           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", src, "-o", out]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"mfma_power_probe build failed:\n{res.stdout}")
+    return out
+
+
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))

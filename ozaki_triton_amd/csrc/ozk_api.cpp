@@ -235,7 +235,7 @@ static int cross_gemm_impl(const void *A_slices, const int64_t a_strides[4], con
                    const int64_t sb_strides[3], int64_t batch, int64_t M, int64_t N, int64_t K,
                    int num_splits, int slice_dtype, int pairs, void *C, int out_dtype,
                    const int64_t c_strides[3], void *workspace, size_t workspace_bytes,
-                   void *stream, const uint32_t *split_fail = nullptr) {
+                   void *stream, const uint32_t *const split_fail[2] = nullptr) {
     if (!a_strides || !b_strides || !sa_strides || !sb_strides || !c_strides)
         return OZK_ERR_NULL;
     if (!is_slice_dtype(slice_dtype) || !is_input_dtype(out_dtype)) return OZK_ERR_DTYPE;
@@ -266,10 +266,12 @@ static int cross_gemm_impl(const void *A_slices, const int64_t a_strides[4], con
     p.out_dtype = out_dtype;
     // one slice is one pair in either set
     p.tri = pairs == OZK_PAIRS_TRIANGULAR && num_splits >= 2;
-    p.split_fail = split_fail;
+    p.split_fail[0] = split_fail ? split_fail[0] : nullptr;
+    p.split_fail[1] = split_fail ? split_fail[1] : nullptr;
     p.dev_status = nullptr;
     p.failed = 0;
-    if (split_fail && !(p.dev_status = ozk::device_status_word())) return OZK_ERR_LAUNCH;
+    if ((p.split_fail[0] || p.split_fail[1]) && !(p.dev_status = ozk::device_status_word()))
+        return OZK_ERR_LAUNCH;
     if (num_splits == 0) return hip_status(ozk::launch_zero_c(p, st));
     if (!A_slices || !B_slices || !A_scales || !B_scales) return OZK_ERR_NULL;
 
@@ -532,18 +534,22 @@ int ozk_matmul_pairs(const void *A, const int64_t a_strides[3], const void *B,
         ozk::split_workspace_bytes(pa, plan_a, dtype, slice_dtype) > lay.scratch_bytes)
         return OZK_ERR_WORKSPACE;
     pb.resid = pa.resid = (float *)(ws + lay.scratch);
-    // The status word of the last cooperative launch before the cross-GEMM
-    // goes to the cross-GEMM, which stores a NaN C and sets the device status
-    // if a wait gave up, in place of the poison kernel after that launch.
-    // That is B's split when it shares the launch with A's or when A's split
-    // uses no scratch (which would overwrite B's status word), else A's
-    // (B's split then keeps its poison kernel).
-    const uint32_t *split_fail = nullptr;
-    if (ozk::split_pair_ok(plan_a, plan_b, dtype) ||
-        ozk::split_workspace_bytes(pa, plan_a, dtype, slice_dtype) == 0)
-        pb.fail_out = &split_fail;
-    else
-        pa.fail_out = &split_fail;
+    // The status words of the cooperative split launches go to the
+    // cross-GEMM, which stores a NaN C and sets the device status if a wait
+    // gave up, in place of the poison kernels after those launches.  A's split
+    // runs last, so its word survives until then; B's word is the last 8
+    // bytes of B's share of the scratch, and survives A's split where A's
+    // share ends before it (else B keeps its poison kernel).  Both splits in
+    // one launch: B's word, the only one.
+    const uint32_t *split_fail[2] = {nullptr, nullptr};
+    const size_t wa = ozk::split_workspace_bytes(pa, plan_a, dtype, slice_dtype);
+    const size_t wb = ozk::split_workspace_bytes(pb, plan_b, dtype, slice_dtype);
+    if (ozk::split_pair_ok(plan_a, plan_b, dtype)) {
+        pb.fail_out = &split_fail[1];
+    } else {
+        pa.fail_out = &split_fail[0];
+        if (wa + 8 <= wb) pb.fail_out = &split_fail[1];
+    }
     if ((e = record(events, 0, st)) != OZK_OK) return e;
     if (ozk::split_pair_ok(plan_a, plan_b, dtype)) {
         // both in one launch; the second event marks the same point (the B

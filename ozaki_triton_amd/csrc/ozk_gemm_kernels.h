@@ -132,16 +132,20 @@ OZK_DEV void store_c(const GemmParams &p, int64_t idx, float v) {
     }
 }
 
-// Kernel entry: reads the status word of the cooperative split that ran
+// Kernel entry: reads the status words of the cooperative splits that ran
 // before on the same stream (complete when the kernel starts) into p.failed,
 // and records a failure in the device's sticky status (one lane).
 OZK_DEV void resolve_split_fail(GemmParams &p) {
     p.failed = 0;
-    if (!p.split_fail) return;
-    // a scalar load (the constant address space): the word does not change
+    // scalar loads (the constant address space): the words do not change
     // while the kernel runs, and the value stays in a scalar register
-    p.failed = *(const __attribute__((address_space(4))) uint32_t *)(uintptr_t)p.split_fail != 0;
-    if (p.failed && blockIdx.x == 0 && threadIdx.x == 0)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        if (p.split_fail[i] &&
+            *(const __attribute__((address_space(4))) uint32_t *)(uintptr_t)p.split_fail[i] != 0)
+            p.failed = 1;
+    if (!p.failed) return;
+    if (blockIdx.x == 0 && threadIdx.x == 0)
         __hip_atomic_fetch_or(p.dev_status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 

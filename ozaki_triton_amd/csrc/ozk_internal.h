@@ -129,13 +129,14 @@ struct GemmParams {
     int kb_per_split;
     uint32_t *kpart;
     uint32_t *kcount;
-    // Status word of the cooperative split that ran before this launch on the
-    // same stream in place of its poison kernel (SplitParams::fail_out), or
-    // null.  Non-zero there: every C entry is stored as NaN (0 in an int8 C)
-    // and workgroup 0 sets bit 0 of *dev_status, the device's sticky status.
-    const uint32_t *split_fail;
+    // Status words of the cooperative splits that ran before this launch on
+    // the same stream in place of their poison kernels (SplitParams::fail_out),
+    // or null.  Non-zero in either: every C entry is stored as NaN (0 in an
+    // int8 C) and workgroup 0 sets bit 0 of *dev_status, the device's sticky
+    // status.
+    const uint32_t *split_fail[2];
     uint32_t *dev_status;
-    int failed;   // set on the device from *split_fail at kernel entry
+    int failed;   // set on the device from the split_fail words at kernel entry
 };
 
 enum GemmKind {

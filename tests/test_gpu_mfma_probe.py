@@ -1,0 +1,29 @@
+"""The MFMA rate probe (tests/mfma_power_probe.hip, built by build()): with
+constant operands and no memory traffic a v_mfma_i32_32x32x32_i8 stream
+reaches the dense INT8 peak the cross-GEMM's roofline divides by (5.0 POP/s),
+and the probe's clock reading is a plausible shader clock.  The other cases
+(operands from registers, the LDS, the LDS plus DMA) are reported, not judged:
+their rates depend on the power limit."""
+import json
+import os
+import subprocess
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def test_mfma_probe_reaches_the_published_peak(gpu):
+    exe = os.path.join(os.path.dirname(os.path.abspath(__file__)), "mfma_power_probe")
+    if not os.path.exists(exe):
+        pytest.fail("tests/mfma_power_probe is not built: run __graft_entry__.build()")
+    print("[probe] mfma_power_probe --quick", flush=True)
+    r = subprocess.run([exe, "--quick"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    cases = {d["case"]: d for d in (json.loads(ln) for ln in r.stdout.splitlines())
+             if "case" in d}
+    assert set(cases) == {"const", "random_regs", "lds", "lds_dma", "lds_dma_miss", "zeros"}
+    assert cases["const"]["frac_of_int8_peak"] >= 0.9, cases["const"]
+    for d in cases.values():
+        assert 0.05 < d["frac_of_int8_peak"] <= 1.05, d
+        assert 0.3 < d["clock_GHz"] < 3.0, d

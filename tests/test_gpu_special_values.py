@@ -111,17 +111,21 @@ def test_matmul_nan_and_signed_zero_int8(oracle, gpu, xdt, shape):
     assert_bitwise_equal(got, want, f"matmul {xdt} {shape}")
 
 
-@pytest.mark.parametrize("case", ["pair_f64", "coop_f32", "rowscoop_f64", "int8_input"])
+@pytest.mark.parametrize("case", ["pair_f64", "coop_f32", "rowscoop_f64", "int8_input",
+                                  "int8_poison"])
 def test_matmul_wait_timeout_reported_by_cross_gemm(gpu, case, force):
     """Every cooperative wait forced to give up at its first check (a tag no
     member writes): the kernels still finish; C is NaN everywhere (a float
     C) or 0 everywhere (an int8 C: its conversion maps NaN to 0); the device
-    status reports OZK_ERR_DEVICE_WAIT once.  The cases take the deferred
-    check on each route: B's columns in one launch with A's rows (pair_f64),
-    B's cooperative split before A's row kernel, which uses no scratch
-    (coop_f32), A's shared row kernel after B's cooperative split, whose
-    poison kernel runs (rowscoop_f64), and narrow inputs converted into the
-    workspace, then split by the shared row kernel (int8_input).  The normal path afterwards sets no status."""
+    status reports OZK_ERR_DEVICE_WAIT once.  The cases take each route:
+    B's columns in one launch with A's rows, the cross-GEMM checking B's
+    status word (pair_f64); B's cooperative split before A's row kernel
+    (coop_f32); B's cooperative split and A's shared row kernel, both words
+    checked by the cross-GEMM (rowscoop_f64); narrow inputs converted into
+    the workspace, then split by the shared row kernel, both words checked
+    by the cross-GEMM (int8_input), or, where A's converted copy covers B's
+    status word, B's poison kernel and A's word (int8_poison).  The normal
+    path afterwards sets no status."""
     import ozaki_triton_amd as ozk
     from ozaki_triton_amd import _lib
     g = torch.Generator().manual_seed(5)
@@ -138,9 +142,11 @@ def test_matmul_wait_timeout_reported_by_cross_gemm(gpu, case, force):
         B = torch.randn(20000, 16, generator=g, dtype=torch.float64)
     else:
         # both converted into K-contiguous fp32 copies, whose 40000-long rows
-        # take the shared row kernel (three members per row)
+        # take the shared row kernel (three members per row); with 4 columns
+        # B's share of the scratch is smaller than A's
         A = torch.randint(-100, 100, (40, 40000), generator=g, dtype=torch.int8)
-        B = torch.randint(-100, 100, (40000, 64), generator=g, dtype=torch.int8)
+        n = 4 if case == "int8_poison" else 64
+        B = torch.randint(-100, 100, (40000, n), generator=g, dtype=torch.int8)
     Ad, Bd = A.to(gpu), B.to(gpu)
     ozk.device_status()                       # clear anything older
     force(coop_timeout=True)
