@@ -40,10 +40,21 @@ int ozk_debug_force_split_kernel(const char *name);
 /*
  * on != 0: every cooperative split wait of later calls on this thread gives
  * up at its first check (it looks for a tag that is never written), so the
- * timeout path runs: the split's scales become NaN and the sticky device
- * status is set (ozk_device_status).  No kernel waits longer than one poll.
+ * timeout path runs: after ozk_split the split's scales become NaN, after
+ * ozk_matmul C does (0 for an int8 C), and the sticky device status is set
+ * (ozk_device_status).  No kernel waits longer than one poll.
  */
 int ozk_debug_force_coop_timeout(int on);
+
+/*
+ * The workgroups one XCD holds for the cooperative split kernels (their
+ * occupancy per CU times the CUs of one XCD, 32 on gfx950), written to
+ * *resident_out (may be NULL).  The split planner gives a cooperative group
+ * at most that many members minus 8, so that every group becomes resident.
+ * force > 0: later plans on this thread assume `force` instead; 0: the
+ * current device's figure again; < 0: no change.
+ */
+int ozk_debug_coop_residency(int force, int *resident_out);
 
 /*
  * Force the split-K ranges of later calls on this thread whose cross-GEMM

@@ -51,6 +51,7 @@ EXPORTED_DEBUG = (
     "ozk_debug_force_gemm_ksplit",
     "ozk_debug_force_split_kernel",
     "ozk_debug_force_coop_timeout",
+    "ozk_debug_coop_residency",
     "ozk_debug_gemm_kernel",
     "ozk_debug_gemm_kernel_pairs",
     "ozk_debug_split_kernel",
@@ -120,6 +121,8 @@ def load() -> ctypes.CDLL:
     L.ozk_debug_force_split_kernel.restype = i32
     L.ozk_debug_force_coop_timeout.argtypes = [i32]
     L.ozk_debug_force_coop_timeout.restype = i32
+    L.ozk_debug_coop_residency.argtypes = [i32, ctypes.POINTER(ctypes.c_int)]
+    L.ozk_debug_coop_residency.restype = i32
     L.ozk_debug_force_gemm_ksplit.argtypes = [i32]
     L.ozk_debug_force_gemm_ksplit.restype = i32
     L.ozk_debug_gemm_kernel.argtypes = [i64, i64, i64, i64, i32, i32, i32,

@@ -694,6 +694,12 @@ int ozk_debug_force_coop_timeout(int on) {
     return OZK_OK;
 }
 
+int ozk_debug_coop_residency(int force, int *resident_out) {
+    if (force >= 0) ozk::debug_overrides().coop_resident = force;
+    if (resident_out) *resident_out = ozk::coop_resident_per_xcd();
+    return OZK_OK;
+}
+
 int ozk_debug_gemm_kernel(int64_t batch, int64_t M, int64_t N, int64_t K, int num_splits,
                           int slice_dtype, int cus, const char **name_out, int *ksplit_out) {
     return ozk_debug_gemm_kernel_pairs(batch, M, N, K, num_splits, slice_dtype, OZK_PAIRS_ALL,

@@ -28,6 +28,8 @@ struct DebugOverrides {
     int split = kForceSplitNone;
     int coop_timeout = 0;   // 1: every cooperative wait gives up at once (its timeout path)
     int ksplit = 0;         // > 0: split-K ranges of the ring and wide kernels (0: the planner's)
+    int coop_resident = 0;  // > 0: workgroups one XCD holds for the cooperative split kernels
+                            // (0: the current device's)
 };
 DebugOverrides &debug_overrides();
 
@@ -81,6 +83,10 @@ size_t split_workspace_bytes(const SplitParams &p, const SplitPlan &plan, int x_
                              int slice_dtype);
 hipError_t launch_split(const SplitParams &p, const SplitPlan &plan, int x_dtype,
                         int slice_dtype, hipStream_t stream);
+// Workgroups one XCD of the current device holds for the cooperative split
+// kernels (the debug override, if set); a cooperative group has at most this
+// many members minus 8
+int coop_resident_per_xcd();
 // Both splits of a matmul in one launch (split_pair_kernel): A's rows by a
 // 4-wave row configuration and B's columns by the cooperative kernel, fp64
 // input, no split kernel forced by the test hooks.  pb.resid holds B's

@@ -551,14 +551,15 @@ __global__ __launch_bounds__(NT) void split_strip_kernel(SplitParams p) {
 //     and polls the P * SW words of its group and level with agent-scope
 //     loads until all carry the tag.  Every word validates itself, so no
 //     fence (no L2 write-back or invalidation) is needed;
-//   * the members of a group are consecutive workgroup ids.  Workgroups are
-//     dispatched in id order, so the group of the oldest resident workgroup
-//     is entirely resident once P + 8 is below the workgroups that fit an
-//     XCD (two or three per CU: 64 or more); the planner keeps P <= 32.  A wait is still bounded (2 s of the
-//     100 MHz real-time counter): a member that gives up sets the launch's
-//     status word, member 0 stores NaN scales, and the poison kernel that
-//     follows the launch makes every scale of the split NaN and records the
-//     failure in the sticky device status (ozk_device_status).
+//   * the members of a group are consecutive workgroup ids, and the planner
+//     keeps P at most 8 below the workgroups one XCD holds (the residency
+//     limit before plan_split_raw), so every group becomes resident and its
+//     waits end.  A wait is still bounded (2 s of the 100 MHz real-time
+//     counter): a member that gives up sets the launch's status word and
+//     member 0 stores NaN scales.  After ozk_split the poison kernel then
+//     makes every scale of the split NaN and records the failure in the
+//     sticky device status (ozk_device_status); in a matmul the cross-GEMM
+//     reads the status word instead, writes NaN for C and records it.
 // slot and the status word after it must be zero at launch (the launcher
 // clears them first).
 // ---------------------------------------------------------------------------
@@ -566,7 +567,8 @@ constexpr int kCoopNT = 256;
 constexpr int kCoopMaxP = 32;
 constexpr int64_t kCoopMinColumnBytes = 64 * 1024;
 // rows kernel shared by workgroups: 256 lanes, 64 (fp32) or 32 (fp64) values
-// per lane, for rows longer than 16384 elements, at most 64 chunks
+// per lane, for rows longer than 16384 elements, at most 64 chunks by its own
+// layout (one polling lane each) and 56 by the residency limit on MI355X
 constexpr int kRowsCoopVariant = 100;
 constexpr int64_t kRowsCoopMinK = 16384;
 constexpr int kRowsCoopMaxP = 64;
@@ -1222,6 +1224,79 @@ static SplitParams converted_params(const SplitParams &p) {
     return q;
 }
 
+// ---------------------------------------------------------------------------
+// Residency limit of the cooperative kernels.  The members of a group are
+// consecutive workgroup ids and workgroups are dispatched in id order.  While
+// the group of the oldest unfinished workgroup is not wholly resident, every
+// workgroup that holds back the next id is a member of that group: the ids
+// before it have finished, the next id is the group's own.  If the hardware
+// sends each id to a fixed XCD, that XCD is full of members; if to any XCD
+// with room, every XCD is.  Either way the group has more members than one
+// XCD holds, so a group of at most that many (less a margin of 8) always
+// becomes resident and its waits end.  One XCD holds the kernels' occupancy
+// (the fewest workgroups per CU over every kernel that waits) times its CUs:
+// 32 on gfx950, or all of a smaller partition.  Asked once per device; where
+// the runtime cannot say (no device: a workspace query on a host without a
+// GPU) MI355X's figure is assumed: 2 workgroups per CU (the kernels with
+// 169-205 VGPRs, one wave per SIMD each, fit twice in 512), so 64 per XCD
+// and at most 56 members (the row kernel's 64 chunks are cut to 56).
+// ---------------------------------------------------------------------------
+constexpr int kCusPerXcd = 32;
+constexpr int kMi355xResident = 2 * kCusPerXcd;
+
+template <typename Kern> static void min_occupancy(Kern kernel, int &occ, bool &ok) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kCoopNT, 0) != hipSuccess ||
+        n <= 0) {
+        ok = false;
+        return;
+    }
+    occ = n < occ ? n : occ;
+}
+
+template <typename ST> static void coop_occupancy(int &occ, bool &ok) {
+    min_occupancy(split_rows_coop_kernel<double, ST, 4, 8>, occ, ok);
+    min_occupancy(split_rows_coop_kernel<float, ST, 4, 16>, occ, ok);
+    min_occupancy(split_coop_kernel<double, ST, 32, 8>, occ, ok);
+    min_occupancy(split_coop_kernel<double, ST, 32, 2>, occ, ok);
+    min_occupancy(split_coop_kernel<float, ST, 16, 8>, occ, ok);
+    min_occupancy(split_coop_kernel<float, ST, 16, 2>, occ, ok);
+    min_occupancy(split_pair_kernel<double, ST, 32, 4>, occ, ok);
+    min_occupancy(split_pair_kernel<double, ST, 32, 8>, occ, ok);
+}
+
+int coop_resident_per_xcd() {
+    if (debug_overrides().coop_resident > 0) return debug_overrides().coop_resident;
+    static std::atomic<int> cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return kMi355xResident;
+    int r = cached[dev].load(std::memory_order_relaxed);
+    if (r > 0) return r;
+    int cus = 0, occ = 1 << 20;
+    bool ok = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) ==
+                  hipSuccess && cus > 0;
+    if (ok) {
+        coop_occupancy<int8_t>(occ, ok);
+        coop_occupancy<_Float16>(occ, ok);
+        coop_occupancy<__bf16>(occ, ok);
+        coop_occupancy<float>(occ, ok);
+    }
+    if (!ok) {
+        (void)hipGetLastError();   // a failed query is not a launch error
+        return kMi355xResident;
+    }
+    r = occ * (cus < kCusPerXcd ? cus : kCusPerXcd);
+    cached[dev].store(r, std::memory_order_relaxed);
+    return r;
+}
+
+// the most members a cooperative group may have on the current device (at
+// least 1: a group of one never waits)
+static int64_t coop_member_limit(int64_t kernel_max) {
+    const int64_t r = (int64_t)coop_resident_per_xcd() - 8;
+    return r < 1 ? 1 : (r < kernel_max ? r : kernel_max);
+}
+
 static SplitPlan plan_split_raw(const SplitParams &p, int x_dtype, int slice_dtype) {
     // narrow inputs: the reference loads them into its fp32 RES exactly
     // (ozaki_triton.py:188), so they are converted into the workspace first and
@@ -1240,7 +1315,7 @@ static SplitPlan plan_split_raw(const SplitParams &p, int x_dtype, int slice_dty
     const int force = debug_overrides().split;
     auto forced = [&](int which) { return force == which; };
     // long rows: the row kernel shared by workgroups
-    const bool rows_coop = rows_coop_members(p.K, xsz) <= kRowsCoopMaxP &&
+    const bool rows_coop = rows_coop_members(p.K, xsz) <= coop_member_limit(kRowsCoopMaxP) &&
                            (forced(kForceSplitRowsCoop) || (!forced(kForceSplitRows) && p.K > kRowsCoopMinK));
     if (k4 && slice_ok && p.xs_k == 1 && aligned(p.X, 16) && (p.xs_r * xsz) % 16 == 0 &&
         (p.xs_b * xsz) % 16 == 0 && !forced(kForceSplitGeneric)) {
@@ -1266,14 +1341,15 @@ static SplitPlan plan_split_raw(const SplitParams &p, int x_dtype, int slice_dty
     // 394.2 / 1197 for M x N = 128 x 2048, 1024 x 4096, 2048 x 8192, while 1
     // slice is 7-11% slower and 2 even.  A forced coop takes it for any length
     // it holds
-    const bool coop_fits = cols_ok && coop_members(p.K, xsz, 8) <= kCoopMaxP;
+    const int64_t coop_max = coop_member_limit(kCoopMaxP);
+    const bool coop_fits = cols_ok && coop_members(p.K, xsz, 8) <= coop_max;
     // columns too long for 32 chunks of 128-byte groups: 32-byte groups, whose
     // chunks hold 4x the rows, when the cooperative kernel is forced.  By
     // default such columns are transposed instead: at config 5 (fp32, K =
     // 65536, 32 chunks of 2048 rows) the 32-byte groups took 0.255-0.265 ms
     // against 0.216 ms for the transpose path, the exchange waiting on 32
     // members per group.
-    const bool coop2_fits = cols_ok && !coop_fits && coop_members(p.K, xsz, 2) <= kCoopMaxP;
+    const bool coop2_fits = cols_ok && !coop_fits && coop_members(p.K, xsz, 2) <= coop_max;
     const bool other = forced(kForceSplitStrip) || forced(kForceSplitTranspose) || forced(kForceSplitGeneric);
     const bool coop_long = p.K * xsz >= kCoopMinColumnBytes ||
                            (xsz == 8 && ssz == 1 && p.L <= 2 &&

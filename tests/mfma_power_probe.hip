@@ -172,13 +172,15 @@ struct Ctx {
 };
 
 template <int MODE>
-int run_case(const char *name, const Ctx &c, int iters, int launches, int miss_every, int zero) {
+int run_case(const char *name, const Ctx &c, int iters, int launches, int warm, int miss_every,
+             int zero) {
     const size_t lds = kOpLds + (MODE == kLdsDma ? kDmaLds : 0);
     auto k = probe<MODE>;
     CHECK(hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize,
                               (int)lds));
     const int8_t *sb = zero ? c.zero_small : c.small_buf, *bb = zero ? c.zero_big : c.big_buf;
-    for (int w = 0; w < 2; ++w)
+    // untimed launches first (about 0.1 s): the clock settles to the load
+    for (int w = 0; w < warm; ++w)
         hipLaunchKernelGGL(k, dim3(c.cus), dim3(kThreads), lds, 0, iters, sb, c.small_bytes, bb,
                            c.big_bytes, miss_every, zero, c.out, c.clk);
     CHECK(hipGetLastError());
@@ -246,15 +248,16 @@ int main(int argc, char **argv) {
     CHECK(hipMalloc(&c.clk, (size_t)c.cus * 2 * sizeof(unsigned long long)));
     printf("{\"cus\": %d, \"wall_clock_MHz\": %.1f, \"quick\": %s}\n", c.cus, c.rtc_hz / 1e6,
            quick ? "true" : "false");
-    // about 10 ms per launch at the peak rate; 30 launches (quick: 5 of 2 ms)
-    const int iters = quick ? 6144 : 32768, launches = quick ? 5 : 30;
+    // about 10 ms per launch at the peak rate; 30 launches after 10 (quick: 5
+    // of 2 ms after 50)
+    const int iters = quick ? 6144 : 32768, launches = quick ? 5 : 30, warm = quick ? 50 : 10;
     int rc = 0;
-    rc |= run_case<kConst>("const", c, iters, launches, 0, 0);
-    rc |= run_case<kRegs>("random_regs", c, iters, launches, 0, 0);
-    rc |= run_case<kLds>("lds", c, iters, launches, 0, 0);
-    rc |= run_case<kLdsDma>("lds_dma", c, iters, launches, 0, 0);
-    rc |= run_case<kLdsDma>("lds_dma_miss", c, iters, launches, 5, 0);
-    rc |= run_case<kLdsDma>("zeros", c, iters, launches, 5, 1);
+    rc |= run_case<kConst>("const", c, iters, launches, warm, 0, 0);
+    rc |= run_case<kRegs>("random_regs", c, iters, launches, warm, 0, 0);
+    rc |= run_case<kLds>("lds", c, iters, launches, warm, 0, 0);
+    rc |= run_case<kLdsDma>("lds_dma", c, iters, launches, warm, 0, 0);
+    rc |= run_case<kLdsDma>("lds_dma_miss", c, iters, launches, warm, 5, 0);
+    rc |= run_case<kLdsDma>("zeros", c, iters, launches, warm, 5, 1);
     CHECK(hipFree(c.small_buf));
     CHECK(hipFree(c.big_buf));
     CHECK(hipFree(c.zero_small));

@@ -679,3 +679,62 @@ def test_workspace_covers_both_pair_sets():
     # wide split-K: 1 tile x 4 ranges x 8 waves x 144 registers x 64 lanes x 4 bytes
     wide = 1 * 4 * 8 * 144 * 64 * 4
     assert nb.value >= wide
+
+
+def _residency(L, force):
+    got = ctypes.c_int(0)
+    assert L.ozk_debug_coop_residency(force, ctypes.byref(got)) == 0
+    return got.value
+
+
+@pytest.mark.parametrize("resident,max_rows_members,max_col_members",
+                         [(None, 56, 32), (72, 64, 32), (40, 32, 32), (24, 16, 16), (9, 1, 1)])
+def test_coop_member_limit_follows_residency(resident, max_rows_members, max_col_members):
+    """A cooperative group's members wait on each other, so the planner gives a
+    group at most (workgroups one XCD holds - 8) members, and never more than
+    the kernel's own maximum (64 row chunks, 32 column chunks).  With no GPU
+    the MI355X figure is assumed (2 workgroups per CU x 32 CUs per XCD: at
+    most 56 members); the override stands in for other devices (a partition
+    whose XCD holds fewer).  Longer operands fall to the kernels that do not
+    wait."""
+    from ozaki_triton_amd import _lib
+    L = _lib.load()
+    try:
+        if resident is not None:
+            assert _residency(L, resident) == resident
+        else:
+            assert _residency(L, 0) == 64
+        nsp, sd, xd = 3, 4, 0                       # fp64 into int8 slices
+        rows_chunk, col_chunk = 4 * 8 * 256, 1024   # fp64 elements per member
+
+        def plan(K, xs, rows):
+            ss = [nsp * rows * K, rows * K, K, 1]
+            return _split_plan(L, 0x10000, xd, 1, rows, K, xs, nsp, sd, 0x20000, ss)
+
+        def row_path(K):
+            # the shared row kernel from 16384 elements while its chunks fit the
+            # limit; else the plain row kernel (up to 32768 fp64) or the generic one
+            if K > 16384 and -(-K // rows_chunk) <= max_rows_members:
+                return "rowscoop"
+            return "rows" if K <= 32768 else "generic"
+
+        for P in (3, max_rows_members, max_rows_members + 1, 65):
+            K = P * rows_chunk
+            assert plan(K, [4 * K, K, 1], 4)[0] == row_path(K), P
+        # columns of 64 KB and more: the cooperative column kernel while its
+        # chunks fit the limit; else the strip kernel (K <= 16384) or a
+        # transpose into the row path
+        rows = 4096
+        for P in (8, 16, max_col_members, max_col_members + 1, 33):
+            K = P * col_chunk
+            name = plan(K, [K * rows, 1, rows], rows)[0]
+            if 8 <= P <= max_col_members:   # 64 KB columns and longer
+                want = "coop"
+            elif K <= 16384:
+                want = "strip"
+            else:
+                want = {"rowscoop": "transposerowscoop", "rows": "transpose",
+                        "generic": "generic"}[row_path(K)]
+            assert name == want, (P, name)
+    finally:
+        _residency(L, 0)

@@ -69,6 +69,48 @@ def test_split_rows_coop_long(oracle, gpu, xdt, sdt, batch, rows, K, L):
     _check_split(oracle, ozk, X.to(xdt).to(gpu), L, sdt, f"rowscoop {xdt} {sdt} {rows}x{K}")
 
 
+def _coop_residency():
+    import ctypes
+    from ozaki_triton_amd import _lib
+    got = ctypes.c_int(0)
+    assert _lib.load().ozk_debug_coop_residency(-1, ctypes.byref(got)) == 0
+    return got.value
+
+
+def test_coop_residency_matches_the_host_assumption(gpu):
+    """One XCD of an MI355X holds 64 workgroups of every cooperative split
+    kernel (2 per CU, the fewest over the kernels, x 32 CUs): the figure the
+    planner assumes where it sees no device, so a workspace query on such a
+    host plans as the device does.  A build that changes the kernels'
+    registers can change it; the library's assumption must follow."""
+    torch.zeros(1, device=gpu)
+    r = _coop_residency()
+    print(f"cooperative split kernels: {r} workgroups per XCD", flush=True)
+    assert r == 64
+
+
+@pytest.mark.parametrize("xdt,sdt", [(torch.float64, torch.int8), (torch.float32, torch.float16)])
+def test_split_beyond_the_residency_limit(oracle, gpu, xdt, sdt, force):
+    """A device assumed to hold 16 workgroups per XCD (as a small partition
+    might): groups of more than 8 members are not planned, so rows of 9
+    chunks take the generic kernel and 64 KB+ columns the strip kernel, with
+    the oracle's bits."""
+    import ozaki_triton_amd as ozk
+    force(coop_resident=16)
+    assert _coop_residency() == 16
+    xsz = torch.empty(0, dtype=xdt).element_size()
+    g = torch.Generator().manual_seed(16)
+    K = 9 * (8192 if xsz == 8 else 16384)
+    X = torch.randn(1, 3, K, generator=g, dtype=torch.float64)
+    X = X * torch.pow(2.0, torch.randint(-8, 9, (1, 3, 1), generator=g).double())
+    _check_split(oracle, ozk, X.to(xdt).to(gpu), 3, sdt, f"rows beyond residency {xdt} {K}")
+    K = 9216 if xsz == 8 else 16384                 # 72 / 64 KB columns: 9 / 32 chunks
+    B = torch.randn(1, K, 16, generator=g, dtype=torch.float64)
+    B = B * torch.pow(2.0, torch.randint(-8, 9, (1, 1, 16), generator=g).double())
+    _check_split(oracle, ozk, B.to(xdt).to(gpu).transpose(-1, -2), 3, sdt,
+                 f"columns beyond residency {xdt} {K}")
+
+
 @pytest.mark.parametrize("xdt,sdt", COMBOS)
 @pytest.mark.parametrize("L", [1, 3, 4])
 @pytest.mark.parametrize("N,K", [(8, 256), (40, 1000), (96, 2048), (24, 8192), (16, 16000)])

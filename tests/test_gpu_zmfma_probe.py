@@ -1,9 +1,12 @@
 """The MFMA rate probe (tests/mfma_power_probe.hip, built by build()): with
 constant operands and no memory traffic a v_mfma_i32_32x32x32_i8 stream
-reaches the dense INT8 peak the cross-GEMM's roofline divides by (5.0 POP/s),
-and the probe's clock reading is a plausible shader clock.  The other cases
-(operands from registers, the LDS, the LDS plus DMA) are reported, not judged:
-their rates depend on the power limit."""
+reaches the dense INT8 peak the cross-GEMM's roofline divides by (5.0 POP/s):
+at least 0.85 of it (0.96-0.99 measured once the clock has settled; the
+probe warms each case for about 0.1 s), and the probe's clock reading is a
+plausible shader clock.  The other cases (operands from registers, the LDS,
+the LDS plus DMA) are reported, not judged: their rates depend on the power
+limit.  The file name sorts after the parity tests, so that a box whose clock
+runs low fails this measurement after them, not before."""
 import json
 import os
 import subprocess
@@ -23,7 +26,7 @@ def test_mfma_probe_reaches_the_published_peak(gpu):
     cases = {d["case"]: d for d in (json.loads(ln) for ln in r.stdout.splitlines())
              if "case" in d}
     assert set(cases) == {"const", "random_regs", "lds", "lds_dma", "lds_dma_miss", "zeros"}
-    assert cases["const"]["frac_of_int8_peak"] >= 0.9, cases["const"]
+    assert cases["const"]["frac_of_int8_peak"] >= 0.85, cases["const"]
     for d in cases.values():
         assert 0.05 < d["frac_of_int8_peak"] <= 1.05, d
         assert 0.3 < d["clock_GHz"] < 3.0, d

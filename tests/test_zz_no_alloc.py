@@ -4,6 +4,7 @@ workspace entry point ozk_matmul on the same inputs, bit for bit, on calls in
 a row (a smaller one after a larger one, then the larger one again), and
 against the OZK_STATIC_SCRATCH_BYTES limit."""
 import ctypes
+import gc
 
 import pytest
 import torch
@@ -31,16 +32,23 @@ def _matmul(static, A, B, L, xd, sd, batch):
         # the device at all (free device memory; the runtime places the
         # library's scratch array, like the kernels' code, in device memory
         # when the module is first used on the device, so _warm_up runs a
-        # call first)
-        torch.cuda.synchronize()
-        before = torch.cuda.memory_allocated()
-        free0 = torch.cuda.mem_get_info()[0]
-        st = lib.ozk_matmul_static(ctypes.c_void_p(A.data_ptr()), a_st,
-                                   ctypes.c_void_p(B.data_ptr()), b_st, xd, batch, M, N, K, L,
-                                   sd, ctypes.c_void_p(C.data_ptr()), c_st, None, stream)
-        torch.cuda.synchronize()
-        assert torch.cuda.memory_allocated() == before
-        assert torch.cuda.mem_get_info()[0] == free0, "device memory was allocated"
+        # call first).  Python's cycle collector is held off meanwhile: a
+        # collection could free other tests' tensors inside the window.
+        gc.collect()
+        gc.disable()
+        try:
+            torch.cuda.synchronize()
+            before = torch.cuda.memory_allocated()
+            free0 = torch.cuda.mem_get_info()[0]
+            st = lib.ozk_matmul_static(ctypes.c_void_p(A.data_ptr()), a_st,
+                                       ctypes.c_void_p(B.data_ptr()), b_st, xd, batch, M, N, K,
+                                       L, sd, ctypes.c_void_p(C.data_ptr()), c_st, None, stream)
+            torch.cuda.synchronize()
+            allocated, free1 = torch.cuda.memory_allocated(), torch.cuda.mem_get_info()[0]
+        finally:
+            gc.enable()
+        assert allocated <= before, (allocated, before)
+        assert free1 >= free0, ("device memory was allocated", free0, free1)
         return st, C
     nb = ctypes.c_size_t(0)
     assert lib.ozk_matmul_workspace_bytes(xd, batch, M, N, K, a_st, b_st, L, sd,
