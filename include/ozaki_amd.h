@@ -83,8 +83,10 @@ int ozk_version(void);
  * Sticky device status -- no counterpart in the reference, whose kernels have
  * no bounded waits.  The cooperative split kernels (long columns of B, long
  * rows of A) combine their level maxima across workgroups with waits bounded
- * at 2 s.  A wait that gives up makes every scale of that split NaN (so C is
- * NaN, never silently wrong) and sets a per-device status word.  This call
+ * at 2 s.  A wait that gives up sets a per-device status word and marks what
+ * the split feeds: after ozk_split every scale of that split is NaN; after
+ * ozk_matmul every entry of C is NaN (0 in an int8 C, see
+ * OZK_ERR_DEVICE_WAIT), never a silently wrong value.  This call
  * waits for `stream`, reads the current device's word into *status_out
  * (OZK_OK or OZK_ERR_DEVICE_WAIT) and clears it when `clear` is non-zero.
  * Calls are asynchronous, so a failure is seen by the first status read

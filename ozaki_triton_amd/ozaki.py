@@ -114,8 +114,10 @@ def compute_split_bits(n: int, slice_dtype: torch.dtype = torch.float16,
 def device_status(clear: bool = True) -> None:
     """Raise if a cooperative split wait gave up on the current device since
     the last check (no counterpart in the reference, whose kernels have no
-    bounded waits).  Such a split's scales, and every C computed from them,
-    are NaN.  Waits for the current stream; ``clear`` resets the status."""
+    bounded waits).  What such a split fed is marked: after ``split_matrix``
+    its scales are NaN, after ``ozaki_matmul`` every entry of C is NaN (0 in
+    an int8 C, where only this check tells it from a valid result).  Waits
+    for the current stream; ``clear`` resets the status."""
     stream = torch.cuda.current_stream().cuda_stream
     st = _lib.device_status(clear, stream)
     if st != _lib.OZK_OK:
