@@ -2185,6 +2185,8 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide4_kernel(GemmParams p, 
     // fetched by dword DMA into the buffer of stage nkb, which holds no stage
     // the tile still reads, at the start of the last stage: instruction
     // u < NSC (wave u and wave u - 8) fetches entries 64 u .. 64 u + 63.
+    // The lane is read where the scales are fetched (lane_here), so that
+    // their offsets are not computed before the K loop and held through it.
     char *const scl = buf(nkb);
     auto issue_scales = [&]() {
 #pragma unroll
@@ -2192,7 +2194,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide4_kernel(GemmParams p, 
             const int u = q * Sh::NW + wave;
             if (u >= Sh::NSC) break;
             const bool isa = u < L * BM / 64;
-            const int e = (isa ? u : u - L * BM / 64) * 64 + lane;
+            const int e = (isa ? u : u - L * BM / 64) * 64 + lane_here();
             const int s = isa ? e / BM : e / BN;                 // slice
             const int64_t rc = isa ? m0 + e % BM : n0 + e % BN;  // row of A / column of B
             const int64_t ext = isa ? ((int64_t)(L - 1) * p.sas_l + (p.M - 1) * p.sas_m + 1)
@@ -2316,7 +2318,12 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide4_kernel(GemmParams p, 
     wait_vmcnt<0>();
     __builtin_amdgcn_s_waitcnt(0xC07F);
     exec_barrier();
-    const int ct = wy * 32 + lr;
+    // the epilogue's lane values are read afresh (lane_here), so that none is
+    // held through the K loop, where the registers are all taken and such
+    // values were spilled to scratch
+    const int elane = lane_here();
+    const int eh = elane >> 5;
+    const int ct = wy * 32 + (elane & 31);
     const int64_t col = n0 + ct;
     const int64_t cbase = bidx * p.cs_b;
     float sbv[L];
@@ -2324,7 +2331,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide4_kernel(GemmParams p, 
     for (int j = 0; j < L; ++j) sbv[j] = sb_lds[j * BN + ct];
     // rows of accumulator registers 4 q .. 4 q + 3 of A fragment u, inside the
     // tile, start at row4(u, q): their 4 scales are one 16-byte LDS read
-    auto row4 = [&](int u, int q) { return (last_i ? u * 32 : wx * 32) + 8 * q + 4 * h; };
+    auto row4 = [&](int u, int q) { return (last_i ? u * 32 : wx * 32) + 8 * q + 4 * eh; };
     auto sa4 = [&](int i, int u, int q) {
         return *(const f32x4 *)(sa_lds + i * BM + row4(u, q));
     };
@@ -2375,7 +2382,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide4_kernel(GemmParams p, 
                         const float t1 = MF::to_f32(acc[i][j][r]) * s4[i][e];
                         out = out + (OA)(t1 * sbv[j]);
                     }
-                part[(wave * 16 + r) * 64 + lane] = out;
+                part[(wave * 16 + r) * 64 + elane] = out;
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -2391,7 +2398,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide4_kernel(GemmParams p, 
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int64_t row = m0 + row4(u, r >> 2) + (r & 3);
-                OA out = part[((u * 2 + wy) * 16 + r) * 64 + lane];
+                OA out = part[((u * 2 + wy) * 16 + r) * 64 + elane];
 #pragma unroll
                 for (int j = 0; j < (TRI ? 1 : L); ++j) out = out + (OA)tv[j][r];
                 if (col < p.N && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
