@@ -2408,6 +2408,420 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide4_kernel(GemmParams p, 
 }
 
 // ---------------------------------------------------------------------------
+// The num_splits 4 wide kernel on 16 x 16 x 64 MFMAs (int8 slices:
+// v_mfma_i32_16x16x64_i8).  At the chip's power limit the rate is set by the
+// energy of each MFMA's operands, and one 16 x 16 x 64 instruction moves a
+// quarter of the accumulator registers of a 32 x 32 x 32 one for half its
+// work: on random int8 data with wide4's LDS reads and DMA per MFMA, a probe
+// of the two streams ran 0.58 against 0.53 of the dense peak.
+// Tile, waves, pair assignment, LDS stages and DMA are wide4's.  A K step is
+// 64 bytes (two per 128-byte stage).  Lane l of a fragment reads row l % 16 of
+// 16 rows, bytes 16 (l / 16) .. + 15 of the step; the instruction pairs the
+// same bytes of A and B, so the int32 dot products are wide4's exactly.  A
+// wave's 12 accumulator tiles of 32 x 32 become 48 of 16 x 16,
+// acc[u][j][rh][ch] (row half rh, column half ch of its 32 x 32 blocks), whose
+// register e of lane l holds row 16 rh + 4 (l / 16) + e, column 16 ch + l % 16.
+// Per K step a wave reads 6 A fragments p = (u, rh) and 8 B fragments g =
+// (j, ch) and runs 48 MFMAs, B-outer: the A fragments stay in registers and
+// each is re-read for the next step right after its last MFMA (6 MFMAs before
+// its next use); B fragment g + 1 is read while g's 6 MFMAs run.  So the
+// step's own B fragments come from the LDS during the step, and the stage
+// barrier sits before the last B fragment's group of the stage's second step:
+// every wave has then read the stage, whose buffer the DMA of stage kb + 2
+// refills from that group on, and stage kb + 1 has landed for the next step's
+// reads.  Registers: 192 accumulators, 24 for A, 8 for B (wide4: 192, 24, 16).
+// ---------------------------------------------------------------------------
+// At two waves per SIMD a wave has 256 registers, which the compiler splits
+// into 128 VGPRs and 128 AGPRs once AGPRs are used; left to itself it keeps
+// all 192 accumulator registers in VGPRs beside the fragments, and the K loop
+// spills.  So the MFMAs are placed by hand: the accumulators of u = 1, 2 (128
+// registers) in the AGPRs, those of u = 0 (64) in VGPRs, which the epilogue
+// reads first.  Hazards the
+// compiler's recogniser cannot see into the inline assembly: an accumulator
+// is first read as srcC after its zero fill and 8 wait states, accumulated
+// again only 48 MFMAs later, and read by other instructions only in the
+// epilogue, after 64 wait states.  The fragment registers an MFMA reads as
+// srcA / srcB may be rewritten by the next LDS read right after it (srcA /
+// srcB are read as the instruction issues).
+template <typename ST> struct Mfma16;
+template <> struct Mfma16<int8_t> {
+    using Acc = i32x4;
+    OZK_DEV static Acc zero() { return Acc{0}; }
+    template <bool AG> OZK_DEV static void run(Acc &c, i32x4 a, i32x4 b) {
+        if constexpr (AG) asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+        else asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+    }
+    OZK_DEV static float to_f32(int x) { return (float)x; }
+};
+
+template <typename ST, typename AccT, bool TRI>
+__global__ __launch_bounds__(512, 1) void cross_gemm_wide4q_kernel(GemmParams p, int group_m,
+                                                                   uint32_t a_records,
+                                                                   uint32_t b_records) {
+    resolve_split_fail(p);
+    using Sh = Wide4Shape;
+    using MF = Mfma16<ST>;
+    using Acc = typename MF::Acc;
+    using OA = AccT;
+    constexpr int L = Sh::L, BM = Sh::BM, BN = Sh::BN;
+    constexpr int ES = (int)sizeof(ST);
+    constexpr uint32_t kOOB = 0x80000000u;
+    constexpr int P1 = 4;   // DMA instructions of stage kb + 2 in the groups after the barrier
+    static_assert(Sh::NW == 8 && Sh::LA == 6 && Sh::LB == 4 && BM == 96 && BN == 64,
+                  "the window arithmetic below is written for this shape");
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool last_i = wave >= 6;                 // holds the pairs i = 3
+    const int wy = last_i ? wave - 6 : (wave & 1);
+    const int wx = last_i ? 0 : (wave >> 1);
+
+    const int64_t tiles_m = (p.M + BM - 1) / BM;
+    const int64_t tiles_n = (p.N + BN - 1) / BN;
+    const int64_t tiles = tiles_m * tiles_n;
+    const int64_t g = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
+    const int64_t bidx = g / tiles;
+    const int64_t t = g % tiles;
+    const int64_t width = (int64_t)group_m * tiles_n;
+    const int64_t first_m = (t / width) * group_m;
+    const int64_t gsz = (tiles_m - first_m < group_m) ? (tiles_m - first_m) : group_m;
+    const int64_t tm = first_m + (t % width) % gsz;
+    const int64_t tn = (t % width) / gsz;
+    const int64_t m0 = tm * BM, n0 = tn * BN;
+
+    const uint32_t kbytes = (uint32_t)(p.K * ES);
+    const int nkb = (int)((kbytes + kDmaRB - 1) / kDmaRB);
+
+    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const char *)p.A + bidx * p.as_b * ES), (short)0, (int)a_records, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const char *)p.B + bidx * p.bs_b * ES), (short)0, (int)b_records, 0x00020000);
+
+    // Stage DMA, wide4's windows: a 1 KB window is 8 whole 128-byte rows
+    // (lane -> row lane / 8, physical chunk lane % 8, which holds logical
+    // chunk c0 = (lane % 8) ^ (lane / 16) in an even window and c0 ^ 4 in an
+    // odd one).  Wave w fetches A windows 6 w .. 6 w + 5 (slice w / 2, rows
+    // m0 + 48 (w % 2) + 8 q) and B windows 4 w .. 4 w + 3 (slice w / 2, rows
+    // n0 + 32 (w % 2) + 8 q), so a window's parity is that of q.  The source
+    // offset of window q of stage kb is base + q step + 128 kb, plus the
+    // lane's part (4 registers: A / B, parity); the bounds are tested per lane
+    // only where a window has fewer than 8 rows in the operand or the stage
+    // runs past K.
+    const int half = wave & 1, wsl = wave >> 1;
+    const int64_t a_first = m0 + 48 * half, b_first = n0 + 32 * half;
+    const uint32_t a_base = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)(((int64_t)wsl * p.as_l + a_first * p.as_m) * ES));
+    const uint32_t b_base = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)(((int64_t)wsl * p.bs_l + b_first * p.bs_n) * ES));
+    const uint32_t a_step = (uint32_t)__builtin_amdgcn_readfirstlane((int)(8 * p.as_m * ES));
+    const uint32_t b_step = (uint32_t)__builtin_amdgcn_readfirstlane((int)(8 * p.bs_n * ES));
+    // windows whose 8 rows are all inside the operand, and stages whose 128
+    // bytes are all inside K
+    const int a_full = (int)(p.M - a_first <= 0 ? 0 : ((p.M - a_first) / 8 < 6 ? (p.M - a_first) / 8 : 6));
+    const int b_full = (int)(p.N - b_first <= 0 ? 0 : ((p.N - b_first) / 8 < 4 ? (p.N - b_first) / 8 : 4));
+    const int nkb_full = (int)(kbytes / kDmaRB);
+    uint32_t lane_src[2][2];   // [A, B][window parity]
+    {
+        const int lrow = lane >> 3;
+        const int c0 = (lane & 7) ^ (lane >> 4);
+#pragma unroll
+        for (int par = 0; par < 2; ++par) {
+            const uint32_t chb = (uint32_t)(par ? (c0 ^ 4) : c0) * 16;
+            lane_src[0][par] = (uint32_t)(lrow * p.as_m * ES) + chb;
+            lane_src[1][par] = (uint32_t)(lrow * p.bs_n * ES) + chb;
+        }
+    }
+    auto buf = [&](int kb) { return smem + (kb & 1) * Sh::STAGE; };
+    // DMA instruction q (< LA: A window q of this wave; else B window q - LA)
+    // of stage kb; q is a constant at every call
+    auto issue = [&](int kb, int q) {
+        const bool isa = q < Sh::LA;
+        const int qq = isa ? q : q - Sh::LA;
+        const uint32_t ub = (isa ? a_base + (uint32_t)qq * a_step : b_base + (uint32_t)qq * b_step) +
+                            (uint32_t)kb * kDmaRB;
+        const uint32_t lsrc = lane_src[isa ? 0 : 1][qq & 1];
+        uint32_t vo;
+        if (qq < (isa ? a_full : b_full) && kb < nkb_full) {
+            vo = lsrc + ub;
+        } else {
+            const int64_t first = (isa ? a_first : b_first) + 8 * qq;
+            const int64_t rl = (isa ? p.M : p.N) - first;
+            const int rows_left = (int)(rl < 8 ? rl : 8);               // may be <= 0
+            const int kleft = (int)kbytes - kb * kDmaRB;                // > 0
+            const int ln = lane_here();
+            const int c0 = (ln & 7) ^ (ln >> 4);
+            const int chb = ((qq & 1) ? (c0 ^ 4) : c0) * 16;
+            vo = ((ln >> 3) < rows_left && chb < kleft) ? lsrc + ub : kOOB;
+        }
+        auto *ldsp = (__attribute__((address_space(3))) void *)(
+            buf(kb) + (isa ? 0 : Sh::A_BYTES) + (wave * (isa ? Sh::LA : Sh::LB) + qq) * 1024);
+        if (isa) __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, ldsp, 16, vo, 0, 0, 0);
+        else __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, ldsp, 16, vo, 0, 0, 0);
+    };
+    // the tile's scales, as in wide4: into the buffer of stage nkb during the
+    // last stage (the lane read where they are fetched), at the start of the
+    // LDS (nkb even) or at its end (nkb odd), so that the rest of it is one
+    // free range for the epilogue
+    char *const scl = (nkb & 1) ? smem + 2 * Sh::STAGE - Sh::NSC * 256 : smem;
+    auto issue_scales = [&]() {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int u = q * Sh::NW + wave;
+            if (u >= Sh::NSC) break;
+            const bool isa = u < L * BM / 64;
+            const int e = (isa ? u : u - L * BM / 64) * 64 + lane_here();
+            const int s = isa ? e / BM : e / BN;                 // slice
+            const int64_t rc = isa ? m0 + e % BM : n0 + e % BN;  // row of A / column of B
+            const int64_t ext = isa ? ((int64_t)(L - 1) * p.sas_l + (p.M - 1) * p.sas_m + 1)
+                                    : ((int64_t)(L - 1) * p.sbs_l + (p.N - 1) * p.sbs_n + 1);
+            const bool ok = rc < (isa ? p.M : p.N);
+            const uint32_t vo = ok ? (uint32_t)(((int64_t)s * (isa ? p.sas_l : p.sbs_l) +
+                                                 rc * (isa ? p.sas_m : p.sbs_n)) * 4)
+                                   : kOOB;
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)(isa ? p.sa + bidx * p.sas_b : p.sb + bidx * p.sbs_b), (short)0,
+                (int)(ext * 4 < 0x7FFFFFFF ? ext * 4 : 0x7FFFFFFF), 0x00020000);
+            auto *ldsp = (__attribute__((address_space(3))) void *)(scl + u * 256);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, ldsp, 4, vo, 0, 0, 0);
+        }
+    };
+    const float *sa_lds = (const float *)scl, *sb_lds = (const float *)(scl + L * BM * 4);
+
+    // prologue: stages 0 and 1; stage 0 must land before the first reads
+#pragma unroll
+    for (int q = 0; q < Sh::LPS; ++q) issue(0, q);
+    if (nkb > 1) {
+#pragma unroll
+        for (int q = 0; q < Sh::LPS; ++q) issue(1, q);
+        wait_vmcnt<Sh::LPS>();
+    } else {
+        wait_vmcnt<0>();
+    }
+    exec_barrier();
+
+    // Fragment rows start at multiples of 16, so the swizzle key of a lane's
+    // row, ((row >> 1) & 7), is that of lane % 16 for every fragment.  Per K
+    // step a wave computes the address of its A region's and B region's row
+    // 0 for its lane once; each fragment is a constant offset from it (the
+    // LDS read's immediate).
+    const int qrow = lane & 15;
+    const int key = (qrow >> 1) & 7;
+    int lane_rd[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) lane_rd[kk] = qrow * kDmaRB + (((4 * kk + (lane >> 4)) ^ key) << 4);
+    const int smem_base = (int)(uintptr_t)(__attribute__((address_space(3))) char *)smem;
+    using lds_cptr = const __attribute__((address_space(3))) char *;
+    const int a_org = (last_i ? 3 * BM : wx * 32) * kDmaRB;
+    const int b_org = Sh::A_BYTES + wy * 32 * kDmaRB;
+    auto region = [&](int kb, int kk, int org) {
+        const int u = __builtin_amdgcn_readfirstlane(smem_base + (kb & 1) * Sh::STAGE + org);
+        return (lds_cptr)(uintptr_t)(u + lane_rd[kk]);
+    };
+
+    i32x4 fa[6];   // A fragments (u, rh), resident through a K step
+    i32x4 fb[4];   // B fragments g .. g + 3 (g mod 4)
+    Acc acc[3][L][2][2];
+#pragma unroll
+    for (int u = 0; u < 3; ++u)
+#pragma unroll
+        for (int j = 0; j < L; ++j)
+#pragma unroll
+            for (int rh = 0; rh < 2; ++rh)
+#pragma unroll
+                for (int ch = 0; ch < 2; ++ch) {
+                    acc[u][j][rh][ch] = MF::zero();
+                    // pinned where the hand-placed MFMAs keep it
+                    if (u > 0) asm volatile("" : "+a"(acc[u][j][rh][ch]));
+                    else asm volatile("" : "+v"(acc[u][j][rh][ch]));
+                }
+    asm volatile("s_nop 7" ::: "memory");
+
+    // A fragment (u, rh) of a K step: row 16 rh of the step's A region for u
+    // (a_org + u * a_rstep rows), B fragment (j, ch): row j * BN + 16 ch of
+    // its B region; 16 rh and j * BN + 16 ch are the LDS reads' immediates
+    const int a_rstep = (last_i ? 32 : BM) * kDmaRB;   // bytes between A fragments u and u + 1
+    auto read_a = [&](lds_cptr ra, int rh) {
+        return *(const __attribute__((address_space(3))) i32x4 *)(ra + 16 * rh * kDmaRB);
+    };
+    auto read_b = [&](lds_cptr rb, int gb) {   // B fragment gb = (j, ch)
+        return *(const __attribute__((address_space(3))) i32x4 *)(
+            rb + ((gb >> 1) * BN + 16 * (gb & 1)) * kDmaRB);
+    };
+    // One K step on the fragments of stage ckb, step ckk (fa and fb hold its
+    // A fragments and B fragments 0, 1 on entry).  Group gb runs the 6 MFMAs
+    // of B fragment gb and first reads B fragment gb + 2 (groups 6, 7: B
+    // fragments 0, 1 of the next step, stage nkb_, step nkk); in group 7, each
+    // A fragment of the next step is read right after its last MFMA.  With
+    // `bar`, group 6 starts behind the stage barrier.  DMA instructions [lo,
+    // hi) of stage dkb are spread over the MFMAs of groups dg0 .. 7 (lo, hi
+    // and dg0 are constants at every call).
+    auto stepq = [&](int ckb, int ckk, int nkb_, int nkk, bool bar, int dkb, bool on, int lo,
+                     int hi, int dg0) {
+        const int cnt = hi - lo;
+        const int span = (8 - dg0) * 6;
+        const lds_cptr rb_cur = region(ckb, ckk, b_org);
+#pragma unroll
+        for (int gb = 0; gb < 8; ++gb) {
+            if (gb < 6) {
+                fb[(gb + 2) & 3] = read_b(rb_cur, gb + 2);
+            } else {
+                if (gb == 6 && bar) {
+                    // stage nkb_ has landed (this wave's DMA, then every
+                    // wave's through the barrier), and every wave's reads of
+                    // stage ckb are complete before its buffer is refilled
+                    wait_vmcnt<0>();
+                    __builtin_amdgcn_s_waitcnt(0xC07F);
+                    exec_barrier();
+                }
+                fb[(gb + 2) & 3] = read_b(region(nkb_, nkk, b_org), gb - 6);
+            }
+            const int j = gb >> 1, ch = gb & 1;
+#pragma unroll
+            for (int pa = 0; pa < 6; ++pa) {
+                const int u = pa >> 1, rh = pa & 1;
+                // the pair (u, j) in a wave of the first kind, (3, j) in one of the second
+                const bool first = !TRI || u + j <= L - 1, second = !TRI || j == 0;
+                auto mfma = [&]() {
+                    if (u > 0) MF::template run<true>(acc[u][j][rh][ch], fa[pa], fb[gb & 3]);
+                    else MF::template run<false>(acc[u][j][rh][ch], fa[pa], fb[gb & 3]);
+                };
+                if (first && second) {
+                    mfma();
+                } else if (first || second) {
+                    if (first != last_i) mfma();
+                }
+                if (gb == 7) fa[pa] = read_a(region(nkb_, nkk, a_org + u * a_rstep), rh);
+                const int n = (gb - dg0) * 6 + pa;
+#pragma unroll
+                for (int d = 0; d < Sh::LPS; ++d) {
+                    // instruction lo + d goes after MFMA (d * span) / cnt of the span
+                    if (gb >= dg0 && d < cnt && (d * span) / cnt == n && on) issue(dkb, lo + d);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+
+    if (nkb > 0) {
+#pragma unroll
+        for (int pa = 0; pa < 6; ++pa) fa[pa] = read_a(region(0, 0, a_org + (pa >> 1) * a_rstep), pa & 1);
+        const lds_cptr rb0 = region(0, 0, b_org);
+        fb[0] = read_b(rb0, 0);
+        fb[1] = read_b(rb0, 1);
+    }
+    static_assert(kDmaRB / 64 == 2, "two 64-byte K steps per stage");
+    if (nkb == 0) issue_scales();
+    for (int kb = 0; kb < nkb; ++kb) {
+        const bool nb = kb + 1 < nkb, n2 = kb + 2 < nkb;
+        // no DMA is outstanding in the last stage: its waits are unaffected
+        if (!nb) issue_scales();
+        // the rest of stage kb + 1 (stage 1 went out whole in the prologue)
+        stepq(kb, 0, kb, 1, false, kb + 1, nb && kb >= 1, P1, Sh::LPS, 0);
+        // groups 6, 7 read stage kb + 1's step 0 (unused past the end) and
+        // start stage kb + 2 in stage kb's buffer
+        stepq(kb, 1, kb + 1, 0, nb, kb + 2, n2, 0, P1, 6);
+    }
+
+    // the hand-placed MFMAs' results are read below: 64 wait states first
+    asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory");
+
+    // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
+    wait_vmcnt<0>();
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    exec_barrier();
+    // the epilogue's lane values are read afresh (lane_here), not held
+    // through the K loop
+    const int elane = lane_here();
+    const int eq = elane & 15, eg = elane >> 4;
+    float sbv[L][2];
+#pragma unroll
+    for (int j = 0; j < L; ++j)
+#pragma unroll
+        for (int ch = 0; ch < 2; ++ch) sbv[j][ch] = sb_lds[j * BN + wy * 32 + 16 * ch + eq];
+    // rows of registers 0..3 of row half rh of A fragment u, inside the tile,
+    // start at row4(u, rh): their 4 scales are one 16-byte LDS read
+    auto row4 = [&](int u, int rh) { return (last_i ? u * 32 : wx * 32) + 16 * rh + 4 * eg; };
+    auto sa4 = [&](int i, int u, int rh) {
+        return *(const f32x4 *)(sa_lds + i * BM + row4(u, rh));
+    };
+    // Every wave turns its accumulator tiles into t = fl32(fl32(fl32(acc) *
+    // sa_i) * sb_j), tile by tile in one order (u, j, rh, ch), each tile dead
+    // after it: a wave of the first kind adds them to the running sums of its
+    // 16 elements (the pairs i = u = 0..2, j = 0..3 of its block: i-major,
+    // j-minor), one of the second kind (the pairs (3, j) of block u) stores
+    // them to the LDS.  After the barrier the first kind adds the (3, j) terms
+    // of its block in order and stores C.  T: [wave - 6][u][j][rh, ch][lane]
+    // x 4 floats, 96 KB in the free range of the LDS.
+    float *const tsm = (float *)(smem + ((nkb & 1) ? 0 : 4096));
+    static_assert(4096 + 2 * 3 * L * 4 * 64 * 16 <= 2 * Sh::STAGE - Sh::NSC * 256 &&
+                      Sh::NSC * 256 <= 4096,
+                  "the t values fit beside the scales");
+    auto tslot = [&](int w6, int u, int j, int q) {
+        return (f32x4 *)(tsm + ((((w6 * 3 + u) * L + j) * 4 + q) * 64 + elane) * 4);
+    };
+    OA out[2][2][4];
+#pragma unroll
+    for (int rh = 0; rh < 2; ++rh)
+#pragma unroll
+        for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) out[rh][ch][e] = (OA)0;
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+        f32x4 s4[2];
+#pragma unroll
+        for (int rh = 0; rh < 2; ++rh) s4[rh] = sa4(last_i ? 3 : u, u, rh);
+#pragma unroll
+        for (int j = 0; j < L; ++j) {
+            // the kept pairs: (u, j) in the first kind, (3, j) in the second
+            const bool keep = last_i ? (!TRI || j == 0) : (!TRI || u + j <= L - 1);
+            if (keep) {
+#pragma unroll
+                for (int rh = 0; rh < 2; ++rh)
+#pragma unroll
+                    for (int ch = 0; ch < 2; ++ch) {
+                        f32x4 tv;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            tv[e] = (MF::to_f32(acc[u][j][rh][ch][e]) * s4[rh][e]) * sbv[j][ch];
+                        if (last_i) {
+                            *tslot(wave - 6, u, j, rh * 2 + ch) = tv;
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) out[rh][ch][e] = out[rh][ch][e] + (OA)tv[e];
+                        }
+                    }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    exec_barrier();
+    if (!last_i) {
+        const int64_t cbase = bidx * p.cs_b;
+#pragma unroll
+        for (int rh = 0; rh < 2; ++rh)
+#pragma unroll
+            for (int ch = 0; ch < 2; ++ch) {
+                const int64_t col = n0 + wy * 32 + 16 * ch + eq;
+                f32x4 t3[TRI ? 1 : L];
+#pragma unroll
+                for (int j = 0; j < (TRI ? 1 : L); ++j) t3[j] = *tslot(wy, wx, j, rh * 2 + ch);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int64_t row = m0 + row4(0, rh) + e;
+                    OA o = out[rh][ch][e];
+#pragma unroll
+                    for (int j = 0; j < (TRI ? 1 : L); ++j) o = o + (OA)t3[j][e];
+                    if (col < p.N && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, o);
+                }
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // num_splits 5: one wave per SIMD, each holding all 25 slice pairs of one
 // 32 x 32 block ("solo" kernel).  4 waves of 512 registers cover a 64 x 64
 // tile: wave (x, y) = (w / 2, w % 2) reads 5 A fragments (slice u, rows of
@@ -2818,7 +3232,11 @@ static hipError_t launch_wide(const GemmParams &p, const GemmPlan &plan, hipStre
 template <typename ST, typename AccT, bool TRI>
 static hipError_t launch_wide4(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     using Sh = Wide4Shape;
-    auto kern = cross_gemm_wide4_kernel<ST, AccT, TRI>;
+    // int8 slices: the 16 x 16 x 64 form (the same tile, pairs and bits)
+    auto kern = [] {
+        if constexpr (std::is_same<ST, int8_t>::value) return cross_gemm_wide4q_kernel<ST, AccT, TRI>;
+        else return cross_gemm_wide4_kernel<ST, AccT, TRI>;
+    }();
     static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
     if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
     const int es = (int)sizeof(ST);
