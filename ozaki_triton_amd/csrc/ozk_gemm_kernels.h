@@ -2446,12 +2446,38 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide4_kernel(GemmParams p, 
 template <typename ST> struct Mfma16;
 template <> struct Mfma16<int8_t> {
     using Acc = i32x4;
+    static constexpr bool kExactAcc = true;    // int32 sums: exact in any order
     OZK_DEV static Acc zero() { return Acc{0}; }
     template <bool AG> OZK_DEV static void run(Acc &c, i32x4 a, i32x4 b) {
         if constexpr (AG) asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
         else asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
     }
+    // the compiler's own form (it places the accumulator and sees the hazards)
+    OZK_DEV static Acc mfma(i32x4 a, i32x4 b, Acc c) {
+        return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+    }
     OZK_DEV static float to_f32(int x) { return (float)x; }
+};
+// fp16 / bf16 slices: 16 x 16 x 32, 16 bytes of K per lane as for int8
+template <> struct Mfma16<_Float16> {
+    using Acc = f32x4;
+    static constexpr bool kExactAcc = false;
+    OZK_DEV static Acc zero() { return Acc{0.0f}; }
+    OZK_DEV static Acc mfma(i32x4 a, i32x4 b, Acc c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    }
+    OZK_DEV static float to_f32(float x) { return x; }
+};
+template <> struct Mfma16<__bf16> {
+    using Acc = f32x4;
+    static constexpr bool kExactAcc = false;
+    OZK_DEV static Acc zero() { return Acc{0.0f}; }
+    OZK_DEV static Acc mfma(i32x4 a, i32x4 b, Acc c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    }
+    OZK_DEV static float to_f32(float x) { return x; }
 };
 
 template <typename ST, typename AccT, bool TRI>
@@ -2819,6 +2845,372 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide4q_kernel(GemmParams p,
                 }
             }
     }
+}
+
+// ---------------------------------------------------------------------------
+// The num_splits 3 wide kernel on 16 x 16 MFMAs (int8: v_mfma_i32_16x16x64_i8,
+// fp16 / bf16: v_mfma_f32_16x16x32_f16 / _bf16): the same tile (64 x 128, 8
+// waves in a 2 x 4 grid of 32 x 32 blocks, each wave all 9 pairs of its
+// block), stages, DMA and split-K as cross_gemm_wide_kernel, with a K step of
+// 64 bytes (two per stage) as in cross_gemm_wide4q_kernel (there: why).  A
+// wave's 9 accumulator tiles of 32 x 32 become 36 of 16 x 16,
+// acc[i][j][rh][ch]; register e of lane l holds row 16 rh + 4 (l / 16) + e,
+// column 16 ch + l % 16 of the block.  Per K step a wave reads 6 A fragments
+// (i, rh) and 6 B fragments (j, ch) and runs 36 MFMAs, B-outer: the A
+// fragments stay in registers, each re-read for the next step right after its
+// last MFMA; B fragment g + 2 is read while g's 6 MFMAs run (a ring of 3).
+// The stage barrier sits before the last two B groups of the stage's second
+// step, whose reads are the next stage's.  144 accumulator registers, 24 for
+// A, 12 for B: the compiler places them.  The epilogue sums each element's pairs tile by
+// tile (i-major, j-minor), so each tile is dead after it.
+// ---------------------------------------------------------------------------
+template <typename ST, typename AccT, bool TRI>
+__global__ __launch_bounds__(512, 1) void cross_gemm_wideq_kernel(GemmParams p, int group_m,
+                                                                  uint32_t a_records,
+                                                                  uint32_t b_records) {
+    resolve_split_fail(p);
+    using Sh = WideShape;
+    using MF = Mfma16<ST>;
+    using Acc = typename MF::Acc;
+    using OA = AccT;
+    constexpr int L = Sh::L, BM = Sh::BM, BN = Sh::BN;
+    using PS = Pairs<L, TRI>;
+    constexpr int ES = (int)sizeof(ST);
+    constexpr uint32_t kOOB = 0x80000000u;
+    constexpr int P1 = 4;   // DMA instructions of stage kb + 2 in the groups after the barrier
+    static_assert(Sh::NW == 8 && Sh::LA == 3 && Sh::LB == 6 && BM == 64 && BN == 128,
+                  "the window arithmetic below is written for this shape");
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 2, wn = wave & 3;
+
+    const int64_t tiles_m = (p.M + BM - 1) / BM;
+    const int64_t tiles_n = (p.N + BN - 1) / BN;
+    const int64_t tiles = tiles_m * tiles_n;
+    // split-K: workgroup g0 is K range g0 % S of tile g0 / S
+    const int S = p.ksplit > 1 ? p.ksplit : 1;
+    const int64_t g0 = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
+    const int krange = (int)(g0 % S);
+    const int64_t g = g0 / S;
+    const int64_t bidx = g / tiles;
+    const int64_t t = g % tiles;
+    const int64_t width = (int64_t)group_m * tiles_n;
+    const int64_t first_m = (t / width) * group_m;
+    const int64_t gsz = (tiles_m - first_m < group_m) ? (tiles_m - first_m) : group_m;
+    const int64_t tm = first_m + (t % width) % gsz;
+    const int64_t tn = (t % width) / gsz;
+    const int64_t m0 = tm * BM, n0 = tn * BN;
+
+    const uint32_t kbytes = (uint32_t)(p.K * ES);
+    const int nkb_all = (int)((kbytes + kDmaRB - 1) / kDmaRB);
+    const int kb0 = S > 1 ? krange * p.kb_per_split : 0;   // this range's first stage
+    const int nkb = S > 1 ? min(p.kb_per_split, nkb_all - kb0) : nkb_all;
+    const uint32_t kbyte0 = (uint32_t)kb0 * kDmaRB;
+
+    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const char *)p.A + bidx * p.as_b * ES), (short)0, (int)a_records, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const char *)p.B + bidx * p.bs_b * ES), (short)0, (int)b_records, 0x00020000);
+
+    // Stage DMA: a 1 KB window is 8 whole 128-byte rows (lane -> row lane /
+    // 8, physical chunk lane % 8, which holds logical chunk c0 = (lane % 8) ^
+    // (lane / 16) in an even window and c0 ^ 4 in an odd one); the stage's A
+    // windows r = 8 s + x (slice s, rows m0 + 8 x) and B windows r = 16 s + x
+    // (rows n0 + 8 x) sit at r KB of their regions.  Wave w fetches the A
+    // windows w + 8 q (q < 3: slice q, row window w) and the B windows w + 8 q
+    // (q < 6: slice q / 2, row window w + 8 (q % 2)), so its windows share
+    // its parity and their sources are a base plus multiples of a slice
+    // stride: all uniform values fixed before the loop.  The lane's part of
+    // the source is held (2 registers); the bounds are tested per lane only
+    // where a window has fewer than 8 rows in the operand or the stage runs
+    // past K.
+    const int64_t a_first = m0 + 8 * wave, b_first = n0 + 8 * wave;
+    const uint32_t a_base = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)((a_first * p.as_m) * ES + kbyte0));
+    const uint32_t b_base = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)((b_first * p.bs_n) * ES + kbyte0));
+    const uint32_t a_sstep = (uint32_t)__builtin_amdgcn_readfirstlane((int)(p.as_l * ES));
+    const uint32_t b_sstep = (uint32_t)__builtin_amdgcn_readfirstlane((int)(p.bs_l * ES));
+    const uint32_t b_hstep = (uint32_t)__builtin_amdgcn_readfirstlane((int)(64 * p.bs_n * ES));
+    // rows of this wave's windows inside the operand (may be <= 0)
+    const int a_rows = (int)(p.M - a_first < 8 ? p.M - a_first : 8);
+    const int b_rows0 = (int)(p.N - b_first < 8 ? p.N - b_first : 8);
+    const int b_rows1 = (int)(p.N - b_first - 64 < 8 ? p.N - b_first - 64 : 8);
+    uint32_t lane_src[2];   // [A, B]
+    {
+        const int c0 = (lane & 7) ^ (lane >> 4);
+        const uint32_t chb = (uint32_t)((wave & 1) ? (c0 ^ 4) : c0) * 16;
+        lane_src[0] = (uint32_t)((lane >> 3) * p.as_m * ES) + chb;
+        lane_src[1] = (uint32_t)((lane >> 3) * p.bs_n * ES) + chb;
+    }
+    const int nkb_full = (int)(kbytes / kDmaRB);   // stages (counted from K = 0) inside K
+    auto buf = [&](int kb) { return smem + (kb & 1) * Sh::STAGE; };
+    // DMA instruction q (< LA: A window q of this wave; else B window q - LA)
+    // of stage kb (of this range); q is a constant at every call
+    auto issue = [&](int kb, int q) {
+        const bool isa = q < Sh::LA;
+        const int qq = isa ? q : q - Sh::LA;
+        const uint32_t ub = (isa ? a_base + (uint32_t)qq * a_sstep
+                                 : b_base + (uint32_t)(qq >> 1) * b_sstep + ((qq & 1) ? b_hstep : 0u)) +
+                            (uint32_t)kb * kDmaRB;
+        const uint32_t lsrc = lane_src[isa ? 0 : 1];
+        const int rows = isa ? a_rows : ((qq & 1) ? b_rows1 : b_rows0);
+        uint32_t vo;
+        if (rows == 8 && kb0 + kb < nkb_full) {
+            vo = lsrc + ub;
+        } else {
+            const int kleft = (int)kbytes - (int)kbyte0 - kb * kDmaRB;   // > 0
+            const int ln = lane_here();
+            const int c0 = (ln & 7) ^ (ln >> 4);
+            const int chb = ((wave & 1) ? (c0 ^ 4) : c0) * 16;
+            vo = ((ln >> 3) < rows && chb < kleft) ? lsrc + ub : kOOB;
+        }
+        auto *ldsp = (__attribute__((address_space(3))) void *)(
+            buf(kb) + (isa ? 0 : Sh::A_BYTES) + (wave + 8 * qq) * 1024);
+        if (isa) __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, ldsp, 16, vo, 0, 0, 0);
+        else __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, ldsp, 16, vo, 0, 0, 0);
+    };
+
+    // The tile's scales (A's [L][BM], then B's [L][BN]: 2304 bytes), as in
+    // the wide kernel: into the buffer of stage nkb at the start of the last
+    // stage (the lane read where they are fetched).
+    char *const scl = buf(nkb);
+    auto issue_scales = [&]() {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int u = q * Sh::NW + wave;
+            if (u >= L * (BM + BN) / 64) break;
+            const bool isa = u < L * BM / 64;
+            const int e = (isa ? u : u - L * BM / 64) * 64 + lane_here();
+            const int s = isa ? e / BM : e / BN;                 // slice
+            const int64_t rc = isa ? m0 + e % BM : n0 + e % BN;  // row of A / column of B
+            const int64_t ext = isa ? ((int64_t)(L - 1) * p.sas_l + (p.M - 1) * p.sas_m + 1)
+                                    : ((int64_t)(L - 1) * p.sbs_l + (p.N - 1) * p.sbs_n + 1);
+            const bool ok = rc < (isa ? p.M : p.N);
+            const uint32_t vo = ok ? (uint32_t)(((int64_t)s * (isa ? p.sas_l : p.sbs_l) +
+                                                 rc * (isa ? p.sas_m : p.sbs_n)) * 4)
+                                   : kOOB;
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)(isa ? p.sa + bidx * p.sas_b : p.sb + bidx * p.sbs_b), (short)0,
+                (int)(ext * 4 < 0x7FFFFFFF ? ext * 4 : 0x7FFFFFFF), 0x00020000);
+            auto *ldsp = (__attribute__((address_space(3))) void *)(scl + u * 256);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, ldsp, 4, vo, 0, 0, 0);
+        }
+    };
+    const float *sa_lds = (const float *)scl, *sb_lds = (const float *)(scl + L * BM * 4);
+
+    // prologue: stages 0 and 1; stage 0 must land before the first reads
+#pragma unroll
+    for (int q = 0; q < Sh::LPS; ++q) issue(0, q);
+    if (nkb > 1) {
+#pragma unroll
+        for (int q = 0; q < Sh::LPS; ++q) issue(1, q);
+        wait_vmcnt<Sh::LPS>();
+    } else {
+        wait_vmcnt<0>();
+    }
+    exec_barrier();
+
+    // fragments: as in cross_gemm_wide4q_kernel, one lane address per region
+    // and K step, the fragment's row its LDS read's immediate
+    const int qrow = lane & 15;
+    const int key = (qrow >> 1) & 7;
+    int lane_rd[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) lane_rd[kk] = qrow * kDmaRB + (((4 * kk + (lane >> 4)) ^ key) << 4);
+    const int smem_base = (int)(uintptr_t)(__attribute__((address_space(3))) char *)smem;
+    using lds_cptr = const __attribute__((address_space(3))) char *;
+    const int a_org = wm * 32 * kDmaRB;
+    const int b_org = Sh::A_BYTES + wn * 32 * kDmaRB;
+    auto region = [&](int kb, int kk, int org) {
+        const int u = __builtin_amdgcn_readfirstlane(smem_base + (kb & 1) * Sh::STAGE + org);
+        return (lds_cptr)(uintptr_t)(u + lane_rd[kk]);
+    };
+    auto read_a = [&](lds_cptr ra, int pa) {   // A fragment pa = (i, rh)
+        return *(const __attribute__((address_space(3))) i32x4 *)(
+            ra + ((pa >> 1) * BM + 16 * (pa & 1)) * kDmaRB);
+    };
+    auto read_b = [&](lds_cptr rb, int gb) {   // B fragment gb = (j, ch)
+        return *(const __attribute__((address_space(3))) i32x4 *)(
+            rb + ((gb >> 1) * BN + 16 * (gb & 1)) * kDmaRB);
+    };
+
+    i32x4 fa[2 * L];   // A fragments (i, rh), resident through a K step
+    i32x4 fb[3];       // B fragments g .. g + 2 (g mod 3: 6 groups a step close the ring)
+    Acc acc[L][L][2][2];
+#pragma unroll
+    for (int i = 0; i < L; ++i)
+#pragma unroll
+        for (int j = 0; j < L; ++j)
+#pragma unroll
+            for (int rh = 0; rh < 2; ++rh)
+#pragma unroll
+                for (int ch = 0; ch < 2; ++ch) acc[i][j][rh][ch] = MF::zero();
+
+    // One K step (as in cross_gemm_wide4q_kernel): group gb runs the MFMAs
+    // of B fragment gb (the kept pairs) and first reads B fragment gb + 2
+    // (groups 4, 5: fragments 0, 1 of the next step, stage nkb_, step nkk);
+    // in group 5 each A fragment of the next step is read right after its
+    // last MFMA.  With `bar`, group 4 starts behind the stage barrier.  DMA
+    // instructions [lo, hi) of stage dkb go between the MFMAs of groups
+    // dg0 .. 5 (lo, hi and dg0 are constants at every call).
+    constexpr int NG = 2 * L, NPA = 2 * L;
+    auto stepq = [&](int ckb, int ckk, int nkb_, int nkk, bool bar, int dkb, bool on, int lo,
+                     int hi, int dg0) {
+        const int cnt = hi - lo;
+        const int span = (NG - dg0) * NPA;
+        const lds_cptr rb_cur = region(ckb, ckk, b_org);
+#pragma unroll
+        for (int gb = 0; gb < NG; ++gb) {
+            if (gb < NG - 2) {
+                fb[(gb + 2) % 3] = read_b(rb_cur, gb + 2);
+            } else {
+                if (gb == NG - 2 && bar) {
+                    // stage nkb_ has landed (this wave's DMA, then every
+                    // wave's through the barrier), and every wave's reads of
+                    // stage ckb are complete before its buffer is refilled
+                    wait_vmcnt<0>();
+                    __builtin_amdgcn_s_waitcnt(0xC07F);
+                    exec_barrier();
+                }
+                fb[(gb + 2) % 3] = read_b(region(nkb_, nkk, b_org), gb - (NG - 2));
+            }
+            const int j = gb >> 1, ch = gb & 1;
+            const lds_cptr ra_next = region(nkb_, nkk, a_org);
+#pragma unroll
+            for (int pa = 0; pa < NPA; ++pa) {
+                const int i = pa >> 1, rh = pa & 1;
+                if (PS::kept(i, j))
+                    acc[i][j][rh][ch] = MF::mfma(fa[pa], fb[gb % 3], acc[i][j][rh][ch]);
+                if (gb == NG - 1) fa[pa] = read_a(ra_next, pa);
+                const int n = (gb - dg0) * NPA + pa;
+#pragma unroll
+                for (int d = 0; d < Sh::LPS; ++d) {
+                    // instruction lo + d goes after MFMA (d * span) / cnt of the span
+                    if (gb >= dg0 && d < cnt && (d * span) / cnt == n && on) issue(dkb, lo + d);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+
+    if (nkb > 0) {
+        const lds_cptr ra0 = region(0, 0, a_org), rb0 = region(0, 0, b_org);
+#pragma unroll
+        for (int pa = 0; pa < NPA; ++pa) fa[pa] = read_a(ra0, pa);
+        fb[0] = read_b(rb0, 0);
+        fb[1] = read_b(rb0, 1);
+    }
+    static_assert(kDmaRB / 64 == 2 && NG % 3 == 0, "two 64-byte K steps per stage; the B ring closes");
+    if (nkb == 0) issue_scales();
+    for (int kb = 0; kb < nkb; ++kb) {
+        const bool nb = kb + 1 < nkb, n2 = kb + 2 < nkb;
+        // no DMA is outstanding in the last stage: its waits are unaffected
+        if (!nb) issue_scales();
+        // the rest of stage kb + 1 (stage 1 went out whole in the prologue)
+        stepq(kb, 0, kb, 1, false, kb + 1, nb && kb >= 1, P1, Sh::LPS, 0);
+        // the last two groups read stage kb + 1's step 0 (unused past the
+        // end) and start stage kb + 2 in stage kb's buffer
+        stepq(kb, 1, kb + 1, 0, nb, kb + 2, n2, 0, P1, NG - 2);
+    }
+
+    // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
+    wait_vmcnt<0>();
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    exec_barrier();
+    if (S > 1) {
+        // split-K, as in the wide kernel: each range stores its raw
+        // accumulators (register (rh, ch, e) of pair n at (n * 16 + (2 rh +
+        // ch) * 4 + e) * 64 + lane); the last range to arrive adds the others
+        constexpr int RW = L * L * 16;
+        const int ln = lane_here();
+        uint32_t *mine = splitk_slot(p, g, krange, wave, RW, ln);
+#pragma unroll
+        for (int n = 0; n < L * L; ++n) {
+            if (!PS::kept(n / L, n % L)) continue;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const i32x4 u = __builtin_bit_cast(i32x4, acc[n / L][n % L][q >> 1][q & 1]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) splitk_put(mine + (n * 16 + q * 4 + e) * 64, (uint32_t)u[e]);
+            }
+        }
+        if (!splitk_arrive(p, g, (int *)buf(nkb + 1))) return;
+        auto get4 = [&](const uint32_t *src) {
+            i32x4 u;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) u[e] = (int)splitk_get(src + e * 64);
+            return __builtin_bit_cast(Acc, u);
+        };
+        // int32 sums are exact in any order: this range's accumulators stay
+        // and the others are added; float sums: every range read back, this
+        // one's too, in range order from range 0
+        for (int s2 = 0; s2 < S; ++s2) {
+            if (MF::kExactAcc && s2 == krange) continue;
+            const uint32_t *src = splitk_slot(p, g, s2, wave, RW, ln);
+#pragma unroll
+            for (int n = 0; n < L * L; ++n) {
+                if (!PS::kept(n / L, n % L)) continue;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const Acc v = get4(src + (n * 16 + q * 4) * 64);
+                    Acc &a = acc[n / L][n % L][q >> 1][q & 1];
+                    a = (!MF::kExactAcc && s2 == 0) ? v : a + v;
+                }
+            }
+        }
+    }
+    const int elane = lane_here();
+    const int eq = elane & 15, eg = elane >> 4;
+    const int64_t cbase = bidx * p.cs_b;
+    float sbv[L][2];
+#pragma unroll
+    for (int j = 0; j < L; ++j)
+#pragma unroll
+        for (int ch = 0; ch < 2; ++ch) sbv[j][ch] = sb_lds[j * BN + wn * 32 + 16 * ch + eq];
+    OA out[2][2][4];
+#pragma unroll
+    for (int rh = 0; rh < 2; ++rh)
+#pragma unroll
+        for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) out[rh][ch][e] = (OA)0;
+#pragma unroll
+    for (int i = 0; i < L; ++i) {
+        f32x4 s4[2];
+#pragma unroll
+        for (int rh = 0; rh < 2; ++rh)
+            s4[rh] = *(const f32x4 *)(sa_lds + i * BM + wm * 32 + 16 * rh + 4 * eg);
+#pragma unroll
+        for (int j = 0; j < L; ++j) {
+            if (!PS::kept(i, j)) continue;
+#pragma unroll
+            for (int rh = 0; rh < 2; ++rh)
+#pragma unroll
+                for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        // fl32(fl32(fl32(acc) * sa_i) * sb_j), summed i-major, j-minor
+                        const float t1 = MF::to_f32(acc[i][j][rh][ch][e]) * s4[rh][e];
+                        out[rh][ch][e] = out[rh][ch][e] + (OA)(t1 * sbv[j][ch]);
+                    }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int rh = 0; rh < 2; ++rh)
+#pragma unroll
+        for (int ch = 0; ch < 2; ++ch) {
+            const int64_t col = n0 + wn * 32 + 16 * ch + eq;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int64_t row = m0 + wm * 32 + 16 * rh + 4 * eg + e;
+                if (col < p.N && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, out[rh][ch][e]);
+            }
+        }
 }
 
 // ---------------------------------------------------------------------------
@@ -3215,7 +3607,12 @@ static hipError_t launch_ring(const GemmParams &p, const GemmPlan &plan, hipStre
 template <typename ST, typename AccT, bool TRI>
 static hipError_t launch_wide(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     using Sh = WideShape;
-    auto kern = cross_gemm_wide_kernel<ST, AccT, TRI>;
+    // int8 / fp16 / bf16 slices: the 16 x 16 MFMA form (fp32 slices keep the
+    // 32 x 32 x 2 one)
+    auto kern = [] {
+        if constexpr (std::is_same<ST, float>::value) return cross_gemm_wide_kernel<ST, AccT, TRI>;
+        else return cross_gemm_wideq_kernel<ST, AccT, TRI>;
+    }();
     static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
     if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
     const int es = (int)sizeof(ST);
