@@ -3214,6 +3214,374 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wideq_kernel(GemmParams p, 
 }
 
 // ---------------------------------------------------------------------------
+// The num_splits 2 ring configuration (128 x 128 tiles; wave w holds 64 x 64
+// block w % 4 for the pairs of A slice w / 4, (i, 0) and (i, 1)) on 16 x 16
+// MFMAs (int8, fp16, bf16 slices), in the double-buffered whole stages of
+// cross_gemm_wideq_kernel (two 64 KB stages; the ring of half stages is not
+// needed where two whole stages fit).  Per 64-byte K step a wave reads its 4 A
+// fragments (rh) once and its 8 B fragments (j, ch) through a ring of 4, B
+// fragment g + 2 read while g's 4 MFMAs run: 32 MFMAs a step, 32 accumulator
+// tiles acc[j][rh][ch] (128 registers).  The epilogue hands the partial sums
+// of slice 0's waves to slice 1's through the LDS, which add their own pairs
+// in the reference's order.
+// ---------------------------------------------------------------------------
+struct RingQShape {
+    static constexpr int L = 2;
+    static constexpr int NW = 8;                         // waves
+    static constexpr int BM = 128, BN = 128;
+    static constexpr int A_BYTES = L * BM * kDmaRB;      // 32 KB
+    static constexpr int B_BYTES = L * BN * kDmaRB;      // 32 KB
+    static constexpr int STAGE = A_BYTES + B_BYTES;
+    static constexpr int LA = A_BYTES / (NW * 1024);     // A instructions per wave per stage
+    static constexpr int LB = B_BYTES / (NW * 1024);     // B instructions per wave per stage
+    static constexpr int LPS = LA + LB;
+    static constexpr int LDS_BYTES = 2 * STAGE;          // also the fp64 hand-off: 128 x 128 x 8
+    static_assert(LDS_BYTES <= 160 * 1024 && BM * BN * 8 <= LDS_BYTES, "LDS");
+    static_assert(L * (BM + BN) * 4 == NW * 256, "the tile's scales: one 256-byte unit per wave");
+    static_assert(kDmaRB == 128, "128-byte stage rows");
+};
+
+template <typename ST, typename AccT>
+__global__ __launch_bounds__(512, 1) void cross_gemm_ringq_kernel(GemmParams p, int group_m,
+                                                                  uint32_t a_records,
+                                                                  uint32_t b_records) {
+    resolve_split_fail(p);
+    using Sh = RingQShape;
+    using MF = Mfma16<ST>;
+    using Acc = typename MF::Acc;
+    using OA = AccT;
+    constexpr int L = Sh::L, BM = Sh::BM, BN = Sh::BN;
+    constexpr int ES = (int)sizeof(ST);
+    constexpr uint32_t kOOB = 0x80000000u;
+    constexpr int P1 = 2;   // DMA instructions of stage kb + 2 in the groups after the barrier
+    static_assert(Sh::NW == 8 && Sh::LA == 4 && Sh::LB == 4 && BM == 128 && BN == 128,
+                  "the window arithmetic below is written for this shape");
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int blk = wave & 3, gi = wave >> 2;   // block; A slice of the wave's pairs
+    const int wm = blk >> 1, wn = blk & 1;
+
+    const int64_t tiles_m = (p.M + BM - 1) / BM;
+    const int64_t tiles_n = (p.N + BN - 1) / BN;
+    const int64_t tiles = tiles_m * tiles_n;
+    // split-K: workgroup g0 is K range g0 % S of tile g0 / S
+    const int S = p.ksplit > 1 ? p.ksplit : 1;
+    const int64_t g0 = xcd_remap_gemm(blockIdx.x, (int64_t)gridDim.x);
+    const int krange = (int)(g0 % S);
+    const int64_t g = g0 / S;
+    const int64_t bidx = g / tiles;
+    const int64_t t = g % tiles;
+    const int64_t width = (int64_t)group_m * tiles_n;
+    const int64_t first_m = (t / width) * group_m;
+    const int64_t gsz = (tiles_m - first_m < group_m) ? (tiles_m - first_m) : group_m;
+    const int64_t tm = first_m + (t % width) % gsz;
+    const int64_t tn = (t % width) / gsz;
+    const int64_t m0 = tm * BM, n0 = tn * BN;
+
+    const uint32_t kbytes = (uint32_t)(p.K * ES);
+    const int nkb_all = (int)((kbytes + kDmaRB - 1) / kDmaRB);
+    const int kb0 = S > 1 ? krange * p.kb_per_split : 0;   // this range's first stage
+    const int nkb = S > 1 ? min(p.kb_per_split, nkb_all - kb0) : nkb_all;
+    const uint32_t kbyte0 = (uint32_t)kb0 * kDmaRB;
+
+    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const char *)p.A + bidx * p.as_b * ES), (short)0, (int)a_records, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const char *)p.B + bidx * p.bs_b * ES), (short)0, (int)b_records, 0x00020000);
+
+    // Stage DMA: 1 KB windows of 8 whole 128-byte rows (lane -> row lane / 8,
+    // physical chunk lane % 8, which holds logical chunk c0 = (lane % 8) ^
+    // (lane / 16) in an even window and c0 ^ 4 in an odd one); the stage's
+    // windows r = 16 s + x (slice s, rows 8 x of the tile) sit at r KB of the
+    // A and B regions.  Wave w fetches windows w + 8 q of each (q < 4: slice
+    // q / 2, row window w + 8 (q % 2)): its windows share its parity, and
+    // their sources are a base, plus a slice stride, plus 64 rows.  The
+    // lane's part of the source is held; the bounds are tested per lane only
+    // where a window has fewer than 8 rows in the operand or the stage runs
+    // past K.
+    const int64_t a_first = m0 + 8 * wave, b_first = n0 + 8 * wave;
+    const uint32_t a_base = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)((a_first * p.as_m) * ES + kbyte0));
+    const uint32_t b_base = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)((b_first * p.bs_n) * ES + kbyte0));
+    const uint32_t a_sstep = (uint32_t)__builtin_amdgcn_readfirstlane((int)(p.as_l * ES));
+    const uint32_t b_sstep = (uint32_t)__builtin_amdgcn_readfirstlane((int)(p.bs_l * ES));
+    const uint32_t a_hstep = (uint32_t)__builtin_amdgcn_readfirstlane((int)(64 * p.as_m * ES));
+    const uint32_t b_hstep = (uint32_t)__builtin_amdgcn_readfirstlane((int)(64 * p.bs_n * ES));
+    // rows of this wave's windows inside the operand (may be <= 0)
+    const int a_rows0 = (int)(p.M - a_first < 8 ? p.M - a_first : 8);
+    const int a_rows1 = (int)(p.M - a_first - 64 < 8 ? p.M - a_first - 64 : 8);
+    const int b_rows0 = (int)(p.N - b_first < 8 ? p.N - b_first : 8);
+    const int b_rows1 = (int)(p.N - b_first - 64 < 8 ? p.N - b_first - 64 : 8);
+    uint32_t lane_src[2];   // [A, B]
+    {
+        const int c0 = (lane & 7) ^ (lane >> 4);
+        const uint32_t chb = (uint32_t)((wave & 1) ? (c0 ^ 4) : c0) * 16;
+        lane_src[0] = (uint32_t)((lane >> 3) * p.as_m * ES) + chb;
+        lane_src[1] = (uint32_t)((lane >> 3) * p.bs_n * ES) + chb;
+    }
+    const int nkb_full = (int)(kbytes / kDmaRB);   // stages (counted from K = 0) inside K
+    auto buf = [&](int kb) { return smem + (kb & 1) * Sh::STAGE; };
+    // DMA instruction q (< LA: A window q of this wave; else B window q - LA)
+    // of stage kb (of this range); q is a constant at every call
+    auto issue = [&](int kb, int q) {
+        const bool isa = q < Sh::LA;
+        const int qq = isa ? q : q - Sh::LA;
+        const uint32_t ub = (isa ? a_base + (uint32_t)(qq >> 1) * a_sstep + ((qq & 1) ? a_hstep : 0u)
+                                 : b_base + (uint32_t)(qq >> 1) * b_sstep + ((qq & 1) ? b_hstep : 0u)) +
+                            (uint32_t)kb * kDmaRB;
+        const uint32_t lsrc = lane_src[isa ? 0 : 1];
+        const int rows = isa ? ((qq & 1) ? a_rows1 : a_rows0) : ((qq & 1) ? b_rows1 : b_rows0);
+        uint32_t vo;
+        if (rows == 8 && kb0 + kb < nkb_full) {
+            vo = lsrc + ub;
+        } else {
+            const int kleft = (int)kbytes - (int)kbyte0 - kb * kDmaRB;   // > 0
+            const int ln = lane_here();
+            const int c0 = (ln & 7) ^ (ln >> 4);
+            const int chb = ((wave & 1) ? (c0 ^ 4) : c0) * 16;
+            vo = ((ln >> 3) < rows && chb < kleft) ? lsrc + ub : kOOB;
+        }
+        auto *ldsp = (__attribute__((address_space(3))) void *)(
+            buf(kb) + (isa ? 0 : Sh::A_BYTES) + (wave + 8 * qq) * 1024);
+        if (isa) __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, ldsp, 16, vo, 0, 0, 0);
+        else __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, ldsp, 16, vo, 0, 0, 0);
+    };
+
+    // The tile's scales (A's [L][BM], then B's [L][BN]: 2 KB, one 256-byte
+    // unit per wave) into the buffer of stage nkb at the start of the last
+    // stage (the lane read where they are fetched).
+    char *const scl = buf(nkb);
+    auto issue_scales = [&]() {
+        const bool isa = wave < L * BM / 64;
+        const int e = (isa ? wave : wave - L * BM / 64) * 64 + lane_here();
+        const int s = isa ? e / BM : e / BN;                 // slice
+        const int64_t rc = isa ? m0 + e % BM : n0 + e % BN;  // row of A / column of B
+        const int64_t ext = isa ? ((int64_t)(L - 1) * p.sas_l + (p.M - 1) * p.sas_m + 1)
+                                : ((int64_t)(L - 1) * p.sbs_l + (p.N - 1) * p.sbs_n + 1);
+        const bool ok = rc < (isa ? p.M : p.N);
+        const uint32_t vo = ok ? (uint32_t)(((int64_t)s * (isa ? p.sas_l : p.sbs_l) +
+                                             rc * (isa ? p.sas_m : p.sbs_n)) * 4)
+                               : kOOB;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(isa ? p.sa + bidx * p.sas_b : p.sb + bidx * p.sbs_b), (short)0,
+            (int)(ext * 4 < 0x7FFFFFFF ? ext * 4 : 0x7FFFFFFF), 0x00020000);
+        auto *ldsp = (__attribute__((address_space(3))) void *)(scl + wave * 256);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, ldsp, 4, vo, 0, 0, 0);
+    };
+    const float *sa_lds = (const float *)scl, *sb_lds = (const float *)(scl + L * BM * 4);
+
+    // prologue: stages 0 and 1; stage 0 must land before the first reads
+#pragma unroll
+    for (int q = 0; q < Sh::LPS; ++q) issue(0, q);
+    if (nkb > 1) {
+#pragma unroll
+        for (int q = 0; q < Sh::LPS; ++q) issue(1, q);
+        wait_vmcnt<Sh::LPS>();
+    } else {
+        wait_vmcnt<0>();
+    }
+    exec_barrier();
+
+    // fragments: as in cross_gemm_wide4q_kernel, one lane address per region
+    // and K step, the fragment's row its LDS read's immediate
+    const int qrow = lane & 15;
+    const int key = (qrow >> 1) & 7;
+    int lane_rd[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) lane_rd[kk] = qrow * kDmaRB + (((4 * kk + (lane >> 4)) ^ key) << 4);
+    const int smem_base = (int)(uintptr_t)(__attribute__((address_space(3))) char *)smem;
+    using lds_cptr = const __attribute__((address_space(3))) char *;
+    const int a_org = (gi * BM + wm * 64) * kDmaRB;
+    const int b_org = Sh::A_BYTES + wn * 64 * kDmaRB;
+    auto region = [&](int kb, int kk, int org) {
+        const int u = __builtin_amdgcn_readfirstlane(smem_base + (kb & 1) * Sh::STAGE + org);
+        return (lds_cptr)(uintptr_t)(u + lane_rd[kk]);
+    };
+    auto read_a = [&](lds_cptr ra, int rh) {   // A fragment rh of slice gi
+        return *(const __attribute__((address_space(3))) i32x4 *)(ra + 16 * rh * kDmaRB);
+    };
+    auto read_b = [&](lds_cptr rb, int gb) {   // B fragment gb = (j, ch)
+        return *(const __attribute__((address_space(3))) i32x4 *)(
+            rb + ((gb >> 2) * BN + 16 * (gb & 3)) * kDmaRB);
+    };
+
+    constexpr int NG = 4 * L, NPA = 4;   // B fragments (j, ch), A fragments rh
+    i32x4 fa[NPA];   // A fragments, resident through a K step
+    i32x4 fb[4];     // B fragments g .. g + 3 (g mod 4: 8 groups a step close the ring)
+    Acc acc[L][4][4];
+#pragma unroll
+    for (int j = 0; j < L; ++j)
+#pragma unroll
+        for (int rh = 0; rh < 4; ++rh)
+#pragma unroll
+            for (int ch = 0; ch < 4; ++ch) acc[j][rh][ch] = MF::zero();
+
+    // One K step, as in cross_gemm_wideq_kernel: group gb runs the 4 MFMAs
+    // of B fragment gb and first reads B fragment gb + 2 (groups 6, 7:
+    // fragments 0, 1 of the next step, stage nkb_, step nkk); in group 7 each
+    // A fragment of the next step is read right after its MFMA.  With `bar`,
+    // group 6 starts behind the stage barrier.  DMA instructions [lo, hi) of
+    // stage dkb go between the MFMAs of groups dg0 .. 7.
+    auto stepq = [&](int ckb, int ckk, int nkb_, int nkk, bool bar, int dkb, bool on, int lo,
+                     int hi, int dg0) {
+        const int cnt = hi - lo;
+        const int span = (NG - dg0) * NPA;
+        const lds_cptr rb_cur = region(ckb, ckk, b_org);
+#pragma unroll
+        for (int gb = 0; gb < NG; ++gb) {
+            if (gb < NG - 2) {
+                fb[(gb + 2) & 3] = read_b(rb_cur, gb + 2);
+            } else {
+                if (gb == NG - 2 && bar) {
+                    // stage nkb_ has landed (this wave's DMA, then every
+                    // wave's through the barrier), and every wave's reads of
+                    // stage ckb are complete before its buffer is refilled
+                    wait_vmcnt<0>();
+                    __builtin_amdgcn_s_waitcnt(0xC07F);
+                    exec_barrier();
+                }
+                fb[(gb + 2) & 3] = read_b(region(nkb_, nkk, b_org), gb - (NG - 2));
+            }
+            const int j = gb >> 2, ch = gb & 3;
+            const lds_cptr ra_next = region(nkb_, nkk, a_org);
+#pragma unroll
+            for (int rh = 0; rh < NPA; ++rh) {
+                acc[j][rh][ch] = MF::mfma(fa[rh], fb[gb & 3], acc[j][rh][ch]);
+                if (gb == NG - 1) fa[rh] = read_a(ra_next, rh);
+                const int n = (gb - dg0) * NPA + rh;
+#pragma unroll
+                for (int d = 0; d < Sh::LPS; ++d) {
+                    // instruction lo + d goes after MFMA (d * span) / cnt of the span
+                    if (gb >= dg0 && d < cnt && (d * span) / cnt == n && on) issue(dkb, lo + d);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+
+    if (nkb > 0) {
+        const lds_cptr ra0 = region(0, 0, a_org), rb0 = region(0, 0, b_org);
+#pragma unroll
+        for (int rh = 0; rh < NPA; ++rh) fa[rh] = read_a(ra0, rh);
+        fb[0] = read_b(rb0, 0);
+        fb[1] = read_b(rb0, 1);
+    }
+    static_assert(kDmaRB / 64 == 2 && NG % 4 == 0, "two 64-byte K steps per stage; the B ring closes");
+    if (nkb == 0) issue_scales();
+    for (int kb = 0; kb < nkb; ++kb) {
+        const bool nb = kb + 1 < nkb, n2 = kb + 2 < nkb;
+        // no DMA is outstanding in the last stage: its waits are unaffected
+        if (!nb) issue_scales();
+        // the rest of stage kb + 1 (stage 1 went out whole in the prologue)
+        stepq(kb, 0, kb, 1, false, kb + 1, nb && kb >= 1, P1, Sh::LPS, 0);
+        // the last two groups read stage kb + 1's step 0 (unused past the
+        // end) and start stage kb + 2 in stage kb's buffer
+        stepq(kb, 1, kb + 1, 0, nb, kb + 2, n2, 0, P1, NG - 2);
+    }
+
+    // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
+    wait_vmcnt<0>();
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    exec_barrier();
+    if (S > 1) {
+        // split-K, as in the ring kernel: each range stores its raw
+        // accumulators (register e of tile n = (j, rh, ch) at (n * 4 + e) *
+        // 64 + lane); the last range to arrive adds the others
+        constexpr int RW = L * 16 * 4;
+        const int ln = lane_here();
+        uint32_t *mine = splitk_slot(p, g, krange, wave, RW, ln);
+#pragma unroll
+        for (int n = 0; n < L * 16; ++n) {
+            const i32x4 u = __builtin_bit_cast(i32x4, acc[n >> 4][(n >> 2) & 3][n & 3]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) splitk_put(mine + (n * 4 + e) * 64, (uint32_t)u[e]);
+        }
+        if (!splitk_arrive(p, g, (int *)buf(nkb + 1))) return;
+        auto get4 = [&](const uint32_t *src) {
+            i32x4 u;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) u[e] = (int)splitk_get(src + e * 64);
+            return __builtin_bit_cast(Acc, u);
+        };
+        // int32 sums are exact in any order: this range's accumulators stay
+        // and the others are added; float sums: every range read back, this
+        // one's too, in range order from range 0
+        for (int s2 = 0; s2 < S; ++s2) {
+            if (MF::kExactAcc && s2 == krange) continue;
+            const uint32_t *src = splitk_slot(p, g, s2, wave, RW, ln);
+#pragma unroll
+            for (int n = 0; n < L * 16; ++n) {
+                const Acc v = get4(src + n * 4 * 64);
+                Acc &a = acc[n >> 4][(n >> 2) & 3][n & 3];
+                a = (!MF::kExactAcc && s2 == 0) ? v : a + v;
+            }
+        }
+    }
+    const int elane = lane_here();
+    const int eq = elane & 15, eg = elane >> 4;
+    // this wave's scales into registers: sa of its rows (slice gi), sb of its
+    // columns
+    f32x4 sav[4];
+    float sbv[L][4];
+#pragma unroll
+    for (int rh = 0; rh < 4; ++rh)
+        sav[rh] = *(const f32x4 *)(sa_lds + gi * BM + wm * 64 + 16 * rh + 4 * eg);
+#pragma unroll
+    for (int j = 0; j < L; ++j)
+#pragma unroll
+        for (int ch = 0; ch < 4; ++ch) sbv[j][ch] = sb_lds[j * BN + wn * 64 + 16 * ch + eq];
+    // the partial sums overwrite the scales: every wave has read them
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    exec_barrier();
+    OA *part = (OA *)smem;   // [4 blocks][rh][ch][e][64 lanes]
+    const int64_t cbase = bidx * p.cs_b;
+    // fl32(fl32(fl32(acc) * sa_i) * sb_j) of pair (gi, j), summed i-major,
+    // j-minor: slice 0's waves sum their two pairs from zero, slice 1's add
+    // theirs to that
+    if (gi == 0) {
+#pragma unroll
+        for (int rh = 0; rh < 4; ++rh)
+#pragma unroll
+            for (int ch = 0; ch < 4; ++ch)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    OA out = (OA)0;
+#pragma unroll
+                    for (int j = 0; j < L; ++j) {
+                        const float t1 = MF::to_f32(acc[j][rh][ch][e]) * sav[rh][e];
+                        out = out + (OA)(t1 * sbv[j][ch]);
+                    }
+                    part[(((blk * 4 + rh) * 4 + ch) * 4 + e) * 64 + elane] = out;
+                }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        exec_barrier();
+    } else {
+        exec_barrier();
+#pragma unroll
+        for (int rh = 0; rh < 4; ++rh)
+#pragma unroll
+            for (int ch = 0; ch < 4; ++ch) {
+                const int64_t col = n0 + wn * 64 + 16 * ch + eq;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int64_t row = m0 + wm * 64 + 16 * rh + 4 * eg + e;
+                    OA out = part[(((blk * 4 + rh) * 4 + ch) * 4 + e) * 64 + elane];
+#pragma unroll
+                    for (int j = 0; j < L; ++j) {
+                        const float t1 = MF::to_f32(acc[j][rh][ch][e]) * sav[rh][e];
+                        out = out + (OA)(t1 * sbv[j][ch]);
+                    }
+                    if (col < p.N && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
+                }
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // num_splits 5: one wave per SIMD, each holding all 25 slice pairs of one
 // 32 x 32 block ("solo" kernel).  4 waves of 512 registers cover a 64 x 64
 // tile: wave (x, y) = (w / 2, w % 2) reads 5 A fragments (slice u, rows of
@@ -3589,8 +3957,15 @@ static hipError_t launch_pair(const GemmParams &p, const GemmPlan &plan, hipStre
 template <typename ST, int L, typename AccT>
 static hipError_t launch_ring(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     constexpr int W = (L <= 2) ? 2 : 1;
-    using Sh = RingShape<L, W>;
-    auto kern = cross_gemm_ring_kernel<ST, L, AccT, W>;
+    // num_splits 2 with int8 / fp16 / bf16 slices: the 16 x 16 MFMA form (same
+    // tiles, waves and split-K hand-over)
+    constexpr bool kQ = L == 2 && !std::is_same<ST, float>::value;
+    using Sh = std::conditional_t<kQ, RingQShape, RingShape<L, W>>;
+    auto kern = [] {
+        if constexpr (kQ) return cross_gemm_ringq_kernel<ST, AccT>;
+        else return cross_gemm_ring_kernel<ST, L, AccT, W>;
+    }();
+    static_assert(Sh::BM == 64 * W && Sh::BN == 64 * W, "the planner's tile size");
     static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
     if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
     const int es = (int)sizeof(ST);
