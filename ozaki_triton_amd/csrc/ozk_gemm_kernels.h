@@ -2561,13 +2561,22 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide4q_kernel(GemmParams p,
     }
     auto buf = [&](int kb) { return smem + (kb & 1) * Sh::STAGE; };
     // DMA instruction q (< LA: A window q of this wave; else B window q - LA)
-    // of stage kb; q is a constant at every call
-    auto issue = [&](int kb, int q) {
+    // of stage kb; q is a constant at every call.  FAST: the window's rows
+    // and the stage are known to lie inside the operand, and the uniform part
+    // of the source is the instruction's scalar offset.
+    auto issue = [&](int kb, int q, auto FAST) {
         const bool isa = q < Sh::LA;
         const int qq = isa ? q : q - Sh::LA;
         const uint32_t ub = (isa ? a_base + (uint32_t)qq * a_step : b_base + (uint32_t)qq * b_step) +
                             (uint32_t)kb * kDmaRB;
         const uint32_t lsrc = lane_src[isa ? 0 : 1][qq & 1];
+        if constexpr (decltype(FAST)::value) {
+            auto *ldsp = (__attribute__((address_space(3))) void *)(
+                buf(kb) + (isa ? 0 : Sh::A_BYTES) + (wave * (isa ? Sh::LA : Sh::LB) + qq) * 1024);
+            if (isa) __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, ldsp, 16, lsrc, (int)ub, 0, 0);
+            else __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, ldsp, 16, lsrc, (int)ub, 0, 0);
+            return;
+        }
         uint32_t vo;
         if (qq < (isa ? a_full : b_full) && kb < nkb_full) {
             vo = lsrc + ub;
@@ -2616,11 +2625,13 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide4q_kernel(GemmParams p,
     const float *sa_lds = (const float *)scl, *sb_lds = (const float *)(scl + L * BM * 4);
 
     // prologue: stages 0 and 1; stage 0 must land before the first reads
+    constexpr std::false_type kChecked{};
+    constexpr std::true_type kFast{};
 #pragma unroll
-    for (int q = 0; q < Sh::LPS; ++q) issue(0, q);
+    for (int q = 0; q < Sh::LPS; ++q) issue(0, q, kChecked);
     if (nkb > 1) {
 #pragma unroll
-        for (int q = 0; q < Sh::LPS; ++q) issue(1, q);
+        for (int q = 0; q < Sh::LPS; ++q) issue(1, q, kChecked);
         wait_vmcnt<Sh::LPS>();
     } else {
         wait_vmcnt<0>();
@@ -2682,9 +2693,9 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide4q_kernel(GemmParams p,
     // A fragment of the next step is read right after its last MFMA.  With
     // `bar`, group 6 starts behind the stage barrier.  DMA instructions [lo,
     // hi) of stage dkb are spread over the MFMAs of groups dg0 .. 7 (lo, hi
-    // and dg0 are constants at every call).
+    // and dg0 are constants at every call; FAST: as issue's).
     auto stepq = [&](int ckb, int ckk, int nkb_, int nkk, bool bar, int dkb, bool on, int lo,
-                     int hi, int dg0) {
+                     int hi, int dg0, auto FAST) __attribute__((always_inline)) {
         const int cnt = hi - lo;
         const int span = (8 - dg0) * 6;
         const lds_cptr rb_cur = region(ckb, ckk, b_org);
@@ -2723,7 +2734,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide4q_kernel(GemmParams p,
 #pragma unroll
                 for (int d = 0; d < Sh::LPS; ++d) {
                     // instruction lo + d goes after MFMA (d * span) / cnt of the span
-                    if (gb >= dg0 && d < cnt && (d * span) / cnt == n && on) issue(dkb, lo + d);
+                    if (gb >= dg0 && d < cnt && (d * span) / cnt == n && on) issue(dkb, lo + d, FAST);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -2739,15 +2750,29 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide4q_kernel(GemmParams p,
     }
     static_assert(kDmaRB / 64 == 2, "two 64-byte K steps per stage");
     if (nkb == 0) issue_scales();
-    for (int kb = 0; kb < nkb; ++kb) {
-        const bool nb = kb + 1 < nkb, n2 = kb + 2 < nkb;
+    auto stage = [&](int kb, auto FAST) __attribute__((always_inline)) {
+        // FAST stages are 1 .. nkb - 3: the tests below hold
+        constexpr bool F = decltype(FAST)::value;
+        const bool nb = F || kb + 1 < nkb, n2 = F || kb + 2 < nkb;
         // no DMA is outstanding in the last stage: its waits are unaffected
         if (!nb) issue_scales();
         // the rest of stage kb + 1 (stage 1 went out whole in the prologue)
-        stepq(kb, 0, kb, 1, false, kb + 1, nb && kb >= 1, P1, Sh::LPS, 0);
+        stepq(kb, 0, kb, 1, false, kb + 1, nb && (F || kb >= 1), P1, Sh::LPS, 0, FAST);
         // groups 6, 7 read stage kb + 1's step 0 (unused past the end) and
         // start stage kb + 2 in stage kb's buffer
-        stepq(kb, 1, kb + 1, 0, nb, kb + 2, n2, 0, P1, 6);
+        stepq(kb, 1, kb + 1, 0, nb, kb + 2, n2, 0, P1, 6, FAST);
+    };
+    // Stages 1 .. kfast - 1 of a tile whose windows all lie inside M and N
+    // issue all their DMA (stages kb + 1 and kb + 2 exist and lie inside K)
+    // with no tests; the others test each instruction.
+    const bool tile_full = a_full == Sh::LA && b_full == Sh::LB;
+    const int kfast = min(nkb - 2, nkb_full - 2);
+    {
+        int kb = 0;
+        if (nkb > 0) stage(kb++, kChecked);
+        if (tile_full)
+            for (; kb < kfast; ++kb) stage(kb, kFast);
+        for (; kb < nkb; ++kb) stage(kb, kChecked);
     }
 
     // the hand-placed MFMAs' results are read below: 64 wait states first
@@ -2949,14 +2974,23 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wideq_kernel(GemmParams p, 
     const int nkb_full = (int)(kbytes / kDmaRB);   // stages (counted from K = 0) inside K
     auto buf = [&](int kb) { return smem + (kb & 1) * Sh::STAGE; };
     // DMA instruction q (< LA: A window q of this wave; else B window q - LA)
-    // of stage kb (of this range); q is a constant at every call
-    auto issue = [&](int kb, int q) {
+    // of stage kb (of this range); q is a constant at every call.  FAST: the
+    // window's rows and the stage are known to lie inside the operand, and
+    // the uniform part of the source is the instruction's scalar offset.
+    auto issue = [&](int kb, int q, auto FAST) {
         const bool isa = q < Sh::LA;
         const int qq = isa ? q : q - Sh::LA;
         const uint32_t ub = (isa ? a_base + (uint32_t)qq * a_sstep
                                  : b_base + (uint32_t)(qq >> 1) * b_sstep + ((qq & 1) ? b_hstep : 0u)) +
                             (uint32_t)kb * kDmaRB;
         const uint32_t lsrc = lane_src[isa ? 0 : 1];
+        auto *ldsp = (__attribute__((address_space(3))) void *)(
+            buf(kb) + (isa ? 0 : Sh::A_BYTES) + (wave + 8 * qq) * 1024);
+        if constexpr (decltype(FAST)::value) {
+            if (isa) __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, ldsp, 16, lsrc, (int)ub, 0, 0);
+            else __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, ldsp, 16, lsrc, (int)ub, 0, 0);
+            return;
+        }
         const int rows = isa ? a_rows : ((qq & 1) ? b_rows1 : b_rows0);
         uint32_t vo;
         if (rows == 8 && kb0 + kb < nkb_full) {
@@ -2968,8 +3002,6 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wideq_kernel(GemmParams p, 
             const int chb = ((wave & 1) ? (c0 ^ 4) : c0) * 16;
             vo = ((ln >> 3) < rows && chb < kleft) ? lsrc + ub : kOOB;
         }
-        auto *ldsp = (__attribute__((address_space(3))) void *)(
-            buf(kb) + (isa ? 0 : Sh::A_BYTES) + (wave + 8 * qq) * 1024);
         if (isa) __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, ldsp, 16, vo, 0, 0, 0);
         else __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, ldsp, 16, vo, 0, 0, 0);
     };
@@ -3003,11 +3035,13 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wideq_kernel(GemmParams p, 
     const float *sa_lds = (const float *)scl, *sb_lds = (const float *)(scl + L * BM * 4);
 
     // prologue: stages 0 and 1; stage 0 must land before the first reads
+    constexpr std::false_type kChecked{};
+    constexpr std::true_type kFast{};
 #pragma unroll
-    for (int q = 0; q < Sh::LPS; ++q) issue(0, q);
+    for (int q = 0; q < Sh::LPS; ++q) issue(0, q, kChecked);
     if (nkb > 1) {
 #pragma unroll
-        for (int q = 0; q < Sh::LPS; ++q) issue(1, q);
+        for (int q = 0; q < Sh::LPS; ++q) issue(1, q, kChecked);
         wait_vmcnt<Sh::LPS>();
     } else {
         wait_vmcnt<0>();
@@ -3056,10 +3090,10 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wideq_kernel(GemmParams p, 
     // in group 5 each A fragment of the next step is read right after its
     // last MFMA.  With `bar`, group 4 starts behind the stage barrier.  DMA
     // instructions [lo, hi) of stage dkb go between the MFMAs of groups
-    // dg0 .. 5 (lo, hi and dg0 are constants at every call).
+    // dg0 .. 5 (lo, hi and dg0 are constants at every call; FAST: as issue's).
     constexpr int NG = 2 * L, NPA = 2 * L;
     auto stepq = [&](int ckb, int ckk, int nkb_, int nkk, bool bar, int dkb, bool on, int lo,
-                     int hi, int dg0) {
+                     int hi, int dg0, auto FAST) __attribute__((always_inline)) {
         const int cnt = hi - lo;
         const int span = (NG - dg0) * NPA;
         const lds_cptr rb_cur = region(ckb, ckk, b_org);
@@ -3090,7 +3124,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wideq_kernel(GemmParams p, 
 #pragma unroll
                 for (int d = 0; d < Sh::LPS; ++d) {
                     // instruction lo + d goes after MFMA (d * span) / cnt of the span
-                    if (gb >= dg0 && d < cnt && (d * span) / cnt == n && on) issue(dkb, lo + d);
+                    if (gb >= dg0 && d < cnt && (d * span) / cnt == n && on) issue(dkb, lo + d, FAST);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -3106,15 +3140,29 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wideq_kernel(GemmParams p, 
     }
     static_assert(kDmaRB / 64 == 2 && NG % 3 == 0, "two 64-byte K steps per stage; the B ring closes");
     if (nkb == 0) issue_scales();
-    for (int kb = 0; kb < nkb; ++kb) {
-        const bool nb = kb + 1 < nkb, n2 = kb + 2 < nkb;
+    auto stage = [&](int kb, auto FAST) __attribute__((always_inline)) {
+        // FAST stages are 1 .. nkb - 3: the tests below hold
+        constexpr bool F = decltype(FAST)::value;
+        const bool nb = F || kb + 1 < nkb, n2 = F || kb + 2 < nkb;
         // no DMA is outstanding in the last stage: its waits are unaffected
         if (!nb) issue_scales();
         // the rest of stage kb + 1 (stage 1 went out whole in the prologue)
-        stepq(kb, 0, kb, 1, false, kb + 1, nb && kb >= 1, P1, Sh::LPS, 0);
+        stepq(kb, 0, kb, 1, false, kb + 1, nb && (F || kb >= 1), P1, Sh::LPS, 0, FAST);
         // the last two groups read stage kb + 1's step 0 (unused past the
         // end) and start stage kb + 2 in stage kb's buffer
-        stepq(kb, 1, kb + 1, 0, nb, kb + 2, n2, 0, P1, NG - 2);
+        stepq(kb, 1, kb + 1, 0, nb, kb + 2, n2, 0, P1, NG - 2, FAST);
+    };
+    // Stages 1 .. kfast - 1 of a tile whose windows all lie inside M and N
+    // issue all their DMA (stages kb + 1 and kb + 2 exist and lie inside K)
+    // with no tests; the others test each instruction.
+    const bool tile_full = a_rows == 8 && b_rows0 == 8 && b_rows1 == 8;
+    const int kfast = min(nkb - 2, nkb_full - kb0 - 2);
+    {
+        int kb = 0;
+        if (nkb > 0) stage(kb++, kChecked);
+        if (tile_full)
+            for (; kb < kfast; ++kb) stage(kb, kFast);
+        for (; kb < nkb; ++kb) stage(kb, kChecked);
     }
 
     // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
@@ -3436,7 +3484,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ringq_kernel(GemmParams p, 
     // group 6 starts behind the stage barrier.  DMA instructions [lo, hi) of
     // stage dkb go between the MFMAs of groups dg0 .. 7 (FAST: as issue's).
     auto stepq = [&](int ckb, int ckk, int nkb_, int nkk, bool bar, int dkb, bool on, int lo,
-                     int hi, int dg0, auto FAST) {
+                     int hi, int dg0, auto FAST) __attribute__((always_inline)) {
         const int cnt = hi - lo;
         const int span = (NG - dg0) * NPA;
         const lds_cptr rb_cur = region(ckb, ckk, b_org);
@@ -3481,7 +3529,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ringq_kernel(GemmParams p, 
     }
     static_assert(kDmaRB / 64 == 2 && NG % 4 == 0, "two 64-byte K steps per stage; the B ring closes");
     if (nkb == 0) issue_scales();
-    auto stage = [&](int kb, auto FAST) {
+    auto stage = [&](int kb, auto FAST) __attribute__((always_inline)) {
         // FAST stages are 1 .. nkb - 3: the tests below hold
         constexpr bool F = decltype(FAST)::value;
         const bool nb = F || kb + 1 < nkb, n2 = F || kb + 2 < nkb;
