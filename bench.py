@@ -236,6 +236,16 @@ def planned_gemm_kernel(batch, M, N, K, L, sdt, pairs="all"):
     return name.value.decode()
 
 
+def gemm_kernel_symbol(plan, L, sdt):
+    """Name of the kernel function a planned cross-GEMM launches: the
+    launchers take the 16 x 16 MFMA forms ("...q") of the ring (two slices),
+    wide, wide4 (int8) and solo5 configurations for the slice dtypes
+    benchmarked here."""
+    q = ((plan == "ring" and L == 2) or plan in ("wide", "solo5") or
+         (plan == "wide4" and sdt == "int8"))
+    return f"cross_gemm_{plan}{'q' if q else ''}_kernel"
+
+
 def planned_split_kernel(X, xdt, sdt, L, columns):
     """Split path the planner picks for A's rows or B's columns (through its
     transposed view), as ozaki_matmul hands them over (ozk_debug_split_kernel)."""
@@ -340,7 +350,7 @@ def vendor_probes():
                                     torch.randint(-128, 128, b_sl.shape, dtype=torch.int8,
                                                   device=dev, generator=g)),
                  "zeros": (torch.zeros_like(a_sl), torch.zeros_like(b_sl))}
-        res = {"kernel": planned_gemm_kernel(1, m, m, K, L, "int8")}
+        res = {"kernel": gemm_kernel_symbol(planned_gemm_kernel(1, m, m, K, L, "int8"), L, "int8")}
         for name, (xa, xb) in kinds.items():
             ms = time_ms(lambda: ozk.cross_gemm(xa, xb.transpose(-1, -2), a_sc, b_sc, L,
                                                 torch.float64), 5)
@@ -361,7 +371,8 @@ def vendor_probes():
     del a16, z16
     for name, (L, bt, M, N, K) in (("C2", (2, 1, 4096, 4096, 4096)),
                                    ("C4", (3, 16, 1024, 1024, 2048))):
-        res = {"kernel": planned_gemm_kernel(bt, M, N, K, L, "float16")}
+        res = {"kernel": gemm_kernel_symbol(planned_gemm_kernel(bt, M, N, K, L, "float16"), L,
+                                            "float16")}
         sa = torch.ones(bt, L, M, device=dev)
         sb = torch.ones(bt, L, N, device=dev)
         for kind in ("uniform_random", "zeros"):
@@ -571,7 +582,7 @@ def main():
     achieved = cross_ops / (t_cross * 1e-3) / 1e12
     # the kernels the library chose, asked from its planner (the test hooks of
     # include/ozaki_amd_debug.h), so the profiled name is the one that ran
-    gemm_kernel = f"cross_gemm_{planned_gemm_kernel(batch, M, N, K, L, sdt, args.pairs)}_kernel"
+    gemm_kernel = gemm_kernel_symbol(planned_gemm_kernel(batch, M, N, K, L, sdt, args.pairs), L, sdt)
     # split: read the unique inputs, write the unique slices and scales
     xsz = 8 if xdt == "float64" else 4
     ssz = 1 if sdt == "int8" else 2

@@ -200,12 +200,14 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
         // default, else the wide kernel at L = 3 (with split-K on small
         // grids), wide4 at L = 4 where its rounds rule holds, the LDS-DMA
         // kernel at L = 2 and otherwise at L = 4 (its 10 pairs of a 32 x 32
-        // block take 160 accumulator registers), and at L = 5 the pair-split
-        // kernel over all i-rows: its two waves per SIMD overlap the stage
-        // DMA, which the one-wave-per-SIMD kernel serializes (measured,
-        // cross-GEMM alone, int8, pair / solo5: 8192^3 8.08 / 8.68 ms, 4096^2
-        // x 8192 2.05 / 2.43, 2048^2 x 8192 0.504 / 0.537, 1024^2 x 65536
-        // 1.05 / 1.26).  At L = 4 wide4 against the LDS-DMA kernel: 8192^3
+        // block take 160 accumulator registers), and at L = 5 the
+        // one-wave-per-SIMD kernel (int8 / fp16 / bf16; fp32 slices: the
+        // pair-split kernel over all i-rows).  Measured, cross-GEMM alone,
+        // full-range random int8 slices, pair / solo5: 8192^3 8.12 / 6.99 ms,
+        // 4096^2 x 8192 2.04 / 1.75, 2048^2 x 8192 0.487 / 0.399, 1024^2 x
+        // 65536 1.16 / 1.04, 1024^2 x 8192 0.127 / 0.101 (all 25 pairs: 14.05
+        // / 9.29, 3.52 / 2.26, 0.816 / 0.562, 1.77 / 1.12, 0.209 / 0.142).
+        // At L = 4 wide4 against the LDS-DMA kernel: 8192^3
         // 5.88 / 6.54 ms, 4096^2 x 8192 1.47-1.64 / 1.66-1.81, 2048^2 x 8192
         // 0.382 / 0.391, 1024^2 x 65536 1.05 / 0.80.  L > 5 has no kernel
         // (the caller rejects it).
@@ -214,6 +216,7 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
                     : L == 3  ? kGemmWide
                     : wide4   ? kGemmWide4
                     : L <= 4  ? kGemmDMA
+                    : solo5   ? kGemmSolo5
                               : kGemmPair;
         if (L <= 4) {
             if (forced(kGemmStaged)) plan.kind = kGemmStaged;
@@ -226,6 +229,8 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
             else if (fits && forced(kGemmKStep2) && L >= 2) plan.kind = kGemmKStep2;
         } else if (fits && forced(kGemmSolo5) && solo5) {
             plan.kind = kGemmSolo5;
+        } else if (fits && forced(kGemmPair)) {
+            plan.kind = kGemmPair;
         }
         if (plan.kind == kGemmWide4) plan.group_m = 4;
         plan.kb_per_split = nkb_all;

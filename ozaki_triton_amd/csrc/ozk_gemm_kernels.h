@@ -2463,6 +2463,10 @@ template <> struct Mfma16<_Float16> {
     using Acc = f32x4;
     static constexpr bool kExactAcc = false;
     OZK_DEV static Acc zero() { return Acc{0.0f}; }
+    template <bool AG> OZK_DEV static void run(Acc &c, i32x4 a, i32x4 b) {
+        if constexpr (AG) asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+        else asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+    }
     OZK_DEV static Acc mfma(i32x4 a, i32x4 b, Acc c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
                                                       __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
@@ -2473,6 +2477,10 @@ template <> struct Mfma16<__bf16> {
     using Acc = f32x4;
     static constexpr bool kExactAcc = false;
     OZK_DEV static Acc zero() { return Acc{0.0f}; }
+    template <bool AG> OZK_DEV static void run(Acc &c, i32x4 a, i32x4 b) {
+        if constexpr (AG) asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+        else asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+    }
     OZK_DEV static Acc mfma(i32x4 a, i32x4 b, Acc c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                        __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
@@ -3651,29 +3659,9 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ringq_kernel(GemmParams p, 
 }
 
 // ---------------------------------------------------------------------------
-// num_splits 5: one wave per SIMD, each holding all 25 slice pairs of one
-// 32 x 32 block ("solo" kernel).  4 waves of 512 registers cover a 64 x 64
-// tile: wave (x, y) = (w / 2, w % 2) reads 5 A fragments (slice u, rows of
-// x) and 5 B fragments (slice j, columns of y) per 32-byte K step for 25
-// MFMAs (0.4 fragment reads per MFMA), and sums its own pairs in the
-// reference's i-major order: one launch, no hand-off, C written once.
-// The 25 accumulator tiles take 400 registers, more than either register
-// file holds (256 each), so each MFMA is written out with its accumulator
-// placed explicitly: tiles 0..15 in AGPRs, 16..24 in VGPRs (the compiler
-// does not split a kernel's MFMA accumulators between the two files by
-// itself).  With the triangular pair set (TRI) a wave holds the 15 pairs
-// i + j <= 4, all in AGPRs, and runs 15 MFMAs per K step on the same reads.
-// The fragments are double-buffered: a K step's 10 reads are
-// issued one whole K step ahead.  A lone wave issues independent MFMAs at
-// 92-95% of the rate two waves reach (measured with 12 accumulators).
-// Hazards of the hand-placed MFMAs that the compiler cannot see: their
-// results are read by other instructions only in the epilogue, after 64 wait
-// states; an accumulator is first read as srcC after its zero fill and the
-// prologue's barrier; each one is accumulated again only 25 (TRI: 15) MFMAs
-// later.
-// The LDS holds two whole stages of 128 bytes of K (2 x 80 KB); stage kb + 2
-// is fetched into stage kb's buffer after the barrier of stage kb, spread
-// over the two K steps that follow it.
+// num_splits 5: the tile and stage of the one-wave-per-SIMD ("solo") kernel
+// below: 64 x 64 tiles, 4 waves, two whole stages of 128 bytes of K (2 x 80
+// KB of LDS).
 // ---------------------------------------------------------------------------
 struct Solo5Shape {
     static constexpr int L = 5, BM = 64, BN = 64;
@@ -3684,37 +3672,92 @@ struct Solo5Shape {
     static constexpr int LA = A_BYTES / (NW * 1024);     // A instructions per wave per stage
     static constexpr int LB = B_BYTES / (NW * 1024);
     static constexpr int LPS = LA + LB;
-    static constexpr int P1 = LPS / 2;                   // issued in the K step after the barrier
     static constexpr int LDS_BYTES = 2 * STAGE;
     static constexpr int NSC = L * (BM + BN) / 64;       // scale instructions (64 entries each)
     static constexpr int SCQ = (NSC + NW - 1) / NW;
-    static constexpr int NAGPR = 16;                     // accumulator tiles in AGPRs
     static_assert(A_BYTES % (NW * 1024) == 0 && B_BYTES % (NW * 1024) == 0,
                   "a half stage must be whole 1 KB windows per wave");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS");
     static_assert(kDmaRB == 128, "128-byte stage rows");
 };
 
+// The B group order and A read plan of cross_gemm_solo5q_kernel (below).
+template <bool TRI> struct Solo5QPlan {
+    static constexpr int NG = 10, D = 3;
+    // group p of a K step is B fragment (gj(p), p / 5)
+    static constexpr int gj(int pos) {
+        constexpr int jo[5] = {0, 4, 1, 3, 2};
+        return jo[pos % 5];
+    }
+    // the group after which A fragment row i is read for the next step: its
+    // last use in the step, and not before the barrier group NG - D
+    static constexpr int a_next(int i) {
+        int last = 0;
+        for (int pos = 0; pos < NG; ++pos)
+            if (Pairs<5, TRI>::kept(i, gj(pos))) last = pos;
+        return last > NG - D ? last : NG - D;
+    }
+};
+static_assert(Solo5QPlan<true>::a_next(4) == 7 && Solo5QPlan<true>::a_next(3) == 7 &&
+                  Solo5QPlan<true>::a_next(2) == 9 && Solo5QPlan<false>::a_next(4) == 9,
+              "solo5q read plan");
+
+// ---------------------------------------------------------------------------
+// The solo configuration for num_splits 5 on 16 x 16 MFMAs (int8, fp16, bf16
+// slices): 64 x 64 tiles, 4 waves (one per SIMD), wave (x, y) = (w / 2, w %
+// 2) holding every kept pair of 32 x 32 block (x, y) as 4 tiles of 16 x 16:
+// acc[n][rh][ch] for pair n (i-major, j-minor), register e of lane l at row
+// 16 rh + 4 (l / 16) + e, column 16 ch + l % 16 of the block.  All 25 pairs:
+// 100 tiles, 400 registers, pairs 0..15 in AGPRs and 16..24 in VGPRs; the
+// triangle i + j <= 4: 60 tiles, all in AGPRs.  The MFMAs are inline
+// assembly with the accumulator's file fixed (as in the 32 x 32 form: the
+// compiler does not split accumulators between the files itself).
+// Per 64-byte K step a wave reads its 10 A fragments (i, rh), resident
+// through the step, and its 10 B fragments (j, ch) through a ring of 5, B
+// group p + 3 read while group p's MFMAs run; group p is B fragment (jo[p %
+// 5], p / 5), jo = 0, 4, 1, 3, 2, so that any three groups of the triangle
+// hold at least 12 MFMAs.  The next step's A fragment (i, rh) is read after
+// its last MFMA of the step, and not before group 7, where the stage barrier
+// sits.  The LDS holds two whole stages (2 x 80 KB); DMA windows and the
+// unchecked DMA of interior stages as in cross_gemm_ringq_kernel.  Hazards of
+// the hand-placed MFMAs: results read only in the epilogue, after 64 wait
+// states; an accumulator read as srcC first after its zero fill and the
+// prologue barrier, and again only 60 (25 pairs) or 36 (triangle) MFMAs
+// later.
+// ---------------------------------------------------------------------------
 template <typename ST, typename AccT, bool TRI>
-__global__ __launch_bounds__(256, 1) void cross_gemm_solo5_kernel(GemmParams p, int group_m,
-                                                                  uint32_t a_records,
-                                                                  uint32_t b_records) {
+__global__ __launch_bounds__(256, 1) void cross_gemm_solo5q_kernel(GemmParams p, int group_m,
+                                                                   uint32_t a_records,
+                                                                   uint32_t b_records) {
     resolve_split_fail(p);
     using Sh = Solo5Shape;
-    using MF = Mfma<ST>;
+    using MF = Mfma16<ST>;
     using Acc = typename MF::Acc;
     using OA = AccT;
     constexpr int L = Sh::L, BM = Sh::BM, BN = Sh::BN;
     using PS = Pairs<L, TRI>;
     constexpr int ES = (int)sizeof(ST);
     constexpr uint32_t kOOB = 0x80000000u;
+    // DMA of stage kb + 2: P1 instructions after the barrier of stage kb, the
+    // rest in groups 0 .. G0 - 1 of stage kb + 1's first step.  The triangle's
+    // steps are 60 MFMAs long, and its DMA goes out earlier (8192^3, int8,
+    // TFLOP/s end to end against (4, 10): (10, 4) 158.8, (12, 5) 156.8, (8, 5)
+    // 156.7, (8, 3) 155.9, (8, 10) 153.7, (4, 5) 151.3, (4, 10) 149.5; all
+    // pairs: (4, 10) 121.9, (8, 10) 121.4, (8, 5) 120.2, (4, 5) 118.9).
+    constexpr int P1 = TRI ? 10 : 4;
+    constexpr int G0 = TRI ? 4 : 10;
+    constexpr int NAG = TRI ? PS::N : 16;      // pairs whose tiles sit in AGPRs
+    constexpr int NG = 2 * L, D = 3, R = 5;    // B groups per step, read distance, ring slots
+    constexpr int NPA = 2 * L;                 // A fragments (i, rh)
+    static_assert(Sh::NW == 4 && Sh::LA == 10 && Sh::LB == 10 && BM == 64 && BN == 64,
+                  "the window arithmetic below is written for this shape");
+    static_assert(NG % R == 0 && R > D && NAG * 4 * 4 <= 256, "ring; AGPR file");
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wx = wave >> 1, wy = wave & 1;
-    const int h = lane >> 5, lr = lane & 31;
 
     const int64_t tiles_m = (p.M + BM - 1) / BM;
     const int64_t tiles_n = (p.N + BN - 1) / BN;
@@ -3737,49 +3780,70 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_solo5_kernel(GemmParams p, 
     const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc(
         (void *)((const char *)p.B + bidx * p.bs_b * ES), (short)0, (int)b_records, 0x00020000);
 
-    // DMA: window wave * LA + q of the A half (q < LA), else wave * LB + q - LA
-    // of the B half; a 1 KB window is 8 whole 128-byte rows of one slice
-    // (lane -> row lane / 8, physical chunk lane % 8, holding logical chunk
-    // (lane % 8) ^ (lane / 16) ^ (4 in an odd window)).  The source offset is
-    // a uniform part, through readfirstlane at each use, plus one of four lane
-    // parts.
-    auto window = [&](int q) { return q < Sh::LA ? wave * Sh::LA + q : wave * Sh::LB + q - Sh::LA; };
-    const int lrow = lane >> 3;
-    const int c0 = (lane & 7) ^ (lane >> 4);
-    const uint32_t ch16[2] = {(uint32_t)c0 * 16, (uint32_t)(c0 ^ 4) * 16};
-    const uint32_t a_lp[2] = {(uint32_t)(lrow * p.as_m * ES) + ch16[0],
-                              (uint32_t)(lrow * p.as_m * ES) + ch16[1]};
-    const uint32_t b_lp[2] = {(uint32_t)(lrow * p.bs_n * ES) + ch16[0],
-                              (uint32_t)(lrow * p.bs_n * ES) + ch16[1]};
+    // Stage DMA: 1 KB windows of 8 whole 128-byte rows (lane -> row lane / 8,
+    // physical chunk lane % 8, which holds logical chunk c0 = (lane % 8) ^
+    // (lane / 16) in an even window and c0 ^ 4 in an odd one); the stage's
+    // windows r = 8 s + x (slice s, rows 8 x of the tile) sit at r KB of the A
+    // and B regions.  Wave w fetches windows w + 4 q of each (q < 10: slice q
+    // / 2, row window w + 4 (q % 2)): its windows share its parity, and their
+    // sources are a base, plus a slice stride, plus 32 rows.
+    const int64_t a_first = m0 + 8 * wave, b_first = n0 + 8 * wave;
+    const uint32_t a_base = (uint32_t)__builtin_amdgcn_readfirstlane((int)((a_first * p.as_m) * ES));
+    const uint32_t b_base = (uint32_t)__builtin_amdgcn_readfirstlane((int)((b_first * p.bs_n) * ES));
+    const uint32_t a_sstep = (uint32_t)__builtin_amdgcn_readfirstlane((int)(p.as_l * ES));
+    const uint32_t b_sstep = (uint32_t)__builtin_amdgcn_readfirstlane((int)(p.bs_l * ES));
+    const uint32_t a_hstep = (uint32_t)__builtin_amdgcn_readfirstlane((int)(32 * p.as_m * ES));
+    const uint32_t b_hstep = (uint32_t)__builtin_amdgcn_readfirstlane((int)(32 * p.bs_n * ES));
+    // rows of this wave's windows inside the operand (may be <= 0)
+    const int a_rows0 = (int)(p.M - a_first < 8 ? p.M - a_first : 8);
+    const int a_rows1 = (int)(p.M - a_first - 32 < 8 ? p.M - a_first - 32 : 8);
+    const int b_rows0 = (int)(p.N - b_first < 8 ? p.N - b_first : 8);
+    const int b_rows1 = (int)(p.N - b_first - 32 < 8 ? p.N - b_first - 32 : 8);
+    uint32_t lane_src[2];   // [A, B]
+    {
+        const int c0 = (lane & 7) ^ (lane >> 4);
+        const uint32_t chb = (uint32_t)((wave & 1) ? (c0 ^ 4) : c0) * 16;
+        lane_src[0] = (uint32_t)((lane >> 3) * p.as_m * ES) + chb;
+        lane_src[1] = (uint32_t)((lane >> 3) * p.bs_n * ES) + chb;
+    }
+    const int nkb_full = (int)(kbytes / kDmaRB);   // stages inside K
     auto buf = [&](int kb) { return smem + (kb & 1) * Sh::STAGE; };
-    auto issue = [&](int kb, int q) {
-        const int w = window(q);
-        const int par = w & 1;
-        int64_t first, rows, ubase;
-        if (q < Sh::LA) {
-            first = m0 + (w % (BM / 8)) * 8;
-            rows = p.M;
-            ubase = ((int64_t)(w / (BM / 8)) * p.as_l + first * p.as_m) * ES;
-        } else {
-            first = n0 + (w % (BN / 8)) * 8;
-            rows = p.N;
-            ubase = ((int64_t)(w / (BN / 8)) * p.bs_l + first * p.bs_n) * ES;
-        }
-        const int rows_left = (int)(rows - first < 8 ? rows - first : 8);   // may be <= 0
-        const int kleft = (int)kbytes - kb * kDmaRB;                       // > 0
-        const uint32_t ub = (uint32_t)__builtin_amdgcn_readfirstlane((int)(ubase + kb * kDmaRB));
-        const bool ok = lrow < rows_left && (int)ch16[par] < kleft;
-        const uint32_t vo = ok ? (q < Sh::LA ? a_lp[par] : b_lp[par]) + ub : kOOB;
+    // DMA instruction q (< LA: A window q of this wave; else B window q - LA)
+    // of stage kb; q is a constant at every call.  FAST: the window's rows and
+    // the stage are known to lie inside the operand, and the uniform part of
+    // the source is the instruction's scalar offset.
+    auto issue = [&](int kb, int q, auto FAST) {
+        const bool isa = q < Sh::LA;
+        const int qq = isa ? q : q - Sh::LA;
+        const uint32_t ub = (isa ? a_base + (uint32_t)(qq >> 1) * a_sstep + ((qq & 1) ? a_hstep : 0u)
+                                 : b_base + (uint32_t)(qq >> 1) * b_sstep + ((qq & 1) ? b_hstep : 0u)) +
+                            (uint32_t)kb * kDmaRB;
+        const uint32_t lsrc = lane_src[isa ? 0 : 1];
         auto *ldsp = (__attribute__((address_space(3))) void *)(
-            buf(kb) + (q < Sh::LA ? 0 : Sh::A_BYTES) + w * 1024);
-        if (q < Sh::LA) __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, ldsp, 16, vo, 0, 0, 0);
+            buf(kb) + (isa ? 0 : Sh::A_BYTES) + (wave + 4 * qq) * 1024);
+        if constexpr (decltype(FAST)::value) {
+            if (isa) __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, ldsp, 16, lsrc, (int)ub, 0, 0);
+            else __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, ldsp, 16, lsrc, (int)ub, 0, 0);
+            return;
+        }
+        const int rows = isa ? ((qq & 1) ? a_rows1 : a_rows0) : ((qq & 1) ? b_rows1 : b_rows0);
+        uint32_t vo;
+        if (rows == 8 && kb < nkb_full) {
+            vo = lsrc + ub;
+        } else {
+            const int kleft = (int)kbytes - kb * kDmaRB;   // > 0
+            const int ln = lane_here();
+            const int c0 = (ln & 7) ^ (ln >> 4);
+            const int chb = ((wave & 1) ? (c0 ^ 4) : c0) * 16;
+            vo = ((ln >> 3) < rows && chb < kleft) ? lsrc + ub : kOOB;
+        }
+        if (isa) __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, ldsp, 16, vo, 0, 0, 0);
         else __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, ldsp, 16, vo, 0, 0, 0);
     };
 
-    // The tile's scales (A's [L][BM], then B's [L][BN]: 2560 bytes) come by
-    // dword DMA into the buffer of stage nkb, which holds no stage the tile
-    // still reads, at the start of the last stage: instruction u (wave u % 4)
-    // fetches entries 64 u .. 64 u + 63.
+    // The tile's scales (A's [L][BM], then B's [L][BN]: 2560 bytes) into the
+    // buffer of stage nkb at the start of the last stage: instruction u (wave
+    // u % 4) fetches entries 64 u .. 64 u + 63.
     char *const scl = buf(nkb);
     auto issue_scales = [&]() {
 #pragma unroll
@@ -3787,7 +3851,7 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_solo5_kernel(GemmParams p, 
             const int u = q * Sh::NW + wave;
             if (u >= Sh::NSC) break;
             const bool isa = u < L * BM / 64;
-            const int e = (isa ? u : u - L * BM / 64) * 64 + lane;
+            const int e = (isa ? u : u - L * BM / 64) * 64 + lane_here();
             const int s = isa ? e / BM : e / BN;                 // slice
             const int64_t rc = isa ? m0 + e % BM : n0 + e % BN;  // row of A / column of B
             const int64_t ext = isa ? ((int64_t)(L - 1) * p.sas_l + (p.M - 1) * p.sas_m + 1)
@@ -3805,104 +3869,148 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_solo5_kernel(GemmParams p, 
     };
     const float *sa_lds = (const float *)scl, *sb_lds = (const float *)(scl + L * BM * 4);
 
-    Acc acc[L][L];
-#pragma unroll
-    for (int u = 0; u < L; ++u)
-#pragma unroll
-        for (int j = 0; j < L; ++j) acc[u][j] = MF::zero();
-    // The MFMAs below are inline assembly, which the compiler's hazard
-    // recogniser does not see into: the zeroed accumulators are pinned in
-    // their register files here, before the prologue, and 8 wait states
-    // separate those writes from any MFMA that reads them.
+    Acc acc[PS::N][2][2];
     static_for<PS::N>([&](auto n_) {
         constexpr int n = decltype(n_)::value;
-        constexpr int i = PS::i_of(n), j = PS::j_of(n);
-        (void)acc;   // an ordinary use, so that the capture does not hinge on the asm operands
-        if constexpr (n < Sh::NAGPR) asm volatile("" : "+a"(acc[i][j]));
-        else asm volatile("" : "+v"(acc[i][j]));
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+            acc[n][x >> 1][x & 1] = MF::zero();
+            // pinned where the hand-placed MFMAs keep it
+            if constexpr (n < NAG) asm volatile("" : "+a"(acc[n][x >> 1][x & 1]));
+            else asm volatile("" : "+v"(acc[n][x >> 1][x & 1]));
+        }
     });
     asm volatile("s_nop 7" ::: "memory");
 
     // prologue: stages 0 and 1; stage 0 must land before the first reads
+    constexpr std::false_type kChecked{};
+    constexpr std::true_type kFast{};
 #pragma unroll
-    for (int q = 0; q < Sh::LPS; ++q) issue(0, q);
+    for (int q = 0; q < Sh::LPS; ++q) issue(0, q, kChecked);
     if (nkb > 1) {
 #pragma unroll
-        for (int q = 0; q < Sh::LPS; ++q) issue(1, q);
+        for (int q = 0; q < Sh::LPS; ++q) issue(1, q, kChecked);
         wait_vmcnt<Sh::LPS>();
     } else {
         wait_vmcnt<0>();
     }
     exec_barrier();
 
-    struct Frags {
-        i32x4 a[L];
-        i32x4 b[L];
-    };
-    // Fragment rows start at multiples of 32, so a lane's swizzle key is that
-    // of lr for every fragment: the address is a uniform row offset (through
-    // readfirstlane) plus one of four per-lane offsets, one per K step.
-    const int key = (lr >> 1) & 7;
-    int lane_rd[4];
+    // fragments: one lane address per region and K step, the fragment's row
+    // its LDS read's immediate
+    const int qrow = lane & 15;
+    const int key = (qrow >> 1) & 7;
+    int lane_rd[2];
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) lane_rd[kk] = lr * kDmaRB + (((2 * kk + h) ^ key) << 4);
+    for (int kk = 0; kk < 2; ++kk) lane_rd[kk] = qrow * kDmaRB + (((4 * kk + (lane >> 4)) ^ key) << 4);
     const int smem_base = (int)(uintptr_t)(__attribute__((address_space(3))) char *)smem;
-    auto lds_at = [&](int uniform, int kk) {
-        const int u = __builtin_amdgcn_readfirstlane(uniform);
-        return (const __attribute__((address_space(3))) i32x4 *)(uintptr_t)(u + lane_rd[kk]);
+    using lds_cptr = const __attribute__((address_space(3))) char *;
+    const int a_org = wx * 32 * kDmaRB;
+    const int b_org = Sh::A_BYTES + wy * 32 * kDmaRB;
+    auto region = [&](int kb, int kk, int org) {
+        const int u = __builtin_amdgcn_readfirstlane(smem_base + (kb & 1) * Sh::STAGE + org);
+        return (lds_cptr)(uintptr_t)(u + lane_rd[kk]);
     };
-    auto read_all = [&](int kb, int kk, Frags &f) {
-        const int base = smem_base + (kb & 1) * Sh::STAGE;
-#pragma unroll
-        for (int u = 0; u < L; ++u) f.a[u] = *lds_at(base + (u * BM + wx * 32) * kDmaRB, kk);
-#pragma unroll
-        for (int j = 0; j < L; ++j)
-            f.b[j] = *lds_at(base + Sh::A_BYTES + (j * BN + wy * 32) * kDmaRB, kk);
+    auto read_a = [&](lds_cptr ra, int pa) {   // A fragment pa = (i, rh)
+        return *(const __attribute__((address_space(3))) i32x4 *)(
+            ra + ((pa >> 1) * BM + 16 * (pa & 1)) * kDmaRB);
     };
-    // One K step: all reads of the next K step (stage rkb, step nkk) into
-    // `nxt`, issued first, then the 25 MFMAs of `cur`, with, if `on`, DMA
-    // instructions [lo, hi) of stage dkb spread between them.
-    auto step = [&](const Frags &cur, Frags &nxt, int rkb, int nkk, int dkb, bool on, int lo,
-                    int hi) {
-        constexpr int NMF = PS::N;
-        const int cnt = hi - lo;
-        read_all(rkb, nkk, nxt);
-        static_for<NMF>([&](auto n_) {
-            constexpr int n = decltype(n_)::value;
-            constexpr int u = PS::i_of(n), j = PS::j_of(n);
-            HandMfma<ST, (n < Sh::NAGPR)>::run(acc[u][j], cur.a[u], cur.b[j]);
-#pragma unroll
-            for (int d = 0; d < Sh::LPS; ++d) {
-                // instruction lo + d goes after MFMA (d * NMF) / cnt
-                if (d < cnt && (d * NMF) / cnt == n && on) issue(dkb, lo + d);
+    using QP = Solo5QPlan<TRI>;
+    auto read_b = [&](lds_cptr rb, int pos) {   // B fragment of group pos
+        return *(const __attribute__((address_space(3))) i32x4 *)(
+            rb + (QP::gj(pos) * BN + 16 * (pos / 5)) * kDmaRB);
+    };
+
+    i32x4 fa[NPA];   // A fragments, resident through a K step
+    i32x4 fb[R];     // B groups p .. p + 4 (p mod 5)
+
+    // One K step: group pos runs the MFMAs of B fragment pos with every kept
+    // A fragment and first reads B group pos + 3 (groups 7..9: groups 0..2 of
+    // the next step, stage nkb_, step nkk).  With `bar`, group 7 starts behind
+    // the stage barrier.  DMA instructions [lo, hi) of stage dkb go between
+    // the MFMA slots of groups dg0 .. dg1 - 1 (LO, HI, DG0, DG1: compile-time
+    // constants; FAST: as issue's).
+    auto stepq = [&](int ckb, int ckk, int nkb_, int nkk, bool bar, int dkb, bool on, auto LO,
+                     auto HI, auto DG0, auto DG1, auto FAST) __attribute__((always_inline)) {
+        constexpr int lo = decltype(LO)::value, cnt = decltype(HI)::value - lo;
+        constexpr int dg0 = decltype(DG0)::value, dg1 = decltype(DG1)::value;
+        constexpr int span = (dg1 - dg0) * NPA;
+        const lds_cptr rb_cur = region(ckb, ckk, b_org);
+        static_for<NG>([&](auto pos_) {
+            constexpr int pos = decltype(pos_)::value;
+            if constexpr (pos + D < NG) {
+                fb[(pos + D) % R] = read_b(rb_cur, pos + D);
+            } else {
+                if (pos == NG - D && bar) {
+                    // stage nkb_ has landed (this wave's DMA, then every
+                    // wave's through the barrier), and every wave's reads of
+                    // stage ckb are complete before its buffer is refilled
+                    wait_vmcnt<0>();
+                    __builtin_amdgcn_s_waitcnt(0xC07F);
+                    exec_barrier();
+                }
+                fb[(pos + D) % R] = read_b(region(nkb_, nkk, b_org), pos + D - NG);
             }
-            __builtin_amdgcn_sched_barrier(0);
+            constexpr int j = QP::gj(pos), ch = pos / 5;
+            static_for<NPA>([&](auto pa_) {
+                constexpr int pa = decltype(pa_)::value;
+                constexpr int i = pa >> 1, rh = pa & 1;
+                if constexpr (PS::kept(i, j)) {
+                    constexpr int n = PS::first(i) + j;
+                    MF::template run<(n < NAG)>(acc[n][rh][ch], fa[pa], fb[pos % R]);
+                }
+                if constexpr (pos == QP::a_next(i)) fa[pa] = read_a(region(nkb_, nkk, a_org), pa);
+                constexpr int n = (pos - dg0) * NPA + pa;
+                static_for<cnt>([&](auto d_) {
+                    // instruction lo + d goes after slot (d * span) / cnt of the span
+                    constexpr int d = decltype(d_)::value;
+                    if constexpr (pos >= dg0 && pos < dg1 && (d * span) / cnt == n) {
+                        if (on) issue(dkb, lo + d, FAST);
+                    }
+                });
+                __builtin_amdgcn_sched_barrier(0);
+            });
         });
     };
 
-    Frags f0, f1;
-    if (nkb > 0) read_all(0, 0, f0);
-    static_assert(kDmaRB / 32 == 4, "four 32-byte K steps per stage");
+    if (nkb > 0) {
+        const lds_cptr ra0 = region(0, 0, a_org), rb0 = region(0, 0, b_org);
+#pragma unroll
+        for (int pa = 0; pa < NPA; ++pa) fa[pa] = read_a(ra0, pa);
+#pragma unroll
+        for (int pos = 0; pos < D; ++pos) fb[pos] = read_b(rb0, pos);
+    }
+    static_assert(kDmaRB / 64 == 2, "two 64-byte K steps per stage");
     if (nkb == 0) issue_scales();
-    for (int kb = 0; kb < nkb; ++kb) {
-        const bool nb = kb + 1 < nkb, n2 = kb + 2 < nkb;
+    auto stage = [&](int kb, auto FAST) __attribute__((always_inline)) {
+        // FAST stages are 1 .. nkb - 3: the tests below hold
+        constexpr bool F = decltype(FAST)::value;
+        const bool nb = F || kb + 1 < nkb, n2 = F || kb + 2 < nkb;
         // no DMA is outstanding in the last stage: its waits are unaffected
         if (!nb) issue_scales();
         // the rest of stage kb + 1 (stage 1 went out whole in the prologue)
-        step(f0, f1, kb, 1, kb + 1, nb && kb >= 1, Sh::P1, Sh::LPS);
-        step(f1, f0, kb, 2, kb + 1, false, 0, 0);
-        step(f0, f1, kb, 3, kb + 1, false, 0, 0);
-        if (nb) {
-            // stage kb + 1 is the only DMA outstanding; the barrier publishes
-            // every wave's DMA writes, and the lgkmcnt wait makes this wave's
-            // reads of stage kb complete before its buffer is refilled
-            wait_vmcnt<0>();
-            __builtin_amdgcn_s_waitcnt(0xC07F);
-            exec_barrier();
-        }
-        // the last step reads stage kb + 1's step 0 (unused past the end)
-        step(f1, f0, kb + 1, 0, kb + 2, n2, 0, Sh::P1);
+        stepq(kb, 0, kb, 1, false, kb + 1, nb && (F || kb >= 1), std::integral_constant<int, P1>{},
+              std::integral_constant<int, Sh::LPS>{}, std::integral_constant<int, 0>{},
+              std::integral_constant<int, G0>{}, FAST);
+        // groups 7..9 read stage kb + 1's step 0 (unused past the end) and
+        // start stage kb + 2 in stage kb's buffer
+        stepq(kb, 1, kb + 1, 0, nb, kb + 2, n2, std::integral_constant<int, 0>{},
+              std::integral_constant<int, P1>{}, std::integral_constant<int, NG - D>{},
+              std::integral_constant<int, NG>{}, FAST);
+    };
+    // Stages 1 .. kfast - 1 of a tile whose windows all lie inside M and N
+    // issue all their DMA (stages kb + 1 and kb + 2 exist and lie inside K)
+    // with no tests; the others test each instruction.
+    const bool tile_full = a_rows0 == 8 && a_rows1 == 8 && b_rows0 == 8 && b_rows1 == 8;
+    const int kfast = min(nkb - 2, nkb_full - 2);
+    {
+        int kb = 0;
+        if (nkb > 0) stage(kb++, kChecked);
+        if (tile_full)
+            for (; kb < kfast; ++kb) stage(kb, kFast);
+        for (; kb < nkb; ++kb) stage(kb, kChecked);
     }
+
     // the hand-placed MFMAs' results are read below: 64 wait states first
     asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory");
 
@@ -3910,36 +4018,55 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_solo5_kernel(GemmParams p, 
     wait_vmcnt<0>();
     __builtin_amdgcn_s_waitcnt(0xC07F);
     exec_barrier();
-    const int ct = wy * 32 + lr;
-    const int64_t col = n0 + ct;
+    const int elane = lane_here();
+    const int eq = elane & 15, eg = elane >> 4;
     const int64_t cbase = bidx * p.cs_b;
-    float sbv[L];
+    float sbv[L][2];
 #pragma unroll
-    for (int j = 0; j < L; ++j) sbv[j] = sb_lds[j * BN + ct];
+    for (int j = 0; j < L; ++j)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        // scales of accumulator registers 4 q .. 4 q + 3: one 16-byte read per slice
-        f32x4 s4[L];
+        for (int ch = 0; ch < 2; ++ch) sbv[j][ch] = sb_lds[j * BN + wy * 32 + 16 * ch + eq];
+    OA out[2][2][4];
 #pragma unroll
-        for (int i = 0; i < L; ++i) s4[i] = *(const f32x4 *)(sa_lds + i * BM + wx * 32 + 8 * q + 4 * h);
+    for (int rh = 0; rh < 2; ++rh)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int r = 4 * q + e;
-            const int64_t row = m0 + wx * 32 + 8 * q + 4 * h + e;
-            OA out = (OA)0;
+        for (int ch = 0; ch < 2; ++ch)
 #pragma unroll
-            for (int i = 0; i < L; ++i)
+            for (int e = 0; e < 4; ++e) out[rh][ch][e] = (OA)0;
+    static_for<L>([&](auto i_) {
+        constexpr int i = decltype(i_)::value;
+        f32x4 s4[2];
 #pragma unroll
-                for (int j = 0; j < L; ++j) {
-                    if (!PS::kept(i, j)) continue;
-                    // fl32(fl32(fl32(acc) * sa_i) * sb_j), summed i-major, j-minor
-                    const float t1 = MF::to_f32(acc[i][j][r]) * s4[i][e];
-                    out = out + (OA)(t1 * sbv[j]);
-                }
-            if (col < p.N && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
+        for (int rh = 0; rh < 2; ++rh) s4[rh] = *(const f32x4 *)(sa_lds + i * BM + wx * 32 + 16 * rh + 4 * eg);
+        static_for<L>([&](auto j_) {
+            constexpr int j = decltype(j_)::value;
+            if constexpr (PS::kept(i, j)) {
+                constexpr int n = PS::first(i) + j;
+#pragma unroll
+                for (int rh = 0; rh < 2; ++rh)
+#pragma unroll
+                    for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            // fl32(fl32(fl32(acc) * sa_i) * sb_j), summed i-major, j-minor
+                            const float t1 = MF::to_f32(acc[n][rh][ch][e]) * s4[rh][e];
+                            out[rh][ch][e] = out[rh][ch][e] + (OA)(t1 * sbv[j][ch]);
+                        }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        });
+    });
+#pragma unroll
+    for (int rh = 0; rh < 2; ++rh)
+#pragma unroll
+        for (int ch = 0; ch < 2; ++ch) {
+            const int64_t col = n0 + wy * 32 + 16 * ch + eq;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int64_t row = m0 + wx * 32 + 16 * rh + 4 * eg + e;
+                if (col < p.N && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, out[rh][ch][e]);
+            }
         }
-        __builtin_amdgcn_sched_barrier(0);
-    }
 }
 
 // ---------------------------------------------------------------------------
@@ -4096,7 +4223,7 @@ static hipError_t launch_solo5(const GemmParams &p, const GemmPlan &plan, hipStr
         return hipErrorInvalidValue;   // no fp32-slice form
     } else {
         using Sh = Solo5Shape;
-        auto kern = cross_gemm_solo5_kernel<ST, AccT, TRI>;
+        auto kern = cross_gemm_solo5q_kernel<ST, AccT, TRI>;
         static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
         if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
         const int es = (int)sizeof(ST);

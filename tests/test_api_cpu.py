@@ -617,16 +617,18 @@ def _gemm_kernel_pairs(L, batch, M, N, K, nsp, sd, pairs, cus=256):
 def test_triangular_planner():
     """The triangular pair set runs on the kernels that hold every pair of a
     block in one wave: the K-step kernel on small grids as for all pairs, else
-    the wide kernel at 3 slices (split-K on small grids), the pair-split kernel
-    in one launch at 5, the LDS-DMA kernel at 2, and at 4 wide4 where its
-    rounds rule holds and the LDS-DMA kernel elsewhere; one slice plans as all
-    pairs."""
+    the wide kernel at 3 slices (split-K on small grids), the one-wave-per-SIMD
+    kernel at 5 (the pair-split kernel for fp32 slices), the LDS-DMA kernel at
+    2, and at 4 wide4 where its rounds rule holds and the LDS-DMA kernel
+    elsewhere; one slice plans as all pairs."""
     from ozaki_triton_amd import _lib
     L = _lib.load()
     I8, F16, F32 = _lib.OZK_I8, _lib.OZK_F16, _lib.OZK_F32
     T, A = _lib.OZK_PAIRS_TRIANGULAR, _lib.OZK_PAIRS_ALL
     c3 = (1, 8192, 8192, 8192)
-    assert _gemm_kernel_pairs(L, *c3, 5, I8, T) == ("pair", 1)
+    assert _gemm_kernel_pairs(L, *c3, 5, I8, T) == ("solo5", 1)
+    assert _gemm_kernel_pairs(L, *c3, 5, F16, T) == ("solo5", 1)
+    assert _gemm_kernel_pairs(L, *c3, 5, F32, T) == ("pair", 1)
     assert _gemm_kernel_pairs(L, *c3, 5, I8, A) == ("solo5", 1)
     assert _gemm_kernel_pairs(L, *c3, 4, I8, T) == ("wide4", 1)
     assert _gemm_kernel_pairs(L, 1, 2048, 2048, 8192, 4, I8, T) == ("dma", 1)
