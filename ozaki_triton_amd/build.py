@@ -82,8 +82,26 @@ def build(verbose: bool = False) -> str:
     res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}")
+    _check_no_undefined_own_symbols(tmp)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
+
+
+def _check_no_undefined_own_symbols(lib: str) -> None:
+    """A shared library links with undefined symbols, and the loader reports
+    them only at run time.  The host pass can leave a kernel's launch stub
+    undefined without a diagnostic (a local type it cannot lay out, for
+    instance): every symbol of the library's own namespace must be defined."""
+    nm = shutil.which("nm") or shutil.which("llvm-nm") or "/opt/rocm/llvm/bin/llvm-nm"
+    if not os.path.exists(nm):
+        return
+    res = subprocess.run([nm, "-D", "--undefined-only", lib], stdout=subprocess.PIPE,
+                         stderr=subprocess.STDOUT, text=True)
+    own = [ln.split()[-1] for ln in res.stdout.splitlines() if "_ZN3ozk" in ln]
+    if res.returncode != 0 or own:
+        os.remove(lib)
+        raise RuntimeError("libozaki_amd.so leaves symbols of its own undefined:\n" +
+                           ("\n".join(own) if own else res.stdout))
 
 
 def build_c_example(verbose: bool = False) -> str:
