@@ -4200,10 +4200,11 @@ static hipError_t launch_wide(const GemmParams &p, const GemmPlan &plan, hipStre
 template <typename ST, typename AccT, bool TRI>
 static hipError_t launch_wide4(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     using Sh = Wide4Shape;
-    // int8 slices: the 16 x 16 x 64 form (the same tile, pairs and bits)
+    // int8 / fp16 / bf16 slices: the 16 x 16 form (the same tile, pairs and bits; fp32 slices keep
+    // the 32 x 32 x 2 one)
     auto kern = [] {
-        if constexpr (std::is_same<ST, int8_t>::value) return cross_gemm_wide4q_kernel<ST, AccT, TRI>;
-        else return cross_gemm_wide4_kernel<ST, AccT, TRI>;
+        if constexpr (std::is_same<ST, float>::value) return cross_gemm_wide4_kernel<ST, AccT, TRI>;
+        else return cross_gemm_wide4q_kernel<ST, AccT, TRI>;
     }();
     static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
     if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
