@@ -3270,54 +3270,59 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wideq_kernel(GemmParams p, 
 }
 
 // ---------------------------------------------------------------------------
-// The num_splits 2 ring configuration (128 x 128 tiles; wave w holds 64 x 64
-// block w % 4 for the pairs of A slice w / 4, (i, 0) and (i, 1)) on 16 x 16
-// MFMAs (int8, fp16, bf16 slices), in the double-buffered whole stages of
-// cross_gemm_wideq_kernel (two 64 KB stages; the ring of half stages is not
-// needed where two whole stages fit).  Per 64-byte K step a wave reads its 4 A
-// fragments (rh) once and its 8 B fragments (j, ch) through a ring of 4, B
-// fragment g + 2 read while g's 4 MFMAs run: 32 MFMAs a step, 32 accumulator
-// tiles acc[j][rh][ch] (128 registers).  The epilogue hands the partial sums
-// of slice 0's waves to slice 1's through the LDS, which add their own pairs
-// in the reference's order.
+// The ring configuration on 16 x 16 MFMAs (int8, fp16, bf16 slices): 64 W x
+// 64 W tiles (W = 2 for num_splits 2, 1 for 3 and 4), 8 waves; wave w holds
+// block w % 4 (32 W x 32 W) for the pairs (i, j) of its group's A slices
+// (group 0: i < IA, group 1 the rest; IA = L / 2 rounded up, the pair
+// split's i-row), every j, as 4 W^2 tiles of 16 x 16 per pair.  The stages
+// are double-buffered whole (two fit the LDS where the 32 x 32 ring kernel
+// needs a ring of half stages).  Per 64-byte K step a wave reads its A
+// fragments (i, rh) once and its B fragments (j, ch) through a ring, B group
+// g + 2 read while group g's MFMAs run; the next step's A fragments are read
+// in the last group, each after its MFMA.  The epilogue hands group 0's
+// partial sums to group 1 through the LDS, which adds its own pairs in the
+// reference's order.  Interior stages of interior tiles issue their DMA
+// unchecked, as in cross_gemm_wideq_kernel.
 // ---------------------------------------------------------------------------
-struct RingQShape {
-    static constexpr int L = 2;
+template <int L_, int W_> struct RingQShape {
+    static constexpr int L = L_, W = W_;
     static constexpr int NW = 8;                         // waves
-    static constexpr int BM = 128, BN = 128;
-    static constexpr int A_BYTES = L * BM * kDmaRB;      // 32 KB
-    static constexpr int B_BYTES = L * BN * kDmaRB;      // 32 KB
+    static constexpr int BM = 64 * W, BN = 64 * W;
+    static constexpr int A_BYTES = L * BM * kDmaRB;
+    static constexpr int B_BYTES = L * BN * kDmaRB;
     static constexpr int STAGE = A_BYTES + B_BYTES;
     static constexpr int LA = A_BYTES / (NW * 1024);     // A instructions per wave per stage
     static constexpr int LB = B_BYTES / (NW * 1024);     // B instructions per wave per stage
     static constexpr int LPS = LA + LB;
-    static constexpr int LDS_BYTES = 2 * STAGE;          // also the fp64 hand-off: 128 x 128 x 8
+    static constexpr int LDS_BYTES = 2 * STAGE;          // also the fp64 hand-off: 4 blocks x (32 W)^2 x 8
+    static constexpr int IA = PairSplit<L, L>::P0 / L;   // A slices of group 0
+    static constexpr int NSC = L * (BM + BN) / 64;       // the tile's scales: 256-byte units
+    static_assert(PairSplit<L, L>::P0 % L == 0, "the pair groups split at an i-row");
+    static_assert(A_BYTES % (NW * 1024) == 0 && LA == LB, "whole 1 KB windows per wave");
     static_assert(LDS_BYTES <= 160 * 1024 && BM * BN * 8 <= LDS_BYTES, "LDS");
-    static_assert(L * (BM + BN) * 4 == NW * 256, "the tile's scales: one 256-byte unit per wave");
+    static_assert(NSC <= NW, "one scale unit per wave");
     static_assert(kDmaRB == 128, "128-byte stage rows");
 };
 
-template <typename ST, typename AccT>
+template <typename ST, int L, int W, typename AccT>
 __global__ __launch_bounds__(512, 1) void cross_gemm_ringq_kernel(GemmParams p, int group_m,
                                                                   uint32_t a_records,
                                                                   uint32_t b_records) {
     resolve_split_fail(p);
-    using Sh = RingQShape;
+    using Sh = RingQShape<L, W>;
     using MF = Mfma16<ST>;
     using Acc = typename MF::Acc;
     using OA = AccT;
-    constexpr int L = Sh::L, BM = Sh::BM, BN = Sh::BN;
+    constexpr int BM = Sh::BM, BN = Sh::BN, IA = Sh::IA;
     constexpr int ES = (int)sizeof(ST);
     constexpr uint32_t kOOB = 0x80000000u;
     constexpr int P1 = 2;   // DMA instructions of stage kb + 2 in the groups after the barrier
-    static_assert(Sh::NW == 8 && Sh::LA == 4 && Sh::LB == 4 && BM == 128 && BN == 128,
-                  "the window arithmetic below is written for this shape");
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int blk = wave & 3, gi = wave >> 2;   // block; A slice of the wave's pairs
+    const int blk = wave & 3, grp = wave >> 2;   // block; pair group
     const int wm = blk >> 1, wn = blk & 1;
 
     const int64_t tiles_m = (p.M + BM - 1) / BM;
@@ -3351,13 +3356,12 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ringq_kernel(GemmParams p, 
     // Stage DMA: 1 KB windows of 8 whole 128-byte rows (lane -> row lane / 8,
     // physical chunk lane % 8, which holds logical chunk c0 = (lane % 8) ^
     // (lane / 16) in an even window and c0 ^ 4 in an odd one); the stage's
-    // windows r = 16 s + x (slice s, rows 8 x of the tile) sit at r KB of the
-    // A and B regions.  Wave w fetches windows w + 8 q of each (q < 4: slice
-    // q / 2, row window w + 8 (q % 2)): its windows share its parity, and
-    // their sources are a base, plus a slice stride, plus 64 rows.  The
-    // lane's part of the source is held; the bounds are tested per lane only
-    // where a window has fewer than 8 rows in the operand or the stage runs
-    // past K.
+    // windows r = 8 W s + x (slice s, rows 8 x of the tile) sit at r KB of the
+    // A and B regions.  Wave w fetches windows w + 8 q of each (q < LA: slice
+    // q / W, row window w + 8 (q % W)): its windows share its parity, and
+    // their sources are a base, plus a slice stride, plus 64 rows.  The lane's
+    // part of the source is held; the bounds are tested per lane only where a
+    // window has fewer than 8 rows in the operand or the stage runs past K.
     const int64_t a_first = m0 + 8 * wave, b_first = n0 + 8 * wave;
     const uint32_t a_base = (uint32_t)__builtin_amdgcn_readfirstlane(
         (int)((a_first * p.as_m) * ES + kbyte0));
@@ -3388,8 +3392,9 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ringq_kernel(GemmParams p, 
     auto issue = [&](int kb, int q, auto FAST) {
         const bool isa = q < Sh::LA;
         const int qq = isa ? q : q - Sh::LA;
-        const uint32_t ub = (isa ? a_base + (uint32_t)(qq >> 1) * a_sstep + ((qq & 1) ? a_hstep : 0u)
-                                 : b_base + (uint32_t)(qq >> 1) * b_sstep + ((qq & 1) ? b_hstep : 0u)) +
+        const bool hi = (qq % W) != 0;
+        const uint32_t ub = (isa ? a_base + (uint32_t)(qq / W) * a_sstep + (hi ? a_hstep : 0u)
+                                 : b_base + (uint32_t)(qq / W) * b_sstep + (hi ? b_hstep : 0u)) +
                             (uint32_t)kb * kDmaRB;
         const uint32_t lsrc = lane_src[isa ? 0 : 1];
         auto *ldsp = (__attribute__((address_space(3))) void *)(
@@ -3399,7 +3404,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ringq_kernel(GemmParams p, 
             else __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, ldsp, 16, lsrc, (int)ub, 0, 0);
             return;
         }
-        const int rows = isa ? ((qq & 1) ? a_rows1 : a_rows0) : ((qq & 1) ? b_rows1 : b_rows0);
+        const int rows = isa ? (hi ? a_rows1 : a_rows0) : (hi ? b_rows1 : b_rows0);
         uint32_t vo;
         if (rows == 8 && kb0 + kb < nkb_full) {
             vo = lsrc + ub;
@@ -3414,11 +3419,12 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ringq_kernel(GemmParams p, 
         else __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, ldsp, 16, vo, 0, 0, 0);
     };
 
-    // The tile's scales (A's [L][BM], then B's [L][BN]: 2 KB, one 256-byte
-    // unit per wave) into the buffer of stage nkb at the start of the last
+    // The tile's scales (A's [L][BM], then B's [L][BN]: NSC 256-byte units,
+    // one per wave) into the buffer of stage nkb at the start of the last
     // stage (the lane read where they are fetched).
     char *const scl = buf(nkb);
     auto issue_scales = [&]() {
+        if (wave >= Sh::NSC) return;
         const bool isa = wave < L * BM / 64;
         const int e = (isa ? wave : wave - L * BM / 64) * 64 + lane_here();
         const int s = isa ? e / BM : e / BN;                 // slice
@@ -3460,202 +3466,226 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ringq_kernel(GemmParams p, 
     for (int kk = 0; kk < 2; ++kk) lane_rd[kk] = qrow * kDmaRB + (((4 * kk + (lane >> 4)) ^ key) << 4);
     const int smem_base = (int)(uintptr_t)(__attribute__((address_space(3))) char *)smem;
     using lds_cptr = const __attribute__((address_space(3))) char *;
-    const int a_org = (gi * BM + wm * 64) * kDmaRB;
-    const int b_org = Sh::A_BYTES + wn * 64 * kDmaRB;
+    const int b_org = Sh::A_BYTES + wn * 32 * W * kDmaRB;
     auto region = [&](int kb, int kk, int org) {
         const int u = __builtin_amdgcn_readfirstlane(smem_base + (kb & 1) * Sh::STAGE + org);
         return (lds_cptr)(uintptr_t)(u + lane_rd[kk]);
     };
-    auto read_a = [&](lds_cptr ra, int rh) {   // A fragment rh of slice gi
-        return *(const __attribute__((address_space(3))) i32x4 *)(ra + 16 * rh * kDmaRB);
-    };
+    constexpr int NR = 2 * W;   // 16-row (16-column) fragments of a 32 W block
     auto read_b = [&](lds_cptr rb, int gb) {   // B fragment gb = (j, ch)
         return *(const __attribute__((address_space(3))) i32x4 *)(
-            rb + ((gb >> 2) * BN + 16 * (gb & 3)) * kDmaRB);
+            rb + ((gb / NR) * BN + 16 * (gb % NR)) * kDmaRB);
     };
-
-    constexpr int NG = 4 * L, NPA = 4;   // B fragments (j, ch), A fragments rh
-    i32x4 fa[NPA];   // A fragments, resident through a K step
-    i32x4 fb[4];     // B fragments g .. g + 3 (g mod 4: 8 groups a step close the ring)
-    Acc acc[L][4][4];
-#pragma unroll
-    for (int j = 0; j < L; ++j)
-#pragma unroll
-        for (int rh = 0; rh < 4; ++rh)
-#pragma unroll
-            for (int ch = 0; ch < 4; ++ch) acc[j][rh][ch] = MF::zero();
-
-    // One K step, as in cross_gemm_wideq_kernel: group gb runs the 4 MFMAs
-    // of B fragment gb and first reads B fragment gb + 2 (groups 6, 7:
-    // fragments 0, 1 of the next step, stage nkb_, step nkk); in group 7 each
-    // A fragment of the next step is read right after its MFMA.  With `bar`,
-    // group 6 starts behind the stage barrier.  DMA instructions [lo, hi) of
-    // stage dkb go between the MFMAs of groups dg0 .. 7 (FAST: as issue's).
-    auto stepq = [&](int ckb, int ckk, int nkb_, int nkk, bool bar, int dkb, bool on, int lo,
-                     int hi, int dg0, auto FAST) __attribute__((always_inline)) {
-        const int cnt = hi - lo;
-        const int span = (NG - dg0) * NPA;
-        const lds_cptr rb_cur = region(ckb, ckk, b_org);
-#pragma unroll
-        for (int gb = 0; gb < NG; ++gb) {
-            if (gb < NG - 2) {
-                fb[(gb + 2) & 3] = read_b(rb_cur, gb + 2);
-            } else {
-                if (gb == NG - 2 && bar) {
-                    // stage nkb_ has landed (this wave's DMA, then every
-                    // wave's through the barrier), and every wave's reads of
-                    // stage ckb are complete before its buffer is refilled
-                    wait_vmcnt<0>();
-                    __builtin_amdgcn_s_waitcnt(0xC07F);
-                    exec_barrier();
-                }
-                fb[(gb + 2) & 3] = read_b(region(nkb_, nkk, b_org), gb - (NG - 2));
-            }
-            const int j = gb >> 2, ch = gb & 3;
-            const lds_cptr ra_next = region(nkb_, nkk, a_org);
-#pragma unroll
-            for (int rh = 0; rh < NPA; ++rh) {
-                acc[j][rh][ch] = MF::mfma(fa[rh], fb[gb & 3], acc[j][rh][ch]);
-                if (gb == NG - 1) fa[rh] = read_a(ra_next, rh);
-                const int n = (gb - dg0) * NPA + rh;
-#pragma unroll
-                for (int d = 0; d < Sh::LPS; ++d) {
-                    // instruction lo + d goes after MFMA (d * span) / cnt of the span
-                    if (gb >= dg0 && d < cnt && (d * span) / cnt == n && on) issue(dkb, lo + d, FAST);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-    };
-
-    if (nkb > 0) {
-        const lds_cptr ra0 = region(0, 0, a_org), rb0 = region(0, 0, b_org);
-#pragma unroll
-        for (int rh = 0; rh < NPA; ++rh) fa[rh] = read_a(ra0, rh);
-        fb[0] = read_b(rb0, 0);
-        fb[1] = read_b(rb0, 1);
-    }
-    static_assert(kDmaRB / 64 == 2 && NG % 4 == 0, "two 64-byte K steps per stage; the B ring closes");
-    if (nkb == 0) issue_scales();
-    auto stage = [&](int kb, auto FAST) __attribute__((always_inline)) {
-        // FAST stages are 1 .. nkb - 3: the tests below hold
-        constexpr bool F = decltype(FAST)::value;
-        const bool nb = F || kb + 1 < nkb, n2 = F || kb + 2 < nkb;
-        // no DMA is outstanding in the last stage: its waits are unaffected
-        if (!nb) issue_scales();
-        // the rest of stage kb + 1 (stage 1 went out whole in the prologue)
-        stepq(kb, 0, kb, 1, false, kb + 1, nb && (F || kb >= 1), P1, Sh::LPS, 0, FAST);
-        // the last two groups read stage kb + 1's step 0 (unused past the
-        // end) and start stage kb + 2 in stage kb's buffer
-        stepq(kb, 1, kb + 1, 0, nb, kb + 2, n2, 0, P1, NG - 2, FAST);
-    };
-    // Stages 1 .. kfast - 1 of a tile whose windows all lie inside M and N
-    // issue all their DMA (stages kb + 1 and kb + 2 exist and lie inside K)
-    // with no tests; the others test each instruction.
-    const bool tile_full = a_rows0 == 8 && a_rows1 == 8 && b_rows0 == 8 && b_rows1 == 8;
-    const int kfast = min(nkb - 2, nkb_full - kb0 - 2);
-    int kb = 0;
-    if (nkb > 0) stage(kb++, kChecked);
-    if (tile_full)
-        for (; kb < kfast; ++kb) stage(kb, kFast);
-    for (; kb < nkb; ++kb) stage(kb, kChecked);
-
-    // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
-    wait_vmcnt<0>();
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    exec_barrier();
-    if (S > 1) {
-        // split-K, as in the ring kernel: each range stores its raw
-        // accumulators (register e of tile n = (j, rh, ch) at (n * 4 + e) *
-        // 64 + lane); the last range to arrive adds the others
-        constexpr int RW = L * 16 * 4;
-        const int ln = lane_here();
-        uint32_t *mine = splitk_slot(p, g, krange, wave, RW, ln);
-#pragma unroll
-        for (int n = 0; n < L * 16; ++n) {
-            const i32x4 u = __builtin_bit_cast(i32x4, acc[n >> 4][(n >> 2) & 3][n & 3]);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) splitk_put(mine + (n * 4 + e) * 64, (uint32_t)u[e]);
-        }
-        if (!splitk_arrive(p, g, (int *)buf(nkb + 1))) return;
-        auto get4 = [&](const uint32_t *src) {
-            i32x4 u;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) u[e] = (int)splitk_get(src + e * 64);
-            return __builtin_bit_cast(Acc, u);
-        };
-        // int32 sums are exact in any order: this range's accumulators stay
-        // and the others are added; float sums: every range read back, this
-        // one's too, in range order from range 0
-        for (int s2 = 0; s2 < S; ++s2) {
-            if (MF::kExactAcc && s2 == krange) continue;
-            const uint32_t *src = splitk_slot(p, g, s2, wave, RW, ln);
-#pragma unroll
-            for (int n = 0; n < L * 16; ++n) {
-                const Acc v = get4(src + n * 4 * 64);
-                Acc &a = acc[n >> 4][(n >> 2) & 3][n & 3];
-                a = (!MF::kExactAcc && s2 == 0) ? v : a + v;
-            }
-        }
-    }
-    const int elane = lane_here();
-    const int eq = elane & 15, eg = elane >> 4;
-    // this wave's scales into registers: sa of its rows (slice gi), sb of its
-    // columns
-    f32x4 sav[4];
-    float sbv[L][4];
-#pragma unroll
-    for (int rh = 0; rh < 4; ++rh)
-        sav[rh] = *(const f32x4 *)(sa_lds + gi * BM + wm * 64 + 16 * rh + 4 * eg);
-#pragma unroll
-    for (int j = 0; j < L; ++j)
-#pragma unroll
-        for (int ch = 0; ch < 4; ++ch) sbv[j][ch] = sb_lds[j * BN + wn * 64 + 16 * ch + eq];
-    // the partial sums overwrite the scales: every wave has read them
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    exec_barrier();
-    OA *part = (OA *)smem;   // [4 blocks][rh][ch][e][64 lanes]
+    const int cbase_row = wm * 32 * W, cbase_col = wn * 32 * W;
     const int64_t cbase = bidx * p.cs_b;
-    // fl32(fl32(fl32(acc) * sa_i) * sb_j) of pair (gi, j), summed i-major,
-    // j-minor: slice 0's waves sum their two pairs from zero, slice 1's add
-    // theirs to that
-    if (gi == 0) {
+    OA *part = (OA *)smem;   // the hand-off: [4 blocks][rh][ch][e][64 lanes]
+    auto pslot = [&](int rh, int ch, int e, int ln) {
+        return part + (((blk * NR + rh) * NR + ch) * 4 + e) * 64 + ln;
+    };
+
+    auto body = [&](auto G_) __attribute__((always_inline)) {
+        constexpr int G = decltype(G_)::value;
+        constexpr int ILO = G ? IA : 0, NI = G ? L - IA : IA;   // A slices of this group
+        constexpr int NG = L * NR, NPA = NI * NR;               // B groups (j, ch); A fragments (i, rh)
+        constexpr int R = NG % 4 == 0 ? 4 : 3;                  // B ring slots
+        static_assert(NG % R == 0 && R >= 3, "the B ring closes at the end of a step");
+        const int a_org = (ILO * BM + cbase_row) * kDmaRB;
+        auto read_a = [&](lds_cptr ra, int pa) {   // A fragment pa = (i - ILO, rh)
+            return *(const __attribute__((address_space(3))) i32x4 *)(
+                ra + ((pa / NR) * BM + 16 * (pa % NR)) * kDmaRB);
+        };
+        i32x4 fa[NPA];   // A fragments, resident through a K step
+        i32x4 fb[R];     // B groups g .. g + R - 1 (g mod R)
+        Acc acc[NI][L][NR][NR];
 #pragma unroll
-        for (int rh = 0; rh < 4; ++rh)
+        for (int i = 0; i < NI; ++i)
 #pragma unroll
-            for (int ch = 0; ch < 4; ++ch)
+            for (int j = 0; j < L; ++j)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    OA out = (OA)0;
+                for (int rh = 0; rh < NR; ++rh)
 #pragma unroll
-                    for (int j = 0; j < L; ++j) {
-                        const float t1 = MF::to_f32(acc[j][rh][ch][e]) * sav[rh][e];
-                        out = out + (OA)(t1 * sbv[j][ch]);
+                    for (int ch = 0; ch < NR; ++ch) acc[i][j][rh][ch] = MF::zero();
+
+        // One K step: group gb runs the MFMAs of B fragment gb with every A
+        // fragment and first reads B fragment gb + 2 (the last two groups:
+        // fragments 0, 1 of the next step, stage nkb_, step nkk); in the last
+        // group each A fragment of the next step is read right after its MFMA.
+        // With `bar`, group NG - 2 starts behind the stage barrier.  DMA
+        // instructions [lo, hi) of stage dkb go between the MFMAs of groups
+        // dg0 .. NG - 1 (FAST: as issue's).
+        auto stepq = [&](int ckb, int ckk, int nkb_, int nkk, bool bar, int dkb, bool on, int lo,
+                         int hi, int dg0, auto FAST) __attribute__((always_inline)) {
+            const int cnt = hi - lo;
+            const int span = (NG - dg0) * NPA;
+            const lds_cptr rb_cur = region(ckb, ckk, b_org);
+#pragma unroll
+            for (int gb = 0; gb < NG; ++gb) {
+                if (gb < NG - 2) {
+                    fb[(gb + 2) % R] = read_b(rb_cur, gb + 2);
+                } else {
+                    if (gb == NG - 2 && bar) {
+                        // stage nkb_ has landed (this wave's DMA, then every
+                        // wave's through the barrier), and every wave's reads
+                        // of stage ckb are complete before its buffer is refilled
+                        wait_vmcnt<0>();
+                        __builtin_amdgcn_s_waitcnt(0xC07F);
+                        exec_barrier();
                     }
-                    part[(((blk * 4 + rh) * 4 + ch) * 4 + e) * 64 + elane] = out;
+                    fb[(gb + 2) % R] = read_b(region(nkb_, nkk, b_org), gb - (NG - 2));
                 }
+                const int j = gb / NR, ch = gb % NR;
+                const lds_cptr ra_next = region(nkb_, nkk, a_org);
+#pragma unroll
+                for (int pa = 0; pa < NPA; ++pa) {
+                    const int i = pa / NR, rh = pa % NR;
+                    acc[i][j][rh][ch] = MF::mfma(fa[pa], fb[gb % R], acc[i][j][rh][ch]);
+                    if (gb == NG - 1) fa[pa] = read_a(ra_next, pa);
+                    const int n = (gb - dg0) * NPA + pa;
+#pragma unroll
+                    for (int d = 0; d < Sh::LPS; ++d) {
+                        // instruction lo + d goes after MFMA (d * span) / cnt of the span
+                        if (gb >= dg0 && d < cnt && (d * span) / cnt == n && on) issue(dkb, lo + d, FAST);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        };
+
+        if (nkb > 0) {
+            const lds_cptr ra0 = region(0, 0, a_org), rb0 = region(0, 0, b_org);
+#pragma unroll
+            for (int pa = 0; pa < NPA; ++pa) fa[pa] = read_a(ra0, pa);
+            fb[0] = read_b(rb0, 0);
+            fb[1] = read_b(rb0, 1);
+        }
+        static_assert(kDmaRB / 64 == 2, "two 64-byte K steps per stage");
+        if (nkb == 0) issue_scales();
+        auto stage = [&](int kb, auto FAST) __attribute__((always_inline)) {
+            // FAST stages are 1 .. nkb - 3: the tests below hold
+            constexpr bool F = decltype(FAST)::value;
+            const bool nb = F || kb + 1 < nkb, n2 = F || kb + 2 < nkb;
+            // no DMA is outstanding in the last stage: its waits are unaffected
+            if (!nb) issue_scales();
+            // the rest of stage kb + 1 (stage 1 went out whole in the prologue)
+            stepq(kb, 0, kb, 1, false, kb + 1, nb && (F || kb >= 1), P1, Sh::LPS, 0, FAST);
+            // the last two groups read stage kb + 1's step 0 (unused past the
+            // end) and start stage kb + 2 in stage kb's buffer
+            stepq(kb, 1, kb + 1, 0, nb, kb + 2, n2, 0, P1, NG - 2, FAST);
+        };
+        // Stages 1 .. kfast - 1 of a tile whose windows all lie inside M and
+        // N issue all their DMA (stages kb + 1 and kb + 2 exist and lie inside
+        // K) with no tests; the others test each instruction.
+        const bool tile_full = a_rows0 == 8 && b_rows0 == 8 && (W == 1 || (a_rows1 == 8 && b_rows1 == 8));
+        const int kfast = min(nkb - 2, nkb_full - kb0 - 2);
+        {
+            int kb = 0;
+            if (nkb > 0) stage(kb++, kChecked);
+            if (tile_full)
+                for (; kb < kfast; ++kb) stage(kb, kFast);
+            for (; kb < nkb; ++kb) stage(kb, kChecked);
+        }
+
+        // ---- epilogue: ordered outer accumulation, ozaki_triton.py:420-452 ----
+        wait_vmcnt<0>();
         __builtin_amdgcn_s_waitcnt(0xC07F);
         exec_barrier();
-    } else {
-        exec_barrier();
+        if (S > 1) {
+            // split-K, as in the ring kernel: each range stores its raw
+            // accumulators (register e of tile n = (i, j, rh, ch) at (n * 4 + e)
+            // * 64 + lane); the last range to arrive adds the others
+            constexpr int NT = NI * L * NR * NR;
+            constexpr int P0 = PairSplit<L, L>::P0, P = L * L;
+            constexpr int RW = (P0 > P - P0 ? P0 : P - P0) * W * W * 16;
+            static_assert(NT * 4 <= RW, "the hand-over slot holds the wave's tiles");
+            const int ln = lane_here();
+            uint32_t *mine = splitk_slot(p, g, krange, wave, RW, ln);
+            auto tile = [&](int n) -> Acc & {
+                return acc[n / (L * NR * NR)][(n / (NR * NR)) % L][(n / NR) % NR][n % NR];
+            };
 #pragma unroll
-        for (int rh = 0; rh < 4; ++rh)
+            for (int n = 0; n < NT; ++n) {
+                const i32x4 u = __builtin_bit_cast(i32x4, tile(n));
 #pragma unroll
-            for (int ch = 0; ch < 4; ++ch) {
-                const int64_t col = n0 + wn * 64 + 16 * ch + eq;
+                for (int e = 0; e < 4; ++e) splitk_put(mine + (n * 4 + e) * 64, (uint32_t)u[e]);
+            }
+            if (!splitk_arrive(p, g, (int *)buf(nkb + 1))) return;
+            auto get4 = [&](const uint32_t *src) {
+                i32x4 u;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int64_t row = m0 + wm * 64 + 16 * rh + 4 * eg + e;
-                    OA out = part[(((blk * 4 + rh) * 4 + ch) * 4 + e) * 64 + elane];
+                for (int e = 0; e < 4; ++e) u[e] = (int)splitk_get(src + e * 64);
+                return __builtin_bit_cast(Acc, u);
+            };
+            // int32 sums are exact in any order: this range's accumulators
+            // stay and the others are added; float sums: every range read
+            // back, this one's too, in range order from range 0
+            for (int s2 = 0; s2 < S; ++s2) {
+                if (MF::kExactAcc && s2 == krange) continue;
+                const uint32_t *src = splitk_slot(p, g, s2, wave, RW, ln);
 #pragma unroll
-                    for (int j = 0; j < L; ++j) {
-                        const float t1 = MF::to_f32(acc[j][rh][ch][e]) * sav[rh][e];
-                        out = out + (OA)(t1 * sbv[j][ch]);
-                    }
-                    if (col < p.N && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
+                for (int n = 0; n < NT; ++n) {
+                    const Acc v = get4(src + n * 4 * 64);
+                    Acc &a = tile(n);
+                    a = (!MF::kExactAcc && s2 == 0) ? v : a + v;
                 }
             }
-    }
+        }
+        const int elane = lane_here();
+        const int eq = elane & 15, eg = elane >> 4;
+        // this wave's scales into registers: sa of its rows (its group's
+        // slices), sb of its columns
+        f32x4 sav[NI][NR];
+        float sbv[L][NR];
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int rh = 0; rh < NR; ++rh)
+                sav[i][rh] = *(const f32x4 *)(sa_lds + (ILO + i) * BM + cbase_row + 16 * rh + 4 * eg);
+#pragma unroll
+        for (int j = 0; j < L; ++j)
+#pragma unroll
+            for (int ch = 0; ch < NR; ++ch) sbv[j][ch] = sb_lds[j * BN + cbase_col + 16 * ch + eq];
+        // the partial sums overwrite the scales: every wave has read them
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        exec_barrier();
+        // fl32(fl32(fl32(acc) * sa_i) * sb_j) of pair (i, j), summed i-major,
+        // j-minor: group 0 from zero, group 1 onto group 0's sums
+        auto sum_pairs = [&](OA out, int rh, int ch, int e) {
+#pragma unroll
+            for (int i = 0; i < NI; ++i)
+#pragma unroll
+                for (int j = 0; j < L; ++j) {
+                    const float t1 = MF::to_f32(acc[i][j][rh][ch][e]) * sav[i][rh][e];
+                    out = out + (OA)(t1 * sbv[j][ch]);
+                }
+            return out;
+        };
+        if constexpr (G == 0) {
+#pragma unroll
+            for (int rh = 0; rh < NR; ++rh)
+#pragma unroll
+                for (int ch = 0; ch < NR; ++ch)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) *pslot(rh, ch, e, elane) = sum_pairs((OA)0, rh, ch, e);
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            exec_barrier();
+        } else {
+            exec_barrier();
+#pragma unroll
+            for (int rh = 0; rh < NR; ++rh)
+#pragma unroll
+                for (int ch = 0; ch < NR; ++ch) {
+                    const int64_t col = n0 + cbase_col + 16 * ch + eq;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int64_t row = m0 + cbase_row + 16 * rh + 4 * eg + e;
+                        const OA out = sum_pairs(*pslot(rh, ch, e, elane), rh, ch, e);
+                        if (col < p.N && row < p.M) store_c(p, cbase + row * p.cs_m + col * p.cs_n, out);
+                    }
+                }
+        }
+    };
+    if (grp == 0) body(std::integral_constant<int, 0>{});
+    else body(std::integral_constant<int, 1>{});
 }
 
 // ---------------------------------------------------------------------------
@@ -4153,12 +4183,12 @@ static hipError_t launch_pair(const GemmParams &p, const GemmPlan &plan, hipStre
 template <typename ST, int L, typename AccT>
 static hipError_t launch_ring(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     constexpr int W = (L <= 2) ? 2 : 1;
-    // num_splits 2 with int8 / fp16 / bf16 slices: the 16 x 16 MFMA form (same
-    // tiles, waves and split-K hand-over)
-    constexpr bool kQ = L == 2 && !std::is_same<ST, float>::value;
-    using Sh = std::conditional_t<kQ, RingQShape, RingShape<L, W>>;
+    // int8 / fp16 / bf16 slices: the 16 x 16 MFMA form (same tiles, pair
+    // groups and split-K hand-over; fp32 slices keep the 32 x 32 x 2 one)
+    constexpr bool kQ = !std::is_same<ST, float>::value;
+    using Sh = std::conditional_t<kQ, RingQShape<L, W>, RingShape<L, W>>;
     auto kern = [] {
-        if constexpr (kQ) return cross_gemm_ringq_kernel<ST, AccT>;
+        if constexpr (kQ) return cross_gemm_ringq_kernel<ST, L, W, AccT>;
         else return cross_gemm_ring_kernel<ST, L, AccT, W>;
     }();
     static_assert(Sh::BM == 64 * W && Sh::BN == 64 * W, "the planner's tile size");
