@@ -148,13 +148,21 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
     const int sr = ksplit_for(nt(1, 1)), sw = ksplit_for(wide_tiles);
     const int64_t wide_rounds = (wide_tiles * sw + kCUs - 1) / kCUs;
     const int64_t ring_rounds = (nt(1, 1) * sr + kCUs - 1) / kCUs;
-    // with split-K a round of S ranges takes 1 / S of a tile's time
-    const bool wide3 = L == 3 && 12 * wide_rounds * sr < 7 * ring_rounds * sw;
+    // with split-K a round of S ranges takes 1 / S of a tile's time.  The 16
+    // x 16 forms (int8 / fp16 / bf16 slices): a wide round takes 1.42-1.56
+    // ring rounds (cross-GEMM alone, wide / ring time: rounds 2 / 3 at 1024 x
+    // 2304 x 4096 0.961, 1024 x 3072 x 4096 0.944, 1536^2 x 8192 0.982 (fp16
+    // 1.017); 2 / 4 at 2048^2 x 4096 0.771; 1 / 2 at 1280^2 x 8192 0.725; 8 /
+    // 16 at 4096^3 0.782), so the wide kernel takes ties at 3 : 2; the 32 x
+    // 32 forms (fp32 slices) about 12 : 7
+    const bool wide3 = L == 3 && (slice_dtype == 1 ? 12 * wide_rounds * sr < 7 * ring_rounds * sw
+                                                   : 3 * wide_rounds * sr <= 2 * ring_rounds * sw);
     // L = 4: the 96 x 64 wide kernel (one workgroup per CU, like the ring
-    // kernel) does 1.5 ring tiles of work per tile at 1.04-1.14x the ring's
-    // rate, about 1.45 ring tiles' time (measured: 8192^3 43 rounds against
-    // 64, 0.965x the ring's time; 4096^2 x 8192 11 / 16, 0.875x; 2048^2 x
-    // 8192 3 / 4, 0.99x; 1024^2 x 65536 1 / 1, 1.10x)
+    // kernel) does 1.5 ring tiles of work per tile in about 1.45 ring tiles'
+    // time (measured, 16 x 16 forms, wide4 / ring time: 8192^3 43 rounds
+    // against 64, 0.966; 4096^2 x 8192 11 / 16, 0.957; 3072^2 x 8192 6 / 9,
+    // 0.949; 1536^2 x 8192 2 / 3, 0.929 (fp16 0.928); 2048^2 x 8192 3 / 4,
+    // 1.133 (fp16 1.184); 1024^2 x 65536 1 / 1, 1.219 (fp16 1.328))
     const int64_t wide4_rounds = (p.batch * ((p.M + 95) / 96) * ((p.N + 63) / 64) + kCUs - 1) / kCUs;
     const bool wide4 = L == 4 && 29 * wide4_rounds < 20 * ring_rounds;
     // L = 5: the one-wave-per-SIMD kernel (one launch; int8 / fp16 / bf16

@@ -536,23 +536,25 @@ def _gemm_kernel(L, batch, M, N, K, nsp, sd, cus, with_ksplit=False):
 
 def test_planner_kernel_choice():
     """num_splits 3: the wide kernel where its rounds of one workgroup per CU
-    finish sooner (12 * wide rounds < 7 * ring rounds), measured crossovers at
-    200 / 288 / 384 / 480 / 512 wide tiles on 256 CUs; the rule follows the
-    device's compute-unit count (a 32-CU partition)."""
+    finish no later (16 x 16 forms: 3 * wide rounds <= 2 * ring rounds; the 32
+    x 32 forms of fp32 slices: 12 * wide rounds < 7 * ring rounds), measured
+    crossovers at 200 / 288 / 384 / 512 wide tiles on 256 CUs; the rule
+    follows the device's compute-unit count (a 32-CU partition)."""
     from ozaki_triton_amd import _lib
     L = _lib.load()
     I8 = _lib.OZK_I8
     # wide tiles = (M / 64) * (N / 128)
     assert _gemm_kernel(L, 1, 640, 2560, 4096, 3, I8, 256) == "wide"      # 200 tiles
-    assert _gemm_kernel(L, 1, 1024, 2304, 4096, 3, I8, 256) == "ring"     # 288
-    assert _gemm_kernel(L, 1, 1024, 3072, 4096, 3, I8, 256) == "ring"     # 384
+    assert _gemm_kernel(L, 1, 1024, 2304, 4096, 3, I8, 256) == "wide"     # 288: 2 vs 3 rounds
+    assert _gemm_kernel(L, 1, 1024, 3072, 4096, 3, I8, 256) == "wide"     # 384
+    assert _gemm_kernel(L, 1, 1024, 2304, 4096, 3, _lib.OZK_F32, 256) == "ring"   # 32 x 32 forms
     assert _gemm_kernel(L, 1, 1024, 3840, 4096, 3, I8, 256) == "wide"     # 480
     assert _gemm_kernel(L, 1, 1024, 4096, 4096, 3, I8, 256) == "wide"     # 512
     assert _gemm_kernel(L, 16, 1024, 1024, 2048, 3, _lib.OZK_F16, 256) == "wide"   # config 4
     # config 5: 128 wide tiles with 2 split-K ranges each, one round, against
-    # 256 ring tiles in one round (12 * 1 * 1 < 7 * 1 * 2)
+    # 256 ring tiles in one round (3 * 1 * 1 <= 2 * 1 * 2)
     assert _gemm_kernel(L, 1, 1024, 1024, 65536, 3, I8, 256) == "wide"
-    # 200 wide tiles on 32 CUs: 7 rounds against 13 -> 84 < 91: wide; 288: 9 vs 18 -> wide
+    # 200 wide tiles on 32 CUs: 7 rounds against 13 -> 21 <= 26: wide; 288: 9 vs 18 -> wide
     assert _gemm_kernel(L, 1, 640, 2560, 4096, 3, I8, 32) == "wide"
     assert _gemm_kernel(L, 1, 1024, 2304, 4096, 3, I8, 32) == "wide"
     # other slice counts
