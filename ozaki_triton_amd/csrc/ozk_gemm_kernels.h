@@ -2500,7 +2500,12 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide4q_kernel(GemmParams p,
     constexpr int L = Sh::L, BM = Sh::BM, BN = Sh::BN;
     constexpr int ES = (int)sizeof(ST);
     constexpr uint32_t kOOB = 0x80000000u;
-    constexpr int P1 = 4;   // DMA instructions of stage kb + 2 in the groups after the barrier
+    // DMA of stage kb + 2: P1 instructions in the groups after stage kb's
+    // barrier, the rest in groups 0 .. G0 - 1 of stage kb + 1's first step
+    // (C3, cross-GEMM ms, four paired runs on two boxes: G0 = 4 6.09-6.27
+    // against 6.23-6.33 with the rest spread over all 8 groups; P1 = 6 or 8
+    // slower)
+    constexpr int P1 = 4, G0 = 4;
     static_assert(Sh::NW == 8 && Sh::LA == 6 && Sh::LB == 4 && BM == 96 && BN == 64,
                   "the window arithmetic below is written for this shape");
     extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -2705,7 +2710,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_wide4q_kernel(GemmParams p,
     auto stepq = [&](int ckb, int ckk, int nkb_, int nkk, bool bar, int dkb, bool on, int lo,
                      int hi, int dg0, auto FAST) __attribute__((always_inline)) {
         const int cnt = hi - lo;
-        const int span = (8 - dg0) * 6;
+        const int span = ((dg0 == 0 ? G0 : 8) - dg0) * 6;   // the slots the instructions spread over
         const lds_cptr rb_cur = region(ckb, ckk, b_org);
 #pragma unroll
         for (int gb = 0; gb < 8; ++gb) {
