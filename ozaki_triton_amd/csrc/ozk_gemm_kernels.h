@@ -3321,7 +3321,11 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ringq_kernel(GemmParams p, 
     constexpr int BM = Sh::BM, BN = Sh::BN, IA = Sh::IA;
     constexpr int ES = (int)sizeof(ST);
     constexpr uint32_t kOOB = 0x80000000u;
-    constexpr int P1 = 2;   // DMA instructions of stage kb + 2 in the groups after the barrier
+    // DMA of stage kb + 2: P1 instructions in the groups after stage kb's
+    // barrier, the rest in the first half of stage kb + 1's first step (C2,
+    // cross-GEMM, three paired runs: 0.409 against 0.412 ms spread over the
+    // whole step; 4 after the barrier: 0.414)
+    constexpr int P1 = 2;
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
     const int tid = threadIdx.x;
@@ -3521,7 +3525,7 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ringq_kernel(GemmParams p, 
         auto stepq = [&](int ckb, int ckk, int nkb_, int nkk, bool bar, int dkb, bool on, int lo,
                          int hi, int dg0, auto FAST) __attribute__((always_inline)) {
             const int cnt = hi - lo;
-            const int span = (NG - dg0) * NPA;
+            const int span = ((dg0 == 0 ? NG / 2 : NG) - dg0) * NPA;   // the slots they spread over
             const lds_cptr rb_cur = region(ckb, ckk, b_org);
 #pragma unroll
             for (int gb = 0; gb < NG; ++gb) {
