@@ -239,9 +239,9 @@ def planned_gemm_kernel(batch, M, N, K, L, sdt, pairs="all"):
 def gemm_kernel_symbol(plan, L, sdt):
     """Name of the kernel function a planned cross-GEMM launches: the
     launchers take the 16 x 16 MFMA forms ("...q") of the ring (two slices),
-    wide, wide4 and solo5 configurations for the slice dtypes benchmarked
+    wide, wide4 and solo configurations for the slice dtypes benchmarked
     here (int8, fp16)."""
-    q = (plan == "ring" and L == 2) or plan in ("wide", "wide4", "solo5")
+    q = plan in ("ring", "wide", "wide4", "solo")
     return f"cross_gemm_{plan}{'q' if q else ''}_kernel"
 
 

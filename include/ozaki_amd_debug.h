@@ -22,8 +22,8 @@ extern "C" {
 
 /*
  * Force the cross-GEMM kernel of later calls on this thread: one of "staged",
- * "dma", "pair", "ring", "wide", "wide4", "solo5", "kstep", "kstep2", or NULL / ""
- * for the planner's choice.  A kernel that cannot take a call (operand
+ * "dma", "pair", "ring", "wide", "wide4", "solo" ("solo5" too), "kstep",
+ * "kstep2", or NULL / "" for the planner's choice.  A kernel that cannot take a call (operand
  * extents, slice count) is not used for it.  Returns OZK_ERR_DTYPE for an
  * unknown name.
  */
@@ -69,7 +69,7 @@ int ozk_debug_force_gemm_ksplit(int ranges);
 /*
  * The cross-GEMM kernel the planner would choose for K-contiguous,
  * 16-byte aligned slice operands of this shape, as a name ("dma", "ring",
- * "wide", "wide4", "solo5", "kstep", "kstep2", "pair", "staged") written to
+ * "wide", "wide4", "solo", "kstep", "kstep2", "pair", "staged") written to
  * *name_out (a static string), and its split-K ranges per tile to *ksplit_out (1: none;
  * may be NULL).  cus: compute units to plan for (0: those of the current
  * device).

@@ -167,7 +167,7 @@ def device_status(clear: bool = True, stream=None) -> int:
 
 class forced_kernels:
     """Context manager for tests: force the cross-GEMM kernel (`gemm`: "staged",
-    "dma", "pair", "ring", "wide", "wide4", "solo5"), its split-K ranges
+    "dma", "pair", "ring", "wide", "wide4", "solo"), its split-K ranges
     (`ksplit`, ring and wide kernels; 1: none) and / or the split kernel
     (`split`: "coop", "strip", "transpose", "generic", "rows", "rowscoop") of
     the calls this host thread makes inside it, and optionally make every

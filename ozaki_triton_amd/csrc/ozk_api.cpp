@@ -321,7 +321,7 @@ static int cross_gemm_impl(const void *A_slices, const int64_t a_strides[4], con
     // 8 (or a forced pair-split kernel) into an fp64 C, which holds the
     // partial sum between the i-row launches
     if (num_splits > 4) {
-        const bool solo = plan.kind == ozk::kGemmSolo5;
+        const bool solo = plan.kind == ozk::kGemmSolo;
         // (the triangular set sums all its pairs in one launch, so any C)
         const bool pair = plan.kind == ozk::kGemmPair && slice_dtype != OZK_F32 &&
                           (out_dtype == OZK_F64 || p.tri);
@@ -415,7 +415,7 @@ int matmul_layout(int dtype, int64_t batch, int64_t M, int64_t N, int64_t K,
         gp.batch = batch; gp.M = M; gp.N = N; gp.K = K; gp.out_dtype = dtype;
         gp.tri = pairs == OZK_PAIRS_TRIANGULAR;
         const int kind = ozk::plan_gemm(gp, L, sd, 256).kind;
-        if (kind != ozk::kGemmSolo5 &&
+        if (kind != ozk::kGemmSolo &&
             !(kind == ozk::kGemmPair && (dtype == OZK_F64 || gp.tri)))
             return OZK_ERR_SPLITS;
     }
@@ -646,8 +646,9 @@ struct Named {
 const Named kGemmNames[] = {{"staged", ozk::kGemmStaged}, {"dma", ozk::kGemmDMA},
                             {"pair", ozk::kGemmPair},
                             {"ring", ozk::kGemmRing},     {"wide", ozk::kGemmWide},
-                            {"wide4", ozk::kGemmWide4},   {"solo5", ozk::kGemmSolo5},
-                            {"kstep", ozk::kGemmKStep},   {"kstep2", ozk::kGemmKStep2}};
+                            {"wide4", ozk::kGemmWide4},   {"solo", ozk::kGemmSolo},
+                            {"kstep", ozk::kGemmKStep},   {"kstep2", ozk::kGemmKStep2},
+                            {"solo5", ozk::kGemmSolo}};   // an earlier name of "solo"
 const Named kSplitNames[] = {{"coop", ozk::kForceSplitCoop},
                              {"strip", ozk::kForceSplitStrip},
                              {"transpose", ozk::kForceSplitTranspose},

@@ -194,7 +194,7 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
                 : wide3            ? kGemmWide
                 : wide4            ? kGemmWide4
                 : L <= 4           ? kGemmRing
-                : solo5            ? kGemmSolo5
+                : solo5            ? kGemmSolo
                                    : kGemmPair;
     // two slices or more: the K-step kernel's 8-wave form, two pair groups
     // whose waves share the SIMDs (the same bits; cross-GEMM alone at
@@ -207,11 +207,11 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
         // The triangular pair set: the K-step kernel where it runs by
         // default, else the wide kernel at L = 3 (with split-K on small
         // grids), wide4 at L = 4 where its rounds rule holds, the LDS-DMA
-        // kernel at L = 2 and otherwise at L = 4 (its 10 pairs of a 32 x 32
-        // block take 160 accumulator registers), and at L = 5 the
-        // one-wave-per-SIMD kernel (int8 / fp16 / bf16; fp32 slices: the
-        // pair-split kernel over all i-rows).  Measured, cross-GEMM alone,
-        // full-range random int8 slices, pair / solo5: 8192^3 8.12 / 6.99 ms,
+        // kernel at L = 2, the one-wave-per-SIMD kernel otherwise at L = 4
+        // (below) and at L = 5 (int8 / fp16 / bf16; fp32 slices: the LDS-DMA
+        // kernel at L = 4, the pair-split kernel over all i-rows at L = 5).
+        // Measured, cross-GEMM alone, full-range random int8 slices, pair /
+        // solo at L = 5: 8192^3 8.12 / 6.99 ms,
         // 4096^2 x 8192 2.04 / 1.75, 2048^2 x 8192 0.487 / 0.399, 1024^2 x
         // 65536 1.16 / 1.04, 1024^2 x 8192 0.127 / 0.101 (all 25 pairs: 14.05
         // / 9.29, 3.52 / 2.26, 0.816 / 0.562, 1.77 / 1.12, 0.209 / 0.142).
@@ -219,12 +219,18 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
         // 5.88 / 6.54 ms, 4096^2 x 8192 1.47-1.64 / 1.66-1.81, 2048^2 x 8192
         // 0.382 / 0.391, 1024^2 x 65536 1.05 / 0.80.  L > 5 has no kernel
         // (the caller rejects it).
+        // At L = 4 off wide4's rounds rule: the one-wave-per-SIMD kernel,
+        // except a single round over a long K (cross-GEMM alone, int8, solo /
+        // LDS-DMA: 2048^2 x 8192 0.277 / 0.349 ms, 2048^2 x 4096 0.148 /
+        // 0.188, 1024^2 x 8192 0.075 / 0.094, 1024^2 x 65536 0.910 / 0.782)
+        const bool solo4 = L == 4 && slice_dtype != 1 && !(nt(1, 1) <= kCUs && nkb_all >= 256);
         plan.kind = !fits     ? kGemmStaged
                     : kstep   ? kGemmKStep2
                     : L == 3  ? kGemmWide
                     : wide4   ? kGemmWide4
+                    : solo4   ? kGemmSolo
                     : L <= 4  ? kGemmDMA
-                    : solo5   ? kGemmSolo5
+                    : solo5   ? kGemmSolo
                               : kGemmPair;
         if (L <= 4) {
             if (forced(kGemmStaged)) plan.kind = kGemmStaged;
@@ -235,8 +241,9 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
             else if (fits && forced(kGemmKStep) && !(L == 4 && slice_dtype == 1))
                 plan.kind = kGemmKStep;
             else if (fits && forced(kGemmKStep2) && L >= 2) plan.kind = kGemmKStep2;
-        } else if (fits && forced(kGemmSolo5) && solo5) {
-            plan.kind = kGemmSolo5;
+            else if (fits && forced(kGemmSolo) && L == 4 && slice_dtype != 1) plan.kind = kGemmSolo;
+        } else if (fits && forced(kGemmSolo) && solo5) {
+            plan.kind = kGemmSolo;
         } else if (fits && forced(kGemmPair)) {
             plan.kind = kGemmPair;
         }
@@ -267,6 +274,7 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
     else if (fits && forced(kGemmWide4)) plan.kind = L == 4 ? kGemmWide4 : plan.kind;
     else if (fits && forced(kGemmKStep)) plan.kind = (L == 4 && slice_dtype == 1) ? plan.kind : kGemmKStep;
     else if (fits && forced(kGemmKStep2) && L >= 2) plan.kind = kGemmKStep2;
+    else if (fits && forced(kGemmSolo) && L == 4 && slice_dtype != 1) plan.kind = kGemmSolo;
     // 96 x 64 tiles: groups of 4 tile rows (C3: 7.12-7.16 ms against 7.21-7.23
     // with 8, 7.33-7.35 with 16; cross-GEMM alone, one box)
     if (plan.kind == kGemmWide4) plan.group_m = 4;

@@ -3698,12 +3698,12 @@ __global__ __launch_bounds__(512, 1) void cross_gemm_ringq_kernel(GemmParams p, 
 }
 
 // ---------------------------------------------------------------------------
-// num_splits 5: the tile and stage of the one-wave-per-SIMD ("solo") kernel
-// below: 64 x 64 tiles, 4 waves, two whole stages of 128 bytes of K (2 x 80
-// KB of LDS).
+// The tile and stage of the one-wave-per-SIMD ("solo") kernel below, for
+// num_splits L = 4, 5: 64 x 64 tiles, 4 waves, two whole stages of 128 bytes
+// of K (2 x 16 L KB of LDS).
 // ---------------------------------------------------------------------------
-struct Solo5Shape {
-    static constexpr int L = 5, BM = 64, BN = 64;
+template <int L_> struct SoloShape {
+    static constexpr int L = L_, BM = 64, BN = 64;
     static constexpr int NW = 4;                         // waves
     static constexpr int A_BYTES = L * BM * kDmaRB;      // 40 KB
     static constexpr int B_BYTES = L * BN * kDmaRB;      // 40 KB
@@ -3720,56 +3720,58 @@ struct Solo5Shape {
     static_assert(kDmaRB == 128, "128-byte stage rows");
 };
 
-// The B group order and A read plan of cross_gemm_solo5q_kernel (below).
-template <bool TRI> struct Solo5QPlan {
-    static constexpr int NG = 10, D = 3;
-    // group p of a K step is B fragment (gj(p), p / 5)
+// The B group order and A read plan of cross_gemm_soloq_kernel (below).
+template <int L, bool TRI> struct SoloQPlan {
+    static constexpr int NG = 2 * L, D = 3;
+    // group p of a K step is B fragment (gj(p), p / L): heavy and light
+    // groups of the triangle alternate
     static constexpr int gj(int pos) {
-        constexpr int jo[5] = {0, 4, 1, 3, 2};
-        return jo[pos % 5];
+        constexpr int jo5[5] = {0, 4, 1, 3, 2}, jo4[4] = {0, 3, 1, 2};
+        return L == 5 ? jo5[pos % 5] : jo4[pos % 4];
     }
     // the group after which A fragment row i is read for the next step: its
     // last use in the step, and not before the barrier group NG - D
     static constexpr int a_next(int i) {
         int last = 0;
         for (int pos = 0; pos < NG; ++pos)
-            if (Pairs<5, TRI>::kept(i, gj(pos))) last = pos;
+            if (Pairs<L, TRI>::kept(i, gj(pos))) last = pos;
         return last > NG - D ? last : NG - D;
     }
 };
-static_assert(Solo5QPlan<true>::a_next(4) == 7 && Solo5QPlan<true>::a_next(3) == 7 &&
-                  Solo5QPlan<true>::a_next(2) == 9 && Solo5QPlan<false>::a_next(4) == 9,
-              "solo5q read plan");
+static_assert(SoloQPlan<5, true>::a_next(4) == 7 && SoloQPlan<5, true>::a_next(3) == 7 &&
+                  SoloQPlan<5, true>::a_next(2) == 9 && SoloQPlan<5, false>::a_next(4) == 9 &&
+                  SoloQPlan<4, true>::a_next(3) == 5 && SoloQPlan<4, true>::a_next(0) == 7,
+              "solo read plan");
 
 // ---------------------------------------------------------------------------
-// The solo configuration for num_splits 5 on 16 x 16 MFMAs (int8, fp16, bf16
-// slices): 64 x 64 tiles, 4 waves (one per SIMD), wave (x, y) = (w / 2, w %
-// 2) holding every kept pair of 32 x 32 block (x, y) as 4 tiles of 16 x 16:
-// acc[n][rh][ch] for pair n (i-major, j-minor), register e of lane l at row
-// 16 rh + 4 (l / 16) + e, column 16 ch + l % 16 of the block.  All 25 pairs:
-// 100 tiles, 400 registers, pairs 0..15 in AGPRs and 16..24 in VGPRs; the
-// triangle i + j <= 4: 60 tiles, all in AGPRs.  The MFMAs are inline
-// assembly with the accumulator's file fixed (as in the 32 x 32 form: the
-// compiler does not split accumulators between the files itself).
-// Per 64-byte K step a wave reads its 10 A fragments (i, rh), resident
-// through the step, and its 10 B fragments (j, ch) through a ring of 5, B
-// group p + 3 read while group p's MFMAs run; group p is B fragment (jo[p %
-// 5], p / 5), jo = 0, 4, 1, 3, 2, so that any three groups of the triangle
-// hold at least 12 MFMAs.  The next step's A fragment (i, rh) is read after
-// its last MFMA of the step, and not before group 7, where the stage barrier
-// sits.  The LDS holds two whole stages (2 x 80 KB); DMA windows and the
-// unchecked DMA of interior stages as in cross_gemm_ringq_kernel.  Hazards of
-// the hand-placed MFMAs: results read only in the epilogue, after 64 wait
-// states; an accumulator read as srcC first after its zero fill and the
-// prologue barrier, and again only 60 (25 pairs) or 36 (triangle) MFMAs
-// later.
+// The solo configuration on 16 x 16 MFMAs (int8, fp16, bf16 slices), for
+// num_splits L = 5 and the triangle at 4: 64 x 64 tiles, 4 waves (one per
+// SIMD), wave (x, y) = (w / 2, w % 2) holding every kept pair of 32 x 32
+// block (x, y) as 4 tiles of 16 x 16: acc[n][rh][ch] for pair n (i-major,
+// j-minor), register e of lane l at row 16 rh + 4 (l / 16) + e, column 16 ch
+// + l % 16 of the block.  L = 5, all 25 pairs: 100 tiles, 400 registers,
+// pairs 0..15 in AGPRs and 16..24 in VGPRs; the triangles (60 and 40 tiles)
+// and L = 4's 16 pairs all in AGPRs.  The MFMAs are inline assembly with the
+// accumulator's file fixed (the compiler does not split accumulators between
+// the files itself).  Per 64-byte K step a wave reads its 2 L A fragments (i,
+// rh), resident through the step, and its 2 L B fragments (j, ch) through a
+// ring (5 slots at L = 5, 4 at L = 4), B group p + 3 read while group p's
+// MFMAs run; group p is B fragment (jo[p % L], p / L), jo = 0, 4, 1, 3, 2 (L
+// = 4: 0, 3, 1, 2), so that any three groups of a triangle hold at least 12
+// MFMAs.  The next step's A fragment (i, rh) is read after its last MFMA of
+// the step, and not before group 2 L - 3, where the stage barrier sits.  The
+// LDS holds two whole stages (2 x 16 L KB); DMA windows and the unchecked DMA
+// of interior stages as in cross_gemm_ringq_kernel.  Hazards of the
+// hand-placed MFMAs: results read only in the epilogue, after 64 wait states;
+// an accumulator read as srcC first after its zero fill and the prologue
+// barrier, and again only tens of MFMAs later.
 // ---------------------------------------------------------------------------
-template <typename ST, typename AccT, bool TRI>
-__global__ __launch_bounds__(256, 1) void cross_gemm_solo5q_kernel(GemmParams p, int group_m,
-                                                                   uint32_t a_records,
-                                                                   uint32_t b_records) {
+template <typename ST, int L_, typename AccT, bool TRI>
+__global__ __launch_bounds__(256, 1) void cross_gemm_soloq_kernel(GemmParams p, int group_m,
+                                                                  uint32_t a_records,
+                                                                  uint32_t b_records) {
     resolve_split_fail(p);
-    using Sh = Solo5Shape;
+    using Sh = SoloShape<L_>;
     using MF = Mfma16<ST>;
     using Acc = typename MF::Acc;
     using OA = AccT;
@@ -3783,12 +3785,13 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_solo5q_kernel(GemmParams p,
     // TFLOP/s end to end against (4, 10): (10, 4) 158.8, (12, 5) 156.8, (8, 5)
     // 156.7, (8, 3) 155.9, (8, 10) 153.7, (4, 5) 151.3, (4, 10) 149.5; all
     // pairs: (4, 10) 121.9, (8, 10) 121.4, (8, 5) 120.2, (4, 5) 118.9).
-    constexpr int P1 = TRI ? 10 : 4;
-    constexpr int G0 = TRI ? 4 : 10;
-    constexpr int NAG = TRI ? PS::N : 16;      // pairs whose tiles sit in AGPRs
-    constexpr int NG = 2 * L, D = 3, R = 5;    // B groups per step, read distance, ring slots
-    constexpr int NPA = 2 * L;                 // A fragments (i, rh)
-    static_assert(Sh::NW == 4 && Sh::LA == 10 && Sh::LB == 10 && BM == 64 && BN == 64,
+    constexpr int P1 = L == 5 ? (TRI ? 10 : 4) : (TRI ? 8 : 4);
+    constexpr int G0 = L == 5 ? (TRI ? 4 : 10) : (TRI ? 3 : 8);
+    constexpr int NAG = TRI || PS::N <= 16 ? PS::N : 16;   // pairs whose tiles sit in AGPRs
+    constexpr int NG = 2 * L, D = 3;                       // B groups per step, read distance
+    constexpr int R = NG % 5 == 0 ? 5 : 4;                 // B ring slots
+    constexpr int NPA = 2 * L;                             // A fragments (i, rh)
+    static_assert(Sh::NW == 4 && Sh::LA == 2 * L && Sh::LB == 2 * L && BM == 64 && BN == 64,
                   "the window arithmetic below is written for this shape");
     static_assert(NG % R == 0 && R > D && NAG * 4 * 4 <= 256, "ring; AGPR file");
     extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -3954,10 +3957,10 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_solo5q_kernel(GemmParams p,
         return *(const __attribute__((address_space(3))) i32x4 *)(
             ra + ((pa >> 1) * BM + 16 * (pa & 1)) * kDmaRB);
     };
-    using QP = Solo5QPlan<TRI>;
+    using QP = SoloQPlan<L, TRI>;
     auto read_b = [&](lds_cptr rb, int pos) {   // B fragment of group pos
         return *(const __attribute__((address_space(3))) i32x4 *)(
-            rb + (QP::gj(pos) * BN + 16 * (pos / 5)) * kDmaRB);
+            rb + (QP::gj(pos) * BN + 16 * (pos / L)) * kDmaRB);
     };
 
     i32x4 fa[NPA];   // A fragments, resident through a K step
@@ -3990,7 +3993,7 @@ __global__ __launch_bounds__(256, 1) void cross_gemm_solo5q_kernel(GemmParams p,
                 }
                 fb[(pos + D) % R] = read_b(region(nkb_, nkk, b_org), pos + D - NG);
             }
-            constexpr int j = QP::gj(pos), ch = pos / 5;
+            constexpr int j = QP::gj(pos), ch = pos / L;
             static_for<NPA>([&](auto pa_) {
                 constexpr int pa = decltype(pa_)::value;
                 constexpr int i = pa >> 1, rh = pa & 1;
@@ -4257,13 +4260,13 @@ static hipError_t launch_wide4(const GemmParams &p, const GemmPlan &plan, hipStr
     return hipGetLastError();
 }
 
-template <typename ST, typename AccT, bool TRI>
-static hipError_t launch_solo5(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
+template <typename ST, int L, typename AccT, bool TRI>
+static hipError_t launch_solo(const GemmParams &p, const GemmPlan &plan, hipStream_t st) {
     if constexpr (std::is_same<ST, float>::value) {
         return hipErrorInvalidValue;   // no fp32-slice form
     } else {
-        using Sh = Solo5Shape;
-        auto kern = cross_gemm_solo5q_kernel<ST, AccT, TRI>;
+        using Sh = SoloShape<L>;
+        auto kern = cross_gemm_soloq_kernel<ST, L, AccT, TRI>;
         static std::atomic<uint64_t> lds_set{0};   // devices whose LDS limit is raised
         if (hipError_t e = set_lds_limit((const void *)kern, Sh::LDS_BYTES, lds_set)) return e;
         const int es = (int)sizeof(ST);
@@ -4358,9 +4361,11 @@ static hipError_t launch_L(const GemmParams &p, const GemmPlan &plan, hipStream_
         case 11: return launch_one<ST, 2, 1, 1, AccT, TRI>(p, plan, st);
         }
     } else if constexpr (L <= 4) {
+        if constexpr (L == 4)
+            if (plan.kind == kGemmSolo) return launch_solo<ST, 4, AccT, TRI>(p, plan, st);
         if (key == 11) return launch_one<ST, L, 1, 1, AccT, TRI>(p, plan, st);
     } else if constexpr (L == 5) {
-        if (plan.kind == kGemmSolo5) return launch_solo5<ST, AccT, TRI>(p, plan, st);
+        if (plan.kind == kGemmSolo) return launch_solo<ST, 5, AccT, TRI>(p, plan, st);
         if constexpr (!TRI) return launch_chunks<ST, L, AccT>(p, plan, st);
         // the 15 kept pairs split 8 / 7 over the wave groups: one launch
         else if (plan.kind == kGemmPair && !std::is_same_v<ST, float>)

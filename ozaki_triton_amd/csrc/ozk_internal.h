@@ -156,8 +156,9 @@ enum GemmKind {
                       // of a 32 x 32 block, two whole stages in the LDS
     kGemmWide4 = 6,   // num_splits 4: 96 x 64 tiles, 8 waves of 12 accumulator tiles
                       // (3 A x 4 B fragments), two whole stages in the LDS
-    kGemmSolo5 = 7,   // num_splits 5: 64 x 64 tiles, 4 waves (one per SIMD) each holding
-                      // all 25 pairs of a 32 x 32 block, two whole stages in the LDS
+    kGemmSolo = 7,    // num_splits 5 (and 4 on the triangle): 64 x 64 tiles, 4 waves (one
+                      // per SIMD) each holding every pair of a 32 x 32 block, two whole
+                      // stages in the LDS
     kGemmKStep = 8,   // num_splits 1-4 on small grids: 32 x 32 tiles, 4 waves, wave w takes
                       // K step w of every stage and all pairs; summed through the LDS
     kGemmKStep2 = 9   // the same with 8 waves: two pair groups, two waves per SIMD (L = 2..4)

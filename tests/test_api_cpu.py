@@ -519,7 +519,7 @@ def test_debug_hooks_reject_unknown_names():
     L = _lib.load()
     assert L.ozk_debug_force_gemm_kernel(b"fastest") == _lib.OZK_ERR_DTYPE
     assert L.ozk_debug_force_split_kernel(b"fastest") == _lib.OZK_ERR_DTYPE
-    for k in (b"staged", b"dma", b"pair", b"ring", b"wide", b"wide4", b"solo5", b"",
+    for k in (b"staged", b"dma", b"pair", b"ring", b"wide", b"wide4", b"solo", b"solo5", b"",
               None):
         assert L.ozk_debug_force_gemm_kernel(k) == 0
     for k in (b"coop", b"strip", b"transpose", b"generic", b"rows", b"rowscoop", None):
@@ -601,9 +601,9 @@ def test_planner_kernel_choice():
     assert _gemm_kernel(L, 16, 1024, 1024, 2048, 3, _lib.OZK_F16, 256, True) == ("wide", 1)
     # num_splits 5: the one-wave-per-SIMD kernel, in one launch, for int8 /
     # fp16 / bf16 slices; fp32 slices and 6 to 8 slices: the pair-split kernel
-    assert _gemm_kernel(L, 1, 1024, 1024, 1024, 5, I8, 256) == "solo5"
-    assert _gemm_kernel(L, 1, 8192, 8192, 8192, 5, I8, 256) == "solo5"
-    assert _gemm_kernel(L, 1, 4096, 4096, 4096, 5, _lib.OZK_BF16, 256) == "solo5"
+    assert _gemm_kernel(L, 1, 1024, 1024, 1024, 5, I8, 256) == "solo"
+    assert _gemm_kernel(L, 1, 8192, 8192, 8192, 5, I8, 256) == "solo"
+    assert _gemm_kernel(L, 1, 4096, 4096, 4096, 5, _lib.OZK_BF16, 256) == "solo"
     assert _gemm_kernel(L, 1, 1024, 1024, 1024, 5, _lib.OZK_F32, 256) == "pair"
     assert _gemm_kernel(L, 1, 1024, 1024, 1024, 6, I8, 256) == "pair"
 
@@ -621,19 +621,22 @@ def test_triangular_planner():
     block in one wave: the K-step kernel on small grids as for all pairs, else
     the wide kernel at 3 slices (split-K on small grids), the one-wave-per-SIMD
     kernel at 5 (the pair-split kernel for fp32 slices), the LDS-DMA kernel at
-    2, and at 4 wide4 where its rounds rule holds and the LDS-DMA kernel
-    elsewhere; one slice plans as all pairs."""
+    2, and at 4 wide4 where its rounds rule holds, else the one-wave-per-SIMD
+    kernel (the LDS-DMA kernel for one round over a long K, and for fp32
+    slices); one slice plans as all pairs."""
     from ozaki_triton_amd import _lib
     L = _lib.load()
     I8, F16, F32 = _lib.OZK_I8, _lib.OZK_F16, _lib.OZK_F32
     T, A = _lib.OZK_PAIRS_TRIANGULAR, _lib.OZK_PAIRS_ALL
     c3 = (1, 8192, 8192, 8192)
-    assert _gemm_kernel_pairs(L, *c3, 5, I8, T) == ("solo5", 1)
-    assert _gemm_kernel_pairs(L, *c3, 5, F16, T) == ("solo5", 1)
+    assert _gemm_kernel_pairs(L, *c3, 5, I8, T) == ("solo", 1)
+    assert _gemm_kernel_pairs(L, *c3, 5, F16, T) == ("solo", 1)
     assert _gemm_kernel_pairs(L, *c3, 5, F32, T) == ("pair", 1)
-    assert _gemm_kernel_pairs(L, *c3, 5, I8, A) == ("solo5", 1)
+    assert _gemm_kernel_pairs(L, *c3, 5, I8, A) == ("solo", 1)
     assert _gemm_kernel_pairs(L, *c3, 4, I8, T) == ("wide4", 1)
-    assert _gemm_kernel_pairs(L, 1, 2048, 2048, 8192, 4, I8, T) == ("dma", 1)
+    assert _gemm_kernel_pairs(L, 1, 2048, 2048, 8192, 4, I8, T) == ("solo", 1)
+    assert _gemm_kernel_pairs(L, 1, 1024, 1024, 65536, 4, I8, T) == ("dma", 1)   # one round, long K
+    assert _gemm_kernel_pairs(L, 1, 2048, 2048, 8192, 4, F32, T) == ("dma", 1)
     assert _gemm_kernel_pairs(L, *c3, 4, I8, A) == ("wide4", 1)
     assert _gemm_kernel_pairs(L, *c3, 3, I8, T) == ("wide", 1)
     assert _gemm_kernel_pairs(L, *c3, 2, I8, T) == ("dma", 1)

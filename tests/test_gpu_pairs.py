@@ -2,7 +2,7 @@
 cross-GEMM sums every slice pair, ozaki_triton.py:403-447): C sums only the
 pairs i + j <= L - 1, in the reference's i-major / j-minor order.
 
-Every kernel that takes the set (staged, dma, kstep, wide, wide4, pair, solo5) runs it
+Every kernel that takes the set (staged, dma, kstep, wide, wide4, pair, solo) runs it
 forced and must equal the oracle's triangular sum bit for bit: int8 slices on
 random values, float slices on integer values (exact in fp32 in any order,
 tests/helpers.py:int_valued_slices).  The oracle's triangular sum is pinned on
@@ -37,7 +37,7 @@ def _cross(ozk, gpu, As, BsT, sa, sb, L, out, pairs):
 TRI_KERNELS = [("staged", 2), ("staged", 3), ("staged", 4), ("dma", 2), ("dma", 3), ("dma", 4),
                ("kstep", 2), ("kstep", 3), ("kstep", 4),
                ("kstep2", 2), ("kstep2", 3), ("kstep2", 4),
-               ("wide", 3), ("wide4", 4), ("pair", 3), ("pair", 4), ("pair", 5), ("solo5", 5)]
+               ("wide", 3), ("wide4", 4), ("pair", 3), ("pair", 4), ("pair", 5), ("solo", 4), ("solo", 5)]
 
 
 @pytest.mark.parametrize("sdt", [torch.int8, torch.float16, torch.bfloat16, torch.float32])
@@ -68,7 +68,7 @@ def test_triangular_each_kernel_bitexact(oracle, gpu, kernel, L, M, N, K, sdt, f
 
 @pytest.mark.parametrize("out", [torch.float32, torch.float16, torch.bfloat16, torch.int8])
 @pytest.mark.parametrize("kernel,L", [("dma", 4), ("kstep", 3), ("wide", 3), ("wide4", 4),
-                                      ("pair", 5), ("solo5", 5)])
+                                      ("pair", 5), ("solo", 4), ("solo", 5)])
 def test_triangular_output_dtypes(oracle, gpu, kernel, L, out, force):
     """The fp32 outer accumulator and C's conversions under the triangular set."""
     import ozaki_triton_amd as ozk

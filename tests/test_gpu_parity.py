@@ -418,7 +418,7 @@ def test_ozaki_matmul_degenerate_shapes(gpu):
 
 
 @pytest.mark.parametrize("kernel", ["staged", "dma", "pair", "ring", "wide", "wide4",
-                                    "kstep", "kstep2"])
+                                    "kstep", "kstep2", "solo"])
 @pytest.mark.parametrize("L", [1, 2, 3, 4])
 def test_cross_gemm_each_kernel_bitexact(oracle, gpu, L, kernel, force):
     """Every cross-GEMM kernel, forced: the VGPR-staged one (taken when an
@@ -426,7 +426,8 @@ def test_cross_gemm_each_kernel_bitexact(oracle, gpu, L, kernel, force):
     the 2 x 2 LDS-DMA kernel, the pair-split kernel, its
     five-slot ring form (L >= 3; for L <= 2 the request falls back to the
     2 x 2 kernel), the wide kernel (L = 3), the 96 x 64 wide kernel (L = 4;
-    otherwise the default kernel) and the K-step kernel (32 x 32 tiles)."""
+    otherwise the default kernel), the K-step kernel (32 x 32 tiles) and the
+    one-wave-per-SIMD kernel (L = 4, all 16 pairs in AGPRs)."""
     import ozaki_triton_amd as ozk
     force(gemm=kernel)
     g = torch.Generator().manual_seed(77 + L)
@@ -459,6 +460,8 @@ def test_cross_gemm_each_kernel_bitexact(oracle, gpu, L, kernel, force):
     ("kstep2", 4, 100, 72, 1040),
     ("kstep2", 3, 130, 72, 4096),
     ("kstep2", 2, 64, 96, 2064),
+    ("solo", 4, 100, 72, 1040),     # (fp32 slices: the planner's kernel)
+    ("solo", 4, 130, 200, 4096),
 ])
 def test_float_slice_kernels_bitexact(oracle, gpu, kernel, L, M, N, K, sdt, force):
     """Every cross-GEMM kernel with float slices, at the tile shapes and K of
@@ -638,7 +641,7 @@ def test_solo5_kernel_stage_counts(oracle, gpu, K, MN, sdt):
     integer-valued fp16 slices bit-exact against the oracle."""
     import ozaki_triton_amd as ozk
     L, (M, N) = 5, MN
-    assert _planned(1, M, N, K, L, sdt) == "solo5"
+    assert _planned(1, M, N, K, L, sdt) == "solo"
     g = torch.Generator().manual_seed(K * 10 + 7 * M + N)
     As, BsT, sa, sb = _slices_for(g, 2, L, M, N, K, sdt)
     args = (As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), L, torch.float64)
@@ -647,6 +650,29 @@ def test_solo5_kernel_stage_counts(oracle, gpu, K, MN, sdt):
         want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[b]), to_np(sa[b]), to_np(sb[b]),
                                  "float64")
         assert_bitwise_equal(C[b], want, f"solo5 {sdt} K{K} M{M} N{N} b{b}")
+
+
+@pytest.mark.parametrize("sdt", [torch.int8, torch.float16])
+@pytest.mark.parametrize("MN", [(130, 200), (65, 63), (1, 300)])
+@pytest.mark.parametrize("K", [16, 128, 200, 520, 1040, 2064])
+def test_solo_kernel_four_slices_triangle(oracle, gpu, K, MN, sdt):
+    """The one-wave-per-SIMD kernel at num_splits 4 on the triangular pair set
+    (10 pairs of a 32 x 32 block in 160 AGPRs; the planner's kernel off wide4's
+    rounds rule), over 1 to 17 stages of 128 bytes of K, with M and N cutting
+    tiles and batch 2: int8 and integer-valued fp16 slices bit-exact against
+    the oracle."""
+    import ozaki_triton_amd as ozk
+    from ozaki_triton_amd import _lib
+    L, (M, N) = 4, MN
+    g = torch.Generator().manual_seed(K * 10 + 7 * M + N + 4)
+    As, BsT, sa, sb = _slices_for(g, 2, L, M, N, K, sdt)
+    args = (As.to(gpu), BsT.to(gpu).transpose(-1, -2), sa.to(gpu), sb.to(gpu), L, torch.float64)
+    with _lib.forced_kernels(gemm="solo"):
+        C = to_np(ozk.cross_gemm(*args, pairs="triangular"))
+    for b in range(2):
+        want = oracle.cross_gemm(to_np(As[b]), to_np(BsT[b]), to_np(sa[b]), to_np(sb[b]),
+                                 "float64", pairs="triangular")
+        assert_bitwise_equal(C[b], want, f"solo L4 tri {sdt} K{K} M{M} N{N} b{b}")
 
 
 @pytest.mark.parametrize("out", [torch.float64, torch.float32, torch.float16, torch.bfloat16,
