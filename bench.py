@@ -390,6 +390,58 @@ def vendor_probes():
     print(json.dumps(out), flush=True)
 
 
+class TimingEvent:
+    """A HIP event for timing only, created with hipEventDisableSystemFence:
+    recording it writes back and invalidates no caches, which torch's events
+    (a system-scope release each) do, so it perturbs the work around it less.
+    Created through the HIP runtime torch has loaded (the library's own), as
+    a `cuda_event` handle the library records; `factory()` falls back to
+    torch's events where that runtime cannot be found."""
+    _hip = None
+    DISABLE_SYSTEM_FENCE = 0x20000000
+
+    @classmethod
+    def factory(cls):
+        import ctypes
+        import torch
+        if cls._hip is None:
+            paths = sorted({ln.split()[-1] for ln in open("/proc/self/maps")
+                            if "libamdhip64" in ln and "/" in ln})
+            if len(paths) != 1:
+                return lambda: torch.cuda.Event(enable_timing=True)
+            cls._hip = ctypes.CDLL(paths[0])
+        return cls
+
+    def __init__(self):
+        import ctypes
+        h = ctypes.c_void_p()
+        rc = self._hip.hipEventCreateWithFlags(ctypes.byref(h),
+                                               ctypes.c_uint(self.DISABLE_SYSTEM_FENCE))
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
+        self._h = h
+        self.cuda_event = h.value
+
+    def record(self):
+        import ctypes
+        import torch
+        rc = self._hip.hipEventRecord(self._h, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"hipEventRecord failed ({rc})")
+
+    def elapsed_time(self, end) -> float:
+        import ctypes
+        ms = ctypes.c_float()
+        rc = self._hip.hipEventElapsedTime(ctypes.byref(ms), self._h, end._h)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return ms.value
+
+    def __del__(self):
+        if self._hip is not None and getattr(self, "_h", None) is not None:
+            self._hip.hipEventDestroy(self._h)
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -472,13 +524,19 @@ def main():
     print(f"[bench] {args.config}: {xdt}->{sdt} L={L} A{tuple(A.shape)} B{tuple(B.shape)}",
           file=sys.stderr, flush=True)
 
-    # four timing events per step, recorded by the library on the launch
-    # stream between the phases (before the B split, the A split, the
-    # cross-GEMM, and after it); each is recorded once here so that it exists
+    # Timing events, recorded by the library on the launch stream between the
+    # phases: before the B split, before the A split, before the cross-GEMM,
+    # after it (it skips NULL entries).  Each event costs the stream a few
+    # microseconds (four per step added 13-18 us to C2's 0.47 ms step and 20 us
+    # to C3's 6.6 ms, one box), so a timed step records only the bounds of one
+    # part: even steps the splits' (with the B / A boundary only where the
+    # splits are separate launches), odd steps the cross-GEMM's.  The events
+    # carry no system-scope fence (TimingEvent).
     phases = ("split_b", "split_a", "cross_gemm", "end")
+    mk_event = TimingEvent.factory()
     events = []
     for _ in range(args.steps):
-        evs = [torch.cuda.Event(enable_timing=True) for _ in phases]
+        evs = [mk_event() for _ in phases]
         for e in evs:
             e.record()
         events.append(evs)
@@ -495,21 +553,33 @@ def main():
             torch.cuda.synchronize()
         done = 2
         warmup = max(3, min(5000, int(0.2 / max(time.perf_counter() - tw, 1e-6)) + 1))
-    for _ in range(warmup - done):
+    warmup = max(warmup, done + 1)
+    for _ in range(warmup - done - 1):
         _ozaki_matmul_impl(A, B, L, slice_dtype, False, None, max_splits=8, pairs=args.pairs)
+    # the last warmup step with all four events: are the splits one launch
+    # (split_pair_kernel / split_duo_kernel)?  Then the B phase's two events
+    # fall at one point
+    _ozaki_matmul_impl(A, B, L, slice_dtype, False, events[0], max_splits=8, pairs=args.pairs)
     torch.cuda.synchronize()
+    one_launch = events[0][0].elapsed_time(events[0][1]) < 0.02
+    step_events = [
+        ([e[0], None if one_launch else e[1], e[2], None] if s % 2 == 0 else
+         [None, None, e[2], e[3]]) for s, e in enumerate(events)] if args.steps > 1 else events
 
     t0 = time.perf_counter()
     for s in range(args.steps):
-        C = _ozaki_matmul_impl(A, B, L, slice_dtype, False, events[s], max_splits=8,
+        C = _ozaki_matmul_impl(A, B, L, slice_dtype, False, step_events[s], max_splits=8,
                                pairs=args.pairs)
     torch.cuda.synchronize()
     t = time.perf_counter() - t0
     ms = t / args.steps * 1e3
 
     def avg_ms(a, b):
+        """Mean time between phases a and b over the timed steps that recorded both."""
         ia, ib = phases.index(a), phases.index(b)
-        return sum(e[ia].elapsed_time(e[ib]) for e in events) / len(events)
+        got = [ev[ia].elapsed_time(ev[ib]) for ev in step_events
+               if ev[ia] is not None and ev[ib] is not None]
+        return sum(got) / len(got)
 
     # single calls, each after a 512 MiB write that evicts L2 and MALL (as
     # triton.testing.do_bench, which reference test.py:125 times with, clears
@@ -558,8 +628,10 @@ def main():
     copy21_gbs = 3.0 * ca.numel() / (e0.elapsed_time(e1) / 10 * 1e-3) / 1e9
     del csrc, ca, cb, cc
 
-    t_split_b = avg_ms("split_b", "split_a")
-    t_split_a = avg_ms("split_a", "cross_gemm")
+    if one_launch:
+        t_split_b, t_split_a = 0.0, avg_ms("split_b", "cross_gemm")
+    else:
+        t_split_b, t_split_a = avg_ms("split_b", "split_a"), avg_ms("split_a", "cross_gemm")
     t_cross = avg_ms("cross_gemm", "end")
 
     emu_flops = 2.0 * M * N * K * batch
@@ -645,9 +717,8 @@ def main():
         "split": {
             "kernels": {"A": planned_split_kernel(A, xdt, sdt, L, False),
                         "B": planned_split_kernel(B, xdt, sdt, L, True)},
-            # both splits in one launch (split_pair_kernel): the library then
-            # records the B phase's two events at one point, and ms_a covers both
-            "one_launch": t_split_b < 0.02,
+            # both splits in one launch: ms_a covers both
+            "one_launch": one_launch,
             "bound": "hbm",
             "bytes": split_bytes,
             "achieved": round(split_gbs, 1),

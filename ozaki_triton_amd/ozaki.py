@@ -403,6 +403,12 @@ _CALLS: dict = {}
 _CALLS_MAX = 256
 
 
+def _event_array(events):
+    """The C ABI's four hipEvent_t (NULL where an entry is None)."""
+    return (ctypes.c_void_p * 4)(*[ctypes.c_void_p(None if e is None else e.cuda_event)
+                                   for e in events])
+
+
 def _matmul_cached(hit, A, B, events):
     xd, sd, pc, BN, M, N, K, L, a_st, b_st, c_st, c_shape, out_shape = hit
     dev = A.device
@@ -415,7 +421,7 @@ def _matmul_cached(hit, A, B, events):
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes else None
     ev = None
     if events is not None:
-        ev = (ctypes.c_void_p * 4)(*[ctypes.c_void_p(e.cuda_event) for e in events])
+        ev = _event_array(events)
     args = (A.data_ptr(), a_st, B.data_ptr(), b_st, xd, BN, M, N, K, L, sd, pc, C.data_ptr(),
             c_st, ws.data_ptr() if ws is not None else None, nbytes, ev)
     if dev.index is None or dev.index == torch.cuda.current_device():
@@ -450,8 +456,9 @@ def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, events, max_split
 
     The splits and the cross-GEMM are enqueued by one C call (ozk_matmul) with
     one workspace holding the slices and scales.  ``events`` (internal, used by
-    bench.py) is None or four torch.cuda.Event objects that the call records
-    before the B split, before the A split, before the cross-GEMM and after it.
+    bench.py) is None or four event objects (a `cuda_event` handle each, or None
+    to skip one) that the call records before the B split, before the A split,
+    before the cross-GEMM and after it.
     ``max_splits`` is the reference's limit of 4 (ozaki_triton.py:563) unless
     the caller raises it, up to the C ABI's OZK_MAX_SPLITS (8).
     """
@@ -512,7 +519,7 @@ def _ozaki_matmul_impl(A, B, num_splits, slice_dtype, verbose, events, max_split
     ws, wsp = _workspace(int(nbytes.value), dev)
     ev = None
     if events is not None:
-        ev = (ctypes.c_void_p * 4)(*[ctypes.c_void_p(e.cuda_event) for e in events])
+        ev = _event_array(events)
     c_st = _lib.i64arr(C.stride())
     with _on_device(dev):
         st = L.ozk_matmul_pairs(ctypes.c_void_p(A3.data_ptr()), a_st,

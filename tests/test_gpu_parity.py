@@ -1514,3 +1514,32 @@ def test_repeated_call_fast_path(oracle, gpu):
     torch.cuda.synchronize()
     assert evs[0].elapsed_time(evs[3]) > 0
     assert_bitwise_equal(to_np(C), oracle.ozaki_matmul(to_np(A1), to_np(B1), 3, "int8"), "events")
+
+
+def test_bench_timing_events_partial(oracle, gpu):
+    """bench.py's timed steps pass the library two of its four phase events
+    (None for the others), created by bench.TimingEvent without the
+    system-scope fence: the call records only those, on the launch stream,
+    and stays bit-exact, on the cached and the uncached path."""
+    from ozaki_triton_amd import ozaki as oz
+    from ozaki_triton_amd.ozaki import _ozaki_matmul_impl
+    from tests.helpers import c3_like
+    import bench
+    mk = bench.TimingEvent.factory()
+    assert mk is bench.TimingEvent, "HIP runtime of torch not found"
+    A, B = c3_like((1, 200, 3000), (3000, 136), 41)
+    Ad, Bd = A.to(gpu), B.to(gpu)
+    want = oracle.ozaki_matmul(to_np(A), to_np(B), 4, "int8")
+    for cached in (False, True):
+        if not cached:
+            oz._CALLS.clear()
+        evs = [mk() for _ in range(4)]
+        for e in evs:
+            e.record()
+        torch.cuda.synchronize()
+        for k, part in enumerate(([evs[0], None, evs[2], None], [None, None, evs[2], evs[3]])):
+            C = _ozaki_matmul_impl(Ad, Bd, 4, torch.int8, False, part)
+            torch.cuda.synchronize()
+            assert_bitwise_equal(to_np(C), want, f"partial events cached={cached}")
+            # the splits, then the cross-GEMM: both take time
+            assert (evs[0].elapsed_time(evs[2]) if k == 0 else evs[2].elapsed_time(evs[3])) > 0
