@@ -222,7 +222,10 @@ GemmPlan plan_gemm(const GemmParams &p, int L, int slice_dtype, int cus) {
         // At L = 4 off wide4's rounds rule: the one-wave-per-SIMD kernel,
         // except a single round over a long K (cross-GEMM alone, int8, solo /
         // LDS-DMA: 2048^2 x 8192 0.277 / 0.349 ms, 2048^2 x 4096 0.148 /
-        // 0.188, 1024^2 x 8192 0.075 / 0.094, 1024^2 x 65536 0.910 / 0.782)
+        // 0.188, 1024^2 x 8192 0.075 / 0.094, 1024^2 x 65536 0.910 / 0.782).
+        // Where the rules hold, wide4 keeps the triangle (solo / wide4, one
+        // box: 8192^3 5.36 / 5.41 ms, 4096 x 8192 x 8192 2.64 / 2.63, 4096^2
+        // x 8192 1.33 / 1.30, 8192^2 x 4096 2.88 / 2.64)
         const bool solo4 = L == 4 && slice_dtype != 1 && !(nt(1, 1) <= kCUs && nkb_all >= 256);
         plan.kind = !fits     ? kGemmStaged
                     : kstep   ? kGemmKStep2
