@@ -1543,3 +1543,23 @@ def test_bench_timing_events_partial(oracle, gpu):
             assert_bitwise_equal(to_np(C), want, f"partial events cached={cached}")
             # the splits, then the cross-GEMM: both take time
             assert (evs[0].elapsed_time(evs[2]) if k == 0 else evs[2].elapsed_time(evs[3])) > 0
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.bfloat16, torch.int8])
+def test_ozaki_matmul_narrow_inputs_long_k(oracle, gpu, xdt):
+    """Narrow inputs over a K that takes the long-row paths after the exact
+    fp32 conversion: A's rows through the shared row kernel (K > 16384) and
+    B's columns through the cooperative column kernel or the transpose, end
+    to end with int8 slices, bit-exact against the oracle; broadcast batch."""
+    import ozaki_triton_amd as ozk
+    g = torch.Generator().manual_seed(71 + ALL_INPUTS.index(xdt))
+    K = 20000
+    A = _random_input(g, (2, 24, K), xdt)
+    B = _random_input(g, (K, 40), xdt)
+    print(f"narrow long K {xdt} A{tuple(A.shape)} B{tuple(B.shape)}", flush=True)
+    C = ozk.ozaki_matmul(A.to(gpu), B.to(gpu), 3, torch.int8)
+    torch.cuda.synchronize()
+    assert C.dtype == xdt and C.shape == (2, 24, 40)
+    want = oracle.ozaki_matmul(to_np(A), to_np(B), 3, "int8")
+    assert_bitwise_equal(to_np(C), want, f"narrow long K {xdt}")
+    ozk.device_status()                     # raises if a cooperative wait gave up
